@@ -1,0 +1,171 @@
+/*
+ * lonnx.h -- C ABI of the MI355X (gfx950) device path for the Lokad.Onnx
+ * elementwise / broadcast / reduction operators.
+ *
+ * The ABI is plain C (cdecl, POD structs, no C++ or torch types) so that the
+ * unchanged C# operator layer can bind it with [DllImport] exactly as it binds
+ * any native library; a Python ctypes binding of the same symbols is what the
+ * tests use.  Every operator entry point mirrors one static method of
+ * CPUExecutionProvider (src/Lokad.Onnx.Backend/CPUExecutionProvider.cs) with
+ * the same argument meaning; the status codes mirror the OpResult factories
+ * (src/Lokad.Onnx.Backend/OpResult.cs:34-60) and the exceptions that
+ * Node.Execute converts into OpResult.Failure (Node.cs:107-118).
+ *
+ * Threading: one device per process, one stream at a time (lx_set_stream).
+ * Calls are stream ordered; lx_tensor_download synchronises.  The library is
+ * not re-entrant across host threads.
+ */
+#ifndef LONNX_H
+#define LONNX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LX_MAX_RANK 8
+
+/* Element type codes: TensorElementType (src/Lokad.Onnx.Tensors/Tensor.cs:31-50). */
+enum lx_dtype {
+    LX_FLOAT = 1, LX_UINT8 = 2, LX_INT8 = 3, LX_UINT16 = 4, LX_INT16 = 5,
+    LX_INT32 = 6, LX_INT64 = 7, LX_BOOL = 9, LX_DOUBLE = 11, LX_UINT32 = 12,
+    LX_UINT64 = 13
+};
+
+/* Status codes returned by every entry point (0 = success). */
+enum lx_status {
+    LX_OK = 0,
+    LX_ERR_MISSING_INPUT = 1,            /* OpResult.MissingInput            (OpResult.cs:46) */
+    LX_ERR_WRONG_INPUT_TYPE = 2,         /* OpResult.WrongInputType          (OpResult.cs:50-52) */
+    LX_ERR_CANNOT_BROADCAST = 3,         /* OpResult.CannotBroadcast         (OpResult.cs:60) */
+    LX_ERR_INPUT_TYPE_NOT_SUPPORTED = 4, /* OpResult.InputTypeNotSupported   (OpResult.cs:40) */
+    LX_ERR_NOT_SUPPORTED = 5,            /* OpResult.NotSupported            (OpResult.cs:38) */
+    LX_ERR_ATTRIBUTE_NOT_SUPPORTED = 6,  /* OpResult.AttributeNotSupported   (OpResult.cs:42) */
+    LX_ERR_WRONG_INPUT_SHAPE = 7,        /* OpResult.WrongInputShape         (OpResult.cs:54-58) */
+    LX_ERR_INVALID_ARGUMENT = 8,         /* ArgumentException  -> OpResult.Failure (Node.cs:115-118) */
+    LX_ERR_DIVIDE_BY_ZERO = 9,           /* DivideByZeroException -> OpResult.Failure */
+    LX_ERR_OVERFLOW = 10,                /* OverflowException -> OpResult.Failure */
+    LX_ERR_OUT_OF_MEMORY = 11,           /* hipMalloc failure (device path only) */
+    LX_ERR_HIP = 12,                     /* any other HIP runtime error (device path only) */
+    LX_ERR_NOT_INITIALIZED = 13,         /* lx_init not called (device path only) */
+    LX_ERR_BUFFER_TOO_SMALL = 14         /* caller-provided output storage too small */
+};
+
+/*
+ * Device tensor handle: the device twin of DenseTensor<T>
+ * (src/Lokad.Onnx.Tensors/DenseTensor.cs:31-278): row-major contiguous
+ * storage, int64 dims, explicit host/device residency.
+ *   data     : device address (hipMalloc'd by lx_tensor_alloc, or wrapped)
+ *   capacity : bytes usable at data
+ *   owns     : 1 if lx_tensor_free must release data
+ * Operator outputs: if Y->data is NULL the operator allocates Y (owns = 1);
+ * otherwise it writes into Y->data (capacity checked, LX_ERR_BUFFER_TOO_SMALL)
+ * and only updates dtype/rank/dims.  Inputs are never modified.
+ */
+typedef struct lx_tensor {
+    int32_t dtype;
+    int32_t rank;
+    int64_t dims[LX_MAX_RANK];
+    void *data;
+    int64_t capacity;
+    int32_t owns;
+    int32_t reserved;
+} lx_tensor;
+
+/*
+ * Broadcast plan (host only, no device call): ITensor.Broadcast shape rule
+ * (src/Lokad.Onnx.Tensors/ITensor.cs:64-120) plus the stride-0 view of
+ * BroadcastedTensor (BroadcastedTensor.cs:24-31), with size-1 axes dropped and
+ * adjacent axes merged where both operands stay contiguous.
+ */
+enum lx_plan_kind {
+    LX_PLAN_EMPTY = 0,    /* zero output elements */
+    LX_PLAN_SAME = 1,     /* both operands dense over the whole output */
+    LX_PLAN_SCALAR_A = 2, /* A is one value, B dense */
+    LX_PLAN_SCALAR_B = 3, /* B is one value, A dense */
+    LX_PLAN_ND = 4        /* general: per-axis strides, 0 on broadcast axes */
+};
+
+typedef struct lx_bcast_plan {
+    int32_t status;                 /* LX_OK or LX_ERR_CANNOT_BROADCAST */
+    int32_t out_rank;               /* rank of the broadcast result */
+    int64_t out_dims[LX_MAX_RANK];  /* shape of the broadcast result */
+    int32_t kind;                   /* lx_plan_kind */
+    int32_t rank;                   /* collapsed rank (>= 1 unless EMPTY) */
+    int64_t dims[LX_MAX_RANK];      /* collapsed dims, outermost first */
+    int64_t a_strides[LX_MAX_RANK]; /* element strides of A per collapsed axis */
+    int64_t b_strides[LX_MAX_RANK]; /* element strides of B per collapsed axis */
+    int64_t numel;                  /* output element count */
+} lx_bcast_plan;
+
+/* ---- library lifecycle ------------------------------------------------- */
+int lx_init(int32_t device);          /* select device, create the library stream and workspace */
+int lx_shutdown(void);
+const char *lx_last_error(void);      /* message of the last failure on this thread (OpResult.Message) */
+const char *lx_version(void);
+int lx_set_stream(void *hip_stream);  /* NULL = the library's own stream */
+void *lx_get_stream(void);
+int lx_synchronize(void);
+
+/* ---- device tensors (residency) ---------------------------------------- */
+int64_t lx_dtype_size(int32_t dtype);
+int lx_tensor_alloc(int32_t dtype, int32_t rank, const int64_t *dims, lx_tensor *out);
+int lx_tensor_wrap(int32_t dtype, int32_t rank, const int64_t *dims, void *device_ptr,
+                   int64_t capacity, lx_tensor *out);
+int lx_tensor_free(lx_tensor *t);
+int lx_tensor_upload(lx_tensor *t, const void *host, int64_t nbytes);         /* host -> device, synchronous */
+int lx_tensor_download(const lx_tensor *t, void *host, int64_t nbytes);       /* device -> host, synchronous */
+/* Reshape / Unsqueeze alias: same storage, new dims (DenseTensor.cs:231-242). */
+int lx_tensor_reshape(const lx_tensor *t, int32_t rank, const int64_t *dims, lx_tensor *out);
+
+/* ---- planner ------------------------------------------------------------ */
+int lx_plan_broadcast(int32_t rank_a, const int64_t *dims_a, int32_t rank_b, const int64_t *dims_b,
+                      lx_bcast_plan *plan);
+
+/* ---- operators: CPUExecutionProvider twins ------------------------------ */
+/* CPUExecutionProvider.Add (CPUExecutionProvider.cs:82-112).  dtypes: UInt8, Int32, Float, Double,
+ * and Int64 (C# unchecked semantics; the reference returns InputTypeNotSupported for Int64). */
+int lx_Add(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
+/* CPUExecutionProvider.Sub (CPUExecutionProvider.cs:114-143). */
+int lx_Sub(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
+/* CPUExecutionProvider.Mul (CPUExecutionProvider.cs:145-175). */
+int lx_Mul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
+/* CPUExecutionProvider.Div (CPUExecutionProvider.cs:177-206).  UInt8, Float, Double, plus Int32 and
+ * Int64 (truncating; x/0 -> LX_ERR_DIVIDE_BY_ZERO, MIN/-1 -> LX_ERR_OVERFLOW). */
+int lx_Div(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
+/* CPUExecutionProvider.Pow (CPUExecutionProvider.cs:208-236).  Float, Double. */
+int lx_Pow(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
+/* CPUExecutionProvider.Sqrt (CPUExecutionProvider.cs:380-396). */
+int lx_Sqrt(const lx_tensor *A, lx_tensor *Y);
+/* CPUExecutionProvider.Erf (CPUExecutionProvider.cs:398-409); MathOps.Erf (MathOps.cs:988-1034). */
+int lx_Erf(const lx_tensor *X, lx_tensor *Y);
+/* CPUExecutionProvider.Cast (CPUExecutionProvider.cs:451-476); ITensor.Cast (ITensor.cs:161-170). */
+int lx_Cast(const lx_tensor *input, int64_t to, lx_tensor *Y);
+/* CPUExecutionProvider.ReduceSum (CPUExecutionProvider.cs:623-640).
+ * axes: n_axes < 0 means the axes input is absent; keepdims / noop: < 0 means attribute absent. */
+int lx_ReduceSum(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims,
+                 int32_t noop_with_empty_axes, lx_tensor *Y);
+/* CPUExecutionProvider.ReduceMean (CPUExecutionProvider.cs:642-660). */
+int lx_ReduceMean(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims,
+                  int32_t noop_with_empty_axes, lx_tensor *Y);
+/* CPUExecutionProvider.ReduceMax (CPUExecutionProvider.cs:662-678). */
+int lx_ReduceMax(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims, lx_tensor *Y);
+/* CPUExecutionProvider.Softmax (CPUExecutionProvider.cs:680-695); has_axis = 0 means default -1. */
+int lx_Softmax(const lx_tensor *input, int32_t axis, int32_t has_axis, lx_tensor *Y);
+
+/* ---- fused subgraphs (one kernel each; every intermediate keeps the float32
+ * rounding of the separate ONNX node it replaces) ------------------------- */
+/* Div(X, sqrt2) -> Erf -> Add 1 -> Mul X -> Mul 0.5 (the ONNX GELU subgraph;
+ * each node runs through CPUExecutionProvider.Div/Erf/Add/Mul in the reference). */
+int lx_GeluErf(const lx_tensor *X, lx_tensor *Y);
+/* ReduceMean(-1) -> Sub -> Pow 2 -> ReduceMean(-1) -> Add eps -> Sqrt -> Div -> Mul gamma -> Add beta. */
+int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_tensor *beta, float eps,
+                           lx_tensor *Y);
+/* Add(S, mask) -> Softmax(axis) with the mask broadcast against S. */
+int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_tensor *Y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LONNX_H */

@@ -1,0 +1,133 @@
+"""ctypes binding of the C ABI in include/lonnx.h (the same cdecl symbols a C#
+[DllImport] table binds).  Loading fails loudly when the HIP library is not
+built: there is no CPU fallback."""
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liblonnx_hip.so")
+MAX_RANK = 8
+
+# TensorElementType codes (Tensor.cs:31-50)
+FLOAT, UINT8, INT8, UINT16, INT16, INT32, INT64, BOOL, DOUBLE, UINT32, UINT64 = 1, 2, 3, 4, 5, 6, 7, 9, 11, 12, 13
+
+# lx_status
+OK = 0
+ERR_MISSING_INPUT = 1
+ERR_WRONG_INPUT_TYPE = 2
+ERR_CANNOT_BROADCAST = 3
+ERR_INPUT_TYPE_NOT_SUPPORTED = 4
+ERR_NOT_SUPPORTED = 5
+ERR_ATTRIBUTE_NOT_SUPPORTED = 6
+ERR_WRONG_INPUT_SHAPE = 7
+ERR_INVALID_ARGUMENT = 8
+ERR_DIVIDE_BY_ZERO = 9
+ERR_OVERFLOW = 10
+ERR_OUT_OF_MEMORY = 11
+ERR_HIP = 12
+ERR_NOT_INITIALIZED = 13
+ERR_BUFFER_TOO_SMALL = 14
+
+PLAN_EMPTY, PLAN_SAME, PLAN_SCALAR_A, PLAN_SCALAR_B, PLAN_ND = 0, 1, 2, 3, 4
+
+
+class LxTensor(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * MAX_RANK),
+        ("data", ctypes.c_void_p),
+        ("capacity", ctypes.c_int64),
+        ("owns", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class LxPlan(ctypes.Structure):
+    _fields_ = [
+        ("status", ctypes.c_int32),
+        ("out_rank", ctypes.c_int32),
+        ("out_dims", ctypes.c_int64 * MAX_RANK),
+        ("kind", ctypes.c_int32),
+        ("rank", ctypes.c_int32),
+        ("dims", ctypes.c_int64 * MAX_RANK),
+        ("a_strides", ctypes.c_int64 * MAX_RANK),
+        ("b_strides", ctypes.c_int64 * MAX_RANK),
+        ("numel", ctypes.c_int64),
+    ]
+
+
+# name -> (restype, argtypes); every symbol declared in include/lonnx.h
+_T = ctypes.POINTER(LxTensor)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_c = ctypes
+SIGNATURES = {
+    "lx_init": (_c.c_int, [_c.c_int32]),
+    "lx_shutdown": (_c.c_int, []),
+    "lx_last_error": (_c.c_char_p, []),
+    "lx_version": (_c.c_char_p, []),
+    "lx_set_stream": (_c.c_int, [_c.c_void_p]),
+    "lx_get_stream": (_c.c_void_p, []),
+    "lx_synchronize": (_c.c_int, []),
+    "lx_dtype_size": (_c.c_int64, [_c.c_int32]),
+    "lx_tensor_alloc": (_c.c_int, [_c.c_int32, _c.c_int32, _i64p, _T]),
+    "lx_tensor_wrap": (_c.c_int, [_c.c_int32, _c.c_int32, _i64p, _c.c_void_p, _c.c_int64, _T]),
+    "lx_tensor_free": (_c.c_int, [_T]),
+    "lx_tensor_upload": (_c.c_int, [_T, _c.c_void_p, _c.c_int64]),
+    "lx_tensor_download": (_c.c_int, [_T, _c.c_void_p, _c.c_int64]),
+    "lx_tensor_reshape": (_c.c_int, [_T, _c.c_int32, _i64p, _T]),
+    "lx_plan_broadcast": (_c.c_int, [_c.c_int32, _i64p, _c.c_int32, _i64p, _c.POINTER(LxPlan)]),
+    "lx_Add": (_c.c_int, [_T, _T, _T]),
+    "lx_Sub": (_c.c_int, [_T, _T, _T]),
+    "lx_Mul": (_c.c_int, [_T, _T, _T]),
+    "lx_Div": (_c.c_int, [_T, _T, _T]),
+    "lx_Pow": (_c.c_int, [_T, _T, _T]),
+    "lx_Sqrt": (_c.c_int, [_T, _T]),
+    "lx_Erf": (_c.c_int, [_T, _T]),
+    "lx_Cast": (_c.c_int, [_T, _c.c_int64, _T]),
+    "lx_ReduceSum": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _c.c_int32, _T]),
+    "lx_ReduceMean": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _c.c_int32, _T]),
+    "lx_ReduceMax": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _T]),
+    "lx_Softmax": (_c.c_int, [_T, _c.c_int32, _c.c_int32, _T]),
+    "lx_GeluErf": (_c.c_int, [_T, _T]),
+    "lx_LayerNormDecomposed": (_c.c_int, [_T, _T, _T, _c.c_float, _T]),
+    "lx_AddSoftmax": (_c.c_int, [_T, _T, _c.c_int32, _T]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises if it is not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"HIP library not built: {LIB_PATH}. Run `python -m onnx_amd.build` (hipcc, gfx950).")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error():
+    m = lib().lx_last_error()
+    return m.decode() if m else ""
+
+
+def dims_array(shape):
+    shape = [int(d) for d in shape]
+    if len(shape) > MAX_RANK:
+        raise ValueError(f"rank {len(shape)} > {MAX_RANK}")
+    return (ctypes.c_int64 * MAX_RANK)(*(shape + [0] * (MAX_RANK - len(shape))))
+
+
+def plan_broadcast(shape_a, shape_b):
+    """Host-only planner call (no device needed)."""
+    p = LxPlan()
+    st = lib().lx_plan_broadcast(len(shape_a), dims_array(shape_a), len(shape_b), dims_array(shape_b),
+                                 ctypes.byref(p))
+    return st, p

@@ -1,0 +1,936 @@
+// lx_api.cpp -- host side of the C ABI declared in include/lonnx.h.
+//
+// Mirrors CPUExecutionProvider (src/Lokad.Onnx.Backend/CPUExecutionProvider.cs):
+// the same validation order, the same dtype tables, the same failure kinds and
+// messages (OpResult.cs:34-60, Node.cs:107-118), then hands the planned work to
+// the gfx950 kernels.  Broadcasting is planned here once (ITensor.Broadcast,
+// ITensor.cs:64-120) and executed by the kernels through stride-0 addressing.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/lonnx.h"
+#include "lx_kernels.h"
+
+using namespace lx;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// state
+// ---------------------------------------------------------------------------
+struct State {
+    bool init = false;
+    int device = -1;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    void *workspace = nullptr;
+    int64_t ws_bytes = 0;
+    ErrFlags *errs = nullptr;      // device
+    ErrFlags *errs_host = nullptr; // pinned host
+};
+State g;
+thread_local std::string g_err;
+
+int set_err(int code, const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory)
+        return set_err(LX_ERR_OUT_OF_MEMORY, "%s: out of device memory", what);
+    return set_err(LX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIPCHECK(call, what)                       \
+    do {                                           \
+        hipError_t e_ = (call);                    \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+#define REQUIRE_INIT()                                                                    \
+    do {                                                                                  \
+        if (!g.init) return set_err(LX_ERR_NOT_INITIALIZED, "lx_init has not been called"); \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// dtype helpers (TensorElementType, Tensor.cs:31-50)
+// ---------------------------------------------------------------------------
+int64_t esize(int dt) {
+    switch (dt) {
+    case LX_FLOAT: case LX_INT32: case LX_UINT32: return 4;
+    case LX_DOUBLE: case LX_INT64: case LX_UINT64: return 8;
+    case LX_UINT8: case LX_INT8: case LX_BOOL: return 1;
+    case LX_UINT16: case LX_INT16: return 2;
+    default: return 0;
+    }
+}
+
+const char *dtype_name(int dt) {
+    switch (dt) {
+    case 1: return "Float"; case 2: return "UInt8"; case 3: return "Int8"; case 4: return "UInt16";
+    case 5: return "Int16"; case 6: return "Int32"; case 7: return "Int64"; case 8: return "String";
+    case 9: return "Bool"; case 10: return "Float16"; case 11: return "Double"; case 12: return "UInt32";
+    case 13: return "UInt64"; case 14: return "Complex64"; case 15: return "Complex128"; case 16: return "BFloat16";
+    default: return "Unknown";
+    }
+}
+
+std::string lower(std::string s) {
+    for (auto &c : s) c = (char)tolower(c);
+    return s;
+}
+
+// ITensor.TensorNameDesc (ITensor.cs:158) with an empty tensor name.
+std::string name_desc(const lx_tensor *t) {
+    std::string s = ":" + lower(dtype_name(t->dtype)) + ":";
+    for (int i = 0; i < t->rank; i++) {
+        if (i) s += "x";
+        s += std::to_string(t->dims[i]);
+    }
+    return s;
+}
+
+// Tensor.PrintShape (Tensor.cs:1724)
+std::string print_shape(const lx_tensor *t) {
+    std::string s = "[";
+    for (int i = 0; i < t->rank; i++) {
+        if (i) s += ",";
+        s += std::to_string(t->dims[i]);
+    }
+    return s + "]";
+}
+
+int64_t numel_of(int rank, const int64_t *dims) {
+    int64_t n = 1;
+    for (int i = 0; i < rank; i++) n *= dims[i];
+    return n;
+}
+
+int64_t numel(const lx_tensor *t) { return numel_of(t->rank, t->dims); }
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// structural validity of a caller-provided tensor
+int check_tensor(const lx_tensor *t, const char *name) {
+    if (t->rank < 0 || t->rank > LX_MAX_RANK)
+        return set_err(LX_ERR_NOT_SUPPORTED, "Tensor %s has rank %d; at most %d axes are supported.", name, t->rank,
+                       LX_MAX_RANK);
+    for (int i = 0; i < t->rank; i++)
+        if (t->dims[i] < 0) return set_err(LX_ERR_INVALID_ARGUMENT, "Tensor %s has a negative dimension.", name);
+    int64_t es = esize(t->dtype);
+    int64_t bytes = numel(t) * (es ? es : 1);
+    if (bytes > 0 && (t->data == nullptr || t->capacity < bytes))
+        return set_err(LX_ERR_INVALID_ARGUMENT, "Tensor %s has no device storage for its %lld bytes.", name,
+                       (long long)bytes);
+    return LX_OK;
+}
+
+// ---- failure messages (OpResult.cs) ------------------------------------------------
+int missing_input(const char *op, const char *name) {
+    return set_err(LX_ERR_MISSING_INPUT, "The required input parameter %s is missing or null.", name);
+}
+int wrong_type_same(const char *name) {
+    return set_err(LX_ERR_WRONG_INPUT_TYPE,
+                   "The input tensor  for parameter %s has the wrong type: Input tensors must be of the same type..",
+                   name);
+}
+int type_not_supported(const char *op, const char *name, const lx_tensor *t) {
+    return set_err(LX_ERR_INPUT_TYPE_NOT_SUPPORTED,
+                   "The type %s for input parameter %s is not supported for operation %s. ", dtype_name(t->dtype), name,
+                   op);
+}
+int not_supported(const char *op) {
+    return set_err(LX_ERR_NOT_SUPPORTED, "The operation %s is not supported by the backend.", op);
+}
+int cannot_broadcast(const lx_tensor *a, const lx_tensor *b) {
+    return set_err(LX_ERR_CANNOT_BROADCAST, "The tensors %s and %s are not compatible for broadcasting.",
+                   name_desc(a).c_str(), name_desc(b).c_str());
+}
+// .NET ArgumentException(message, paramName).Message as the reference raises it
+int argument_error(const char *message, const char *param) {
+    return set_err(LX_ERR_INVALID_ARGUMENT, "%s (Parameter '%s')", message, param);
+}
+
+// ---------------------------------------------------------------------------
+// output preparation: allocate (Y->data == NULL) or validate caller storage
+// ---------------------------------------------------------------------------
+int prepare_output(lx_tensor *Y, int dtype, int rank, const int64_t *dims) {
+    if (!Y) return set_err(LX_ERR_INVALID_ARGUMENT, "The output tensor handle is null.");
+    int64_t bytes = numel_of(rank, dims) * esize(dtype);
+    if (Y->data) {
+        if (Y->capacity < bytes)
+            return set_err(LX_ERR_BUFFER_TOO_SMALL, "Output storage holds %lld bytes, %lld needed.",
+                           (long long)Y->capacity, (long long)bytes);
+    } else {
+        void *p = nullptr;
+        HIPCHECK(hipMalloc(&p, bytes > 0 ? bytes : 16), "hipMalloc(output)");
+        Y->data = p;
+        Y->capacity = bytes;
+        Y->owns = 1;
+    }
+    Y->dtype = dtype;
+    Y->rank = rank;
+    for (int i = 0; i < LX_MAX_RANK; i++) Y->dims[i] = i < rank ? dims[i] : 0;
+    return LX_OK;
+}
+
+int ensure_workspace(int64_t bytes) {
+    if (bytes <= g.ws_bytes) return LX_OK;
+    HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    if (g.workspace) (void)hipFree(g.workspace);
+    g.workspace = nullptr;
+    g.ws_bytes = 0;
+    int64_t want = std::max<int64_t>(bytes, 1 << 20);
+    HIPCHECK(hipMalloc(&g.workspace, want), "hipMalloc(workspace)");
+    g.ws_bytes = want;
+    return LX_OK;
+}
+
+// reads back the device error record (synchronises the stream)
+int read_errs(ErrFlags *out) {
+    HIPCHECK(hipMemcpyAsync(g.errs_host, g.errs, sizeof(ErrFlags), hipMemcpyDeviceToHost, g.stream),
+             "hipMemcpyAsync(errors)");
+    HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    *out = *g.errs_host;
+    return LX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// broadcast planner
+// ---------------------------------------------------------------------------
+int plan(int ra, const int64_t *da, int rb, const int64_t *db, lx_bcast_plan *p) {
+    memset(p, 0, sizeof *p);
+    if (ra < 0 || rb < 0 || ra > LX_MAX_RANK || rb > LX_MAX_RANK) {
+        p->status = LX_ERR_NOT_SUPPORTED;
+        return set_err(LX_ERR_NOT_SUPPORTED, "At most %d axes are supported.", LX_MAX_RANK);
+    }
+    int64_t out[LX_MAX_RANK];
+    int r;
+    // ITensor.Broadcast shape rule (ITensor.cs:64-120)
+    if (ra == 0 && rb != 0) {
+        r = rb;
+        for (int i = 0; i < r; i++) out[i] = db[i];
+    } else if (rb == 0 && ra != 0) {
+        r = ra;
+        for (int i = 0; i < r; i++) out[i] = da[i];
+    } else {
+        r = std::max(ra, rb);
+        for (int i = 0; i < r; i++) {
+            int ia = i - r + ra, ib = i - r + rb;
+            if (i < r - ra) out[i] = db[ib];
+            else if (i < r - rb) out[i] = da[ia];
+            else if (da[ia] == db[ib]) out[i] = da[ia];
+            else if (da[ia] == 1) out[i] = db[ib];
+            else if (db[ib] == 1) out[i] = da[ia];
+            else {
+                p->status = LX_ERR_CANNOT_BROADCAST;
+                return LX_ERR_CANNOT_BROADCAST;
+            }
+        }
+    }
+    p->out_rank = r;
+    for (int i = 0; i < r; i++) p->out_dims[i] = out[i];
+    p->numel = numel_of(r, out);
+    if (p->numel == 0) {
+        p->kind = LX_PLAN_EMPTY;
+        return LX_OK;
+    }
+    // per-operand strides in the output frame (0 on broadcast or missing axes)
+    int64_t sa[LX_MAX_RANK], sb[LX_MAX_RANK];
+    auto fill = [&](int ro, const int64_t *dd, int64_t *s) {
+        int64_t st = 1;
+        for (int i = r - 1; i >= 0; i--) {
+            int k = i - (r - ro);
+            if (k < 0) { s[i] = 0; continue; }
+            s[i] = (dd[k] == 1 && out[i] != 1) ? 0 : st;
+            st *= dd[k];
+        }
+    };
+    fill(ra, da, sa);
+    fill(rb, db, sb);
+    // drop size-1 axes, merge adjacent axes that stay contiguous for both operands
+    int64_t cd[LX_MAX_RANK], ca[LX_MAX_RANK], cb[LX_MAX_RANK];
+    int n = 0;
+    for (int i = r - 1; i >= 0; i--) {  // inner to outer
+        if (out[i] == 1) continue;
+        if (n > 0 && sa[i] == ca[n - 1] * cd[n - 1] && sb[i] == cb[n - 1] * cd[n - 1]) {
+            cd[n - 1] *= out[i];
+            continue;
+        }
+        cd[n] = out[i];
+        ca[n] = sa[i];
+        cb[n] = sb[i];
+        n++;
+    }
+    if (n == 0) {  // single element
+        cd[0] = 1;
+        ca[0] = 1;
+        cb[0] = 1;
+        n = 1;
+    }
+    p->rank = n;
+    for (int i = 0; i < n; i++) {  // store outermost first
+        p->dims[i] = cd[n - 1 - i];
+        p->a_strides[i] = ca[n - 1 - i];
+        p->b_strides[i] = cb[n - 1 - i];
+    }
+    if (n == 1) {
+        if (p->a_strides[0] == 1 && p->b_strides[0] == 1) p->kind = LX_PLAN_SAME;
+        else if (p->a_strides[0] == 0) p->kind = LX_PLAN_SCALAR_A;
+        else p->kind = LX_PLAN_SCALAR_B;
+        if (p->dims[0] == 1) p->kind = LX_PLAN_SAME;
+    } else {
+        p->kind = LX_PLAN_ND;
+    }
+    p->status = LX_OK;
+    return LX_OK;
+}
+
+// NdLayout over the outer axes of a plan (innermost outer axis first)
+void nd_layout(const lx_bcast_plan &p, int vec, NdLayout &L, BinArgs *big) {
+    memset(&L, 0, sizeof L);
+    const int R = p.rank;
+    L.nouter = R - 1;
+    for (int d = 0; d < R - 1; d++) {
+        int ax = R - 2 - d;
+        L.odiv[d] = make_fastdiv((uint32_t)std::min<int64_t>(p.dims[ax], 0x7fffffff));
+        L.a_str[d] = p.a_strides[ax];
+        L.b_str[d] = p.b_strides[ax];
+        if (big) big->nd_osize[d] = p.dims[ax];
+    }
+    L.inner = p.dims[R - 1];
+    int64_t inner_v = p.dims[R - 1] / vec;
+    L.inner_v = make_fastdiv((uint32_t)std::min<int64_t>(inner_v, 0x7fffffff));
+    if (big) big->nd_inner_vn = inner_v;
+}
+
+// ---------------------------------------------------------------------------
+// binary operators (CPUExecutionProvider.cs:82-236)
+// ---------------------------------------------------------------------------
+bool binary_dtype_ok(int op, int dt) {
+    switch (op) {
+    case kAdd: case kSub: case kMul: case kDiv:
+        return dt == LX_UINT8 || dt == LX_INT32 || dt == LX_INT64 || dt == LX_FLOAT || dt == LX_DOUBLE;
+    case kPow: return dt == LX_FLOAT || dt == LX_DOUBLE;
+    default: return false;
+    }
+}
+
+const char *binop_name(int op) {
+    switch (op) {
+    case kAdd: return "Add"; case kSub: return "Sub"; case kMul: return "Mul"; case kDiv: return "Div";
+    case kPow: return "Pow"; default: return "?";
+    }
+}
+
+int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
+    REQUIRE_INIT();
+    const char *opn = binop_name(op);
+    if (!A) return missing_input(opn, "A");
+    if (!B) return missing_input(opn, "B");
+    if (A->dtype != B->dtype) return wrong_type_same("B");
+    int st;
+    if ((st = check_tensor(A, "A")) || (st = check_tensor(B, "B"))) return st;
+    lx_bcast_plan p;
+    st = plan(A->rank, A->dims, B->rank, B->dims, &p);
+    if (st == LX_ERR_CANNOT_BROADCAST) return cannot_broadcast(A, B);
+    if (st) return st;
+    if (!binary_dtype_ok(op, A->dtype)) return type_not_supported(opn, "A", A);
+    if ((st = prepare_output(Y, A->dtype, p.out_rank, p.out_dims))) return st;
+    if (p.kind == LX_PLAN_EMPTY) return LX_OK;
+
+    BinArgs args;
+    memset(&args, 0, sizeof args);
+    args.op = op;
+    args.dtype = A->dtype;
+    args.a = A->data;
+    args.b = B->data;
+    args.y = Y->data;
+    args.n = p.numel;
+    const int64_t es = esize(A->dtype);
+    const int64_t V = 16 / es;
+    const bool al = aligned16(A->data) && aligned16(B->data) && aligned16(Y->data);
+    switch (p.kind) {
+    case LX_PLAN_SAME: args.layout = kSame; args.vec = al ? (int)V : 1; break;
+    case LX_PLAN_SCALAR_A: args.layout = kScalarA; args.vec = aligned16(B->data) && aligned16(Y->data) ? (int)V : 1; break;
+    case LX_PLAN_SCALAR_B: args.layout = kScalarB; args.vec = aligned16(A->data) && aligned16(Y->data) ? (int)V : 1; break;
+    default: {
+        args.layout = kNd;
+        const int64_t inner = p.dims[p.rank - 1];
+        args.a_inner = p.a_strides[p.rank - 1] != 0;
+        args.b_inner = p.b_strides[p.rank - 1] != 0;
+        args.vec = (al && inner % V == 0) ? (int)V : 1;
+        nd_layout(p, args.vec, args.nd, &args);
+        break;
+    }
+    }
+    const bool int_div = op == kDiv && (A->dtype == LX_INT32 || A->dtype == LX_INT64 || A->dtype == LX_UINT8);
+    if (int_div) HIPCHECK(launch_reset_errs(g.errs, g.stream), "reset error flags");
+    HIPCHECK(launch_binary(args, g.errs, g.stream), opn);
+    if (int_div) {
+        ErrFlags e;
+        if ((st = read_errs(&e))) return st;
+        if (e.first_dbz != ~0ull || e.first_ovf != ~0ull) {
+            if (e.first_dbz <= e.first_ovf)
+                return set_err(LX_ERR_DIVIDE_BY_ZERO, "Attempted to divide by zero.");
+            return set_err(LX_ERR_OVERFLOW, "Arithmetic operation resulted in an overflow.");
+        }
+    }
+    return LX_OK;
+}
+
+int run_unary(const char *opn, int op, const lx_tensor *X, const char *xname, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!X) return missing_input(opn, xname);
+    int st;
+    if ((st = check_tensor(X, xname))) return st;
+    if (X->dtype != LX_FLOAT && X->dtype != LX_DOUBLE) return type_not_supported(opn, xname, X);
+    if ((st = prepare_output(Y, X->dtype, X->rank, X->dims))) return st;
+    const int64_t n = numel(X);
+    const int vec = aligned16(X->data) && aligned16(Y->data) ? 2 : 1;
+    HIPCHECK(launch_unary(op, X->dtype, X->data, Y->data, n, vec, g.stream), opn);
+    return LX_OK;
+}
+
+// ---------------------------------------------------------------------------
+// reductions (CPUExecutionProvider.cs:623-678, TensorOps.cs:1561-1891)
+// ---------------------------------------------------------------------------
+int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims,
+               lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!X) return missing_input(opn, "data");
+    int st;
+    if ((st = check_tensor(X, "data"))) return st;
+    const int dt = X->dtype;
+    bool ok = (op == kMax) ? (dt == LX_FLOAT || dt == LX_DOUBLE)
+                           : (dt == LX_FLOAT || dt == LX_DOUBLE || dt == LX_INT32 || dt == LX_INT64);
+    if (!ok) return not_supported(opn);
+    const int rank = X->rank;
+    // axes validation as TensorOps (1566-1571): count, range, repeats, normalisation
+    int ax[LX_MAX_RANK];
+    int nax = 0;
+    if (n_axes > 0) {
+        if (!axes) return missing_input(opn, "axes");
+        if (n_axes > rank) return argument_error("axes", "The number of axes specified must be less than the tensor rank.");
+        for (int i = 0; i < n_axes; i++) {
+            if (axes[i] >= rank) return argument_error("axes", "Each axis specified must be less than the rank of the tensor.");
+            if (axes[i] < INT32_MIN || axes[i] > INT32_MAX)
+                return set_err(LX_ERR_OVERFLOW, "Value was either too large or too small for an Int32.");
+            for (int j = 0; j < i; j++)
+                if (axes[j] == axes[i]) return argument_error("axes", "axes contains a repeated dimension.");
+        }
+        for (int i = 0; i < n_axes; i++) {
+            int64_t a = axes[i] < 0 ? axes[i] + rank : axes[i];
+            if (a < 0) return argument_error("axes", "Each axis specified must be less than the rank of the tensor.");
+            for (int j = 0; j < i; j++)
+                if (ax[j] == a) return argument_error("axes", "axes contains a repeated dimension.");
+            ax[nax++] = (int)a;
+        }
+    } else {
+        for (int i = 0; i < rank; i++) ax[nax++] = i;
+    }
+    bool red[LX_MAX_RANK] = {false};
+    for (int i = 0; i < nax; i++) red[ax[i]] = true;
+    const bool keep = keepdims < 0 ? true : keepdims != 0;
+    int64_t odims[LX_MAX_RANK];
+    int orank = 0;
+    int64_t R = 1;
+    for (int d = 0; d < rank; d++) {
+        if (red[d]) {
+            R *= X->dims[d];
+            if (keep) odims[orank++] = 1;
+        } else {
+            odims[orank++] = X->dims[d];
+        }
+    }
+    if ((st = prepare_output(Y, dt, orank, odims))) return st;
+    const int64_t nout = numel_of(orank, odims);
+    if (nout == 0) return LX_OK;
+    const int64_t es = esize(dt);
+    if (R == 0) {
+        // folds over nothing: 0 (sum, max seed), mean float = 0/0
+        uint64_t bits = 0;
+        if (op == kMean && dt == LX_FLOAT) {
+            float nanv = __builtin_nanf("");
+            uint32_t u;
+            memcpy(&u, &nanv, 4);
+            bits = u;
+        }
+        HIPCHECK(launch_fill(Y->data, nout, (int)es, bits, g.stream), "fill");
+        return LX_OK;
+    }
+    // collapse into groups of consecutive kept / reduced axes, size-1 axes dropped
+    struct Grp { int64_t size; bool red; };
+    std::vector<Grp> grps;
+    for (int d = 0; d < rank; d++) {
+        if (X->dims[d] == 1) continue;
+        if (!grps.empty() && grps.back().red == red[d]) grps.back().size *= X->dims[d];
+        else grps.push_back({X->dims[d], red[d]});
+    }
+    int nred = 0;
+    for (auto &gp : grps) nred += gp.red;
+    if (nred == 0) {  // reduced axes all of size 1: each output folds one element
+        grps.clear();
+        grps.push_back({1, true});
+        grps.push_back({nout, false});
+        nred = 1;
+    }
+    // passes: reduce the innermost reduced group first
+    const void *src = X->data;
+    void *tmp[2] = {nullptr, nullptr};
+    int pass = 0;
+    int result = LX_OK;
+    while (nred > 0) {
+        int gi = -1;
+        for (int i = (int)grps.size() - 1; i >= 0; i--)
+            if (grps[i].red) { gi = i; break; }
+        int64_t outer = 1, inner = 1;
+        for (int i = 0; i < gi; i++) outer *= grps[i].size;
+        for (int i = gi + 1; i < (int)grps.size(); i++) inner *= grps[i].size;
+        const int64_t r = grps[gi].size;
+        const bool last = nred == 1;
+        void *dst;
+        if (last) dst = Y->data;
+        else {
+            int slot = pass & 1;
+            if (tmp[slot]) (void)hipFreeAsync(tmp[slot], g.stream);
+            hipError_t e = hipMallocAsync(&tmp[slot], std::max<int64_t>(outer * inner * es, 16), g.stream);
+            if (e != hipSuccess) { result = hip_fail(e, "hipMallocAsync(temporary)"); break; }
+            dst = tmp[slot];
+        }
+        ReduceArgs ra;
+        memset(&ra, 0, sizeof ra);
+        ra.op = op;
+        ra.dtype = dt;
+        ra.x = src;
+        ra.y = dst;
+        ra.outer = outer;
+        ra.r = r;
+        ra.inner = inner;
+        ra.pre_div = pass == 0;
+        ra.post_div = last;
+        ra.r_total = R;
+        const int64_t V = 16 / es;
+        const bool al = aligned16(src);
+        ra.vec = (al && ((inner == 1 && r % V == 0) || (inner > 1 && inner % V == 0))) ? (int)V : 1;
+        int64_t wsb = reduce_workspace_bytes(dt, outer, r, inner);
+        if ((result = ensure_workspace(wsb))) break;
+        ra.workspace = g.workspace;
+        ra.ws_bytes = g.ws_bytes;
+        hipError_t e = launch_reduce(ra, g.stream);
+        if (e != hipSuccess) { result = hip_fail(e, opn); break; }
+        src = dst;
+        grps.erase(grps.begin() + gi);
+        // merge neighbours that became adjacent kept groups
+        std::vector<Grp> m;
+        for (auto &gp : grps) {
+            if (!m.empty() && m.back().red == gp.red) m.back().size *= gp.size;
+            else m.push_back(gp);
+        }
+        grps.swap(m);
+        nred--;
+        pass++;
+    }
+    for (void *t : tmp)
+        if (t) (void)hipFreeAsync(t, g.stream);
+    return result;
+}
+
+int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
+                const char *opn);
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+const char *lx_last_error(void) { return g_err.c_str(); }
+const char *lx_version(void) { return "lonnx-mi355x 0.1 (gfx950)"; }
+int64_t lx_dtype_size(int32_t dtype) { return esize(dtype); }
+
+int lx_init(int32_t device) {
+    if (g.init) {
+        if (device == g.device) return LX_OK;
+        return set_err(LX_ERR_INVALID_ARGUMENT, "The library is already initialised on device %d.", g.device);
+    }
+    int count = 0;
+    HIPCHECK(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count)
+        return set_err(LX_ERR_INVALID_ARGUMENT, "Device %d does not exist (%d devices).", device, count);
+    HIPCHECK(hipSetDevice(device), "hipSetDevice");
+    HIPCHECK(hipStreamCreateWithFlags(&g.own_stream, hipStreamNonBlocking), "hipStreamCreate");
+    g.stream = g.own_stream;
+    HIPCHECK(hipMalloc(&g.errs, sizeof(ErrFlags)), "hipMalloc(errors)");
+    HIPCHECK(hipHostMalloc((void **)&g.errs_host, sizeof(ErrFlags), hipHostMallocDefault), "hipHostMalloc");
+    g.device = device;
+    g.init = true;
+    int st = ensure_workspace(1 << 20);
+    if (st) return st;
+    return LX_OK;
+}
+
+int lx_shutdown(void) {
+    if (!g.init) return LX_OK;
+    (void)hipDeviceSynchronize();
+    if (g.workspace) (void)hipFree(g.workspace);
+    if (g.errs) (void)hipFree(g.errs);
+    if (g.errs_host) (void)hipHostFree(g.errs_host);
+    if (g.own_stream) (void)hipStreamDestroy(g.own_stream);
+    g = State();
+    return LX_OK;
+}
+
+int lx_set_stream(void *s) {
+    REQUIRE_INIT();
+    g.stream = s ? (hipStream_t)s : g.own_stream;
+    return LX_OK;
+}
+
+void *lx_get_stream(void) { return (void *)g.stream; }
+
+int lx_synchronize(void) {
+    REQUIRE_INIT();
+    HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    return LX_OK;
+}
+
+int lx_tensor_alloc(int32_t dtype, int32_t rank, const int64_t *dims, lx_tensor *out) {
+    REQUIRE_INIT();
+    if (!out) return set_err(LX_ERR_INVALID_ARGUMENT, "out is null");
+    if (!esize(dtype)) return set_err(LX_ERR_NOT_SUPPORTED, "Element type %s is not supported.", dtype_name(dtype));
+    if (rank < 0 || rank > LX_MAX_RANK) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d axes are supported.", LX_MAX_RANK);
+    if (rank > 0 && !dims) return set_err(LX_ERR_INVALID_ARGUMENT, "dims is null");
+    for (int i = 0; i < rank; i++)
+        if (dims[i] < 0) return set_err(LX_ERR_INVALID_ARGUMENT, "negative dimension");
+    memset(out, 0, sizeof *out);
+    return prepare_output(out, dtype, rank, dims);
+}
+
+int lx_tensor_wrap(int32_t dtype, int32_t rank, const int64_t *dims, void *ptr, int64_t capacity, lx_tensor *out) {
+    if (!out) return set_err(LX_ERR_INVALID_ARGUMENT, "out is null");
+    if (!esize(dtype)) return set_err(LX_ERR_NOT_SUPPORTED, "Element type %s is not supported.", dtype_name(dtype));
+    if (rank < 0 || rank > LX_MAX_RANK) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d axes are supported.", LX_MAX_RANK);
+    memset(out, 0, sizeof *out);
+    out->dtype = dtype;
+    out->rank = rank;
+    for (int i = 0; i < rank; i++) out->dims[i] = dims[i];
+    out->data = ptr;
+    out->capacity = capacity;
+    out->owns = 0;
+    return check_tensor(out, "wrapped");
+}
+
+int lx_tensor_free(lx_tensor *t) {
+    if (!t) return LX_OK;
+    if (t->owns && t->data) {
+        if (g.init) (void)hipStreamSynchronize(g.stream);
+        HIPCHECK(hipFree(t->data), "hipFree");
+    }
+    t->data = nullptr;
+    t->capacity = 0;
+    t->owns = 0;
+    return LX_OK;
+}
+
+int lx_tensor_upload(lx_tensor *t, const void *host, int64_t nbytes) {
+    REQUIRE_INIT();
+    if (!t || (!host && nbytes > 0)) return set_err(LX_ERR_INVALID_ARGUMENT, "null argument");
+    if (nbytes > t->capacity) return set_err(LX_ERR_BUFFER_TOO_SMALL, "upload larger than the tensor storage");
+    if (nbytes == 0) return LX_OK;
+    HIPCHECK(hipMemcpyAsync(t->data, host, nbytes, hipMemcpyHostToDevice, g.stream), "hipMemcpyAsync(H2D)");
+    HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    return LX_OK;
+}
+
+int lx_tensor_download(const lx_tensor *t, void *host, int64_t nbytes) {
+    REQUIRE_INIT();
+    if (!t || (!host && nbytes > 0)) return set_err(LX_ERR_INVALID_ARGUMENT, "null argument");
+    if (nbytes > t->capacity) return set_err(LX_ERR_BUFFER_TOO_SMALL, "download larger than the tensor storage");
+    if (nbytes == 0) return LX_OK;
+    HIPCHECK(hipMemcpyAsync(host, t->data, nbytes, hipMemcpyDeviceToHost, g.stream), "hipMemcpyAsync(D2H)");
+    HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    return LX_OK;
+}
+
+int lx_tensor_reshape(const lx_tensor *t, int32_t rank, const int64_t *dims, lx_tensor *out) {
+    if (!t || !out) return set_err(LX_ERR_INVALID_ARGUMENT, "null argument");
+    if (rank < 0 || rank > LX_MAX_RANK) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d axes are supported.", LX_MAX_RANK);
+    if (numel_of(rank, dims) != numel(t))
+        return set_err(LX_ERR_INVALID_ARGUMENT,
+                       "Cannot reshape array due to mismatch in lengths, currently %lld would become %lld. "
+                       "(Parameter 'dimensions')",
+                       (long long)numel(t), (long long)numel_of(rank, dims));
+    lx_tensor o = *t;
+    o.rank = rank;
+    for (int i = 0; i < LX_MAX_RANK; i++) o.dims[i] = i < rank ? dims[i] : 0;
+    o.owns = 0;  // alias: the original keeps ownership
+    *out = o;
+    return LX_OK;
+}
+
+int lx_plan_broadcast(int32_t ra, const int64_t *da, int32_t rb, const int64_t *db, lx_bcast_plan *p) {
+    if (!p) return set_err(LX_ERR_INVALID_ARGUMENT, "plan is null");
+    int st = plan(ra, da, rb, db, p);
+    if (st == LX_ERR_CANNOT_BROADCAST) set_err(st, "The shapes are not compatible for broadcasting.");
+    return st;
+}
+
+int lx_Add(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kAdd, A, B, Y); }
+int lx_Sub(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kSub, A, B, Y); }
+int lx_Mul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kMul, A, B, Y); }
+int lx_Div(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kDiv, A, B, Y); }
+int lx_Pow(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kPow, A, B, Y); }
+int lx_Sqrt(const lx_tensor *A, lx_tensor *Y) { return run_unary("Sqrt", kSqrt, A, "A", Y); }
+int lx_Erf(const lx_tensor *X, lx_tensor *Y) { return run_unary("Erf", kErf, X, "X", Y); }
+
+int lx_Cast(const lx_tensor *X, int64_t to, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!X) return missing_input("Cast", "input");
+    int st;
+    if ((st = check_tensor(X, "input"))) return st;
+    const int dst = (int)to;
+    if (to != dst || !esize(dst))  // Float16 / BFloat16 / Complex / String targets (CPUExecutionProvider.cs:470-473)
+        return set_err(LX_ERR_ATTRIBUTE_NOT_SUPPORTED,
+                       "The attribute to with value %lld is not supported for operation Cast. ", (long long)to);
+    if (!esize(X->dtype))
+        return set_err(LX_ERR_INPUT_TYPE_NOT_SUPPORTED, "Object must implement IConvertible.");
+    if ((st = prepare_output(Y, dst, X->rank, X->dims))) return st;
+    const int64_t n = numel(X);
+    if (n == 0) return LX_OK;
+    const int src = X->dtype;
+    // only conversions into an integer type can raise OverflowException
+    const bool can_overflow = dst != LX_FLOAT && dst != LX_DOUBLE && dst != LX_BOOL && src != dst;
+    const int vec = aligned16(X->data) && aligned16(Y->data) ? 2 : 1;
+    if (can_overflow) HIPCHECK(launch_reset_errs(g.errs, g.stream), "reset error flags");
+    HIPCHECK(launch_cast(src, dst, X->data, Y->data, n, vec, g.errs, g.stream), "Cast");
+    if (can_overflow) {
+        ErrFlags e;
+        if ((st = read_errs(&e))) return st;
+        if (e.first_ovf != ~0ull) {
+            const char *what = "an Int32";
+            switch (dst) {
+            case LX_UINT8: what = "an unsigned byte"; break;
+            case LX_INT8: what = "a signed byte"; break;
+            case LX_INT16: what = "an Int16"; break;
+            case LX_UINT16: what = "a UInt16"; break;
+            case LX_UINT32: what = "a UInt32"; break;
+            case LX_INT64: what = "an Int64"; break;
+            case LX_UINT64: what = "a UInt64"; break;
+            }
+            return set_err(LX_ERR_OVERFLOW, "Value was either too large or too small for %s.", what);
+        }
+    }
+    return LX_OK;
+}
+
+int lx_ReduceSum(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
+                 lx_tensor *Y) {
+    (void)noop;  // read but unused by TensorOps.ReduceSum (TensorOps.cs:1615)
+    return run_reduce("ReduceSum", kSum, X, axes, n_axes, keepdims, Y);
+}
+
+int lx_ReduceMean(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
+                  lx_tensor *Y) {
+    (void)noop;
+    return run_reduce("ReduceMean", kMean, X, axes, n_axes, keepdims, Y);
+}
+
+int lx_ReduceMax(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, lx_tensor *Y) {
+    return run_reduce("ReduceMax", kMax, X, axes, n_axes, keepdims, Y);
+}
+
+int lx_Softmax(const lx_tensor *X, int32_t axis, int32_t has_axis, lx_tensor *Y) {
+    return run_softmax(X, nullptr, axis, has_axis, Y, "Softmax");
+}
+
+int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!S) return missing_input("Add", "A");
+    if (!mask) return missing_input("Add", "B");
+    return run_softmax(S, mask, axis, 1, Y, "Softmax");
+}
+
+int lx_GeluErf(const lx_tensor *X, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!X) return missing_input("Div", "A");
+    int st;
+    if ((st = check_tensor(X, "A"))) return st;
+    if (X->dtype != LX_FLOAT) {
+        // node by node for other element types
+        if (X->dtype != LX_DOUBLE) return type_not_supported("Erf", "X", X);
+        double c[3] = {1.4142135623730951, 1.0, 0.5};
+        lx_tensor k[3], t1{}, t2{}, t3{}, t4{};
+        for (int i = 0; i < 3; i++) {
+            if ((st = lx_tensor_alloc(LX_DOUBLE, 0, nullptr, &k[i]))) return st;
+            if ((st = lx_tensor_upload(&k[i], &c[i], 8))) return st;
+        }
+        st = lx_Div(X, &k[0], &t1);
+        if (!st) st = lx_Erf(&t1, &t2);
+        if (!st) st = lx_Add(&t2, &k[1], &t3);
+        if (!st) st = lx_Mul(X, &t3, &t4);
+        if (!st) st = lx_Mul(&t4, &k[2], Y);
+        for (lx_tensor *t : {&k[0], &k[1], &k[2], &t1, &t2, &t3, &t4}) lx_tensor_free(t);
+        return st;
+    }
+    if ((st = prepare_output(Y, LX_FLOAT, X->rank, X->dims))) return st;
+    const int vec = aligned16(X->data) && aligned16(Y->data) ? 4 : 1;
+    HIPCHECK(launch_gelu_erf((const float *)X->data, (float *)Y->data, numel(X), vec, g.stream), "GeluErf");
+    return LX_OK;
+}
+
+int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_tensor *beta, float eps,
+                           lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!X) return missing_input("ReduceMean", "data");
+    if (!gamma) return missing_input("Mul", "B");
+    if (!beta) return missing_input("Add", "B");
+    int st;
+    if ((st = check_tensor(X, "data")) || (st = check_tensor(gamma, "gamma")) || (st = check_tensor(beta, "beta")))
+        return st;
+    const int64_t r = X->rank > 0 ? X->dims[X->rank - 1] : 0;
+    const bool fused = X->dtype == LX_FLOAT && gamma->dtype == LX_FLOAT && beta->dtype == LX_FLOAT && X->rank >= 1 &&
+                       numel(gamma) == r && numel(beta) == r && gamma->rank >= 1 && beta->rank >= 1 &&
+                       gamma->rank <= X->rank && beta->rank <= X->rank && layernorm_supported(r) &&
+                       aligned16(X->data) && aligned16(gamma->data) && aligned16(beta->data);
+    if (fused) {
+        if ((st = prepare_output(Y, LX_FLOAT, X->rank, X->dims))) return st;
+        if (!aligned16(Y->data)) return set_err(LX_ERR_INVALID_ARGUMENT, "output storage must be 16-byte aligned");
+        HIPCHECK(launch_layernorm((const float *)X->data, (const float *)gamma->data, (const float *)beta->data, eps,
+                                  (float *)Y->data, numel(X) / (r ? r : 1), r, g.stream),
+                 "LayerNorm");
+        return LX_OK;
+    }
+    // node by node (same numbers, more passes)
+    if (X->dtype != LX_FLOAT) return type_not_supported("ReduceMean", "data", X);
+    const int64_t ax = -1;
+    float two = 2.0f;
+    lx_tensor mean{}, d{}, p{}, var{}, ve{}, sd{}, nrm{}, m{}, k2{}, ke{};
+    if ((st = lx_tensor_alloc(LX_FLOAT, 0, nullptr, &k2)) || (st = lx_tensor_upload(&k2, &two, 4))) return st;
+    if ((st = lx_tensor_alloc(LX_FLOAT, 0, nullptr, &ke)) || (st = lx_tensor_upload(&ke, &eps, 4))) return st;
+    st = lx_ReduceMean(X, &ax, 1, 1, -1, &mean);
+    if (!st) st = lx_Sub(X, &mean, &d);
+    if (!st) st = lx_Pow(&d, &k2, &p);
+    if (!st) st = lx_ReduceMean(&p, &ax, 1, 1, -1, &var);
+    if (!st) st = lx_Add(&var, &ke, &ve);
+    if (!st) st = lx_Sqrt(&ve, &sd);
+    if (!st) st = lx_Div(&d, &sd, &nrm);
+    if (!st) st = lx_Mul(&nrm, gamma, &m);
+    if (!st) st = lx_Add(&m, beta, Y);
+    for (lx_tensor *t : {&mean, &d, &p, &var, &ve, &sd, &nrm, &m, &k2, &ke}) lx_tensor_free(t);
+    return st;
+}
+
+}  // extern "C"
+
+namespace {
+
+int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
+                const char *opn) {
+    REQUIRE_INIT();
+    if (!X) return missing_input(opn, "input");
+    int st;
+    if ((st = check_tensor(X, "input"))) return st;
+    if (mask) {
+        if ((st = check_tensor(mask, "mask"))) return st;
+        if (mask->dtype != X->dtype) return wrong_type_same("B");
+    }
+    const int rank = X->rank;
+    int ax = has_axis ? axis : -1;
+    if (ax < 0) ax += rank;
+    if (ax < 0 || ax >= rank)
+        return argument_error("axis", "The specified axis must be less than the rank of the tensor.");
+    int64_t outer = 1, inner = 1;
+    for (int i = 0; i < ax; i++) outer *= X->dims[i];
+    for (int i = ax + 1; i < rank; i++) inner *= X->dims[i];
+    const int64_t r = X->dims[ax];
+    const int64_t V = X->dtype == LX_FLOAT ? 4 : 2;
+    const int vec = aligned16(X->data) ? (int)V : 1;
+
+    SoftmaxArgs sa;
+    memset(&sa, 0, sizeof sa);
+    sa.dtype = X->dtype;
+    sa.outer = outer;
+    sa.r = r;
+    sa.inner = inner;
+    sa.vec = vec;
+    if (mask) {
+        lx_bcast_plan p;
+        st = plan(X->rank, X->dims, mask->rank, mask->dims, &p);
+        if (st == LX_ERR_CANNOT_BROADCAST) return cannot_broadcast(X, mask);
+        if (st) return st;
+        if (X->dtype != LX_FLOAT && X->dtype != LX_DOUBLE) return type_not_supported("Add", "A", X);
+        bool same_shape = p.out_rank == X->rank;
+        for (int i = 0; same_shape && i < X->rank; i++) same_shape = p.out_dims[i] == X->dims[i];
+        bool fusable = same_shape && softmax_mask_fusable(X->dtype, r, inner, outer, vec) &&
+                       (vec == 1 || aligned16(mask->data));
+        if (fusable) {
+            // mask strides in X's frame (no collapsing of the softmax axis)
+            int64_t ms[LX_MAX_RANK];
+            int64_t stv = 1;
+            for (int i = rank - 1; i >= 0; i--) {
+                int k = i - (rank - mask->rank);
+                if (k < 0) { ms[i] = 0; continue; }
+                ms[i] = (mask->dims[k] == 1 && X->dims[i] != 1) ? 0 : stv;
+                stv *= mask->dims[k];
+            }
+            sa.mask_inner = (r > 1 && ms[rank - 1] != 0) ? 1 : 0;
+            if (r == 1) sa.mask_inner = 0;
+            if (sa.mask_inner && vec > 1 && r % V != 0) fusable = false;
+            // row axes 0..rank-2: collapse (drop size 1, merge contiguous)
+            int64_t cd[LX_MAX_RANK], cs[LX_MAX_RANK];
+            int n = 0;
+            for (int i = rank - 2; i >= 0; i--) {
+                if (X->dims[i] == 1) continue;
+                if (n > 0 && ms[i] == cs[n - 1] * cd[n - 1]) {
+                    cd[n - 1] *= X->dims[i];
+                    continue;
+                }
+                cd[n] = X->dims[i];
+                cs[n] = ms[i];
+                n++;
+            }
+            if (n > kMaxOuter) fusable = false;
+            if (fusable) {
+                sa.mask = mask->data;
+                sa.mask_rows.nouter = n;
+                for (int d = 0; d < n; d++) {
+                    sa.mask_rows.odiv[d] = make_fastdiv((uint32_t)cd[d]);
+                    sa.mask_rows.a_str[d] = cs[d];
+                }
+            }
+        }
+        if (!fusable) {
+            lx_tensor t{};
+            st = run_binary(kAdd, X, mask, &t);
+            if (!st) st = run_softmax(&t, nullptr, ax, 1, Y, opn);
+            lx_tensor_free(&t);
+            return st;
+        }
+    }
+    if (X->dtype != LX_FLOAT && X->dtype != LX_DOUBLE) return type_not_supported(opn, "input", X);
+    if ((st = prepare_output(Y, X->dtype, X->rank, X->dims))) return st;
+    if (vec > 1 && !aligned16(Y->data)) {
+        sa.vec = 1;
+        if (sa.mask && sa.r > 64 * 8) return set_err(LX_ERR_INVALID_ARGUMENT, "output storage must be 16-byte aligned");
+    }
+    sa.x = X->data;
+    sa.y = Y->data;
+    HIPCHECK(launch_softmax(sa, g.stream), opn);
+    return LX_OK;
+}
+
+}  // namespace

@@ -1,0 +1,185 @@
+// lx_device.h -- device-side building blocks shared by the gfx950 kernels.
+//
+// Compiled with -ffp-contract=off: every float/double operation written here
+// rounds separately unless an explicit fma() is written, so the elementwise
+// results keep the per-operation IEEE roundings of the C# reference.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lx_plan.h"
+
+#pragma clang fp contract(off)
+
+namespace lx {
+
+// ---------------------------------------------------------------------------
+// 16-byte (or smaller) register vectors used for coalesced global access.
+// ---------------------------------------------------------------------------
+template <typename T, int N>
+struct alignas((sizeof(T) * N) >= 16 ? 16 : (sizeof(T) * N)) Vec {
+    T v[N];
+};
+
+template <typename T>
+struct VecWidth {
+    static constexpr int value = 16 / sizeof(T);
+};
+
+template <typename T, int N>
+__device__ __forceinline__ Vec<T, N> vload(const T *p) {
+    return *reinterpret_cast<const Vec<T, N> *>(p);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void vstore(T *p, const Vec<T, N> &v) {
+    *reinterpret_cast<Vec<T, N> *>(p) = v;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv &f) {
+    return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (butterfly over __shfl_xor; fixed order -> deterministic).
+// ---------------------------------------------------------------------------
+template <typename T, typename F>
+__device__ __forceinline__ T wave_reduce(T v, F f) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        T o = __shfl_xor(v, off, 64);
+        v = f(v, o);
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// expf bit-identical to the host glibc expf that .NET's MathF.Exp calls.
+//
+// Method: ARM Optimized Routines expf (Szabolcs Nagy, 2017; the expf of glibc
+// >= 2.27, selected as its FMA variant on x86-64 CPUs with FMA):
+//   x*N/ln2 = k + r, N = 32, |r| <= 1/2
+//   2^(k/N) from a 32-entry table T[i] = bits(2^(i/32)) - (i << 47)
+//   2^(r/N) ~= C0 r^3 + C1 r^2 + C2 r + 1
+// evaluated in double with fused multiply-adds, rounded once to float.
+// The table entries are the correctly rounded doubles of 2^(i/32); the
+// polynomial coefficients are the published ones of that routine.  The host
+// evaluation of this same function (tests/native/expf_check.cpp) is
+// compared with the host expf over all 2^32 inputs by the test suite.
+// ---------------------------------------------------------------------------
+#define LX_EXP2F_TABLE                                                                              \
+    {0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,    \
+     0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,    \
+     0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,    \
+     0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,    \
+     0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,    \
+     0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,    \
+     0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,    \
+     0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL}
+
+#define LX_EXPF_INVLN2N (0x1.71547652b82fep+0 * 32.0)
+#define LX_EXPF_SHIFT 0x1.8p+52
+#define LX_EXPF_C0 (0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0)
+#define LX_EXPF_C1 (0x1.ebfce50fac4f3p-3 / 32.0 / 32.0)
+#define LX_EXPF_C2 (0x1.62e42ff0c52d6p-1 / 32.0)
+
+// Table copy held in LDS by every kernel that evaluates expf.
+struct ExpTable {
+    uint64_t t[32];
+};
+
+__device__ __forceinline__ void exp_table_fill(ExpTable &s) {
+    constexpr uint64_t tab[32] = LX_EXP2F_TABLE;
+    if (threadIdx.x < 32) {
+        // select from the constant list without a divergent memory lookup
+        uint64_t v = 0;
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            if ((int)threadIdx.x == i) v = tab[i];
+        s.t[threadIdx.x] = v;
+    }
+}
+
+// Fills a table on the host (host restatement used by the tests).
+__host__ inline void exp_table_fill_host(ExpTable &s) {
+    constexpr uint64_t tab[32] = LX_EXP2F_TABLE;
+    for (int i = 0; i < 32; i++) s.t[i] = tab[i];
+}
+
+__host__ __device__ __forceinline__ float expf_lx(float x, const ExpTable &tab) {
+    uint32_t ux = __builtin_bit_cast(uint32_t, x);
+    uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (__builtin_expect(abstop >= 0x42b, 0)) {  // top12(88.0f) == 0x42b
+        if (ux == 0xff800000u) return 0.0f;          // -inf
+        if (abstop >= 0x7f8) return x + x;            // inf or nan
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    double xd = (double)x;
+    double kd = __builtin_fma(LX_EXPF_INVLN2N, xd, LX_EXPF_SHIFT);
+    uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= LX_EXPF_SHIFT;
+    double r = __builtin_fma(LX_EXPF_INVLN2N, xd, -kd);
+    uint64_t t = tab.t[ki & 31];
+    t += ki << 47;
+    double s = __builtin_bit_cast(double, t);
+    double z = __builtin_fma(LX_EXPF_C0, r, LX_EXPF_C1);
+    double r2 = r * r;
+    double y = __builtin_fma(LX_EXPF_C2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// ---------------------------------------------------------------------------
+// MathOps.Erf(float) (MathOps.cs:988-1010): Abramowitz & Stegun 7.1.26 in
+// float32, one rounding per operation, exp = expf_lx.
+// ---------------------------------------------------------------------------
+__host__ __device__ __forceinline__ float erf_lx(float x, const ExpTable &tab) {
+    const float a1 = 0.254829592f;
+    const float a2 = -0.284496736f;
+    const float a3 = 1.421413741f;
+    const float a4 = -1.453152027f;
+    const float a5 = 1.061405429f;
+    const float p = 0.3275911f;
+    float sign = x < 0.0f ? -1.0f : 1.0f;
+    x = __builtin_fabsf(x);
+    float t = 1.0f / (1.0f + p * x);
+    float poly = ((((a5 * t + a4) * t) + a3) * t + a2) * t + a1;
+    float e = expf_lx(-x * x, tab);
+    float y = 1.0f - poly * t * e;
+    return sign * y;
+}
+
+// MathOps.Erf(double) (MathOps.cs:1012-1034) with the device double exp.
+__device__ __forceinline__ double erf_lx(double x) {
+    const double a1 = 0.254829592;
+    const double a2 = -0.284496736;
+    const double a3 = 1.421413741;
+    const double a4 = -1.453152027;
+    const double a5 = 1.061405429;
+    const double p = 0.3275911;
+    double sign = x < 0.0 ? -1.0 : 1.0;
+    x = __builtin_fabs(x);
+    double t = 1.0 / (1.0 + p * x);
+    double poly = ((((a5 * t + a4) * t) + a3) * t + a2) * t + a1;
+    double e = ::exp(-x * x);
+    double y = 1.0 - poly * t * e;
+    return sign * y;
+}
+
+// MathF.Pow -> powf; evaluated as a double pow rounded once to float (within
+// one float ulp of the host powf).  Exponent 2 is the correctly rounded x*x
+// (the host powf(x, 2) equals it except for 1-ulp differences on ~0.04% of
+// inputs).
+__device__ __forceinline__ float pow_lx(float x, float y) {
+    if (y == 2.0f) return x * x;
+    return (float)::pow((double)x, (double)y);
+}
+__device__ __forceinline__ double pow_lx(double x, double y) {
+    if (y == 2.0) return x * x;
+    return ::pow(x, y);
+}
+
+}  // namespace lx

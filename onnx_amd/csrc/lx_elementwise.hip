@@ -1,0 +1,606 @@
+// lx_elementwise.hip -- gfx950 kernels for the binary / unary / cast operators
+// and the fused GELU subgraph.
+//
+// Replaces the C# elementwise engines Apply / VectorizedApply
+// (TensorOps.cs:18-123) and the broadcast materialisation ToDenseTensor
+// (Tensor.cs:1605-1613): broadcast operands are read in place through stride-0
+// addressing instead of being copied.
+//
+// Memory-bound design: every lane moves 16 bytes per access (dwordx4), a block
+// of 256 lanes (4 waves of 64) walks the arrays with a grid stride, and each
+// lane keeps UNROLL independent loads in flight before computing.
+#include <limits>
+#include <type_traits>
+
+#include "lx_device.h"
+#include "lx_kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace lx {
+
+constexpr int kBlock = 256;
+constexpr int kMaxBlocks = 8192;
+
+template <int CODE> struct CType;
+template <> struct CType<kFloat> { using T = float; };
+template <> struct CType<kDouble> { using T = double; };
+template <> struct CType<kUInt8> { using T = uint8_t; };
+template <> struct CType<kInt8> { using T = int8_t; };
+template <> struct CType<kUInt16> { using T = uint16_t; };
+template <> struct CType<kInt16> { using T = int16_t; };
+template <> struct CType<kInt32> { using T = int32_t; };
+template <> struct CType<kUInt32> { using T = uint32_t; };
+template <> struct CType<kInt64> { using T = int64_t; };
+template <> struct CType<kUInt64> { using T = uint64_t; };
+template <> struct CType<kBool> { using T = uint8_t; };
+
+static inline int grid_for(int64_t work_items, int per_block) {
+    int64_t g = (work_items + per_block - 1) / per_block;
+    if (g < 1) g = 1;
+    if (g > kMaxBlocks) g = kMaxBlocks;
+    return (int)g;
+}
+
+__global__ void k_reset_errs(ErrFlags *e) {
+    if (threadIdx.x == 0) {
+        e->first_dbz = ~0ull;
+        e->first_ovf = ~0ull;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void k_fill(T *y, int64_t n, T v) {
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kBlock) y[i] = v;
+}
+
+hipError_t launch_fill(void *y, int64_t n, int esize, uint64_t bits, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    int g = grid_for(n, kBlock);
+    switch (esize) {
+    case 1: hipLaunchKernelGGL(k_fill<uint8_t>, dim3(g), dim3(kBlock), 0, s, (uint8_t *)y, n, (uint8_t)bits); break;
+    case 2: hipLaunchKernelGGL(k_fill<uint16_t>, dim3(g), dim3(kBlock), 0, s, (uint16_t *)y, n, (uint16_t)bits); break;
+    case 4: hipLaunchKernelGGL(k_fill<uint32_t>, dim3(g), dim3(kBlock), 0, s, (uint32_t *)y, n, (uint32_t)bits); break;
+    case 8: hipLaunchKernelGGL(k_fill<uint64_t>, dim3(g), dim3(kBlock), 0, s, (uint64_t *)y, n, (uint64_t)bits); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_reset_errs(ErrFlags *e, hipStream_t s) {
+    hipLaunchKernelGGL(k_reset_errs, dim3(1), dim3(64), 0, s, e);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Binary element operation with C# semantics.
+//   float/double: IEEE-754 round to nearest even (TensorOps.cs:241-297).
+//   byte: (byte)(l op r) after int promotion (TensorOps.cs:235, 253, 271, 289).
+//   int32/int64: unchecked two's-complement wrap, '/' truncates; x/0 and
+//   MIN/-1 record the element index (DivideByZero / Overflow exceptions).
+// ---------------------------------------------------------------------------
+template <int OP, typename T>
+__device__ __forceinline__ T bin_apply(T l, T r, uint64_t idx, ErrFlags *e) {
+    if constexpr (std::is_floating_point<T>::value) {
+        if constexpr (OP == kAdd) return l + r;
+        else if constexpr (OP == kSub) return l - r;
+        else if constexpr (OP == kMul) return l * r;
+        else if constexpr (OP == kDiv) return l / r;
+        else return pow_lx(l, r);
+    } else if constexpr (sizeof(T) == 1) {
+        int li = l, ri = r;
+        if constexpr (OP == kAdd) return (T)(li + ri);
+        else if constexpr (OP == kSub) return (T)(li - ri);
+        else if constexpr (OP == kMul) return (T)(li * ri);
+        else {
+            if (ri == 0) {
+                atomicMin(&e->first_dbz, (unsigned long long)idx);
+                return 0;
+            }
+            return (T)(li / ri);
+        }
+    } else {
+        using U = typename std::make_unsigned<T>::type;
+        if constexpr (OP == kAdd) return (T)((U)l + (U)r);
+        else if constexpr (OP == kSub) return (T)((U)l - (U)r);
+        else if constexpr (OP == kMul) return (T)((U)l * (U)r);
+        else {
+            if (r == 0) {
+                atomicMin(&e->first_dbz, (unsigned long long)idx);
+                return 0;
+            }
+            if (l == std::numeric_limits<T>::min() && r == (T)-1) {
+                atomicMin(&e->first_ovf, (unsigned long long)idx);
+                return 0;
+            }
+            if constexpr (sizeof(T) == 8) {
+                // both operands inside int32: the 32-bit quotient is the same value
+                if (l == (T)(int32_t)l && r == (T)(int32_t)r) return (T)((int32_t)l / (int32_t)r);
+            }
+            return l / r;
+        }
+    }
+}
+
+// SAME / SCALAR_A / SCALAR_B: dense output walk with 16-byte vectors.
+template <int OP, typename T, int LAYOUT, int V, int U>
+__global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a, const T *__restrict__ b,
+                                                        T *__restrict__ y, int64_t n, ErrFlags *errs) {
+    const int64_t nv = n / V;
+    T sa = T(), sb = T();
+    if constexpr (LAYOUT == kScalarA) sa = a[0];
+    if constexpr (LAYOUT == kScalarB) sb = b[0];
+    const int64_t step = (int64_t)gridDim.x * kBlock * U;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < nv; base += step) {
+        Vec<T, V> va[U], vb[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < nv) {
+                if constexpr (LAYOUT != kScalarA) va[u] = vload<T, V>(a + i * V);
+                if constexpr (LAYOUT != kScalarB) vb[u] = vload<T, V>(b + i * V);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < nv) {
+                Vec<T, V> vy;
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    T l = (LAYOUT == kScalarA) ? sa : va[u].v[k];
+                    T r = (LAYOUT == kScalarB) ? sb : vb[u].v[k];
+                    vy.v[k] = bin_apply<OP, T>(l, r, (uint64_t)(i * V + k), errs);
+                }
+                vstore<T, V>(y + i * V, vy);
+            }
+        }
+    }
+    const int64_t tail = n - nv * V;
+    if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
+        int64_t i = nv * V + threadIdx.x;
+        T l = (LAYOUT == kScalarA) ? sa : a[i];
+        T r = (LAYOUT == kScalarB) ? sb : b[i];
+        y[i] = bin_apply<OP, T>(l, r, (uint64_t)i, errs);
+    }
+}
+
+// General broadcast: output row-major [rows, inner]; operands addressed via
+// per-axis strides (0 on broadcast axes).  AIN/BIN: innermost axis contiguous
+// (1) or broadcast (0) for A/B.  32-bit vector index with fast division.
+template <int OP, typename T, int AIN, int BIN, int V>
+__global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, const T *__restrict__ b,
+                                                      T *__restrict__ y, uint32_t nv, NdLayout L,
+                                                      ErrFlags *errs) {
+    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += gridDim.x * kBlock) {
+        uint32_t row = fdiv(v, L.inner_v);
+        uint32_t cv = v - row * L.inner_v.d;
+        int64_t ao = 0, bo = 0;
+        uint32_t rr = row;
+#pragma unroll
+        for (int d = 0; d < kMaxOuter; d++) {
+            if (d < L.nouter) {
+                uint32_t q = fdiv(rr, L.odiv[d]);
+                uint32_t id = rr - q * L.odiv[d].d;
+                ao += (int64_t)id * L.a_str[d];
+                bo += (int64_t)id * L.b_str[d];
+                rr = q;
+            }
+        }
+        const int64_t col = (int64_t)cv * V;
+        Vec<T, V> va, vb, vy;
+        if constexpr (AIN) va = vload<T, V>(a + ao + col);
+        else {
+            T s = a[ao];
+#pragma unroll
+            for (int k = 0; k < V; k++) va.v[k] = s;
+        }
+        if constexpr (BIN) vb = vload<T, V>(b + bo + col);
+        else {
+            T s = b[bo];
+#pragma unroll
+            for (int k = 0; k < V; k++) vb.v[k] = s;
+        }
+#pragma unroll
+        for (int k = 0; k < V; k++)
+            vy.v[k] = bin_apply<OP, T>(va.v[k], vb.v[k], (uint64_t)v * V + k, errs);
+        vstore<T, V>(y + (int64_t)v * V, vy);
+    }
+}
+
+// Same as k_binary_nd for more than 2^31 vectors: 64-bit index arithmetic.
+template <int OP, typename T, int AIN, int BIN, int V>
+__global__ __launch_bounds__(kBlock) void k_binary_nd64(const T *__restrict__ a, const T *__restrict__ b,
+                                                        T *__restrict__ y, int64_t nv, NdLayout L,
+                                                        BinArgs big, ErrFlags *errs) {
+    for (int64_t v = (int64_t)blockIdx.x * kBlock + threadIdx.x; v < nv; v += (int64_t)gridDim.x * kBlock) {
+        int64_t row = v / big.nd_inner_vn;
+        int64_t cv = v - row * big.nd_inner_vn;
+        int64_t ao = 0, bo = 0, rr = row;
+        for (int d = 0; d < L.nouter; d++) {
+            int64_t q = rr / big.nd_osize[d];
+            int64_t id = rr - q * big.nd_osize[d];
+            ao += id * L.a_str[d];
+            bo += id * L.b_str[d];
+            rr = q;
+        }
+        const int64_t col = cv * V;
+        Vec<T, V> vy;
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            T l = AIN ? a[ao + col + k] : a[ao];
+            T r = BIN ? b[bo + col + k] : b[bo];
+            vy.v[k] = bin_apply<OP, T>(l, r, (uint64_t)(v * V + k), errs);
+        }
+        vstore<T, V>(y + v * V, vy);
+    }
+}
+
+template <int OP, typename T, int V>
+static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
+    const T *a = (const T *)A.a;
+    const T *b = (const T *)A.b;
+    T *y = (T *)A.y;
+    constexpr int U = 4;
+    if (A.layout != kNd) {
+        int64_t nv = A.n / V;
+        int g = grid_for(nv > 0 ? nv : 1, kBlock * U);
+        switch (A.layout) {
+        case kSame: hipLaunchKernelGGL((k_binary_flat<OP, T, kSame, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
+        case kScalarA: hipLaunchKernelGGL((k_binary_flat<OP, T, kScalarA, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
+        default: hipLaunchKernelGGL((k_binary_flat<OP, T, kScalarB, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
+        }
+        return hipGetLastError();
+    }
+    const int64_t nv = A.n / V;
+    const int g = grid_for(nv, kBlock * 4);
+    const int key = A.a_inner * 2 + A.b_inner;
+    if (nv < (1ll << 31)) {
+        switch (key) {
+        case 3: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
+        case 2: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
+        case 1: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
+        default: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
+        }
+    } else {
+        switch (key) {
+        case 3: hipLaunchKernelGGL((k_binary_nd64<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nv, A.nd, A, errs); break;
+        case 2: hipLaunchKernelGGL((k_binary_nd64<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nv, A.nd, A, errs); break;
+        case 1: hipLaunchKernelGGL((k_binary_nd64<OP, T, 0, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nv, A.nd, A, errs); break;
+        default: hipLaunchKernelGGL((k_binary_nd64<OP, T, 0, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nv, A.nd, A, errs); break;
+        }
+    }
+    return hipGetLastError();
+}
+
+template <int OP, typename T>
+static hipError_t binary_typed(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
+    if (A.vec > 1) return binary_typed_v<OP, T, VecWidth<T>::value>(A, errs, s);
+    return binary_typed_v<OP, T, 1>(A, errs, s);
+}
+
+template <typename T>
+static hipError_t binary_by_op(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
+    switch (A.op) {
+    case kAdd: return binary_typed<kAdd, T>(A, errs, s);
+    case kSub: return binary_typed<kSub, T>(A, errs, s);
+    case kMul: return binary_typed<kMul, T>(A, errs, s);
+    case kDiv: return binary_typed<kDiv, T>(A, errs, s);
+    case kPow:
+        if constexpr (std::is_floating_point<T>::value) return binary_typed<kPow, T>(A, errs, s);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_binary(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
+    if (A.n == 0) return hipSuccess;
+    switch (A.dtype) {
+    case kFloat: return binary_by_op<float>(A, errs, s);
+    case kDouble: return binary_by_op<double>(A, errs, s);
+    case kUInt8: return binary_by_op<uint8_t>(A, errs, s);
+    case kInt32: return binary_by_op<int32_t>(A, errs, s);
+    case kInt64: return binary_by_op<int64_t>(A, errs, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Unary: Sqrt (correctly rounded, TensorOps.cs:315-317), Erf (MathOps.cs:988),
+// Neg (TensorOps.cs:299-301), Exp (MathF.Exp), Square (Pow with exponent 2).
+// ---------------------------------------------------------------------------
+template <int OP, typename T>
+__device__ __forceinline__ T un_apply(T x, const ExpTable &tab) {
+    if constexpr (OP == kSqrt) {
+        if constexpr (std::is_same<T, float>::value) return __builtin_sqrtf(x);
+        else return __builtin_sqrt(x);
+    } else if constexpr (OP == kNeg) return -x;
+    else if constexpr (OP == kSquare) return x * x;
+    else if constexpr (OP == kErf) {
+        if constexpr (std::is_same<T, float>::value) return erf_lx(x, tab);
+        else return erf_lx((double)x);
+    } else {
+        if constexpr (std::is_same<T, float>::value) return expf_lx(x, tab);
+        else return ::exp((double)x);
+    }
+}
+
+template <int OP, typename T, int V, int U>
+__global__ __launch_bounds__(kBlock) void k_unary(const T *__restrict__ x, T *__restrict__ y, int64_t n) {
+    __shared__ ExpTable tab;
+    constexpr bool kNeedTab = (OP == kErf || OP == kExp) && std::is_same<T, float>::value;
+    if constexpr (kNeedTab) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    const int64_t nv = n / V;
+    const int64_t step = (int64_t)gridDim.x * kBlock * U;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < nv; base += step) {
+        Vec<T, V> vx[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < nv) vx[u] = vload<T, V>(x + i * V);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < nv) {
+                Vec<T, V> vy;
+#pragma unroll
+                for (int k = 0; k < V; k++) vy.v[k] = un_apply<OP, T>(vx[u].v[k], tab);
+                vstore<T, V>(y + i * V, vy);
+            }
+        }
+    }
+    const int64_t tail = n - nv * V;
+    if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
+        int64_t i = nv * V + threadIdx.x;
+        y[i] = un_apply<OP, T>(x[i], tab);
+    }
+}
+
+template <int OP, typename T>
+static hipError_t unary_typed(const void *x, void *y, int64_t n, int vec, hipStream_t s) {
+    constexpr int U = 4;
+    if (vec > 1) {
+        constexpr int V = VecWidth<T>::value;
+        int g = grid_for(n / V, kBlock * U);
+        hipLaunchKernelGGL((k_unary<OP, T, V, U>), dim3(g), dim3(kBlock), 0, s, (const T *)x, (T *)y, n);
+    } else {
+        int g = grid_for(n, kBlock * U);
+        hipLaunchKernelGGL((k_unary<OP, T, 1, U>), dim3(g), dim3(kBlock), 0, s, (const T *)x, (T *)y, n);
+    }
+    return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t unary_by_op(int op, const void *x, void *y, int64_t n, int vec, hipStream_t s) {
+    switch (op) {
+    case kSqrt: return unary_typed<kSqrt, T>(x, y, n, vec, s);
+    case kErf: return unary_typed<kErf, T>(x, y, n, vec, s);
+    case kNeg: return unary_typed<kNeg, T>(x, y, n, vec, s);
+    case kExp: return unary_typed<kExp, T>(x, y, n, vec, s);
+    case kSquare: return unary_typed<kSquare, T>(x, y, n, vec, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, int vec, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    if (dtype == kFloat) return unary_by_op<float>(op, x, y, n, vec, s);
+    if (dtype == kDouble) return unary_by_op<double>(op, x, y, n, vec, s);
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Cast: ITensor.Cast<U> = Convert.ChangeType per element (ITensor.cs:161-170),
+// i.e. System.Convert rules:
+//   -> Bool: v != 0;  Bool -> number: 1 / 0
+//   integer -> integer: must be representable, else OverflowException
+//   float/double -> Int32/Int16/UInt16/SByte/Byte: round half to even inside
+//     [-2147483648.5, 2147483647.5) (Convert.ToInt32(double)), then the range
+//   float/double -> UInt32: (-0.5, 4294967295.5), round half to even
+//   float/double -> Int64/UInt64: checked((long)Math.Round(v))
+//   integer -> float/double: one round-to-nearest-even conversion
+//   double -> float: (float)v
+// ---------------------------------------------------------------------------
+template <int DST>
+__device__ __forceinline__ bool int_fits(int64_t v) {
+    switch (DST) {
+    case kInt32: return v >= INT32_MIN && v <= INT32_MAX;
+    case kInt16: return v >= INT16_MIN && v <= INT16_MAX;
+    case kUInt16: return v >= 0 && v <= 65535;
+    case kInt8: return v >= -128 && v <= 127;
+    case kUInt8: return v >= 0 && v <= 255;
+    case kUInt32: return v >= 0 && v <= 4294967295ll;
+    default: return true;
+    }
+}
+
+template <int SRC, int DST>
+__device__ __forceinline__ typename CType<DST>::T cast_apply(typename CType<SRC>::T v, bool &ovf) {
+    using D = typename CType<DST>::T;
+    constexpr bool kSrcFloat = (SRC == kFloat || SRC == kDouble);
+    if constexpr (SRC == DST) {
+        return v;
+    } else if constexpr (DST == kBool) {
+        return (D)(v != 0);
+    } else if constexpr (DST == kFloat || DST == kDouble) {
+        if constexpr (SRC == kBool) return v ? (D)1 : (D)0;
+        else return (D)v;
+    } else if constexpr (kSrcFloat) {
+        double d = (double)v;
+        if constexpr (DST == kInt64) {
+            double r = __builtin_rint(d);
+            if (!(r >= -9223372036854775808.0 && r < 9223372036854775808.0)) { ovf = true; return 0; }
+            return (D)(int64_t)r;
+        } else if constexpr (DST == kUInt64) {
+            double r = __builtin_rint(d);
+            if (!(r > -1.0 && r < 18446744073709551616.0)) { ovf = true; return 0; }
+            return (D)(uint64_t)(r < 0.0 ? 0.0 : r);
+        } else if constexpr (DST == kUInt32) {
+            if (!(d > -0.5 && d < 4294967295.5)) { ovf = true; return 0; }
+            return (D)(uint32_t)(int64_t)__builtin_rint(d);
+        } else {
+            if (!(d >= -2147483648.5 && d < 2147483647.5)) { ovf = true; return 0; }
+            int64_t iv = (int64_t)__builtin_rint(d);
+            if (!int_fits<DST>(iv)) { ovf = true; return 0; }
+            return (D)iv;
+        }
+    } else if constexpr (SRC == kUInt64) {
+        uint64_t u = v;
+        if constexpr (DST == kInt64) {
+            if (u > (uint64_t)INT64_MAX) { ovf = true; return 0; }
+            return (D)u;
+        } else {
+            if (u > (uint64_t)INT64_MAX || !int_fits<DST>((int64_t)u)) { ovf = true; return 0; }
+            return (D)u;
+        }
+    } else {
+        int64_t iv = (int64_t)v;  // Bool, UInt8, Int8, UInt16, Int16, Int32, UInt32, Int64
+        if constexpr (DST == kUInt64) {
+            if (iv < 0) { ovf = true; return 0; }
+            return (D)iv;
+        } else {
+            if (!int_fits<DST>(iv)) { ovf = true; return 0; }
+            return (D)iv;
+        }
+    }
+}
+
+template <int SRC, int DST, int E>
+__global__ __launch_bounds__(kBlock) void k_cast(const typename CType<SRC>::T *__restrict__ x,
+                                                 typename CType<DST>::T *__restrict__ y, int64_t n,
+                                                 ErrFlags *errs) {
+    using S = typename CType<SRC>::T;
+    using D = typename CType<DST>::T;
+    const int64_t nv = n / E;
+    bool ovf = false;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kBlock) {
+        Vec<S, E> vx = vload<S, E>(x + i * E);
+        Vec<D, E> vy;
+#pragma unroll
+        for (int k = 0; k < E; k++) vy.v[k] = cast_apply<SRC, DST>(vx.v[k], ovf);
+        vstore<D, E>(y + i * E, vy);
+    }
+    const int64_t tail = n - nv * E;
+    if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
+        int64_t i = nv * E + threadIdx.x;
+        y[i] = cast_apply<SRC, DST>(x[i], ovf);
+    }
+    if (ovf) atomicMin(&errs->first_ovf, 0ull);
+}
+
+template <int SRC, int DST>
+static hipError_t cast_typed(const void *x, void *y, int64_t n, int vec, ErrFlags *errs, hipStream_t s) {
+    using S = typename CType<SRC>::T;
+    using D = typename CType<DST>::T;
+    constexpr int E = 16 / (sizeof(S) > sizeof(D) ? sizeof(S) : sizeof(D));
+    if (vec > 1) {
+        int g = grid_for(n / E, kBlock * 4);
+        hipLaunchKernelGGL((k_cast<SRC, DST, E>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);
+    } else {
+        int g = grid_for(n, kBlock * 4);
+        hipLaunchKernelGGL((k_cast<SRC, DST, 1>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);
+    }
+    return hipGetLastError();
+}
+
+template <int SRC>
+static hipError_t cast_to(int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs, hipStream_t s) {
+    switch (dst) {
+    case kFloat: return cast_typed<SRC, kFloat>(x, y, n, vec, errs, s);
+    case kDouble: return cast_typed<SRC, kDouble>(x, y, n, vec, errs, s);
+    case kUInt8: return cast_typed<SRC, kUInt8>(x, y, n, vec, errs, s);
+    case kInt8: return cast_typed<SRC, kInt8>(x, y, n, vec, errs, s);
+    case kUInt16: return cast_typed<SRC, kUInt16>(x, y, n, vec, errs, s);
+    case kInt16: return cast_typed<SRC, kInt16>(x, y, n, vec, errs, s);
+    case kInt32: return cast_typed<SRC, kInt32>(x, y, n, vec, errs, s);
+    case kUInt32: return cast_typed<SRC, kUInt32>(x, y, n, vec, errs, s);
+    case kInt64: return cast_typed<SRC, kInt64>(x, y, n, vec, errs, s);
+    case kUInt64: return cast_typed<SRC, kUInt64>(x, y, n, vec, errs, s);
+    case kBool: return cast_typed<SRC, kBool>(x, y, n, vec, errs, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,
+                       hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    switch (src) {
+    case kFloat: return cast_to<kFloat>(dst, x, y, n, vec, errs, s);
+    case kDouble: return cast_to<kDouble>(dst, x, y, n, vec, errs, s);
+    case kUInt8: return cast_to<kUInt8>(dst, x, y, n, vec, errs, s);
+    case kInt8: return cast_to<kInt8>(dst, x, y, n, vec, errs, s);
+    case kUInt16: return cast_to<kUInt16>(dst, x, y, n, vec, errs, s);
+    case kInt16: return cast_to<kInt16>(dst, x, y, n, vec, errs, s);
+    case kInt32: return cast_to<kInt32>(dst, x, y, n, vec, errs, s);
+    case kUInt32: return cast_to<kUInt32>(dst, x, y, n, vec, errs, s);
+    case kInt64: return cast_to<kInt64>(dst, x, y, n, vec, errs, s);
+    case kUInt64: return cast_to<kUInt64>(dst, x, y, n, vec, errs, s);
+    case kBool: return cast_to<kBool>(dst, x, y, n, vec, errs, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused GELU subgraph, one rounding per ONNX node:
+//   a = x / 1.4142135f (Div), e = Erf(a), b = e + 1f (Add), c = x * b (Mul),
+//   y = c * 0.5f (Mul)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float gelu_apply(float x, const ExpTable &tab) {
+    const float kSqrt2 = 1.41421353816986083984375f;  // float32(sqrt(2))
+    float a = x / kSqrt2;
+    float e = erf_lx(a, tab);
+    float b = e + 1.0f;
+    float c = x * b;
+    return c * 0.5f;
+}
+
+template <int V, int U>
+__global__ __launch_bounds__(kBlock) void k_gelu_erf(const float *__restrict__ x, float *__restrict__ y, int64_t n) {
+    __shared__ ExpTable tab;
+    exp_table_fill(tab);
+    __syncthreads();
+    const int64_t nv = n / V;
+    const int64_t step = (int64_t)gridDim.x * kBlock * U;
+    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < nv; base += step) {
+        Vec<float, V> vx[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < nv) vx[u] = vload<float, V>(x + i * V);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int64_t i = base + (int64_t)u * kBlock;
+            if (i < nv) {
+                Vec<float, V> vy;
+#pragma unroll
+                for (int k = 0; k < V; k++) vy.v[k] = gelu_apply(vx[u].v[k], tab);
+                vstore<float, V>(y + i * V, vy);
+            }
+        }
+    }
+    const int64_t tail = n - nv * V;
+    if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
+        int64_t i = nv * V + threadIdx.x;
+        y[i] = gelu_apply(x[i], tab);
+    }
+}
+
+hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    constexpr int U = 2;
+    if (vec > 1) {
+        int g = grid_for(n / 4, kBlock * U);
+        hipLaunchKernelGGL((k_gelu_erf<4, U>), dim3(g), dim3(kBlock), 0, s, x, y, n);
+    } else {
+        int g = grid_for(n, kBlock * U);
+        hipLaunchKernelGGL((k_gelu_erf<1, U>), dim3(g), dim3(kBlock), 0, s, x, y, n);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace lx

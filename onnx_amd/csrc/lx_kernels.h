@@ -1,0 +1,99 @@
+// lx_kernels.h -- internal launch interface between the host layer (lx_api.cpp)
+// and the gfx950 kernels (lx_elementwise.hip, lx_reduce.hip, lx_softmax.hip).
+// Not part of the public C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lx_plan.h"
+
+namespace lx {
+
+// TensorElementType codes (Tensor.cs:31-50)
+enum DType : int {
+    kFloat = 1, kUInt8 = 2, kInt8 = 3, kUInt16 = 4, kInt16 = 5, kInt32 = 6, kInt64 = 7,
+    kBool = 9, kDouble = 11, kUInt32 = 12, kUInt64 = 13
+};
+
+enum BinOp : int { kAdd = 0, kSub = 1, kMul = 2, kDiv = 3, kPow = 4 };
+enum UnOp : int { kSqrt = 0, kErf = 1, kNeg = 2, kExp = 3, kSquare = 4 };
+enum RedOp : int { kSum = 0, kMean = 1, kMax = 2 };
+
+// Binary layouts chosen by the planner.
+enum BinLayout : int {
+    kSame = 0,      // a[i] op b[i]
+    kScalarA = 1,   // a[0] op b[i]
+    kScalarB = 2,   // a[i] op b[0]
+    kNd = 3         // NdLayout with inner strides given by a_inner / b_inner
+};
+
+// Device-side error record: first element index that raised each exception
+// (UINT64_MAX = none).  Lives in device memory owned by the host layer.
+struct ErrFlags {
+    unsigned long long first_dbz;   // DivideByZeroException
+    unsigned long long first_ovf;   // OverflowException
+};
+
+struct BinArgs {
+    int op, dtype, layout;
+    int a_inner, b_inner;   // kNd: 1 = contiguous innermost axis, 0 = broadcast
+    int vec;                // 1 = scalar element access, else 16-byte vectors
+    const void *a;
+    const void *b;
+    void *y;
+    int64_t n;              // output elements
+    NdLayout nd;            // kNd only
+    int64_t nd_osize[kMaxOuter];  // outer sizes as int64 (large-index path)
+    int64_t nd_inner_vn;          // inner axis in vector units (large-index path)
+};
+
+hipError_t launch_reset_errs(ErrFlags *e, hipStream_t s);
+hipError_t launch_binary(const BinArgs &args, ErrFlags *errs, hipStream_t s);
+hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, int vec, hipStream_t s);
+hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,
+                       hipStream_t s);
+hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStream_t s);
+// y[i] = value (bit pattern of one element of esize bytes), used for empty reductions.
+hipError_t launch_fill(void *y, int64_t n, int esize, uint64_t bits, hipStream_t s);
+
+// Reduction of x viewed as [outer, r, inner] (row-major) into y[outer, inner].
+//   pre_div : divide every element by R_total before accumulating (ReduceMean int/double)
+//   post_div: divide the result by (float)R_total (ReduceMean float)
+// workspace: device scratch of ws_bytes (partials of split reductions).
+struct ReduceArgs {
+    int op, dtype;
+    const void *x;
+    void *y;
+    int64_t outer, r, inner;
+    int pre_div, post_div;
+    int64_t r_total;
+    int vec;
+    void *workspace;
+    int64_t ws_bytes;
+};
+hipError_t launch_reduce(const ReduceArgs &args, hipStream_t s);
+// Bytes of workspace launch_reduce needs for these sizes.
+int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner);
+
+// Softmax of x viewed as [outer, r, inner] along r, with an optional additive
+// mask (already planned against x as an NdLayout over [outer*inner rows, r]).
+struct SoftmaxArgs {
+    int dtype;
+    const void *x;
+    void *y;
+    int64_t outer, r, inner;
+    int vec;
+    const void *mask;        // nullptr = no mask (only for inner == 1)
+    int mask_inner;          // 1 = mask contiguous along r, 0 = broadcast along r
+    NdLayout mask_rows;      // row -> mask offset (nouter axes over the rows)
+};
+hipError_t launch_softmax(const SoftmaxArgs &args, hipStream_t s);
+bool softmax_mask_fusable(int dtype, int64_t r, int64_t inner, int64_t outer, int vec);
+
+// LayerNorm decomposed into its ONNX nodes, rows of length r (r % 4 == 0, r <= 4096).
+hipError_t launch_layernorm(const float *x, const float *gamma, const float *beta, float eps, float *y,
+                            int64_t rows, int64_t r, hipStream_t s);
+bool layernorm_supported(int64_t r);
+
+}  // namespace lx

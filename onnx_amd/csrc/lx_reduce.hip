@@ -1,0 +1,487 @@
+// lx_reduce.hip -- gfx950 reductions (ReduceSum / ReduceMean / ReduceMax) and
+// the fused LayerNorm subgraph.
+//
+// Replaces the C# reductions (TensorOps.cs:1561-1891), which transpose the
+// tensor so that the reduced axes are innermost (Transpose, 1358-1407) and then
+// fold each slice serially.  Here the tensor is read in place as
+// [outer, r, inner]:
+//   inner == 1 : one wave64 per row (butterfly reduce), or a split of long rows
+//                over many blocks followed by a finishing pass;
+//   inner  > 1 : column tiles coalesced along inner, row slices combined in
+//                LDS, optional split of r over blocks plus a finishing pass.
+// Every combination order is fixed, so results are run-to-run deterministic.
+// Integer sums wrap (two's complement); ReduceMax keeps the reference's seed
+// of 0 (TensorOps.cs:1820): max(0, max_j x_j), NaN elements never win.
+#include <type_traits>
+
+#include "lx_device.h"
+#include "lx_kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace lx {
+
+constexpr int kRBlock = 256;
+
+template <typename T> struct AccOf { using A = T; };
+template <> struct AccOf<int32_t> { using A = uint32_t; };
+template <> struct AccOf<int64_t> { using A = uint64_t; };
+
+template <int OP, typename T>
+struct Red {
+    using A = typename AccOf<T>::A;
+    __device__ __forceinline__ static A ident() { return A(0); }
+    // ReduceMean for int32 / int64 / double divides each element by R first
+    // (TensorOps.cs:1723-1724, 1777-1778).
+    __device__ __forceinline__ static A load(T x, int pre, int64_t R) {
+        if constexpr (OP == kMean && !std::is_same<T, float>::value) {
+            if (pre) {
+                if constexpr (std::is_same<T, double>::value) return x / (double)R;
+                else if constexpr (std::is_same<T, int32_t>::value) return (A)(x / (int32_t)R);
+                else return (A)(x / R);
+            }
+        }
+        return (A)x;
+    }
+    __device__ __forceinline__ static A comb(A a, A b) {
+        if constexpr (OP == kMax) return b > a ? b : a;
+        else return a + b;
+    }
+    // ReduceMean float: sum, then divide by (float)R (TensorOps.cs:1747-1751).
+    __device__ __forceinline__ static T fin(A a, int post, int64_t R) {
+        if constexpr (OP == kMean && std::is_same<T, float>::value) {
+            if (post) return a / (float)R;
+        }
+        return (T)a;
+    }
+};
+
+template <int OP, typename T>
+__device__ __forceinline__ typename Red<OP, T>::A block_reduce(typename Red<OP, T>::A v) {
+    using R = Red<OP, T>;
+    using A = typename R::A;
+    __shared__ A part[kRBlock / 64];
+    v = wave_reduce(v, [](A x, A y) { return R::comb(x, y); });
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) part[wave] = v;
+    __syncthreads();
+    A t = R::ident();
+    if (threadIdx.x == 0) {
+        t = part[0];
+#pragma unroll
+        for (int w = 1; w < kRBlock / 64; w++) t = R::comb(t, part[w]);
+    }
+    return t;  // valid in thread 0
+}
+
+// inner == 1, one wave per row.
+template <int OP, typename T, int V>
+__global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
+                                                              int64_t r, int pre, int post, int64_t R) {
+    using RD = Red<OP, T>;
+    using A = typename RD::A;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T *p = x + row * r;
+    A acc = RD::ident();
+    const int64_t nv = r / V;
+    int64_t j = lane;
+    for (; j + 64 * 3 < nv; j += 64 * 4) {
+        Vec<T, V> v0 = vload<T, V>(p + j * V);
+        Vec<T, V> v1 = vload<T, V>(p + (j + 64) * V);
+        Vec<T, V> v2 = vload<T, V>(p + (j + 128) * V);
+        Vec<T, V> v3 = vload<T, V>(p + (j + 192) * V);
+#pragma unroll
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v0.v[k], pre, R));
+#pragma unroll
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v1.v[k], pre, R));
+#pragma unroll
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v2.v[k], pre, R));
+#pragma unroll
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v3.v[k], pre, R));
+    }
+    for (; j < nv; j += 64) {
+        Vec<T, V> v0 = vload<T, V>(p + j * V);
+#pragma unroll
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v0.v[k], pre, R));
+    }
+    for (int64_t t = nv * V + lane; t < r; t += 64) acc = RD::comb(acc, RD::load(p[t], pre, R));
+    acc = wave_reduce(acc, [](A a, A b) { return RD::comb(a, b); });
+    if (lane == 0) y[row] = RD::fin(acc, post, R);
+}
+
+// inner == 1, long rows: grid (nchunks, rows); each block folds one chunk.
+template <int OP, typename T, int V>
+__global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restrict__ x,
+                                                               typename Red<OP, T>::A *__restrict__ partial,
+                                                               T *__restrict__ y, int64_t r, int64_t chunk,
+                                                               int nchunks, int pre, int post, int64_t R) {
+    using RD = Red<OP, T>;
+    using A = typename RD::A;
+    const int64_t row = blockIdx.y;
+    const int c = blockIdx.x;
+    const int64_t j0 = (int64_t)c * chunk;
+    int64_t j1 = j0 + chunk;
+    if (j1 > r) j1 = r;
+    const T *p = x + row * r;
+    A acc = RD::ident();
+    if (j0 < j1) {
+        const int64_t v0i = j0 / V, v1i = j1 / V;  // chunk is a multiple of V
+        int64_t j = v0i + threadIdx.x;
+        for (; j + kRBlock * 3 < v1i; j += kRBlock * 4) {
+            Vec<T, V> a0 = vload<T, V>(p + j * V);
+            Vec<T, V> a1 = vload<T, V>(p + (j + kRBlock) * V);
+            Vec<T, V> a2 = vload<T, V>(p + (j + 2 * kRBlock) * V);
+            Vec<T, V> a3 = vload<T, V>(p + (j + 3 * kRBlock) * V);
+#pragma unroll
+            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
+#pragma unroll
+            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a1.v[k], pre, R));
+#pragma unroll
+            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a2.v[k], pre, R));
+#pragma unroll
+            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a3.v[k], pre, R));
+        }
+        for (; j < v1i; j += kRBlock) {
+            Vec<T, V> a0 = vload<T, V>(p + j * V);
+#pragma unroll
+            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
+        }
+        for (int64_t t = v1i * V + threadIdx.x; t < j1; t += kRBlock) acc = RD::comb(acc, RD::load(p[t], pre, R));
+    }
+    acc = block_reduce<OP, T>(acc);
+    if (threadIdx.x == 0) {
+        if (nchunks == 1) y[row] = RD::fin(acc, post, R);
+        else partial[row * nchunks + c] = acc;
+    }
+}
+
+// Finishing pass of the split row reduction: one wave per row over its partials.
+template <int OP, typename T>
+__global__ __launch_bounds__(kRBlock) void k_reduce_rows_finish(const typename Red<OP, T>::A *__restrict__ partial,
+                                                                T *__restrict__ y, int64_t rows, int nchunks,
+                                                                int post, int64_t R) {
+    using RD = Red<OP, T>;
+    using A = typename RD::A;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    A acc = RD::ident();
+    for (int c = lane; c < nchunks; c += 64) acc = RD::comb(acc, partial[row * nchunks + c]);
+    acc = wave_reduce(acc, [](A a, A b) { return RD::comb(a, b); });
+    if (lane == 0) y[row] = RD::fin(acc, post, R);
+}
+
+// inner > 1: grid (column tiles * outer, rsplit).  ct lanes cover ct column
+// vectors, 256/ct row slices stride over the rows of this split.
+template <int OP, typename T, int V>
+__global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x,
+                                                         typename Red<OP, T>::A *__restrict__ partial,
+                                                         T *__restrict__ y, int64_t outer, int64_t r, int64_t inner,
+                                                         int ct, int64_t rchunk, int rsplit, int pre, int post,
+                                                         int64_t R) {
+    using RD = Red<OP, T>;
+    using A = typename RD::A;
+    __shared__ A sm[kRBlock * V];
+    const int t = threadIdx.x;
+    const int cvt = t % ct, rs = t / ct, nrs = kRBlock / ct;
+    const int64_t inner_v = inner / V;
+    const int64_t tiles = (inner_v + ct - 1) / ct;
+    const int64_t o = (int64_t)blockIdx.x / tiles;
+    const int64_t cv = ((int64_t)blockIdx.x - o * tiles) * ct + cvt;
+    const int s = blockIdx.y;
+    const int64_t j0 = (int64_t)s * rchunk;
+    int64_t j1 = j0 + rchunk;
+    if (j1 > r) j1 = r;
+    A acc[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) acc[k] = RD::ident();
+    if (cv < inner_v) {
+        const T *p = x + (o * r) * inner + cv * V;
+        int64_t j = j0 + rs;
+        for (; j + 3 * nrs < j1; j += 4 * nrs) {
+            Vec<T, V> a0 = vload<T, V>(p + j * inner);
+            Vec<T, V> a1 = vload<T, V>(p + (j + nrs) * inner);
+            Vec<T, V> a2 = vload<T, V>(p + (j + 2 * nrs) * inner);
+            Vec<T, V> a3 = vload<T, V>(p + (j + 3 * nrs) * inner);
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
+                acc[k] = RD::comb(acc[k], RD::load(a1.v[k], pre, R));
+                acc[k] = RD::comb(acc[k], RD::load(a2.v[k], pre, R));
+                acc[k] = RD::comb(acc[k], RD::load(a3.v[k], pre, R));
+            }
+        }
+        for (; j < j1; j += nrs) {
+            Vec<T, V> a0 = vload<T, V>(p + j * inner);
+#pragma unroll
+            for (int k = 0; k < V; k++) acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < V; k++) sm[(rs * ct + cvt) * V + k] = acc[k];
+    __syncthreads();
+    if (rs == 0 && cv < inner_v) {
+        A tot[V];
+#pragma unroll
+        for (int k = 0; k < V; k++) tot[k] = sm[cvt * V + k];
+        for (int q = 1; q < nrs; q++) {
+#pragma unroll
+            for (int k = 0; k < V; k++) tot[k] = RD::comb(tot[k], sm[(q * ct + cvt) * V + k]);
+        }
+        const int64_t out = o * inner + cv * V;
+        if (rsplit == 1) {
+#pragma unroll
+            for (int k = 0; k < V; k++) y[out + k] = RD::fin(tot[k], post, R);
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; k++) partial[(int64_t)s * outer * inner + out + k] = tot[k];
+        }
+    }
+}
+
+template <int OP, typename T>
+__global__ __launch_bounds__(kRBlock) void k_reduce_cols_finish(const typename Red<OP, T>::A *__restrict__ partial,
+                                                                T *__restrict__ y, int64_t nout, int rsplit, int post,
+                                                                int64_t R) {
+    using RD = Red<OP, T>;
+    using A = typename RD::A;
+    for (int64_t i = (int64_t)blockIdx.x * kRBlock + threadIdx.x; i < nout; i += (int64_t)gridDim.x * kRBlock) {
+        A acc = partial[i];
+        for (int s = 1; s < rsplit; s++) acc = RD::comb(acc, partial[(int64_t)s * nout + i]);
+        y[i] = RD::fin(acc, post, R);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side planning of one reduction pass.
+// ---------------------------------------------------------------------------
+static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct RedPlan {
+    int kind;  // 0 wave rows, 1 split rows, 2 cols
+    int64_t chunk;
+    int nchunks;
+    int ct;
+    int64_t rchunk;
+    int rsplit;
+    int64_t ws;  // workspace bytes
+};
+
+static constexpr int64_t kTargetBlocks = 2048;
+
+template <typename A>
+static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
+    RedPlan p{};
+    if (inner == 1) {
+        const int64_t rows = outer;
+        if (r <= 8192 || rows >= kTargetBlocks) {
+            p.kind = 0;
+            return p;
+        }
+        int64_t nch = ceil_div(kTargetBlocks, rows);
+        int64_t maxch = ceil_div(r, 4096);
+        if (nch > maxch) nch = maxch;
+        if (nch < 1) nch = 1;
+        int64_t chunk = ceil_div(r, nch);
+        chunk = ceil_div(chunk, V * 64) * (V * 64);
+        nch = ceil_div(r, chunk);
+        p.kind = 1;
+        p.chunk = chunk;
+        p.nchunks = (int)nch;
+        p.ws = nch > 1 ? rows * nch * (int64_t)sizeof(A) : 0;
+        return p;
+    }
+    const int64_t inner_v = inner / V;
+    int ct = 1;
+    while (ct < 64 && ct < inner_v) ct <<= 1;
+    const int64_t tiles = ceil_div(inner_v, ct);
+    const int64_t base = tiles * outer;
+    int64_t rsplit = 1;
+    const int nrs = kRBlock / ct;
+    if (base < kTargetBlocks) {
+        rsplit = ceil_div(kTargetBlocks, base);
+        int64_t maxs = ceil_div(r, (int64_t)nrs * 16);  // keep >= 16 rows per slice
+        if (rsplit > maxs) rsplit = maxs;
+        if (rsplit > 65535) rsplit = 65535;
+        if (rsplit < 1) rsplit = 1;
+    }
+    int64_t rchunk = ceil_div(r, rsplit);
+    rsplit = ceil_div(r, rchunk);
+    if (rsplit < 1) rsplit = 1;
+    p.kind = 2;
+    p.ct = ct;
+    p.rchunk = rchunk;
+    p.rsplit = (int)rsplit;
+    p.ws = rsplit > 1 ? rsplit * outer * inner * (int64_t)sizeof(A) : 0;
+    return p;
+}
+
+template <int OP, typename T, int V>
+static hipError_t reduce_typed_v(const ReduceArgs &a, hipStream_t s) {
+    using A = typename Red<OP, T>::A;
+    const T *x = (const T *)a.x;
+    T *y = (T *)a.y;
+    RedPlan p = plan_reduce<A>(a.outer, a.r, a.inner, V);
+    if (p.ws > a.ws_bytes) return hipErrorInvalidValue;
+    A *ws = (A *)a.workspace;
+    if (p.kind == 0) {
+        int g = (int)ceil_div(a.outer, kRBlock / 64);
+        hipLaunchKernelGGL((k_reduce_rows_wave<OP, T, V>), dim3(g), dim3(kRBlock), 0, s, x, y, a.outer, a.r,
+                           a.pre_div, a.post_div, a.r_total);
+    } else if (p.kind == 1) {
+        hipLaunchKernelGGL((k_reduce_rows_split<OP, T, V>), dim3(p.nchunks, (unsigned)a.outer), dim3(kRBlock), 0, s, x,
+                           ws, y, a.r, p.chunk, p.nchunks, a.pre_div, a.post_div, a.r_total);
+        if (p.nchunks > 1) {
+            int g = (int)ceil_div(a.outer, kRBlock / 64);
+            hipLaunchKernelGGL((k_reduce_rows_finish<OP, T>), dim3(g), dim3(kRBlock), 0, s, ws, y, a.outer, p.nchunks,
+                               a.post_div, a.r_total);
+        }
+    } else {
+        const int64_t tiles = ceil_div(a.inner / V, p.ct);
+        hipLaunchKernelGGL((k_reduce_cols<OP, T, V>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
+                           dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rchunk, p.rsplit, a.pre_div,
+                           a.post_div, a.r_total);
+        if (p.rsplit > 1) {
+            int64_t nout = a.outer * a.inner;
+            int g = (int)ceil_div(nout, kRBlock);
+            if (g > 8192) g = 8192;
+            hipLaunchKernelGGL((k_reduce_cols_finish<OP, T>), dim3(g), dim3(kRBlock), 0, s, ws, y, nout, p.rsplit,
+                               a.post_div, a.r_total);
+        }
+    }
+    return hipGetLastError();
+}
+
+template <int OP, typename T>
+static hipError_t reduce_typed(const ReduceArgs &a, hipStream_t s) {
+    if (a.vec > 1) return reduce_typed_v<OP, T, VecWidth<T>::value>(a, s);
+    return reduce_typed_v<OP, T, 1>(a, s);
+}
+
+template <typename T>
+static hipError_t reduce_by_op(const ReduceArgs &a, hipStream_t s) {
+    switch (a.op) {
+    case kSum: return reduce_typed<kSum, T>(a, s);
+    case kMean: return reduce_typed<kMean, T>(a, s);
+    case kMax:
+        if constexpr (std::is_floating_point<T>::value) return reduce_typed<kMax, T>(a, s);
+        return hipErrorInvalidValue;
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_reduce(const ReduceArgs &a, hipStream_t s) {
+    if (a.outer * a.inner == 0) return hipSuccess;
+    if (a.inner > 1 && a.outer * ((a.inner + 63) / 64) > 0x7fffffffll) return hipErrorInvalidValue;  // grid.x limit
+    switch (a.dtype) {
+    case kFloat: return reduce_by_op<float>(a, s);
+    case kDouble: return reduce_by_op<double>(a, s);
+    case kInt32: return reduce_by_op<int32_t>(a, s);
+    case kInt64: return reduce_by_op<int64_t>(a, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner) {
+    const int64_t asz = (dtype == kFloat || dtype == kInt32) ? 4 : 8;
+    const int V = (int)(16 / asz);
+    // the vectorised plan needs the most partials when V is largest; evaluate both
+    int64_t w = 0;
+    for (int v : {1, V}) {
+        RedPlan p = (asz == 4) ? plan_reduce<float>(outer, r, inner, v) : plan_reduce<double>(outer, r, inner, v);
+        if (p.ws > w) w = p.ws;
+    }
+    return w;
+}
+
+// ---------------------------------------------------------------------------
+// Fused LayerNorm subgraph over rows of length r, one wave per row, the row
+// held in registers (NV float4 per lane).  Each ONNX node keeps its float32
+// rounding:  mean = sum(x)/(float)r;  d = x - mean;  p = d*d (Pow 2);
+// var = sum(p)/(float)r;  ve = var + eps;  sd = sqrtf(ve);  n = d / sd;
+// m = n * gamma;  y = m + beta.  Only the two sums run in a different order
+// from the reference's serial fold.
+// ---------------------------------------------------------------------------
+template <int NV>
+__global__ __launch_bounds__(kRBlock) void k_layernorm(const float *__restrict__ x, const float *__restrict__ gamma,
+                                                       const float *__restrict__ beta, float eps,
+                                                       float *__restrict__ y, int64_t rows, int r) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *p = x + row * (int64_t)r;
+    float *q = y + row * (int64_t)r;
+    Vec<float, 4> v[NV];
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) v[c] = vload<float, 4>(p + col);
+        else v[c] = Vec<float, 4>{{0.0f, 0.0f, 0.0f, 0.0f}};
+    }
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) s = s + ((v[c].v[0] + v[c].v[1]) + (v[c].v[2] + v[c].v[3]));
+    }
+    s = wave_reduce(s, [](float a, float b) { return a + b; });
+    const float fr = (float)r;
+    const float mean = s / fr;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[c].v[k] = v[c].v[k] - mean;
+            float p0 = v[c].v[0] * v[c].v[0], p1 = v[c].v[1] * v[c].v[1];
+            float p2 = v[c].v[2] * v[c].v[2], p3 = v[c].v[3] * v[c].v[3];
+            s2 = s2 + ((p0 + p1) + (p2 + p3));
+        }
+    }
+    s2 = wave_reduce(s2, [](float a, float b) { return a + b; });
+    const float var = s2 / fr;
+    const float ve = var + eps;
+    const float sd = __builtin_sqrtf(ve);
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) {
+            Vec<float, 4> g = vload<float, 4>(gamma + col);
+            Vec<float, 4> b = vload<float, 4>(beta + col);
+            Vec<float, 4> o;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float nrm = v[c].v[k] / sd;
+                float m = nrm * g.v[k];
+                o.v[k] = m + b.v[k];
+            }
+            vstore<float, 4>(q + col, o);
+        }
+    }
+}
+
+bool layernorm_supported(int64_t r) { return r >= 4 && r <= 4096 && (r % 4) == 0; }
+
+hipError_t launch_layernorm(const float *x, const float *gamma, const float *beta, float eps, float *y, int64_t rows,
+                            int64_t r, hipStream_t s) {
+    if (rows == 0) return hipSuccess;
+    if (!layernorm_supported(r)) return hipErrorInvalidValue;
+    const int nv = (int)ceil_div(r, 256);
+    const int g = (int)ceil_div(rows, kRBlock / 64);
+    const int ri = (int)r;
+#define LX_LN_CASE(N) \
+    case N: hipLaunchKernelGGL((k_layernorm<N>), dim3(g), dim3(kRBlock), 0, s, x, gamma, beta, eps, y, rows, ri); break;
+    switch (nv) {
+        LX_LN_CASE(1) LX_LN_CASE(2) LX_LN_CASE(3) LX_LN_CASE(4) LX_LN_CASE(5) LX_LN_CASE(6) LX_LN_CASE(7) LX_LN_CASE(8)
+        LX_LN_CASE(9) LX_LN_CASE(10) LX_LN_CASE(11) LX_LN_CASE(12) LX_LN_CASE(13) LX_LN_CASE(14) LX_LN_CASE(15)
+        LX_LN_CASE(16)
+    default: return hipErrorInvalidValue;
+    }
+#undef LX_LN_CASE
+    return hipGetLastError();
+}
+
+}  // namespace lx

@@ -1,0 +1,232 @@
+// lx_softmax.hip -- gfx950 Softmax, optionally fused with a broadcast additive
+// mask (the Add node that precedes attention softmax).
+//
+// Reference composite (TensorOps.cs:1312-1330), five passes and three
+// temporaries on the CPU:
+//   m = ReduceMax(x, axis) (seed 0)   d = x - m   e = MathF.Exp(d)
+//   s = ReduceSum(e, axis)            y = e / s   (true division)
+// Here: one wave64 per row with the row in registers (rows up to 2048 floats),
+// the exponential bit-identical to the host expf (expf_lx), the sum as a
+// wave butterfly.  Only the order of the sum differs from the reference.
+// Other shapes (axis not innermost, long rows) take a three-pass kernel.
+#include <type_traits>
+
+#include "lx_device.h"
+#include "lx_kernels.h"
+
+#pragma clang fp contract(off)
+
+namespace lx {
+
+constexpr int kSBlock = 256;
+
+template <typename T>
+__device__ __forceinline__ T exp_elem(T d, const ExpTable &tab) {
+    if constexpr (std::is_same<T, float>::value) return expf_lx(d, tab);
+    else return ::exp(d);
+}
+
+// One wave per row; NV vectors of V elements per lane.  MASK: add the mask
+// element (row offset from the NdLayout decomposition, column stride mask_inner).
+template <typename T, int V, int NV, bool MASK>
+__global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
+                                                          int r, const T *__restrict__ mask, int mask_inner,
+                                                          NdLayout mrows) {
+    __shared__ ExpTable tab;
+    if constexpr (std::is_same<T, float>::value) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T *p = x + row * (int64_t)r;
+    T *q = y + row * (int64_t)r;
+    Vec<T, V> v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (col < r) v[c] = vload<T, V>(p + col);
+    }
+    if constexpr (MASK) {
+        int64_t moff = 0;
+        uint32_t rr = (uint32_t)row;
+#pragma unroll
+        for (int d = 0; d < kMaxOuter; d++) {
+            if (d < mrows.nouter) {
+                uint32_t qq = fdiv(rr, mrows.odiv[d]);
+                uint32_t id = rr - qq * mrows.odiv[d].d;
+                moff += (int64_t)id * mrows.a_str[d];
+                rr = qq;
+            }
+        }
+        const T *m = mask + moff;
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const int col = (c * 64 + lane) * V;
+            if (col < r) {
+                if (mask_inner) {
+                    Vec<T, V> mv = vload<T, V>(m + col);
+#pragma unroll
+                    for (int k = 0; k < V; k++) v[c].v[k] = v[c].v[k] + mv.v[k];
+                } else {
+                    const T mv = m[0];
+#pragma unroll
+                    for (int k = 0; k < V; k++) v[c].v[k] = v[c].v[k] + mv;
+                }
+            }
+        }
+    }
+    // ReduceMax with seed 0 (TensorOps.cs:1820-1827)
+    T mx = T(0);
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (col < r) {
+#pragma unroll
+            for (int k = 0; k < V; k++) mx = v[c].v[k] > mx ? v[c].v[k] : mx;
+        }
+    }
+    mx = wave_reduce(mx, [](T a, T b) { return b > a ? b : a; });
+    T s = T(0);
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (col < r) {
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                v[c].v[k] = exp_elem<T>(v[c].v[k] - mx, tab);
+                s = s + v[c].v[k];
+            }
+        }
+    }
+    s = wave_reduce(s, [](T a, T b) { return a + b; });
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (col < r) {
+            Vec<T, V> o;
+#pragma unroll
+            for (int k = 0; k < V; k++) o.v[k] = v[c].v[k] / s;
+            vstore<T, V>(q + col, o);
+        }
+    }
+}
+
+// inner == 1, long rows: one block per row, three passes over the row.
+template <typename T>
+__global__ __launch_bounds__(kSBlock) void k_softmax_block(const T *__restrict__ x, T *__restrict__ y, int64_t r) {
+    __shared__ ExpTable tab;
+    __shared__ T red[kSBlock / 64];
+    if constexpr (std::is_same<T, float>::value) exp_table_fill(tab);
+    __syncthreads();
+    const int64_t row = blockIdx.x;
+    const T *p = x + row * r;
+    T *q = y + row * r;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    T mx = T(0);
+    for (int64_t j = threadIdx.x; j < r; j += kSBlock) mx = p[j] > mx ? p[j] : mx;
+    mx = wave_reduce(mx, [](T a, T b) { return b > a ? b : a; });
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = red[0];
+    for (int w = 1; w < kSBlock / 64; w++) mx = red[w] > mx ? red[w] : mx;
+    __syncthreads();
+    T s = T(0);
+    for (int64_t j = threadIdx.x; j < r; j += kSBlock) s = s + exp_elem<T>(p[j] - mx, tab);
+    s = wave_reduce(s, [](T a, T b) { return a + b; });
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    s = red[0];
+    for (int w = 1; w < kSBlock / 64; w++) s = s + red[w];
+    for (int64_t j = threadIdx.x; j < r; j += kSBlock) q[j] = exp_elem<T>(p[j] - mx, tab) / s;
+}
+
+// inner > 1: one thread per (outer, inner) column, coalesced along inner.
+// The sum runs serially along the axis, in the reference's order.
+template <typename T>
+__global__ __launch_bounds__(kSBlock) void k_softmax_cols(const T *__restrict__ x, T *__restrict__ y, int64_t outer,
+                                                          int64_t r, int64_t inner) {
+    __shared__ ExpTable tab;
+    if constexpr (std::is_same<T, float>::value) exp_table_fill(tab);
+    __syncthreads();
+    const int64_t ncol = outer * inner;
+    for (int64_t c = (int64_t)blockIdx.x * kSBlock + threadIdx.x; c < ncol; c += (int64_t)gridDim.x * kSBlock) {
+        const int64_t o = c / inner, i = c - o * inner;
+        const T *p = x + o * r * inner + i;
+        T *q = y + o * r * inner + i;
+        T mx = T(0);
+        for (int64_t j = 0; j < r; j++) {
+            T v = p[j * inner];
+            mx = v > mx ? v : mx;
+        }
+        T s = T(0);
+        for (int64_t j = 0; j < r; j++) s = s + exp_elem<T>(p[j * inner] - mx, tab);
+        for (int64_t j = 0; j < r; j++) q[j * inner] = exp_elem<T>(p[j * inner] - mx, tab) / s;
+    }
+}
+
+template <typename T, int V, bool MASK>
+static hipError_t softmax_wave_dispatch(const SoftmaxArgs &a, hipStream_t s) {
+    const int r = (int)a.r;
+    const int nv = (r + 64 * V - 1) / (64 * V);
+    const int g = (int)((a.outer + kSBlock / 64 - 1) / (kSBlock / 64));
+    const T *x = (const T *)a.x;
+    T *y = (T *)a.y;
+    const T *m = (const T *)a.mask;
+#define LX_SM_CASE(N)                                                                                        \
+    case N:                                                                                                  \
+        hipLaunchKernelGGL((k_softmax_wave<T, V, N, MASK>), dim3(g), dim3(kSBlock), 0, s, x, y, a.outer, r, m, \
+                           a.mask_inner, a.mask_rows);                                                       \
+        break;
+    switch (nv) {
+        LX_SM_CASE(1) LX_SM_CASE(2) LX_SM_CASE(3) LX_SM_CASE(4) LX_SM_CASE(5) LX_SM_CASE(6) LX_SM_CASE(7) LX_SM_CASE(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef LX_SM_CASE
+    return hipGetLastError();
+}
+
+template <typename T>
+static hipError_t softmax_typed(const SoftmaxArgs &a, hipStream_t s) {
+    constexpr int VW = VecWidth<T>::value;
+    const bool wave_ok = a.inner == 1 && a.r <= 64 * VW * 8 && a.outer < (1ll << 31);
+    if (wave_ok) {
+        if (a.vec > 1 && a.r % VW == 0) {
+            if (a.mask) return softmax_wave_dispatch<T, VW, true>(a, s);
+            return softmax_wave_dispatch<T, VW, false>(a, s);
+        }
+        if (a.r <= 64 * 8) {
+            if (a.mask) return softmax_wave_dispatch<T, 1, true>(a, s);
+            return softmax_wave_dispatch<T, 1, false>(a, s);
+        }
+    }
+    if (a.mask) return hipErrorInvalidValue;  // the host falls back to Add + Softmax
+    if (a.inner == 1) {
+        hipLaunchKernelGGL((k_softmax_block<T>), dim3((unsigned)a.outer), dim3(kSBlock), 0, s, (const T *)a.x, (T *)a.y,
+                           a.r);
+    } else {
+        int64_t ncol = a.outer * a.inner;
+        int64_t g = (ncol + kSBlock - 1) / kSBlock;
+        if (g > 8192) g = 8192;
+        hipLaunchKernelGGL((k_softmax_cols<T>), dim3((unsigned)g), dim3(kSBlock), 0, s, (const T *)a.x, (T *)a.y,
+                           a.outer, a.r, a.inner);
+    }
+    return hipGetLastError();
+}
+
+// True when launch_softmax can apply the mask inside the kernel.
+bool softmax_mask_fusable(int dtype, int64_t r, int64_t inner, int64_t outer, int vec) {
+    const int vw = dtype == kFloat ? 4 : 2;
+    if (inner != 1 || outer >= (1ll << 31) || r > 64 * vw * 8) return false;
+    return (vec > 1 && r % vw == 0) || r <= 64 * 8;
+}
+
+hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s) {
+    if (a.outer * a.r * a.inner == 0) return hipSuccess;
+    if (a.dtype == kFloat) return softmax_typed<float>(a, s);
+    if (a.dtype == kDouble) return softmax_typed<double>(a, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace lx

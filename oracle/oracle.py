@@ -1,0 +1,197 @@
+"""TEST INFRASTRUCTURE ONLY -- ctypes front of the CPU oracle (lonnx_oracle.c).
+
+The oracle is a C restatement of the Lokad.Onnx C# CPU operators (see the file
+header of lonnx_oracle.c for the reference lines each function follows).  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this
+module; the product package never does.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_build", "liblonnx_oracle.so")
+
+# TensorElementType codes (Tensor.cs:31-50)
+FLOAT, UINT8, INT8, UINT16, INT16, INT32, INT64, BOOL, DOUBLE, UINT32, UINT64 = 1, 2, 3, 4, 5, 6, 7, 9, 11, 12, 13
+NP_OF = {FLOAT: np.float32, UINT8: np.uint8, INT8: np.int8, UINT16: np.uint16, INT16: np.int16,
+         INT32: np.int32, INT64: np.int64, BOOL: np.bool_, DOUBLE: np.float64, UINT32: np.uint32,
+         UINT64: np.uint64}
+CODE_OF = {np.dtype(v): k for k, v in NP_OF.items()}
+
+ADD, SUB, MUL, DIV, POW = 0, 1, 2, 3, 4
+SQRT, ERF, NEG, EXP = 0, 1, 2, 3
+RSUM, RMEAN, RMAX = 0, 1, 2
+
+OK, ERR_CANNOT_BROADCAST, ERR_NOT_SUPPORTED, ERR_ATTRIBUTE_NOT_SUPPORTED = 0, 3, 5, 6
+ERR_INVALID_ARGUMENT, ERR_DIVIDE_BY_ZERO, ERR_OVERFLOW, ERR_OUT_OF_MEMORY = 8, 9, 10, 11
+
+MAX_RANK = 8
+
+
+class OracleError(Exception):
+    def __init__(self, status, msg=""):
+        super().__init__(f"oracle status {status} {msg}")
+        self.status = status
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library not built: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        i64p = ctypes.POINTER(ctypes.c_int64)
+        ip = ctypes.POINTER(ctypes.c_int)
+        vp = ctypes.c_void_p
+        L.lxo_broadcast_shape.argtypes = [ctypes.c_int, i64p, ctypes.c_int, i64p, ip, i64p]
+        L.lxo_op_binary.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, i64p, vp, ctypes.c_int, i64p, vp,
+                                    vp, ip, i64p, i64p]
+        L.lxo_binary.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, vp, vp, vp, i64p]
+        L.lxo_unary.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, vp, vp]
+        L.lxo_cast.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int64, vp, vp]
+        L.lxo_reduce.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, i64p, vp, ctypes.c_int, i64p,
+                                 ctypes.c_int, vp, ip, i64p]
+        L.lxo_softmax.argtypes = [ctypes.c_int, ctypes.c_int, i64p, vp, ctypes.c_int, vp]
+        L.lxo_erf_f32.argtypes = [ctypes.c_float]
+        L.lxo_erf_f32.restype = ctypes.c_float
+        L.lxo_erf_f64.argtypes = [ctypes.c_double]
+        L.lxo_erf_f64.restype = ctypes.c_double
+        L.lxo_expf.argtypes = [ctypes.c_float]
+        L.lxo_expf.restype = ctypes.c_float
+        L.lxo_powf.argtypes = [ctypes.c_float, ctypes.c_float]
+        L.lxo_powf.restype = ctypes.c_float
+        _lib = L
+    return _lib
+
+
+def _dims(shape):
+    arr = (ctypes.c_int64 * MAX_RANK)(*([int(d) for d in shape] + [0] * (MAX_RANK - len(shape))))
+    return arr
+
+
+def _ptr(a):
+    return ctypes.c_void_p(a.ctypes.data) if a.size else ctypes.c_void_p(0)
+
+
+def broadcast_shape(sa, sb):
+    """ITensor.Broadcast shape rule; returns a tuple or None."""
+    ro = ctypes.c_int(0)
+    do = _dims([])
+    st = lib().lxo_broadcast_shape(len(sa), _dims(sa), len(sb), _dims(sb), ctypes.byref(ro), do)
+    if st != 0:
+        return None
+    return tuple(do[i] for i in range(ro.value))
+
+
+def binary(op, a, b):
+    """CPUExecutionProvider.Add/Sub/Mul/Div/Pow on numpy arrays (same dtype)."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    assert a.dtype == b.dtype
+    code = CODE_OF[a.dtype]
+    shape = broadcast_shape(a.shape, b.shape)
+    if shape is None:
+        raise OracleError(ERR_CANNOT_BROADCAST)
+    out = np.empty(shape, dtype=a.dtype)
+    ro = ctypes.c_int(0)
+    do = _dims([])
+    err = ctypes.c_int64(-1)
+    st = lib().lxo_op_binary(op, code, a.ndim, _dims(a.shape), _ptr(a), b.ndim, _dims(b.shape), _ptr(b),
+                             _ptr(out), ctypes.byref(ro), do, ctypes.byref(err))
+    if st != 0:
+        raise OracleError(st, f"at element {err.value}")
+    return out
+
+
+def unary(op, x):
+    x = np.ascontiguousarray(x)
+    out = np.empty_like(x)
+    st = lib().lxo_unary(op, CODE_OF[x.dtype], x.size, _ptr(x), _ptr(out))
+    if st != 0:
+        raise OracleError(st)
+    return out
+
+
+def cast(x, to_code):
+    x = np.ascontiguousarray(x)
+    out = np.empty(x.shape, dtype=NP_OF[to_code])
+    st = lib().lxo_cast(CODE_OF[x.dtype], to_code, x.size, _ptr(x), _ptr(out))
+    if st != 0:
+        raise OracleError(st)
+    return out
+
+
+def reduce(op, x, axes=None, keepdims=True):
+    """ReduceSum/ReduceMean/ReduceMax; axes None or [] = all axes."""
+    x = np.ascontiguousarray(x)
+    ax = list(axes) if axes is not None else []
+    axarr = (ctypes.c_int64 * max(1, len(ax)))(*ax) if ax else (ctypes.c_int64 * 1)(0)
+    # output buffer large enough for any result shape
+    nred = 1
+    norm = [a + x.ndim if a < 0 else a for a in ax] if ax else list(range(x.ndim))
+    for a in norm:
+        if 0 <= a < x.ndim:
+            nred *= x.shape[a]
+    nout = max(1, x.size // nred if nred else int(np.prod([d for i, d in enumerate(x.shape) if i not in norm])))
+    out = np.empty(nout, dtype=x.dtype)
+    ro = ctypes.c_int(0)
+    do = _dims([])
+    st = lib().lxo_reduce(op, CODE_OF[x.dtype], x.ndim, _dims(x.shape), _ptr(x), len(ax), axarr,
+                          1 if keepdims else 0, _ptr(out), ctypes.byref(ro), do)
+    if st != 0:
+        raise OracleError(st)
+    shape = tuple(do[i] for i in range(ro.value))
+    return out[: int(np.prod(shape)) if shape else 1].reshape(shape)
+
+
+def softmax(x, axis=-1):
+    x = np.ascontiguousarray(x)
+    out = np.empty_like(x)
+    st = lib().lxo_softmax(CODE_OF[x.dtype], x.ndim, _dims(x.shape), _ptr(x), axis, _ptr(out))
+    if st != 0:
+        raise OracleError(st)
+    return out
+
+
+def erf_f32(v):
+    return lib().lxo_erf_f32(float(v))
+
+
+def expf(v):
+    return lib().lxo_expf(float(v))
+
+
+# ---------------------------------------------------------------------------
+# Composite graphs of the BASELINE configs, run op by op exactly as the
+# reference's graph executor would run the ONNX nodes.
+# ---------------------------------------------------------------------------
+def layernorm_decomposed(x, gamma, beta, eps=np.float32(1e-12)):
+    """ReduceMean, Sub, Pow(2), ReduceMean, Add eps, Sqrt, Div, Mul gamma, Add beta."""
+    mean = reduce(RMEAN, x, [-1], True)
+    d = binary(SUB, x, mean)
+    p = binary(POW, d, np.array(2.0, dtype=np.float32))
+    var = reduce(RMEAN, p, [-1], True)
+    ve = binary(ADD, var, np.array(eps, dtype=np.float32))
+    sd = unary(SQRT, ve)
+    nrm = binary(DIV, d, sd)
+    m = binary(MUL, nrm, gamma)
+    return binary(ADD, m, beta)
+
+
+def gelu_erf(x):
+    """Div(x, sqrt2) -> Erf -> Add 1 -> Mul x -> Mul 0.5 (BERT-style GELU subgraph)."""
+    a = binary(DIV, x, np.array(np.float32(np.sqrt(2.0)), dtype=np.float32))
+    e = unary(ERF, a)
+    b = binary(ADD, e, np.array(1.0, dtype=np.float32))
+    c = binary(MUL, x, b)
+    return binary(MUL, c, np.array(0.5, dtype=np.float32))
+
+
+def add_softmax(s, mask, axis=-1):
+    """Add(S, mask) then Softmax(axis)."""
+    return softmax(binary(ADD, s, mask), axis)

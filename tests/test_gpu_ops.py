@@ -1,0 +1,449 @@
+"""GPU parity tests: every operator of the HIP path against the CPU oracle on
+the same seeded inputs, through the C ABI (HipExecutionProvider over ctypes).
+
+Bars (written per test):
+  bit-exact : integer ops, Cast, float Add/Sub/Mul/Div, Sqrt, Erf (expf is
+              bit-identical to the host expf), the fused GELU chain
+  <= 2 ulp  : Pow with a non-2 exponent (device pow vs host powf)
+  reductions: |gpu - ref| <= 1e-5 * sum|x| over the reduced slice (the
+              reference folds serially; any parallel order differs)
+  softmax   : |gpu - ref| <= 1e-5 * |ref| (+1e-30 for underflowed entries)
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from onnx_amd import DeviceTensor, HipExecutionProvider as HIP, OpStatus
+from onnx_amd import _lib as L
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+KATS = json.load(open(os.path.join(HERE, "golden", "reference_kats.json")))
+
+
+def dev(a):
+    return DeviceTensor.from_numpy(np.asarray(a))
+
+
+def ok(r):
+    assert r.Status == OpStatus.Success, r.Message
+    return r.Outputs[0].to_numpy()
+
+
+def ulps(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, -(a & 0x7fffffff), a)
+    b = np.where(b < 0, -(b & 0x7fffffff), b)
+    return np.abs(a - b)
+
+
+def assert_bits(gpu, ref):
+    assert gpu.shape == ref.shape and gpu.dtype == ref.dtype
+    g = gpu.view(np.uint8).reshape(-1)
+    r = ref.view(np.uint8).reshape(-1)
+    if not np.array_equal(g, r):
+        bad = np.flatnonzero(gpu.reshape(-1) != ref.reshape(-1))
+        raise AssertionError(f"{bad.size} mismatches, first at {bad[:5]}: gpu {gpu.reshape(-1)[bad[:5]]} "
+                             f"ref {ref.reshape(-1)[bad[:5]]}")
+
+
+def assert_reduction(gpu, ref, x_abs_sum):
+    assert gpu.shape == ref.shape
+    err = np.abs(gpu.astype(np.float64) - ref.astype(np.float64))
+    tol = 1e-5 * x_abs_sum + 1e-30
+    assert np.all(err <= tol), f"max err {err.max()} tol {tol.reshape(-1)[np.argmax(err)]}"
+
+
+SHAPES = [
+    ((1, 128, 384), (384,)),          # C1 bias
+    ((1, 128, 384), ()),              # scalar
+    ((8, 512, 768), (8, 512, 1)),     # per-row
+    ((8, 512, 768), (768,)),          # gamma
+    ((4, 3, 64, 64), (4, 1, 1, 64)),  # C3 mask pattern
+    ((8, 1, 256), (1, 16, 256)),      # C4 pattern
+    ((7, 5, 33), (5, 1)),             # ragged, outer broadcast
+    ((5, 1), (7, 5, 33)),             # broadcast on A
+    ((1001,), (1001,)),               # odd length
+    ((3, 1, 5), (1, 4, 1)),           # two-sided, odd inner
+    ((2, 3), (0, 1, 3)),              # empty output
+    ((), ()),                          # scalars
+    ((13,), ()),
+    ((), (6, 7)),
+]
+
+
+@pytest.mark.parametrize("sa,sb", SHAPES)
+@pytest.mark.parametrize("op", ["Add", "Sub", "Mul", "Div"])
+def test_float_binary_bit_exact(hip, op, sa, sb):
+    rng = np.random.default_rng(hash((op, sa, sb)) & 0xffff)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    code = {"Add": O.ADD, "Sub": O.SUB, "Mul": O.MUL, "Div": O.DIV}[op]
+    ref = O.binary(code, np.asarray(a), np.asarray(b))
+    got = ok(getattr(HIP, op)(dev(a), dev(b)))
+    assert_bits(got, ref)
+
+
+@pytest.mark.parametrize("op", ["Add", "Sub", "Mul", "Div"])
+def test_double_binary_bit_exact(hip, op):
+    rng = np.random.default_rng(11)
+    a = rng.standard_normal((6, 7, 9))
+    b = rng.standard_normal((7, 1))
+    code = {"Add": O.ADD, "Sub": O.SUB, "Mul": O.MUL, "Div": O.DIV}[op]
+    assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
+
+
+def test_float_special_values(hip):
+    a = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -1e-45, 3.4e38, 1.0, -2.5, 1e-30, 7.0], np.float32)
+    b = np.array([-0.0, 0.0, np.inf, 1.0, 2.0, 1e-40, 3.0, 10.0, 0.0, -0.0, 1e30, 3.0], np.float32)
+    for op, code in [("Add", O.ADD), ("Sub", O.SUB), ("Mul", O.MUL), ("Div", O.DIV)]:
+        assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("op", ["Add", "Sub", "Mul", "Div"])
+def test_int_binary_bit_exact(hip, op, dt):
+    rng = np.random.default_rng(12)
+    info = np.iinfo(dt)
+    a = rng.integers(info.min, info.max, (9, 1, 130), dtype=dt, endpoint=True)
+    b = rng.integers(info.min, info.max, (1, 5, 130), dtype=dt, endpoint=True)
+    if op == "Div":
+        b[b == 0] = 3
+        if dt != np.uint8:
+            a[0, 0, :4] = info.min  # MIN / -1 itself is covered by test_int_div_errors
+    code = {"Add": O.ADD, "Sub": O.SUB, "Mul": O.MUL, "Div": O.DIV}[op]
+    if op == "Div" and dt != np.uint8:
+        b[b == -1] = 5
+    assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
+
+
+def test_int64_div_large_operands(hip):
+    rng = np.random.default_rng(13)
+    a = rng.integers(-(2**62), 2**62, 4099, dtype=np.int64)
+    b = rng.integers(-(2**40), 2**40, 4099, dtype=np.int64)
+    b[b == 0] = 1
+    a[:100] = rng.integers(-(2**20), 2**20, 100)  # 32-bit fast path mixed in
+    b[:50] = rng.integers(1, 1024, 50)
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), O.binary(O.DIV, a, b))
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
+def test_int_div_errors(hip, dt):
+    info = np.iinfo(dt)
+    r = HIP.Div(dev(np.array([4, 5, 6, 7], dt)), dev(np.array([1, 2, 0, 1], dt)))
+    assert r.Status == OpStatus.Failure and r.Code == L.ERR_DIVIDE_BY_ZERO
+    assert "divide by zero" in r.Message
+    r = HIP.Div(dev(np.array([info.min, 5], dt)), dev(np.array([-1, 2], dt)))
+    assert r.Status == OpStatus.Failure and r.Code == L.ERR_OVERFLOW
+    # the first failing element decides, as in the C# loop
+    r = HIP.Div(dev(np.array([info.min, 5], dt)), dev(np.array([-1, 0], dt)))
+    assert r.Code == L.ERR_OVERFLOW
+    r = HIP.Div(dev(np.array([1, info.min], dt)), dev(np.array([0, -1], dt)))
+    assert r.Code == L.ERR_DIVIDE_BY_ZERO
+    # the device flags are reset: the next division succeeds
+    ok(HIP.Div(dev(np.array([4], dt)), dev(np.array([2], dt))))
+
+
+def test_operator_failures_mirror_reference(hip):
+    a = dev(np.ones((1, 3), np.float32))
+    r = HIP.Add(a, dev(np.ones((2,), np.float32)))
+    assert r.Status == OpStatus.Failure and r.Code == L.ERR_CANNOT_BROADCAST
+    assert "not compatible for broadcasting" in r.Message
+    r = HIP.Add(a, dev(np.ones((1, 3), np.float64)))
+    assert r.Code == L.ERR_WRONG_INPUT_TYPE
+    r = HIP.Add(None, a)
+    assert r.Code == L.ERR_MISSING_INPUT and "parameter A" in r.Message
+    r = HIP.Pow(dev(np.ones(3, np.int32)), dev(np.ones(3, np.int32)))
+    assert r.Code == L.ERR_INPUT_TYPE_NOT_SUPPORTED and "Int32" in r.Message
+    r = HIP.Sqrt(dev(np.ones(3, np.int64)))
+    assert r.Code == L.ERR_INPUT_TYPE_NOT_SUPPORTED
+    r = HIP.Cast(a, 10)  # Float16
+    assert r.Code == L.ERR_ATTRIBUTE_NOT_SUPPORTED
+    r = HIP.ReduceMax(dev(np.ones(3, np.int32)), [0])
+    assert r.Code == L.ERR_NOT_SUPPORTED
+    r = HIP.ReduceSum(dev(np.ones((2, 3), np.float32)), [2])
+    assert r.Code == L.ERR_INVALID_ARGUMENT
+    r = HIP.Softmax(dev(np.ones((2, 3), np.float32)), 2)
+    assert r.Code == L.ERR_INVALID_ARGUMENT
+
+
+def test_reference_kats(hip):
+    for k in KATS["broadcast_shape"]:
+        r = HIP.Add(dev(np.ones(k["a"], np.float32)), dev(np.ones(k["b"], np.float32)))
+        if k["out"] is None:
+            assert r.Code == L.ERR_CANNOT_BROADCAST, k["src"]
+        else:
+            y = ok(r)
+            assert y.shape == tuple(k["out"]) and np.all(y == 2.0), k["src"]
+    k = KATS["add_int"]
+    a = np.zeros(k["shape"], np.int32)
+    a[tuple(k["set_index"])] = k["set_value"]
+    c = ok(HIP.Add(dev(a), dev(a)))
+    for e in k["expect"]:
+        assert c[tuple(e["index"])] == e["value"]
+    for name, op in [("sub_f32", "Sub"), ("mul_f32", "Mul"), ("div_f32", "Div")]:
+        k = KATS[name]
+        z = ok(getattr(HIP, op)(dev(np.array(k["x"], np.float32)), dev(np.array(k["y"], np.float32))))
+        np.testing.assert_array_equal(z, np.array(k["z"], np.float32))
+    for k in KATS["pow"]:
+        z = ok(HIP.Pow(dev(np.array(k["x"], np.float32)), dev(np.array(k["y"], np.float32))))
+        np.testing.assert_array_equal(z, np.array(k["z"], np.float32))
+    for k in KATS["softmax"]:
+        y = ok(HIP.Softmax(dev(np.array(k["x"], np.float32)), k["axis"]))
+        np.testing.assert_almost_equal(y, np.array(k["y"], np.float32), decimal=k["decimal"])
+    for k in KATS["reduce_sum_int"]:
+        y = ok(HIP.ReduceSum(dev(np.array(k["data"], np.int32)), k["axes"], k["keepdims"]))
+        np.testing.assert_array_equal(y, np.array(k["out"], np.int32))
+    for k in KATS["reduce_mean_f32"]:
+        y = ok(HIP.ReduceMean(dev(np.array(k["data"], np.float32)), k["axes"], k["keepdims"]))
+        np.testing.assert_almost_equal(y, np.array(k["out"], np.float32), decimal=6)
+    k = KATS["reduce_mean_double"]
+    for c in k["cases"]:
+        y = ok(HIP.ReduceMean(dev(np.array(k["data"], np.float64)), c["axes"]))
+        np.testing.assert_almost_equal(y, np.array(c["out"]))
+    k = KATS["cast_dtypes"]
+    for to in k["to"]:
+        y = ok(HIP.Cast(dev(np.array(k["input"], np.int64)), to))
+        assert y.dtype == np.dtype(O.NP_OF[to])
+
+
+def test_pow(hip):
+    rng = np.random.default_rng(14)
+    x = (rng.uniform(0, 1, 5000) / 2 + 0.5).astype(np.float32)
+    y = (rng.uniform(-1, 1, 5000) / 2 + 0.5).astype(np.float32)
+    got = ok(HIP.Pow(dev(x), dev(y)))
+    assert ulps(got, O.binary(O.POW, x, y)).max() <= 2
+    x2 = rng.standard_normal((64, 768)).astype(np.float32) * 3
+    two = np.array(2.0, np.float32)
+    got2 = ok(HIP.Pow(dev(x2), dev(two)))
+    # exponent 2 evaluates x*x; host powf(x, 2) differs by at most 1 ulp
+    assert ulps(got2, O.binary(O.POW, x2, two)).max() <= 1
+    np.testing.assert_array_equal(got2, x2 * x2)
+    xn = np.array([-2.0, -2.0, 0.0, 0.0, 1.0, np.nan, -1.0, 4.0], np.float32)
+    yn = np.array([3.0, 0.5, -1.0, 0.0, np.nan, 0.0, np.inf, -0.5], np.float32)
+    g, r = ok(HIP.Pow(dev(xn), dev(yn))), O.binary(O.POW, xn, yn)
+    same = (g == r) | (np.isnan(g) & np.isnan(r))
+    assert same.all(), (g, r)
+
+
+def test_sqrt_bit_exact(hip):
+    rng = np.random.default_rng(15)
+    x = np.concatenate([rng.uniform(0, 1e6, 100000), [0.0, -0.0, 1e-45, 1e-40, np.inf, -1.0, np.nan]]).astype(np.float32)
+    assert_bits(ok(HIP.Sqrt(dev(x))), O.unary(O.SQRT, x))
+    bits = np.arange(0, 1 << 31, 4093, dtype=np.uint32).view(np.float32)  # positive floats, all exponents
+    assert_bits(ok(HIP.Sqrt(dev(bits))), O.unary(O.SQRT, bits))
+
+
+def test_erf_bit_exact(hip):
+    rng = np.random.default_rng(16)
+    x = np.concatenate([rng.standard_normal(200000) / np.sqrt(2), np.linspace(-6, 6, 50001),
+                        [0.0, -0.0, 1e-6, -1e-6, 1e-40, np.inf, -np.inf, np.nan, 9.5, -9.5, 1e-3]]).astype(np.float32)
+    got = ok(HIP.Erf(dev(x)))
+    ref = O.unary(O.ERF, x)
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all(), f"{(~same).sum()} mismatches, max ulp {ulps(got[~same], ref[~same]).max()}"
+    bits = np.arange(0, 1 << 32, 65521, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    g2, r2 = ok(HIP.Erf(dev(bits))), O.unary(O.ERF, bits)
+    same = (g2.view(np.uint32) == r2.view(np.uint32)) | (np.isnan(g2) & np.isnan(r2))
+    assert same.all()
+
+
+def test_erf_double(hip):
+    x = np.linspace(-5, 5, 10001)
+    got = ok(HIP.Erf(dev(x)))
+    ref = O.unary(O.ERF, x)
+    assert np.max(np.abs(got - ref)) <= 1e-15  # device exp vs host exp inside the double formula
+
+
+CAST_TYPES = [O.FLOAT, O.DOUBLE, O.UINT8, O.INT8, O.UINT16, O.INT16, O.INT32, O.UINT32, O.INT64, O.UINT64, O.BOOL]
+
+
+def _cast_inputs(src, rng):
+    dt = np.dtype(O.NP_OF[src])
+    if dt == np.bool_:
+        return rng.integers(0, 2, 517).astype(np.bool_)
+    if dt.kind == "f":
+        return np.concatenate([rng.uniform(-3, 300, 500), [0.5, 1.5, 2.5, -0.5, -0.4, 254.5, 255.5]]).astype(dt)
+    info = np.iinfo(dt)
+    lo, hi = max(info.min, -200), min(info.max, 300)
+    return rng.integers(lo, hi, 517, dtype=dt, endpoint=True)
+
+
+@pytest.mark.parametrize("src", CAST_TYPES)
+def test_cast_matrix(hip, src):
+    rng = np.random.default_rng(17 + src)
+    x = _cast_inputs(src, rng)
+    for dst in CAST_TYPES:
+        r = HIP.Cast(dev(x), dst)
+        try:
+            ref = O.cast(x, dst)
+        except O.OracleError as e:
+            assert r.Status == OpStatus.Failure and r.Code == e.status, (src, dst)
+            continue
+        assert_bits(ok(r), ref)
+
+
+def test_cast_int64_to_float_rounding(hip):
+    rng = np.random.default_rng(18)
+    x = rng.integers(-(2**62), 2**62, 100000, dtype=np.int64)
+    x[:1000] = rng.integers(-(2**25), 2**25, 1000)
+    x[1000:1010] = [2**24 + 1, 2**24 + 3, 2**53 + 1, -(2**53) - 3, 2**63 - 1, -(2**63), 0, -1, 1, 2**25 + 2]
+    assert_bits(ok(HIP.Cast(dev(x), O.FLOAT)), O.cast(x, O.FLOAT))
+
+
+def test_cast_overflow_errors(hip):
+    for vals, dt, to in [([1.0, 2147483647.5], np.float64, O.INT32), ([np.nan], np.float32, O.INT64),
+                         ([300], np.int32, O.UINT8), ([-1], np.int64, O.UINT64), ([2**40], np.int64, O.INT32)]:
+        r = HIP.Cast(dev(np.array(vals, dt)), to)
+        assert r.Status == OpStatus.Failure and r.Code == L.ERR_OVERFLOW, (vals, to)
+        assert "too large or too small" in r.Message
+
+
+REDUCE_CASES = [
+    ((64, 768), [-1]),
+    ((8, 512, 768), [-1]),
+    ((3, 50000), [1]),            # long rows, split path
+    ((2, 700001), [1]),           # long ragged rows
+    ((16, 300, 64), [1]),         # strided middle axis
+    ((4, 4096, 33), [1]),         # ragged inner
+    ((256, 64, 256), [1]),
+    ((5, 6, 7, 8), [0, 2]),       # two passes
+    ((5, 6, 7, 8), [3, 1]),
+    ((4, 5, 6), None),            # all axes
+    ((3000000,), None),           # full reduction, split
+    ((7, 1, 9), [1]),             # size-1 reduced axis
+    ((6, 0, 4), [1]),             # empty reduced axis
+]
+
+
+@pytest.mark.parametrize("shape,axes", REDUCE_CASES)
+@pytest.mark.parametrize("kd", [1, 0])
+def test_reduce_float(hip, shape, axes, kd):
+    rng = np.random.default_rng(19)
+    x = rng.uniform(-1, 1, shape).astype(np.float32)
+    ax = tuple(range(len(shape))) if axes is None else tuple(a % len(shape) for a in axes)
+    absum = np.abs(x.astype(np.float64)).sum(axis=ax, keepdims=bool(kd))
+    for name, code in [("ReduceSum", O.RSUM), ("ReduceMean", O.RMEAN), ("ReduceMax", O.RMAX)]:
+        got = ok(getattr(HIP, name)(dev(x), axes, kd))
+        ref = O.reduce(code, x, axes, bool(kd))
+        if name == "ReduceMax":
+            assert_bits(got, ref)
+        elif name == "ReduceMean":
+            r = max(1, int(np.prod([shape[a] for a in ax])))
+            if 0 in shape:
+                assert got.shape == ref.shape
+                np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+            else:
+                assert_reduction(got, ref, absum / r)
+        else:
+            assert_reduction(got, ref, absum)
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
+@pytest.mark.parametrize("shape,axes", [((64, 256, 40), [1]), ((9, 777), [-1]), ((3, 4, 5, 6), [0, 2]), ((2, 300000), None),
+                                        ((2, 5, 3), [1])])
+def test_reduce_int_exact(hip, dt, shape, axes):
+    rng = np.random.default_rng(20)
+    info = np.iinfo(dt)
+    x = rng.integers(info.min // 2, info.max // 2, shape, dtype=dt)
+    for name, code in [("ReduceSum", O.RSUM), ("ReduceMean", O.RMEAN)]:
+        assert_bits(ok(getattr(HIP, name)(dev(x), axes)), O.reduce(code, x, axes, True))
+
+
+def test_reduce_double(hip):
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((33, 1000, 17))
+    for name, code in [("ReduceSum", O.RSUM), ("ReduceMean", O.RMEAN), ("ReduceMax", O.RMAX)]:
+        got = ok(getattr(HIP, name)(dev(x), [1]))
+        ref = O.reduce(code, x, [1], True)
+        np.testing.assert_allclose(got, ref, rtol=0, atol=1e-12)
+
+
+def test_reduce_max_seed_zero_and_nan(hip):
+    x = np.array([[-3, -1, -2], [1, np.nan, 5], [np.nan, np.nan, -1]], np.float32)
+    assert_bits(ok(HIP.ReduceMax(dev(x), [1])), O.reduce(O.RMAX, x, [1], True))
+
+
+@pytest.mark.parametrize("shape,axis", [((64, 512), -1), ((5, 12, 77, 128), -1), ((10, 2048), -1), ((4, 3001), 1),
+                                        ((3, 4, 5), 0), ((6, 100, 7), 1), ((2, 3, 1000), 1), ((9, 3), -1)])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_softmax(hip, shape, axis, dt):
+    rng = np.random.default_rng(22)
+    x = (rng.standard_normal(shape) * 3).astype(dt)
+    got = ok(HIP.Softmax(dev(x), axis))
+    ref = O.softmax(x, axis)
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * np.abs(ref) + 1e-30), err.max()
+
+
+def test_softmax_default_axis_and_masked_rows(hip):
+    x = np.full((4, 64), -20000.0, np.float32)  # every row below the seed 0 of ReduceMax
+    x[1, 3] = 5.0
+    got = ok(HIP.Softmax(dev(x)))
+    ref = O.softmax(x, -1)
+    assert_bits(got, ref)  # exp underflows to exactly 0 or the row is one-hot
+
+
+@pytest.mark.parametrize("s_shape,m_shape", [((4, 3, 64, 512), (4, 1, 1, 512)), ((2, 3, 5, 96), (3, 1, 96)),
+                                             ((2, 8, 128), (8, 1)), ((6, 77), (77,)), ((3, 4, 5, 6), (3, 4, 5, 6)),
+                                             ((2, 2, 4000), (2, 1, 4000))])
+def test_add_softmax(hip, s_shape, m_shape):
+    rng = np.random.default_rng(23)
+    s = (rng.standard_normal(s_shape) * 3).astype(np.float32)
+    m = np.where(rng.uniform(size=m_shape) < 0.125, -10000.0, 0.0).astype(np.float32)
+    got = ok(HIP.AddSoftmax(dev(s), dev(m), -1))
+    ref = O.add_softmax(s, m, -1)
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * np.abs(ref) + 1e-30), err.max()
+
+
+def test_gelu_chain_bit_exact(hip):
+    rng = np.random.default_rng(24)
+    x = np.concatenate([rng.standard_normal(300001), [0.0, -0.0, 1e-7, -8.0, 8.0, np.inf, -np.inf]]).astype(np.float32)
+    assert_bits(ok(HIP.GeluErf(dev(x))), O.gelu_erf(x))
+    # the same chain op by op through the C ABI
+    sq2 = np.array(np.float32(np.sqrt(2.0)), np.float32)
+    a = ok(HIP.Div(dev(x), dev(sq2)))
+    e = ok(HIP.Erf(dev(a)))
+    b = ok(HIP.Add(dev(e), dev(np.array(1.0, np.float32))))
+    c = ok(HIP.Mul(dev(x), dev(b)))
+    y = ok(HIP.Mul(dev(c), dev(np.array(0.5, np.float32))))
+    assert_bits(y, O.gelu_erf(x))
+
+
+@pytest.mark.parametrize("shape", [(8, 512, 768), (3, 5, 1024), (7, 4096), (4, 12), (2, 3, 770)])
+def test_layernorm(hip, shape):
+    rng = np.random.default_rng(25)
+    r = shape[-1]
+    x = (rng.standard_normal(shape) * 2).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(r)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(r)).astype(np.float32)
+    got = ok(HIP.LayerNormDecomposed(dev(x), dev(g), dev(b), 1e-12))
+    ref = O.layernorm_decomposed(x, g, b, np.float32(1e-12))
+    # mean / variance are sums in a different order: 1e-5 relative to max(1, |y|)
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * np.maximum(1.0, np.abs(ref))), err.max()
+
+
+def test_output_reuse_and_capacity(hip):
+    a = dev(np.arange(12, dtype=np.float32).reshape(3, 4))
+    out = DeviceTensor.empty((3, 4), np.float32)
+    r = HIP.Add(a, a, out=out)
+    assert r.Status == OpStatus.Success and r.Outputs[0].h.data == out.h.data
+    np.testing.assert_array_equal(out.to_numpy(), 2 * np.arange(12, dtype=np.float32).reshape(3, 4))
+    small = DeviceTensor.empty((2,), np.float32)
+    r = HIP.Add(a, a, out=small)
+    assert r.Code == L.ERR_BUFFER_TOO_SMALL
+
+
+def test_reshape_alias(hip):
+    a = dev(np.arange(24, dtype=np.float32))
+    v = a.reshape((2, 3, 4))
+    assert v.shape == (2, 3, 4) and v.h.data == a.h.data
+    y = ok(HIP.ReduceSum(v, [2], 0))
+    np.testing.assert_array_equal(y, np.arange(24, dtype=np.float32).reshape(2, 3, 4).sum(2))
