@@ -34,7 +34,7 @@ if ROOT not in sys.path:
 PEAK_HBM_GBS = 8000.0
 LN_SHAPE = (8, 512, 768)
 # algorithmic bytes of the fused LayerNorm: X read + Y written + gamma + beta
-LN_BYTES = 2 * 8 * 512 * 768 * 4 + 2 * 768 * 4 + 4  # 25,172,000 (eps counted as 4 bytes)
+LN_BYTES = 2 * 8 * 512 * 768 * 4 + 2 * 768 * 4 + 4  # 25,171,972 (X + Y + gamma + beta + eps)
 LN_SETS = 16
 
 
@@ -42,13 +42,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+EAGER = False
+
+
 def graph_time(torch, launch, steps, warmup, set_stream):
     """Run `launch(i)` warmup times eagerly, capture `steps` launches in a HIP
     graph, replay it once untimed, then time one replay with HIP events.
-    Returns milliseconds per step."""
+    Returns milliseconds per step.  With EAGER (--eager, used under rocprofv3
+    counter collection) the steps run as ordinary launches instead."""
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
+    if EAGER:
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            launch(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -69,6 +82,19 @@ def graph_time(torch, launch, steps, warmup, set_stream):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def measured_traffic():
+    """HBM bytes per LayerNorm launch from the committed rocprofv3 counter
+    summary (profiles/k_layernorm_c2_traffic.txt), or None when absent."""
+    path = os.path.join(ROOT, "profiles", "k_layernorm_c2_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline_ln(target_s=10.0):
@@ -239,7 +265,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--all", action="store_true", help="also measure every BASELINE config op")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--eager", action="store_true", help="time ordinary launches instead of a HIP graph")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 256 MiB device copy (Cast float->float) 4 times, the known-size "
+                         "reference for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
               file=sys.stderr)
@@ -271,6 +303,13 @@ def main():
 
     ms = graph_time(torch, step, args.steps, args.warmup, set_stream)
     gbs = LN_BYTES / (ms * 1e-3) / 1e9
+    if args.copy_calibration:
+        src = torch.randn(64 * 1024 * 1024, device=dev, generator=gen)
+        dst = torch.empty_like(src)
+        ws, wd = DeviceTensor.wrap_torch(src), DeviceTensor.wrap_torch(dst)
+        for _ in range(4):
+            HIP.Cast(ws, 1, out=wd)
+        torch.cuda.synchronize()
     out = {
         "metric": "achieved HBM GB/s (% of MI355X peak) per op + elements/s vs C# CPU path",
         "value": round(gbs, 2),
@@ -288,7 +327,7 @@ def main():
                    "algorithmic_bytes_per_step": LN_BYTES, "buffer_sets": LN_SETS,
                    "elements_per_s": round(8 * 512 * 768 / (ms * 1e-3), 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": None},
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic()},
     }
     if args.all:
         res = bench_all(torch, HIP, DeviceTensor, set_stream, args.steps, args.warmup)

@@ -371,6 +371,11 @@ int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
         const int64_t inner = p.dims[p.rank - 1];
         args.a_inner = p.a_strides[p.rank - 1] != 0;
         args.b_inner = p.b_strides[p.rank - 1] != 0;
+        args.a_once = args.b_once = 1;
+        for (int i = 0; i < p.rank; i++) {
+            if (p.a_strides[i] == 0) args.a_once = 0;
+            if (p.b_strides[i] == 0) args.b_once = 0;
+        }
         args.vec = (al && inner % V == 0) ? (int)V : 1;
         nd_layout(p, args.vec, args.nd, &args);
         break;
@@ -525,7 +530,7 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         const int64_t V = 16 / es;
         const bool al = aligned16(src);
         ra.vec = (al && ((inner == 1 && r % V == 0) || (inner > 1 && inner % V == 0))) ? (int)V : 1;
-        int64_t wsb = reduce_workspace_bytes(dt, outer, r, inner);
+        int64_t wsb = reduce_workspace_bytes(dt, outer, r, inner, ra.vec);
         if ((result = ensure_workspace(wsb))) break;
         ra.workspace = g.workspace;
         ra.ws_bytes = g.ws_bytes;

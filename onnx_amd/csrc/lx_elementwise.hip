@@ -6,9 +6,10 @@
 // (Tensor.cs:1605-1613): broadcast operands are read in place through stride-0
 // addressing instead of being copied.
 //
-// Memory-bound design: every lane moves 16 bytes per access (dwordx4), a block
-// of 256 lanes (4 waves of 64) walks the arrays with a grid stride, and each
-// lane keeps UNROLL independent loads in flight before computing.
+// Memory-bound design: every lane moves 16 bytes per access (dwordx4) with
+// nontemporal loads and stores, and the grid covers the whole array with one
+// vector per lane (measured faster on MI355X than grid-stride loops with
+// several loads in flight per lane).
 #include <limits>
 #include <type_traits>
 
@@ -20,7 +21,7 @@
 namespace lx {
 
 constexpr int kBlock = 256;
-constexpr int kMaxBlocks = 8192;
+constexpr int kMaxBlocks = 1 << 24;  // beyond this the kernels loop
 
 template <int CODE> struct CType;
 template <> struct CType<kFloat> { using T = float; };
@@ -123,38 +124,24 @@ __device__ __forceinline__ T bin_apply(T l, T r, uint64_t idx, ErrFlags *e) {
 }
 
 // SAME / SCALAR_A / SCALAR_B: dense output walk with 16-byte vectors.
-template <int OP, typename T, int LAYOUT, int V, int U>
+template <int OP, typename T, int LAYOUT, int V>
 __global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a, const T *__restrict__ b,
                                                         T *__restrict__ y, int64_t n, ErrFlags *errs) {
     const int64_t nv = n / V;
     T sa = T(), sb = T();
     if constexpr (LAYOUT == kScalarA) sa = a[0];
     if constexpr (LAYOUT == kScalarB) sb = b[0];
-    const int64_t step = (int64_t)gridDim.x * kBlock * U;
-    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < nv; base += step) {
-        Vec<T, V> va[U], vb[U];
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kBlock) {
+        Vec<T, V> va, vb, vy;
+        if constexpr (LAYOUT != kScalarA) va = vload_nt<T, V>(a + i * V);
+        if constexpr (LAYOUT != kScalarB) vb = vload_nt<T, V>(b + i * V);
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int64_t i = base + (int64_t)u * kBlock;
-            if (i < nv) {
-                if constexpr (LAYOUT != kScalarA) va[u] = vload<T, V>(a + i * V);
-                if constexpr (LAYOUT != kScalarB) vb[u] = vload<T, V>(b + i * V);
-            }
+        for (int k = 0; k < V; k++) {
+            T l = (LAYOUT == kScalarA) ? sa : va.v[k];
+            T r = (LAYOUT == kScalarB) ? sb : vb.v[k];
+            vy.v[k] = bin_apply<OP, T>(l, r, (uint64_t)(i * V + k), errs);
         }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            int64_t i = base + (int64_t)u * kBlock;
-            if (i < nv) {
-                Vec<T, V> vy;
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    T l = (LAYOUT == kScalarA) ? sa : va[u].v[k];
-                    T r = (LAYOUT == kScalarB) ? sb : vb[u].v[k];
-                    vy.v[k] = bin_apply<OP, T>(l, r, (uint64_t)(i * V + k), errs);
-                }
-                vstore<T, V>(y + i * V, vy);
-            }
-        }
+        vstore_nt<T, V>(y + i * V, vy);
     }
     const int64_t tail = n - nv * V;
     if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
@@ -168,9 +155,12 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a,
 // General broadcast: output row-major [rows, inner]; operands addressed via
 // per-axis strides (0 on broadcast axes).  AIN/BIN: innermost axis contiguous
 // (1) or broadcast (0) for A/B.  32-bit vector index with fast division.
+// a_nt / b_nt: the operand is read exactly once (no broadcast axis), so it is
+// streamed with nontemporal loads; broadcast operands are re-read and must stay
+// cacheable.
 template <int OP, typename T, int AIN, int BIN, int V>
 __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, const T *__restrict__ b,
-                                                      T *__restrict__ y, uint32_t nv, NdLayout L,
+                                                      T *__restrict__ y, uint32_t nv, NdLayout L, int a_nt, int b_nt,
                                                       ErrFlags *errs) {
     for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += gridDim.x * kBlock) {
         uint32_t row = fdiv(v, L.inner_v);
@@ -189,13 +179,13 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, c
         }
         const int64_t col = (int64_t)cv * V;
         Vec<T, V> va, vb, vy;
-        if constexpr (AIN) va = vload<T, V>(a + ao + col);
+        if constexpr (AIN) va = a_nt ? vload_nt<T, V>(a + ao + col) : vload<T, V>(a + ao + col);
         else {
             T s = a[ao];
 #pragma unroll
             for (int k = 0; k < V; k++) va.v[k] = s;
         }
-        if constexpr (BIN) vb = vload<T, V>(b + bo + col);
+        if constexpr (BIN) vb = b_nt ? vload_nt<T, V>(b + bo + col) : vload<T, V>(b + bo + col);
         else {
             T s = b[bo];
 #pragma unroll
@@ -204,7 +194,7 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, c
 #pragma unroll
         for (int k = 0; k < V; k++)
             vy.v[k] = bin_apply<OP, T>(va.v[k], vb.v[k], (uint64_t)v * V + k, errs);
-        vstore<T, V>(y + (int64_t)v * V, vy);
+        vstore_nt<T, V>(y + (int64_t)v * V, vy);
     }
 }
 
@@ -241,26 +231,25 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
     const T *a = (const T *)A.a;
     const T *b = (const T *)A.b;
     T *y = (T *)A.y;
-    constexpr int U = 4;
     if (A.layout != kNd) {
         int64_t nv = A.n / V;
-        int g = grid_for(nv > 0 ? nv : 1, kBlock * U);
+        int g = grid_for(nv > 0 ? nv : 1, kBlock);
         switch (A.layout) {
-        case kSame: hipLaunchKernelGGL((k_binary_flat<OP, T, kSame, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
-        case kScalarA: hipLaunchKernelGGL((k_binary_flat<OP, T, kScalarA, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
-        default: hipLaunchKernelGGL((k_binary_flat<OP, T, kScalarB, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
+        case kSame: hipLaunchKernelGGL((k_binary_flat<OP, T, kSame, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
+        case kScalarA: hipLaunchKernelGGL((k_binary_flat<OP, T, kScalarA, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
+        default: hipLaunchKernelGGL((k_binary_flat<OP, T, kScalarB, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, A.n, errs); break;
         }
         return hipGetLastError();
     }
     const int64_t nv = A.n / V;
-    const int g = grid_for(nv, kBlock * 4);
+    const int g = grid_for(nv, kBlock);
     const int key = A.a_inner * 2 + A.b_inner;
     if (nv < (1ll << 31)) {
         switch (key) {
-        case 3: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
-        case 2: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
-        case 1: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
-        default: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, errs); break;
+        case 3: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        case 2: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        case 1: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        default: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
         }
     } else {
         switch (key) {
@@ -325,7 +314,7 @@ __device__ __forceinline__ T un_apply(T x, const ExpTable &tab) {
     }
 }
 
-template <int OP, typename T, int V, int U>
+template <int OP, typename T, int V>
 __global__ __launch_bounds__(kBlock) void k_unary(const T *__restrict__ x, T *__restrict__ y, int64_t n) {
     __shared__ ExpTable tab;
     constexpr bool kNeedTab = (OP == kErf || OP == kExp) && std::is_same<T, float>::value;
@@ -334,24 +323,11 @@ __global__ __launch_bounds__(kBlock) void k_unary(const T *__restrict__ x, T *__
         __syncthreads();
     }
     const int64_t nv = n / V;
-    const int64_t step = (int64_t)gridDim.x * kBlock * U;
-    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < nv; base += step) {
-        Vec<T, V> vx[U];
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kBlock) {
+        Vec<T, V> vx = vload_nt<T, V>(x + i * V), vy;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int64_t i = base + (int64_t)u * kBlock;
-            if (i < nv) vx[u] = vload<T, V>(x + i * V);
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            int64_t i = base + (int64_t)u * kBlock;
-            if (i < nv) {
-                Vec<T, V> vy;
-#pragma unroll
-                for (int k = 0; k < V; k++) vy.v[k] = un_apply<OP, T>(vx[u].v[k], tab);
-                vstore<T, V>(y + i * V, vy);
-            }
-        }
+        for (int k = 0; k < V; k++) vy.v[k] = un_apply<OP, T>(vx.v[k], tab);
+        vstore_nt<T, V>(y + i * V, vy);
     }
     const int64_t tail = n - nv * V;
     if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
@@ -362,14 +338,13 @@ __global__ __launch_bounds__(kBlock) void k_unary(const T *__restrict__ x, T *__
 
 template <int OP, typename T>
 static hipError_t unary_typed(const void *x, void *y, int64_t n, int vec, hipStream_t s) {
-    constexpr int U = 4;
     if (vec > 1) {
         constexpr int V = VecWidth<T>::value;
-        int g = grid_for(n / V, kBlock * U);
-        hipLaunchKernelGGL((k_unary<OP, T, V, U>), dim3(g), dim3(kBlock), 0, s, (const T *)x, (T *)y, n);
+        int g = grid_for(n / V > 0 ? n / V : 1, kBlock);
+        hipLaunchKernelGGL((k_unary<OP, T, V>), dim3(g), dim3(kBlock), 0, s, (const T *)x, (T *)y, n);
     } else {
-        int g = grid_for(n, kBlock * U);
-        hipLaunchKernelGGL((k_unary<OP, T, 1, U>), dim3(g), dim3(kBlock), 0, s, (const T *)x, (T *)y, n);
+        int g = grid_for(n, kBlock);
+        hipLaunchKernelGGL((k_unary<OP, T, 1>), dim3(g), dim3(kBlock), 0, s, (const T *)x, (T *)y, n);
     }
     return hipGetLastError();
 }
@@ -478,11 +453,11 @@ __global__ __launch_bounds__(kBlock) void k_cast(const typename CType<SRC>::T *_
     const int64_t nv = n / E;
     bool ovf = false;
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kBlock) {
-        Vec<S, E> vx = vload<S, E>(x + i * E);
+        Vec<S, E> vx = vload_nt<S, E>(x + i * E);
         Vec<D, E> vy;
 #pragma unroll
         for (int k = 0; k < E; k++) vy.v[k] = cast_apply<SRC, DST>(vx.v[k], ovf);
-        vstore<D, E>(y + i * E, vy);
+        vstore_nt<D, E>(y + i * E, vy);
     }
     const int64_t tail = n - nv * E;
     if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
@@ -498,10 +473,10 @@ static hipError_t cast_typed(const void *x, void *y, int64_t n, int vec, ErrFlag
     using D = typename CType<DST>::T;
     constexpr int E = 16 / (sizeof(S) > sizeof(D) ? sizeof(S) : sizeof(D));
     if (vec > 1) {
-        int g = grid_for(n / E, kBlock * 4);
+        int g = grid_for(n / E > 0 ? n / E : 1, kBlock);
         hipLaunchKernelGGL((k_cast<SRC, DST, E>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);
     } else {
-        int g = grid_for(n, kBlock * 4);
+        int g = grid_for(n, kBlock);
         hipLaunchKernelGGL((k_cast<SRC, DST, 1>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);
     }
     return hipGetLastError();
@@ -550,38 +525,24 @@ hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int 
 //   y = c * 0.5f (Mul)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float gelu_apply(float x, const ExpTable &tab) {
-    const float kSqrt2 = 1.41421353816986083984375f;  // float32(sqrt(2))
-    float a = x / kSqrt2;
-    float e = erf_lx(a, tab);
+    float a = div_sqrt2f_lx(x);  // == x / 1.4142135f, float32(sqrt(2))
+    float e = erf_fast_lx(a, tab);
     float b = e + 1.0f;
     float c = x * b;
     return c * 0.5f;
 }
 
-template <int V, int U>
+template <int V>
 __global__ __launch_bounds__(kBlock) void k_gelu_erf(const float *__restrict__ x, float *__restrict__ y, int64_t n) {
     __shared__ ExpTable tab;
     exp_table_fill(tab);
     __syncthreads();
     const int64_t nv = n / V;
-    const int64_t step = (int64_t)gridDim.x * kBlock * U;
-    for (int64_t base = (int64_t)blockIdx.x * kBlock * U + threadIdx.x; base < nv; base += step) {
-        Vec<float, V> vx[U];
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kBlock) {
+        Vec<float, V> vx = vload_nt<float, V>(x + i * V), vy;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            int64_t i = base + (int64_t)u * kBlock;
-            if (i < nv) vx[u] = vload<float, V>(x + i * V);
-        }
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-            int64_t i = base + (int64_t)u * kBlock;
-            if (i < nv) {
-                Vec<float, V> vy;
-#pragma unroll
-                for (int k = 0; k < V; k++) vy.v[k] = gelu_apply(vx[u].v[k], tab);
-                vstore<float, V>(y + i * V, vy);
-            }
-        }
+        for (int k = 0; k < V; k++) vy.v[k] = gelu_apply(vx.v[k], tab);
+        vstore_nt<float, V>(y + i * V, vy);
     }
     const int64_t tail = n - nv * V;
     if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
@@ -592,13 +553,12 @@ __global__ __launch_bounds__(kBlock) void k_gelu_erf(const float *__restrict__ x
 
 hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    constexpr int U = 2;
     if (vec > 1) {
-        int g = grid_for(n / 4, kBlock * U);
-        hipLaunchKernelGGL((k_gelu_erf<4, U>), dim3(g), dim3(kBlock), 0, s, x, y, n);
+        int g = grid_for(n / 4 > 0 ? n / 4 : 1, kBlock);
+        hipLaunchKernelGGL((k_gelu_erf<4>), dim3(g), dim3(kBlock), 0, s, x, y, n);
     } else {
-        int g = grid_for(n, kBlock * U);
-        hipLaunchKernelGGL((k_gelu_erf<1, U>), dim3(g), dim3(kBlock), 0, s, x, y, n);
+        int g = grid_for(n, kBlock);
+        hipLaunchKernelGGL((k_gelu_erf<1>), dim3(g), dim3(kBlock), 0, s, x, y, n);
     }
     return hipGetLastError();
 }

@@ -38,6 +38,7 @@ struct ErrFlags {
 struct BinArgs {
     int op, dtype, layout;
     int a_inner, b_inner;   // kNd: 1 = contiguous innermost axis, 0 = broadcast
+    int a_once, b_once;     // kNd: operand has no broadcast axis (read once: streamed)
     int vec;                // 1 = scalar element access, else 16-byte vectors
     const void *a;
     const void *b;
@@ -73,8 +74,9 @@ struct ReduceArgs {
     int64_t ws_bytes;
 };
 hipError_t launch_reduce(const ReduceArgs &args, hipStream_t s);
-// Bytes of workspace launch_reduce needs for these sizes.
-int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner);
+// Bytes of workspace launch_reduce needs for these sizes and vector width
+// (vec = 1 or the 16-byte element count, as in ReduceArgs::vec).
+int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner, int vec);
 
 // Softmax of x viewed as [outer, r, inner] along r, with an optional additive
 // mask (already planned against x as an NdLayout over [outer*inner rows, r]).

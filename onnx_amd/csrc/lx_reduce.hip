@@ -88,10 +88,10 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
     const int64_t nv = r / V;
     int64_t j = lane;
     for (; j + 64 * 3 < nv; j += 64 * 4) {
-        Vec<T, V> v0 = vload<T, V>(p + j * V);
-        Vec<T, V> v1 = vload<T, V>(p + (j + 64) * V);
-        Vec<T, V> v2 = vload<T, V>(p + (j + 128) * V);
-        Vec<T, V> v3 = vload<T, V>(p + (j + 192) * V);
+        Vec<T, V> v0 = vload_nt<T, V>(p + j * V);
+        Vec<T, V> v1 = vload_nt<T, V>(p + (j + 64) * V);
+        Vec<T, V> v2 = vload_nt<T, V>(p + (j + 128) * V);
+        Vec<T, V> v3 = vload_nt<T, V>(p + (j + 192) * V);
 #pragma unroll
         for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v0.v[k], pre, R));
 #pragma unroll
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
         for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v3.v[k], pre, R));
     }
     for (; j < nv; j += 64) {
-        Vec<T, V> v0 = vload<T, V>(p + j * V);
+        Vec<T, V> v0 = vload_nt<T, V>(p + j * V);
 #pragma unroll
         for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v0.v[k], pre, R));
     }
@@ -130,10 +130,10 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restri
         const int64_t v0i = j0 / V, v1i = j1 / V;  // chunk is a multiple of V
         int64_t j = v0i + threadIdx.x;
         for (; j + kRBlock * 3 < v1i; j += kRBlock * 4) {
-            Vec<T, V> a0 = vload<T, V>(p + j * V);
-            Vec<T, V> a1 = vload<T, V>(p + (j + kRBlock) * V);
-            Vec<T, V> a2 = vload<T, V>(p + (j + 2 * kRBlock) * V);
-            Vec<T, V> a3 = vload<T, V>(p + (j + 3 * kRBlock) * V);
+            Vec<T, V> a0 = vload_nt<T, V>(p + j * V);
+            Vec<T, V> a1 = vload_nt<T, V>(p + (j + kRBlock) * V);
+            Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * kRBlock) * V);
+            Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * kRBlock) * V);
 #pragma unroll
             for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
 #pragma unroll
@@ -144,7 +144,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restri
             for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a3.v[k], pre, R));
         }
         for (; j < v1i; j += kRBlock) {
-            Vec<T, V> a0 = vload<T, V>(p + j * V);
+            Vec<T, V> a0 = vload_nt<T, V>(p + j * V);
 #pragma unroll
             for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
         }
@@ -201,10 +201,10 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x
         const T *p = x + (o * r) * inner + cv * V;
         int64_t j = j0 + rs;
         for (; j + 3 * nrs < j1; j += 4 * nrs) {
-            Vec<T, V> a0 = vload<T, V>(p + j * inner);
-            Vec<T, V> a1 = vload<T, V>(p + (j + nrs) * inner);
-            Vec<T, V> a2 = vload<T, V>(p + (j + 2 * nrs) * inner);
-            Vec<T, V> a3 = vload<T, V>(p + (j + 3 * nrs) * inner);
+            Vec<T, V> a0 = vload_nt<T, V>(p + j * inner);
+            Vec<T, V> a1 = vload_nt<T, V>(p + (j + nrs) * inner);
+            Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * nrs) * inner);
+            Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * nrs) * inner);
 #pragma unroll
             for (int k = 0; k < V; k++) {
                 acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
@@ -214,7 +214,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x
             }
         }
         for (; j < j1; j += nrs) {
-            Vec<T, V> a0 = vload<T, V>(p + j * inner);
+            Vec<T, V> a0 = vload_nt<T, V>(p + j * inner);
 #pragma unroll
             for (int k = 0; k < V; k++) acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
         }
@@ -293,7 +293,7 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
         p.ws = nch > 1 ? rows * nch * (int64_t)sizeof(A) : 0;
         return p;
     }
-    const int64_t inner_v = inner / V;
+    const int64_t inner_v = inner / V > 0 ? inner / V : 1;
     int ct = 1;
     while (ct < 64 && ct < inner_v) ct <<= 1;
     const int64_t tiles = ceil_div(inner_v, ct);
@@ -384,16 +384,10 @@ hipError_t launch_reduce(const ReduceArgs &a, hipStream_t s) {
     }
 }
 
-int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner) {
+int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner, int vec) {
     const int64_t asz = (dtype == kFloat || dtype == kInt32) ? 4 : 8;
-    const int V = (int)(16 / asz);
-    // the vectorised plan needs the most partials when V is largest; evaluate both
-    int64_t w = 0;
-    for (int v : {1, V}) {
-        RedPlan p = (asz == 4) ? plan_reduce<float>(outer, r, inner, v) : plan_reduce<double>(outer, r, inner, v);
-        if (p.ws > w) w = p.ws;
-    }
-    return w;
+    RedPlan p = (asz == 4) ? plan_reduce<float>(outer, r, inner, vec) : plan_reduce<double>(outer, r, inner, vec);
+    return p.ws;
 }
 
 // ---------------------------------------------------------------------------
@@ -418,7 +412,7 @@ __global__ __launch_bounds__(kRBlock) void k_layernorm(const float *__restrict__
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * 4;
-        if (col < r) v[c] = vload<float, 4>(p + col);
+        if (col < r) v[c] = vload_nt<float, 4>(p + col);
         else v[c] = Vec<float, 4>{{0.0f, 0.0f, 0.0f, 0.0f}};
     }
 #pragma unroll
@@ -445,6 +439,7 @@ __global__ __launch_bounds__(kRBlock) void k_layernorm(const float *__restrict__
     const float var = s2 / fr;
     const float ve = var + eps;
     const float sd = __builtin_sqrtf(ve);
+    const float rsd = 1.0f / sd;
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * 4;
@@ -454,11 +449,11 @@ __global__ __launch_bounds__(kRBlock) void k_layernorm(const float *__restrict__
             Vec<float, 4> o;
 #pragma unroll
             for (int k = 0; k < 4; k++) {
-                float nrm = v[c].v[k] / sd;
+                float nrm = div_by_row_lx(v[c].v[k], sd, rsd);
                 float m = nrm * g.v[k];
                 o.v[k] = m + b.v[k];
             }
-            vstore<float, 4>(q + col, o);
+            vstore_nt<float, 4>(q + col, o);
         }
     }
 }

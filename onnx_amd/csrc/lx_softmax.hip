@@ -20,10 +20,17 @@ namespace lx {
 
 constexpr int kSBlock = 256;
 
+// argument x - max is <= 0 (or NaN): the early-out-free expf applies
 template <typename T>
 __device__ __forceinline__ T exp_elem(T d, const ExpTable &tab) {
-    if constexpr (std::is_same<T, float>::value) return expf_lx(d, tab);
+    if constexpr (std::is_same<T, float>::value) return expf_nonpos_lx(d, tab);
     else return ::exp(d);
+}
+
+template <typename T>
+__device__ __forceinline__ T div_row(T e, T s, T rs) {
+    if constexpr (std::is_same<T, float>::value) return div_by_row_lx(e, s, rs);
+    else return e / s;
 }
 
 // One wave per row; NV vectors of V elements per lane.  MASK: add the mask
@@ -46,7 +53,7 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * V;
-        if (col < r) v[c] = vload<T, V>(p + col);
+        if (col < r) v[c] = vload_nt<T, V>(p + col);
     }
     if constexpr (MASK) {
         int64_t moff = 0;
@@ -101,14 +108,15 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
         }
     }
     s = wave_reduce(s, [](T a, T b) { return a + b; });
+    const T rs = T(1) / s;
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * V;
         if (col < r) {
             Vec<T, V> o;
 #pragma unroll
-            for (int k = 0; k < V; k++) o.v[k] = v[c].v[k] / s;
-            vstore<T, V>(q + col, o);
+            for (int k = 0; k < V; k++) o.v[k] = div_row<T>(v[c].v[k], s, rs);
+            vstore_nt<T, V>(q + col, o);
         }
     }
 }

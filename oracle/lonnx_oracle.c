@@ -665,3 +665,21 @@ int lxo_softmax(int dtype, int rank, const int64_t *dims, const void *x, int axi
     free(m); free(s); free(bm); free(e);
     return st;
 }
+
+/* ------------------------------------------------------------------------ */
+/* The BERT GELU subgraph node by node without materialising its scalar     */
+/* operands (the values are those of CPUExecutionProvider.Div/Erf/Add/Mul   */
+/* run in sequence: every node rounds to float32):                          */
+/*   a = x / 1.4142135f; e = Erf(a); b = e + 1f; c = x * b; y = c * 0.5f    */
+/* ------------------------------------------------------------------------ */
+void lxo_gelu_chain(int64_t n, const float *x, float *y)
+{
+    const float c2 = 1.41421353816986083984375f;
+    for (int64_t i = 0; i < n; i++) {
+        float a = x[i] / c2;
+        float e = lxo_erf_f32(a);
+        float b = e + 1.0f;
+        float c = x[i] * b;
+        y[i] = c * 0.5f;
+    }
+}

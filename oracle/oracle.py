@@ -57,6 +57,7 @@ def lib():
         L.lxo_reduce.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, i64p, vp, ctypes.c_int, i64p,
                                  ctypes.c_int, vp, ip, i64p]
         L.lxo_softmax.argtypes = [ctypes.c_int, ctypes.c_int, i64p, vp, ctypes.c_int, vp]
+        L.lxo_gelu_chain.argtypes = [ctypes.c_int64, vp, vp]
         L.lxo_erf_f32.argtypes = [ctypes.c_float]
         L.lxo_erf_f32.restype = ctypes.c_float
         L.lxo_erf_f64.argtypes = [ctypes.c_double]
@@ -190,6 +191,14 @@ def gelu_erf(x):
     b = binary(ADD, e, np.array(1.0, dtype=np.float32))
     c = binary(MUL, x, b)
     return binary(MUL, c, np.array(0.5, dtype=np.float32))
+
+
+def gelu_chain_fast(x):
+    """gelu_erf without materialising the scalar operands (same values)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().lxo_gelu_chain(x.size, _ptr(x), _ptr(out))
+    return out
 
 
 def add_softmax(s, mask, axis=-1):

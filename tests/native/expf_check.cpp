@@ -40,4 +40,83 @@ float lx_test_erf(float x) {
 }
 
 uint32_t lx_test_fastdiv(uint32_t n, uint32_t d) { return lx::fastdiv_host(n, lx::make_fastdiv(d)); }
+
+static inline uint32_t bits(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+static inline float fbits(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+static inline bool same(float a, float b) { return bits(a) == bits(b) || (a != a && b != b); }
+
+// all 2^32 x: div_sqrt2f_lx(x) == x / 1.4142135f
+long long lx_test_div_sqrt2_mismatches(void) {
+    const volatile float c = 1.41421353816986083984375f;
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long u = 0; u < (1ll << 32); u++) {
+        float x = fbits((uint32_t)u);
+        if (!same(lx::div_sqrt2f_lx(x), x / c)) bad++;
+    }
+    return bad;
+}
+
+// every d in [1, 2^126) with every seed within 1 ulp of 1/d, plus d >= 2^126, inf, NaN
+long long lx_test_recip_mismatches(void) {
+    long long bad = 0;
+    const uint32_t lo = bits(1.0f), hi = bits(0x1p126f);
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long u = lo; u < (long long)hi; u++) {
+        float d = fbits((uint32_t)u);
+        float cr = 1.0f / d;
+        for (int k = -1; k <= 1; k++) {
+            float seed = fbits(bits(cr) + k);
+            if (!same(lx::recip_ge1_from_seed(d, seed), cr)) bad++;
+        }
+    }
+    float extra[] = {0x1p126f, 0x1.fffffep127f, __builtin_inff(), __builtin_nanf("")};
+    for (float d : extra)
+        if (!same(lx::recip_ge1_from_seed(d, 0.0f), 1.0f / d)) bad++;
+    return bad;
+}
+
+// every x <= 0 (sign bit set), +0 and NaN: expf_nonpos_lx(x) == expf(x)
+long long lx_test_expf_nonpos_mismatches(void) {
+    lx::ExpTable tab;
+    lx::exp_table_fill_host(tab);
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long u = 0x80000000ll; u < (1ll << 32); u++) {
+        float x = fbits((uint32_t)u);
+        if (!same(lx::expf_nonpos_lx(x, tab), expf(x))) bad++;
+    }
+    if (!same(lx::expf_nonpos_lx(0.0f, tab), expf(0.0f))) bad++;
+    if (!same(lx::expf_nonpos_lx(__builtin_nanf(""), tab), expf(__builtin_nanf("")))) bad++;
+    return bad;
+}
+}
+
+namespace {
+struct ExactSeed {
+    float operator()(float d) const { return 1.0f / d; }
+};
+}  // namespace
+
+extern "C" {
+// all 2^32 x: the branch-free device erf core == erf_lx (A&S formula with the host-equal expf)
+long long lx_test_erf_fast_mismatches(void) {
+    lx::ExpTable tab;
+    lx::exp_table_fill_host(tab);
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long u = 0; u < (1ll << 32); u++) {
+        float x = fbits((uint32_t)u);
+        if (!same(lx::erf_fast_core(x, tab, ExactSeed()), lx::erf_lx(x, tab))) bad++;
+    }
+    return bad;
+}
 }

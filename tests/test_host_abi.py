@@ -106,7 +106,7 @@ def _native():
     src = os.path.join(NATIVE, "expf_check.cpp")
     if not os.path.exists(so) or os.path.getmtime(so) < os.path.getmtime(src):
         subprocess.check_call(["/opt/rocm/bin/hipcc", "-O2", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off",
-                               "--offload-host-only", "-x", "hip", "-fno-builtin", src, "-o", so])
+                               "--offload-host-only", "-x", "hip", "-fno-builtin", "-fopenmp", src, "-o", so])
     lib = ctypes.CDLL(so)
     lib.lx_test_expf_mismatches.restype = ctypes.c_longlong
     lib.lx_test_expf_mismatches.argtypes = [ctypes.c_uint64] * 3
@@ -114,6 +114,8 @@ def _native():
     lib.lx_test_erf.argtypes = [ctypes.c_float]
     lib.lx_test_fastdiv.restype = ctypes.c_uint32
     lib.lx_test_fastdiv.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
+    for f in ("lx_test_div_sqrt2_mismatches", "lx_test_recip_mismatches", "lx_test_expf_nonpos_mismatches"):
+        getattr(lib, f).restype = ctypes.c_longlong
     return lib
 
 
@@ -147,3 +149,24 @@ def test_fastdiv():
         for n in ns:
             if 0 <= n < (1 << 31):
                 assert lib.lx_test_fastdiv(n, d) == n // d, (n, d)
+
+
+def test_division_free_sequences_are_exact():
+    """The device Erf / GELU replace IEEE divisions and the expf early-outs by
+    exact equivalents; each is proven here by exhaustion on the host:
+      x / 1.4142135f  == (float)(x * (double)(1/1.4142135f))   for all 2^32 x
+      1 / d           == two double Newton steps from any seed within 1 ulp,
+                         for every float d in [1, 2^126)
+      expf(x)         == the clamped early-out-free expf for every x <= 0."""
+    lib = _native()
+    assert lib.lx_test_div_sqrt2_mismatches() == 0
+    assert lib.lx_test_recip_mismatches() == 0
+    assert lib.lx_test_expf_nonpos_mismatches() == 0
+
+
+def test_branch_free_erf_equals_reference_formula():
+    """The device Erf core (clamped reciprocal argument, early-out-free expf)
+    returns the A&S 7.1.26 formula's bits for all 2^32 inputs."""
+    lib = _native()
+    lib.lx_test_erf_fast_mismatches.restype = ctypes.c_longlong
+    assert lib.lx_test_erf_fast_mismatches() == 0
