@@ -534,6 +534,7 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         if ((result = ensure_workspace(wsb))) break;
         ra.workspace = g.workspace;
         ra.ws_bytes = g.ws_bytes;
+
         hipError_t e = launch_reduce(ra, g.stream);
         if (e != hipSuccess) { result = hip_fail(e, opn); break; }
         src = dst;
@@ -581,6 +582,7 @@ int lx_init(int32_t device) {
     g.stream = g.own_stream;
     HIPCHECK(hipMalloc(&g.errs, sizeof(ErrFlags)), "hipMalloc(errors)");
     HIPCHECK(hipHostMalloc((void **)&g.errs_host, sizeof(ErrFlags), hipHostMallocDefault), "hipHostMalloc");
+
     g.device = device;
     g.init = true;
     int st = ensure_workspace(1 << 20);
@@ -593,6 +595,7 @@ int lx_shutdown(void) {
     (void)hipDeviceSynchronize();
     if (g.workspace) (void)hipFree(g.workspace);
     if (g.errs) (void)hipFree(g.errs);
+
     if (g.errs_host) (void)hipHostFree(g.errs_host);
     if (g.own_stream) (void)hipStreamDestroy(g.own_stream);
     g = State();

@@ -57,7 +57,13 @@ __device__ __forceinline__ Vec<T, N> vload_nt(const T *p) {
     } else if constexpr (B == 1) {
         return __builtin_bit_cast(Vec<T, N>, __builtin_nontemporal_load(reinterpret_cast<const uint8_t *>(p)));
     } else {
-        return vload<T, N>(p);
+        static_assert(B % 16 == 0, "multi-chunk vectors are whole 16-byte chunks");
+        struct Chunks {
+            u32x4 c[B / 16];
+        } r;
+#pragma unroll
+        for (int i = 0; i < B / 16; i++) r.c[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p) + i);
+        return __builtin_bit_cast(Vec<T, N>, r);
     }
 }
 
@@ -75,7 +81,13 @@ __device__ __forceinline__ void vstore_nt(T *p, const Vec<T, N> &v) {
     } else if constexpr (B == 1) {
         __builtin_nontemporal_store(__builtin_bit_cast(uint8_t, v), reinterpret_cast<uint8_t *>(p));
     } else {
-        vstore<T, N>(p, v);
+        static_assert(B % 16 == 0, "multi-chunk vectors are whole 16-byte chunks");
+        struct Chunks {
+            u32x4 c[B / 16];
+        };
+        Chunks r = __builtin_bit_cast(Chunks, v);
+#pragma unroll
+        for (int i = 0; i < B / 16; i++) __builtin_nontemporal_store(r.c[i], reinterpret_cast<u32x4 *>(p) + i);
     }
 }
 

@@ -471,7 +471,7 @@ template <int SRC, int DST>
 static hipError_t cast_typed(const void *x, void *y, int64_t n, int vec, ErrFlags *errs, hipStream_t s) {
     using S = typename CType<SRC>::T;
     using D = typename CType<DST>::T;
-    constexpr int E = 16 / (sizeof(S) > sizeof(D) ? sizeof(S) : sizeof(D));
+    constexpr int E = 16 / (sizeof(S) < sizeof(D) ? sizeof(S) : sizeof(D));  // 16 bytes on the narrower side
     if (vec > 1) {
         int g = grid_for(n / E > 0 ? n / E : 1, kBlock);
         hipLaunchKernelGGL((k_cast<SRC, DST, E>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);

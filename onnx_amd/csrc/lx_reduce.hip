@@ -111,76 +111,77 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
     if (lane == 0) y[row] = RD::fin(acc, post, R);
 }
 
-// inner == 1, long rows: grid (nchunks, rows); each block folds one chunk.
+// inner == 1, long rows: grid (nchunks, rows).  The row is cut into tiles of
+// 4 x 256 vectors; block c takes tiles c, c + nchunks, ... and each lane loads
+// the 4 vectors t, t+256, t+512, t+768 of a tile together, so at any moment
+// the grid streams one contiguous front of the row.
 template <int OP, typename T, int V>
 __global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restrict__ x,
                                                                typename Red<OP, T>::A *__restrict__ partial,
-                                                               T *__restrict__ y, int64_t r, int64_t chunk,
-                                                               int nchunks, int pre, int post, int64_t R) {
+                                                               T *__restrict__ y, int64_t r, int nchunks, int pre,
+                                                               int post, int64_t R) {
     using RD = Red<OP, T>;
     using A = typename RD::A;
+    constexpr int64_t kTile = 4 * kRBlock;
     const int64_t row = blockIdx.y;
     const int c = blockIdx.x;
-    const int64_t j0 = (int64_t)c * chunk;
-    int64_t j1 = j0 + chunk;
-    if (j1 > r) j1 = r;
     const T *p = x + row * r;
+    const int64_t nv = r / V;  // r % V == 0 whenever V > 1
+    const int64_t step = (int64_t)nchunks * kTile;
     A acc = RD::ident();
-    if (j0 < j1) {
-        const int64_t v0i = j0 / V, v1i = j1 / V;  // chunk is a multiple of V
-        int64_t j = v0i + threadIdx.x;
-        for (; j + kRBlock * 3 < v1i; j += kRBlock * 4) {
-            Vec<T, V> a0 = vload_nt<T, V>(p + j * V);
-            Vec<T, V> a1 = vload_nt<T, V>(p + (j + kRBlock) * V);
-            Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * kRBlock) * V);
-            Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * kRBlock) * V);
+    int64_t j = (int64_t)c * kTile + threadIdx.x;
+    for (; j + 3 * kRBlock < nv; j += step) {
+        Vec<T, V> a0 = vload_nt<T, V>(p + j * V);
+        Vec<T, V> a1 = vload_nt<T, V>(p + (j + kRBlock) * V);
+        Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * kRBlock) * V);
+        Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * kRBlock) * V);
 #pragma unroll
-            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
 #pragma unroll
-            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a1.v[k], pre, R));
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a1.v[k], pre, R));
 #pragma unroll
-            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a2.v[k], pre, R));
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a2.v[k], pre, R));
 #pragma unroll
-            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a3.v[k], pre, R));
-        }
-        for (; j < v1i; j += kRBlock) {
-            Vec<T, V> a0 = vload_nt<T, V>(p + j * V);
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a3.v[k], pre, R));
+    }
+    // the partial tile at the end of the row (j points into it for one block)
+    for (; j < nv; j += kRBlock) {
+        Vec<T, V> a0 = vload_nt<T, V>(p + j * V);
 #pragma unroll
-            for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
-        }
-        for (int64_t t = v1i * V + threadIdx.x; t < j1; t += kRBlock) acc = RD::comb(acc, RD::load(p[t], pre, R));
+        for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(a0.v[k], pre, R));
     }
     acc = block_reduce<OP, T>(acc);
-    if (threadIdx.x == 0) {
-        if (nchunks == 1) y[row] = RD::fin(acc, post, R);
-        else partial[row * nchunks + c] = acc;
+    if (nchunks == 1) {
+        if (threadIdx.x == 0) y[row] = RD::fin(acc, post, R);
+        return;
     }
+    if (threadIdx.x == 0) partial[row * nchunks + c] = acc;
 }
 
-// Finishing pass of the split row reduction: one wave per row over its partials.
+// Finishing pass of the split row reduction: one block per row folds the
+// row's partials (each lane a fixed stride of them, then the block tree).
 template <int OP, typename T>
 __global__ __launch_bounds__(kRBlock) void k_reduce_rows_finish(const typename Red<OP, T>::A *__restrict__ partial,
-                                                                T *__restrict__ y, int64_t rows, int nchunks,
-                                                                int post, int64_t R) {
+                                                                T *__restrict__ y, int nchunks, int post, int64_t R) {
     using RD = Red<OP, T>;
     using A = typename RD::A;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    A acc = RD::ident();
-    for (int c = lane; c < nchunks; c += 64) acc = RD::comb(acc, partial[row * nchunks + c]);
-    acc = wave_reduce(acc, [](A a, A b) { return RD::comb(a, b); });
-    if (lane == 0) y[row] = RD::fin(acc, post, R);
+    const int64_t row = blockIdx.x;
+    A t = RD::ident();
+    for (int q = threadIdx.x; q < nchunks; q += kRBlock) t = RD::comb(t, partial[row * nchunks + q]);
+    t = block_reduce<OP, T>(t);
+    if (threadIdx.x == 0) y[row] = RD::fin(t, post, R);
 }
 
 // inner > 1: grid (column tiles * outer, rsplit).  ct lanes cover ct column
-// vectors, 256/ct row slices stride over the rows of this split.
+// vectors; 256/ct row slices.  Rows are taken in groups of nrs consecutive
+// rows, group g going to split g % rsplit, so the splits sweep the slab
+// together.  Slices are combined in LDS; with rsplit > 1 each split writes a
+// partial and k_reduce_cols_finish folds them in split order.
 template <int OP, typename T, int V>
 __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x,
                                                          typename Red<OP, T>::A *__restrict__ partial,
                                                          T *__restrict__ y, int64_t outer, int64_t r, int64_t inner,
-                                                         int ct, int64_t rchunk, int rsplit, int pre, int post,
-                                                         int64_t R) {
+                                                         int ct, int rsplit, int pre, int post, int64_t R) {
     using RD = Red<OP, T>;
     using A = typename RD::A;
     __shared__ A sm[kRBlock * V];
@@ -189,22 +190,21 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x
     const int64_t inner_v = inner / V;
     const int64_t tiles = (inner_v + ct - 1) / ct;
     const int64_t o = (int64_t)blockIdx.x / tiles;
-    const int64_t cv = ((int64_t)blockIdx.x - o * tiles) * ct + cvt;
+    const int64_t tile = (int64_t)blockIdx.x - o * tiles;
+    const int64_t cv = tile * ct + cvt;
     const int s = blockIdx.y;
-    const int64_t j0 = (int64_t)s * rchunk;
-    int64_t j1 = j0 + rchunk;
-    if (j1 > r) j1 = r;
+    const int64_t G = (int64_t)nrs * rsplit;  // row stride between this split's groups
     A acc[V];
 #pragma unroll
     for (int k = 0; k < V; k++) acc[k] = RD::ident();
     if (cv < inner_v) {
         const T *p = x + (o * r) * inner + cv * V;
-        int64_t j = j0 + rs;
-        for (; j + 3 * nrs < j1; j += 4 * nrs) {
+        int64_t j = (int64_t)s * nrs + rs;
+        for (; j + 3 * G < r; j += 4 * G) {
             Vec<T, V> a0 = vload_nt<T, V>(p + j * inner);
-            Vec<T, V> a1 = vload_nt<T, V>(p + (j + nrs) * inner);
-            Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * nrs) * inner);
-            Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * nrs) * inner);
+            Vec<T, V> a1 = vload_nt<T, V>(p + (j + G) * inner);
+            Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * G) * inner);
+            Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * G) * inner);
 #pragma unroll
             for (int k = 0; k < V; k++) {
                 acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x
                 acc[k] = RD::comb(acc[k], RD::load(a3.v[k], pre, R));
             }
         }
-        for (; j < j1; j += nrs) {
+        for (; j < r; j += G) {
             Vec<T, V> a0 = vload_nt<T, V>(p + j * inner);
 #pragma unroll
             for (int k = 0; k < V; k++) acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
@@ -222,22 +222,26 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x
 #pragma unroll
     for (int k = 0; k < V; k++) sm[(rs * ct + cvt) * V + k] = acc[k];
     __syncthreads();
-    if (rs == 0 && cv < inner_v) {
-        A tot[V];
+    A tot[V];
+    if (rs == 0) {
 #pragma unroll
         for (int k = 0; k < V; k++) tot[k] = sm[cvt * V + k];
         for (int q = 1; q < nrs; q++) {
 #pragma unroll
             for (int k = 0; k < V; k++) tot[k] = RD::comb(tot[k], sm[(q * ct + cvt) * V + k]);
         }
-        const int64_t out = o * inner + cv * V;
-        if (rsplit == 1) {
+    }
+    const int64_t out = o * inner + cv * V;
+    if (rsplit == 1) {
+        if (rs == 0 && cv < inner_v) {
 #pragma unroll
             for (int k = 0; k < V; k++) y[out + k] = RD::fin(tot[k], post, R);
-        } else {
-#pragma unroll
-            for (int k = 0; k < V; k++) partial[(int64_t)s * outer * inner + out + k] = tot[k];
         }
+        return;
+    }
+    if (rs == 0 && cv < inner_v) {
+#pragma unroll
+        for (int k = 0; k < V; k++) partial[(int64_t)s * outer * inner + out + k] = tot[k];
     }
 }
 
@@ -249,7 +253,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols_finish(const typename R
     using A = typename RD::A;
     for (int64_t i = (int64_t)blockIdx.x * kRBlock + threadIdx.x; i < nout; i += (int64_t)gridDim.x * kRBlock) {
         A acc = partial[i];
-        for (int s = 1; s < rsplit; s++) acc = RD::comb(acc, partial[(int64_t)s * nout + i]);
+        for (int q = 1; q < rsplit; q++) acc = RD::comb(acc, partial[(int64_t)q * nout + i]);
         y[i] = RD::fin(acc, post, R);
     }
 }
@@ -261,12 +265,10 @@ static int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 struct RedPlan {
     int kind;  // 0 wave rows, 1 split rows, 2 cols
-    int64_t chunk;
     int nchunks;
     int ct;
-    int64_t rchunk;
     int rsplit;
-    int64_t ws;  // workspace bytes
+    int64_t ws;  // partial bytes
 };
 
 static constexpr int64_t kTargetBlocks = 2048;
@@ -281,14 +283,10 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
             return p;
         }
         int64_t nch = ceil_div(kTargetBlocks, rows);
-        int64_t maxch = ceil_div(r, 4096);
+        int64_t maxch = ceil_div(r / V, (int64_t)kRBlock * 4);  // >= 4 vectors per lane
         if (nch > maxch) nch = maxch;
         if (nch < 1) nch = 1;
-        int64_t chunk = ceil_div(r, nch);
-        chunk = ceil_div(chunk, V * 64) * (V * 64);
-        nch = ceil_div(r, chunk);
         p.kind = 1;
-        p.chunk = chunk;
         p.nchunks = (int)nch;
         p.ws = nch > 1 ? rows * nch * (int64_t)sizeof(A) : 0;
         return p;
@@ -298,21 +296,17 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
     while (ct < 64 && ct < inner_v) ct <<= 1;
     const int64_t tiles = ceil_div(inner_v, ct);
     const int64_t base = tiles * outer;
-    int64_t rsplit = 1;
     const int nrs = kRBlock / ct;
+    int64_t rsplit = 1;
     if (base < kTargetBlocks) {
         rsplit = ceil_div(kTargetBlocks, base);
-        int64_t maxs = ceil_div(r, (int64_t)nrs * 16);  // keep >= 16 rows per slice
+        int64_t maxs = ceil_div(r, (int64_t)nrs * 16);  // >= 16 rows per slice
         if (rsplit > maxs) rsplit = maxs;
         if (rsplit > 65535) rsplit = 65535;
         if (rsplit < 1) rsplit = 1;
     }
-    int64_t rchunk = ceil_div(r, rsplit);
-    rsplit = ceil_div(r, rchunk);
-    if (rsplit < 1) rsplit = 1;
     p.kind = 2;
     p.ct = ct;
-    p.rchunk = rchunk;
     p.rsplit = (int)rsplit;
     p.ws = rsplit > 1 ? rsplit * outer * inner * (int64_t)sizeof(A) : 0;
     return p;
@@ -332,23 +326,21 @@ static hipError_t reduce_typed_v(const ReduceArgs &a, hipStream_t s) {
                            a.pre_div, a.post_div, a.r_total);
     } else if (p.kind == 1) {
         hipLaunchKernelGGL((k_reduce_rows_split<OP, T, V>), dim3(p.nchunks, (unsigned)a.outer), dim3(kRBlock), 0, s, x,
-                           ws, y, a.r, p.chunk, p.nchunks, a.pre_div, a.post_div, a.r_total);
-        if (p.nchunks > 1) {
-            int g = (int)ceil_div(a.outer, kRBlock / 64);
-            hipLaunchKernelGGL((k_reduce_rows_finish<OP, T>), dim3(g), dim3(kRBlock), 0, s, ws, y, a.outer, p.nchunks,
-                               a.post_div, a.r_total);
-        }
+                           ws, y, a.r, p.nchunks, a.pre_div, a.post_div, a.r_total);
+        if (p.nchunks > 1)
+            hipLaunchKernelGGL((k_reduce_rows_finish<OP, T>), dim3((unsigned)a.outer), dim3(kRBlock), 0, s, ws, y,
+                               p.nchunks, a.post_div, a.r_total);
     } else {
         const int64_t tiles = ceil_div(a.inner / V, p.ct);
         hipLaunchKernelGGL((k_reduce_cols<OP, T, V>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
-                           dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rchunk, p.rsplit, a.pre_div,
+                           dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rsplit, a.pre_div,
                            a.post_div, a.r_total);
         if (p.rsplit > 1) {
-            int64_t nout = a.outer * a.inner;
-            int g = (int)ceil_div(nout, kRBlock);
+            const int64_t nout = a.outer * a.inner;
+            int64_t g = ceil_div(nout, kRBlock);
             if (g > 8192) g = 8192;
-            hipLaunchKernelGGL((k_reduce_cols_finish<OP, T>), dim3(g), dim3(kRBlock), 0, s, ws, y, nout, p.rsplit,
-                               a.post_div, a.r_total);
+            hipLaunchKernelGGL((k_reduce_cols_finish<OP, T>), dim3((unsigned)g), dim3(kRBlock), 0, s, ws, y, nout,
+                               p.rsplit, a.post_div, a.r_total);
         }
     }
     return hipGetLastError();
@@ -389,6 +381,7 @@ int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inne
     RedPlan p = (asz == 4) ? plan_reduce<float>(outer, r, inner, vec) : plan_reduce<double>(outer, r, inner, vec);
     return p.ws;
 }
+
 
 // ---------------------------------------------------------------------------
 // Fused LayerNorm subgraph over rows of length r, one wave per row, the row

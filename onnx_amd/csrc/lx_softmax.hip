@@ -19,6 +19,7 @@
 namespace lx {
 
 constexpr int kSBlock = 256;
+constexpr int64_t kSoftmaxMaxBlocks = 8192;  // 32768 waves; each loops over its share of rows
 
 // argument x - max is <= 0 (or NaN): the early-out-free expf applies
 template <typename T>
@@ -33,91 +34,117 @@ __device__ __forceinline__ T div_row(T e, T s, T rs) {
     else return e / s;
 }
 
-// One wave per row; NV vectors of V elements per lane.  MASK: add the mask
-// element (row offset from the NdLayout decomposition, column stride mask_inner).
-template <typename T, int V, int NV, bool MASK>
+// Mask row offset: the row index decomposed over the mask's row axes
+// (innermost first).  NOUT >= 0 is the compile-time axis count, -1 = runtime.
+template <int NOUT>
+__device__ __forceinline__ int64_t mask_row_offset(uint32_t row, const NdLayout &L) {
+    int64_t off = 0;
+    if constexpr (NOUT >= 0) {
+#pragma unroll
+        for (int d = 0; d < NOUT; d++) {
+            uint32_t q = fdiv(row, L.odiv[d]);
+            off += (int64_t)(row - q * L.odiv[d].d) * L.a_str[d];
+            row = q;
+        }
+    } else {
+        for (int d = 0; d < L.nouter; d++) {
+            uint32_t q = fdiv(row, L.odiv[d]);
+            off += (int64_t)(row - q * L.odiv[d].d) * L.a_str[d];
+            row = q;
+        }
+    }
+    return off;
+}
+
+// Rows of length r <= 64*V*NV held in registers, one wave per row at a time.
+// Each wave walks rows w, w + W, ... (W = all waves of the grid) and loads the
+// next row while it finishes the current one.  NOUT: mask row axes (0 = no
+// mask; see mask_row_offset).
+template <typename T, int V, int NV, int NOUT>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
                                                           NdLayout mrows) {
+    constexpr bool MASK = NOUT != 0;
     __shared__ ExpTable tab;
     if constexpr (std::is_same<T, float>::value) {
         exp_table_fill(tab);
         __syncthreads();
     }
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6);
+    const int64_t W = (int64_t)gridDim.x * (kSBlock / 64);
+    int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const T *p = x + row * (int64_t)r;
-    T *q = y + row * (int64_t)r;
-    Vec<T, V> v[NV];
+    Vec<T, V> cur[NV], nxt[NV];
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * V;
-        if (col < r) v[c] = vload_nt<T, V>(p + col);
+        if (col < r) cur[c] = vload_nt<T, V>(x + row * (int64_t)r + col);
     }
-    if constexpr (MASK) {
-        int64_t moff = 0;
-        uint32_t rr = (uint32_t)row;
+    for (; row < rows; row += W) {
+        const int64_t next = row + W;
+        if (next < rows) {
 #pragma unroll
-        for (int d = 0; d < kMaxOuter; d++) {
-            if (d < mrows.nouter) {
-                uint32_t qq = fdiv(rr, mrows.odiv[d]);
-                uint32_t id = rr - qq * mrows.odiv[d].d;
-                moff += (int64_t)id * mrows.a_str[d];
-                rr = qq;
+            for (int c = 0; c < NV; c++) {
+                const int col = (c * 64 + lane) * V;
+                if (col < r) nxt[c] = vload_nt<T, V>(x + next * (int64_t)r + col);
             }
         }
-        const T *m = mask + moff;
+        if constexpr (MASK) {
+            const T *m = mask + mask_row_offset<NOUT>((uint32_t)row, mrows);
+#pragma unroll
+            for (int c = 0; c < NV; c++) {
+                const int col = (c * 64 + lane) * V;
+                if (col < r) {
+                    if (mask_inner) {
+                        Vec<T, V> mv = vload<T, V>(m + col);
+#pragma unroll
+                        for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mv.v[k];
+                    } else {
+                        const T mv = m[0];
+#pragma unroll
+                        for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mv;
+                    }
+                }
+            }
+        }
+        // ReduceMax with seed 0 (TensorOps.cs:1820-1827)
+        T mx = T(0);
 #pragma unroll
         for (int c = 0; c < NV; c++) {
             const int col = (c * 64 + lane) * V;
             if (col < r) {
-                if (mask_inner) {
-                    Vec<T, V> mv = vload<T, V>(m + col);
 #pragma unroll
-                    for (int k = 0; k < V; k++) v[c].v[k] = v[c].v[k] + mv.v[k];
-                } else {
-                    const T mv = m[0];
+                for (int k = 0; k < V; k++) mx = cur[c].v[k] > mx ? cur[c].v[k] : mx;
+            }
+        }
+        mx = wave_reduce(mx, [](T a, T b) { return b > a ? b : a; });
+        T sum = T(0);
 #pragma unroll
-                    for (int k = 0; k < V; k++) v[c].v[k] = v[c].v[k] + mv;
+        for (int c = 0; c < NV; c++) {
+            const int col = (c * 64 + lane) * V;
+            if (col < r) {
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    cur[c].v[k] = exp_elem<T>(cur[c].v[k] - mx, tab);
+                    sum = sum + cur[c].v[k];
                 }
             }
         }
-    }
-    // ReduceMax with seed 0 (TensorOps.cs:1820-1827)
-    T mx = T(0);
+        sum = wave_reduce(sum, [](T a, T b) { return a + b; });
+        const T rs = T(1) / sum;
+        T *q = y + row * (int64_t)r;
 #pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * V;
-        if (col < r) {
+        for (int c = 0; c < NV; c++) {
+            const int col = (c * 64 + lane) * V;
+            if (col < r) {
+                Vec<T, V> o;
 #pragma unroll
-            for (int k = 0; k < V; k++) mx = v[c].v[k] > mx ? v[c].v[k] : mx;
-        }
-    }
-    mx = wave_reduce(mx, [](T a, T b) { return b > a ? b : a; });
-    T s = T(0);
-#pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * V;
-        if (col < r) {
-#pragma unroll
-            for (int k = 0; k < V; k++) {
-                v[c].v[k] = exp_elem<T>(v[c].v[k] - mx, tab);
-                s = s + v[c].v[k];
+                for (int k = 0; k < V; k++) o.v[k] = div_row<T>(cur[c].v[k], sum, rs);
+                vstore_nt<T, V>(q + col, o);
             }
         }
-    }
-    s = wave_reduce(s, [](T a, T b) { return a + b; });
-    const T rs = T(1) / s;
 #pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * V;
-        if (col < r) {
-            Vec<T, V> o;
-#pragma unroll
-            for (int k = 0; k < V; k++) o.v[k] = div_row<T>(v[c].v[k], s, rs);
-            vstore_nt<T, V>(q + col, o);
-        }
+        for (int c = 0; c < NV; c++) cur[c] = nxt[c];
     }
 }
 
@@ -174,18 +201,19 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_cols(const T *__restrict__ 
     }
 }
 
-template <typename T, int V, bool MASK>
-static hipError_t softmax_wave_dispatch(const SoftmaxArgs &a, hipStream_t s) {
+template <typename T, int V, int NOUT>
+static hipError_t softmax_wave_launch(const SoftmaxArgs &a, hipStream_t s) {
     const int r = (int)a.r;
     const int nv = (r + 64 * V - 1) / (64 * V);
-    const int g = (int)((a.outer + kSBlock / 64 - 1) / (kSBlock / 64));
+    int64_t g = (a.outer + kSBlock / 64 - 1) / (kSBlock / 64);
+    if (g > kSoftmaxMaxBlocks) g = kSoftmaxMaxBlocks;
     const T *x = (const T *)a.x;
     T *y = (T *)a.y;
     const T *m = (const T *)a.mask;
-#define LX_SM_CASE(N)                                                                                        \
-    case N:                                                                                                  \
-        hipLaunchKernelGGL((k_softmax_wave<T, V, N, MASK>), dim3(g), dim3(kSBlock), 0, s, x, y, a.outer, r, m, \
-                           a.mask_inner, a.mask_rows);                                                       \
+#define LX_SM_CASE(N)                                                                                           \
+    case N:                                                                                                     \
+        hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, a.outer, r, \
+                           m, a.mask_inner, a.mask_rows);                                                       \
         break;
     switch (nv) {
         LX_SM_CASE(1) LX_SM_CASE(2) LX_SM_CASE(3) LX_SM_CASE(4) LX_SM_CASE(5) LX_SM_CASE(6) LX_SM_CASE(7) LX_SM_CASE(8)
@@ -193,6 +221,17 @@ static hipError_t softmax_wave_dispatch(const SoftmaxArgs &a, hipStream_t s) {
     }
 #undef LX_SM_CASE
     return hipGetLastError();
+}
+
+template <typename T, int V, bool MASK>
+static hipError_t softmax_wave_dispatch(const SoftmaxArgs &a, hipStream_t s) {
+    if constexpr (!MASK) return softmax_wave_launch<T, V, 0>(a, s);
+    switch (a.mask_rows.nouter) {
+    case 1: return softmax_wave_launch<T, V, 1>(a, s);
+    case 2: return softmax_wave_launch<T, V, 2>(a, s);
+    case 3: return softmax_wave_launch<T, V, 3>(a, s);
+    default: return softmax_wave_launch<T, V, -1>(a, s);
+    }
 }
 
 template <typename T>
