@@ -114,11 +114,19 @@ __device__ __forceinline__ T bin_apply(T l, T r, uint64_t idx, ErrFlags *e) {
                 atomicMin(&e->first_ovf, (unsigned long long)idx);
                 return 0;
             }
-            if constexpr (sizeof(T) == 8) {
-                // both operands inside int32: the 32-bit quotient is the same value
-                if (l == (T)(int32_t)l && r == (T)(int32_t)r) return (T)((int32_t)l / (int32_t)r);
+            if constexpr (sizeof(T) == 4) {
+                return l / r;
+            } else {
+                // both operands inside int32: divide the magnitudes in 32 bits,
+                // apply the sign in 64 (so -2^31 / -1 = 2^31 stays exact)
+                if (l == (T)(int32_t)l && r == (T)(int32_t)r) {
+                    const uint32_t ua = l < 0 ? (uint32_t)(-l) : (uint32_t)l;
+                    const uint32_t ub = r < 0 ? (uint32_t)(-r) : (uint32_t)r;
+                    const int64_t q = (int64_t)(ua / ub);
+                    return ((l < 0) != (r < 0)) ? (T)(-q) : (T)q;
+                }
+                return l / r;
             }
-            return l / r;
         }
     }
 }

@@ -133,6 +133,37 @@ def test_int64_div_large_operands(hip):
 
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64])
+def test_int_div_reused_divisor(hip, dt):
+    """Broadcast and scalar divisors, all magnitudes: bit-exact quotients,
+    wide int64 operands, errors keep the first-element rule."""
+    rng = np.random.default_rng(26)
+    info = np.iinfo(dt)
+    a = rng.integers(info.min, info.max, (40, 1, 96), dtype=dt, endpoint=True)
+    b = rng.integers(-3000, 3000, (1, 24, 96), dtype=dt)
+    b[b == 0] = 7
+    b[0, 0, :8] = [1, -1, 2, -2, info.max, info.min, 3, -3]
+    if dt == np.int64:
+        b[0, 1, :4] = [2**40, -(2**40), 2**33 + 1, -(2**35)]
+        a[1, 0, :4] = [2**20, -(2**31), 2**31 - 1, -(2**20)]
+    a[0, 0, :6] = [info.min + 1, info.max, 0, -1, 1, info.min + 2]
+    a[a == info.min] = info.min + 1  # MIN / -1 is the error case below
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), O.binary(O.DIV, a, b))
+    for d in [1, -1, 7, -13, 1 << 20, info.max, info.min]:
+        s = np.array(d, dt)
+        assert_bits(ok(HIP.Div(dev(a), dev(s))), O.binary(O.DIV, a, s))
+    b0 = b.copy()
+    b0[0, 5, 3] = 0
+    r = HIP.Div(dev(a), dev(b0))
+    assert r.Code == L.ERR_DIVIDE_BY_ZERO
+    a1 = a.copy()
+    a1[2, 0, 1] = info.min  # meets divisor -1 at b[0, 0, 1]
+    r = HIP.Div(dev(a1), dev(b))
+    assert r.Code == L.ERR_OVERFLOW
+    r = HIP.Div(dev(a1), dev(np.array(0, dt)))
+    assert r.Code == L.ERR_DIVIDE_BY_ZERO
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
 def test_int_div_errors(hip, dt):
     info = np.iinfo(dt)
     r = HIP.Div(dev(np.array([4, 5, 6, 7], dt)), dev(np.array([1, 2, 0, 1], dt)))
