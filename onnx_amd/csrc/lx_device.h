@@ -157,6 +157,34 @@ __host__ inline void exp_table_fill_host(ExpTable &s) {
     for (int i = 0; i < 32; i++) s.t[i] = tab[i];
 }
 
+// 2^(k/32) as a double: the table entry for k mod 32 plus k << 47 added to its
+// bit pattern.  The added term has no bits below 47, so only the upper 32-bit
+// word changes: one 32-bit shift-add instead of a 64-bit shift and add.
+typedef uint32_t u32x2_lx __attribute__((ext_vector_type(2)));
+__host__ __device__ __forceinline__ double expf_scale(uint64_t ki, const ExpTable &tab) {
+    u32x2_lx t = __builtin_bit_cast(u32x2_lx, tab.t[ki & 31]);
+    t.y += (uint32_t)ki << 15;
+    return __builtin_bit_cast(double, t);
+}
+
+// The glibc expf method (ARM optimized-routines, N = 32 table, degree-3
+// polynomial, FMA variant) without its special-case early-outs: equal to the
+// host expf for every x in [-104, 88] (callers bound the argument).
+__host__ __device__ __forceinline__ float expf_core_lx(float x, const ExpTable &tab) {
+    double xd = (double)x;
+    double kd = __builtin_fma(LX_EXPF_INVLN2N, xd, LX_EXPF_SHIFT);
+    uint64_t ki = __builtin_bit_cast(uint64_t, kd);
+    kd -= LX_EXPF_SHIFT;
+    double r = __builtin_fma(LX_EXPF_INVLN2N, xd, -kd);
+    double s = expf_scale(ki, tab);
+    double z = __builtin_fma(LX_EXPF_C0, r, LX_EXPF_C1);
+    double r2 = r * r;
+    double y = __builtin_fma(LX_EXPF_C2, r, 1.0);
+    y = __builtin_fma(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
 __host__ __device__ __forceinline__ float expf_lx(float x, const ExpTable &tab) {
     uint32_t ux = __builtin_bit_cast(uint32_t, x);
     uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -166,20 +194,7 @@ __host__ __device__ __forceinline__ float expf_lx(float x, const ExpTable &tab) 
         if (x > 0x1.62e42ep6f) return __builtin_inff();
         if (x < -0x1.9fe368p6f) return 0.0f;
     }
-    double xd = (double)x;
-    double kd = __builtin_fma(LX_EXPF_INVLN2N, xd, LX_EXPF_SHIFT);
-    uint64_t ki = __builtin_bit_cast(uint64_t, kd);
-    kd -= LX_EXPF_SHIFT;
-    double r = __builtin_fma(LX_EXPF_INVLN2N, xd, -kd);
-    uint64_t t = tab.t[ki & 31];
-    t += ki << 47;
-    double s = __builtin_bit_cast(double, t);
-    double z = __builtin_fma(LX_EXPF_C0, r, LX_EXPF_C1);
-    double r2 = r * r;
-    double y = __builtin_fma(LX_EXPF_C2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return (float)y;
+    return expf_core_lx(x, tab);
 }
 
 // expf for arguments <= 0 (or NaN), as produced by Erf (-x*x) and Softmax
@@ -190,20 +205,7 @@ __host__ __device__ __forceinline__ float expf_lx(float x, const ExpTable &tab) 
 // non-positive float by the test suite.
 __host__ __device__ __forceinline__ float expf_nonpos_lx(float x, const ExpTable &tab) {
     x = x < -104.0f ? -104.0f : x;
-    double xd = (double)x;
-    double kd = __builtin_fma(LX_EXPF_INVLN2N, xd, LX_EXPF_SHIFT);
-    uint64_t ki = __builtin_bit_cast(uint64_t, kd);
-    kd -= LX_EXPF_SHIFT;
-    double r = __builtin_fma(LX_EXPF_INVLN2N, xd, -kd);
-    uint64_t t = tab.t[ki & 31];
-    t += ki << 47;
-    double s = __builtin_bit_cast(double, t);
-    double z = __builtin_fma(LX_EXPF_C0, r, LX_EXPF_C1);
-    double r2 = r * r;
-    double y = __builtin_fma(LX_EXPF_C2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
-    y = y * s;
-    return (float)y;
+    return expf_core_lx(x, tab);
 }
 
 // Correctly rounded float quotient x / 1.4142135f (= float32(sqrt 2)) without a
@@ -214,23 +216,19 @@ __host__ __device__ __forceinline__ float expf_nonpos_lx(float x, const ExpTable
 #define LX_INV_SQRT2F_D (1.0 / 1.41421353816986083984375)
 __host__ __device__ __forceinline__ float div_sqrt2f_lx(float x) { return (float)((double)x * LX_INV_SQRT2F_D); }
 
-// Correctly rounded 1/d for d >= 1 from a float reciprocal seed within 1 ulp
-// (v_rcp_f32 is specified to 1 ulp) refined by two Newton steps in double and
-// rounded once.  d >= 2^126 (denormal results), +inf and NaN take the IEEE
-// division.  Checked for every float d in [1, 2^126) and every seed within
-// 1 ulp by the test suite.
-__host__ __device__ __forceinline__ float recip_ge1_from_seed(float d, float seed) {
-    if (!(d < 0x1p126f)) return 1.0f / d;
-    double dd = (double)d;
-    double r = (double)seed;
-    double e = __builtin_fma(-dd, r, 1.0);
-    r = __builtin_fma(r, e, r);
-    e = __builtin_fma(-dd, r, 1.0);
-    r = __builtin_fma(r, e, r);
-    return (float)r;
+// Correctly rounded 1/d for d in [1, 2^126) from a float seed, two float
+// Newton steps:  e = 1 - d*y,  y' = y + e*y  (each one FMA).  Exact for every
+// such d and every seed within 1 ulp of 1/d, except that a d whose significand
+// is all ones (2^k * (2 - 2^-23)) needs the correctly rounded reciprocal as its
+// seed: from the seed one ulp below, y' stops on the tie 2^-k/2.  Checked for
+// all d and seeds by the test suite on the host; the device test checks the
+// v_rcp_f32-seeded result against IEEE division for every d in [1, 2^125].
+__host__ __device__ __forceinline__ float recip_newton2(float d, float seed) {
+    float e = __builtin_fmaf(-d, seed, 1.0f);
+    float y = __builtin_fmaf(e, seed, seed);
+    e = __builtin_fmaf(-d, y, 1.0f);
+    return __builtin_fmaf(e, y, y);
 }
-
-__device__ __forceinline__ float recip_ge1_lx(float d) { return recip_ge1_from_seed(d, __builtin_amdgcn_rcpf(d)); }
 
 // ---------------------------------------------------------------------------
 // MathOps.Erf(float) (MathOps.cs:988-1010): Abramowitz & Stegun 7.1.26 in
@@ -262,25 +260,13 @@ __device__ __forceinline__ float div_by_row_lx(float a, float s, float rs) {
     return __builtin_fmaf(rem, rs, q);
 }
 
-// Two double Newton steps from a seed within 1 ulp of 1/d, rounded once: the
-// correctly rounded 1/d for every float d in [1, 2^126) (the branch-free core
-// of recip_ge1_from_seed).
-__host__ __device__ __forceinline__ float recip_newton2(float d, float seed) {
-    double dd = (double)d;
-    double r = (double)seed;
-    double e = __builtin_fma(-dd, r, 1.0);
-    r = __builtin_fma(r, e, r);
-    e = __builtin_fma(-dd, r, 1.0);
-    r = __builtin_fma(r, e, r);
-    return (float)r;
-}
-
 // erf_lx with its division and exponential replaced by exact equivalents.
 // d = 1 + p|x| is clamped to 2^125 before the reciprocal: d >= 2^125 means
 // |x| > 1.3e38, where expf(-x*x) is exactly 0 and the product poly*t*0 is 0
 // for any finite t; NaN also clamps and still yields NaN through expf.  The
 // result equals erf_lx bit for bit for all 2^32 inputs (checked on the host
-// with the exact seed, any seed within 1 ulp giving the same reciprocal).
+// with the correctly rounded seed; recip_newton2 gives the same reciprocal
+// from the device seed).
 template <typename SeedFn>
 __host__ __device__ __forceinline__ float erf_fast_core(float x, const ExpTable &tab, SeedFn seed) {
     const float a1 = 0.254829592f;
@@ -305,6 +291,37 @@ struct RcpSeed {
 };
 
 __device__ __forceinline__ float erf_fast_lx(float x, const ExpTable &tab) { return erf_fast_core(x, tab, RcpSeed()); }
+
+// One element of the GELU subgraph Div(x, sqrt 2) -> Erf -> Add 1 -> Mul x ->
+// Mul 0.5, every node rounded as the reference rounds it, with two rewrites
+// of the Erf node that the chain's output cannot see: the sign of erf is
+// copied from its argument (erf(-0) becomes -0, and -0 + 1 == +0 + 1), and the
+// exponential's argument is clamped with a max that sends NaN to -104 (a NaN
+// argument comes from a NaN x, which reaches the output through x * b either
+// way).  Equal to the unfused chain bit for bit for all 2^32 inputs (NaN for
+// NaN), checked on the host with the correctly rounded seed.
+template <typename SeedFn>
+__host__ __device__ __forceinline__ float gelu_erf_core(float x, const ExpTable &tab, SeedFn seed) {
+    const float a1 = 0.254829592f;
+    const float a2 = -0.284496736f;
+    const float a3 = 1.421413741f;
+    const float a4 = -1.453152027f;
+    const float a5 = 1.061405429f;
+    const float p = 0.3275911f;
+    const float a = div_sqrt2f_lx(x);
+    const float ax = __builtin_fabsf(a);
+    float d = 1.0f + p * ax;
+    d = d < 0x1p125f ? d : 0x1p125f;
+    const float t = recip_newton2(d, seed(d));
+    const float poly = ((((a5 * t + a4) * t) + a3) * t + a2) * t + a1;
+    const float e = expf_core_lx(__builtin_fmaxf(-ax * ax, -104.0f), tab);
+    const float erf = __builtin_copysignf(1.0f - poly * t * e, a);
+    const float b = erf + 1.0f;
+    const float c = x * b;
+    return c * 0.5f;
+}
+
+__device__ __forceinline__ float gelu_erf_lx(float x, const ExpTable &tab) { return gelu_erf_core(x, tab, RcpSeed()); }
 
 // MathOps.Erf(double) (MathOps.cs:1012-1034) with the device double exp.
 __device__ __forceinline__ double erf_lx(double x) {

@@ -65,23 +65,28 @@ long long lx_test_div_sqrt2_mismatches(void) {
     return bad;
 }
 
-// every d in [1, 2^126) with every seed within 1 ulp of 1/d, plus d >= 2^126, inf, NaN
-long long lx_test_recip_mismatches(void) {
-    long long bad = 0;
+// every d in [1, 2^126) with every seed within 1 ulp of 1/d: number of
+// (d, seed) pairs where recip_newton2 differs from 1/d, split into d with an
+// all-ones significand (out[1]) and every other d (out[0])
+void lx_test_recip_mismatches(long long *out) {
+    long long bad = 0, ones = 0;
     const uint32_t lo = bits(1.0f), hi = bits(0x1p126f);
-#pragma omp parallel for reduction(+ : bad) schedule(static)
+#pragma omp parallel for reduction(+ : bad, ones) schedule(static)
     for (long long u = lo; u < (long long)hi; u++) {
         float d = fbits((uint32_t)u);
         float cr = 1.0f / d;
         for (int k = -1; k <= 1; k++) {
             float seed = fbits(bits(cr) + k);
-            if (!same(lx::recip_ge1_from_seed(d, seed), cr)) bad++;
+            if (!same(lx::recip_newton2(d, seed), cr)) {
+                if ((u & 0x7fffff) == 0x7fffff) ones++;
+                else bad++;
+            }
         }
+        // the correctly rounded seed itself is always a fixed point
+        if (!same(lx::recip_newton2(d, cr), cr)) bad++;
     }
-    float extra[] = {0x1p126f, 0x1.fffffep127f, __builtin_inff(), __builtin_nanf("")};
-    for (float d : extra)
-        if (!same(lx::recip_ge1_from_seed(d, 0.0f), 1.0f / d)) bad++;
-    return bad;
+    out[0] = bad;
+    out[1] = ones;
 }
 
 // every x <= 0 (sign bit set), +0 and NaN: expf_nonpos_lx(x) == expf(x)
@@ -116,6 +121,28 @@ long long lx_test_erf_fast_mismatches(void) {
     for (long long u = 0; u < (1ll << 32); u++) {
         float x = fbits((uint32_t)u);
         if (!same(lx::erf_fast_core(x, tab, ExactSeed()), lx::erf_lx(x, tab))) bad++;
+    }
+    return bad;
+}
+}
+
+extern "C" {
+// all 2^32 x: the fused device GELU element == the unfused chain
+// Div(x, 1.4142135f) -> Erf (erf_lx) -> Add 1 -> Mul x -> Mul 0.5 in IEEE float
+long long lx_test_gelu_mismatches(void) {
+    lx::ExpTable tab;
+    lx::exp_table_fill_host(tab);
+    const volatile float c = 1.41421353816986083984375f;
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long u = 0; u < (1ll << 32); u++) {
+        float x = fbits((uint32_t)u);
+        float a = x / c;
+        float e = lx::erf_lx(a, tab);
+        float b = e + 1.0f;
+        float cc = x * b;
+        float ref = cc * 0.5f;
+        if (!same(lx::gelu_erf_core(x, tab, ExactSeed()), ref)) bad++;
     }
     return bad;
 }

@@ -1,0 +1,49 @@
+// TEST HELPER (device): checks on the GPU that the v_rcp_f32-seeded reciprocal
+// used by the Erf / GELU kernels (recip_newton2 in lx_device.h) equals IEEE
+// float division 1.0f / d for every float d in [1, 2^126).  Built for gfx950
+// by __graft_entry__.build(); called by the GPU tests through ctypes.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../onnx_amd/csrc/lx_device.h"
+
+namespace {
+
+constexpr uint32_t kLo = 0x3f800000u;  // 1.0f
+constexpr uint32_t kHi = 0x7e800000u;  // 2^126
+
+// counts[0]: recip_newton2 != 1/d; counts[1]: seed != 1/d (informational);
+// counts[2]: seed != 1/d where d's significand is all ones
+__global__ void k_check(unsigned long long *counts) {
+    unsigned long long bad = 0, seed_off = 0, ones_off = 0;
+    const uint32_t stride = gridDim.x * blockDim.x;
+    for (uint32_t u = kLo + blockIdx.x * blockDim.x + threadIdx.x; u < kHi; u += stride) {
+        const float d = __builtin_bit_cast(float, u);
+        const float cr = 1.0f / d;
+        const float seed = __builtin_amdgcn_rcpf(d);
+        const float y = lx::recip_newton2(d, seed);
+        bad += __builtin_bit_cast(uint32_t, y) != __builtin_bit_cast(uint32_t, cr);
+        const bool off = __builtin_bit_cast(uint32_t, seed) != __builtin_bit_cast(uint32_t, cr);
+        seed_off += off;
+        ones_off += off && (u & 0x7fffffu) == 0x7fffffu;
+    }
+    if (bad) atomicAdd(&counts[0], bad);
+    if (seed_off) atomicAdd(&counts[1], seed_off);
+    if (ones_off) atomicAdd(&counts[2], ones_off);
+}
+
+}  // namespace
+
+extern "C" int lx_test_device_recip(long long *out) {
+    unsigned long long *d = nullptr;
+    hipError_t e = hipMalloc(&d, 3 * sizeof(unsigned long long));
+    if (e != hipSuccess) return (int)e;
+    e = hipMemset(d, 0, 3 * sizeof(unsigned long long));
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(k_check, dim3(8192), dim3(256), 0, 0, d);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipMemcpy(out, d, 3 * sizeof(unsigned long long), hipMemcpyDeviceToHost);
+    (void)hipFree(d);
+    return (int)e;
+}

@@ -9,6 +9,7 @@ Bars (written per test):
               reference folds serially; any parallel order differs)
   softmax   : |gpu - ref| <= 1e-5 * |ref| (+1e-30 for underflowed entries)
 """
+import ctypes
 import json
 import os
 
@@ -439,6 +440,18 @@ def test_add_softmax(hip, s_shape, m_shape):
     np.testing.assert_array_equal(np.isnan(got), nan)
     err = np.abs(got.astype(np.float64) - ref)[~nan]
     assert np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30), err.max()
+
+
+def test_device_reciprocal_is_correctly_rounded(hip):
+    """The Erf / GELU reciprocal (v_rcp_f32 seed, two float Newton steps)
+    equals IEEE 1.0f / d on the device for every float d in [1, 2^126); in
+    particular v_rcp_f32 is exact on the all-ones significands, the one case
+    the Newton steps do not repair from an off-by-one seed."""
+    lib = ctypes.CDLL(os.path.join(HERE, "native", "librcp_check.so"))
+    out = (ctypes.c_longlong * 3)()
+    assert lib.lx_test_device_recip(out) == 0
+    assert out[0] == 0, f"{out[0]} reciprocals differ from 1/d ({out[1]} seeds off by one ulp)"
+    assert out[2] == 0
 
 
 def test_gelu_chain_bit_exact(hip):

@@ -114,7 +114,8 @@ def _native():
     lib.lx_test_erf.argtypes = [ctypes.c_float]
     lib.lx_test_fastdiv.restype = ctypes.c_uint32
     lib.lx_test_fastdiv.argtypes = [ctypes.c_uint32, ctypes.c_uint32]
-    for f in ("lx_test_div_sqrt2_mismatches", "lx_test_recip_mismatches", "lx_test_expf_nonpos_mismatches"):
+    for f in ("lx_test_div_sqrt2_mismatches", "lx_test_expf_nonpos_mismatches", "lx_test_erf_fast_mismatches",
+              "lx_test_gelu_mismatches"):
         getattr(lib, f).restype = ctypes.c_longlong
     return lib
 
@@ -155,12 +156,18 @@ def test_division_free_sequences_are_exact():
     """The device Erf / GELU replace IEEE divisions and the expf early-outs by
     exact equivalents; each is proven here by exhaustion on the host:
       x / 1.4142135f  == (float)(x * (double)(1/1.4142135f))   for all 2^32 x
-      1 / d           == two double Newton steps from any seed within 1 ulp,
-                         for every float d in [1, 2^126)
+      1 / d           == two float Newton steps from any seed within 1 ulp,
+                         for every float d in [1, 2^126), except that a d with
+                         an all-ones significand needs the correctly rounded
+                         seed (the device check covers v_rcp_f32 there)
       expf(x)         == the clamped early-out-free expf for every x <= 0."""
     lib = _native()
     assert lib.lx_test_div_sqrt2_mismatches() == 0
-    assert lib.lx_test_recip_mismatches() == 0
+    out = (ctypes.c_longlong * 2)()
+    lib.lx_test_recip_mismatches(out)
+    assert out[0] == 0
+    # exactly the two off-by-one seeds of each of the 126 all-ones significands
+    assert out[1] == 2 * 126
     assert lib.lx_test_expf_nonpos_mismatches() == 0
 
 
@@ -168,5 +175,11 @@ def test_branch_free_erf_equals_reference_formula():
     """The device Erf core (clamped reciprocal argument, early-out-free expf)
     returns the A&S 7.1.26 formula's bits for all 2^32 inputs."""
     lib = _native()
-    lib.lx_test_erf_fast_mismatches.restype = ctypes.c_longlong
     assert lib.lx_test_erf_fast_mismatches() == 0
+
+
+def test_fused_gelu_equals_unfused_chain():
+    """The fused GELU element (sign copied onto erf, max-clamped exponential
+    argument) returns the unfused five-node chain's bits for all 2^32 inputs."""
+    lib = _native()
+    assert lib.lx_test_gelu_mismatches() == 0
