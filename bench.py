@@ -45,11 +45,12 @@ def log(*a):
 EAGER = False
 
 
-def graph_time(torch, launch, steps, warmup, set_stream):
+def graph_time(torch, launch, steps, warmup, set_stream, reps=1):
     """Run `launch(i)` warmup times eagerly, capture `steps` launches in a HIP
-    graph, replay it once untimed, then time one replay with HIP events.
-    Returns milliseconds per step.  With EAGER (--eager, used under rocprofv3
-    counter collection) the steps run as ordinary launches instead."""
+    graph, replay it once untimed, then time `reps` replays with HIP events.
+    Returns milliseconds per step (the median replay).  With EAGER (--eager,
+    used under rocprofv3 counter collection) the steps run as ordinary launches
+    instead."""
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
@@ -74,14 +75,17 @@ def graph_time(torch, launch, steps, warmup, set_stream):
     torch.cuda.synchronize()
     g.replay()
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    times = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) / steps)
+    return sorted(times)[len(times) // 2]
 
 
 def measured_traffic():
@@ -138,7 +142,7 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
         res.append(d)
 
     def run(name, nbytes, elems, fn, nsets, k=None):
-        ms = graph_time(torch, fn, k or steps, warmup, set_stream)
+        ms = graph_time(torch, fn, k or steps, warmup, set_stream, reps=5)
         record(name, nbytes, elems, ms)
 
     # C1: A[1,128,384] + B[384], then * 0.125 (700 rotating sets: > 256 MB)

@@ -19,7 +19,7 @@
 namespace lx {
 
 constexpr int kSBlock = 256;
-constexpr int64_t kSoftmaxMaxBlocks = 8192;  // 32768 waves; each loops over its share of rows
+constexpr int64_t kSoftmaxMaxBlocks = 16384;  // 65536 waves; each loops over its share of rows
 
 // argument x - max is <= 0 (or NaN): the early-out-free expf applies
 template <typename T>
@@ -56,10 +56,40 @@ __device__ __forceinline__ int64_t mask_row_offset(uint32_t row, const NdLayout 
     return off;
 }
 
+// Loads one row's vectors (and, with a mask, the mask vectors it adds): the
+// mask loads go first so that a wave waiting for them never waits for loads
+// issued after them.
+template <typename T, int V, int NV, int NOUT>
+__device__ __forceinline__ void softmax_row_load(const T *__restrict__ x, int64_t row, int r, int lane,
+                                                 const T *__restrict__ mask, int mask_inner, const NdLayout &mrows,
+                                                 Vec<T, V> (&xv)[NV], Vec<T, V> (&mv)[NV]) {
+    if constexpr (NOUT != 0) {
+        const T *m = mask + mask_row_offset<NOUT>((uint32_t)row, mrows);
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const int col = (c * 64 + lane) * V;
+            if (col < r) {
+                if (mask_inner) {
+                    mv[c] = vload<T, V>(m + col);
+                } else {
+                    const T m0 = m[0];
+#pragma unroll
+                    for (int k = 0; k < V; k++) mv[c].v[k] = m0;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (col < r) xv[c] = vload_nt<T, V>(x + row * (int64_t)r + col);
+    }
+}
+
 // Rows of length r <= 64*V*NV held in registers, one wave per row at a time.
 // Each wave walks rows w, w + W, ... (W = all waves of the grid) and loads the
-// next row while it finishes the current one.  NOUT: mask row axes (0 = no
-// mask; see mask_row_offset).
+// next row (and its mask vectors) while it finishes the current one.  NOUT:
+// mask row axes (0 = no mask; see mask_row_offset).
 template <typename T, int V, int NV, int NOUT>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
@@ -74,36 +104,18 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     const int64_t W = (int64_t)gridDim.x * (kSBlock / 64);
     int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6);
     if (row >= rows) return;
-    Vec<T, V> cur[NV], nxt[NV];
-#pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * V;
-        if (col < r) cur[c] = vload_nt<T, V>(x + row * (int64_t)r + col);
-    }
+    Vec<T, V> cur[NV], nxt[NV], mcur[NV], mnxt[NV];
+    softmax_row_load<T, V, NV, NOUT>(x, row, r, lane, mask, mask_inner, mrows, cur, mcur);
     for (; row < rows; row += W) {
         const int64_t next = row + W;
-        if (next < rows) {
-#pragma unroll
-            for (int c = 0; c < NV; c++) {
-                const int col = (c * 64 + lane) * V;
-                if (col < r) nxt[c] = vload_nt<T, V>(x + next * (int64_t)r + col);
-            }
-        }
+        if (next < rows) softmax_row_load<T, V, NV, NOUT>(x, next, r, lane, mask, mask_inner, mrows, nxt, mnxt);
         if constexpr (MASK) {
-            const T *m = mask + mask_row_offset<NOUT>((uint32_t)row, mrows);
 #pragma unroll
             for (int c = 0; c < NV; c++) {
                 const int col = (c * 64 + lane) * V;
                 if (col < r) {
-                    if (mask_inner) {
-                        Vec<T, V> mv = vload<T, V>(m + col);
 #pragma unroll
-                        for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mv.v[k];
-                    } else {
-                        const T mv = m[0];
-#pragma unroll
-                        for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mv;
-                    }
+                    for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mcur[c].v[k];
                 }
             }
         }
@@ -144,7 +156,10 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
             }
         }
 #pragma unroll
-        for (int c = 0; c < NV; c++) cur[c] = nxt[c];
+        for (int c = 0; c < NV; c++) {
+            cur[c] = nxt[c];
+            if constexpr (MASK) mcur[c] = mnxt[c];
+        }
     }
 }
 
