@@ -813,6 +813,7 @@ int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_
     const bool fused = X->dtype == LX_FLOAT && gamma->dtype == LX_FLOAT && beta->dtype == LX_FLOAT && X->rank >= 1 &&
                        numel(gamma) == r && numel(beta) == r && gamma->rank >= 1 && beta->rank >= 1 &&
                        gamma->rank <= X->rank && beta->rank <= X->rank && layernorm_supported(r) &&
+                       numel(X) / r < (1ll << 31) &&  // one block per row
                        aligned16(X->data) && aligned16(gamma->data) && aligned16(beta->data);
     if (fused) {
         if ((st = prepare_output(Y, LX_FLOAT, X->rank, X->dims))) return st;

@@ -391,12 +391,16 @@ int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inne
 // m = n * gamma;  y = m + beta.  Only the two sums run in a different order
 // from the reference's serial fold.
 // ---------------------------------------------------------------------------
+// One row per 64-thread block (4096 blocks for C2): measured 3% faster on
+// MI355X than four rows per 256-thread block.
+constexpr int kLnBlock = 64;
+
 template <int NV>
-__global__ __launch_bounds__(kRBlock) void k_layernorm(const float *__restrict__ x, const float *__restrict__ gamma,
+__global__ __launch_bounds__(kLnBlock) void k_layernorm(const float *__restrict__ x, const float *__restrict__ gamma,
                                                        const float *__restrict__ beta, float eps,
                                                        float *__restrict__ y, int64_t rows, int r) {
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6);
+    const int64_t row = (int64_t)blockIdx.x * (kLnBlock / 64) + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float *p = x + row * (int64_t)r;
     float *q = y + row * (int64_t)r;
@@ -458,10 +462,10 @@ hipError_t launch_layernorm(const float *x, const float *gamma, const float *bet
     if (rows == 0) return hipSuccess;
     if (!layernorm_supported(r)) return hipErrorInvalidValue;
     const int nv = (int)ceil_div(r, 256);
-    const int g = (int)ceil_div(rows, kRBlock / 64);
+    const int g = (int)ceil_div(rows, kLnBlock / 64);
     const int ri = (int)r;
 #define LX_LN_CASE(N) \
-    case N: hipLaunchKernelGGL((k_layernorm<N>), dim3(g), dim3(kRBlock), 0, s, x, gamma, beta, eps, y, rows, ri); break;
+    case N: hipLaunchKernelGGL((k_layernorm<N>), dim3(g), dim3(kLnBlock), 0, s, x, gamma, beta, eps, y, rows, ri); break;
     switch (nv) {
         LX_LN_CASE(1) LX_LN_CASE(2) LX_LN_CASE(3) LX_LN_CASE(4) LX_LN_CASE(5) LX_LN_CASE(6) LX_LN_CASE(7) LX_LN_CASE(8)
         LX_LN_CASE(9) LX_LN_CASE(10) LX_LN_CASE(11) LX_LN_CASE(12) LX_LN_CASE(13) LX_LN_CASE(14) LX_LN_CASE(15)
