@@ -56,9 +56,9 @@ enum lx_status {
  * Device tensor handle: the device twin of DenseTensor<T>
  * (src/Lokad.Onnx.Tensors/DenseTensor.cs:31-278): row-major contiguous
  * storage, int64 dims, explicit host/device residency.
- *   data     : device address (hipMalloc'd by lx_tensor_alloc, or wrapped)
+ *   data     : device address (from the library's pool by lx_tensor_alloc, or wrapped)
  *   capacity : bytes usable at data
- *   owns     : 1 if lx_tensor_free must release data
+ *   owns     : 1 if lx_tensor_free must release data (back to the pool)
  * Operator outputs: if Y->data is NULL the operator allocates Y (owns = 1);
  * otherwise it writes into Y->data (capacity checked, LX_ERR_BUFFER_TOO_SMALL)
  * and only updates dtype/rank/dims.  Inputs are never modified.
@@ -119,6 +119,13 @@ int lx_tensor_download(const lx_tensor *t, void *host, int64_t nbytes);       /*
 /* Reshape / Unsqueeze alias: same storage, new dims (DenseTensor.cs:231-242). */
 int lx_tensor_reshape(const lx_tensor *t, int32_t rank, const int64_t *dims, lx_tensor *out);
 
+/* Device memory pool: released tensor storage is cached per size class and
+ * reused by later allocations on the library stream (no reference counterpart:
+ * the reference's storage is GC-managed managed arrays, DenseTensor.cs:34-35).
+ * lx_pool_trim synchronises and returns every cached block to HIP. */
+int lx_pool_trim(void);
+int lx_pool_stats(int64_t *live_bytes, int64_t *cached_bytes);
+
 /* ---- planner ------------------------------------------------------------ */
 int lx_plan_broadcast(int32_t rank_a, const int64_t *dims_a, int32_t rank_b, const int64_t *dims_b,
                       lx_bcast_plan *plan);
@@ -164,6 +171,74 @@ int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_
                            lx_tensor *Y);
 /* Add(S, mask) -> Softmax(axis) with the mask broadcast against S. */
 int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_tensor *Y);
+
+/* ---- graph runtime: ComputationalGraph + Node.Execute on the device -------
+ * (src/Lokad.Onnx.Backend/ComputationalGraph.cs, Node.cs, Model.cs).  Graph
+ * inputs, initializers, intermediates and outputs stay in HBM for the whole
+ * execution; only the caller's uploads and downloads cross PCIe.  Nodes run in
+ * the order they were added (the ONNX topological order the reference keeps,
+ * Model.cs:56-60) and execution stops at the first failing node
+ * (ComputationalGraph.cs:245-250) with lx_last_error naming it. */
+typedef struct lx_graph lx_graph;
+
+/* new ComputationalGraph() with Opset[""] = opset (Model.cs:33-37). */
+int lx_graph_create(int64_t opset, lx_graph **out);
+int lx_graph_free(lx_graph *g);
+/* graph.Inputs / graph.Outputs entries from ValueInfoProto (Model.cs:48-50,
+ * TensorUtil.cs:62-84); dims < 0 or a symbolic dim are stored as 0 like
+ * DimValue of a dim_param. */
+int lx_graph_add_input(lx_graph *g, const char *name, int32_t dtype, int32_t rank, const int64_t *dims);
+int lx_graph_add_output(lx_graph *g, const char *name);
+/* graph.Initializers[name] = TensorProto.ToTensor() (Model.cs:44-47, TensorUtil.cs:14-58); the host
+ * bytes (row-major) are uploaded to HBM once, on the first execution if the graph was built before
+ * lx_init. */
+int lx_graph_add_initializer(lx_graph *g, const char *name, int32_t dtype, int32_t rank, const int64_t *dims,
+                             const void *host, int64_t nbytes);
+/* NodeProto.ToNode (NodeUtil.cs:25-50): op_type must name an ONNX operator (OpType.cs); the node
+ * index is returned through *index for the attribute setters. */
+int lx_graph_add_node(lx_graph *g, const char *name, const char *op_type, int32_t n_in, const char *const *inputs,
+                      int32_t n_out, const char *const *outputs, int32_t *index);
+/* Node.Attributes values (AttributeProto.Value, NodeUtil.cs:9-22). */
+int lx_graph_set_attr_int(lx_graph *g, int32_t node, const char *attr, int64_t v);
+int lx_graph_set_attr_ints(lx_graph *g, int32_t node, const char *attr, const int64_t *v, int32_t n);
+int lx_graph_set_attr_float(lx_graph *g, int32_t node, const char *attr, float v);
+int lx_graph_set_attr_floats(lx_graph *g, int32_t node, const char *attr, const float *v, int32_t n);
+int lx_graph_set_attr_string(lx_graph *g, int32_t node, const char *attr, const char *v);
+int lx_graph_set_attr_tensor(lx_graph *g, int32_t node, const char *attr, int32_t dtype, int32_t rank,
+                             const int64_t *dims, const void *host, int64_t nbytes);
+/* Model.Parse + Model.Load (Model.cs:14-63) from the bytes of an ONNX ModelProto. */
+int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
+/* Pattern fusion (no reference counterpart; the reference runs every node):
+ * replaces the GELU subgraph (Div sqrt2 -> Erf -> Add 1 -> Mul x -> Mul 0.5), the decomposed
+ * LayerNorm (ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul -> Add) and
+ * Add(mask) -> Softmax by the fused kernels when every intermediate has exactly one consumer and is
+ * not a graph output.  *n_fused = number of subgraphs replaced. */
+int lx_graph_fuse(lx_graph *g, int32_t *n_fused);
+/* ComputationalGraph.Execute(userInputs, useInitializers) (ComputationalGraph.cs:199-272) with the
+ * inputs given by name (the Dictionary overload, ComputationalGraph.cs:105-130) or, when names is
+ * NULL, by position (the ITensor[] overload, 73-103).  Input tensors are borrowed. */
+int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs,
+                     int32_t use_initializers);
+/* ComputationalGraph.ExecuteNode (ComputationalGraph.cs:274-334). */
+int lx_graph_execute_node(lx_graph *g, const char *node, int32_t n, const char *const *names,
+                          const lx_tensor *inputs, int32_t use_initializers);
+/* graph.Outputs[name] after an execution: a view (owns = 0) of device storage the graph keeps
+ * until lx_graph_reset, the next execution or lx_graph_free. */
+int lx_graph_output(lx_graph *g, const char *name, lx_tensor *out);
+/* ComputationalGraph.Reset (ComputationalGraph.cs:336-349): drops intermediates and outputs (their
+ * storage returns to the pool). */
+int lx_graph_reset(lx_graph *g);
+/* introspection for callers and tests */
+int32_t lx_graph_node_count(const lx_graph *g);
+int lx_graph_node_info(const lx_graph *g, int32_t i, char *op_type, int32_t op_len, char *name, int32_t name_len);
+int32_t lx_graph_input_count(const lx_graph *g);
+int lx_graph_input_info(const lx_graph *g, int32_t i, char *name, int32_t name_len, int32_t *dtype, int32_t *rank,
+                        int64_t *dims);
+int32_t lx_graph_initializer_count(const lx_graph *g);
+int lx_graph_initializer_info(const lx_graph *g, int32_t i, char *name, int32_t name_len, int32_t *dtype,
+                              int32_t *rank, int64_t *dims);
+int32_t lx_graph_output_count(const lx_graph *g);
+int lx_graph_output_name(const lx_graph *g, int32_t i, char *name, int32_t name_len);
 
 #ifdef __cplusplus
 }

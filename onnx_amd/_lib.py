@@ -92,6 +92,42 @@ SIGNATURES = {
     "lx_GeluErf": (_c.c_int, [_T, _T]),
     "lx_LayerNormDecomposed": (_c.c_int, [_T, _T, _T, _c.c_float, _T]),
     "lx_AddSoftmax": (_c.c_int, [_T, _T, _c.c_int32, _T]),
+    "lx_pool_trim": (_c.c_int, []),
+    "lx_pool_stats": (_c.c_int, [_i64p, _i64p]),
+    # graph runtime
+    "lx_graph_create": (_c.c_int, [_c.c_int64, _c.POINTER(_c.c_void_p)]),
+    "lx_graph_free": (_c.c_int, [_c.c_void_p]),
+    "lx_graph_add_input": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_int32, _c.c_int32, _i64p]),
+    "lx_graph_add_output": (_c.c_int, [_c.c_void_p, _c.c_char_p]),
+    "lx_graph_add_initializer": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_int32, _c.c_int32, _i64p, _c.c_void_p,
+                                            _c.c_int64]),
+    "lx_graph_add_node": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_char_p, _c.c_int32, _c.POINTER(_c.c_char_p),
+                                     _c.c_int32, _c.POINTER(_c.c_char_p), _c.POINTER(_c.c_int32)]),
+    "lx_graph_set_attr_int": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int64]),
+    "lx_graph_set_attr_ints": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _i64p, _c.c_int32]),
+    "lx_graph_set_attr_float": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_float]),
+    "lx_graph_set_attr_floats": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.POINTER(_c.c_float),
+                                            _c.c_int32]),
+    "lx_graph_set_attr_string": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_char_p]),
+    "lx_graph_set_attr_tensor": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int32, _c.c_int32, _i64p,
+                                            _c.c_void_p, _c.c_int64]),
+    "lx_graph_load_onnx": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.POINTER(_c.c_void_p)]),
+    "lx_graph_fuse": (_c.c_int, [_c.c_void_p, _c.POINTER(_c.c_int32)]),
+    "lx_graph_execute": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.POINTER(_c.c_char_p), _T, _c.c_int32]),
+    "lx_graph_execute_node": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_int32, _c.POINTER(_c.c_char_p), _T,
+                                         _c.c_int32]),
+    "lx_graph_output": (_c.c_int, [_c.c_void_p, _c.c_char_p, _T]),
+    "lx_graph_reset": (_c.c_int, [_c.c_void_p]),
+    "lx_graph_node_count": (_c.c_int32, [_c.c_void_p]),
+    "lx_graph_node_info": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int32, _c.c_char_p, _c.c_int32]),
+    "lx_graph_input_count": (_c.c_int32, [_c.c_void_p]),
+    "lx_graph_input_info": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int32, _c.POINTER(_c.c_int32),
+                                       _c.POINTER(_c.c_int32), _i64p]),
+    "lx_graph_initializer_count": (_c.c_int32, [_c.c_void_p]),
+    "lx_graph_initializer_info": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int32,
+                                             _c.POINTER(_c.c_int32), _c.POINTER(_c.c_int32), _i64p]),
+    "lx_graph_output_count": (_c.c_int32, [_c.c_void_p]),
+    "lx_graph_output_name": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int32]),
 }
 
 _lib = None

@@ -16,6 +16,7 @@
 
 #include "../../include/lonnx.h"
 #include "lx_kernels.h"
+#include "lx_pool.h"
 
 using namespace lx;
 
@@ -175,15 +176,31 @@ int prepare_output(lx_tensor *Y, int dtype, int rank, const int64_t *dims) {
                            (long long)Y->capacity, (long long)bytes);
     } else {
         void *p = nullptr;
-        HIPCHECK(hipMalloc(&p, bytes > 0 ? bytes : 16), "hipMalloc(output)");
+        size_t cap = 0;
+        HIPCHECK(pool_alloc((size_t)bytes, &p, &cap, g.stream), "device allocation (output)");
         Y->data = p;
-        Y->capacity = bytes;
+        Y->capacity = bytes;  // the tensor's own size, not the pool block's rounded one
         Y->owns = 1;
     }
     Y->dtype = dtype;
     Y->rank = rank;
     for (int i = 0; i < LX_MAX_RANK; i++) Y->dims[i] = i < rank ? dims[i] : 0;
     return LX_OK;
+}
+
+// Temporaries of multi-pass work: from the pool, or, while the stream is being
+// captured into a HIP graph, stream-ordered allocations that the graph owns
+// (a pooled block could be handed to other work while the graph still replays
+// into it).
+hipError_t alloc_temp(void **p, int64_t bytes, bool capturing) {
+    if (capturing) return hipMallocAsync(p, bytes, g.stream);
+    return pool_alloc((size_t)bytes, p, nullptr, g.stream);
+}
+
+void release_temp(void *p, bool capturing) {
+    if (!p) return;
+    if (capturing) (void)hipFreeAsync(p, g.stream);
+    else (void)pool_release(p);
 }
 
 int ensure_workspace(int64_t bytes) {
@@ -495,6 +512,9 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
     // passes: reduce the innermost reduced group first
     const void *src = X->data;
     void *tmp[2] = {nullptr, nullptr};
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void)hipStreamIsCapturing(g.stream, &cs);
+    const bool capturing = cs != hipStreamCaptureStatusNone;
     int pass = 0;
     int result = LX_OK;
     while (nred > 0) {
@@ -510,9 +530,10 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         if (last) dst = Y->data;
         else {
             int slot = pass & 1;
-            if (tmp[slot]) (void)hipFreeAsync(tmp[slot], g.stream);
-            hipError_t e = hipMallocAsync(&tmp[slot], std::max<int64_t>(outer * inner * es, 16), g.stream);
-            if (e != hipSuccess) { result = hip_fail(e, "hipMallocAsync(temporary)"); break; }
+            release_temp(tmp[slot], capturing);
+            tmp[slot] = nullptr;
+            hipError_t e = alloc_temp(&tmp[slot], std::max<int64_t>(outer * inner * es, 16), capturing);
+            if (e != hipSuccess) { result = hip_fail(e, "device allocation (temporary)"); break; }
             dst = tmp[slot];
         }
         ReduceArgs ra;
@@ -549,8 +570,7 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         nred--;
         pass++;
     }
-    for (void *t : tmp)
-        if (t) (void)hipFreeAsync(t, g.stream);
+    for (void *t : tmp) release_temp(t, capturing);
     return result;
 }
 
@@ -558,6 +578,20 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
                 const char *opn);
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// internal interface for the graph runtime (lx_internal.h)
+// ---------------------------------------------------------------------------
+namespace lx {
+int api_set_error(int code, const std::string &message) {
+    g_err = message;
+    return code;
+}
+bool api_initialized() { return g.init; }
+hipStream_t api_stream() { return g.stream; }
+int64_t api_esize(int dtype) { return esize(dtype); }
+const char *api_dtype_name(int dtype) { return dtype_name(dtype); }
+}  // namespace lx
 
 // ===========================================================================
 // C ABI
@@ -593,6 +627,7 @@ int lx_init(int32_t device) {
 int lx_shutdown(void) {
     if (!g.init) return LX_OK;
     (void)hipDeviceSynchronize();
+    (void)pool_trim(g.stream);
     if (g.workspace) (void)hipFree(g.workspace);
     if (g.errs) (void)hipFree(g.errs);
 
@@ -604,7 +639,15 @@ int lx_shutdown(void) {
 
 int lx_set_stream(void *s) {
     REQUIRE_INIT();
-    g.stream = s ? (hipStream_t)s : g.own_stream;
+    hipStream_t ns = s ? (hipStream_t)s : g.own_stream;
+    // pooled blocks released by work on the old stream may be reused by work on
+    // the new one: the old stream's work completes first
+    if (ns != g.stream) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        (void)hipStreamIsCapturing(g.stream, &cs);
+        if (cs == hipStreamCaptureStatusNone) HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+    }
+    g.stream = ns;
     return LX_OK;
 }
 
@@ -644,7 +687,7 @@ int lx_tensor_wrap(int32_t dtype, int32_t rank, const int64_t *dims, void *ptr, 
 
 int lx_tensor_free(lx_tensor *t) {
     if (!t) return LX_OK;
-    if (t->owns && t->data) {
+    if (t->owns && t->data && !pool_release(t->data)) {
         if (g.init) (void)hipStreamSynchronize(g.stream);
         HIPCHECK(hipFree(t->data), "hipFree");
     }
@@ -687,6 +730,17 @@ int lx_tensor_reshape(const lx_tensor *t, int32_t rank, const int64_t *dims, lx_
     for (int i = 0; i < LX_MAX_RANK; i++) o.dims[i] = i < rank ? dims[i] : 0;
     o.owns = 0;  // alias: the original keeps ownership
     *out = o;
+    return LX_OK;
+}
+
+int lx_pool_trim(void) {
+    REQUIRE_INIT();
+    HIPCHECK(pool_trim(g.stream), "pool trim");
+    return LX_OK;
+}
+
+int lx_pool_stats(int64_t *live_bytes, int64_t *cached_bytes) {
+    pool_stats(live_bytes, cached_bytes);
     return LX_OK;
 }
 

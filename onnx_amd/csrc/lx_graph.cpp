@@ -1,0 +1,1118 @@
+// lx_graph.cpp -- ComputationalGraph.Execute / Node.Execute on the device.
+//
+// Follows src/Lokad.Onnx.Backend/ComputationalGraph.cs:199-272 (input
+// resolution, node loop, stop at the first failure, output assignment) and
+// Node.cs:80-181 (the op switch and its attribute conventions), with every
+// tensor resident in HBM: user inputs are borrowed device tensors, initializers
+// are uploaded once, intermediates live in pooled device blocks that return to
+// the pool right after their last consumer ran, and Reshape / Unsqueeze are
+// views.  The only host round trips are those an op needs by definition: the
+// values of shape / axes tensors that were computed on the device, and the
+// error record of integer Div and checked Cast.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstring>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/lonnx.h"
+#include "lx_graph.h"
+#include "lx_internal.h"
+#include "lx_pool.h"
+
+namespace lx {
+Storage::~Storage() {
+    if (ptr) (void)pool_release(ptr);
+}
+}  // namespace lx
+
+using namespace lx;
+
+namespace {
+
+std::string fmt(const char *f, ...) {
+    char buf[2048];
+    va_list ap;
+    va_start(ap, f);
+    vsnprintf(buf, sizeof buf, f, ap);
+    va_end(ap);
+    return buf;
+}
+
+int fail(int code, const std::string &m) { return api_set_error(code, m); }
+
+std::string lower(std::string s) {
+    for (auto &c : s) c = (char)tolower(c);
+    return s;
+}
+
+// Tensor.PrintShape (Tensor.cs:1724)
+std::string print_shape(const lx_tensor &t) {
+    std::string s = "[";
+    for (int i = 0; i < t.rank; i++) s += (i ? "," : "") + std::to_string(t.dims[i]);
+    return s + "]";
+}
+
+int64_t numel(const lx_tensor &t) {
+    int64_t n = 1;
+    for (int i = 0; i < t.rank; i++) n *= t.dims[i];
+    return n;
+}
+
+// ---- OpResult factories (OpResult.cs:34-60) ---------------------------------
+int missing_input(const char *name) {
+    return fail(LX_ERR_MISSING_INPUT, fmt("The required input parameter %s is missing or null.", name));
+}
+int not_supported(const std::string &op) {
+    return fail(LX_ERR_NOT_SUPPORTED, fmt("The operation %s is not supported by the backend.", op.c_str()));
+}
+int wrong_input_type(const std::string &tname, const char *param, int want, const lx_tensor &t) {
+    return fail(LX_ERR_WRONG_INPUT_TYPE,
+                fmt("The input tensor %s for parameter %s has type %s but is required to be %s. ", tname.c_str(), param,
+                    api_dtype_name(t.dtype), api_dtype_name(want)));
+}
+// .NET ArgumentException(message, paramName).Message
+int argument_error(const std::string &message, const std::string &param) {
+    return fail(LX_ERR_INVALID_ARGUMENT, message + " (Parameter '" + param + "')");
+}
+int failure(const std::string &message) { return fail(LX_ERR_INVALID_ARGUMENT, message); }
+
+// ---- attributes (Node.cs:21-73) ---------------------------------------------
+const Attr *find_attr(const GNode &n, const char *name) {
+    auto it = n.attrs.find(name);
+    return it == n.attrs.end() ? nullptr : &it->second;
+}
+
+// Node.Int: an int attribute, or a long one converted with Convert.ToInt32.
+// Returns 0 = absent, 1 = present, negative = conversion failure (error set).
+int attr_int(const GNode &n, const char *name, int32_t *v) {
+    const Attr *a = find_attr(n, name);
+    if (!a || a->kind != kAttrInt) return 0;
+    if (a->i < INT32_MIN || a->i > INT32_MAX) {
+        failure("Value was either too large or too small for an Int32.");
+        return -1;
+    }
+    *v = (int32_t)a->i;
+    return 1;
+}
+
+// Node.Ints: int[] or long[] (each converted with Convert.ToInt32).
+int attr_ints(const GNode &n, const char *name, std::vector<int64_t> *v) {
+    const Attr *a = find_attr(n, name);
+    if (!a || a->kind != kAttrInts) return 0;
+    for (int64_t x : a->ints)
+        if (x < INT32_MIN || x > INT32_MAX) {
+            failure("Value was either too large or too small for an Int32.");
+            return -1;
+        }
+    *v = a->ints;
+    return 1;
+}
+
+// ---- device values ------------------------------------------------------------
+Value value_from_output(const lx_tensor &y) {
+    Value v;
+    v.t = y;
+    v.t.owns = 0;  // the Storage releases the block
+    v.store = std::make_shared<Storage>();
+    v.store->ptr = y.data;
+    return v;
+}
+
+// a device tensor holding a copy of host data (Constant, Shape outputs)
+int value_from_host(const std::shared_ptr<HostTensor> &h, Value *out) {
+    lx_tensor t;
+    memset(&t, 0, sizeof t);
+    int st = lx_tensor_alloc(h->dtype, h->rank, h->dims, &t);
+    if (st) return st;
+    Value v = value_from_output(t);
+    if (!h->bytes.empty()) {
+        hipError_t e = hipMemcpyAsync(t.data, h->bytes.data(), h->bytes.size(), hipMemcpyHostToDevice, api_stream());
+        if (e == hipSuccess) e = hipStreamSynchronize(api_stream());
+        if (e != hipSuccess) return fail(LX_ERR_HIP, fmt("upload: %s", hipGetErrorString(e)));
+    }
+    v.host = h;
+    *out = v;
+    return LX_OK;
+}
+
+// Integer values of a small tensor (shape / axes): the host copy if there is
+// one, else one download (which synchronises the stream).
+int host_ints(Value &v, std::vector<int64_t> *out) {
+    const int64_t n = numel(v.t);
+    if (!v.host) {
+        auto h = std::make_shared<HostTensor>();
+        h->dtype = v.t.dtype;
+        h->rank = v.t.rank;
+        for (int i = 0; i < v.t.rank; i++) h->dims[i] = v.t.dims[i];
+        h->bytes.resize((size_t)(n * api_esize(v.t.dtype)));
+        int st = lx_tensor_download(&v.t, h->bytes.data(), (int64_t)h->bytes.size());
+        if (st) return st;
+        v.host = h;
+    }
+    out->resize((size_t)n);
+    const uint8_t *b = v.host->bytes.data();
+    for (int64_t i = 0; i < n; i++) {
+        switch (v.t.dtype) {
+        case LX_INT64: { int64_t x; memcpy(&x, b + 8 * i, 8); (*out)[i] = x; break; }
+        case LX_INT32: { int32_t x; memcpy(&x, b + 4 * i, 4); (*out)[i] = x; break; }
+        default: return failure("shape and axes tensors must hold Int32 or Int64 values");
+        }
+    }
+    return LX_OK;
+}
+
+// ---- execution context ------------------------------------------------------
+struct Exec {
+    lx_graph *g;
+    bool is_node_output(const std::string &name) const {
+        return std::find(g->node_outputs.begin(), g->node_outputs.end(), name) != g->node_outputs.end();
+    }
+    // ComputationalGraph.GetInputTensor (ComputationalGraph.cs:39-41): Inputs, then
+    // Initializers, then IntermediateOutputs.
+    int lookup(const std::string &name, Value **out) {
+        auto it = g->input_vals.find(name);
+        if (it != g->input_vals.end()) { *out = &it->second; return LX_OK; }
+        auto ii = g->init_dev.find(name);
+        if (ii != g->init_dev.end()) { *out = &ii->second; return LX_OK; }
+        auto vi = g->values.find(name);
+        if (vi != g->values.end()) { *out = &vi->second; return LX_OK; }
+        if (is_node_output(name))
+            return failure(fmt("The intermediate output tensor %s has not been assigned a value.", name.c_str()));
+        return failure(fmt("The given key '%s' was not present in the dictionary.", name.c_str()));
+    }
+    // Node.InputTensor (Node.cs:75): null past the node's input list
+    int input(const GNode &n, size_t k, Value **out) {
+        *out = nullptr;
+        if (k >= n.in.size()) return LX_OK;
+        return lookup(n.in[k], out);
+    }
+};
+
+// a freshly allocated output from an lx_* operator call
+template <typename F>
+int run_op(F call, std::vector<Value> &outs) {
+    lx_tensor y;
+    memset(&y, 0, sizeof y);
+    int st = call(&y);
+    if (st) {
+        lx_tensor_free(&y);
+        return st;
+    }
+    outs.push_back(value_from_output(y));
+    return LX_OK;
+}
+
+const lx_tensor *T(Value *v) { return v ? &v->t : nullptr; }
+
+// Tensor<T>.Reshape (TensorOps.cs:1256-1310), allowZero = false
+int reshape_dims(const lx_tensor &x, const std::vector<int64_t> &shape, int rank_of_shape, std::vector<int64_t> *nd) {
+    if (rank_of_shape != 1) return argument_error("shape", "Shape tensors must be of rank 1.");
+    for (int64_t v : shape)
+        if (v < -1) return argument_error("shape", fmt("A shape dimension cannot be < -1, got %lld.", (long long)v));
+    if (std::count(shape.begin(), shape.end(), (int64_t)-1) > 1)
+        return argument_error("shape", "At most 1 shape dimension can be -1.");
+    int unknown = -1;
+    int64_t new_size = 1;
+    nd->clear();
+    for (size_t i = 0; i < shape.size(); i++) {
+        if (shape[i] == -1) {
+            unknown = (int)i;
+            nd->push_back(-1);
+        } else if (shape[i] == 0) {
+            if ((int)i >= x.rank) return failure("Index was outside the bounds of the array.");
+            nd->push_back(x.dims[i]);
+            new_size *= x.dims[i];
+        } else {
+            if (shape[i] > INT32_MAX) return failure("Value was either too large or too small for an Int32.");
+            nd->push_back(shape[i]);
+            new_size *= shape[i];
+        }
+    }
+    const int64_t len = numel(x);
+    if (unknown != -1) {
+        if (new_size == 0) return failure("Attempted to divide by zero.");
+        (*nd)[unknown] = len / new_size;
+        new_size *= (*nd)[unknown];
+    }
+    if (new_size != len) {
+        // List<int>.Print() as ArrayTensorExtensions.cs:118 writes it (each entry is the list's type name)
+        std::string p = "[";
+        for (size_t i = 0; i < nd->size(); i++) p += (i ? ", " : "") + std::string("System.Collections.Generic.List`1[System.Int32]");
+        p += "]";
+        return argument_error("shape", "The input tensor cannot be reshaped to the requested shape. Input shape:" +
+                                           print_shape(x) + ", requested shape:" + p);
+    }
+    if ((int)nd->size() > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
+    return LX_OK;
+}
+
+Value alias(const Value &x, const std::vector<int64_t> &dims) {
+    Value v = x;
+    v.t.rank = (int32_t)dims.size();
+    for (int i = 0; i < LX_MAX_RANK; i++) v.t.dims[i] = i < (int)dims.size() ? dims[i] : 0;
+    v.t.owns = 0;
+    v.host.reset();
+    if (x.host) {  // same bytes, new dims
+        auto h = std::make_shared<HostTensor>(*x.host);
+        h->rank = v.t.rank;
+        for (int i = 0; i < LX_MAX_RANK; i++) h->dims[i] = v.t.dims[i];
+        v.host = h;
+    }
+    return v;
+}
+
+bool reshapable_dtype(int dt) {
+    switch (dt) {
+    case LX_BOOL: case LX_INT8: case LX_UINT8: case LX_INT16: case LX_UINT16: case LX_INT32: case LX_UINT32:
+    case LX_INT64: case LX_UINT64: case LX_FLOAT: case LX_DOUBLE: return true;
+    default: return false;
+    }
+}
+
+// ITensor.Unsqueeze (ITensor.cs:185-208)
+int unsqueeze_dims(const lx_tensor &x, std::vector<int64_t> axes, std::vector<int64_t> *nd) {
+    std::set<int64_t> uniq(axes.begin(), axes.end());
+    if (uniq.size() != axes.size()) return argument_error("axes", "axes contains a repeated dimension.");
+    const int64_t rank = x.rank, k = (int64_t)axes.size();
+    for (auto &a : axes) a = a >= 0 ? a : rank + a;
+    for (int64_t a : axes)
+        if (a > rank + k - 1) {
+            int64_t first = 0;
+            for (int64_t b : axes)
+                if (b > rank - 1) { first = b; break; }
+            return argument_error("axes", fmt("Each specified axis must be less than the rank of the output tensor. Got %lld",
+                                              (long long)first));
+        }
+    std::vector<int64_t> ns((size_t)(rank + k), 0);
+    for (int64_t a : axes) {
+        if (a < 0) return failure("Index was outside the bounds of the array.");
+        ns[(size_t)a] = 1;
+    }
+    int e = 0;
+    for (auto &d : ns)
+        if (d == 0) {
+            if (e >= rank) return failure("Out of dimensions.");
+            d = x.dims[e++];
+        }
+    if ((int)ns.size() > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
+    *nd = ns;
+    return LX_OK;
+}
+
+// axes tensor of ReduceMean / ReduceMax / ReduceSum: rank check (ReduceMean, ReduceMax),
+// Int64 -> Int32 (checked), any other type fails the (Tensor<int>) cast
+int reduce_axes(Value *a, bool check_rank, const char *op, const std::string &aname, std::vector<int64_t> *axes,
+                int *n_axes) {
+    if (!a) {
+        *n_axes = -1;
+        return LX_OK;
+    }
+    if (check_rank && a->t.rank != 1)
+        return fail(LX_ERR_WRONG_INPUT_SHAPE,
+                    fmt("The input tensor %s for parameter axes has shape %s but is required to have rank 1.",
+                        aname.c_str(), print_shape(a->t).c_str()));
+    if (a->t.dtype != LX_INT64 && a->t.dtype != LX_INT32)
+        return failure(fmt("Unable to cast object of type 'DenseTensor`1[%s]' to type 'Tensor`1[System.Int32]'.",
+                           api_dtype_name(a->t.dtype)));
+    int st = host_ints(*a, axes);
+    if (st) return st;
+    for (int64_t v : *axes)
+        if (v < INT32_MIN || v > INT32_MAX) return fail(LX_ERR_OVERFLOW, "Value was either too large or too small for an Int32.");
+    *n_axes = (int)axes->size();
+    (void)op;
+    return LX_OK;
+}
+
+int run_node(Exec &X, const GNode &n, std::vector<Value> &outs);
+
+// the original nodes of a fused subgraph, executed one by one
+int run_unfused(Exec &X, const GNode &n, std::vector<Value> &outs) {
+    std::vector<std::string> made;
+    int st = LX_OK;
+    for (const GNode &m : n.fused_from) {
+        std::vector<Value> o;
+        if ((st = run_node(X, m, o))) break;
+        for (size_t i = 0; i < m.out.size() && i < o.size(); i++) {
+            X.g->values[m.out[i]] = o[i];
+            made.push_back(m.out[i]);
+        }
+    }
+    if (!st) {
+        for (const std::string &o : n.out) {
+            auto it = X.g->values.find(o);
+            if (it == X.g->values.end()) { st = failure("fused subgraph produced no " + o); break; }
+            outs.push_back(it->second);
+        }
+    }
+    for (const std::string &m : made)  // intermediates of the subgraph
+        if (std::find(n.out.begin(), n.out.end(), m) == n.out.end()) X.g->values.erase(m);
+    return st;
+}
+
+// Node.ExecuteCPU (Node.cs:121-181) with the device operators.
+int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
+    const std::string &op = n.op;
+    Value *a = nullptr, *b = nullptr, *c = nullptr;
+    int st;
+    auto in2 = [&]() -> int {
+        int s = X.input(n, 0, &a);
+        if (!s) s = X.input(n, 1, &b);
+        return s;
+    };
+    if (op == "Add" || op == "Sub" || op == "Mul" || op == "Div" || op == "Pow") {
+        if ((st = in2())) return st;
+        auto f = op == "Add" ? lx_Add : op == "Sub" ? lx_Sub : op == "Mul" ? lx_Mul : op == "Div" ? lx_Div : lx_Pow;
+        return run_op([&](lx_tensor *y) { return f(T(a), T(b), y); }, outs);
+    }
+    if (op == "Sqrt" || op == "Erf") {
+        if ((st = X.input(n, 0, &a))) return st;
+        auto f = op == "Sqrt" ? lx_Sqrt : lx_Erf;
+        return run_op([&](lx_tensor *y) { return f(T(a), y); }, outs);
+    }
+    if (op == "Cast") {
+        if ((st = X.input(n, 0, &a))) return st;
+        int32_t to;
+        int r = attr_int(n, "to", &to);
+        if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        if (r == 0) return failure("The Int attribute to is required but was not found.");
+        return run_op([&](lx_tensor *y) { return lx_Cast(T(a), to, y); }, outs);
+    }
+    if (op == "Softmax") {
+        if ((st = X.input(n, 0, &a))) return st;
+        int32_t axis = -1;
+        int r = attr_int(n, "axis", &axis);
+        if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        return run_op([&](lx_tensor *y) { return lx_Softmax(T(a), axis, r, y); }, outs);
+    }
+    if (X.g->opset < 0 && (op == "ReduceMean" || op == "Unsqueeze"))  // graph.OpsetVersion() (ComputationalGraph.cs:37)
+        return failure("The domain  does not ezist in the imported opsets.");
+    if (op == "ReduceSum" || op == "ReduceMean" || op == "ReduceMax") {
+        if ((st = X.input(n, 0, &a))) return st;
+        std::vector<int64_t> axes;
+        int n_axes = -1;
+        const bool attr_axes = op == "ReduceMean" && X.g->opset < 13;
+        if (attr_axes) {
+            // RequiredInts("axes")?.ToTensor<int>()  (Node.cs:168-176)
+            int r = attr_ints(n, "axes", &axes);
+            if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+            if (r == 0) return failure("The Ints attribute axes is required but was not found.");
+            n_axes = (int)axes.size();
+        } else {
+            if ((st = X.input(n, 1, &b))) return st;
+            if (!a) return missing_input("data");
+            const std::string bname = n.in.size() > 1 ? n.in[1] : "";
+            if ((st = reduce_axes(b, op != "ReduceSum", op.c_str(), bname, &axes, &n_axes))) return st;
+        }
+        int32_t keep = -1, noop = -1, v;
+        int r = attr_int(n, "keepdims", &v);
+        if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        if (r) keep = v != 0;
+        if (op != "ReduceMax") {
+            r = attr_int(n, "noop_with_empty_axes", &v);
+            if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+            if (r) noop = v != 0;
+        }
+        const int64_t *ap = axes.empty() ? nullptr : axes.data();
+        if (op == "ReduceSum") return run_op([&](lx_tensor *y) { return lx_ReduceSum(T(a), ap, n_axes, keep, noop, y); }, outs);
+        if (op == "ReduceMean") return run_op([&](lx_tensor *y) { return lx_ReduceMean(T(a), ap, n_axes, keep, noop, y); }, outs);
+        return run_op([&](lx_tensor *y) { return lx_ReduceMax(T(a), ap, n_axes, keep, y); }, outs);
+    }
+    if (op == "Reshape") {
+        // CPUExecutionProvider.Reshape (CPUExecutionProvider.cs:56-80); allow_zero is read as
+        // Attr<bool?> and an AttributeProto int never is a bool, so it is always false
+        if ((st = in2())) return st;
+        if (!a) return missing_input("input");
+        if (!b) return missing_input("shape");
+        if (b->t.dtype != LX_INT64) return wrong_input_type(n.in[1], "shape", LX_INT64, b->t);
+        if (!reshapable_dtype(a->t.dtype)) return not_supported(op);
+        std::vector<int64_t> shape, nd;
+        if ((st = host_ints(*b, &shape))) return st;
+        if ((st = reshape_dims(a->t, shape, b->t.rank, &nd))) return st;
+        outs.push_back(alias(*a, nd));
+        return LX_OK;
+    }
+    if (op == "Unsqueeze") {
+        // CPUExecutionProvider.Unsqueeze (CPUExecutionProvider.cs:602-621): axes from input 1
+        // from opset 13, from the attribute before
+        if ((st = X.input(n, 0, &a))) return st;
+        std::vector<int64_t> axes;
+        if (X.g->opset >= 13) {
+            if ((st = X.input(n, 1, &b))) return st;
+            if (!a) return missing_input("data");
+            if (!b) return missing_input("axes");
+            if ((st = host_ints(*b, &axes))) return st;
+        } else {
+            int r = attr_ints(n, "axes", &axes);
+            if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+            if (r == 0) return failure("The Ints attribute axes is required but was not found.");
+            if (!a) return missing_input("data");
+        }
+        std::vector<int64_t> nd;
+        if ((st = unsqueeze_dims(a->t, axes, &nd))) return st;
+        outs.push_back(alias(*a, nd));
+        return LX_OK;
+    }
+    if (op == "Constant") {
+        // CPUExecutionProvider.Constant (CPUExecutionProvider.cs:435-449) on
+        // Node.OneOfAttr(...) (Node.cs:30-36, 152)
+        static const char *names[] = {"sparse_value", "value", "value_float", "value_floats",
+                                      "value_int", "value_ints", "value_string", "value_strings"};
+        const Attr *v = nullptr;
+        for (const char *nm : names)
+            if ((v = find_attr(n, nm))) break;
+        if (!v) return fail(LX_ERR_MISSING_INPUT, "The required attribute value is missing or null. ");
+        auto h = std::make_shared<HostTensor>();
+        if (v->kind == kAttrTensor && v->t) {
+            *h = *v->t;
+        } else if (v->kind == kAttrFloat) {
+            h->dtype = LX_FLOAT;
+            h->rank = 0;
+            h->bytes.resize(4);
+            memcpy(h->bytes.data(), &v->f, 4);
+        } else if (v->kind == kAttrFloats) {
+            h->dtype = LX_FLOAT;
+            h->rank = 1;
+            h->dims[0] = (int64_t)v->floats.size();
+            h->bytes.resize(4 * v->floats.size());
+            if (!v->floats.empty()) memcpy(h->bytes.data(), v->floats.data(), h->bytes.size());
+        } else {
+            return not_supported(op);  // long / long[] / string values match no case of the switch
+        }
+        Value out;
+        if ((st = value_from_host(h, &out))) return st;
+        outs.push_back(out);
+        return LX_OK;
+    }
+    if (op == "Shape") {
+        // CPUExecutionProvider.Shape (CPUExecutionProvider.cs:503-514)
+        if ((st = X.input(n, 0, &a))) return st;
+        if (!a) return missing_input("data");
+        int32_t s0 = 0, e0 = a->t.rank;
+        int r1 = attr_int(n, "start", &s0), r2 = attr_int(n, "end", &e0);
+        if (r1 < 0 || r2 < 0) return LX_ERR_INVALID_ARGUMENT;
+        const int rank = a->t.rank;
+        int s = s0 >= 0 ? s0 : rank + s0, e = e0 >= 0 ? e0 : rank + e0;
+        s = std::min(std::max(s, 0), rank);
+        e = std::min(std::max(e, 0), rank);
+        if (s > e) return failure("Specified argument was out of the range of valid values. (Parameter 'length')");
+        auto h = std::make_shared<HostTensor>();
+        h->dtype = LX_INT64;
+        h->rank = 1;
+        h->dims[0] = e - s;
+        h->bytes.resize(8 * (size_t)(e - s));
+        for (int i = s; i < e; i++) memcpy(h->bytes.data() + 8 * (i - s), &a->t.dims[i], 8);
+        Value out;
+        if ((st = value_from_host(h, &out))) return st;
+        outs.push_back(out);
+        return LX_OK;
+    }
+    // ---- fused subgraphs (lx_graph_fuse) ----
+    if (op == "GeluErf") {
+        if ((st = X.input(n, 0, &a))) return st;
+        if (!a || a->t.dtype != LX_FLOAT) return run_unfused(X, n, outs);
+        return run_op([&](lx_tensor *y) { return lx_GeluErf(T(a), y); }, outs);
+    }
+    if (op == "LayerNormDecomposed") {
+        if ((st = X.input(n, 0, &a)) || (st = X.input(n, 1, &b)) || (st = X.input(n, 2, &c))) return st;
+        if (!a || !b || !c || a->t.dtype != LX_FLOAT || b->t.dtype != LX_FLOAT || c->t.dtype != LX_FLOAT ||
+            a->t.rank < 1)
+            return run_unfused(X, n, outs);
+        const Attr *eps = find_attr(n, "epsilon");
+        const float e = eps ? eps->f : 1e-12f;
+        return run_op([&](lx_tensor *y) { return lx_LayerNormDecomposed(T(a), T(b), T(c), e, y); }, outs);
+    }
+    if (op == "AddSoftmax") {
+        if ((st = in2())) return st;
+        if (!a || !b || a->t.dtype != LX_FLOAT || b->t.dtype != LX_FLOAT) return run_unfused(X, n, outs);
+        int32_t axis = -1;
+        if (attr_int(n, "axis", &axis) < 0) return LX_ERR_INVALID_ARGUMENT;
+        // the larger operand is S; Add is commutative bit for bit
+        Value *s = a, *m = b;
+        if (numel(a->t) < numel(b->t) || (numel(a->t) == numel(b->t) && a->t.rank < b->t.rank)) std::swap(s, m);
+        lx_bcast_plan p;
+        if (lx_plan_broadcast(s->t.rank, s->t.dims, m->t.rank, m->t.dims, &p) != LX_OK) return run_unfused(X, n, outs);
+        bool same = p.out_rank == s->t.rank;
+        for (int i = 0; same && i < p.out_rank; i++) same = p.out_dims[i] == s->t.dims[i];
+        if (!same) return run_unfused(X, n, outs);
+        return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
+    }
+    return not_supported(op);
+}
+
+// ---- fusion -----------------------------------------------------------------
+struct Fuser {
+    lx_graph *g;
+    std::map<std::string, std::vector<int>> consumers;
+    std::set<std::string> graph_outputs, graph_inputs;
+    std::map<std::string, std::shared_ptr<HostTensor>> consts;
+    std::vector<bool> used;
+
+    void index() {
+        consumers.clear();
+        for (int i = 0; i < (int)g->nodes.size(); i++)
+            for (const auto &nm : g->nodes[i].in) consumers[nm].push_back(i);
+        graph_outputs = std::set<std::string>(g->outputs.begin(), g->outputs.end());
+        graph_inputs.clear();
+        for (auto &in : g->inputs) graph_inputs.insert(in.name);
+        consts.clear();
+        // initializers a caller cannot replace, and Constant nodes with a tensor / float value
+        for (auto &kv : g->initializers)
+            if (!graph_inputs.count(kv.first)) consts[kv.first] = kv.second;
+        for (auto &n : g->nodes) {
+            if (n.op != "Constant" || n.out.empty()) continue;
+            auto it = n.attrs.find("value");
+            if (it != n.attrs.end() && it->second.kind == kAttrTensor && it->second.t && n.attrs.size() == 1)
+                consts[n.out[0]] = it->second.t;
+            it = n.attrs.find("value_float");
+            if (it != n.attrs.end() && it->second.kind == kAttrFloat && n.attrs.size() == 1) {
+                auto h = std::make_shared<HostTensor>();
+                h->dtype = LX_FLOAT;
+                h->bytes.resize(4);
+                memcpy(h->bytes.data(), &it->second.f, 4);
+                consts[n.out[0]] = h;
+            }
+        }
+        used.assign(g->nodes.size(), false);
+    }
+    // the float32 scalar value of a constant (numel 1, rank <= 1)
+    bool scalar_f32(const std::string &name, float *v) const {
+        auto it = consts.find(name);
+        if (it == consts.end()) return false;
+        const HostTensor &h = *it->second;
+        if (h.dtype != LX_FLOAT || h.numel() != 1 || h.rank > 1 || h.bytes.size() != 4) return false;
+        memcpy(v, h.bytes.data(), 4);
+        return true;
+    }
+    bool scalar_bits(const std::string &name, uint32_t bits) const {
+        float v;
+        if (!scalar_f32(name, &v)) return false;
+        uint32_t u;
+        memcpy(&u, &v, 4);
+        return u == bits;
+    }
+    bool int_axes_last(const std::string &name) const {  // a constant [-1]
+        auto it = consts.find(name);
+        if (it == consts.end()) return false;
+        const HostTensor &h = *it->second;
+        if (h.numel() != 1 || h.rank != 1) return false;
+        if (h.dtype == LX_INT64 && h.bytes.size() == 8) { int64_t x; memcpy(&x, h.bytes.data(), 8); return x == -1; }
+        if (h.dtype == LX_INT32 && h.bytes.size() == 4) { int32_t x; memcpy(&x, h.bytes.data(), 4); return x == -1; }
+        return false;
+    }
+    // the single consumer of `name` (or -1), provided `name` is no graph output
+    int only_consumer(const std::string &name) const {
+        if (graph_outputs.count(name)) return -1;
+        auto it = consumers.find(name);
+        if (it == consumers.end() || it->second.size() != 1) return -1;
+        return it->second[0];
+    }
+    const GNode &N(int i) const { return g->nodes[i]; }
+    bool is(int i, const char *op, size_t nin) const {
+        return i >= 0 && !used[i] && N(i).op == op && N(i).in.size() == nin && N(i).out.size() == 1;
+    }
+    // the other input of a two-input node, given one
+    bool other(int i, const std::string &one, std::string *o) const {
+        const GNode &n = N(i);
+        if (n.in[0] == one && n.in[1] != one) { *o = n.in[1]; return true; }
+        if (n.in[1] == one && n.in[0] != one) { *o = n.in[0]; return true; }
+        return false;
+    }
+    // ReduceMean over the last axis with keepdims 1
+    bool mean_last(int i) const {
+        const GNode &n = N(i);
+        auto kd = n.attrs.find("keepdims");
+        if (kd != n.attrs.end() && !(kd->second.kind == kAttrInt && kd->second.i == 1)) return false;
+        if (n.attrs.count("noop_with_empty_axes")) return false;
+        if (g->opset < 13) {
+            auto ax = n.attrs.find("axes");
+            return n.in.size() == 1 && ax != n.attrs.end() && ax->second.kind == kAttrInts && ax->second.ints.size() == 1 &&
+                   ax->second.ints[0] == -1;
+        }
+        return n.in.size() == 2 && int_axes_last(n.in[1]);
+    }
+
+    // Div(x, sqrt2) -> Erf -> Add 1 -> Mul x -> Mul 0.5
+    bool gelu(int i0, GNode *f, std::vector<int> *nodes) {
+        if (!is(i0, "Div", 2) || !scalar_bits(N(i0).in[1], 0x3fb504f3u)) return false;
+        const std::string x = N(i0).in[0];
+        int i1 = only_consumer(N(i0).out[0]);
+        if (!is(i1, "Erf", 1)) return false;
+        int i2 = only_consumer(N(i1).out[0]);
+        std::string o;
+        if (!is(i2, "Add", 2) || !other(i2, N(i1).out[0], &o) || !scalar_bits(o, 0x3f800000u)) return false;
+        int i3 = only_consumer(N(i2).out[0]);
+        if (!is(i3, "Mul", 2) || !other(i3, N(i2).out[0], &o) || o != x) return false;
+        int i4 = only_consumer(N(i3).out[0]);
+        if (!is(i4, "Mul", 2) || !other(i4, N(i3).out[0], &o) || !scalar_bits(o, 0x3f000000u)) return false;
+        *nodes = {i0, i1, i2, i3, i4};
+        f->op = "GeluErf";
+        f->in = {x};
+        f->out = N(i4).out;
+        return true;
+    }
+
+    // ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul gamma -> Add beta
+    bool layernorm(int i0, GNode *f, std::vector<int> *nodes) {
+        if (!is(i0, "ReduceMean", N(i0).in.size()) || !mean_last(i0)) return false;
+        const std::string x = N(i0).in[0], mean = N(i0).out[0];
+        int i1 = only_consumer(mean);
+        if (!is(i1, "Sub", 2) || N(i1).in[0] != x || N(i1).in[1] != mean) return false;
+        const std::string d = N(i1).out[0];
+        if (graph_outputs.count(d)) return false;
+        auto cd = consumers.find(d);
+        if (cd == consumers.end() || cd->second.size() != 2) return false;
+        int ipow = -1, idiv = -1;
+        for (int k : cd->second) {
+            if (is(k, "Pow", 2) && N(k).in[0] == d) ipow = k;
+            else if (is(k, "Div", 2) && N(k).in[0] == d) idiv = k;
+        }
+        if (ipow < 0 || idiv < 0 || !scalar_bits(N(ipow).in[1], 0x40000000u)) return false;
+        int i3 = only_consumer(N(ipow).out[0]);
+        if (!is(i3, "ReduceMean", N(i3 >= 0 ? i3 : 0).in.size()) || !mean_last(i3) || N(i3).in[0] != N(ipow).out[0])
+            return false;
+        int i4 = only_consumer(N(i3).out[0]);
+        std::string o;
+        float eps;
+        if (!is(i4, "Add", 2) || !other(i4, N(i3).out[0], &o) || !scalar_f32(o, &eps)) return false;
+        int i5 = only_consumer(N(i4).out[0]);
+        if (!is(i5, "Sqrt", 1)) return false;
+        if (only_consumer(N(i5).out[0]) != idiv || N(idiv).in[1] != N(i5).out[0]) return false;
+        int i7 = only_consumer(N(idiv).out[0]);
+        std::string gamma, beta;
+        if (!is(i7, "Mul", 2) || !other(i7, N(idiv).out[0], &gamma)) return false;
+        int i8 = only_consumer(N(i7).out[0]);
+        if (!is(i8, "Add", 2) || !other(i8, N(i7).out[0], &beta)) return false;
+        *nodes = {i0, i1, ipow, i3, i4, i5, idiv, i7, i8};
+        f->op = "LayerNormDecomposed";
+        f->in = {x, gamma, beta};
+        f->out = N(i8).out;
+        Attr a;
+        a.kind = kAttrFloat;
+        a.f = eps;
+        f->attrs["epsilon"] = a;
+        return true;
+    }
+
+    // Add(S, mask) -> Softmax
+    bool add_softmax(int i0, GNode *f, std::vector<int> *nodes) {
+        if (!is(i0, "Add", 2)) return false;
+        int i1 = only_consumer(N(i0).out[0]);
+        if (!is(i1, "Softmax", 1)) return false;
+        *nodes = {i0, i1};
+        f->op = "AddSoftmax";
+        f->in = N(i0).in;
+        f->out = N(i1).out;
+        auto ax = N(i1).attrs.find("axis");
+        if (ax != N(i1).attrs.end()) f->attrs["axis"] = ax->second;
+        return true;
+    }
+
+    int run() {
+        index();
+        int fused = 0;
+        std::vector<std::pair<int, GNode>> placed;  // fused node at the index of its last original
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            if (used[i]) continue;
+            GNode f;
+            std::vector<int> nodes;
+            if (layernorm(i, &f, &nodes) || gelu(i, &f, &nodes) || add_softmax(i, &f, &nodes)) {
+                std::sort(nodes.begin(), nodes.end());
+                for (int k : nodes) {
+                    used[k] = true;
+                    f.fused_from.push_back(N(k));
+                }
+                f.name = N(nodes.back()).name;
+                placed.push_back({nodes.back(), f});
+                fused++;
+            }
+        }
+        if (!fused) return 0;
+        std::vector<GNode> out;
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            for (auto &p : placed)
+                if (p.first == i) out.push_back(p.second);
+            if (!used[i]) out.push_back(g->nodes[i]);
+        }
+        g->nodes.swap(out);
+        return fused;
+    }
+};
+
+int upload_initializers(lx_graph *g) {
+    for (auto &kv : g->initializers) {
+        if (g->init_dev.count(kv.first)) continue;
+        Value v;
+        int st = value_from_host(kv.second, &v);
+        if (st) return st;
+        g->init_dev[kv.first] = v;
+    }
+    return LX_OK;
+}
+
+bool same_dims(const lx_tensor &t, const GInput &in) {
+    if (t.rank != in.rank) return false;
+    for (int i = 0; i < t.rank; i++)
+        if (t.dims[i] != in.dims[i]) return false;
+    return true;
+}
+
+// ComputationalGraph.GetRequiredInputs (ComputationalGraph.cs:43-71): graph inputs not
+// served by an initializer of the same dims and element type
+std::vector<const GInput *> required_inputs(lx_graph *g, bool use_init) {
+    std::vector<const GInput *> req;
+    for (auto &in : g->inputs) {
+        if (use_init) {
+            auto it = g->init_dev.find(in.name);
+            if (it != g->init_dev.end() && it->second.t.dtype == in.dtype && same_dims(it->second.t, in)) continue;
+        }
+        req.push_back(&in);
+    }
+    return req;
+}
+
+Value borrowed(const lx_tensor &t) {
+    Value v;
+    v.t = t;
+    v.t.owns = 0;
+    return v;
+}
+
+std::string desc(const std::string &name, const lx_tensor &t) {
+    std::string s = name + ":" + lower(api_dtype_name(t.dtype)) + ":";
+    for (int i = 0; i < t.rank; i++) s += (i ? "x" : "") + std::to_string(t.dims[i]);
+    return s;
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+int lx_graph_create(int64_t opset, lx_graph **out) {
+    if (!out) return failure("out is null");
+    *out = new lx_graph();
+    (*out)->opset = opset;
+    return LX_OK;
+}
+
+int lx_graph_free(lx_graph *g) {
+    if (!g) return LX_OK;
+    if (api_initialized()) (void)hipStreamSynchronize(api_stream());
+    delete g;
+    return LX_OK;
+}
+
+int lx_graph_add_input(lx_graph *g, const char *name, int32_t dtype, int32_t rank, const int64_t *dims) {
+    if (!g || !name) return failure("null argument");
+    if (rank < 0 || rank > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
+    GInput in;
+    in.name = name;
+    in.dtype = dtype;
+    in.rank = rank;
+    for (int i = 0; i < rank; i++) in.dims[i] = dims && dims[i] > 0 ? dims[i] : 0;
+    g->inputs.push_back(in);
+    return LX_OK;
+}
+
+int lx_graph_add_output(lx_graph *g, const char *name) {
+    if (!g || !name) return failure("null argument");
+    g->outputs.push_back(name);
+    return LX_OK;
+}
+
+int lx_graph_add_initializer(lx_graph *g, const char *name, int32_t dtype, int32_t rank, const int64_t *dims,
+                             const void *host, int64_t nbytes) {
+    if (!g || !name) return failure("null argument");
+    if (rank < 0 || rank > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
+    auto h = std::make_shared<HostTensor>();
+    h->dtype = dtype;
+    h->rank = rank;
+    for (int i = 0; i < rank; i++) h->dims[i] = dims[i];
+    const int64_t want = h->numel() * api_esize(dtype);
+    if (!api_esize(dtype)) return fail(LX_ERR_NOT_SUPPORTED, fmt("Element type %s is not supported.", api_dtype_name(dtype)));
+    if (nbytes != want || (want > 0 && !host))
+        return failure(fmt("Initializer %s holds %lld bytes, its shape needs %lld.", name, (long long)nbytes, (long long)want));
+    h->bytes.assign((const uint8_t *)host, (const uint8_t *)host + nbytes);
+    for (auto &kv : g->initializers)
+        if (kv.first == name) return failure(fmt("An item with the same key has already been added. Key: %s", name));
+    g->initializers.push_back({name, h});
+    g->init_dev.erase(name);
+    return LX_OK;
+}
+
+int lx_graph_add_node(lx_graph *g, const char *name, const char *op_type, int32_t n_in, const char *const *inputs,
+                      int32_t n_out, const char *const *outputs, int32_t *index) {
+    if (!g || !op_type || n_in < 0 || n_out < 0) return failure("null argument");
+    GNode n;
+    n.name = name ? name : "";
+    n.op = op_type;
+    for (int i = 0; i < n_in; i++) n.in.push_back(inputs[i] ? inputs[i] : "");
+    for (int i = 0; i < n_out; i++) {
+        n.out.push_back(outputs[i] ? outputs[i] : "");
+        g->node_outputs.push_back(n.out.back());
+    }
+    g->nodes.push_back(n);
+    if (index) *index = (int32_t)g->nodes.size() - 1;
+    return LX_OK;
+}
+
+static int node_at(lx_graph *g, int32_t node, const char *attr, GNode **n) {
+    if (!g || !attr || node < 0 || node >= (int32_t)g->nodes.size()) return failure("invalid node index or attribute name");
+    *n = &g->nodes[node];
+    return LX_OK;
+}
+
+int lx_graph_set_attr_int(lx_graph *g, int32_t node, const char *attr, int64_t v) {
+    GNode *n;
+    int st = node_at(g, node, attr, &n);
+    if (st) return st;
+    Attr a;
+    a.kind = kAttrInt;
+    a.i = v;
+    n->attrs[attr] = a;
+    return LX_OK;
+}
+
+int lx_graph_set_attr_ints(lx_graph *g, int32_t node, const char *attr, const int64_t *v, int32_t cnt) {
+    GNode *n;
+    int st = node_at(g, node, attr, &n);
+    if (st) return st;
+    Attr a;
+    a.kind = kAttrInts;
+    a.ints.assign(v, v + (cnt > 0 ? cnt : 0));
+    n->attrs[attr] = a;
+    return LX_OK;
+}
+
+int lx_graph_set_attr_float(lx_graph *g, int32_t node, const char *attr, float v) {
+    GNode *n;
+    int st = node_at(g, node, attr, &n);
+    if (st) return st;
+    Attr a;
+    a.kind = kAttrFloat;
+    a.f = v;
+    n->attrs[attr] = a;
+    return LX_OK;
+}
+
+int lx_graph_set_attr_floats(lx_graph *g, int32_t node, const char *attr, const float *v, int32_t cnt) {
+    GNode *n;
+    int st = node_at(g, node, attr, &n);
+    if (st) return st;
+    Attr a;
+    a.kind = kAttrFloats;
+    a.floats.assign(v, v + (cnt > 0 ? cnt : 0));
+    n->attrs[attr] = a;
+    return LX_OK;
+}
+
+int lx_graph_set_attr_string(lx_graph *g, int32_t node, const char *attr, const char *v) {
+    GNode *n;
+    int st = node_at(g, node, attr, &n);
+    if (st) return st;
+    Attr a;
+    a.kind = kAttrString;
+    a.s = v ? v : "";
+    n->attrs[attr] = a;
+    return LX_OK;
+}
+
+int lx_graph_set_attr_tensor(lx_graph *g, int32_t node, const char *attr, int32_t dtype, int32_t rank,
+                             const int64_t *dims, const void *host, int64_t nbytes) {
+    GNode *n;
+    int st = node_at(g, node, attr, &n);
+    if (st) return st;
+    if (rank < 0 || rank > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
+    auto h = std::make_shared<HostTensor>();
+    h->dtype = dtype;
+    h->rank = rank;
+    for (int i = 0; i < rank; i++) h->dims[i] = dims[i];
+    if (!api_esize(dtype)) return fail(LX_ERR_NOT_SUPPORTED, fmt("Element type %s is not supported.", api_dtype_name(dtype)));
+    if (nbytes != h->numel() * api_esize(dtype) || (nbytes > 0 && !host))
+        return failure("attribute tensor bytes do not match its shape");
+    h->bytes.assign((const uint8_t *)host, (const uint8_t *)host + nbytes);
+    Attr a;
+    a.kind = kAttrTensor;
+    a.t = h;
+    n->attrs[attr] = a;
+    return LX_OK;
+}
+
+int lx_graph_fuse(lx_graph *g, int32_t *n_fused) {
+    if (!g) return failure("null graph");
+    Fuser f;
+    f.g = g;
+    int k = f.run();
+    if (n_fused) *n_fused = k;
+    return LX_OK;
+}
+
+int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs,
+                     int32_t use_initializers) {
+    if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
+    if (!g || n < 0 || (n > 0 && !inputs)) return failure("null argument");
+    int st = upload_initializers(g);
+    if (st) return st;
+    g->values.clear();
+    g->input_vals.clear();
+    // ResolveInputs (ComputationalGraph.cs:73-130)
+    auto req = required_inputs(g, use_initializers != 0);
+    if ((size_t)n != req.size())
+        return failure(fmt("%d user input(s) required for graph execution but %d specified.", (int)req.size(), n));
+    for (size_t i = 0; i < req.size(); i++) {
+        const lx_tensor *t = nullptr;
+        if (names) {
+            for (int k = 0; k < n; k++)
+                if (names[k] && req[i]->name == names[k]) t = &inputs[k];
+            if (!t) return failure(fmt("User inputs do not contain required input %s.", req[i]->name.c_str()));
+        } else {
+            t = &inputs[i];
+        }
+        if (t->rank != req[i]->rank || t->dtype != req[i]->dtype)
+            return failure(fmt("Cannot use user input %s for required input %s. Tensor type or rank does not match.",
+                               desc("", *t).c_str(), req[i]->name.c_str()));
+        g->input_vals[req[i]->name] = borrowed(*t);
+    }
+    // liveness: the index of each name's last consumer
+    std::map<std::string, int> last;
+    for (int k = 0; k < (int)g->nodes.size(); k++)
+        for (auto &nm : g->nodes[k].in) last[nm] = k;
+    std::set<std::string> keep(g->outputs.begin(), g->outputs.end());
+    Exec X{g};
+    for (int k = 0; k < (int)g->nodes.size(); k++) {
+        const GNode &node = g->nodes[k];
+        std::vector<Value> outs;
+        st = run_node(X, node, outs);
+        if (!st && outs.size() != node.out.size())
+            st = failure(fmt("The operation returned %d outputs but the graph node has %d outputs.", (int)outs.size(),
+                             (int)node.out.size()));
+        if (st) {
+            std::string m = lx_last_error();
+            return fail(st, fmt("Execution of node %d %s with op %s failed: %s", k + 1, node.name.c_str(), node.op.c_str(),
+                                m.c_str()));
+        }
+        for (size_t i = 0; i < outs.size(); i++) g->values[node.out[i]] = outs[i];
+        // intermediates whose last consumer has run go back to the pool (aliases keep their block)
+        for (auto &nm : node.in)
+            if (last[nm] == k && !keep.count(nm)) g->values.erase(nm);
+    }
+    return LX_OK;
+}
+
+int lx_graph_execute_node(lx_graph *g, const char *node, int32_t n, const char *const *names, const lx_tensor *inputs,
+                          int32_t use_initializers) {
+    if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
+    if (!g || !node || n < 0 || (n > 0 && !inputs)) return failure("null argument");
+    const GNode *nd = nullptr;
+    for (auto &x : g->nodes)
+        if (x.name == node) { nd = &x; break; }
+    if (!nd) return failure(fmt("Could not find node %s in graph.", node));
+    int st = upload_initializers(g);
+    if (st) return st;
+    g->values.clear();
+    g->input_vals.clear();
+    // ResolveNodeExecuteInputs (ComputationalGraph.cs:132-197)
+    std::vector<std::string> req;
+    for (auto &i : nd->in) {
+        if (use_initializers && g->init_dev.count(i)) g->input_vals[i] = g->init_dev[i];
+        else req.push_back(i);
+    }
+    if ((size_t)n != req.size())
+        return failure(fmt("%d user input(s) required for node execution but %d specified.", (int)req.size(), n));
+    for (size_t i = 0; i < req.size(); i++) {
+        const lx_tensor *t = nullptr;
+        if (names) {
+            for (int k = 0; k < n; k++)
+                if (names[k] && req[i] == names[k]) t = &inputs[k];
+            if (!t) return failure(fmt("User inputs do not contain required input %s.", req[i].c_str()));
+        } else {
+            t = &inputs[i];
+        }
+        g->input_vals[req[i]] = borrowed(*t);
+    }
+    Exec X{g};
+    std::vector<Value> outs;
+    st = run_node(X, *nd, outs);
+    if (!st && outs.size() != nd->out.size()) st = failure("output count mismatch");
+    if (st) {
+        std::string m = lx_last_error();
+        return fail(st, fmt("Execution of node %s with op %s failed: %s.", nd->name.c_str(), nd->op.c_str(), m.c_str()));
+    }
+    for (size_t i = 0; i < outs.size(); i++) g->values[nd->out[i]] = outs[i];
+    return LX_OK;
+}
+
+int lx_graph_output(lx_graph *g, const char *name, lx_tensor *out) {
+    if (!g || !name || !out) return failure("null argument");
+    auto it = g->values.find(name);
+    if (it == g->values.end()) return failure(fmt("The graph holds no tensor named %s.", name));
+    *out = it->second.t;
+    out->owns = 0;
+    return LX_OK;
+}
+
+int lx_graph_reset(lx_graph *g) {
+    if (!g) return LX_OK;
+    g->values.clear();
+    g->input_vals.clear();
+    return LX_OK;
+}
+
+int32_t lx_graph_node_count(const lx_graph *g) { return g ? (int32_t)g->nodes.size() : 0; }
+
+static void copy_str(const std::string &s, char *buf, int32_t len) {
+    if (!buf || len <= 0) return;
+    size_t n = std::min((size_t)len - 1, s.size());
+    memcpy(buf, s.data(), n);
+    buf[n] = 0;
+}
+
+int lx_graph_node_info(const lx_graph *g, int32_t i, char *op_type, int32_t op_len, char *name, int32_t name_len) {
+    if (!g || i < 0 || i >= (int32_t)g->nodes.size()) return failure("invalid node index");
+    copy_str(g->nodes[i].op, op_type, op_len);
+    copy_str(g->nodes[i].name, name, name_len);
+    return LX_OK;
+}
+
+int32_t lx_graph_input_count(const lx_graph *g) { return g ? (int32_t)g->inputs.size() : 0; }
+
+int lx_graph_input_info(const lx_graph *g, int32_t i, char *name, int32_t name_len, int32_t *dtype, int32_t *rank,
+                        int64_t *dims) {
+    if (!g || i < 0 || i >= (int32_t)g->inputs.size()) return failure("invalid input index");
+    const GInput &in = g->inputs[i];
+    copy_str(in.name, name, name_len);
+    if (dtype) *dtype = in.dtype;
+    if (rank) *rank = in.rank;
+    if (dims)
+        for (int k = 0; k < in.rank; k++) dims[k] = in.dims[k];
+    return LX_OK;
+}
+
+int32_t lx_graph_initializer_count(const lx_graph *g) { return g ? (int32_t)g->initializers.size() : 0; }
+
+int lx_graph_initializer_info(const lx_graph *g, int32_t i, char *name, int32_t name_len, int32_t *dtype,
+                              int32_t *rank, int64_t *dims) {
+    if (!g || i < 0 || i >= (int32_t)g->initializers.size()) return failure("invalid initializer index");
+    const auto &kv = g->initializers[i];
+    copy_str(kv.first, name, name_len);
+    if (dtype) *dtype = kv.second->dtype;
+    if (rank) *rank = kv.second->rank;
+    if (dims)
+        for (int k = 0; k < kv.second->rank; k++) dims[k] = kv.second->dims[k];
+    return LX_OK;
+}
+
+int32_t lx_graph_output_count(const lx_graph *g) { return g ? (int32_t)g->outputs.size() : 0; }
+
+int lx_graph_output_name(const lx_graph *g, int32_t i, char *name, int32_t name_len) {
+    if (!g || i < 0 || i >= (int32_t)g->outputs.size()) return failure("invalid output index");
+    copy_str(g->outputs[i], name, name_len);
+    return LX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// lx_graph.h -- graph runtime structures shared by the executor (lx_graph.cpp)
+// and the ONNX model loader (lx_onnx.cpp).
+#pragma once
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/lonnx.h"
+
+namespace lx {
+
+// A tensor held in host memory: initializers before upload, attribute
+// tensors, and the host copy of small integer tensors (shapes, axes).
+struct HostTensor {
+    int32_t dtype = 0;
+    int32_t rank = 0;
+    int64_t dims[LX_MAX_RANK] = {0};
+    std::vector<uint8_t> bytes;  // row-major
+    int64_t numel() const {
+        int64_t n = 1;
+        for (int i = 0; i < rank; i++) n *= dims[i];
+        return n;
+    }
+};
+
+enum AttrKind { kAttrInt, kAttrInts, kAttrFloat, kAttrFloats, kAttrString, kAttrTensor };
+
+// AttributeProto.Value (NodeUtil.cs:9-22): Int -> long, Ints -> long[],
+// Float -> float, Floats -> float[], String -> string, Tensor -> ITensor.
+struct Attr {
+    AttrKind kind = kAttrInt;
+    int64_t i = 0;
+    std::vector<int64_t> ints;
+    float f = 0.0f;
+    std::vector<float> floats;
+    std::string s;
+    std::shared_ptr<HostTensor> t;
+};
+
+// Device storage shared by a tensor and its Reshape / Unsqueeze aliases.
+struct Storage {
+    void *ptr = nullptr;
+    ~Storage();
+};
+
+// One named tensor of an execution.
+struct Value {
+    lx_tensor t{};                      // device view
+    std::shared_ptr<Storage> store;     // null for borrowed caller tensors
+    std::shared_ptr<HostTensor> host;   // host copy when known
+};
+
+struct GNode {
+    std::string name, op;
+    std::vector<std::string> in, out;
+    std::map<std::string, Attr> attrs;
+    std::vector<GNode> fused_from;  // the original nodes of a fused subgraph
+};
+
+struct GInput {
+    std::string name;
+    int32_t dtype = 0;
+    int32_t rank = 0;
+    int64_t dims[LX_MAX_RANK] = {0};
+};
+
+}  // namespace lx
+
+struct lx_graph {
+    int64_t opset = 13;
+    std::string name;
+    std::vector<lx::GNode> nodes;
+    std::vector<lx::GInput> inputs;
+    std::vector<std::string> outputs;
+    std::vector<std::pair<std::string, std::shared_ptr<lx::HostTensor>>> initializers;
+    std::map<std::string, lx::Value> init_dev;  // initializers resident in HBM
+    std::map<std::string, lx::Value> input_vals;  // graph.Inputs of the current execution
+    std::map<std::string, lx::Value> values;    // node outputs of the current execution
+    std::vector<std::string> node_outputs;      // every name a node produces (IntermediateOutputs + Outputs)
+};

@@ -1,0 +1,108 @@
+// lx_pool.cpp -- see lx_pool.h.
+#include "lx_pool.h"
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+namespace lx {
+
+namespace {
+
+struct PoolState {
+    std::mutex mu;
+    std::unordered_map<size_t, std::vector<void *>> free_lists;  // size class -> cached blocks
+    std::unordered_map<void *, size_t> live;                     // block -> size class
+    int64_t live_bytes = 0, cached_bytes = 0;
+};
+
+PoolState &pool() {
+    static PoolState *p = new PoolState();  // never destroyed: blocks may be released at process exit
+    return *p;
+}
+
+hipError_t free_cached_locked(PoolState &ps) {
+    hipError_t first = hipSuccess;
+    for (auto &kv : ps.free_lists) {
+        for (void *b : kv.second) {
+            hipError_t e = hipFree(b);
+            if (e != hipSuccess && first == hipSuccess) first = e;
+        }
+        kv.second.clear();
+    }
+    ps.free_lists.clear();
+    ps.cached_bytes = 0;
+    return first;
+}
+
+}  // namespace
+
+// Classes: powers of two up to 1 MiB, then multiples of 2 MiB, so a reused
+// block wastes at most half of a small request and under 2 MiB of a large one.
+size_t pool_class(size_t bytes) {
+    if (bytes <= 256) return 256;
+    if (bytes <= (1u << 20)) {
+        size_t c = 512;
+        while (c < bytes) c <<= 1;
+        return c;
+    }
+    const size_t g = 2u << 20;
+    return (bytes + g - 1) / g * g;
+}
+
+hipError_t pool_alloc(size_t bytes, void **p, size_t *cap, hipStream_t s) {
+    PoolState &ps = pool();
+    const size_t c = pool_class(bytes);
+    std::lock_guard<std::mutex> lock(ps.mu);
+    auto it = ps.free_lists.find(c);
+    if (it != ps.free_lists.end() && !it->second.empty()) {
+        *p = it->second.back();
+        it->second.pop_back();
+        ps.cached_bytes -= (int64_t)c;
+    } else {
+        hipError_t e = hipMalloc(p, c);
+        if (e == hipErrorOutOfMemory && ps.cached_bytes > 0) {
+            (void)hipGetLastError();
+            e = hipStreamSynchronize(s);
+            if (e != hipSuccess) return e;
+            e = free_cached_locked(ps);
+            if (e != hipSuccess) return e;
+            e = hipMalloc(p, c);
+        }
+        if (e != hipSuccess) return e;
+    }
+    ps.live[*p] = c;
+    ps.live_bytes += (int64_t)c;
+    if (cap) *cap = c;
+    return hipSuccess;
+}
+
+bool pool_release(void *p) {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    auto it = ps.live.find(p);
+    if (it == ps.live.end()) return false;
+    const size_t c = it->second;
+    ps.live.erase(it);
+    ps.live_bytes -= (int64_t)c;
+    ps.free_lists[c].push_back(p);
+    ps.cached_bytes += (int64_t)c;
+    return true;
+}
+
+hipError_t pool_trim(hipStream_t s) {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return e;
+    return free_cached_locked(ps);
+}
+
+void pool_stats(int64_t *live, int64_t *cached) {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    if (live) *live = ps.live_bytes;
+    if (cached) *cached = ps.cached_bytes;
+}
+
+}  // namespace lx

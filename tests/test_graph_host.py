@@ -1,0 +1,183 @@
+"""CPU checks of the graph runtime's host side: the ONNX loader against an
+independent decode of the reference's mnist-8.onnx fixture and of models built
+here, its error statuses, and the pattern fusion pass (lx_graph_fuse needs no
+device)."""
+import struct
+
+import numpy as np
+import pytest
+
+import onnx_amd  # noqa: F401
+from onnx_amd import _lib as L
+from onnx_amd.graph import ComputationalGraph, Model
+
+import onnx_writer as W
+
+MNIST = __import__("os").path.join(__import__("os").path.dirname(__file__), "golden", "mnist-8.onnx")
+SQRT2 = np.float32(np.sqrt(2.0))
+
+
+def _independent(path):
+    """Node ops/names, inputs, initializer shapes of a ModelProto via the generic decoder."""
+    m = W.decode(open(path, "rb").read())
+    g = W.decode(m[7][0])
+    nodes = []
+    for nb in g.get(1, []):
+        n = W.decode(nb)
+        nodes.append((n.get(3, [b""])[0].decode(), n[4][0].decode()))
+    inits = []
+    for tb in g.get(5, []):
+        t = W.decode(tb)
+        dims = []
+        for d in t.get(1, []):
+            dims += [W._read_varint(d, i)[0] for i in [0]] if isinstance(d, bytes) else [d]
+        inits.append((t[8][0].decode(), t[2][0], tuple(dims)))
+    ins = []
+    for vb in g.get(11, []):
+        v = W.decode(vb)
+        tt = W.decode(W.decode(v[2][0])[1][0])
+        shape = W.decode(tt[2][0]) if 2 in tt else {}
+        dims = tuple(W.decode(d).get(1, [0])[0] for d in shape.get(1, []))
+        ins.append((v[1][0].decode(), tt[1][0], dims))
+    outs = [W.decode(vb)[1][0].decode() for vb in g.get(12, [])]
+    opset = [W.decode(o) for o in m.get(8, [])]
+    return nodes, ins, inits, outs, opset
+
+
+def test_loader_reads_reference_mnist_fixture():
+    nodes, ins, inits, outs, _ = _independent(MNIST)
+    g = Model.Load(MNIST)
+    assert [(n.Name, n.Op) for n in g.Nodes] == nodes
+    assert g.InputInfo == ins
+    assert sorted(g.InitializerInfo) == sorted(inits)
+    assert g.OutputNames == outs
+    # the bias-broadcast Adds the reference's tests name (test_backend.py:85, 96)
+    assert ("Plus30", "Add") in nodes and ("Plus214", "Add") in nodes
+
+
+def _all_kinds_model():
+    nodes = [W.node("Add", ["x", "w"], ["y"], "add1"),
+             W.node("Constant", [], ["c"], "const1", value=np.arange(6, dtype=np.float32).reshape(2, 3)),
+             W.node("Cast", ["y"], ["z"], "cast1", to=7, note="text", ratio=0.5, axes=[0, -1], scales=[1.5, 2.5])]
+    inits = [("w", np.arange(12, dtype=np.float32).reshape(3, 4)), ("i64", np.array([-3, 2**40], np.int64)),
+             ("d", np.array([1.25], np.float64)), ("i32", np.array([[7, -8]], np.int32))]
+    return W.model(nodes, [("x", np.float32, (3, 4)), ("n", np.float32, ("batch", 4))],
+                   [("z", np.int64, (3, 4))], inits)
+
+
+def test_loader_roundtrip_of_written_model():
+    g = Model.Load(W.model([W.node("Add", ["x", "w"], ["y"], "add1")], [("x", np.float32, (3, 4))],
+                           [("y", np.float32, (3, 4))], [("w", np.ones((3, 4), np.float32))]))
+    assert [(n.Name, n.Op) for n in g.Nodes] == [("add1", "Add")]
+    g = Model.Load(_all_kinds_model())
+    assert [(n.Name, n.Op) for n in g.Nodes] == [("add1", "Add"), ("const1", "Constant"), ("cast1", "Cast")]
+    # a symbolic dim reads as DimValue 0 (TensorUtil.cs:62-84)
+    assert g.InputInfo == [("x", L.FLOAT, (3, 4)), ("n", L.FLOAT, (0, 4))]
+    assert g.InitializerInfo == [("w", L.FLOAT, (3, 4)), ("i64", L.INT64, (2,)), ("d", L.DOUBLE, (1,)),
+                                 ("i32", L.INT32, (1, 2))]
+    assert g.OutputNames == ["z"]
+
+
+@pytest.mark.parametrize("typed", [False, True])
+def test_loader_typed_and_raw_initializer_fields(typed):
+    """GetTensorData (TensorUtil.cs:14-31): typed fields when present, else raw_data."""
+    for arr in [np.array([1.5, -2.25], np.float32), np.array([[-3, 2**40]], np.int64),
+                np.array([7, -8, 9], np.int32), np.array([0.1], np.float64)]:
+        t = W.tensor("p", arr, raw=not typed)
+        buf = W.f_varint(1, 7) + W.f_bytes(7, W.f_bytes(5, t)) + W.f_bytes(8, W.f_varint(2, 13))
+        g = Model.Load(buf)
+        assert g.InitializerInfo == [("p", W.ELEM[arr.dtype], arr.shape)]
+
+
+def test_loader_error_statuses():
+    lib = L.lib()
+    import ctypes
+    h = ctypes.c_void_p()
+    junk = b"\x0a\xff\xff\xff\xff\x0f"
+    assert lib.lx_graph_load_onnx(junk, len(junk), ctypes.byref(h)) == L.ERR_INVALID_ARGUMENT
+    assert "Malformed ONNX model" in L.last_error()
+    # uint8 initializers are refused by GetTensorData (TensorUtil.cs:29)
+    bad = W.model([], [], [], [("u", np.array([1, 2], np.uint8))])
+    assert lib.lx_graph_load_onnx(bad, len(bad), ctypes.byref(h)) == L.ERR_NOT_SUPPORTED
+    assert L.last_error() == "Cannot get embedded tensor data of tensor element type 2."
+    # a graph-valued attribute has no conversion in AttributeProto.Value (NodeUtil.cs:20)
+    att = W.f_bytes(1, "body") + W.f_bytes(6, b"") + W.f_varint(20, 5)
+    nd = W.f_bytes(1, "x") + W.f_bytes(2, "y") + W.f_bytes(4, "If") + W.f_bytes(5, att)
+    bad = W.model([nd], [], [])
+    assert lib.lx_graph_load_onnx(bad, len(bad), ctypes.byref(h)) == L.ERR_NOT_SUPPORTED
+    assert L.last_error() == "Cannot convert attribute proto value of type Graph."
+
+
+# ---- fusion ---------------------------------------------------------------------
+def gelu_nodes(x="x", y="y", half="half", extra=()):
+    return [W.node("Div", [x, "sqrt2"], ["a"], "div"), W.node("Erf", ["a"], ["e"], "erf"),
+            W.node("Add", ["e", "one"], ["b"], "add"), W.node("Mul", [x, "b"], ["c"], "mul"),
+            W.node("Mul", ["c", half], [y], "mul2")] + list(extra)
+
+
+GELU_INITS = [("sqrt2", np.array(SQRT2, np.float32)), ("one", np.array(1.0, np.float32)),
+              ("half", np.array(0.5, np.float32))]
+
+
+def ln_nodes(x="x", y="y"):
+    return [W.node("ReduceMean", [x, "axes"], ["mean"], "rm1"), W.node("Sub", [x, "mean"], ["d"], "sub"),
+            W.node("Pow", ["d", "two"], ["p"], "pow"), W.node("ReduceMean", ["p", "axes"], ["var"], "rm2"),
+            W.node("Add", ["var", "eps"], ["ve"], "addeps"), W.node("Sqrt", ["ve"], ["sd"], "sqrt"),
+            W.node("Div", ["d", "sd"], ["n"], "div"), W.node("Mul", ["n", "gamma"], ["m"], "mulg"),
+            W.node("Add", ["m", "beta"], [y], "addb")]
+
+
+def LN_INITS(r=8):
+    return [("axes", np.array([-1], np.int64)), ("two", np.array(2.0, np.float32)),
+            ("eps", np.array(1e-12, np.float32)), ("gamma", np.ones(r, np.float32)), ("beta", np.zeros(r, np.float32))]
+
+
+def _fused(nodes, inits, outputs=("y",), inputs=(("x", np.float32, (2, 8)),)):
+    g = Model.Load(W.model(nodes, list(inputs), [(o, np.float32, (2, 8)) for o in outputs], inits))
+    n = g.Fuse()
+    return n, [(nd.Name, nd.Op) for nd in g.Nodes]
+
+
+def test_fusion_replaces_the_three_subgraphs():
+    assert _fused(gelu_nodes(), GELU_INITS) == (1, [("mul2", "GeluErf")])
+    assert _fused(ln_nodes(), LN_INITS()) == (1, [("addb", "LayerNormDecomposed")])
+    sm = [W.node("Add", ["x", "mask"], ["t"], "add"), W.node("Softmax", ["t"], ["y"], "sm", axis=-1)]
+    assert _fused(sm, [("mask", np.zeros((1, 8), np.float32))]) == (1, [("sm", "AddSoftmax")])
+    # the three in one graph, chained
+    nodes = ln_nodes(y="h") + gelu_nodes(x="h", y="g") + [W.node("Add", ["g", "mask"], ["t"], "add3"),
+                                                          W.node("Softmax", ["t"], ["y"], "sm")]
+    inits = LN_INITS() + GELU_INITS + [("mask", np.zeros((1, 8), np.float32))]
+    assert _fused(nodes, inits) == (3, [("addb", "LayerNormDecomposed"), ("mul2", "GeluErf"), ("sm", "AddSoftmax")])
+
+
+def test_fusion_keeps_subgraphs_whose_intermediates_escape():
+    # an intermediate is also a graph output
+    n, ops = _fused(gelu_nodes(), GELU_INITS, outputs=("y", "e"))
+    assert n == 0 and len(ops) == 5
+    # an intermediate has a consumer outside the pattern
+    n, ops = _fused(gelu_nodes(extra=[W.node("Sqrt", ["b"], ["z"], "other")]), GELU_INITS, outputs=("y", "z"))
+    assert n == 0 and len(ops) == 6
+    # a constant with other bits than float32(sqrt 2)
+    inits = [("sqrt2", np.array(1.4142, np.float32))] + GELU_INITS[1:]
+    assert _fused(gelu_nodes(), inits)[0] == 0
+    # a "constant" the caller may replace (an initializer that is also a graph input)
+    n, _ = _fused(gelu_nodes(), GELU_INITS, inputs=(("x", np.float32, (2, 8)), ("half", np.float32, ())))
+    assert n == 0
+    # LayerNorm reducing another axis
+    inits = LN_INITS()
+    inits[0] = ("axes", np.array([0], np.int64))
+    assert _fused(ln_nodes(), inits)[0] == 0
+
+
+def test_graph_builder_api_and_fusion_without_onnx_bytes():
+    g = ComputationalGraph(13)
+    g.AddInput("x", np.float32, (4, 8))
+    for name, v in GELU_INITS:
+        g.AddInitializer(name, v)
+    g.AddNode("Div", ["x", "sqrt2"], ["a"], "div")
+    g.AddNode("Erf", ["a"], ["e"], "erf")
+    g.AddNode("Add", ["one", "e"], ["b"], "add")   # operands in the other order
+    g.AddNode("Mul", ["b", "x"], ["c"], "mul")
+    g.AddNode("Mul", ["half", "c"], ["y"], "mul2")
+    g.AddOutput("y")
+    assert g.Fuse() == 1 and [n.Op for n in g.Nodes] == ["GeluErf"]
