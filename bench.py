@@ -88,6 +88,19 @@ def graph_time(torch, launch, steps, warmup, set_stream, reps=1):
     return sorted(times)[len(times) // 2]
 
 
+def wall_time(torch, fn, steps, warmup):
+    """Host wall clock per call of `fn(i)` between two device synchronisations
+    (for host-dispatched work that is not captured in a HIP graph)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
 def measured_traffic():
     """HBM bytes per LayerNorm launch from the committed rocprofv3 counter
     summary (profiles/k_layernorm_c2_traffic.txt), or None when absent."""
@@ -185,6 +198,37 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
         HIP.Mul(wf["n"][j], wg, out=wf["m"][j])
         HIP.Add(wf["m"][j], wb, out=wY[j])
     run("C2 LayerNorm 9 separate ops", 151132168, 8 * 512 * 768, ln_unfused, LN_SETS, k=max(8, steps // 4))
+
+    # the same ONNX subgraph through the device graph runtime (the ComputationalGraph twin), one
+    # host-dispatched execution per step (wall clock, ctypes call included): 9 nodes, then fused
+    from onnx_amd.graph import ComputationalGraph
+
+    def ln_graph(fuse):
+        gr = ComputationalGraph(13)
+        gr.AddInput("x", np.float32, LN_SHAPE)
+        for name, v in (("axes", np.array([-1], np.int64)), ("two", np.array(2.0, np.float32)),
+                        ("eps", np.array(1e-12, np.float32)), ("gamma", gam.cpu().numpy()),
+                        ("beta", bet.cpu().numpy())):
+            gr.AddInitializer(name, v)
+        for op, ins, outs in (("ReduceMean", ["x", "axes"], ["mean"]), ("Sub", ["x", "mean"], ["d"]),
+                              ("Pow", ["d", "two"], ["p"]), ("ReduceMean", ["p", "axes"], ["var"]),
+                              ("Add", ["var", "eps"], ["ve"]), ("Sqrt", ["ve"], ["sd"]), ("Div", ["d", "sd"], ["n"]),
+                              ("Mul", ["n", "gamma"], ["m"]), ("Add", ["m", "beta"], ["y"])):
+            gr.AddNode(op, ins, outs, name=outs[0])
+        gr.AddOutput("y")
+        if fuse:
+            assert gr.Fuse() == 1
+        return gr
+
+    for fuse, label, nbytes in ((False, "9 nodes", 151132168), (True, "fused to 1 node", LN_BYTES)):
+        gr = ln_graph(fuse)
+
+        def step(i, gr=gr):
+            if not gr.Execute([wX[i % LN_SETS]]):
+                raise RuntimeError(gr.LastError)
+        ms = wall_time(torch, step, max(16, steps // 2), warmup)
+        record(f"C2 LayerNorm graph executor, {label} (host dispatch per execution)", nbytes, 8 * 512 * 768, ms)
+        gr.close()
     del X, Y, tm, tf, wX, wY, wm, wf
     torch.cuda.empty_cache()
 
