@@ -160,6 +160,10 @@ int lx_ReduceMean(const lx_tensor *data, const int64_t *axes, int32_t n_axes, in
 int lx_ReduceMax(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims, lx_tensor *Y);
 /* CPUExecutionProvider.Softmax (CPUExecutionProvider.cs:680-695); has_axis = 0 means default -1. */
 int lx_Softmax(const lx_tensor *input, int32_t axis, int32_t has_axis, lx_tensor *Y);
+/* CPUExecutionProvider.MatMul (CPUExecutionProvider.cs:359-378); Tensor<T>.MatMul (TensorOps.cs:504-806)
+ * for Int32 (exact, wrapping), Float (fp32 MFMA) and Double (fp64 MFMA), with the reference's batch
+ * broadcast and rank-1 rules. */
+int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
 
 /* ---- fused subgraphs (one kernel each; every intermediate keeps the float32
  * rounding of the separate ONNX node it replaces) ------------------------- */

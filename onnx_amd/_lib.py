@@ -92,6 +92,7 @@ SIGNATURES = {
     "lx_GeluErf": (_c.c_int, [_T, _T]),
     "lx_LayerNormDecomposed": (_c.c_int, [_T, _T, _T, _c.c_float, _T]),
     "lx_AddSoftmax": (_c.c_int, [_T, _T, _c.c_int32, _T]),
+    "lx_MatMul": (_c.c_int, [_T, _T, _T]),
     "lx_pool_trim": (_c.c_int, []),
     "lx_pool_stats": (_c.c_int, [_i64p, _i64p]),
     # graph runtime

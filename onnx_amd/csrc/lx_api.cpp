@@ -997,3 +997,201 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
 }
 
 }  // namespace
+
+// ===========================================================================
+// MatMul: CPUExecutionProvider.MatMul (CPUExecutionProvider.cs:359-378) over
+// Tensor<T>.MatMul (TensorOps.cs:504-806 for Int32, Float, Double): the same
+// shape rules, broadcast cases and exception texts.
+// ===========================================================================
+namespace {
+
+struct MView {  // a tensor as the reference's (possibly broadcast) view: element strides, 0 on broadcast axes
+    int rank = 0;
+    int64_t dims[LX_MAX_RANK] = {0};
+    int64_t str[LX_MAX_RANK] = {0};
+    const void *data = nullptr;
+};
+
+MView dense_view(const lx_tensor *t) {
+    MView v;
+    v.rank = t->rank;
+    int64_t s = 1;
+    for (int d = t->rank - 1; d >= 0; d--) {
+        v.dims[d] = t->dims[d];
+        v.str[d] = s;
+        s *= t->dims[d];
+    }
+    v.data = t->data;
+    return v;
+}
+
+std::string shape_str(const MView &v) {
+    std::string s = "[";
+    for (int i = 0; i < v.rank; i++) s += (i ? "," : "") + std::to_string(v.dims[i]);
+    return s + "]";
+}
+
+// Tensor<T>.Broadcast(x, shape): right-aligned view of x at `dims`
+bool broadcast_view(const MView &x, int rank, const int64_t *dims, MView *out) {
+    if (rank < x.rank || rank > LX_MAX_RANK) return false;
+    MView v;
+    v.rank = rank;
+    v.data = x.data;
+    for (int d = 0; d < rank; d++) {
+        const int xd = d - (rank - x.rank);
+        v.dims[d] = dims[d];
+        if (xd < 0) v.str[d] = 0;
+        else if (x.dims[xd] == dims[d]) v.str[d] = x.str[xd];
+        else if (x.dims[xd] == 1) v.str[d] = 0;
+        else return false;
+    }
+    *out = v;
+    return true;
+}
+
+// numpy / ITensor broadcast shape of two shapes
+bool broadcast_dims(int ra, const int64_t *da, int rb, const int64_t *db, int *ro, int64_t *dout) {
+    const int r = std::max(ra, rb);
+    if (r > LX_MAX_RANK) return false;
+    for (int d = 0; d < r; d++) {
+        const int ia = d - (r - ra), ib = d - (r - rb);
+        const int64_t a = ia >= 0 ? da[ia] : 1, b = ib >= 0 ? db[ib] : 1;
+        if (a != b && a != 1 && b != 1) return false;
+        dout[d] = a == 1 ? b : a;
+    }
+    *ro = r;
+    return true;
+}
+
+const char *net_type(int dt) {
+    switch (dt) {
+    case LX_FLOAT: return "System.Single"; case LX_DOUBLE: return "System.Double"; case LX_INT32: return "System.Int32";
+    case LX_INT64: return "System.Int64"; case LX_UINT8: return "System.Byte"; case LX_INT8: return "System.SByte";
+    case LX_INT16: return "System.Int16"; case LX_UINT16: return "System.UInt16"; case LX_UINT32: return "System.UInt32";
+    case LX_UINT64: return "System.UInt64"; case LX_BOOL: return "System.Boolean"; default: return "System.Object";
+    }
+}
+
+// the matrix part (last two axes) must be row-major dense for the kernels; otherwise
+// the operand is copied to a dense pooled block first
+int densify(int dt, MView *v, std::vector<void *> &temps) {
+    const int r = v->rank;
+    if ((v->dims[r - 1] == 1 || v->str[r - 1] == 1) && (v->dims[r - 2] == 1 || v->str[r - 2] == v->dims[r - 1]))
+        return LX_OK;
+    int64_t n = 1;
+    for (int d = 0; d < r; d++) n *= v->dims[d];
+    void *p = nullptr;
+    HIPCHECK(pool_alloc((size_t)std::max<int64_t>(n * esize(dt), 16), &p, nullptr, g.stream), "device allocation (temporary)");
+    temps.push_back(p);
+    HIPCHECK(launch_strided_copy((int)esize(dt), v->data, p, r, v->dims, v->str, g.stream), "MatMul broadcast copy");
+    int64_t s = 1;
+    for (int d = r - 1; d >= 0; d--) {
+        v->str[d] = s;
+        s *= v->dims[d];
+    }
+    v->data = p;
+    return LX_OK;
+}
+
+int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, lx_tensor *Y,
+               std::vector<void *> &temps) {
+    int st;
+    if ((st = densify(dt, &x, temps)) || (st = densify(dt, &y, temps))) return st;
+    if ((st = prepare_output(Y, dt, out_rank, out_dims))) return st;
+    MatMulArgs p;
+    memset(&p, 0, sizeof p);
+    p.m = (int32_t)x.dims[x.rank - 2];
+    p.k = (int32_t)x.dims[x.rank - 1];
+    p.n = (int32_t)y.dims[y.rank - 1];
+    p.nbatch = x.rank - 2;
+    p.batch = 1;
+    for (int d = 0; d < p.nbatch; d++) {
+        p.bdims[d] = x.dims[d];
+        p.a_bstr[d] = x.str[d];
+        p.b_bstr[d] = y.str[d];
+        p.batch *= x.dims[d];
+    }
+    if (p.nbatch > kMaxOuter) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d batch axes are supported.", kMaxOuter);
+    if (x.dims[x.rank - 2] > INT32_MAX || x.dims[x.rank - 1] > INT32_MAX || y.dims[y.rank - 1] > INT32_MAX)
+        return set_err(LX_ERR_NOT_SUPPORTED, "Matrix dimensions beyond 2^31 are not supported.");
+    if (p.k == 0) {  // empty inner dimension: every output is 0
+        int64_t n = numel(Y);
+        HIPCHECK(launch_fill(Y->data, n, (int)esize(dt), 0, g.stream), "MatMul");
+        return LX_OK;
+    }
+    HIPCHECK(launch_matmul(dt, x.data, y.data, Y->data, p, g.stream), "MatMul");
+    return LX_OK;
+}
+
+int cols_rows_error(int64_t cols, int64_t rows) {
+    return set_err(LX_ERR_INVALID_ARGUMENT,
+                   "The number of columns in the first matrix (%lld) is not equal to the number of rows in the second "
+                   "matrix (%lld).",
+                   (long long)cols, (long long)rows);
+}
+
+// Tensor<T>.MatMul (TensorOps.cs:600-705)
+int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vector<void *> &temps) {
+    if (x.rank == 0 || y.rank == 0)
+        return set_err(LX_ERR_INVALID_ARGUMENT, "The rank of each tensor in matrix multiplication must be greater than 1.");
+    if (x.rank == 2 && y.rank == 2) {  // MatMul2D (TensorOps.cs:356-407)
+        if (x.dims[1] != y.dims[0]) return cols_rows_error(x.dims[1], y.dims[0]);
+        int64_t od[2] = {x.dims[0], y.dims[1]};
+        return matmul_run(dt, x, y, 2, od, Y, temps);
+    }
+    if (x.rank >= 2 && y.rank >= 2) {
+        const int64_t xm = x.dims[x.rank - 2], xk = x.dims[x.rank - 1];
+        const int64_t yk = y.dims[y.rank - 2], yn = y.dims[y.rank - 1];
+        if (xk != yk) return cols_rows_error(xk, yk);
+        int br;
+        int64_t bd[LX_MAX_RANK + 2];
+        if (!broadcast_dims(x.rank - 2, x.dims, y.rank - 2, y.dims, &br, bd) || br + 2 > LX_MAX_RANK)
+            return set_err(LX_ERR_INVALID_ARGUMENT, "The tensor shapes are not compatible for broadcasting.");
+        MView bx, by;
+        int64_t dx[LX_MAX_RANK], dy[LX_MAX_RANK], od[LX_MAX_RANK];
+        for (int d = 0; d < br; d++) dx[d] = dy[d] = od[d] = bd[d];
+        dx[br] = xm; dx[br + 1] = xk;
+        dy[br] = yk; dy[br + 1] = yn;
+        od[br] = xm; od[br + 1] = yn;
+        if (!broadcast_view(x, br + 2, dx, &bx) || !broadcast_view(y, br + 2, dy, &by))
+            return set_err(LX_ERR_INVALID_ARGUMENT, "The tensor shapes are not compatible for broadcasting.");
+        return matmul_run(dt, bx, by, br + 2, od, Y, temps);
+    }
+    if (x.rank >= 2 || y.rank >= 2) {  // one operand of rank 1: element-wise broadcast of both, then MatMul
+        int r;
+        int64_t bd[LX_MAX_RANK];
+        MView bx, by;
+        if (!broadcast_dims(x.rank, x.dims, y.rank, y.dims, &r, bd) || !broadcast_view(x, r, bd, &bx) ||
+            !broadcast_view(y, r, bd, &by))
+            return set_err(LX_ERR_INVALID_ARGUMENT, "The shapes %s and %s are not compatible for broadcasting.",
+                           shape_str(x).c_str(), shape_str(y).c_str());
+        return matmul_views(dt, bx, by, Y, temps);
+    }
+    // both rank 1: [1,n] x [n,1] -> [1,1], then RemoveDim(0) -> [1]
+    MView px, py;
+    px.rank = 2; px.dims[0] = 1; px.dims[1] = x.dims[0]; px.str[0] = x.dims[0]; px.str[1] = x.str[0]; px.data = x.data;
+    py.rank = 2; py.dims[0] = y.dims[0]; py.dims[1] = 1; py.str[0] = y.str[0]; py.str[1] = 1; py.data = y.data;
+    if (px.dims[1] != py.dims[0]) return cols_rows_error(px.dims[1], py.dims[0]);
+    int64_t od[1] = {1};
+    return matmul_run(dt, px, py, 1, od, Y, temps);
+}
+
+}  // namespace
+
+extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!A) return missing_input("MatMul", "A");
+    if (!B) return missing_input("MatMul", "B");
+    int st;
+    if ((st = check_tensor(A, "A")) || (st = check_tensor(B, "B"))) return st;
+    if (A->dtype != LX_INT32 && A->dtype != LX_FLOAT && A->dtype != LX_DOUBLE)
+        return type_not_supported("MatMul", "A", A);
+    if (B->dtype != A->dtype)
+        return set_err(LX_ERR_WRONG_INPUT_TYPE, "Unable to cast object of type 'Lokad.Onnx.DenseTensor`1[%s]' to type "
+                                                "'Lokad.Onnx.Tensor`1[%s]'.",
+                       net_type(B->dtype), net_type(A->dtype));
+    std::vector<void *> temps;
+    st = matmul_views(A->dtype, dense_view(A), dense_view(B), Y, temps);
+    for (void *t : temps) (void)pool_release(t);
+    return st;
+}

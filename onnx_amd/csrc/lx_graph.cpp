@@ -369,6 +369,10 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         auto f = op == "Add" ? lx_Add : op == "Sub" ? lx_Sub : op == "Mul" ? lx_Mul : op == "Div" ? lx_Div : lx_Pow;
         return run_op([&](lx_tensor *y) { return f(T(a), T(b), y); }, outs);
     }
+    if (op == "MatMul") {
+        if ((st = in2())) return st;
+        return run_op([&](lx_tensor *y) { return lx_MatMul(T(a), T(b), y); }, outs);
+    }
     if (op == "Sqrt" || op == "Erf") {
         if ((st = X.input(n, 0, &a))) return st;
         auto f = op == "Sqrt" ? lx_Sqrt : lx_Erf;

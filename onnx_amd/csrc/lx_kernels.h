@@ -98,4 +98,22 @@ hipError_t launch_layernorm(const float *x, const float *gamma, const float *bet
                             int64_t rows, int64_t r, hipStream_t s);
 bool layernorm_supported(int64_t r);
 
+// MatMul C[batch][m][n] = A[batch][m][k] * B[batch][k][n], row-major matrices;
+// batch index decomposed over bdims (outermost first) with per-operand element
+// strides (0 on broadcast axes); C is dense.
+struct MatMulArgs {
+    int32_t m, n, k;
+    int32_t nbatch;
+    int64_t batch;       // batches in this launch (grid z)
+    int64_t batch_base;  // index of the launch's first batch
+    int64_t bdims[kMaxOuter];
+    int64_t a_bstr[kMaxOuter];
+    int64_t b_bstr[kMaxOuter];
+};
+hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);
+
+// y[i] = x[offset(i)] for a strided view (strides in elements, 0 on broadcast axes)
+hipError_t launch_strided_copy(int esize, const void *x, void *y, int rank, const int64_t *dims, const int64_t *strides,
+                               hipStream_t s);
+
 }  // namespace lx

@@ -66,7 +66,8 @@ class DeviceTensor:
 
     @classmethod
     def from_numpy(cls, arr):
-        arr = np.ascontiguousarray(arr)
+        arr = np.asarray(arr)
+        arr = np.ascontiguousarray(arr).reshape(arr.shape)  # keeps rank 0
         t = cls.empty(arr.shape, arr.dtype)
         _check(L.lib().lx_tensor_upload(ctypes.byref(t.h), ctypes.c_void_p(arr.ctypes.data), arr.nbytes),
                "lx_tensor_upload")
@@ -265,6 +266,15 @@ class HipExecutionProvider:
         st = L.lib().lx_Softmax(_ptr(input), 0 if axis is None else int(axis), 0 if axis is None else 1,
                                 ctypes.byref(y))
         return _result("Softmax", st, y, out)
+
+    @staticmethod
+    def MatMul(A, B, out=None):
+        """CPUExecutionProvider.MatMul (CPUExecutionProvider.cs:359-378)."""
+        init()
+        A, B = _as_tensor(A), _as_tensor(B)
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_MatMul(_ptr(A), _ptr(B), ctypes.byref(y))
+        return _result("MatMul", st, y, out)
 
     # ---- fused subgraphs ---------------------------------------------------
     @staticmethod

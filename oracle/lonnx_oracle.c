@@ -683,3 +683,54 @@ void lxo_gelu_chain(int64_t n, const float *x, float *y)
         y[i] = c * 0.5f;
     }
 }
+
+/* ------------------------------------------------------------------------ */
+/* MatMul2D inner loop in the reference's order (MathOps.cs:380-419,         */
+/* mm_unsafe_vectorized): C starts at zero; for each row i, for each inner j */
+/* in order, C[i][k] += A[i][j] * B[j][k] -- the product rounded, then the   */
+/* sum rounded (Vector<T> '+' of '*', no FMA).  x is M x N, y is N x K.      */
+/* Int32 wraps (unchecked C#).                                               */
+/* ------------------------------------------------------------------------ */
+int lxo_matmul2d(int dtype, int64_t M, int64_t N, int64_t K, const void *a, const void *b, void *c)
+{
+    if (dtype == LXO_FLOAT) {
+        const float *A = (const float *)a, *B = (const float *)b;
+        float *C = (float *)c;
+        for (int64_t i = 0; i < M * K; i++) C[i] = 0.0f;
+        for (int64_t i = 0; i < M; i++)
+            for (int64_t j = 0; j < N; j++) {
+                const float av = A[i * N + j];
+                for (int64_t k = 0; k < K; k++) {
+                    const float p = av * B[j * K + k];
+                    C[i * K + k] = C[i * K + k] + p;
+                }
+            }
+        return LXO_OK;
+    }
+    if (dtype == LXO_DOUBLE) {
+        const double *A = (const double *)a, *B = (const double *)b;
+        double *C = (double *)c;
+        for (int64_t i = 0; i < M * K; i++) C[i] = 0.0;
+        for (int64_t i = 0; i < M; i++)
+            for (int64_t j = 0; j < N; j++) {
+                const double av = A[i * N + j];
+                for (int64_t k = 0; k < K; k++) {
+                    const double p = av * B[j * K + k];
+                    C[i * K + k] = C[i * K + k] + p;
+                }
+            }
+        return LXO_OK;
+    }
+    if (dtype == LXO_INT32) {
+        const int32_t *A = (const int32_t *)a, *B = (const int32_t *)b;
+        uint32_t *C = (uint32_t *)c;
+        for (int64_t i = 0; i < M * K; i++) C[i] = 0u;
+        for (int64_t i = 0; i < M; i++)
+            for (int64_t j = 0; j < N; j++) {
+                const uint32_t av = (uint32_t)A[i * N + j];
+                for (int64_t k = 0; k < K; k++) C[i * K + k] += av * (uint32_t)B[j * K + k];
+            }
+        return LXO_OK;
+    }
+    return LXO_ERR_NOT_SUPPORTED;
+}

@@ -50,6 +50,7 @@ int lxo_cast(int src_dtype, int dst_dtype, int64_t n, const void *in, void *out)
 int lxo_reduce(int op, int dtype, int rank, const int64_t *dims, const void *x, int naxes, const int64_t *axes,
                int keepdims, void *out, int *rout, int64_t *dout);
 int lxo_softmax(int dtype, int rank, const int64_t *dims, const void *x, int axis, void *out);
+int lxo_matmul2d(int dtype, int64_t M, int64_t N, int64_t K, const void *a, const void *b, void *c);
 void lxo_gelu_chain(int64_t n, const float *x, float *y);
 
 #endif

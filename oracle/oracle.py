@@ -58,6 +58,7 @@ def lib():
                                  ctypes.c_int, vp, ip, i64p]
         L.lxo_softmax.argtypes = [ctypes.c_int, ctypes.c_int, i64p, vp, ctypes.c_int, vp]
         L.lxo_gelu_chain.argtypes = [ctypes.c_int64, vp, vp]
+        L.lxo_matmul2d.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, vp, vp, vp]
         L.lxo_erf_f32.argtypes = [ctypes.c_float]
         L.lxo_erf_f32.restype = ctypes.c_float
         L.lxo_erf_f64.argtypes = [ctypes.c_double]
@@ -68,6 +69,12 @@ def lib():
         L.lxo_powf.restype = ctypes.c_float
         _lib = L
     return _lib
+
+
+def _contig(a):
+    """C-contiguous copy that keeps rank 0 (np.ascontiguousarray returns at least 1-D)."""
+    a = np.asarray(a)
+    return np.ascontiguousarray(a).reshape(a.shape)
 
 
 def _dims(shape):
@@ -91,8 +98,8 @@ def broadcast_shape(sa, sb):
 
 def binary(op, a, b):
     """CPUExecutionProvider.Add/Sub/Mul/Div/Pow on numpy arrays (same dtype)."""
-    a = np.ascontiguousarray(a)
-    b = np.ascontiguousarray(b)
+    a = _contig(a)
+    b = _contig(b)
     assert a.dtype == b.dtype
     code = CODE_OF[a.dtype]
     shape = broadcast_shape(a.shape, b.shape)
@@ -110,7 +117,7 @@ def binary(op, a, b):
 
 
 def unary(op, x):
-    x = np.ascontiguousarray(x)
+    x = _contig(x)
     out = np.empty_like(x)
     st = lib().lxo_unary(op, CODE_OF[x.dtype], x.size, _ptr(x), _ptr(out))
     if st != 0:
@@ -119,7 +126,7 @@ def unary(op, x):
 
 
 def cast(x, to_code):
-    x = np.ascontiguousarray(x)
+    x = _contig(x)
     out = np.empty(x.shape, dtype=NP_OF[to_code])
     st = lib().lxo_cast(CODE_OF[x.dtype], to_code, x.size, _ptr(x), _ptr(out))
     if st != 0:
@@ -129,7 +136,7 @@ def cast(x, to_code):
 
 def reduce(op, x, axes=None, keepdims=True):
     """ReduceSum/ReduceMean/ReduceMax; axes None or [] = all axes."""
-    x = np.ascontiguousarray(x)
+    x = _contig(x)
     ax = list(axes) if axes is not None else []
     axarr = (ctypes.c_int64 * max(1, len(ax)))(*ax) if ax else (ctypes.c_int64 * 1)(0)
     # output buffer large enough for any result shape
@@ -151,12 +158,54 @@ def reduce(op, x, axes=None, keepdims=True):
 
 
 def softmax(x, axis=-1):
-    x = np.ascontiguousarray(x)
+    x = _contig(x)
     out = np.empty_like(x)
     st = lib().lxo_softmax(CODE_OF[x.dtype], x.ndim, _dims(x.shape), _ptr(x), axis, _ptr(out))
     if st != 0:
         raise OracleError(st)
     return out
+
+
+def _mm2d(x, y):
+    """MatMul2D (TensorOps.cs:356-407): the serial loop of MathOps.mm_unsafe_vectorized."""
+    if x.shape[1] != y.shape[0]:
+        raise OracleError(ERR_INVALID_ARGUMENT, "columns != rows")
+    x = _contig(x)
+    y = _contig(y)
+    out = np.empty((x.shape[0], y.shape[1]), dtype=x.dtype)
+    st = lib().lxo_matmul2d(CODE_OF[x.dtype], x.shape[0], x.shape[1], y.shape[1], _ptr(x), _ptr(y), _ptr(out))
+    if st != 0:
+        raise OracleError(st)
+    return out
+
+
+def matmul(x, y):
+    """Tensor<T>.MatMul (TensorOps.cs:600-705): 2-D, batch-broadcast, rank-1 cases."""
+    x, y = np.asarray(x), np.asarray(y)
+    if x.dtype != y.dtype or x.dtype not in (np.float32, np.float64, np.int32):
+        raise OracleError(ERR_NOT_SUPPORTED)
+    if x.ndim == 0 or y.ndim == 0:
+        raise OracleError(ERR_INVALID_ARGUMENT, "rank 0")
+    if x.ndim == 2 and y.ndim == 2:
+        return _mm2d(x, y)
+    if x.ndim >= 2 and y.ndim >= 2:
+        if x.shape[-1] != y.shape[-2]:
+            raise OracleError(ERR_INVALID_ARGUMENT, "columns != rows")
+        bd = broadcast_shape(x.shape[:-2], y.shape[:-2])
+        if bd is None:
+            raise OracleError(ERR_INVALID_ARGUMENT, "batch shapes")
+        bx = np.broadcast_to(x, bd + x.shape[-2:])
+        by = np.broadcast_to(y, bd + y.shape[-2:])
+        out = np.empty(bd + (x.shape[-2], y.shape[-1]), dtype=x.dtype)
+        for idx in np.ndindex(*bd):
+            out[idx] = _mm2d(bx[idx], by[idx])
+        return out
+    if x.ndim >= 2 or y.ndim >= 2:
+        s = broadcast_shape(x.shape, y.shape)
+        if s is None:
+            raise OracleError(ERR_INVALID_ARGUMENT, "shapes")
+        return matmul(np.broadcast_to(x, s), np.broadcast_to(y, s))
+    return _mm2d(x.reshape(1, -1), y.reshape(-1, 1)).reshape(1)
 
 
 def erf_f32(v):

@@ -1,0 +1,114 @@
+"""GPU parity of MatMul (lx_MatMul: fp32 / fp64 MFMA, exact int32) against the
+oracle's restatement of Tensor<T>.MatMul (TensorOps.cs:356-705, serial inner
+loop of MathOps.mm_unsafe_vectorized).
+
+Bars: Int32 bit-exact (wrapping).  Float / Double: the sums run in another
+order than the reference's serial loop, so |gpu - ref| <= 1e-5 * sum_j |a_ij b_jk|
+(float) and 1e-13 * sum_j |a_ij b_jk| (double), the reduction bar applied to
+each dot product."""
+import numpy as np
+import pytest
+
+from onnx_amd import DeviceTensor, HipExecutionProvider as HIP, OpStatus
+from onnx_amd import _lib as L
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a):
+    return DeviceTensor.from_numpy(np.asarray(a))
+
+
+def mm(a, b):
+    r = HIP.MatMul(dev(a), dev(b))
+    assert r.Status == OpStatus.Success, r.Message
+    return r.Outputs[0].to_numpy()
+
+
+def check_float(a, b, tol):
+    got = mm(a, b)
+    ref = O.matmul(a, b)
+    assert got.shape == ref.shape and got.dtype == ref.dtype
+    # sum_j |a_ij b_jk| under the reference's shape rules (the oracle's float64 MatMul of |a|, |b|)
+    mag = O.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64))
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    assert np.all(err <= tol * mag + 1e-30), float((err / (mag + 1e-30)).max())
+
+
+def test_reference_kats(hip):
+    """MathTests.cs:82-97 and test_backend.py:949-988 shapes."""
+    ones = lambda *s: np.ones(s, np.int32)  # noqa: E731
+    for a, b, shape in [((1, 1, 5, 6), (3, 6, 7), (1, 3, 5, 7)), ((2, 3, 5, 6), (3, 6, 7), (2, 3, 5, 7)),
+                        ((4, 1, 5, 6), (4, 2, 6, 7), (4, 2, 5, 7))]:
+        c = mm(ones(*a), ones(*b))
+        assert c.shape == shape and np.all(c == 6)
+    a = np.arange(16, dtype=np.int32).reshape(2, 2, 4)
+    b = np.arange(16, dtype=np.int32).reshape(2, 4, 2)
+    assert mm(a, b)[0, 1, 1] == 98
+    f = mm(np.ones((1, 1, 5, 6), np.float32), np.ones((3, 6, 7), np.float32))
+    assert f.shape == (1, 3, 5, 7) and np.all(f == 6)
+
+
+@pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 4), (4, 3)), ((2, 3, 4), (2, 4, 3)),
+                                   ((1, 2, 3, 4), (1, 2, 4, 3)), ((127, 65), (65, 129)), ((129, 33), (33, 130)),
+                                   ((64, 7), (7, 9)), ((2, 1, 33, 40), (3, 40, 17)), ((1, 1000), (1000, 1)),
+                                   ((300, 300), (300, 300))])
+def test_float_shapes(hip, sa, sb):
+    rng = np.random.default_rng(50)
+    check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
+
+
+def test_float_bert_sizes(hip):
+    rng = np.random.default_rng(51)
+    x = rng.standard_normal((8, 512, 768)).astype(np.float32)
+    w = (rng.standard_normal((768, 768)) * 0.03).astype(np.float32)
+    check_float(x, w, 1e-5)
+    q = rng.standard_normal((2, 12, 512, 64)).astype(np.float32)
+    k = rng.standard_normal((2, 12, 64, 512)).astype(np.float32)
+    check_float(q, k, 1e-5)
+
+
+@pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 70, 33), (33, 65)), ((2, 1, 40, 17), (3, 17, 66))])
+def test_double(hip, sa, sb):
+    rng = np.random.default_rng(52)
+    check_float(rng.standard_normal(sa), rng.standard_normal(sb), 1e-13)
+
+
+@pytest.mark.parametrize("sa,sb", [((5, 9), (9, 4)), ((3, 70, 33), (33, 65)), ((2, 1, 17, 40), (3, 40, 17))])
+def test_int32_wraps(hip, sa, sb):
+    rng = np.random.default_rng(53)
+    a = rng.integers(-2**31, 2**31, sa, dtype=np.int64).astype(np.int32)
+    b = rng.integers(-2**31, 2**31, sb, dtype=np.int64).astype(np.int32)
+    got = mm(a, b)
+    assert np.array_equal(got, O.matmul(a, b))
+
+
+def test_rank1_and_broadcast_rules(hip):
+    v = np.arange(5, dtype=np.float32)
+    c = mm(v, v)
+    assert c.shape == (1,) and c[0] == 30.0
+    rng = np.random.default_rng(54)
+    m = rng.standard_normal((4, 4)).astype(np.float32)
+    w = rng.standard_normal(4).astype(np.float32)
+    check_float(m, w, 1e-5)   # w broadcast element-wise to [4,4] first, as the reference does
+    check_float(w, m, 1e-5)
+
+
+def test_errors(hip):
+    r = HIP.MatMul(dev(np.ones((2, 3), np.float32)), dev(np.ones((4, 2), np.float32)))
+    assert r.Code == L.ERR_INVALID_ARGUMENT
+    assert r.Message == ("The number of columns in the first matrix (3) is not equal to the number of rows in the "
+                         "second matrix (4).")
+    r = HIP.MatMul(dev(np.ones((3, 4), np.float32)), dev(np.ones(4, np.float32)))
+    assert r.Code == L.ERR_INVALID_ARGUMENT   # [3,4] x [3,4] after the element-wise broadcast
+    r = HIP.MatMul(dev(np.ones((2, 2), np.float32)), dev(np.ones((2, 2), np.int32)))
+    assert r.Code == L.ERR_WRONG_INPUT_TYPE
+    assert r.Message == ("Unable to cast object of type 'Lokad.Onnx.DenseTensor`1[System.Int32]' to type "
+                         "'Lokad.Onnx.Tensor`1[System.Single]'.")
+    r = HIP.MatMul(dev(np.ones((2, 2), np.int64)), dev(np.ones((2, 2), np.int64)))
+    assert r.Code == L.ERR_INPUT_TYPE_NOT_SUPPORTED
+    r = HIP.MatMul(dev(np.array(1.0, np.float32)), dev(np.ones((2, 2), np.float32)))
+    assert r.Message == "The rank of each tensor in matrix multiplication must be greater than 1."
+    r = HIP.MatMul(dev(np.ones((2, 3, 4), np.float32)), dev(np.ones((5, 4, 2), np.float32)))
+    assert r.Message == "The tensor shapes are not compatible for broadcasting."

@@ -263,3 +263,65 @@ def test_composites_against_float64():
     gl = O.gelu_erf(xs)
     tg = np.array([0.5 * v * (1 + math.erf(v / math.sqrt(2))) for v in xs.astype(np.float64)])
     assert np.max(np.abs(gl - tg)) <= 1e-6
+
+
+# ---- MatMul (TensorOps.cs:356-705) ----------------------------------------------
+def test_matmul_reference_kats():
+    """MathTests.cs:82-97 (CanMatMul) and :47-80 (CanMatMul2D)."""
+    ones = lambda *s: np.ones(s, np.int32)  # noqa: E731
+    assert O.matmul(ones(1, 1, 5, 6), ones(3, 6, 7)).shape == (1, 3, 5, 7)
+    assert O.matmul(ones(2, 3, 5, 6), ones(3, 6, 7)).shape == (2, 3, 5, 7)
+    assert O.matmul(ones(4, 1, 5, 6), ones(4, 2, 6, 7)).shape == (4, 2, 5, 7)
+    a = np.arange(16, dtype=np.int32).reshape(2, 2, 4)
+    b = np.arange(16, dtype=np.int32).reshape(2, 4, 2)
+    assert O.matmul(a, b)[0, 1, 1] == 98
+    c = O.matmul(ones(7, 4), ones(4, 3))
+    assert c.shape == (7, 3) and c.size == 21 and np.all(c == 4)
+    f = O.matmul(np.ones((1, 1, 5, 6), np.float32), np.ones((3, 6, 7), np.float32))
+    assert f.shape == (1, 3, 5, 7) and np.all(f == 6)
+
+
+def test_matmul_int32_wraps_like_unchecked_csharp():
+    rng = np.random.default_rng(40)
+    a = rng.integers(-2**31, 2**31, (5, 9), dtype=np.int64)
+    b = rng.integers(-2**31, 2**31, (9, 4), dtype=np.int64)
+    exact = [[sum(int(a[i, j]) * int(b[j, k]) for j in range(9)) for k in range(4)] for i in range(5)]
+    want = ((np.array(exact, dtype=object) + 2**31) % 2**32 - 2**31).astype(np.int64)
+    assert np.array_equal(O.matmul(a.astype(np.int32), b.astype(np.int32)).astype(np.int64), want)
+
+
+def test_matmul_float_closed_forms_and_bound():
+    rng = np.random.default_rng(41)
+    # integer-valued operands: every product and partial sum is exact in float32
+    a = rng.integers(-20, 20, (7, 33)).astype(np.float32)
+    b = rng.integers(-20, 20, (33, 5)).astype(np.float32)
+    assert np.array_equal(O.matmul(a, b), (a.astype(np.int64) @ b.astype(np.int64)).astype(np.float32))
+    # identity: x @ I == x exactly
+    x = rng.standard_normal((6, 10)).astype(np.float32)
+    assert np.array_equal(O.matmul(x, np.eye(10, dtype=np.float32)), x)
+    # random: within the serial-summation bound n*u*sum|a||b| of the float64 product
+    a = rng.standard_normal((9, 300)).astype(np.float32)
+    b = rng.standard_normal((300, 11)).astype(np.float32)
+    truth = a.astype(np.float64) @ b.astype(np.float64)
+    bound = 300 * 2.0**-24 * (np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64))
+    assert np.all(np.abs(O.matmul(a, b) - truth) <= bound)
+    d = O.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert np.allclose(d, truth, rtol=1e-12, atol=1e-12)
+
+
+def test_matmul_broadcast_cases():
+    rng = np.random.default_rng(42)
+    a = rng.integers(-5, 5, (2, 1, 3, 4)).astype(np.int32)
+    b = rng.integers(-5, 5, (5, 4, 6)).astype(np.int32)
+    assert np.array_equal(O.matmul(a, b), np.matmul(a, b))
+    # both rank 1: [1,n] x [n,1] with the leading axis removed -> shape [1]
+    v = np.arange(5, dtype=np.int32)
+    assert O.matmul(v, v).shape == (1,) and O.matmul(v, v)[0] == 30
+    # one operand of rank 1 is broadcast element-wise first (the reference's rule, not ONNX's)
+    m = rng.integers(-5, 5, (4, 4)).astype(np.int32)
+    w = rng.integers(-5, 5, 4).astype(np.int32)
+    assert np.array_equal(O.matmul(m, w), m @ np.broadcast_to(w, (4, 4)))
+    with pytest.raises(O.OracleError):
+        O.matmul(np.ones((3, 4), np.int32), np.ones(4, np.int32))   # [3,4] x [3,4]: 4 != 3
+    with pytest.raises(O.OracleError):
+        O.matmul(np.ones((2, 3), np.float32), np.ones((4, 2), np.float32))
