@@ -612,7 +612,9 @@ int lx_init(int32_t device) {
     if (device < 0 || device >= count)
         return set_err(LX_ERR_INVALID_ARGUMENT, "Device %d does not exist (%d devices).", device, count);
     HIPCHECK(hipSetDevice(device), "hipSetDevice");
-    HIPCHECK(hipStreamCreateWithFlags(&g.own_stream, hipStreamNonBlocking), "hipStreamCreate");
+    // a blocking stream: it orders with the legacy default stream, so work a caller
+    // enqueues there (torch's default stream, events around library calls) sees ours
+    HIPCHECK(hipStreamCreateWithFlags(&g.own_stream, hipStreamDefault), "hipStreamCreate");
     g.stream = g.own_stream;
     HIPCHECK(hipMalloc(&g.errs, sizeof(ErrFlags)), "hipMalloc(errors)");
     HIPCHECK(hipHostMalloc((void **)&g.errs_host, sizeof(ErrFlags), hipHostMallocDefault), "hipHostMalloc");

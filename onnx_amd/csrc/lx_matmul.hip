@@ -40,28 +40,39 @@ __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, in
 // ---------------------------------------------------------------------------
 // float: MFMA 32x32x2
 // ---------------------------------------------------------------------------
-constexpr int kFBM = 128, kFBN = 128, kFBK = 16, kFPad = 4;
 
-template <bool VEC>
+// BM x BN block tile (64 or 128 each), four waves in a 2x2 grid, each wave
+// (BM/2) x (BN/2) = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered
+// in LDS with k as the outer index (A transposed to [k][m], B as [k][n]), so the
+// lanes of a fragment read 32 consecutive floats.  Register-only loops of this
+// MFMA reach about 144 TF/s on MI355X; the 128x128 tile runs large GEMMs at
+// 127-131 TF/s.
+constexpr int kFBK = 16, kFPad = 4;
+
+template <int BM, int BN, bool VEC>
 __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A, const float *__restrict__ B,
                                                     float *__restrict__ C, MatMulArgs p) {
-    __shared__ float As[2][kFBK][kFBM + kFPad];
-    __shared__ float Bs[2][kFBK][kFBN + kFPad];
+    constexpr int MT = BM / 64, NT = BN / 64;  // MFMA tiles per wave
+    constexpr int LA = BM / 64, LB = BN / 64;  // float4 loads per thread per K step
+    constexpr int BQ = BN / 4;                 // float4 per B row
+    constexpr int BROWS = 256 / BQ;            // B rows covered per pass
+    __shared__ float As[2][kFBK][BM + kFPad];
+    __shared__ float Bs[2][kFBK][BN + kFPad];
     const int M = p.m, N = p.n, K = p.k;
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
-    const int row0 = blockIdx.y * kFBM, col0 = blockIdx.x * kFBN;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
     int64_t ao, bo;
     batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
     const float *Ab = A + ao;
     const float *Bb = B + bo;
     float *Cb = C + (p.batch_base + blockIdx.z) * (int64_t)M * N;
 
-    // global -> register staging: two A float4 (rows t/4 and t/4+64, k (t%4)*4) and
-    // two B float4 (k rows t/32 and t/32+8, n (t%32)*4)
-    float4 ra[2], rb[2];
+    // global -> register staging one K step ahead: A float4 along k (rows t/4 + 64h),
+    // B float4 along n (k rows t/BQ + BROWS h)
+    float4 ra[LA], rb[LB];
     auto load = [&](int k0) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < LA; h++) {
             const int r = row0 + t / 4 + 64 * h, kk = k0 + (t % 4) * 4;
             if constexpr (VEC) {
                 ra[h] = (r < M && kk < K) ? *reinterpret_cast<const float4 *>(Ab + (int64_t)r * K + kk)
@@ -72,7 +83,10 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
                 for (int e = 0; e < 4; e++) v[e] = (r < M && kk + e < K) ? Ab[(int64_t)r * K + kk + e] : 0.f;
                 ra[h] = make_float4(v[0], v[1], v[2], v[3]);
             }
-            const int kb = k0 + t / 32 + 8 * h, c = col0 + (t % 32) * 4;
+        }
+#pragma unroll
+        for (int h = 0; h < LB; h++) {
+            const int kb = k0 + t / BQ + BROWS * h, c = col0 + (t % BQ) * 4;
             if constexpr (VEC) {
                 rb[h] = (kb < K && c < N) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)kb * N + c)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -86,22 +100,24 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
     };
     auto store = [&](int buf) {
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
+        for (int h = 0; h < LA; h++) {
             const int r = t / 4 + 64 * h, kk = (t % 4) * 4;
             As[buf][kk + 0][r] = ra[h].x;
             As[buf][kk + 1][r] = ra[h].y;
             As[buf][kk + 2][r] = ra[h].z;
             As[buf][kk + 3][r] = ra[h].w;
-            *reinterpret_cast<float4 *>(&Bs[buf][t / 32 + 8 * h][(t % 32) * 4]) = rb[h];
         }
+#pragma unroll
+        for (int h = 0; h < LB; h++)
+            *reinterpret_cast<float4 *>(&Bs[buf][t / BQ + BROWS * h][(t % BQ) * 4]) = rb[h];
     };
 
-    const int wr = (w >> 1) * 64, wc = (w & 1) * 64;  // this wave's 64x64 sub-tile
-    v16f acc[2][2];
+    const int wr = (w >> 1) * (BM / 2), wc = (w & 1) * (BN / 2);  // this wave's sub-tile
+    v16f acc[MT][NT];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
@@ -115,23 +131,25 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
 #pragma unroll
         for (int kk = 0; kk < kFBK; kk += 2) {
             const int kr = kk + l / 32;
-            float a0 = As[buf][kr][wr + (l % 32)];
-            float a1 = As[buf][kr][wr + 32 + (l % 32)];
-            float b0 = Bs[buf][kr][wc + (l % 32)];
-            float b1 = Bs[buf][kr][wc + 32 + (l % 32)];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
+            float a[MT], b[NT];
+#pragma unroll
+            for (int i = 0; i < MT; i++) a[i] = As[buf][kr][wr + 32 * i + (l % 32)];
+#pragma unroll
+            for (int j = 0; j < NT; j++) b[j] = Bs[buf][kr][wc + 32 * j + (l % 32)];
+#pragma unroll
+            for (int i = 0; i < MT; i++)
+#pragma unroll
+                for (int j = 0; j < NT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) store(buf ^ 1);
         __syncthreads();
         buf ^= 1;
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NT; j++) {
             const int c = col0 + wc + 32 * j + (l % 32);
             if (c >= N) continue;
 #pragma unroll
@@ -140,6 +158,13 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
                 if (row < M) Cb[(int64_t)row * N + c] = acc[i][j][r];
             }
         }
+}
+
+template <int BM, int BN>
+static void launch_f32(const float *a, const float *b, float *c, const MatMulArgs &p, bool vec, hipStream_t s) {
+    dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
+    if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, true>), g, dim3(256), 0, s, a, b, c, p);
+    else hipLaunchKernelGGL((k_matmul_f32<BM, BN, false>), g, dim3(256), 0, s, a, b, c, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -288,14 +313,17 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
     }
     const MatMulArgs &p = p0;
     if (dtype == kFloat) {
-        dim3 g((p.n + kFBN - 1) / kFBN, (p.m + kFBM - 1) / kFBM, (unsigned)p.batch);
-        const bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
-        bool strides_ok = true;
-        for (int d = 0; d < p.nbatch; d++) strides_ok = strides_ok && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
-        if (vec && strides_ok)
-            hipLaunchKernelGGL((k_matmul_f32<true>), g, dim3(256), 0, s, (const float *)a, (const float *)b, (float *)c, p);
-        else
-            hipLaunchKernelGGL((k_matmul_f32<false>), g, dim3(256), 0, s, (const float *)a, (const float *)b, (float *)c, p);
+        bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
+        for (int d = 0; d < p.nbatch; d++) vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
+        // the largest tile that still gives each of the 256 CUs two or more blocks (a lone block
+        // per CU leaves its barrier and load latencies unhidden), else the smallest tile
+        auto tiles = [&](int bm, int bn) { return (int64_t)((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * p.batch; };
+        const float *fa = (const float *)a, *fb = (const float *)b;
+        float *fc = (float *)c;
+        if (tiles(128, 128) >= 512) launch_f32<128, 128>(fa, fb, fc, p, vec, s);
+        else if (p.m >= p.n && tiles(128, 64) >= 512) launch_f32<128, 64>(fa, fb, fc, p, vec, s);
+        else if (p.m < p.n && tiles(64, 128) >= 512) launch_f32<64, 128>(fa, fb, fc, p, vec, s);
+        else launch_f32<64, 64>(fa, fb, fc, p, vec, s);
     } else if (dtype == kDouble) {
         dim3 g((p.n + kDBN - 1) / kDBN, (p.m + kDBM - 1) / kDBM, (unsigned)p.batch);
         hipLaunchKernelGGL(k_matmul_f64, g, dim3(256), 0, s, (const double *)a, (const double *)b, (double *)c, p);
