@@ -32,6 +32,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 PEAK_HBM_GBS = 8000.0
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 LN_SHAPE = (8, 512, 768)
 # algorithmic bytes of the fused LayerNorm: X read + Y written + gamma + beta
 LN_BYTES = 2 * 8 * 512 * 768 * 4 + 2 * 768 * 4 + 4  # 25,171,972 (X + Y + gamma + beta + eps)
@@ -303,6 +304,29 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     record("device copy 1 GiB (torch copy_, ceiling reference)", 2 * Yb.numel() * 4, Yb.numel(), e0.elapsed_time(e1) / 10)
+    del Yb, Zc
+    torch.cuda.empty_cache()
+
+    # MatMul (row f2): fp32 MFMA, compute-bound; BERT-base shapes at batch 8 x 512 tokens
+    for name, sa, sb in (("MatMul fp32 [4096,768]x[768,768] (dense)", (4096, 768), (768, 768)),
+                         ("MatMul fp32 [4096,768]x[768,3072] (FFN in)", (4096, 768), (768, 3072)),
+                         ("MatMul fp32 [4096,3072]x[3072,768] (FFN out)", (4096, 3072), (3072, 768)),
+                         ("MatMul fp32 [16,12,512,64]x[16,12,64,512] (attention scores)", (16, 12, 512, 64),
+                          (16, 12, 64, 512)),
+                         ("MatMul fp32 [4096,4096]x[4096,4096]", (4096, 4096), (4096, 4096))):
+        Am = torch.randn(*sa, device=dev, generator=gen)
+        Bm = torch.randn(*sb, device=dev, generator=gen)
+        Cm = torch.empty(*(sa[:-1] + sb[-1:]), device=dev)
+        wAm, wBm, wCm = wrap(Am), wrap(Bm), wrap(Cm)
+        flops = 2.0 * (Am.numel() // sa[-1]) * sa[-1] * sb[-1]
+        ms = graph_time(torch, lambda i: HIP.MatMul(wAm, wBm, out=wCm), max(4, steps // 8), warmup, set_stream, reps=5)
+        tf = flops / (ms * 1e-3) / 1e12
+        d = {"op": name, "flops": flops, "us": round(ms * 1e3, 3), "TFLOP/s": round(tf, 2),
+             "frac_of_peak": round(tf / PEAK_FP32_MFMA_TFLOPS, 4), "bound": "mfma"}
+        log(json.dumps(d))
+        res.append(d)
+        del Am, Bm, Cm, wAm, wBm, wCm
+    torch.cuda.empty_cache()
     return res
 
 
