@@ -307,6 +307,42 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     del Yb, Zc
     torch.cuda.empty_cache()
 
+    # Data movement (row f3): HBM-bound; every element read once and written once (algorithmic bytes
+    # = input bytes moved + output bytes + index bytes); rotating sets of > 256 MB keep the L2 and the
+    # MALL cold
+    def movement(name, in_shape, make_out, fn, sets=12):
+        xs = [torch.randn(*in_shape, device=dev, generator=gen) for _ in range(sets)]
+        ys = [make_out() for _ in range(sets)]
+        wx, wy = [wrap(t) for t in xs], [wrap(t) for t in ys]
+        out_bytes = ys[0].numel() * ys[0].element_size()  # the elements read equal the elements written
+        run(name, 2 * out_bytes, ys[0].numel(), lambda i: fn(wx[i % sets], wy[i % sets]), sets)
+        del xs, ys, wx, wy
+
+    movement("Transpose [8,512,12,64] perm [0,2,1,3] (attention heads)", (8, 512, 12, 64),
+             lambda: torch.empty(8, 12, 512, 64, device=dev), lambda x, y: HIP.Transpose(x, [0, 2, 1, 3], out=y))
+    movement("Transpose [8,512,12,64] perm [0,2,3,1] (keys, innermost axis moves)", (8, 512, 12, 64),
+             lambda: torch.empty(8, 12, 64, 512, device=dev), lambda x, y: HIP.Transpose(x, [0, 2, 3, 1], out=y))
+    movement("Transpose [3072,768] (weight)", (3072, 768), lambda: torch.empty(768, 3072, device=dev),
+             lambda x, y: HIP.Transpose(x, None, out=y), sets=40)
+    movement("Slice [8,512,2304] -> [8,512,768] (QKV split)", (8, 512, 2304),
+             lambda: torch.empty(8, 512, 768, device=dev),
+             lambda x, y: HIP.Slice(x, [768], [1536], [-1], None, out=y), sets=8)
+    cat_in = [[wrap(torch.randn(8, 512, 768, device=dev, generator=gen)) for _ in range(3)] for _ in range(8)]
+    cat_out = [wrap(torch.empty(8, 512, 2304, device=dev)) for _ in range(8)]
+    run("Concat 3 x [8,512,768] axis -1", 2 * 8 * 512 * 2304 * 4, 8 * 512 * 2304,
+        lambda i: HIP.Concat(cat_in[i % 8], -1, out=cat_out[i % 8]), 8)
+    del cat_in, cat_out
+    table = wrap(torch.randn(30522, 768, device=dev, generator=gen))
+    ids = [wrap(torch.randint(0, 30522, (8, 512), device=dev, generator=gen)) for _ in range(24)]
+    emb = [wrap(torch.empty(8, 512, 768, device=dev)) for _ in range(24)]
+    # Gather checks its indices on the device and reads the verdict back, so it is not captured:
+    # host wall clock per call, the readback included
+    record("Gather [30522,768] by ids [8,512] (word embedding; per call incl. index-check readback)",
+           2 * 8 * 512 * 768 * 4 + 8 * 512 * 8, 8 * 512 * 768,
+           wall_time(torch, lambda i: HIP.Gather(table, ids[i % 24], 0, out=emb[i % 24]), steps, warmup))
+    del table, ids, emb
+    torch.cuda.empty_cache()
+
     # MatMul (row f2): fp32 MFMA, compute-bound; BERT-base shapes at batch 8 x 512 tokens
     for name, sa, sb in (("MatMul fp32 [4096,768]x[768,768] (dense)", (4096, 768), (768, 768)),
                          ("MatMul fp32 [4096,768]x[768,3072] (FFN in)", (4096, 768), (768, 3072)),

@@ -164,6 +164,21 @@ int lx_Softmax(const lx_tensor *input, int32_t axis, int32_t has_axis, lx_tensor
  * for Int32 (exact, wrapping), Float (fp32 MFMA) and Double (fp64 MFMA), with the reference's batch
  * broadcast and rank-1 rules. */
 int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y);
+/* CPUExecutionProvider.Transpose (CPUExecutionProvider.cs:411-433); Tensor<T>.Transpose (TensorOps.cs:1358-1405).
+ * n_perm < 0: perm absent (reversed axes).  Rank <= 1 returns the input itself (a view, owns = 0). */
+int lx_Transpose(const lx_tensor *data, const int64_t *perm, int32_t n_perm, lx_tensor *Y);
+/* CPUExecutionProvider.Concat (CPUExecutionProvider.cs:477-501); Tensor<T>.Concat (TensorOps.cs:1446-1498).
+ * has_axis = 0: axis 0. */
+int lx_Concat(const lx_tensor *const *inputs, int32_t n, int32_t axis, int32_t has_axis, lx_tensor *Y);
+/* CPUExecutionProvider.Gather (CPUExecutionProvider.cs:516-546); Tensor<T>.Gather (TensorOps.cs:1407-1444).
+ * indices: Int32 or Int64 device tensor; negative indices count from the end of the axis once; an
+ * index still outside the axis fails like the reference's IndexOutOfRangeException. */
+int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_t axis, int32_t has_axis, lx_tensor *Y);
+/* CPUExecutionProvider.Slice (CPUExecutionProvider.cs:548-600); Tensor<T>.Slice (TensorOps.cs:1500-1531) with
+ * SliceIndex.ToSliceDef (SliceIndex.cs:271-324): starts / ends / axes / steps as host arrays (axes, steps may be
+ * NULL).  Starts and ends are clamped to [0, dim] after negative wrap-around, as the reference does. */
+int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, const int64_t *ends, int32_t n_ends,
+             const int64_t *axes, int32_t n_axes, const int64_t *steps, int32_t n_steps, lx_tensor *Y);
 
 /* ---- fused subgraphs (one kernel each; every intermediate keeps the float32
  * rounding of the separate ONNX node it replaces) ------------------------- */

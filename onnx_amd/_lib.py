@@ -93,6 +93,10 @@ SIGNATURES = {
     "lx_LayerNormDecomposed": (_c.c_int, [_T, _T, _T, _c.c_float, _T]),
     "lx_AddSoftmax": (_c.c_int, [_T, _T, _c.c_int32, _T]),
     "lx_MatMul": (_c.c_int, [_T, _T, _T]),
+    "lx_Transpose": (_c.c_int, [_T, _i64p, _c.c_int32, _T]),
+    "lx_Concat": (_c.c_int, [_c.POINTER(_T), _c.c_int32, _c.c_int32, _c.c_int32, _T]),
+    "lx_Gather": (_c.c_int, [_T, _T, _c.c_int32, _c.c_int32, _T]),
+    "lx_Slice": (_c.c_int, [_T, _i64p, _c.c_int32, _i64p, _c.c_int32, _i64p, _c.c_int32, _i64p, _c.c_int32, _T]),
     "lx_pool_trim": (_c.c_int, []),
     "lx_pool_stats": (_c.c_int, [_i64p, _i64p]),
     # graph runtime

@@ -217,6 +217,12 @@ int ensure_workspace(int64_t bytes) {
 
 // reads back the device error record (synchronises the stream)
 int read_errs(ErrFlags *out) {
+    // the device-side checks end in a host read; a stream under capture cannot wait for it
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIPCHECK(hipStreamIsCapturing(g.stream, &cs), "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+        return set_err(LX_ERR_NOT_SUPPORTED, "This operator checks its inputs on the device and reads the result "
+                                             "back; it cannot run on a stream under capture.");
     HIPCHECK(hipMemcpyAsync(g.errs_host, g.errs, sizeof(ErrFlags), hipMemcpyDeviceToHost, g.stream),
              "hipMemcpyAsync(errors)");
     HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
@@ -1196,4 +1202,282 @@ extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     st = matmul_views(A->dtype, dense_view(A), dense_view(B), Y, temps);
     for (void *t : temps) (void)pool_release(t);
     return st;
+}
+
+// ===========================================================================
+// Data movement: CPUExecutionProvider.Transpose / Concat / Gather / Slice
+// (CPUExecutionProvider.cs:411-433, 477-501, 516-546, 548-600) over
+// Tensor<T>.Transpose / Gather / Concat / Slice (TensorOps.cs:1358-1532).
+// ===========================================================================
+namespace {
+
+bool movable_dtype(int dt) { return esize(dt) != 0; }
+
+int64_t row_major_strides(int rank, const int64_t *dims, int64_t *str) {
+    int64_t s = 1;
+    for (int d = rank - 1; d >= 0; d--) {
+        str[d] = s;
+        s *= dims[d];
+    }
+    return s;
+}
+
+int view_copy(int dt, const void *src, void *dst, const ViewCopyArgs &a) {
+    int64_t total = 1;
+    for (int k = 0; k < a.rank; k++) total *= a.dims[k];
+    if (total >= (1ll << 31) * (16 / esize(dt)))
+        return set_err(LX_ERR_NOT_SUPPORTED, "Copies of more than 2^31 vectors are not supported.");
+    HIPCHECK(launch_view_copy((int)esize(dt), src, dst, a, g.stream), "view copy");
+    return LX_OK;
+}
+
+}  // namespace
+
+extern "C" int lx_Transpose(const lx_tensor *data, const int64_t *perm, int32_t n_perm, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!data) return missing_input("Transpose", "data");
+    int st;
+    if ((st = check_tensor(data, "data"))) return st;
+    if (!movable_dtype(data->dtype)) return not_supported("Transpose");
+    const int rank = data->rank;
+    int64_t p[LX_MAX_RANK];
+    if (n_perm >= 0) {
+        // validation in the reference's order, the negative entries normalised last
+        if (n_perm != rank)
+            return argument_error(("The size of the permutation array must be the rank of the tensor: " +
+                                   std::to_string(rank) + ".").c_str(), "perm");
+        for (int i = 0; i < n_perm; i++)
+            if (perm[i] >= rank)
+                return argument_error(("The permuted dimension " + std::to_string(perm[i]) +
+                                       " exceeds the number of dimensions in the tensor.").c_str(), "perm");
+        for (int i = 0; i < n_perm; i++)
+            for (int j = 0; j < i; j++)
+                if (perm[i] == perm[j]) return argument_error("The permutation array has a repeated dimension.", "perm");
+        for (int i = 0; i < n_perm; i++) {
+            p[i] = perm[i] >= 0 ? perm[i] : rank + perm[i];
+            if (p[i] < 0) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+        }
+        // a negative entry equal to a positive one after normalisation would write one
+        // output axis twice; the device path refuses it
+        for (int i = 0; i < n_perm; i++)
+            for (int j = 0; j < i; j++)
+                if (p[i] == p[j]) return argument_error("The permutation array has a repeated dimension.", "perm");
+    } else {
+        for (int i = 0; i < rank; i++) p[i] = rank - 1 - i;
+    }
+    if (rank <= 1) {  // the reference returns the input tensor itself
+        if (Y && Y->data) {
+            if ((st = prepare_output(Y, data->dtype, rank, data->dims))) return st;
+            const int64_t bytes = numel(data) * esize(data->dtype);
+            if (bytes) HIPCHECK(hipMemcpyAsync(Y->data, data->data, bytes, hipMemcpyDeviceToDevice, g.stream), "Transpose");
+            return LX_OK;
+        }
+        if (!Y) return set_err(LX_ERR_INVALID_ARGUMENT, "The output tensor handle is null.");
+        *Y = *data;
+        Y->owns = 0;
+        return LX_OK;
+    }
+    int64_t od[LX_MAX_RANK], in_str[LX_MAX_RANK];
+    row_major_strides(rank, data->dims, in_str);
+    for (int i = 0; i < rank; i++) od[i] = data->dims[p[i]];
+    if ((st = prepare_output(Y, data->dtype, rank, od))) return st;
+    ViewCopyArgs a;
+    memset(&a, 0, sizeof a);
+    a.rank = rank;
+    int64_t out_str[LX_MAX_RANK];
+    row_major_strides(rank, od, out_str);
+    for (int i = 0; i < rank; i++) {
+        a.dims[i] = od[i];
+        a.src_str[i] = in_str[p[i]];
+        a.dst_str[i] = out_str[i];
+    }
+    return view_copy(data->dtype, data->data, Y->data, a);
+}
+
+extern "C" int lx_Concat(const lx_tensor *const *inputs, int32_t n, int32_t axis, int32_t has_axis, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!inputs || n < 0) return missing_input("Concat", "inputs");
+    int st;
+    for (int i = 0; i < n; i++) {
+        if (!inputs[i]) return missing_input("Concat", "inputs");
+        if ((st = check_tensor(inputs[i], "inputs"))) return st;
+    }
+    if (n > 0) {
+        for (int i = 1; i < n; i++)
+            if (inputs[i]->dtype != inputs[0]->dtype)  // OpResult.WrongInputType naming inputs[0] (CPUExecutionProvider.cs:481)
+                return set_err(LX_ERR_WRONG_INPUT_TYPE,
+                               "The input tensor  for parameter inputs has type %s but is required to be %s. All tensors "
+                               "in a concat operation must have the same type.",
+                               dtype_name(inputs[0]->dtype), dtype_name(inputs[0]->dtype));
+        if (!movable_dtype(inputs[0]->dtype)) return type_not_supported("Concat", "inputs", inputs[0]);
+    }
+    const int ax0 = has_axis ? axis : 0;
+    // Tensor<T>.Concat(Tensor<T>[], axis) (TensorOps.cs:1487-1498)
+    if (n < 2) return argument_error("At least two tensors must be specified for the concat operation.", "inputs");
+    const int rank = inputs[0]->rank;
+    for (int i = 1; i < n; i++)
+        if (inputs[i]->rank != rank)
+            return argument_error("Each input tensor in a concat operation must be of the same rank.", "inputs");
+    for (int i = 1; i < n; i++)
+        for (int d = 0; d < rank; d++)
+            if (d != ax0 && inputs[i]->dims[d] != inputs[0]->dims[d])
+                return argument_error("The dimensions of each tensor in a concat operation must be the same, with the "
+                                      "exception of the axis dimension.", "inputs");
+    const int ax = ax0 >= 0 ? ax0 : rank + ax0;  // the pairwise Concat normalises (TensorOps.cs:1454)
+    if (ax < 0 || ax >= rank) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+    int64_t od[LX_MAX_RANK];
+    for (int d = 0; d < rank; d++) od[d] = inputs[0]->dims[d];
+    od[ax] = 0;
+    for (int i = 0; i < n; i++) od[ax] += inputs[i]->dims[ax];
+    if ((st = prepare_output(Y, inputs[0]->dtype, rank, od))) return st;
+    // input i is a [outer, dims_i[ax] * inner] block at column off_i * inner of the [outer, total] output
+    int64_t outer = 1, inner = 1;
+    for (int d = 0; d < ax; d++) outer *= od[d];
+    for (int d = ax + 1; d < rank; d++) inner *= od[d];
+    std::vector<ConcatPart> parts;
+    int64_t off = 0;
+    for (int i = 0; i < n; i++) {
+        const int64_t len = inputs[i]->dims[ax] * inner;
+        if (outer * len >= (1ll << 31))
+            return set_err(LX_ERR_NOT_SUPPORTED, "Concat inputs of 2^31 elements or more are not supported.");
+        parts.push_back({inputs[i]->data, len, off});
+        off += len;
+    }
+    if (outer * off == 0) return LX_OK;
+    HIPCHECK(launch_concat((int)esize(inputs[0]->dtype), Y->data, outer, off, parts.data(), n, g.stream), "Concat");
+    return LX_OK;
+}
+
+extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_t axis, int32_t has_axis,
+                         lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!data) return missing_input("Gather", "data");
+    if (!indices) return missing_input("Gather", "indices");
+    int st;
+    if ((st = check_tensor(data, "data")) || (st = check_tensor(indices, "indices"))) return st;
+    if (indices->rank > data->rank)
+        return set_err(LX_ERR_WRONG_INPUT_SHAPE,
+                       "The input tensor  for parameter indices has shape %s but is required to have rank %d.",
+                       print_shape(indices).c_str(), data->rank);
+    if (indices->dtype != LX_INT32 && indices->dtype != LX_INT64)
+        return set_err(LX_ERR_WRONG_INPUT_TYPE, "Unable to cast object of type 'Lokad.Onnx.DenseTensor`1[%s]' to type "
+                                                "'Lokad.Onnx.Tensor`1[System.Int32]'.",
+                       net_type(indices->dtype));
+    if (!movable_dtype(data->dtype)) return not_supported("Gather");
+    if (data->rank == 0) return argument_error("Cannot gather from a tensor of rank 0.", "data");
+    const int rank = data->rank;
+    int ax = has_axis ? (axis >= 0 ? axis : rank + axis) : 0;
+    if (ax > rank - 1)
+        return argument_error(("The specified axis " + std::to_string(axis) +
+                               " exceeds the number of dimensions in the tensor.").c_str(), "axis");
+    if (ax < 0) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+    int64_t od[LX_MAX_RANK * 2];
+    int orank = 0;
+    for (int d = 0; d < ax; d++) od[orank++] = data->dims[d];
+    for (int d = 0; d < indices->rank; d++) od[orank++] = indices->dims[d];
+    for (int d = ax + 1; d < rank; d++) od[orank++] = data->dims[d];
+    if (orank > LX_MAX_RANK) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d axes are supported.", LX_MAX_RANK);
+    if ((st = prepare_output(Y, data->dtype, orank, od))) return st;
+    int64_t outer = 1, inner = 1;
+    for (int d = 0; d < ax; d++) outer *= data->dims[d];
+    for (int d = ax + 1; d < rank; d++) inner *= data->dims[d];
+    const int64_t nidx = numel(indices);
+    if (outer * nidx * inner == 0) return LX_OK;
+    if (outer * nidx * inner >= (1ll << 31))
+        return set_err(LX_ERR_NOT_SUPPORTED, "Gathers of 2^31 elements or more are not supported.");
+    // Int64 indices: ConvertToInt32 (ITensor.cs:172-183) throws on values outside int32; an index
+    // that large is outside the axis anyway, so the range check below reports it
+    HIPCHECK(launch_reset_errs(g.errs, g.stream), "Gather");
+    HIPCHECK(launch_gather((int)esize(data->dtype), indices->dtype, data->data, indices->data, Y->data, outer, nidx,
+                           inner, data->dims[ax], g.errs, g.stream),
+             "Gather");
+    ErrFlags ef;
+    if ((st = read_errs(&ef))) return st;
+    if (ef.first_ovf != ~0ull) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+    return LX_OK;
+}
+
+extern "C" int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, const int64_t *ends,
+                        int32_t n_ends, const int64_t *axes, int32_t n_axes, const int64_t *steps, int32_t n_steps,
+                        lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!data) return missing_input("Slice", "data");
+    if (!starts || n_starts < 0) return missing_input("Slice", "starts");
+    if (!ends || n_ends < 0) return missing_input("Slice", "ends");
+    int st;
+    if ((st = check_tensor(data, "data"))) return st;
+    // CPUExecutionProvider.Slice checks (CPUExecutionProvider.cs:554-560); the rank-1 checks of the
+    // starts / ends / axes / steps tensors are made by the caller that holds them as tensors
+    auto shape_err = [&](const char *param, const std::string &shape, const char *msg) {
+        return set_err(LX_ERR_WRONG_INPUT_SHAPE, "The input tensor  for parameter %s has shape %s. %s.", param,
+                       shape.c_str(), msg);
+    };
+    const std::string sshape = "[" + std::to_string(n_starts) + "]", eshape = "[" + std::to_string(n_ends) + "]";
+    if (data->rank == 0) return shape_err("data", print_shape(data), "Cannot slice a tensor of rank 0");
+    if (n_starts > data->rank)
+        return shape_err("starts", sshape,
+                         "The length of the starts tensor must be less-than or equal to the rank of the data tensor.");
+    if (n_starts != n_ends) return shape_err("ends", eshape, "The ends tensor must be the same length as the start tensor.");
+    if (axes && n_axes != n_starts)
+        return shape_err("axes", "[" + std::to_string(n_axes) + "]",
+                         "The axes tensor must be a rank 1 tensor with the same length as the start tensor.");
+    if (steps && n_steps != n_starts)
+        return shape_err("steps", "[" + std::to_string(n_steps) + "]",
+                         "The steps tensor must be a rank 1 tensor with the same length as the start tensor.");
+    for (int i = 0; i < n_starts; i++) {
+        const int64_t vals[4] = {starts[i], ends[i], axes ? axes[i] : 0, steps ? steps[i] : 1};
+        for (int64_t v : vals)
+            if (v < INT32_MIN || v > INT32_MAX)
+                return set_err(LX_ERR_OVERFLOW, "Value was either too large or too small for an Int32.");
+    }
+    // Tensor<T>.Slice (TensorOps.cs:1500-1531) + SliceIndex.ToSliceDef (SliceIndex.cs:271-324)
+    const int rank = data->rank;
+    int64_t sstart[LX_MAX_RANK], sstep[LX_MAX_RANK], scount[LX_MAX_RANK];
+    for (int d = 0; d < rank; d++) {
+        sstart[d] = 0;
+        sstep[d] = 1;
+        scount[d] = data->dims[d];
+    }
+    int64_t ax[LX_MAX_RANK];
+    for (int i = 0; i < n_starts; i++) {
+        ax[i] = axes ? (axes[i] >= 0 ? axes[i] : rank + axes[i]) : i;
+        if (ax[i] < 0 || ax[i] >= rank) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+    }
+    for (int d = 0; d < rank; d++) {
+        int i = -1;  // axes.IndexOf(d): the first occurrence
+        for (int k = 0; k < n_starts; k++)
+            if (ax[k] == d) { i = k; break; }
+        if (i < 0) continue;
+        const int64_t dim = data->dims[d];
+        auto clampn = [&](int64_t v) {
+            v = v >= 0 ? v : dim + v;
+            return v < 0 ? 0 : (v > dim ? dim : v);
+        };
+        int64_t start = clampn(starts[i]), stop = clampn(ends[i]);
+        const int64_t step = steps ? steps[i] : 1;
+        int64_t count = 0;
+        if (step > 0) {
+            if (start < dim && start < stop) count = (stop - start + step - 1) / step;
+        } else if (step < 0) {
+            if (start >= dim) start = dim - 1;
+            if (start > stop) count = (start - stop + (-step) - 1) / (-step);
+        }
+        sstart[d] = count ? start : 0;
+        sstep[d] = count ? step : 0;
+        scount[d] = count;
+    }
+    if ((st = prepare_output(Y, data->dtype, rank, scount))) return st;
+    ViewCopyArgs a;
+    memset(&a, 0, sizeof a);
+    a.rank = rank;
+    int64_t in_str[LX_MAX_RANK], out_str[LX_MAX_RANK];
+    row_major_strides(rank, data->dims, in_str);
+    row_major_strides(rank, scount, out_str);
+    for (int d = 0; d < rank; d++) {
+        a.dims[d] = scount[d];
+        a.src_str[d] = in_str[d] * sstep[d];
+        a.dst_str[d] = out_str[d];
+        a.src_base += sstart[d] * in_str[d];
+    }
+    return view_copy(data->dtype, data->data, Y->data, a);
 }

@@ -369,6 +369,72 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         auto f = op == "Add" ? lx_Add : op == "Sub" ? lx_Sub : op == "Mul" ? lx_Mul : op == "Div" ? lx_Div : lx_Pow;
         return run_op([&](lx_tensor *y) { return f(T(a), T(b), y); }, outs);
     }
+    if (op == "Transpose") {  // CPU.Transpose(InputTensor(0), Ints("perm")) (Node.cs:146)
+        if ((st = X.input(n, 0, &a))) return st;
+        std::vector<int64_t> perm;
+        int r = attr_ints(n, "perm", &perm);
+        if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        if (!a) return missing_input("data");
+        if (a->t.rank <= 1 && !(r && (int)perm.size() != a->t.rank)) {  // the input tensor itself
+            lx_tensor y;
+            memset(&y, 0, sizeof y);
+            if ((st = lx_Transpose(T(a), r ? perm.data() : nullptr, r ? (int32_t)perm.size() : -1, &y))) return st;
+            outs.push_back(*a);
+            return LX_OK;
+        }
+        return run_op([&](lx_tensor *y) {
+            return lx_Transpose(T(a), r ? perm.data() : nullptr, r ? (int32_t)perm.size() : -1, y);
+        }, outs);
+    }
+    if (op == "Concat") {  // CPU.Concat(graph.GetInputTensors(Inputs), RequiredInt("axis")) (Node.cs:150)
+        std::vector<const lx_tensor *> ins;
+        for (size_t k = 0; k < n.in.size(); k++) {
+            Value *v;
+            if ((st = X.input(n, k, &v))) return st;
+            ins.push_back(T(v));
+        }
+        int32_t axis;
+        int r = attr_int(n, "axis", &axis);
+        if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        if (r == 0) return failure("The Int attribute axis is required but was not found.");
+        return run_op([&](lx_tensor *y) { return lx_Concat(ins.data(), (int32_t)ins.size(), axis, 1, y); }, outs);
+    }
+    if (op == "Gather") {  // CPU.Gather(InputTensor(0), InputTensor(1), Int("axis")) (Node.cs:154)
+        if ((st = in2())) return st;
+        int32_t axis = 0;
+        int r = attr_int(n, "axis", &axis);
+        if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        return run_op([&](lx_tensor *y) { return lx_Gather(T(a), T(b), axis, r, y); }, outs);
+    }
+    if (op == "Slice") {  // CPU.Slice(InputTensor(0..4)) (Node.cs:156; CPUExecutionProvider.cs:548-600)
+        Value *in[5];
+        for (int k = 0; k < 5; k++)
+            if ((st = X.input(n, (size_t)k, &in[k]))) return st;
+        if (!in[0]) return missing_input("data");
+        if (!in[1]) return missing_input("starts");
+        if (!in[2]) return missing_input("ends");
+        auto shape_err = [&](const char *param, int idx, const char *msg) {
+            return fail(LX_ERR_WRONG_INPUT_SHAPE, fmt("The input tensor %s for parameter %s has shape %s. %s.",
+                                                      n.in[idx].c_str(), param, print_shape(in[idx]->t).c_str(), msg));
+        };
+        if (in[0]->t.rank == 0) return shape_err("data", 0, "Cannot slice a tensor of rank 0");
+        if (in[1]->t.rank != 1) return shape_err("starts", 1, "The rank of the starts tensor must be 1");
+        if (in[2]->t.rank != 1) return shape_err("ends", 2, "The rank of the ends tensor must be 1");
+        if (in[3] && in[3]->t.rank != 1)
+            return shape_err("axes", 3, "The axes tensor must be a rank 1 tensor with the same length as the start tensor.");
+        if (in[4] && in[4]->t.rank != 1)
+            return shape_err("steps", 4, "The steps tensor must be a rank 1 tensor with the same length as the start tensor.");
+        std::vector<int64_t> v[5];
+        for (int k = 1; k < 5; k++) {
+            if (in[k] && (st = host_ints(*in[k], &v[k]))) return st;
+            v[k].reserve(1);  // a valid pointer for empty lists
+        }
+        return run_op([&](lx_tensor *y) {
+            return lx_Slice(T(in[0]), v[1].data(), (int32_t)v[1].size(), v[2].data(), (int32_t)v[2].size(),
+                            in[3] ? v[3].data() : nullptr, (int32_t)v[3].size(), in[4] ? v[4].data() : nullptr,
+                            (int32_t)v[4].size(), y);
+        }, outs);
+    }
     if (op == "MatMul") {
         if ((st = in2())) return st;
         return run_op([&](lx_tensor *y) { return lx_MatMul(T(a), T(b), y); }, outs);

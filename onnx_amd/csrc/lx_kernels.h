@@ -112,6 +112,38 @@ struct MatMulArgs {
 };
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);
 
+// Data movement (Transpose, Slice, Concat, expand): for every index j of `dims`
+//   dst[dst_base + sum_k j_k dst_str[k]] = src[src_base + sum_k j_k src_str[k]]
+// (element strides, any sign, 0 on broadcast axes; at most 8 axes, outermost first).
+struct ViewCopyArgs {
+    int32_t rank;
+    int32_t pad;
+    int64_t dims[8];
+    int64_t src_str[8];
+    int64_t dst_str[8];
+    int64_t src_base;
+    int64_t dst_base;
+};
+hipError_t launch_view_copy(int esize, const void *src, void *dst, const ViewCopyArgs &a, hipStream_t s);
+
+// Concat of n inputs into a [outer, total] output: input i is a contiguous
+// [outer, len] block placed at column off (elements).  Each input's
+// outer * len must stay below 2^31 vectors.
+constexpr int kConcatMax = 8;
+struct ConcatPart {
+    const void *src;
+    int64_t len;
+    int64_t off;
+};
+hipError_t launch_concat(int esize, void *dst, int64_t outer, int64_t total, const ConcatPart *parts, int n,
+                         hipStream_t s);
+
+// Gather: out[o][i][r] = data[o][idx[i] (+dim if negative)][r]; an index outside
+// [-dim, dim) records its output position in errs->first_ovf and writes nothing.
+// The output must hold fewer than 2^31 vectors.
+hipError_t launch_gather(int esize, int idx_dtype, const void *data, const void *idx, void *out, int64_t outer,
+                         int64_t nidx, int64_t inner, int64_t dim, ErrFlags *errs, hipStream_t s);
+
 // y[i] = x[offset(i)] for a strided view (strides in elements, 0 on broadcast axes)
 hipError_t launch_strided_copy(int esize, const void *x, void *y, int rank, const int64_t *dims, const int64_t *strides,
                                hipStream_t s);

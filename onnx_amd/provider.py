@@ -276,6 +276,53 @@ class HipExecutionProvider:
         st = L.lib().lx_MatMul(_ptr(A), _ptr(B), ctypes.byref(y))
         return _result("MatMul", st, y, out)
 
+    @staticmethod
+    def Transpose(data, perm=None, out=None):
+        """CPUExecutionProvider.Transpose (CPUExecutionProvider.cs:411-433)."""
+        init()
+        data = _as_tensor(data)
+        parr, n = _axes_args(perm)
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_Transpose(_ptr(data), parr, n, ctypes.byref(y))
+        if st == L.OK and out is None and not y.owns:  # rank <= 1: the input itself
+            return OpResult("Transpose", OpStatus.Success, None, [DeviceTensor(y, keepalive=data)], 0)
+        return _result("Transpose", st, y, out)
+
+    @staticmethod
+    def Concat(inputs, axis=None, out=None):
+        """CPUExecutionProvider.Concat (CPUExecutionProvider.cs:477-501)."""
+        init()
+        ts = [_as_tensor(t) for t in (inputs or [])]
+        arr = (ctypes.POINTER(L.LxTensor) * max(1, len(ts)))(*[ctypes.pointer(t.h) for t in ts])
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_Concat(arr if inputs is not None else None, len(ts), 0 if axis is None else int(axis),
+                               0 if axis is None else 1, ctypes.byref(y))
+        return _result("Concat", st, y, out)
+
+    @staticmethod
+    def Gather(data, indices, axis=None, out=None):
+        """CPUExecutionProvider.Gather (CPUExecutionProvider.cs:516-546)."""
+        init()
+        data, indices = _as_tensor(data), _as_tensor(indices)
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_Gather(_ptr(data), _ptr(indices), 0 if axis is None else int(axis), 0 if axis is None else 1,
+                               ctypes.byref(y))
+        return _result("Gather", st, y, out)
+
+    @staticmethod
+    def Slice(data, starts, ends, axes=None, steps=None, out=None):
+        """CPUExecutionProvider.Slice (CPUExecutionProvider.cs:548-600); starts / ends / axes / steps as
+        integer sequences."""
+        init()
+        data = _as_tensor(data)
+        s_, ns = _axes_args(starts)
+        e_, ne = _axes_args(ends)
+        a_, na = _axes_args(axes)
+        p_, np_ = _axes_args(steps)
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_Slice(_ptr(data), s_, ns, e_, ne, a_, na, p_, np_, ctypes.byref(y))
+        return _result("Slice", st, y, out)
+
     # ---- fused subgraphs ---------------------------------------------------
     @staticmethod
     def GeluErf(X, out=None):

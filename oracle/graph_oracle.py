@@ -91,6 +91,19 @@ def run_node(node, get, opset):
         s, e = (s if s >= 0 else r + s), (e if e >= 0 else r + e)
         s, e = min(max(s, 0), r), min(max(e, 0), r)
         return [np.array(x.shape[s:e], dtype=np.int64)]
+    if op == "MatMul":
+        return [O.matmul(inp(0), inp(1))]
+    if op == "Transpose":
+        return [O.transpose(inp(0), at.get("perm"))]
+    if op == "Concat":
+        return [O.concat([get(n) for n in ins], int(at["axis"]))]
+    if op == "Gather":
+        return [O.gather(inp(0), inp(1), int(at.get("axis", 0)))]
+    if op == "Slice":
+        def ints(k):
+            v = inp(k)
+            return None if v is None else [int(t) for t in np.asarray(v).reshape(-1)]
+        return [O.slice_(inp(0), ints(1), ints(2), ints(3), ints(4))]
     raise NotImplementedError(op)
 
 

@@ -253,3 +253,83 @@ def gelu_chain_fast(x):
 def add_softmax(s, mask, axis=-1):
     """Add(S, mask) then Softmax(axis)."""
     return softmax(binary(ADD, s, mask), axis)
+
+
+# ---------------------------------------------------------------------------
+# Data movement (TensorOps.cs:1358-1531, SliceIndex.cs:271-324): numpy moves
+# the elements; the shape rules, index handling and failures are the
+# reference's.
+# ---------------------------------------------------------------------------
+def transpose(x, perm=None):
+    """Tensor<T>.Transpose (TensorOps.cs:1358-1405)."""
+    x = np.asarray(x)
+    r = x.ndim
+    if perm is not None:
+        perm = [int(p) for p in perm]
+        if len(perm) != r or any(p >= r for p in perm) or len(set(perm)) != len(perm):
+            raise OracleError(ERR_INVALID_ARGUMENT, "perm")
+        perm = [p if p >= 0 else r + p for p in perm]
+    else:
+        perm = list(range(r))[::-1]
+    if r <= 1:
+        return x
+    return np.ascontiguousarray(np.transpose(x, perm))
+
+
+def concat(xs, axis=0):
+    """Tensor<T>.Concat(Tensor<T>[], axis) (TensorOps.cs:1446-1498): the dims check uses the raw axis."""
+    xs = [np.asarray(x) for x in xs]
+    if len(xs) < 2 or any(x.ndim != xs[0].ndim for x in xs):
+        raise OracleError(ERR_INVALID_ARGUMENT, "inputs")
+    r = xs[0].ndim
+    if any(x.shape[d] != xs[0].shape[d] for x in xs for d in range(r) if d != axis):
+        raise OracleError(ERR_INVALID_ARGUMENT, "dims")
+    return np.concatenate(xs, axis if axis >= 0 else r + axis)
+
+
+def gather(data, indices, axis=None):
+    """Tensor<T>.Gather (TensorOps.cs:1407-1444): a negative index counts from the end once."""
+    data, indices = np.asarray(data), np.asarray(indices)
+    if indices.ndim > data.ndim or data.ndim == 0:
+        raise OracleError(ERR_INVALID_ARGUMENT, "rank")
+    ax = 0 if axis is None else (axis if axis >= 0 else data.ndim + axis)
+    if ax > data.ndim - 1 or ax < 0:
+        raise OracleError(ERR_INVALID_ARGUMENT, "axis")
+    dim = data.shape[ax]
+    k = indices.astype(np.int64)
+    k = np.where(k < 0, k + dim, k)
+    if np.any((k < 0) | (k >= dim)):
+        raise OracleError(ERR_INVALID_ARGUMENT, "index")
+    return np.take(data, k, axis=ax)
+
+
+def slice_(data, starts, ends, axes=None, steps=None):
+    """Tensor<T>.Slice (TensorOps.cs:1500-1531) + SliceIndex.ToSliceDef (SliceIndex.cs:271-324): starts and
+    ends wrap once when negative and clamp to [0, dim]; a negative step starts at dim-1 at most."""
+    data = np.asarray(data)
+    r = data.ndim
+    n = len(starts)
+    if r == 0 or n > r or len(ends) != n:
+        raise OracleError(ERR_INVALID_ARGUMENT, "shape")
+    ax = [int(a) if a >= 0 else r + int(a) for a in axes] if axes is not None else list(range(n))
+    st = [int(s) for s in steps] if steps is not None else [1] * n
+    out = data
+    for d in range(r):
+        if d not in ax:
+            continue
+        i = ax.index(d)
+        dim = data.shape[d]
+
+        def clamp(v):
+            v = v if v >= 0 else dim + v
+            return min(max(v, 0), dim)
+        start, stop, step = clamp(int(starts[i])), clamp(int(ends[i])), st[i]
+        idx = []
+        if step > 0 and start < dim and start < stop:
+            idx = list(range(start, stop, step))
+        elif step < 0:
+            start = min(start, dim - 1)
+            if start > stop:
+                idx = list(range(start, stop, step))
+        out = np.take(out, np.array(idx, dtype=np.int64), axis=d)
+    return np.ascontiguousarray(out)

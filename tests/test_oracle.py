@@ -325,3 +325,75 @@ def test_matmul_broadcast_cases():
         O.matmul(np.ones((3, 4), np.int32), np.ones(4, np.int32))   # [3,4] x [3,4]: 4 != 3
     with pytest.raises(O.OracleError):
         O.matmul(np.ones((2, 3), np.float32), np.ones((4, 2), np.float32))
+
+
+# ---- data movement: the reference's own cases (test_backend.py:222-248, 296-342, 379-444, 446-557;
+# ---- SliceTests.cs:6-80), expected values as those tests state them --------------------------
+def test_transpose_reference_cases():
+    import itertools
+    rng = np.random.default_rng(60)
+    x = rng.standard_normal(1000).astype(np.float32).reshape(10, 10, 10)
+    assert np.array_equal(O.transpose(x, [0, 2, 1]), np.transpose(x, (0, 2, 1)))
+    d = rng.random((2, 3, 4)).astype(np.float32)
+    assert np.array_equal(O.transpose(d), np.transpose(d))
+    for p in itertools.permutations(range(3)):
+        assert np.array_equal(O.transpose(d, p), np.transpose(d, p))
+    with pytest.raises(O.OracleError):
+        O.transpose(d, [0, 1])
+    with pytest.raises(O.OracleError):
+        O.transpose(d, [0, 0, 1])
+
+
+def test_concat_reference_cases():
+    rng = np.random.default_rng(61)
+    for axis in range(3):
+        a, b = rng.random((10, 20, 5)).astype(np.float32), rng.random((10, 20, 5)).astype(np.float32)
+        assert np.array_equal(O.concat([a, b], axis), np.concatenate((a, b), axis))
+    cases = [([1, 2], [3, 4]), ([[1, 2], [3, 4]], [[5, 6], [7, 8]]),
+             ([[[1, 2], [3, 4]], [[5, 6], [7, 8]]], [[[9, 10], [11, 12]], [[13, 14], [15, 16]]])]
+    for v in cases:
+        vals = [np.asarray(x, np.float32) for x in v]
+        for axis in range(-vals[0].ndim, vals[0].ndim):
+            assert np.array_equal(O.concat(vals, axis), np.concatenate(vals, axis))
+    with pytest.raises(O.OracleError):
+        O.concat([np.ones((2, 2), np.float32)], 0)
+
+
+def test_gather_reference_cases():
+    rng = np.random.default_rng(62)
+    x = rng.random((10, 10)).astype(np.float32)
+    want = np.stack([x[0:2], x[1:3]])
+    assert np.array_equal(O.gather(x, np.array([[0, 1], [1, 2]])), want)
+    assert np.array_equal(O.gather(x, np.array([[-10, -9], [1, -8]])), want)
+    d = rng.standard_normal((5, 4, 3, 2)).astype(np.float32)
+    assert np.array_equal(O.gather(d, np.array([0, 1, 3]), 0), np.take(d, [0, 1, 3], axis=0))
+    assert np.array_equal(O.gather(d, np.array([0, 1, 3]), 1), np.take(d, [0, 1, 3], axis=1))
+    d2 = rng.standard_normal((3, 3)).astype(np.float32)
+    assert np.array_equal(O.gather(d2, np.array([[0, 2]]), 1), np.take(d2, [[0, 2]], axis=1))
+    a = np.arange(10).astype(np.float32)
+    assert np.array_equal(O.gather(a, np.array([0, -9, -10]), 0), np.take(a, [0, -9, -10], axis=0))
+    assert np.array_equal(O.gather(a, np.array(1), 0), np.take(a, 1, axis=0))
+    # SliceTests.cs CanGather: [[1.0,1.2],[2.3,3.4],[4.5,5.7]] with [[0,1],[1,2]]
+    g = O.gather(np.array([[1.0, 1.2], [2.3, 3.4], [4.5, 5.7]]), np.array([[0, 1], [1, 2]], np.int32))
+    assert g.shape == (2, 2, 2) and g[1, 1, 1] == 5.7
+    with pytest.raises(O.OracleError):
+        O.gather(a, np.array([10]), 0)
+
+
+def test_slice_reference_cases():
+    rng = np.random.default_rng(63)
+    x = rng.random(1000).astype(np.float32).reshape(10, 10, 10)
+    assert np.array_equal(O.slice_(x, [0, 0, 0], [2, 2, 2], [0, 1, 2], [1, 1, 1]), x[0:2, 0:2, 0:2])
+    assert np.array_equal(O.slice_(x, [0, -7], [-8, 20], [0, 2]), x[0:-8, :, -7:20])
+    y = rng.standard_normal((20, 10, 5)).astype(np.float32)
+    assert np.array_equal(O.slice_(y, [0, 0], [3, 10], [0, 1], [1, 1]), y[0:3, 0:10])
+    assert np.array_equal(O.slice_(y, [0], [-1], [1], [1]), y[:, 0:-1])
+    assert np.array_equal(O.slice_(y, [1000], [1000], [1], [1]), y[:, 1000:1000])
+    assert np.array_equal(O.slice_(y, [1], [1000], [1], [1]), y[:, 1:1000])
+    assert np.array_equal(O.slice_(y, [0, 0, 3], [20, 10, 4]), y[:, :, 3:4])
+    assert np.array_equal(O.slice_(y, [0, 0, 3], [20, 10, 4], [0, 1, 2]), y[:, :, 3:4])
+    assert np.array_equal(O.slice_(y, [20, 10, 4], [0, 0, 1], [0, 1, 2], [-1, -3, -2]), y[20:0:-1, 10:0:-3, 4:1:-2])
+    # SliceTests.cs CanSlice: Arange(12).Reshape(3,4)[.., 2..4] -> [[2,3],[6,7],[10,11]]
+    t = np.arange(12, dtype=np.int32).reshape(3, 4)
+    s1 = O.slice_(t, [2], [4], [1])
+    assert s1.shape == (3, 2) and s1[2, 1] == 11 and s1[0, 0] == t[0, 2]
