@@ -138,6 +138,86 @@ def cpu_baseline_ln(target_s=10.0):
             "ms_per_step": round(sec * 1e3, 3)}
 
 
+def cpu_ops(target_s=1.0):
+    """CPU leg of --all: the oracle (C restatement of the reference's CPU algorithm, 1 thread) on a
+    bounded sample of each config op, scaled to the full op by element count.  Returns
+    {op name: (seconds for the full op, sample description)}."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(3)
+
+    def timed(fn, scale, sample):
+        fn()
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= target_s:
+                break
+        return el / n * scale, f"{sample}, {n} runs in {el:.1f} s, scaled x{scale:g}"
+
+    out = {}
+    f32 = np.float32
+    A1 = rng.standard_normal((1, 128, 384)).astype(f32)
+    B1 = rng.uniform(-0.1, 0.1, 384).astype(f32)
+    out["C1 Add bias [1,128,384]+[384]"] = timed(lambda: O.binary(O.ADD, A1, B1), 1, "full op")
+    out["C1 Mul scalar 0.125"] = timed(lambda: O.binary(O.MUL, A1, np.array(0.125, f32)), 1, "full op")
+    X = (rng.standard_normal(LN_SHAPE) * 2).astype(f32)
+    g = (1 + 0.02 * rng.standard_normal(768)).astype(f32)
+    b = (0.02 * rng.standard_normal(768)).astype(f32)
+    ln = timed(lambda: O.layernorm_decomposed(X, g, b), 1, "the 9 ops on X[8,512,768]")
+    for k in ("C2 LayerNorm fused", "C2 LayerNorm 9 separate ops",
+              "C2 LayerNorm graph executor, 9 nodes (host dispatch per execution)",
+              "C2 LayerNorm graph executor, fused to 1 node (host dispatch per execution)"):
+        out[k] = ln
+    S = (rng.standard_normal((1, 12, 512, 512)) * 3).astype(f32)
+    M = np.where(rng.uniform(size=(1, 1, 1, 512)) < 0.125, -10000.0, 0.0).astype(f32)
+    T = O.binary(O.ADD, S, M)
+    out["C3 Add mask"] = timed(lambda: O.binary(O.ADD, S, M), 16, "S[1,12,512,512] + mask[1,1,1,512]")
+    out["C3 Softmax(-1)"] = timed(lambda: O.softmax(T, -1), 16, "[1,12,512,512]")
+    out["C3 Add+Softmax fused"] = timed(lambda: O.add_softmax(S, M, -1), 16, "S[1,12,512,512] + mask, Softmax")
+    for dt in (np.int64, np.int32):
+        nm = np.dtype(dt).name
+        A4 = rng.integers(-(2**20), 2**20 + 1, (4, 1, 4096)).astype(dt)
+        B4 = rng.integers(1, 1025, (1, 256, 4096)).astype(dt)
+        smp = "A[4,1,4096] op B[1,256,4096]"
+        out[f"C4 Add {nm}"] = timed(lambda: O.binary(O.ADD, A4, B4), 16, smp)
+        out[f"C4 Mul {nm}"] = timed(lambda: O.binary(O.MUL, A4, B4), 16, smp)
+        out[f"C4 Div {nm} (eager, includes error-flag readback)"] = timed(lambda: O.binary(O.DIV, A4, B4), 16, smp)
+        if dt == np.int64:
+            Y4 = O.binary(O.ADD, A4, B4)
+            out["C4 Cast i64->f32"] = timed(lambda: O.cast(Y4, 1), 16, "[4,256,4096] int64")
+            out["C4 ReduceSum(axis=1) i64"] = timed(lambda: O.reduce(O.RSUM, Y4, [1], True), 16, "[4,256,4096] int64")
+    X5 = rng.standard_normal((1, 2048, 3072)).astype(f32)
+    out["C5 GELU chain fused"] = timed(lambda: O.gelu_erf(X5), 32, "the 5 ops on X[1,2048,3072]")
+    Yb = rng.uniform(-1, 1, (16, 4096, 256)).astype(f32)
+    out["C5 ReduceSum(axis=1)"] = timed(lambda: O.reduce(O.RSUM, Yb, [1], True), 16, "[16,4096,256]")
+    out["C5 ReduceMean(all)"] = timed(lambda: O.reduce(O.RMEAN, Yb, None, True), 16, "[16,4096,256]")
+    Am = rng.standard_normal((256, 768)).astype(f32)
+    Bm = rng.standard_normal((768, 768)).astype(f32)
+    out["MatMul fp32 [4096,768]x[768,768] (dense)"] = timed(lambda: O.matmul(Am, Bm), 16, "[256,768]x[768,768]")
+    Bf = rng.standard_normal((768, 3072)).astype(f32)
+    out["MatMul fp32 [4096,768]x[768,3072] (FFN in)"] = timed(lambda: O.matmul(Am, Bf), 16, "[256,768]x[768,3072]")
+    return out
+
+
+def attach_cpu(res, cpu):
+    """Adds the CPU leg to each --all record it covers: CPU time of the full op, its GB/s (or TFLOP/s)
+    and the GPU/CPU time ratio."""
+    for d in res:
+        c = cpu.get(d["op"])
+        if c is None:
+            continue
+        sec, sample = c
+        d["cpu_us"] = round(sec * 1e6, 1)
+        if "algorithmic_bytes" in d:
+            d["cpu_GB/s"] = round(d["algorithmic_bytes"] / sec / 1e9, 3)
+        if "flops" in d:
+            d["cpu_TFLOP/s"] = round(d["flops"] / sec / 1e12, 5)
+        d["gpu_speedup"] = round(sec * 1e6 / d["us"], 1)
+        d["cpu_sample"] = sample + " (oracle: C restatement of the reference's CPU algorithm, 1 thread)"
+
+
 def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     """Every BASELINE config op, cold-cache, graph-timed; returns a list of dicts."""
     dev = torch.device("cuda:0")
@@ -439,6 +519,11 @@ def main():
     }
     if args.all:
         res = bench_all(torch, HIP, DeviceTensor, set_stream, args.steps, args.warmup)
+        if not args.no_cpu:
+            attach_cpu(res, cpu_ops())
+            for d in res:
+                if "cpu_us" in d:
+                    log(json.dumps({k: d[k] for k in ("op", "us", "cpu_us", "gpu_speedup")}))
         os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
         with open(os.path.join(ROOT, "gpurun_out", "bench_configs.json"), "w") as f:
             json.dump(res, f, indent=1)

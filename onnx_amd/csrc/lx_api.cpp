@@ -1277,6 +1277,10 @@ extern "C" int lx_Transpose(const lx_tensor *data, const int64_t *perm, int32_t 
         Y->owns = 0;
         return LX_OK;
     }
+    // the reference's copy loop visits index [0, ..., 0] of the output even when it has no
+    // elements (TensorDimensionsIterator yields its first index unconditionally,
+    // TensorDimensionsIterator.cs:36-40) and reads element 0 of the empty input
+    if (numel(data) == 0) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
     int64_t od[LX_MAX_RANK], in_str[LX_MAX_RANK];
     row_major_strides(rank, data->dims, in_str);
     for (int i = 0; i < rank; i++) od[i] = data->dims[p[i]];
@@ -1325,6 +1329,15 @@ extern "C" int lx_Concat(const lx_tensor *const *inputs, int32_t n, int32_t axis
                                       "exception of the axis dimension.", "inputs");
     const int ax = ax0 >= 0 ? ax0 : rank + ax0;  // the pairwise Concat normalises (TensorOps.cs:1454)
     if (ax < 0 || ax >= rank) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+    // the pairwise concatenation (TensorOps.cs:1446-1480) writes index [0, ..., 0] of its output even
+    // when that output is empty (the iterator's first index); so the call fails when the first pair
+    // concatenates to nothing
+    {
+        int64_t first = inputs[0]->dims[ax] + inputs[1]->dims[ax];
+        for (int d = 0; d < rank; d++)
+            if (d != ax) first *= inputs[0]->dims[d];
+        if (first == 0) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+    }
     int64_t od[LX_MAX_RANK];
     for (int d = 0; d < rank; d++) od[d] = inputs[0]->dims[d];
     od[ax] = 0;
@@ -1382,7 +1395,9 @@ extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_
     for (int d = 0; d < ax; d++) outer *= data->dims[d];
     for (int d = ax + 1; d < rank; d++) inner *= data->dims[d];
     const int64_t nidx = numel(indices);
-    if (outer * nidx * inner == 0) return LX_OK;
+    // an empty output still has its index [0, ..., 0] visited by the reference's loop, which then
+    // reads past the empty indices, data or output (TensorOps.cs:1432-1440)
+    if (outer * nidx * inner == 0) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
     if (outer * nidx * inner >= (1ll << 31))
         return set_err(LX_ERR_NOT_SUPPORTED, "Gathers of 2^31 elements or more are not supported.");
     // Int64 indices: ConvertToInt32 (ITensor.cs:172-183) throws on values outside int32; an index

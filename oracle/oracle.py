@@ -273,6 +273,8 @@ def transpose(x, perm=None):
         perm = list(range(r))[::-1]
     if r <= 1:
         return x
+    if x.size == 0:  # the copy loop still visits index [0, ..., 0] (TensorDimensionsIterator.cs:36-40)
+        raise OracleError(ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.")
     return np.ascontiguousarray(np.transpose(x, perm))
 
 
@@ -284,7 +286,13 @@ def concat(xs, axis=0):
     r = xs[0].ndim
     if any(x.shape[d] != xs[0].shape[d] for x in xs for d in range(r) if d != axis):
         raise OracleError(ERR_INVALID_ARGUMENT, "dims")
-    return np.concatenate(xs, axis if axis >= 0 else r + axis)
+    ax = axis if axis >= 0 else r + axis
+    if ax < 0 or ax >= r:
+        raise OracleError(ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.")
+    first = (xs[0].shape[ax] + xs[1].shape[ax]) * int(np.prod([d for k, d in enumerate(xs[0].shape) if k != ax]))
+    if first == 0:  # the first pairwise concat writes index [0, ..., 0] of its empty output
+        raise OracleError(ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.")
+    return np.concatenate(xs, ax)
 
 
 def gather(data, indices, axis=None):
@@ -296,6 +304,8 @@ def gather(data, indices, axis=None):
     if ax > data.ndim - 1 or ax < 0:
         raise OracleError(ERR_INVALID_ARGUMENT, "axis")
     dim = data.shape[ax]
+    if data.size == 0 or indices.size == 0:  # an empty output: the loop still visits its index [0, ..., 0]
+        raise OracleError(ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.")
     k = indices.astype(np.int64)
     k = np.where(k < 0, k + dim, k)
     if np.any((k < 0) | (k >= dim)):

@@ -83,8 +83,10 @@ def test_transpose_rank1_and_empty(hip):
     assert bits(ok(HIP.Transpose(dev(v))), v)
     s = np.array(3.5, np.float32)
     assert bits(ok(HIP.Transpose(dev(s))), s)
-    e = np.zeros((3, 0, 2), np.float32)
-    assert ok(HIP.Transpose(dev(e), [2, 0, 1])).shape == (2, 3, 0)
+    # an empty input of rank >= 2 fails as the reference's copy loop does (it visits index [0, ..., 0])
+    r = HIP.Transpose(dev(np.zeros((3, 0, 2), np.float32)), [2, 0, 1])
+    assert r.Code == L.ERR_INVALID_ARGUMENT and r.Message == "Index was outside the bounds of the array."
+    assert ok(HIP.Transpose(dev(np.zeros((0,), np.float32)))).shape == (0,)
 
 
 def test_transpose_errors(hip):
@@ -133,6 +135,10 @@ def test_concat_errors(hip):
     assert r.Message == "Each input tensor in a concat operation must be of the same rank. (Parameter 'inputs')"
     r = HIP.Concat([a, dev(np.ones((2, 3), np.int32))], 0)
     assert r.Code == L.ERR_WRONG_INPUT_TYPE
+    z = dev(np.zeros((2, 0), np.float32))
+    r = HIP.Concat([z, z, a], 1)   # the first pair concatenates to nothing: fails as in the reference
+    assert r.Code == L.ERR_INVALID_ARGUMENT and r.Message == "Index was outside the bounds of the array."
+    assert bits(ok(HIP.Concat([z, a, z], 1)), np.ones((2, 3), np.float32))
 
 
 # ---- Gather ----------------------------------------------------------------------
@@ -179,7 +185,9 @@ def test_gather_embedding_lookup(hip):
 
 def test_gather_empty_and_errors(hip):
     a = dev(np.arange(10, dtype=np.float32))
-    assert ok(HIP.Gather(a, dev(np.zeros((0,), np.int64)), 0)).shape == (0,)
+    for d, i in ((a, np.zeros((0,), np.int64)), (dev(np.zeros((3, 0), np.float32)), np.array([1], np.int64))):
+        r = HIP.Gather(d, dev(i), 0)   # an empty output fails as in the reference's loop
+        assert r.Code == L.ERR_INVALID_ARGUMENT and r.Message == "Index was outside the bounds of the array."
     for bad in ([10], [-11], [2**40], [3, 2**31]):
         r = HIP.Gather(a, dev(np.array(bad, np.int64)), 0)
         assert r.Code == L.ERR_INVALID_ARGUMENT and r.Message == "Index was outside the bounds of the array.", bad

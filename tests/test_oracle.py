@@ -397,3 +397,24 @@ def test_slice_reference_cases():
     t = np.arange(12, dtype=np.int32).reshape(3, 4)
     s1 = O.slice_(t, [2], [4], [1])
     assert s1.shape == (3, 2) and s1[2, 1] == 11 and s1[0, 0] == t[0, 2]
+
+
+def test_movement_empty_outputs_fail_like_the_reference():
+    """TensorDimensionsIterator yields its first index [0, ..., 0] even for an empty shape
+    (TensorDimensionsIterator.cs:17-20, 36-40), so the reference's Transpose / Gather / pairwise Concat copy
+    loops touch element 0 of an empty buffer and fail with IndexOutOfRangeException; Slice returns a lazy
+    view and does not."""
+    e = np.zeros((3, 0, 2), np.float32)
+    with pytest.raises(O.OracleError, match="outside the bounds"):
+        O.transpose(e, [2, 0, 1])
+    assert O.transpose(np.zeros((0,), np.float32)).shape == (0,)  # rank <= 1: the input itself
+    with pytest.raises(O.OracleError, match="outside the bounds"):
+        O.gather(np.arange(10, dtype=np.float32), np.zeros((0,), np.int64), 0)
+    with pytest.raises(O.OracleError, match="outside the bounds"):
+        O.gather(np.zeros((3, 0), np.float32), np.array([1]), 0)
+    with pytest.raises(O.OracleError, match="outside the bounds"):
+        O.concat([np.zeros((2, 0), np.float32), np.zeros((2, 0), np.float32), np.ones((2, 3), np.float32)], 1)
+    assert O.concat([np.zeros((2, 0), np.float32), np.ones((2, 3), np.float32)], 1).shape == (2, 3)
+    with pytest.raises(O.OracleError, match="outside the bounds"):
+        O.concat([np.zeros((0, 2), np.float32), np.ones((0, 3), np.float32)], 1)
+    assert O.slice_(np.ones((4, 5), np.float32), [3], [1], [0]).shape == (0, 5)
