@@ -425,6 +425,7 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
 
     # MatMul (row f2): fp32 MFMA, compute-bound; BERT-base shapes at batch 8 x 512 tokens
     for name, sa, sb in (("MatMul fp32 [4096,768]x[768,768] (dense)", (4096, 768), (768, 768)),
+                         ("MatMul fp32 [4096,768]x[768,2304] (fused QKV projection)", (4096, 768), (768, 2304)),
                          ("MatMul fp32 [4096,768]x[768,3072] (FFN in)", (4096, 768), (768, 3072)),
                          ("MatMul fp32 [4096,3072]x[3072,768] (FFN out)", (4096, 3072), (3072, 768)),
                          ("MatMul fp32 [16,12,512,64]x[16,12,64,512] (attention scores)", (16, 12, 512, 64),

@@ -3,8 +3,9 @@
 //
 // float : v_mfma_f32_32x32x2f32 (fp32 products, fp32 accumulation -- the
 //         reference's float32 arithmetic, summed in a different order).
-//         128x128 block tile, K step 16, four waves of 64x64 (2x2 MFMA tiles),
-//         double-buffered LDS fed from registers one K step ahead.
+//         block tiles from 64x64 to 128x128 (128x96 for N = 768) chosen per
+//         shape, K step 16, four waves, double-buffered LDS fed from
+//         registers one K step ahead.
 // double: v_mfma_f64_16x16x4f64, 64x64 block tile, four waves of 32x32.
 // int32 : exact two's-complement multiply-add on the VALU (no int32 MFMA),
 //         16x16 LDS tiles.
@@ -41,21 +42,22 @@ __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, in
 // float: MFMA 32x32x2
 // ---------------------------------------------------------------------------
 
-// BM x BN block tile (64 or 128 each), four waves in a 2x2 grid, each wave
-// (BM/2) x (BN/2) = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered
-// in LDS with k as the outer index (A transposed to [k][m], B as [k][n]), so the
-// lanes of a fragment read 32 consecutive floats.  Register-only loops of this
-// MFMA reach about 144 TF/s on MI355X; the 128x128 tile runs large GEMMs at
-// 127-131 TF/s.
+// BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
+// = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered in LDS with k
+// as the outer index (A transposed to [k][m], B as [k][n]), so the lanes of a
+// fragment read 32 consecutive floats.  Register-only loops of this MFMA reach
+// about 144 TF/s on MI355X; the 128x128 tile runs large GEMMs at 127-131 TF/s.
 constexpr int kFBK = 16, kFPad = 4;
 
-template <int BM, int BN, bool VEC>
+template <int BM, int BN, int WM, int WN, bool VEC>
 __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A, const float *__restrict__ B,
                                                     float *__restrict__ C, MatMulArgs p) {
-    constexpr int MT = BM / 64, NT = BN / 64;  // MFMA tiles per wave
-    constexpr int LA = BM / 64, LB = BN / 64;  // float4 loads per thread per K step
-    constexpr int BQ = BN / 4;                 // float4 per B row
-    constexpr int BROWS = 256 / BQ;            // B rows covered per pass
+    constexpr int WTM = BM / WM, WTN = BN / WN;      // wave tile
+    constexpr int MT = WTM / 32, NT = WTN / 32;      // MFMA tiles per wave
+    static_assert(WM * WN == 4 && MT * 32 == WTM && NT * 32 == WTN, "four waves of whole 32x32 tiles");
+    constexpr int AV = BM * kFBK / 4, BV = BN * kFBK / 4;  // float4 of A and of B per K step
+    constexpr int LA = (AV + 255) / 256, LB = (BV + 255) / 256;
+    constexpr int BQ = BN / 4;                       // float4 per B row
     __shared__ float As[2][kFBK][BM + kFPad];
     __shared__ float Bs[2][kFBK][BN + kFPad];
     const int M = p.m, N = p.n, K = p.k;
@@ -67,33 +69,37 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
     const float *Bb = B + bo;
     float *Cb = C + (p.batch_base + blockIdx.z) * (int64_t)M * N;
 
-    // global -> register staging one K step ahead: A float4 along k (rows t/4 + 64h),
-    // B float4 along n (k rows t/BQ + BROWS h)
+    // global -> register staging one K step ahead: float4 e = t + 256 h of the step's
+    // A tile (row e / 4, k 4 (e % 4)) and B tile (k row e / BQ, column 4 (e % BQ))
     float4 ra[LA], rb[LB];
     auto load = [&](int k0) {
 #pragma unroll
         for (int h = 0; h < LA; h++) {
-            const int r = row0 + t / 4 + 64 * h, kk = k0 + (t % 4) * 4;
+            const int e = t + 256 * h;
+            if (AV % 256 != 0 && e >= AV) continue;
+            const int r = row0 + e / 4, kk = k0 + (e % 4) * 4;
             if constexpr (VEC) {
                 ra[h] = (r < M && kk < K) ? *reinterpret_cast<const float4 *>(Ab + (int64_t)r * K + kk)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = (r < M && kk + e < K) ? Ab[(int64_t)r * K + kk + e] : 0.f;
+                for (int q = 0; q < 4; q++) v[q] = (r < M && kk + q < K) ? Ab[(int64_t)r * K + kk + q] : 0.f;
                 ra[h] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
 #pragma unroll
         for (int h = 0; h < LB; h++) {
-            const int kb = k0 + t / BQ + BROWS * h, c = col0 + (t % BQ) * 4;
+            const int e = t + 256 * h;
+            if (BV % 256 != 0 && e >= BV) continue;
+            const int kb = k0 + e / BQ, c = col0 + (e % BQ) * 4;
             if constexpr (VEC) {
                 rb[h] = (kb < K && c < N) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)kb * N + c)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = (kb < K && c + e < N) ? Bb[(int64_t)kb * N + c + e] : 0.f;
+                for (int q = 0; q < 4; q++) v[q] = (kb < K && c + q < N) ? Bb[(int64_t)kb * N + c + q] : 0.f;
                 rb[h] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
@@ -101,18 +107,23 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
     auto store = [&](int buf) {
 #pragma unroll
         for (int h = 0; h < LA; h++) {
-            const int r = t / 4 + 64 * h, kk = (t % 4) * 4;
+            const int e = t + 256 * h;
+            if (AV % 256 != 0 && e >= AV) continue;
+            const int r = e / 4, kk = (e % 4) * 4;
             As[buf][kk + 0][r] = ra[h].x;
             As[buf][kk + 1][r] = ra[h].y;
             As[buf][kk + 2][r] = ra[h].z;
             As[buf][kk + 3][r] = ra[h].w;
         }
 #pragma unroll
-        for (int h = 0; h < LB; h++)
-            *reinterpret_cast<float4 *>(&Bs[buf][t / BQ + BROWS * h][(t % BQ) * 4]) = rb[h];
+        for (int h = 0; h < LB; h++) {
+            const int e = t + 256 * h;
+            if (BV % 256 != 0 && e >= BV) continue;
+            *reinterpret_cast<float4 *>(&Bs[buf][e / BQ][(e % BQ) * 4]) = rb[h];
+        }
     };
 
-    const int wr = (w >> 1) * (BM / 2), wc = (w & 1) * (BN / 2);  // this wave's sub-tile
+    const int wr = (w / WN) * WTM, wc = (w % WN) * WTN;  // this wave's sub-tile
     v16f acc[MT][NT];
 #pragma unroll
     for (int i = 0; i < MT; i++)
@@ -160,11 +171,11 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
         }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WM, int WN>
 static void launch_f32(const float *a, const float *b, float *c, const MatMulArgs &p, bool vec, hipStream_t s) {
     dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
-    if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, true>), g, dim3(256), 0, s, a, b, c, p);
-    else hipLaunchKernelGGL((k_matmul_f32<BM, BN, false>), g, dim3(256), 0, s, a, b, c, p);
+    if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true>), g, dim3(256), 0, s, a, b, c, p);
+    else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false>), g, dim3(256), 0, s, a, b, c, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -315,15 +326,38 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
     if (dtype == kFloat) {
         bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
         for (int d = 0; d < p.nbatch; d++) vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
-        // the largest tile that still gives each of the 256 CUs two or more blocks (a lone block
-        // per CU leaves its barrier and load latencies unhidden), else the smallest tile
-        auto tiles = [&](int bm, int bn) { return (int64_t)((p.m + bm - 1) / bm) * ((p.n + bn - 1) / bn) * p.batch; };
+        // block tile: among the tiles that give each of the 256 CUs two or more blocks (a lone block
+        // per CU leaves its barrier and load latencies unhidden: measured 93 against 104 TF/s for
+        // [4096,3072]x[3072,768]), the one whose busiest CU has the least work -- ceil(blocks / 256)
+        // blocks, each costing its area over the tile's relative efficiency; 64x64 when none does
         const float *fa = (const float *)a, *fb = (const float *)b;
         float *fc = (float *)c;
-        if (tiles(128, 128) >= 512) launch_f32<128, 128>(fa, fb, fc, p, vec, s);
-        else if (p.m >= p.n && tiles(128, 64) >= 512) launch_f32<128, 64>(fa, fb, fc, p, vec, s);
-        else if (p.m < p.n && tiles(64, 128) >= 512) launch_f32<64, 128>(fa, fb, fc, p, vec, s);
-        else launch_f32<64, 64>(fa, fb, fc, p, vec, s);
+        struct Tile {
+            int bm, bn;
+            double eff;
+        };
+        static const Tile cand[] = {{128, 128, 1.0}, {128, 96, 0.93}, {96, 128, 0.93},
+                                    {128, 64, 0.85}, {64, 128, 0.85}, {64, 64, 0.65}};
+        int best = 5;
+        double best_cost = 0;
+        for (int i = 0; i < 6; i++) {
+            const int64_t blocks =
+                (int64_t)((p.m + cand[i].bm - 1) / cand[i].bm) * ((p.n + cand[i].bn - 1) / cand[i].bn) * p.batch;
+            if (blocks < 512) continue;
+            const double cost = (double)((blocks + 255) / 256) * cand[i].bm * cand[i].bn / cand[i].eff;
+            if (best == 5 || cost < best_cost) {
+                best = i;
+                best_cost = cost;
+            }
+        }
+        switch (best) {
+        case 0: launch_f32<128, 128, 2, 2>(fa, fb, fc, p, vec, s); break;
+        case 1: launch_f32<128, 96, 4, 1>(fa, fb, fc, p, vec, s); break;
+        case 2: launch_f32<96, 128, 1, 4>(fa, fb, fc, p, vec, s); break;
+        case 3: launch_f32<128, 64, 2, 2>(fa, fb, fc, p, vec, s); break;
+        case 4: launch_f32<64, 128, 2, 2>(fa, fb, fc, p, vec, s); break;
+        default: launch_f32<64, 64, 2, 2>(fa, fb, fc, p, vec, s); break;
+        }
     } else if (dtype == kDouble) {
         dim3 g((p.n + kDBN - 1) / kDBN, (p.m + kDBM - 1) / kDBM, (unsigned)p.batch);
         hipLaunchKernelGGL(k_matmul_f64, g, dim3(256), 0, s, (const double *)a, (const double *)b, (double *)c, p);

@@ -69,6 +69,15 @@ def test_float_bert_sizes(hip):
     check_float(q, k, 1e-5)
 
 
+@pytest.mark.parametrize("sa,sb", [((4000, 100), (100, 2300)), ((4000, 99), (99, 2300)), ((1536, 72), (72, 4096)),
+                                   ((2100, 40), (40, 2300)), ((2, 1100, 40), (40, 1200)), ((4096, 24), (24, 3072))])
+def test_float_every_block_tile(hip, sa, sb):
+    """Shapes whose tile choice lands on each block tile (128x96, 96x128, 128x64, 64x64, 128x128), with ragged
+    edges and, for K = 99, the unvectorised loads."""
+    rng = np.random.default_rng(55)
+    check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
+
+
 @pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 70, 33), (33, 65)), ((2, 1, 40, 17), (3, 17, 66))])
 def test_double(hip, sa, sb):
     rng = np.random.default_rng(52)
