@@ -249,6 +249,28 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     wA, wB, wC, wD, ws8 = [wrap(t) for t in A], wrap(B), [wrap(t) for t in C], [wrap(t) for t in D], wrap(s8)
     run("C1 Add bias [1,128,384]+[384]", 394752, 49152, lambda i: HIP.Add(wA[i % n1], wB, out=wC[i % n1]), n1)
     run("C1 Mul scalar 0.125", 393220, 49152, lambda i: HIP.Mul(wC[i % n1], ws8, out=wD[i % n1]), n1)
+    # the two nodes as one elementwise-chain kernel (what the graph runtime's fusion runs)
+    run("C1 Add -> Mul as one ElementwiseChain kernel", 394756, 49152,
+        lambda i: HIP.ElementwiseChain([wA[i % n1], wB, ws8], [("Add", 1), ("Mul", 2)], out=wD[i % n1]), n1)
+    # and through the graph runtime, host dispatch per execution: 2 nodes, then fused
+    from onnx_amd.graph import ComputationalGraph
+    for fuse, label, nbytes in ((False, "2 nodes", 394752 + 393220), (True, "fused to 1 chain", 394756)):
+        gr = ComputationalGraph(13)
+        gr.AddInput("x", np.float32, (1, 128, 384))
+        gr.AddInitializer("bias", B.cpu().numpy())
+        gr.AddInitializer("k", np.array(0.125, np.float32))
+        gr.AddNode("Add", ["x", "bias"], ["h"], name="add")
+        gr.AddNode("Mul", ["h", "k"], ["y"], name="mul")
+        gr.AddOutput("y")
+        if fuse:
+            assert gr.Fuse() == 1
+
+        def step(i, gr=gr):
+            if not gr.Execute([wA[i % n1]]):
+                raise RuntimeError(gr.LastError)
+        record(f"C1 graph executor, {label} (host dispatch per execution)", nbytes, 49152,
+               wall_time(torch, step, max(64, steps), warmup))
+        gr.close()
     del A, C, D, wA, wC, wD
     torch.cuda.empty_cache()
 
@@ -282,7 +304,6 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
 
     # the same ONNX subgraph through the device graph runtime (the ComputationalGraph twin), one
     # host-dispatched execution per step (wall clock, ctypes call included): 9 nodes, then fused
-    from onnx_amd.graph import ComputationalGraph
 
     def ln_graph(fuse):
         gr = ComputationalGraph(13)
@@ -364,6 +385,12 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     Y5 = torch.empty_like(X5)
     wX5, wY5 = wrap(X5), wrap(Y5)
     run("C5 GELU chain fused", 1610612736, X5.numel(), lambda i: HIP.GeluErf(wX5, out=wY5), 1, k=k3)
+    # the same five nodes through the generic elementwise-chain kernel (the fusion used when the
+    # constants do not match the GELU pattern)
+    k5 = [wrap(torch.tensor(v, device=dev)) for v in (1.4142135381698608, 1.0, 0.5)]
+    run("C5 GELU chain as a generic ElementwiseChain", 1610612736, X5.numel(),
+        lambda i: HIP.ElementwiseChain([wX5] + k5, [("Div", 1), ("Erf",), ("Add", 2), ("Mul", 0, True), ("Mul", 3)],
+                                       out=wY5), 1, k=k3)
     del X5, Y5, wX5, wY5
     torch.cuda.empty_cache()
     Yb = torch.rand(256, 4096, 256, device=dev, generator=gen) * 2 - 1

@@ -190,6 +190,18 @@ int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_
                            lx_tensor *Y);
 /* Add(S, mask) -> Softmax(axis) with the mask broadcast against S. */
 int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_tensor *Y);
+/* A linear chain of Float elementwise nodes in one pass (no single reference counterpart: it replaces
+ * consecutive CPUExecutionProvider.Add/Sub/Mul/Div/Pow/Sqrt/Erf calls, CPUExecutionProvider.cs:82-236,
+ * 380-409, whose intermediates have no other consumer).  acc = inputs[0]; instruction k applies ops[k]:
+ *   LX_CHAIN_ADD..LX_CHAIN_POW (0..4): acc = acc op inputs[j] for operands[k] = j >= 0,
+ *                                        acc = inputs[j] op acc for operands[k] = -(j + 1);
+ *   LX_CHAIN_SQRT (16), LX_CHAIN_ERF (17): acc = op(acc), operands[k] ignored.
+ * Each step broadcasts like the separate operator and rounds as it does, so the result is bit-identical
+ * to running the nodes one by one.  1..8 inputs, 1..16 instructions, Float only. */
+enum { LX_CHAIN_ADD = 0, LX_CHAIN_SUB = 1, LX_CHAIN_MUL = 2, LX_CHAIN_DIV = 3, LX_CHAIN_POW = 4,
+       LX_CHAIN_SQRT = 16, LX_CHAIN_ERF = 17 };
+int lx_ElementwiseChain(const lx_tensor *const *inputs, int32_t n_in, const int32_t *ops, const int32_t *operands,
+                        int32_t n_ops, lx_tensor *Y);
 
 /* ---- graph runtime: ComputationalGraph + Node.Execute on the device -------
  * (src/Lokad.Onnx.Backend/ComputationalGraph.cs, Node.cs, Model.cs).  Graph
@@ -231,7 +243,9 @@ int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
  * replaces the GELU subgraph (Div sqrt2 -> Erf -> Add 1 -> Mul x -> Mul 0.5), the decomposed
  * LayerNorm (ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul -> Add) and
  * Add(mask) -> Softmax by the fused kernels when every intermediate has exactly one consumer and is
- * not a graph output.  *n_fused = number of subgraphs replaced. */
+ * not a graph output; then every linear chain of two or more Float elementwise nodes
+ * (Add/Sub/Mul/Div/Pow/Sqrt/Erf) whose intermediates have one consumer by an ElementwiseChain node
+ * (lx_ElementwiseChain).  *n_fused = number of fused nodes made. */
 int lx_graph_fuse(lx_graph *g, int32_t *n_fused);
 /* ComputationalGraph.Execute(userInputs, useInitializers) (ComputationalGraph.cs:199-272) with the
  * inputs given by name (the Dictionary overload, ComputationalGraph.cs:105-130) or, when names is

@@ -60,6 +60,7 @@ class LxPlan(ctypes.Structure):
 # name -> (restype, argtypes); every symbol declared in include/lonnx.h
 _T = ctypes.POINTER(LxTensor)
 _i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.POINTER(ctypes.c_int32)
 _c = ctypes
 SIGNATURES = {
     "lx_init": (_c.c_int, [_c.c_int32]),
@@ -97,6 +98,7 @@ SIGNATURES = {
     "lx_Concat": (_c.c_int, [_c.POINTER(_T), _c.c_int32, _c.c_int32, _c.c_int32, _T]),
     "lx_Gather": (_c.c_int, [_T, _T, _c.c_int32, _c.c_int32, _T]),
     "lx_Slice": (_c.c_int, [_T, _i64p, _c.c_int32, _i64p, _c.c_int32, _i64p, _c.c_int32, _i64p, _c.c_int32, _T]),
+    "lx_ElementwiseChain": (_c.c_int, [_c.POINTER(_T), _c.c_int32, _i32p, _i32p, _c.c_int32, _T]),
     "lx_pool_trim": (_c.c_int, []),
     "lx_pool_stats": (_c.c_int, [_i64p, _i64p]),
     # graph runtime

@@ -862,6 +862,106 @@ int lx_GeluErf(const lx_tensor *X, lx_tensor *Y) {
     return LX_OK;
 }
 
+int lx_ElementwiseChain(const lx_tensor *const *inputs, int32_t n_in, const int32_t *ops, const int32_t *operands,
+                        int32_t n_ops, lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!inputs || n_in < 1 || n_in > kChainMaxIn)
+        return set_err(LX_ERR_INVALID_ARGUMENT, "An elementwise chain takes 1 to %d inputs.", kChainMaxIn);
+    if (!ops || n_ops < 1 || n_ops > kChainMaxOps || (!operands && n_ops > 0))
+        return set_err(LX_ERR_INVALID_ARGUMENT, "An elementwise chain takes 1 to %d instructions.", kChainMaxOps);
+    int st;
+    for (int j = 0; j < n_in; j++) {
+        if (!inputs[j]) return missing_input("ElementwiseChain", "inputs");
+        if ((st = check_tensor(inputs[j], "inputs"))) return st;
+        if (inputs[j]->dtype != LX_FLOAT) return type_not_supported("ElementwiseChain", "inputs", inputs[j]);
+    }
+    // the shape after each instruction: binary steps broadcast as the separate operators do
+    int rank = inputs[0]->rank;
+    int64_t dims[LX_MAX_RANK];
+    for (int i = 0; i < rank; i++) dims[i] = inputs[0]->dims[i];
+    bool erf = false;
+    for (int k = 0; k < n_ops; k++) {
+        const int op = ops[k];
+        if (op == kChainUnary + kSqrt || op == kChainUnary + kErf) {
+            erf = erf || op == kChainUnary + kErf;
+            continue;
+        }
+        if (op < kAdd || op > kPow) return set_err(LX_ERR_INVALID_ARGUMENT, "Instruction %d has an unknown op %d.", k, op);
+        const int j = operands[k] < 0 ? -operands[k] - 1 : operands[k];
+        if (j >= n_in) return set_err(LX_ERR_INVALID_ARGUMENT, "Instruction %d reads input %d of %d.", k, j, n_in);
+        lx_bcast_plan bp;
+        st = plan(rank, dims, inputs[j]->rank, inputs[j]->dims, &bp);
+        if (st == LX_ERR_CANNOT_BROADCAST)
+            return set_err(st, "Instruction %d: the tensors are not compatible for broadcasting.", k);
+        if (st) return st;
+        rank = bp.out_rank;
+        for (int i = 0; i < rank; i++) dims[i] = bp.out_dims[i];
+    }
+    if ((st = prepare_output(Y, LX_FLOAT, rank, dims))) return st;
+    const int64_t total = numel_of(rank, dims);
+    if (total == 0) return LX_OK;
+    // strides of every input in the output frame (0 on broadcast or missing axes), then the axes
+    // merged from the inside out while every input stays contiguous across them
+    int64_t str[kChainMaxIn][LX_MAX_RANK];
+    for (int j = 0; j < n_in; j++) {
+        const lx_tensor *t = inputs[j];
+        int64_t acc = 1;
+        for (int i = rank - 1; i >= 0; i--) {
+            const int k = i - (rank - t->rank);
+            if (k < 0) { str[j][i] = 0; continue; }
+            str[j][i] = (t->dims[k] == 1 && dims[i] != 1) ? 0 : acc;
+            acc *= t->dims[k];
+        }
+    }
+    int64_t cd[LX_MAX_RANK], cs[kChainMaxIn][LX_MAX_RANK];
+    int n = 0;
+    for (int i = rank - 1; i >= 0; i--) {
+        if (dims[i] == 1) continue;
+        bool merge = n > 0;
+        for (int j = 0; merge && j < n_in; j++) merge = str[j][i] == cs[j][n - 1] * cd[n - 1];
+        if (merge) {
+            cd[n - 1] *= dims[i];
+            continue;
+        }
+        cd[n] = dims[i];
+        for (int j = 0; j < n_in; j++) cs[j][n] = str[j][i];
+        n++;
+    }
+    if (n == 0) {  // one element
+        cd[0] = 1;
+        for (int j = 0; j < n_in; j++) cs[j][0] = 0;
+        n = 1;
+    }
+    ChainArgs a;
+    memset(&a, 0, sizeof a);
+    a.n_in = n_in;
+    a.n_ops = n_ops;
+    a.uses_erf = erf ? 1 : 0;
+    a.nouter = n - 1;
+    bool vec = cd[0] % 4 == 0 && aligned16(Y->data);
+    for (int j = 0; j < n_in; j++) {
+        a.in[j] = (const float *)inputs[j]->data;
+        if (cs[j][0] != 0) {
+            a.inner_mode |= 1 << j;
+            vec = vec && aligned16(inputs[j]->data);
+            for (int d = 1; d < n; d++) vec = vec && cs[j][d] % 4 == 0;
+        }
+        for (int d = 1; d < n; d++) a.str[j][d - 1] = cs[j][d];
+    }
+    a.vec = vec ? 4 : 1;
+    if (total / a.vec >= (1ll << 31)) return set_err(LX_ERR_NOT_SUPPORTED, "Chains over 2^31 vectors are not supported.");
+    a.nv = (uint32_t)(total / a.vec);
+    a.inner_v = make_fastdiv((uint32_t)(cd[0] / a.vec));
+    for (int d = 1; d < n; d++) a.odiv[d - 1] = make_fastdiv((uint32_t)cd[d]);
+    a.y = (float *)Y->data;
+    for (int k = 0; k < n_ops; k++) {
+        a.op[k] = (int8_t)ops[k];
+        a.operand[k] = (int8_t)operands[k];
+    }
+    HIPCHECK(launch_chain(a, g.stream), "ElementwiseChain");
+    return LX_OK;
+}
+
 int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_tensor *beta, float eps,
                            lx_tensor *Y) {
     REQUIRE_INIT();

@@ -583,4 +583,138 @@ hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStre
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Elementwise chain: a linear sequence of float32 Add/Sub/Mul/Div/Pow/Sqrt/Erf
+// nodes in one pass (the graph runtime's fusion of elementwise chains).  Each
+// instruction calls the same device routine as the separate operator, so the
+// result is bit-identical to running the nodes one by one.  The instruction
+// list is uniform across the launch: the switch below does not diverge.
+// ---------------------------------------------------------------------------
+template <int OP, int V>
+__device__ __forceinline__ void chain_bin(Vec<float, V> &acc, const Vec<float, V> &x, bool x_left) {
+    if (x_left) {
+#pragma unroll
+        for (int k = 0; k < V; k++) acc.v[k] = bin_apply<OP, float>(x.v[k], acc.v[k], 0, nullptr);
+    } else {
+#pragma unroll
+        for (int k = 0; k < V; k++) acc.v[k] = bin_apply<OP, float>(acc.v[k], x.v[k], 0, nullptr);
+    }
+}
+
+// one instruction; op and x_left are uniform, so each branch is taken by the whole
+// wave.  ERF / POW: whether the chain holds those instructions (their code is large
+// and its registers would cost occupancy in the chains that do not).
+template <int V, bool ERF, bool POW>
+__device__ __forceinline__ void chain_step(int op, Vec<float, V> &acc, const Vec<float, V> &x, bool x_left,
+                                           const ExpTable &tab) {
+    switch (op) {
+    case kAdd: chain_bin<kAdd, V>(acc, x, x_left); break;
+    case kSub: chain_bin<kSub, V>(acc, x, x_left); break;
+    case kMul: chain_bin<kMul, V>(acc, x, x_left); break;
+    case kDiv: chain_bin<kDiv, V>(acc, x, x_left); break;
+    case kPow:
+        if constexpr (POW) chain_bin<kPow, V>(acc, x, x_left);
+        break;
+    case kChainUnary + kSqrt:
+#pragma unroll
+        for (int k = 0; k < V; k++) acc.v[k] = un_apply<kSqrt, float>(acc.v[k], tab);
+        break;
+    default:
+        if constexpr (ERF) {
+#pragma unroll
+            for (int k = 0; k < V; k++) acc.v[k] = un_apply<kErf, float>(acc.v[k], tab);
+        }
+        break;
+    }
+}
+
+// NIN: inputs held in registers (n_in <= NIN)
+extern __shared__ ExpTable chain_lds[];  // the expf table of chains with Erf (dynamic LDS: none otherwise)
+
+template <int V, int NIN, bool ERF, bool POW>
+__global__ __launch_bounds__(kBlock) void k_chain(ChainArgs A) {
+    ExpTable &tab = chain_lds[0];
+    if constexpr (ERF) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < A.nv; v += gridDim.x * kBlock) {
+        const uint32_t row = fdiv(v, A.inner_v);
+        const uint32_t cv = v - row * A.inner_v.d;
+        int64_t off[NIN];
+#pragma unroll
+        for (int j = 0; j < NIN; j++) off[j] = 0;
+        uint32_t rr = row;
+#pragma unroll
+        for (int d = 0; d < kMaxOuter; d++) {
+            if (d < A.nouter) {
+                const uint32_t q = fdiv(rr, A.odiv[d]);
+                const int64_t id = rr - q * A.odiv[d].d;
+#pragma unroll
+                for (int j = 0; j < NIN; j++)
+                    if (j < A.n_in) off[j] += id * A.str[j][d];
+                rr = q;
+            }
+        }
+        const int64_t col = (int64_t)cv * V;
+        Vec<float, V> x[NIN];
+#pragma unroll
+        for (int j = 0; j < NIN; j++) {
+            if (j < A.n_in) {
+                if ((A.inner_mode >> j) & 1) {
+                    // ordinary loads: streaming loads measured slower here (C3-sized Add -> Mul
+                    // chain 106 against 86 us on MI355X)
+                    x[j] = vload<float, V>(A.in[j] + off[j] + col);
+                } else {
+                    const float sv = A.in[j][off[j]];
+#pragma unroll
+                    for (int k = 0; k < V; k++) x[j].v[k] = sv;
+                }
+            }
+        }
+        Vec<float, V> acc = x[0];
+        // unrolled: each instruction's op and operand are fixed argument offsets, loaded once
+#pragma unroll
+        for (int i = 0; i < kChainMaxOps; i++) {
+            if (i >= A.n_ops) break;
+            const int o = A.operand[i];
+            const int j = o < 0 ? -o - 1 : o;
+            Vec<float, V> xj = x[0];
+#pragma unroll
+            for (int jj = 1; jj < NIN; jj++)
+                if (jj == j) xj = x[jj];
+            chain_step<V, ERF, POW>(A.op[i], acc, xj, o < 0, tab);
+        }
+        vstore_nt<float, V>(A.y + (int64_t)v * V, acc);
+    }
+}
+
+template <int V, int NIN>
+static void launch_chain_v(const ChainArgs &A, int g, bool pow, hipStream_t s) {
+    const size_t lds = sizeof(ExpTable);
+    if (A.uses_erf && pow) hipLaunchKernelGGL((k_chain<V, NIN, true, true>), dim3(g), dim3(kBlock), lds, s, A);
+    else if (A.uses_erf) hipLaunchKernelGGL((k_chain<V, NIN, true, false>), dim3(g), dim3(kBlock), lds, s, A);
+    else if (pow) hipLaunchKernelGGL((k_chain<V, NIN, false, true>), dim3(g), dim3(kBlock), 0, s, A);
+    else hipLaunchKernelGGL((k_chain<V, NIN, false, false>), dim3(g), dim3(kBlock), 0, s, A);
+}
+
+hipError_t launch_chain(const ChainArgs &A, hipStream_t s) {
+    if (A.nv == 0) return hipSuccess;
+    bool pow = false;
+    for (int i = 0; i < A.n_ops; i++) pow = pow || A.op[i] == kPow;
+    // large chains without the expf table: two vectors per lane, as the binary kernels do
+    const int64_t work = A.uses_erf ? lane_work(A.nv, true) : (A.nv >= (1u << 20) ? (A.nv + 1) / 2 : A.nv);
+    const int g = grid_for(work, kBlock);
+    if (A.vec == 4) {
+        if (A.n_in <= 2) launch_chain_v<4, 2>(A, g, pow, s);
+        else if (A.n_in <= 4) launch_chain_v<4, 4>(A, g, pow, s);
+        else launch_chain_v<4, 8>(A, g, pow, s);
+    } else {
+        if (A.n_in <= 2) launch_chain_v<1, 2>(A, g, pow, s);
+        else if (A.n_in <= 4) launch_chain_v<1, 4>(A, g, pow, s);
+        else launch_chain_v<1, 8>(A, g, pow, s);
+    }
+    return hipGetLastError();
+}
+
 }  // namespace lx

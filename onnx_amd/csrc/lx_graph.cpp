@@ -169,6 +169,7 @@ int host_ints(Value &v, std::vector<int64_t> *out) {
 // ---- execution context ------------------------------------------------------
 struct Exec {
     lx_graph *g;
+    const GNode *failed = nullptr;  // the original node of a fused subgraph that failed
     bool is_node_output(const std::string &name) const {
         return std::find(g->node_outputs.begin(), g->node_outputs.end(), name) != g->node_outputs.end();
     }
@@ -336,7 +337,10 @@ int run_unfused(Exec &X, const GNode &n, std::vector<Value> &outs) {
     int st = LX_OK;
     for (const GNode &m : n.fused_from) {
         std::vector<Value> o;
-        if ((st = run_node(X, m, o))) break;
+        if ((st = run_node(X, m, o))) {
+            if (!X.failed) X.failed = &m;
+            break;
+        }
         for (size_t i = 0; i < m.out.size() && i < o.size(); i++) {
             X.g->values[m.out[i]] = o[i];
             made.push_back(m.out[i]);
@@ -611,10 +615,41 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!same) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
     }
+    if (op == "ElementwiseChain") {
+        std::vector<const lx_tensor *> ts;
+        for (size_t k = 0; k < n.in.size(); k++) {
+            Value *v;
+            if ((st = X.input(n, k, &v))) return st;
+            if (!v || v->t.dtype != LX_FLOAT) return run_unfused(X, n, outs);
+            ts.push_back(T(v));
+        }
+        const Attr *ops = find_attr(n, "ops"), *opd = find_attr(n, "operands");
+        if (!ops || !opd || ops->kind != kAttrInts || opd->kind != kAttrInts || ops->ints.size() != opd->ints.size())
+            return failure("malformed ElementwiseChain node");
+        std::vector<int32_t> o(ops->ints.begin(), ops->ints.end()), p(opd->ints.begin(), opd->ints.end());
+        // shapes that do not broadcast step by step: the original nodes report it
+        int rank = ts[0]->rank;
+        int64_t dims[LX_MAX_RANK];
+        for (int i = 0; i < rank; i++) dims[i] = ts[0]->dims[i];
+        for (size_t k = 0; k < o.size(); k++) {
+            if (o[k] >= 16) continue;
+            const int j = p[k] < 0 ? -p[k] - 1 : p[k];
+            if (j >= (int)ts.size()) return failure("malformed ElementwiseChain node");
+            lx_bcast_plan bp;
+            if (lx_plan_broadcast(rank, dims, ts[j]->rank, ts[j]->dims, &bp) != LX_OK) return run_unfused(X, n, outs);
+            rank = bp.out_rank;
+            for (int i = 0; i < rank; i++) dims[i] = bp.out_dims[i];
+        }
+        return run_op([&](lx_tensor *y) {
+            return lx_ElementwiseChain(ts.data(), (int32_t)ts.size(), o.data(), p.data(), (int32_t)o.size(), y);
+        }, outs);
+    }
     return not_supported(op);
 }
 
 // ---- fusion -----------------------------------------------------------------
+constexpr int kChainMaxInG = 8, kChainMaxOpsG = 16;  // lx_ElementwiseChain's limits
+
 struct Fuser {
     lx_graph *g;
     std::map<std::string, std::vector<int>> consumers;
@@ -782,24 +817,97 @@ struct Fuser {
         return true;
     }
 
+    // a linear chain of Float elementwise nodes (Add/Sub/Mul/Div/Pow/Sqrt/Erf), each intermediate
+    // consumed only by the next node of the chain: one ElementwiseChain node
+    static int chain_op(const GNode &n) {
+        static const char *bin[] = {"Add", "Sub", "Mul", "Div", "Pow"};
+        if (n.out.size() != 1) return -1;
+        for (int k = 0; k < 5; k++)
+            if (n.op == bin[k]) return n.in.size() == 2 ? k : -1;
+        if (n.op == "Sqrt") return n.in.size() == 1 ? 16 : -1;
+        if (n.op == "Erf") return n.in.size() == 1 ? 17 : -1;
+        return -1;
+    }
+    bool chain(int i0, GNode *f, std::vector<int> *nodes) {
+        if (used[i0] || chain_op(N(i0)) < 0) return false;
+        std::vector<std::string> ins;
+        std::vector<int64_t> ops, operands;
+        auto input_index = [&](const std::string &nm) {
+            for (size_t j = 0; j < ins.size(); j++)
+                if (ins[j] == nm) return (int)j;
+            ins.push_back(nm);
+            return (int)ins.size() - 1;
+        };
+        const int op0 = chain_op(N(i0));
+        input_index(N(i0).in[0]);
+        ops.push_back(op0);
+        operands.push_back(op0 < 16 ? input_index(N(i0).in[1]) : 0);
+        std::vector<int> chain_nodes = {i0};
+        int cur = i0;
+        while ((int)ops.size() < kChainMaxOpsG) {
+            const std::string &v = N(cur).out[0];
+            const int c = only_consumer(v);
+            if (c < 0 || used[c]) break;
+            const int op = chain_op(N(c));
+            if (op < 0) break;
+            int64_t operand = 0;
+            if (op < 16) {
+                const bool left = N(c).in[0] == v, right = N(c).in[1] == v;
+                if (left == right) break;  // both operands are the chain value, or neither
+                const std::string &other = left ? N(c).in[1] : N(c).in[0];
+                const size_t before = ins.size();
+                const int j = input_index(other);
+                if ((int)ins.size() > kChainMaxInG) {
+                    ins.resize(before);
+                    break;
+                }
+                operand = left ? j : -(j + 1);
+            }
+            ops.push_back(op);
+            operands.push_back(operand);
+            chain_nodes.push_back(c);
+            cur = c;
+        }
+        if (chain_nodes.size() < 2) return false;
+        *nodes = chain_nodes;
+        f->op = "ElementwiseChain";
+        f->in = ins;
+        f->out = N(cur).out;
+        Attr a;
+        a.kind = kAttrInts;
+        a.ints = ops;
+        f->attrs["ops"] = a;
+        a.ints = operands;
+        f->attrs["operands"] = a;
+        return true;
+    }
+
     int run() {
         index();
         int fused = 0;
         std::vector<std::pair<int, GNode>> placed;  // fused node at the index of its last original
+        auto place = [&](GNode &f, std::vector<int> &nodes) {
+            std::sort(nodes.begin(), nodes.end());
+            for (int k : nodes) {
+                used[k] = true;
+                f.fused_from.push_back(N(k));
+            }
+            f.name = N(nodes.back()).name;
+            f.index = N(nodes.back()).index;
+            placed.push_back({nodes.back(), f});
+            fused++;
+        };
+        // the specific subgraphs first, then elementwise chains among the remaining nodes
         for (int i = 0; i < (int)g->nodes.size(); i++) {
             if (used[i]) continue;
             GNode f;
             std::vector<int> nodes;
-            if (layernorm(i, &f, &nodes) || gelu(i, &f, &nodes) || add_softmax(i, &f, &nodes)) {
-                std::sort(nodes.begin(), nodes.end());
-                for (int k : nodes) {
-                    used[k] = true;
-                    f.fused_from.push_back(N(k));
-                }
-                f.name = N(nodes.back()).name;
-                placed.push_back({nodes.back(), f});
-                fused++;
-            }
+            if (layernorm(i, &f, &nodes) || gelu(i, &f, &nodes) || add_softmax(i, &f, &nodes)) place(f, nodes);
+        }
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            GNode f;
+            std::vector<int> nodes;
+            if (chain(i, &f, &nodes)) place(f, nodes);
         }
         if (!fused) return 0;
         std::vector<GNode> out;
@@ -926,6 +1034,7 @@ int lx_graph_add_node(lx_graph *g, const char *name, const char *op_type, int32_
         n.out.push_back(outputs[i] ? outputs[i] : "");
         g->node_outputs.push_back(n.out.back());
     }
+    n.index = (int)g->nodes.size();
     g->nodes.push_back(n);
     if (index) *index = (int32_t)g->nodes.size() - 1;
     return LX_OK;
@@ -1062,8 +1171,12 @@ int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_
             st = failure(fmt("The operation returned %d outputs but the graph node has %d outputs.", (int)outs.size(),
                              (int)node.out.size()));
         if (st) {
+            // a fused node that fell back to its original nodes reports the one that failed, numbered
+            // as in the graph before fusion, so the message is the unfused graph's
+            const GNode &rep = X.failed ? *X.failed : node;
+            const int num = rep.index >= 0 ? rep.index + 1 : k + 1;
             std::string m = lx_last_error();
-            return fail(st, fmt("Execution of node %d %s with op %s failed: %s", k + 1, node.name.c_str(), node.op.c_str(),
+            return fail(st, fmt("Execution of node %d %s with op %s failed: %s", num, rep.name.c_str(), rep.op.c_str(),
                                 m.c_str()));
         }
         for (size_t i = 0; i < outs.size(); i++) g->values[node.out[i]] = outs[i];

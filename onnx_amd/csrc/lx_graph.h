@@ -57,6 +57,7 @@ struct GNode {
     std::vector<std::string> in, out;
     std::map<std::string, Attr> attrs;
     std::vector<GNode> fused_from;  // the original nodes of a fused subgraph
+    int index = -1;                 // position in the node list as built (before fusion)
 };
 
 struct GInput {

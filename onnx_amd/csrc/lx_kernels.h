@@ -55,6 +55,33 @@ hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, in
 hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,
                        hipStream_t s);
 hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStream_t s);
+
+// Elementwise chain (float32): acc = in[0], then per instruction k
+//   binary op[k] in BinOp:   acc = acc op in[j]   (operand[k] = j >= 0)
+//                            acc = in[j] op acc   (operand[k] = -(j + 1))
+//   unary  op[k] = kChainUnary + UnOp (Sqrt, Erf): acc = op(acc)
+// each op rounded as the separate operator rounds it.  Output row-major
+// [rows, inner]; input j is addressed by its per-axis strides str[j][d] over
+// the outer axes and, along the inner axis, contiguously (bit j of inner_mode)
+// or broadcast.
+constexpr int kChainMaxIn = 8, kChainMaxOps = 16, kChainUnary = 16;
+struct ChainArgs {
+    int32_t n_in, n_ops;
+    int32_t inner_mode;
+    int32_t uses_erf;
+    int32_t vec;             // 4 = 16-byte vectors, 1 = scalars
+    int32_t nouter;
+    uint32_t nv;             // output vectors
+    uint32_t pad;
+    FastDiv odiv[kMaxOuter]; // outer axis sizes, innermost first
+    FastDiv inner_v;         // inner axis in vector units
+    int64_t str[kChainMaxIn][kMaxOuter];
+    const float *in[kChainMaxIn];
+    float *y;
+    int8_t op[kChainMaxOps];
+    int8_t operand[kChainMaxOps];
+};
+hipError_t launch_chain(const ChainArgs &args, hipStream_t s);
 // y[i] = value (bit pattern of one element of esize bytes), used for empty reductions.
 hipError_t launch_fill(void *y, int64_t n, int esize, uint64_t bits, hipStream_t s);
 

@@ -325,6 +325,7 @@ int parse_graph(Reader r, lx_graph *g) {
             st = parse_node(r.sub(), &n);
             if (!st) {
                 for (auto &o : n.out) g->node_outputs.push_back(o);
+                n.index = (int)g->nodes.size();
                 g->nodes.push_back(n);
             }
             break;

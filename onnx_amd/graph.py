@@ -4,7 +4,7 @@ include/lonnx.h (lx_graph_*): the reference's graph API
 an execution resident in HBM.
 
     g = Model.Load("model.onnx")          # Model.Load (Model.cs:65-78); initializers uploaded once
-    g.Fuse()                              # optional: GELU / LayerNorm / mask+Softmax subgraphs -> fused kernels
+    g.Fuse()                              # optional: GELU / LayerNorm / mask+Softmax subgraphs and elementwise chains -> fused kernels
     ok = g.Execute([x], True)             # ComputationalGraph.Execute (ComputationalGraph.cs:199-272)
     y = g.Outputs["output"].to_numpy()
 
@@ -38,7 +38,7 @@ def _check(st, what):
 
 class Node:
     """A graph node as the runtime holds it (after fusion, fused nodes appear with
-    op types GeluErf, LayerNormDecomposed and AddSoftmax)."""
+    op types GeluErf, LayerNormDecomposed, AddSoftmax and ElementwiseChain)."""
 
     def __init__(self, name: str, op: str):
         self.Name, self.Op = name, op
@@ -152,7 +152,8 @@ class ComputationalGraph:
 
     def Fuse(self) -> int:
         """Replace the GELU, decomposed-LayerNorm and Add+Softmax subgraphs by their
-        fused kernels; returns how many were replaced."""
+        fused kernels, then linear chains of Float elementwise nodes by one
+        ElementwiseChain node each; returns how many fused nodes were made."""
         n = ctypes.c_int32()
         _check(L.lib().lx_graph_fuse(self._h, ctypes.byref(n)), "lx_graph_fuse")
         return n.value

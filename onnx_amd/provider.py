@@ -324,6 +324,28 @@ class HipExecutionProvider:
         return _result("Slice", st, y, out)
 
     # ---- fused subgraphs ---------------------------------------------------
+    CHAIN_OPS = {"Add": 0, "Sub": 1, "Mul": 2, "Div": 3, "Pow": 4, "Sqrt": 16, "Erf": 17}
+
+    @staticmethod
+    def ElementwiseChain(inputs, program, out=None):
+        """A linear chain of Float elementwise nodes in one kernel.  acc = inputs[0]; program is a list of
+        (op, j) for binary ops (acc = acc op inputs[j]), (op, j, True) for acc = inputs[j] op acc, or (op,)
+        for Sqrt / Erf.  Bit-identical to running the nodes one by one."""
+        init()
+        ts = [_as_tensor(t) for t in inputs]
+        arr = (ctypes.POINTER(L.LxTensor) * max(1, len(ts)))(*[ctypes.pointer(t.h) for t in ts])
+        ops, operands = [], []
+        for ins in program:
+            ops.append(HipExecutionProvider.CHAIN_OPS[ins[0]])
+            j = ins[1] if len(ins) > 1 else 0
+            operands.append(-(j + 1) if len(ins) > 2 and ins[2] else j)
+        n = max(1, len(ops))
+        o = (ctypes.c_int32 * n)(*ops)
+        p = (ctypes.c_int32 * n)(*operands)
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_ElementwiseChain(arr, len(ts), o, p, len(ops), ctypes.byref(y))
+        return _result("ElementwiseChain", st, y, out)
+
     @staticmethod
     def GeluErf(X, out=None):
         init()

@@ -1,0 +1,166 @@
+"""GPU tests of the elementwise-chain kernel (lx_ElementwiseChain) and of the
+graph runtime's chain fusion: a linear run of Float Add/Sub/Mul/Div/Pow/Sqrt/Erf
+nodes computed in one pass must equal, bit for bit, the reference's node-by-node
+result (the oracle restates CPUExecutionProvider.Add/.../Erf,
+CPUExecutionProvider.cs:82-236, 380-409)."""
+import numpy as np
+import pytest
+
+from onnx_amd import DeviceTensor, HipExecutionProvider as HIP, OpStatus
+from onnx_amd import _lib as L
+from onnx_amd.graph import Model
+from oracle import graph_oracle as GO
+from oracle import oracle as O
+
+import onnx_writer as W
+
+pytestmark = pytest.mark.gpu
+
+BIN = {"Add": O.ADD, "Sub": O.SUB, "Mul": O.MUL, "Div": O.DIV, "Pow": O.POW}
+
+
+def dev(a):
+    return DeviceTensor.from_numpy(np.asarray(a))
+
+
+def bits(a, b):
+    """Bit-identical, any NaN matching any NaN: when both operands of an op are NaNs the payload that
+    survives depends on the operand order of the machine instruction, which the compiler may commute."""
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    if a.shape != b.shape:
+        return False
+    same = (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+    return bool(same.all())
+
+
+def oracle_chain(inputs, program):
+    acc = inputs[0]
+    for ins in program:
+        if ins[0] in ("Sqrt", "Erf"):
+            acc = O.unary(O.SQRT if ins[0] == "Sqrt" else O.ERF, acc)
+        elif len(ins) > 2 and ins[2]:
+            acc = O.binary(BIN[ins[0]], inputs[ins[1]], acc)
+        else:
+            acc = O.binary(BIN[ins[0]], acc, inputs[ins[1]])
+    return acc
+
+
+def device_chain(inputs, program):
+    """The same program node by node through the separate device operators."""
+    d = [dev(x) for x in inputs]
+    acc = d[0]
+    for ins in program:
+        if ins[0] in ("Sqrt", "Erf"):
+            r = getattr(HIP, ins[0])(acc)
+        elif len(ins) > 2 and ins[2]:
+            r = getattr(HIP, ins[0])(d[ins[1]], acc)
+        else:
+            r = getattr(HIP, ins[0])(acc, d[ins[1]])
+        assert r.Status == OpStatus.Success, r.Message
+        acc = r.Outputs[0]
+    return acc.to_numpy()
+
+
+def check(inputs, program):
+    """Bit-identical to the separate device operators; and to the oracle's node-by-node result when the
+    program has no Pow (Pow is within 2 ulp of the host powf, not bit-exact)."""
+    got = run_chain(inputs, program)
+    assert bits(got, device_chain(inputs, program))
+    if not any(p[0] == "Pow" for p in program):
+        assert bits(got, oracle_chain(inputs, program))
+
+
+def run_chain(inputs, program):
+    r = HIP.ElementwiseChain([dev(x) for x in inputs], program)
+    assert r.Status == OpStatus.Success, r.Message
+    return r.Outputs[0].to_numpy()
+
+
+CASES = [
+    # C1: bias Add, scalar Mul
+    ([(1, 128, 384), (384,), ()], [("Add", 1), ("Mul", 2)]),
+    # the GELU chain through the generic kernel: x / sqrt2 -> erf -> + 1 -> x * . -> * 0.5
+    ([(4, 64, 768), (), (), ()], [("Div", 1), ("Erf",), ("Add", 2), ("Mul", 0, True), ("Mul", 3)]),
+    # LayerNorm tail: (var + eps) -> sqrt -> d / . -> * gamma -> + beta
+    ([(8, 33, 1), (), (8, 33, 64), (64,), (64,)], [("Add", 1), ("Sqrt",), ("Div", 2, True), ("Mul", 3), ("Add", 4)]),
+    # every op, operands on both sides, several broadcast patterns, an inner axis that does not divide by 4
+    ([(3, 5, 7), (7,), (3, 1, 7), (5, 1), (), (1, 1, 1)],
+     [("Sub", 1), ("Mul", 2, True), ("Add", 3), ("Div", 4, True), ("Pow", 5), ("Sqrt",), ("Sub", 0, True)]),
+    # the output shape grows along the chain (rank-0 and lower-rank starts)
+    ([(), (6,), (2, 6), (3, 1, 1)], [("Add", 1), ("Mul", 2), ("Sub", 3, True), ("Erf",)]),
+    ([(64,), (16, 64), (4, 16, 1)], [("Mul", 1), ("Add", 2), ("Pow", 0, True)]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_chain_matches_node_by_node(hip, case):
+    shapes, program = CASES[case]
+    rng = np.random.default_rng(100 + case)
+    ins = [(rng.standard_normal(s) * 2).astype(np.float32) for s in shapes]
+    if any(p[0] == "Pow" for p in program):
+        ins = [np.abs(x) + np.float32(0.5) for x in ins]   # real powers of positive bases, plus NaN-free Sqrt
+    check(ins, program)
+
+
+def test_chain_special_values(hip):
+    x = np.array([0.0, -0.0, 1e-45, -1e-45, np.inf, -np.inf, np.nan, 3.4e38, -3.4e38, 1.0, 2.0, 0.5] * 11,
+                 np.float32)
+    y = np.roll(x, 5)
+    check([x, y], [("Div", 1), ("Erf",), ("Mul", 1, True), ("Sub", 0), ("Sqrt",), ("Add", 1)])
+    check([x, y], [("Div", 1), ("Erf",), ("Mul", 1, True), ("Sub", 0), ("Pow", 1), ("Sqrt",), ("Add", 1)])
+
+
+def test_chain_errors(hip):
+    a, b = dev(np.ones((2, 3), np.float32)), dev(np.ones((4,), np.float32))
+    r = HIP.ElementwiseChain([a, b], [("Add", 1)])
+    assert r.Code == L.ERR_CANNOT_BROADCAST
+    r = HIP.ElementwiseChain([a, dev(np.ones((2, 3), np.int32))], [("Add", 1)])
+    assert r.Code == L.ERR_INPUT_TYPE_NOT_SUPPORTED
+    r = HIP.ElementwiseChain([a], [("Add", 1)])
+    assert r.Code == L.ERR_INVALID_ARGUMENT
+
+
+def _graph_run(nodes, inputs, inits, outputs, fuse):
+    model = W.model(nodes, [(k, v.dtype, v.shape) for k, v in inputs.items()],
+                    [(o, np.float32, ()) for o in outputs], inits)
+    g = Model.Load(model)
+    n = g.Fuse() if fuse else 0
+    ok = g.Execute({k: DeviceTensor.from_numpy(v) for k, v in inputs.items()}, True)
+    return g, n, ok
+
+
+def test_graph_c1_chain_fused_bit_exact(hip):
+    from test_gpu_graph import _dict_nodes
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((1, 128, 384)).astype(np.float32)
+    nodes = [W.node("Add", ["x", "bias"], ["h"], "add"), W.node("Mul", ["h", "k"], ["y"], "mul")]
+    inits = [("bias", rng.uniform(-0.1, 0.1, 384).astype(np.float32)), ("k", np.array(0.125, np.float32))]
+    g, n, ok = _graph_run(nodes, {"x": x}, inits, ["y"], True)
+    assert ok, g.LastError
+    assert n == 1 and [nd.Op for nd in g.Nodes] == ["ElementwiseChain"]
+    ref = GO.run(_dict_nodes(nodes), {"x": x}, dict(inits))
+    assert bits(g.Output("y").to_numpy(), ref["y"])
+
+
+def test_graph_chain_with_escaping_intermediate(hip):
+    """GELU-shaped graph whose Erf output is also a graph output: two chains around it."""
+    from test_graph_host import GELU_INITS, gelu_nodes
+    from test_gpu_graph import _dict_nodes
+    x = np.random.default_rng(8).standard_normal((3, 50, 70)).astype(np.float32)
+    g, n, ok = _graph_run(gelu_nodes(), {"x": x}, GELU_INITS, ["y", "e"], True)
+    assert ok, g.LastError
+    assert n == 2
+    ref = GO.run(_dict_nodes(gelu_nodes()), {"x": x}, dict(GELU_INITS))
+    assert bits(g.Output("y").to_numpy(), ref["y"]) and bits(g.Output("e").to_numpy(), ref["e"])
+
+
+def test_graph_chain_broadcast_failure_reports_the_original_node(hip):
+    """Shapes that fail at the second node: the fused node runs its original nodes, so the failure names the
+    same node with the same message as the unfused graph."""
+    x = np.ones((2, 3), np.float32)
+    nodes = [W.node("Add", ["x", "b"], ["h"], "first"), W.node("Mul", ["h", "c"], ["y"], "second")]
+    inits = [("b", np.ones(3, np.float32)), ("c", np.ones(4, np.float32))]
+    g0, _, ok0 = _graph_run(nodes, {"x": x}, inits, ["y"], False)
+    g1, n1, ok1 = _graph_run(nodes, {"x": x}, inits, ["y"], True)
+    assert n1 == 1 and not ok0 and not ok1
+    assert g1.LastError == g0.LastError and "second" in g0.LastError

@@ -151,22 +151,48 @@ def test_fusion_replaces_the_three_subgraphs():
 
 
 def test_fusion_keeps_subgraphs_whose_intermediates_escape():
-    # an intermediate is also a graph output
+    """A pattern whose intermediate escapes is not replaced by its fused kernel; the elementwise-chain pass
+    then fuses only the runs of nodes whose intermediates have no other consumer."""
+    # an intermediate is also a graph output: Div -> Erf stops at the escaping e
     n, ops = _fused(gelu_nodes(), GELU_INITS, outputs=("y", "e"))
-    assert n == 0 and len(ops) == 5
-    # an intermediate has a consumer outside the pattern
+    assert (n, ops) == (2, [("erf", "ElementwiseChain"), ("mul2", "ElementwiseChain")])
+    # an intermediate has a consumer outside the pattern: b feeds Mul and Sqrt
     n, ops = _fused(gelu_nodes(extra=[W.node("Sqrt", ["b"], ["z"], "other")]), GELU_INITS, outputs=("y", "z"))
-    assert n == 0 and len(ops) == 6
-    # a constant with other bits than float32(sqrt 2)
+    assert (n, ops) == (2, [("add", "ElementwiseChain"), ("mul2", "ElementwiseChain"), ("other", "Sqrt")])
+    # a constant with other bits than float32(sqrt 2): no GeluErf, one chain of the five nodes
     inits = [("sqrt2", np.array(1.4142, np.float32))] + GELU_INITS[1:]
-    assert _fused(gelu_nodes(), inits)[0] == 0
+    assert _fused(gelu_nodes(), inits) == (1, [("mul2", "ElementwiseChain")])
     # a "constant" the caller may replace (an initializer that is also a graph input)
-    n, _ = _fused(gelu_nodes(), GELU_INITS, inputs=(("x", np.float32, (2, 8)), ("half", np.float32, ())))
-    assert n == 0
-    # LayerNorm reducing another axis
+    n, ops = _fused(gelu_nodes(), GELU_INITS, inputs=(("x", np.float32, (2, 8)), ("half", np.float32, ())))
+    assert (n, ops) == (1, [("mul2", "ElementwiseChain")])
+    # LayerNorm reducing another axis: only Add eps -> Sqrt -> Div -> Mul -> Add chains
     inits = LN_INITS()
     inits[0] = ("axes", np.array([0], np.int64))
-    assert _fused(ln_nodes(), inits)[0] == 0
+    n, ops = _fused(ln_nodes(), inits)
+    assert n == 1 and [o for _, o in ops] == ["ReduceMean", "Sub", "Pow", "ReduceMean", "ElementwiseChain"]
+
+
+def test_chain_fusion_boundaries():
+    # C1: Add bias -> Mul scalar
+    c1 = [W.node("Add", ["x", "bias"], ["h"], "add"), W.node("Mul", ["h", "k"], ["y"], "mul")]
+    inits = [("bias", np.zeros(8, np.float32)), ("k", np.array(0.125, np.float32))]
+    assert _fused(c1, inits) == (1, [("mul", "ElementwiseChain")])
+    # a node using the chain value twice ends the chain before it
+    sq = [W.node("Sub", ["x", "bias"], ["h"], "sub"), W.node("Mul", ["h", "h"], ["y"], "sq")]
+    assert _fused(sq, inits) == (0, [("sub", "Sub"), ("sq", "Mul")])
+    # a non-elementwise consumer ends it; single nodes are left alone
+    sm = [W.node("Add", ["x", "bias"], ["h"], "add"), W.node("Softmax", ["h"], ["y"], "sm")]
+    assert _fused(sm, inits)[0] == 1   # Add -> Softmax is the AddSoftmax pattern
+    rs = [W.node("Add", ["x", "bias"], ["h"], "add"), W.node("ReduceSum", ["h"], ["y"], "rs")]
+    assert _fused(rs, inits) == (0, [("add", "Add"), ("rs", "ReduceSum")])
+    # at most 8 distinct inputs per chain: a ninth starts a new chain
+    nodes, prev = [], "x"
+    for k in range(9):
+        nodes.append(W.node("Add", [prev, f"c{k}"], [f"t{k}" if k < 8 else "y"], f"n{k}"))
+        prev = f"t{k}"
+    inits9 = [(f"c{k}", np.full(8, k, np.float32)) for k in range(9)]
+    n, ops = _fused(nodes, inits9)
+    assert (n, ops) == (2, [("n6", "ElementwiseChain"), ("n8", "ElementwiseChain")])
 
 
 def test_graph_builder_api_and_fusion_without_onnx_bytes():
