@@ -590,14 +590,15 @@ hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStre
 // result is bit-identical to running the nodes one by one.  The instruction
 // list is uniform across the launch: the switch below does not diverge.
 // ---------------------------------------------------------------------------
+// the operands are ordered by selects rather than by two copies of the op: the division
+// and power sequences are long, and a smaller kernel starts faster on a cold instruction cache
 template <int OP, int V>
 __device__ __forceinline__ void chain_bin(Vec<float, V> &acc, const Vec<float, V> &x, bool x_left) {
-    if (x_left) {
 #pragma unroll
-        for (int k = 0; k < V; k++) acc.v[k] = bin_apply<OP, float>(x.v[k], acc.v[k], 0, nullptr);
-    } else {
-#pragma unroll
-        for (int k = 0; k < V; k++) acc.v[k] = bin_apply<OP, float>(acc.v[k], x.v[k], 0, nullptr);
+    for (int k = 0; k < V; k++) {
+        const float l = x_left ? x.v[k] : acc.v[k];
+        const float r = x_left ? acc.v[k] : x.v[k];
+        acc.v[k] = bin_apply<OP, float>(l, r, 0, nullptr);
     }
 }
 
@@ -645,16 +646,13 @@ __global__ __launch_bounds__(kBlock) void k_chain(ChainArgs A) {
 #pragma unroll
         for (int j = 0; j < NIN; j++) off[j] = 0;
         uint32_t rr = row;
+        for (int d = 0; d < A.nouter; d++) {
+            const uint32_t q = fdiv(rr, A.odiv[d]);
+            const int64_t id = rr - q * A.odiv[d].d;
 #pragma unroll
-        for (int d = 0; d < kMaxOuter; d++) {
-            if (d < A.nouter) {
-                const uint32_t q = fdiv(rr, A.odiv[d]);
-                const int64_t id = rr - q * A.odiv[d].d;
-#pragma unroll
-                for (int j = 0; j < NIN; j++)
-                    if (j < A.n_in) off[j] += id * A.str[j][d];
-                rr = q;
-            }
+            for (int j = 0; j < NIN; j++)
+                if (j < A.n_in) off[j] += id * A.str[j][d];
+            rr = q;
         }
         const int64_t col = (int64_t)cv * V;
         Vec<float, V> x[NIN];
@@ -673,10 +671,7 @@ __global__ __launch_bounds__(kBlock) void k_chain(ChainArgs A) {
             }
         }
         Vec<float, V> acc = x[0];
-        // unrolled: each instruction's op and operand are fixed argument offsets, loaded once
-#pragma unroll
-        for (int i = 0; i < kChainMaxOps; i++) {
-            if (i >= A.n_ops) break;
+        for (int i = 0; i < A.n_ops; i++) {
             const int o = A.operand[i];
             const int j = o < 0 ? -o - 1 : o;
             Vec<float, V> xj = x[0];
