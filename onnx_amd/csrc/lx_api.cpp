@@ -15,6 +15,7 @@
 #include <vector>
 
 #include "../../include/lonnx.h"
+#include "lx_internal.h"
 #include "lx_kernels.h"
 #include "lx_pool.h"
 
@@ -216,6 +217,67 @@ int ensure_workspace(int64_t bytes) {
 }
 
 // reads back the device error record (synchronises the stream)
+// ---------------------------------------------------------------------------
+// device-side checks: immediate (reset, launch, read back) or deferred into a
+// caller's slot (api_defer_checks)
+// ---------------------------------------------------------------------------
+thread_local ErrFlags *t_defer_slot = nullptr;
+thread_local DeferredCheck *t_defer_rec = nullptr;
+
+int read_errs(ErrFlags *out);
+
+// the error record a checking launch writes: the deferred slot (already cleared by its owner) or
+// the library's own record, cleared here
+int check_begin(int kind, int dst, ErrFlags **errs) {
+    if (t_defer_slot) {
+        if (t_defer_rec) {
+            t_defer_rec->kind = kind;
+            t_defer_rec->dst = dst;
+        }
+        *errs = t_defer_slot;
+        return LX_OK;
+    }
+    HIPCHECK(launch_reset_errs(g.errs, g.stream), "reset error flags");
+    *errs = g.errs;
+    return LX_OK;
+}
+
+int check_status(int kind, int dst, const ErrFlags &e) {
+    switch (kind) {
+    case kCheckGather:
+        if (e.first_ovf != ~0ull) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
+        return LX_OK;
+    case kCheckDiv:
+        if (e.first_dbz == ~0ull && e.first_ovf == ~0ull) return LX_OK;
+        if (e.first_dbz <= e.first_ovf) return set_err(LX_ERR_DIVIDE_BY_ZERO, "Attempted to divide by zero.");
+        return set_err(LX_ERR_OVERFLOW, "Arithmetic operation resulted in an overflow.");
+    case kCheckCast: {
+        if (e.first_ovf == ~0ull) return LX_OK;
+        const char *what = "an Int32";
+        switch (dst) {
+        case LX_UINT8: what = "an unsigned byte"; break;
+        case LX_INT8: what = "a signed byte"; break;
+        case LX_INT16: what = "an Int16"; break;
+        case LX_UINT16: what = "a UInt16"; break;
+        case LX_UINT32: what = "a UInt32"; break;
+        case LX_INT64: what = "an Int64"; break;
+        case LX_UINT64: what = "a UInt64"; break;
+        }
+        return set_err(LX_ERR_OVERFLOW, "Value was either too large or too small for %s.", what);
+    }
+    default: return LX_OK;
+    }
+}
+
+// after the launch: nothing when deferred, else the read-back verdict
+int check_end(int kind, int dst) {
+    if (t_defer_slot) return LX_OK;
+    ErrFlags e;
+    int st = read_errs(&e);
+    if (st) return st;
+    return check_status(kind, dst, e);
+}
+
 int read_errs(ErrFlags *out) {
     // the device-side checks end in a host read; a stream under capture cannot wait for it
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -405,18 +467,10 @@ int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     }
     }
     const bool int_div = op == kDiv && (A->dtype == LX_INT32 || A->dtype == LX_INT64 || A->dtype == LX_UINT8);
-    if (int_div) HIPCHECK(launch_reset_errs(g.errs, g.stream), "reset error flags");
-    HIPCHECK(launch_binary(args, g.errs, g.stream), opn);
-    if (int_div) {
-        ErrFlags e;
-        if ((st = read_errs(&e))) return st;
-        if (e.first_dbz != ~0ull || e.first_ovf != ~0ull) {
-            if (e.first_dbz <= e.first_ovf)
-                return set_err(LX_ERR_DIVIDE_BY_ZERO, "Attempted to divide by zero.");
-            return set_err(LX_ERR_OVERFLOW, "Arithmetic operation resulted in an overflow.");
-        }
-    }
-    return LX_OK;
+    ErrFlags *errs = g.errs;
+    if (int_div && (st = check_begin(kCheckDiv, 0, &errs))) return st;
+    HIPCHECK(launch_binary(args, errs, g.stream), opn);
+    return int_div ? check_end(kCheckDiv, 0) : LX_OK;
 }
 
 int run_unary(const char *opn, int op, const lx_tensor *X, const char *xname, lx_tensor *Y) {
@@ -597,6 +651,11 @@ bool api_initialized() { return g.init; }
 hipStream_t api_stream() { return g.stream; }
 int64_t api_esize(int dtype) { return esize(dtype); }
 const char *api_dtype_name(int dtype) { return dtype_name(dtype); }
+void api_defer_checks(ErrFlags *slot, DeferredCheck *rec) {
+    t_defer_slot = slot;
+    t_defer_rec = rec;
+}
+int api_check_status(const DeferredCheck &rec, const ErrFlags &flags) { return check_status(rec.kind, rec.dst, flags); }
 }  // namespace lx
 
 // ===========================================================================
@@ -785,26 +844,10 @@ int lx_Cast(const lx_tensor *X, int64_t to, lx_tensor *Y) {
     // only conversions into an integer type can raise OverflowException
     const bool can_overflow = dst != LX_FLOAT && dst != LX_DOUBLE && dst != LX_BOOL && src != dst;
     const int vec = aligned16(X->data) && aligned16(Y->data) ? 2 : 1;
-    if (can_overflow) HIPCHECK(launch_reset_errs(g.errs, g.stream), "reset error flags");
-    HIPCHECK(launch_cast(src, dst, X->data, Y->data, n, vec, g.errs, g.stream), "Cast");
-    if (can_overflow) {
-        ErrFlags e;
-        if ((st = read_errs(&e))) return st;
-        if (e.first_ovf != ~0ull) {
-            const char *what = "an Int32";
-            switch (dst) {
-            case LX_UINT8: what = "an unsigned byte"; break;
-            case LX_INT8: what = "a signed byte"; break;
-            case LX_INT16: what = "an Int16"; break;
-            case LX_UINT16: what = "a UInt16"; break;
-            case LX_UINT32: what = "a UInt32"; break;
-            case LX_INT64: what = "an Int64"; break;
-            case LX_UINT64: what = "a UInt64"; break;
-            }
-            return set_err(LX_ERR_OVERFLOW, "Value was either too large or too small for %s.", what);
-        }
-    }
-    return LX_OK;
+    ErrFlags *errs = g.errs;
+    if (can_overflow && (st = check_begin(kCheckCast, dst, &errs))) return st;
+    HIPCHECK(launch_cast(src, dst, X->data, Y->data, n, vec, errs, g.stream), "Cast");
+    return can_overflow ? check_end(kCheckCast, dst) : LX_OK;
 }
 
 int lx_ReduceSum(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
@@ -1502,14 +1545,12 @@ extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_
         return set_err(LX_ERR_NOT_SUPPORTED, "Gathers of 2^31 elements or more are not supported.");
     // Int64 indices: ConvertToInt32 (ITensor.cs:172-183) throws on values outside int32; an index
     // that large is outside the axis anyway, so the range check below reports it
-    HIPCHECK(launch_reset_errs(g.errs, g.stream), "Gather");
+    ErrFlags *errs;
+    if ((st = check_begin(kCheckGather, 0, &errs))) return st;
     HIPCHECK(launch_gather((int)esize(data->dtype), indices->dtype, data->data, indices->data, Y->data, outer, nidx,
-                           inner, data->dims[ax], g.errs, g.stream),
+                           inner, data->dims[ax], errs, g.stream),
              "Gather");
-    ErrFlags ef;
-    if ((st = read_errs(&ef))) return st;
-    if (ef.first_ovf != ~0ull) return set_err(LX_ERR_INVALID_ARGUMENT, "Index was outside the bounds of the array.");
-    return LX_OK;
+    return check_end(kCheckGather, 0);
 }
 
 extern "C" int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, const int64_t *ends,

@@ -22,6 +22,7 @@
 #include "../../include/lonnx.h"
 #include "lx_graph.h"
 #include "lx_internal.h"
+#include "lx_kernels.h"
 #include "lx_pool.h"
 
 namespace lx {
@@ -966,6 +967,59 @@ std::string desc(const std::string &name, const lx_tensor &t) {
     return s;
 }
 
+// one 16-byte error record per node, cleared to "no failure" at the start of each execution
+// (a fill kernel, not a memset: the stream may be under capture)
+int prepare_check_slots(lx_graph *g) {
+    const int64_t want = 2 * (int64_t)std::max<size_t>(g->nodes.size(), 1);
+    if (!g->check_slots.store || g->check_slots.t.dims[0] < want) {
+        lx_tensor t;
+        memset(&t, 0, sizeof t);
+        int st = lx_tensor_alloc(LX_UINT64, 1, &want, &t);
+        if (st) return st;
+        g->check_slots = value_from_output(t);
+    }
+    hipError_t e = launch_fill(g->check_slots.t.data, want, 8, ~0ull, api_stream());
+    if (e != hipSuccess) return fail(LX_ERR_HIP, fmt("clearing the check records: %s", hipGetErrorString(e)));
+    return LX_OK;
+}
+
+// the first node before `limit` whose deferred device check failed: its index in *j, the status
+// returned (lx_last_error holds the operator's message), 0 when none failed
+int first_device_failure(lx_graph *g, const std::vector<DeferredCheck> &recs, int limit, int *j) {
+    int last = -1;
+    for (int k = 0; k < limit; k++)
+        if (recs[k].kind != kCheckNone) last = k;
+    if (last < 0) return LX_OK;
+    std::vector<ErrFlags> flags(last + 1);
+    hipError_t e = hipMemcpyAsync(flags.data(), g->check_slots.t.data, flags.size() * sizeof(ErrFlags),
+                                  hipMemcpyDeviceToHost, api_stream());
+    if (e == hipSuccess) e = hipStreamSynchronize(api_stream());
+    if (e != hipSuccess) {
+        *j = last;
+        return fail(LX_ERR_HIP, fmt("reading the check records: %s", hipGetErrorString(e)));
+    }
+    for (int k = 0; k <= last; k++) {
+        if (recs[k].kind == kCheckNone) continue;
+        const int st = api_check_status(recs[k], flags[k]);
+        if (st) {
+            *j = k;
+            return st;
+        }
+    }
+    return LX_OK;
+}
+
+// node j failed on the device: the outputs of j and of every later node are discarded (the reference
+// never ran them) and the failure is reported as node j's
+int report_device_failure(lx_graph *g, int j, int st) {
+    const std::string m = lx_last_error();
+    for (int k = j; k < (int)g->nodes.size(); k++)
+        for (const std::string &o : g->nodes[k].out) g->values.erase(o);
+    const GNode &nd = g->nodes[j];
+    const int num = nd.index >= 0 ? nd.index + 1 : j + 1;
+    return fail(st, fmt("Execution of node %d %s with op %s failed: %s", num, nd.name.c_str(), nd.op.c_str(), m.c_str()));
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1162,20 +1216,32 @@ int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_
     for (int k = 0; k < (int)g->nodes.size(); k++)
         for (auto &nm : g->nodes[k].in) last[nm] = k;
     std::set<std::string> keep(g->outputs.begin(), g->outputs.end());
+    // device checks (Gather indices, integer division, narrowing casts) are deferred: each node records
+    // into its own slot and the slots are read back once, after the last node -- or when a node fails
+    // on the host, to report an earlier device failure first, as node-by-node execution would
+    const int nn = (int)g->nodes.size();
+    if ((st = prepare_check_slots(g))) return st;
+    std::vector<DeferredCheck> recs(nn);
+    ErrFlags *slots = (ErrFlags *)g->check_slots.t.data;
     Exec X{g};
-    for (int k = 0; k < (int)g->nodes.size(); k++) {
+    for (int k = 0; k < nn; k++) {
         const GNode &node = g->nodes[k];
         std::vector<Value> outs;
+        api_defer_checks(slots + k, &recs[k]);
         st = run_node(X, node, outs);
+        api_defer_checks(nullptr, nullptr);
         if (!st && outs.size() != node.out.size())
             st = failure(fmt("The operation returned %d outputs but the graph node has %d outputs.", (int)outs.size(),
                              (int)node.out.size()));
         if (st) {
+            std::string m = lx_last_error();
+            int j = -1;
+            const int dst = first_device_failure(g, recs, k, &j);
+            if (dst) return report_device_failure(g, j, dst);
             // a fused node that fell back to its original nodes reports the one that failed, numbered
             // as in the graph before fusion, so the message is the unfused graph's
             const GNode &rep = X.failed ? *X.failed : node;
             const int num = rep.index >= 0 ? rep.index + 1 : k + 1;
-            std::string m = lx_last_error();
             return fail(st, fmt("Execution of node %d %s with op %s failed: %s", num, rep.name.c_str(), rep.op.c_str(),
                                 m.c_str()));
         }
@@ -1184,6 +1250,9 @@ int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_
         for (auto &nm : node.in)
             if (last[nm] == k && !keep.count(nm)) g->values.erase(nm);
     }
+    int j = -1;
+    const int dst = first_device_failure(g, recs, nn, &j);
+    if (dst) return report_device_failure(g, j, dst);
     return LX_OK;
 }
 

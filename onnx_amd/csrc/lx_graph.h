@@ -79,5 +79,6 @@ struct lx_graph {
     std::map<std::string, lx::Value> init_dev;  // initializers resident in HBM
     std::map<std::string, lx::Value> input_vals;  // graph.Inputs of the current execution
     std::map<std::string, lx::Value> values;    // node outputs of the current execution
+    lx::Value check_slots;                      // per node: device error record of its deferred checks
     std::vector<std::string> node_outputs;      // every name a node produces (IntermediateOutputs + Outputs)
 };

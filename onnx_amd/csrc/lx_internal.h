@@ -14,4 +14,18 @@ hipStream_t api_stream();
 int64_t api_esize(int dtype);
 const char *api_dtype_name(int dtype);
 
+// Deferred device checks (graph executor).  Integer Div, narrowing Cast and Gather check values on
+// the device; called alone they read the verdict back at once (one synchronisation).  While a slot
+// is set, they record into it instead -- the slot and the kind of check -- and return without
+// waiting; the caller reads many slots back in one copy later and turns them into the same status
+// and message with api_check_status.
+enum CheckKind { kCheckNone = 0, kCheckGather = 1, kCheckDiv = 2, kCheckCast = 3 };
+struct DeferredCheck {
+    int kind = kCheckNone;
+    int dst = 0;  // Cast: the target element type
+};
+struct ErrFlags;
+void api_defer_checks(ErrFlags *slot, DeferredCheck *rec);
+int api_check_status(const DeferredCheck &rec, const ErrFlags &flags);  // sets lx_last_error on failure
+
 }  // namespace lx

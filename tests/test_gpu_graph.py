@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from onnx_amd import DeviceTensor
+from onnx_amd import DeviceTensor, HipExecutionProvider as HIP
 from onnx_amd import _lib as L
 from onnx_amd.graph import ComputationalGraph, Model
 from oracle import graph_oracle as GO
@@ -219,3 +219,62 @@ def test_repeated_execution_reuses_device_memory(hip):
         y = g.Output("y").to_numpy()
         assert y1 is None or bits(y, y1)
         y1 = y
+
+
+# ---- device-side checks deferred to one readback per execution ------------------------------
+def _exec(nodes, inputs, inits, outputs, fuse=False):
+    model = W.model(nodes, [(k, v.dtype, v.shape) for k, v in inputs.items()],
+                    [(o, np.float32, ()) for o in outputs], inits)
+    g = Model.Load(model)
+    if fuse:
+        g.Fuse()
+    ok = g.Execute({k: DeviceTensor.from_numpy(v) for k, v in inputs.items()}, True)
+    return g, ok
+
+
+def test_deferred_gather_failure_is_reported_as_its_node(hip):
+    """An out-of-range Gather index is found after the last node ran (one readback per execution); the
+    failure names the Gather node with the operator's own message, and no later node's output is kept."""
+    table = np.arange(12, dtype=np.float32).reshape(4, 3)
+    nodes = [W.node("Gather", ["table", "ids"], ["e"], "gather"), W.node("Add", ["e", "one"], ["h"], "add"),
+             W.node("Mul", ["h", "two"], ["y"], "mul")]
+    inits = [("table", table), ("one", np.array(1.0, np.float32)), ("two", np.array(2.0, np.float32))]
+    g, ok = _exec(nodes, {"ids": np.array([0, 7], np.int64)}, inits, ["y"])
+    assert not ok
+    assert g.LastError == "Execution of node 1 gather with op Gather failed: Index was outside the bounds of the array."
+    assert "y" not in g.Outputs
+    # the same graph with valid indices runs through, and again after the failure
+    g2, ok = _exec(nodes, {"ids": np.array([3, -4], np.int64)}, inits, ["y"])
+    assert ok, g2.LastError
+    assert np.array_equal(g2.Output("y").to_numpy(), (table[[3, 0]] + 1) * 2)
+
+
+def test_deferred_device_failure_precedes_a_later_host_failure(hip):
+    """Node 1 fails on the device (Gather), node 3 on the host (shapes that do not broadcast): node by node
+    the reference stops at node 1, so node 1 is reported."""
+    nodes = [W.node("Gather", ["table", "ids"], ["e"], "gather"), W.node("Add", ["e", "one"], ["h"], "add"),
+             W.node("Mul", ["h", "bad"], ["y"], "mul")]
+    inits = [("table", np.ones((4, 3), np.float32)), ("one", np.array(1.0, np.float32)),
+             ("bad", np.ones(5, np.float32))]
+    g, ok = _exec(nodes, {"ids": np.array([9], np.int64)}, inits, ["y"])
+    assert not ok and g.LastError.startswith("Execution of node 1 gather with op Gather failed")
+    g, ok = _exec(nodes, {"ids": np.array([1], np.int64)}, inits, ["y"])
+    assert not ok and g.LastError.startswith("Execution of node 3 mul with op Mul failed")
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
+def test_deferred_integer_division_and_cast_checks(hip, dt):
+    a = np.array([7, -9, 4], dt)
+    nodes = [W.node("Div", ["a", "b"], ["q"], "div"), W.node("Cast", ["q"], ["y"], "cast", to=3)]  # to Int8
+    g, ok = _exec(nodes, {"a": a, "b": np.array([2, 0, 1], dt)}, [], ["y"])
+    assert not ok and g.LastError == "Execution of node 1 div with op Div failed: Attempted to divide by zero."
+    g, ok = _exec(nodes, {"a": np.array([7, -900, 4], dt), "b": np.array([2, 1, 1], dt)}, [], ["y"])
+    assert not ok
+    assert g.LastError == ("Execution of node 2 cast with op Cast failed: Value was either too large or too small "
+                           "for a signed byte.")
+    # the messages equal the operators' own
+    r = HIP.Div(DeviceTensor.from_numpy(a), DeviceTensor.from_numpy(np.array([2, 0, 1], dt)))
+    assert r.Message == "Attempted to divide by zero."
+    g, ok = _exec(nodes, {"a": a, "b": np.array([2, 3, 1], dt)}, [], ["y"])
+    assert ok, g.LastError
+    assert np.array_equal(g.Output("y").to_numpy(), np.array([3, -3, 4], np.int8))
