@@ -270,7 +270,40 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
                 raise RuntimeError(gr.LastError)
         record(f"C1 graph executor, {label} (host dispatch per execution)", nbytes, 49152,
                wall_time(torch, step, max(64, steps), warmup))
+        # the same execution recorded once into a HIP graph and replayed (one launch per execution)
+        assert gr.Capture([wA[0]]), gr.LastError
+
+        def replay(i, gr=gr):
+            if not gr.Replay():
+                raise RuntimeError(gr.LastError)
+        record(f"C1 graph executor, {label}, captured (replay per execution, one input buffer)", nbytes, 49152,
+               wall_time(torch, replay, max(64, steps), warmup))
         gr.close()
+    # launch-bound graphs of many small nodes: 40 alternating Add / Mul nodes on C1's shape (no fusion),
+    # host dispatch per execution against one captured replay
+    gr = ComputationalGraph(13)
+    gr.AddInput("x", np.float32, (1, 128, 384))
+    gr.AddInitializer("bias", B.cpu().numpy())
+    prev = "x"
+    for k in range(40):
+        gr.AddNode("Add" if k % 2 == 0 else "Mul", [prev, "bias"], [f"t{k}"], name=f"n{k}")
+        prev = f"t{k}"
+    gr.AddOutput(prev)
+
+    def step40(i):
+        if not gr.Execute([wA[0]]):
+            raise RuntimeError(gr.LastError)
+
+    def replay40(i):
+        if not gr.Replay():
+            raise RuntimeError(gr.LastError)
+    nb40 = 40 * 394752
+    record("40-node Add/Mul graph on [1,128,384] (host dispatch per execution)", nb40, 40 * 49152,
+           wall_time(torch, step40, max(32, steps // 4), warmup))
+    assert gr.Capture([wA[0]]), gr.LastError
+    record("40-node Add/Mul graph on [1,128,384], captured (replay per execution)", nb40, 40 * 49152,
+           wall_time(torch, replay40, max(32, steps // 4), warmup))
+    gr.close()
     del A, C, D, wA, wC, wD
     torch.cuda.empty_cache()
 
@@ -330,6 +363,14 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
                 raise RuntimeError(gr.LastError)
         ms = wall_time(torch, step, max(16, steps // 2), warmup)
         record(f"C2 LayerNorm graph executor, {label} (host dispatch per execution)", nbytes, 8 * 512 * 768, ms)
+        if not fuse:
+            assert gr.Capture([wX[0]]), gr.LastError
+
+            def replay(i, gr=gr):
+                if not gr.Replay():
+                    raise RuntimeError(gr.LastError)
+            record(f"C2 LayerNorm graph executor, {label}, captured (replay per execution, one input buffer)", nbytes, 8 * 512 * 768,
+                   wall_time(torch, replay, max(16, steps // 2), warmup))
         gr.close()
     del X, Y, tm, tf, wX, wY, wm, wf
     torch.cuda.empty_cache()

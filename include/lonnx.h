@@ -247,6 +247,21 @@ int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
  * (Add/Sub/Mul/Div/Pow/Sqrt/Erf) whose intermediates have one consumer by an ElementwiseChain node
  * (lx_ElementwiseChain).  *n_fused = number of fused nodes made. */
 int lx_graph_fuse(lx_graph *g, int32_t *n_fused);
+/* Capture (no reference counterpart; the reference dispatches every node from the host on every
+ * execution): runs lx_graph_execute once with these inputs, then records a second execution into a HIP
+ * graph and runs it, so the graph's outputs are those of one execution when it returns.  The record
+ * keeps the inputs' device addresses: lx_graph_replay runs every node's kernels again with one launch,
+ * on whatever the caller has written into those same input buffers since.  Device checks (Gather
+ * indices, integer division, narrowing casts) are read back after each replay and fail it with the
+ * failing node's message, as lx_graph_execute does.  A graph whose execution needs a host value of a
+ * device-computed tensor (a shape computed on the device), or whose constants change, cannot be
+ * captured (LX_ERR_NOT_SUPPORTED).  The device memory of the recorded execution stays reserved until
+ * lx_graph_release_capture, lx_graph_free or a change of the graph (lx_graph_add_*, lx_graph_set_attr_*,
+ * lx_graph_fuse). */
+int lx_graph_capture(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs,
+                     int32_t use_initializers);
+int lx_graph_replay(lx_graph *g);
+int lx_graph_release_capture(lx_graph *g);
 /* ComputationalGraph.Execute(userInputs, useInitializers) (ComputationalGraph.cs:199-272) with the
  * inputs given by name (the Dictionary overload, ComputationalGraph.cs:105-130) or, when names is
  * NULL, by position (the ITensor[] overload, 73-103).  Input tensors are borrowed. */

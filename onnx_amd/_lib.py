@@ -121,6 +121,9 @@ SIGNATURES = {
     "lx_graph_load_onnx": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.POINTER(_c.c_void_p)]),
     "lx_graph_fuse": (_c.c_int, [_c.c_void_p, _c.POINTER(_c.c_int32)]),
     "lx_graph_execute": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.POINTER(_c.c_char_p), _T, _c.c_int32]),
+    "lx_graph_capture": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.POINTER(_c.c_char_p), _T, _c.c_int32]),
+    "lx_graph_replay": (_c.c_int, [_c.c_void_p]),
+    "lx_graph_release_capture": (_c.c_int, [_c.c_void_p]),
     "lx_graph_execute_node": (_c.c_int, [_c.c_void_p, _c.c_char_p, _c.c_int32, _c.POINTER(_c.c_char_p), _T,
                                          _c.c_int32]),
     "lx_graph_output": (_c.c_int, [_c.c_void_p, _c.c_char_p, _T]),
@@ -138,6 +141,13 @@ SIGNATURES = {
 }
 
 _lib = None
+
+
+def pool_stats():
+    """(live, cached) bytes of the library's device memory pool."""
+    live, cached = ctypes.c_int64(), ctypes.c_int64()
+    lib().lx_pool_stats(ctypes.byref(live), ctypes.byref(cached))
+    return live.value, cached.value
 
 
 def lib():

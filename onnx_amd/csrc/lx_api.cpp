@@ -226,19 +226,15 @@ thread_local DeferredCheck *t_defer_rec = nullptr;
 
 int read_errs(ErrFlags *out);
 
-// the error record a checking launch writes: the deferred slot (already cleared by its owner) or
-// the library's own record, cleared here
+// the error record a checking launch writes, cleared first (one small kernel, never a memset:
+// the stream may be under capture): the deferred slot or the library's own record
 int check_begin(int kind, int dst, ErrFlags **errs) {
-    if (t_defer_slot) {
-        if (t_defer_rec) {
-            t_defer_rec->kind = kind;
-            t_defer_rec->dst = dst;
-        }
-        *errs = t_defer_slot;
-        return LX_OK;
+    *errs = t_defer_slot ? t_defer_slot : g.errs;
+    if (t_defer_slot && t_defer_rec) {
+        t_defer_rec->kind = kind;
+        t_defer_rec->dst = dst;
     }
-    HIPCHECK(launch_reset_errs(g.errs, g.stream), "reset error flags");
-    *errs = g.errs;
+    HIPCHECK(launch_reset_errs(*errs, g.stream), "reset error flags");
     return LX_OK;
 }
 

@@ -29,6 +29,14 @@ namespace lx {
 Storage::~Storage() {
     if (ptr) (void)pool_release(ptr);
 }
+
+GraphCapture::~GraphCapture() {
+    if (api_initialized()) (void)hipStreamSynchronize(api_stream());  // no replay may still run
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    values.clear();
+    pool_unhold(held);
+}
 }  // namespace lx
 
 using namespace lx;
@@ -124,8 +132,14 @@ Value value_from_output(const lx_tensor &y) {
     return v;
 }
 
+// set while an execution is being recorded into a HIP graph: no host round trip may happen then
+thread_local bool t_capturing = false;
+
 // a device tensor holding a copy of host data (Constant, Shape outputs)
 int value_from_host(const std::shared_ptr<HostTensor> &h, Value *out) {
+    if (t_capturing)
+        return fail(LX_ERR_NOT_SUPPORTED, "A host value would be uploaded during the recording: a graph whose "
+                                          "constants or shapes change between executions cannot be captured.");
     lx_tensor t;
     memset(&t, 0, sizeof t);
     int st = lx_tensor_alloc(h->dtype, h->rank, h->dims, &t);
@@ -145,6 +159,9 @@ int value_from_host(const std::shared_ptr<HostTensor> &h, Value *out) {
 // one, else one download (which synchronises the stream).
 int host_ints(Value &v, std::vector<int64_t> *out) {
     const int64_t n = numel(v.t);
+    if (!v.host && t_capturing)
+        return fail(LX_ERR_NOT_SUPPORTED, "A node reads a device-computed shape or axes tensor on the host: a "
+                                          "graph with such a node cannot be captured.");
     if (!v.host) {
         auto h = std::make_shared<HostTensor>();
         h->dtype = v.t.dtype;
@@ -164,6 +181,27 @@ int host_ints(Value &v, std::vector<int64_t> *out) {
         default: return failure("shape and axes tensors must hold Int32 or Int64 values");
         }
     }
+    return LX_OK;
+}
+
+bool same_host_tensor(const HostTensor &a, const HostTensor &b) {
+    if (a.dtype != b.dtype || a.rank != b.rank || a.bytes != b.bytes) return false;
+    for (int i = 0; i < a.rank; i++)
+        if (a.dims[i] != b.dims[i]) return false;
+    return true;
+}
+
+// the device copy of a node output computed on the host (Constant, Shape): uploaded once and
+// reused by later executions while the value is unchanged (no upload, no synchronisation)
+int value_from_host_cached(lx_graph *g, const std::string &name, const std::shared_ptr<HostTensor> &h, Value *out) {
+    auto it = g->host_cache.find(name);
+    if (it != g->host_cache.end() && it->second.host && same_host_tensor(*it->second.host, *h)) {
+        *out = it->second;
+        return LX_OK;
+    }
+    int st = value_from_host(h, out);
+    if (st) return st;
+    g->host_cache[name] = *out;
     return LX_OK;
 }
 
@@ -559,7 +597,7 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
             return not_supported(op);  // long / long[] / string values match no case of the switch
         }
         Value out;
-        if ((st = value_from_host(h, &out))) return st;
+        if ((st = value_from_host_cached(X.g, n.out.empty() ? n.name : n.out[0], h, &out))) return st;
         outs.push_back(out);
         return LX_OK;
     }
@@ -582,7 +620,7 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         h->bytes.resize(8 * (size_t)(e - s));
         for (int i = s; i < e; i++) memcpy(h->bytes.data() + 8 * (i - s), &a->t.dims[i], 8);
         Value out;
-        if ((st = value_from_host(h, &out))) return st;
+        if ((st = value_from_host_cached(X.g, n.out.empty() ? n.name : n.out[0], h, &out))) return st;
         outs.push_back(out);
         return LX_OK;
     }
@@ -967,9 +1005,21 @@ std::string desc(const std::string &name, const lx_tensor &t) {
     return s;
 }
 
-// one 16-byte error record per node, cleared to "no failure" at the start of each execution
-// (a fill kernel, not a memset: the stream may be under capture)
+// whether a node can run a device-side check: Gather (indices), Div (integer operands), Cast
+// (narrowing), or a fused node whose original nodes can
+bool may_check(const GNode &n) {
+    if (n.op == "Gather" || n.op == "Div" || n.op == "Cast") return true;
+    for (const GNode &m : n.fused_from)
+        if (may_check(m)) return true;
+    return false;
+}
+
+// one 16-byte error record per node; a node clears its record when it launches a check, so
+// graphs whose checking-capable nodes run on floats (Div) pay nothing
 int prepare_check_slots(lx_graph *g) {
+    bool any = false;
+    for (const GNode &n : g->nodes) any = any || may_check(n);
+    if (!any) return LX_OK;
     const int64_t want = 2 * (int64_t)std::max<size_t>(g->nodes.size(), 1);
     if (!g->check_slots.store || g->check_slots.t.dims[0] < want) {
         lx_tensor t;
@@ -978,8 +1028,6 @@ int prepare_check_slots(lx_graph *g) {
         if (st) return st;
         g->check_slots = value_from_output(t);
     }
-    hipError_t e = launch_fill(g->check_slots.t.data, want, 8, ~0ull, api_stream());
-    if (e != hipSuccess) return fail(LX_ERR_HIP, fmt("clearing the check records: %s", hipGetErrorString(e)));
     return LX_OK;
 }
 
@@ -1020,6 +1068,83 @@ int report_device_failure(lx_graph *g, int j, int st) {
     return fail(st, fmt("Execution of node %d %s with op %s failed: %s", num, nd.name.c_str(), nd.op.c_str(), m.c_str()));
 }
 
+// ComputationalGraph.Execute (ComputationalGraph.cs:199-272).  recording != null: the execution is
+// being captured into a HIP graph -- nothing may wait for the device, so the deferred checks are
+// handed to the caller (who reads them after each replay) instead of read back here.
+int execute_impl(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs, int32_t use_initializers,
+                 std::vector<DeferredCheck> *recording) {
+    int st = upload_initializers(g);
+    if (st) return st;
+    g->values.clear();
+    g->input_vals.clear();
+    // ResolveInputs (ComputationalGraph.cs:73-130)
+    auto req = required_inputs(g, use_initializers != 0);
+    if ((size_t)n != req.size())
+        return failure(fmt("%d user input(s) required for graph execution but %d specified.", (int)req.size(), n));
+    for (size_t i = 0; i < req.size(); i++) {
+        const lx_tensor *t = nullptr;
+        if (names) {
+            for (int k = 0; k < n; k++)
+                if (names[k] && req[i]->name == names[k]) t = &inputs[k];
+            if (!t) return failure(fmt("User inputs do not contain required input %s.", req[i]->name.c_str()));
+        } else {
+            t = &inputs[i];
+        }
+        if (t->rank != req[i]->rank || t->dtype != req[i]->dtype)
+            return failure(fmt("Cannot use user input %s for required input %s. Tensor type or rank does not match.",
+                               desc("", *t).c_str(), req[i]->name.c_str()));
+        g->input_vals[req[i]->name] = borrowed(*t);
+    }
+    // liveness: the index of each name's last consumer
+    std::map<std::string, int> last;
+    for (int k = 0; k < (int)g->nodes.size(); k++)
+        for (auto &nm : g->nodes[k].in) last[nm] = k;
+    std::set<std::string> keep(g->outputs.begin(), g->outputs.end());
+    // device checks (Gather indices, integer division, narrowing casts) are deferred: each node records
+    // into its own slot and the slots are read back once, after the last node -- or when a node fails
+    // on the host, to report an earlier device failure first, as node-by-node execution would
+    const int nn = (int)g->nodes.size();
+    if ((st = prepare_check_slots(g))) return st;
+    std::vector<DeferredCheck> recs(nn);
+    ErrFlags *slots = (ErrFlags *)g->check_slots.t.data;
+    Exec X{g};
+    for (int k = 0; k < nn; k++) {
+        const GNode &node = g->nodes[k];
+        std::vector<Value> outs;
+        // a node that cannot check gets no slot: a check it did make would be read back at once
+        api_defer_checks(slots && may_check(node) ? slots + k : nullptr, &recs[k]);
+        st = run_node(X, node, outs);
+        api_defer_checks(nullptr, nullptr);
+        if (!st && outs.size() != node.out.size())
+            st = failure(fmt("The operation returned %d outputs but the graph node has %d outputs.", (int)outs.size(),
+                             (int)node.out.size()));
+        if (st) {
+            std::string m = lx_last_error();
+            int j = -1;
+            const int dst = recording ? 0 : first_device_failure(g, recs, k, &j);
+            if (dst) return report_device_failure(g, j, dst);
+            // a fused node that fell back to its original nodes reports the one that failed, numbered
+            // as in the graph before fusion, so the message is the unfused graph's
+            const GNode &rep = X.failed ? *X.failed : node;
+            const int num = rep.index >= 0 ? rep.index + 1 : k + 1;
+            return fail(st, fmt("Execution of node %d %s with op %s failed: %s", num, rep.name.c_str(), rep.op.c_str(),
+                                m.c_str()));
+        }
+        for (size_t i = 0; i < outs.size(); i++) g->values[node.out[i]] = outs[i];
+        // intermediates whose last consumer has run go back to the pool (aliases keep their block)
+        for (auto &nm : node.in)
+            if (last[nm] == k && !keep.count(nm)) g->values.erase(nm);
+    }
+    if (recording) {
+        *recording = recs;
+        return LX_OK;
+    }
+    int j = -1;
+    const int dst = first_device_failure(g, recs, nn, &j);
+    if (dst) return report_device_failure(g, j, dst);
+    return LX_OK;
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -1041,6 +1166,7 @@ int lx_graph_free(lx_graph *g) {
 
 int lx_graph_add_input(lx_graph *g, const char *name, int32_t dtype, int32_t rank, const int64_t *dims) {
     if (!g || !name) return failure("null argument");
+    g->capture.reset();
     if (rank < 0 || rank > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
     GInput in;
     in.name = name;
@@ -1053,6 +1179,7 @@ int lx_graph_add_input(lx_graph *g, const char *name, int32_t dtype, int32_t ran
 
 int lx_graph_add_output(lx_graph *g, const char *name) {
     if (!g || !name) return failure("null argument");
+    g->capture.reset();
     g->outputs.push_back(name);
     return LX_OK;
 }
@@ -1060,6 +1187,7 @@ int lx_graph_add_output(lx_graph *g, const char *name) {
 int lx_graph_add_initializer(lx_graph *g, const char *name, int32_t dtype, int32_t rank, const int64_t *dims,
                              const void *host, int64_t nbytes) {
     if (!g || !name) return failure("null argument");
+    g->capture.reset();
     if (rank < 0 || rank > LX_MAX_RANK) return fail(LX_ERR_NOT_SUPPORTED, fmt("At most %d axes are supported.", LX_MAX_RANK));
     auto h = std::make_shared<HostTensor>();
     h->dtype = dtype;
@@ -1080,6 +1208,7 @@ int lx_graph_add_initializer(lx_graph *g, const char *name, int32_t dtype, int32
 int lx_graph_add_node(lx_graph *g, const char *name, const char *op_type, int32_t n_in, const char *const *inputs,
                       int32_t n_out, const char *const *outputs, int32_t *index) {
     if (!g || !op_type || n_in < 0 || n_out < 0) return failure("null argument");
+    g->capture.reset();
     GNode n;
     n.name = name ? name : "";
     n.op = op_type;
@@ -1096,6 +1225,7 @@ int lx_graph_add_node(lx_graph *g, const char *name, const char *op_type, int32_
 
 static int node_at(lx_graph *g, int32_t node, const char *attr, GNode **n) {
     if (!g || !attr || node < 0 || node >= (int32_t)g->nodes.size()) return failure("invalid node index or attribute name");
+    g->capture.reset();
     *n = &g->nodes[node];
     return LX_OK;
 }
@@ -1178,6 +1308,7 @@ int lx_graph_set_attr_tensor(lx_graph *g, int32_t node, const char *attr, int32_
 
 int lx_graph_fuse(lx_graph *g, int32_t *n_fused) {
     if (!g) return failure("null graph");
+    g->capture.reset();
     Fuser f;
     f.g = g;
     int k = f.run();
@@ -1189,70 +1320,78 @@ int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_
                      int32_t use_initializers) {
     if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
     if (!g || n < 0 || (n > 0 && !inputs)) return failure("null argument");
-    int st = upload_initializers(g);
+    return execute_impl(g, n, names, inputs, use_initializers, nullptr);
+}
+
+int lx_graph_capture(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs,
+                     int32_t use_initializers) {
+    if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
+    if (!g || n < 0 || (n > 0 && !inputs)) return failure("null argument");
+    g->capture.reset();
+    hipStream_t s = api_stream();
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return fail(LX_ERR_NOT_SUPPORTED, "The library stream is already being captured.");
+    // one ordinary execution first: it uploads the constants, sizes the reduction workspace and
+    // fills the pool's free lists, so the recording needs no upload and (mostly) no new block
+    int st = execute_impl(g, n, names, inputs, use_initializers, nullptr);
     if (st) return st;
+    hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(LX_ERR_HIP, fmt("capture: %s", hipGetErrorString(e)));
     g->values.clear();
-    g->input_vals.clear();
-    // ResolveInputs (ComputationalGraph.cs:73-130)
-    auto req = required_inputs(g, use_initializers != 0);
-    if ((size_t)n != req.size())
-        return failure(fmt("%d user input(s) required for graph execution but %d specified.", (int)req.size(), n));
-    for (size_t i = 0; i < req.size(); i++) {
-        const lx_tensor *t = nullptr;
-        if (names) {
-            for (int k = 0; k < n; k++)
-                if (names[k] && req[i]->name == names[k]) t = &inputs[k];
-            if (!t) return failure(fmt("User inputs do not contain required input %s.", req[i]->name.c_str()));
-        } else {
-            t = &inputs[i];
-        }
-        if (t->rank != req[i]->rank || t->dtype != req[i]->dtype)
-            return failure(fmt("Cannot use user input %s for required input %s. Tensor type or rank does not match.",
-                               desc("", *t).c_str(), req[i]->name.c_str()));
-        g->input_vals[req[i]->name] = borrowed(*t);
+    auto cap = std::make_unique<GraphCapture>();
+    pool_record_begin();
+    e = hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed);
+    if (e != hipSuccess) {
+        pool_record_end();
+        return fail(LX_ERR_HIP, fmt("hipStreamBeginCapture: %s", hipGetErrorString(e)));
     }
-    // liveness: the index of each name's last consumer
-    std::map<std::string, int> last;
-    for (int k = 0; k < (int)g->nodes.size(); k++)
-        for (auto &nm : g->nodes[k].in) last[nm] = k;
-    std::set<std::string> keep(g->outputs.begin(), g->outputs.end());
-    // device checks (Gather indices, integer division, narrowing casts) are deferred: each node records
-    // into its own slot and the slots are read back once, after the last node -- or when a node fails
-    // on the host, to report an earlier device failure first, as node-by-node execution would
-    const int nn = (int)g->nodes.size();
-    if ((st = prepare_check_slots(g))) return st;
-    std::vector<DeferredCheck> recs(nn);
-    ErrFlags *slots = (ErrFlags *)g->check_slots.t.data;
-    Exec X{g};
-    for (int k = 0; k < nn; k++) {
-        const GNode &node = g->nodes[k];
-        std::vector<Value> outs;
-        api_defer_checks(slots + k, &recs[k]);
-        st = run_node(X, node, outs);
-        api_defer_checks(nullptr, nullptr);
-        if (!st && outs.size() != node.out.size())
-            st = failure(fmt("The operation returned %d outputs but the graph node has %d outputs.", (int)outs.size(),
-                             (int)node.out.size()));
-        if (st) {
-            std::string m = lx_last_error();
-            int j = -1;
-            const int dst = first_device_failure(g, recs, k, &j);
-            if (dst) return report_device_failure(g, j, dst);
-            // a fused node that fell back to its original nodes reports the one that failed, numbered
-            // as in the graph before fusion, so the message is the unfused graph's
-            const GNode &rep = X.failed ? *X.failed : node;
-            const int num = rep.index >= 0 ? rep.index + 1 : k + 1;
-            return fail(st, fmt("Execution of node %d %s with op %s failed: %s", num, rep.name.c_str(), rep.op.c_str(),
-                                m.c_str()));
-        }
-        for (size_t i = 0; i < outs.size(); i++) g->values[node.out[i]] = outs[i];
-        // intermediates whose last consumer has run go back to the pool (aliases keep their block)
-        for (auto &nm : node.in)
-            if (last[nm] == k && !keep.count(nm)) g->values.erase(nm);
+    t_capturing = true;
+    st = execute_impl(g, n, names, inputs, use_initializers, &cap->recs);
+    t_capturing = false;
+    const std::string msg = st ? std::string(lx_last_error()) : std::string();
+    e = hipStreamEndCapture(s, &cap->graph);
+    cap->held = pool_record_end();
+    if (!st && e != hipSuccess) st = fail(LX_ERR_HIP, fmt("hipStreamEndCapture: %s", hipGetErrorString(e)));
+    if (!st) {
+        e = hipGraphInstantiate(&cap->exec, cap->graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) st = fail(LX_ERR_HIP, fmt("hipGraphInstantiate: %s", hipGetErrorString(e)));
     }
+    if (st) {  // nothing of the recording ran: its blocks go back as they were released
+        if (!msg.empty()) fail(st, msg);
+        g->values.clear();
+        cap->held.clear();
+        return st;
+    }
+    // the recording's blocks stay reserved, and every older device tensor it reads stays alive
+    pool_hold(cap->held);
+    cap->values = g->values;
+    cap->input_vals = g->input_vals;
+    for (auto &kv : g->init_dev) cap->pinned.push_back(kv.second);
+    for (auto &kv : g->host_cache) cap->pinned.push_back(kv.second);
+    cap->pinned.push_back(g->check_slots);
+    g->capture = std::move(cap);
+    return lx_graph_replay(g);
+}
+
+int lx_graph_replay(lx_graph *g) {
+    if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
+    if (!g) return failure("null argument");
+    if (!g->capture) return fail(LX_ERR_INVALID_ARGUMENT, "The graph has no captured execution.");
+    GraphCapture &c = *g->capture;
+    g->values = c.values;
+    g->input_vals = c.input_vals;
+    hipError_t e = hipGraphLaunch(c.exec, api_stream());
+    if (e != hipSuccess) return fail(LX_ERR_HIP, fmt("hipGraphLaunch: %s", hipGetErrorString(e)));
     int j = -1;
-    const int dst = first_device_failure(g, recs, nn, &j);
-    if (dst) return report_device_failure(g, j, dst);
+    const int st = first_device_failure(g, c.recs, (int)c.recs.size(), &j);
+    if (st) return report_device_failure(g, j, st);
+    return LX_OK;
+}
+
+int lx_graph_release_capture(lx_graph *g) {
+    if (!g) return failure("null argument");
+    g->capture.reset();
     return LX_OK;
 }
 

@@ -7,7 +7,10 @@
 #include <string>
 #include <vector>
 
+#include <hip/hip_runtime.h>
+
 #include "../../include/lonnx.h"
+#include "lx_internal.h"
 
 namespace lx {
 
@@ -67,6 +70,20 @@ struct GInput {
     int64_t dims[LX_MAX_RANK] = {0};
 };
 
+// One execution recorded into a HIP graph (lx_graph_capture): the instantiated
+// graph, the pool blocks its kernels use (held until release), references to
+// every pre-existing device tensor it reads, and the outputs it writes.
+struct GraphCapture {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    std::vector<void *> held;                   // pool blocks allocated while recording
+    std::map<std::string, Value> values;        // node outputs of the recorded execution
+    std::map<std::string, Value> input_vals;    // the caller's inputs it was recorded with
+    std::vector<Value> pinned;                  // initializers, cached constants, check records
+    std::vector<DeferredCheck> recs;            // the device checks recorded per node
+    ~GraphCapture();
+};
+
 }  // namespace lx
 
 struct lx_graph {
@@ -80,5 +97,7 @@ struct lx_graph {
     std::map<std::string, lx::Value> input_vals;  // graph.Inputs of the current execution
     std::map<std::string, lx::Value> values;    // node outputs of the current execution
     lx::Value check_slots;                      // per node: device error record of its deferred checks
+    std::map<std::string, lx::Value> host_cache;  // uploaded Constant / Shape outputs, reused while unchanged
+    std::unique_ptr<lx::GraphCapture> capture;    // lx_graph_capture's record, if any
     std::vector<std::string> node_outputs;      // every name a node produces (IntermediateOutputs + Outputs)
 };

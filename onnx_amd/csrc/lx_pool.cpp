@@ -1,6 +1,7 @@
 // lx_pool.cpp -- see lx_pool.h.
 #include "lx_pool.h"
 
+#include <algorithm>
 #include <mutex>
 #include <unordered_map>
 #include <vector>
@@ -14,6 +15,9 @@ struct PoolState {
     std::unordered_map<size_t, std::vector<void *>> free_lists;  // size class -> cached blocks
     std::unordered_map<void *, size_t> live;                     // block -> size class
     int64_t live_bytes = 0, cached_bytes = 0;
+    bool recording = false;
+    std::vector<void *> recorded;                                // blocks handed out while recording
+    std::unordered_map<void *, bool> held;                       // held block -> released by its owner
 };
 
 PoolState &pool() {
@@ -73,6 +77,7 @@ hipError_t pool_alloc(size_t bytes, void **p, size_t *cap, hipStream_t s) {
     }
     ps.live[*p] = c;
     ps.live_bytes += (int64_t)c;
+    if (ps.recording) ps.recorded.push_back(*p);
     if (cap) *cap = c;
     return hipSuccess;
 }
@@ -82,6 +87,11 @@ bool pool_release(void *p) {
     std::lock_guard<std::mutex> lock(ps.mu);
     auto it = ps.live.find(p);
     if (it == ps.live.end()) return false;
+    auto h = ps.held.find(p);
+    if (h != ps.held.end()) {  // reserved for a captured graph: stays live until unheld
+        h->second = true;
+        return true;
+    }
     const size_t c = it->second;
     ps.live.erase(it);
     ps.live_bytes -= (int64_t)c;
@@ -96,6 +106,66 @@ hipError_t pool_trim(hipStream_t s) {
     hipError_t e = hipStreamSynchronize(s);
     if (e != hipSuccess) return e;
     return free_cached_locked(ps);
+}
+
+void pool_record_begin() {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    ps.recording = true;
+    ps.recorded.clear();
+}
+
+std::vector<void *> pool_record_end() {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    ps.recording = false;
+    std::vector<void *> out;
+    out.swap(ps.recorded);
+    std::sort(out.begin(), out.end());
+    out.erase(std::unique(out.begin(), out.end()), out.end());
+    return out;
+}
+
+void pool_hold(const std::vector<void *> &blocks) {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    for (void *p : blocks) {
+        if (ps.held.count(p)) continue;
+        if (ps.live.count(p)) {  // still owned
+            ps.held[p] = false;
+            continue;
+        }
+        // released into a free list during the recording: take it back out
+        for (auto &kv : ps.free_lists) {
+            auto f = std::find(kv.second.begin(), kv.second.end(), p);
+            if (f == kv.second.end()) continue;
+            kv.second.erase(f);
+            ps.cached_bytes -= (int64_t)kv.first;
+            ps.live[p] = kv.first;
+            ps.live_bytes += (int64_t)kv.first;
+            ps.held[p] = true;
+            break;
+        }
+    }
+}
+
+void pool_unhold(const std::vector<void *> &blocks) {
+    PoolState &ps = pool();
+    std::lock_guard<std::mutex> lock(ps.mu);
+    for (void *p : blocks) {
+        auto h = ps.held.find(p);
+        if (h == ps.held.end()) continue;
+        const bool released = h->second;
+        ps.held.erase(h);
+        if (!released) continue;  // its owner still holds it and releases it later
+        auto it = ps.live.find(p);
+        if (it == ps.live.end()) continue;
+        const size_t c = it->second;
+        ps.live.erase(it);
+        ps.live_bytes -= (int64_t)c;
+        ps.free_lists[c].push_back(p);
+        ps.cached_bytes += (int64_t)c;
+    }
 }
 
 void pool_stats(int64_t *live, int64_t *cached) {

@@ -12,6 +12,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace lx {
 
 // Rounded capacity a request of `bytes` occupies (>= bytes, >= 256).
@@ -30,5 +32,15 @@ hipError_t pool_trim(hipStream_t s);
 
 // Bytes held by live blocks and by cached (released) blocks.
 void pool_stats(int64_t *live, int64_t *cached);
+
+// HIP-graph capture support.  pool_record_begin / pool_record_end return every
+// block pool_alloc handed out in between (work captured into a HIP graph uses
+// them on every replay).  pool_hold keeps such blocks from being handed out
+// again -- a held block released by its owner stays reserved -- until
+// pool_unhold, which returns the released ones to the free lists.
+void pool_record_begin();
+std::vector<void *> pool_record_end();
+void pool_hold(const std::vector<void *> &blocks);
+void pool_unhold(const std::vector<void *> &blocks);
 
 }  // namespace lx

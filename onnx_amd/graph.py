@@ -58,6 +58,7 @@ class ComputationalGraph:
             _check(L.lib().lx_graph_create(opset, ctypes.byref(self._h)), "lx_graph_create")
         self.LastError = ""
         self._borrowed = []
+        self._captured = []
 
     # ---- construction (what Model.Load does from a ModelProto) -------------
     def AddInput(self, name: str, dtype, shape):
@@ -183,6 +184,29 @@ class ComputationalGraph:
         self.LastError = "" if st == L.OK else L.last_error()
         self.LastStatus = st
         return st == L.OK
+
+    def Capture(self, user_inputs: Union[Sequence, Dict[str, object]], use_initializers: bool = True) -> bool:
+        """Execute once, then record an execution into a HIP graph and run it (lx_graph_capture).  The
+        record keeps the inputs' device addresses: write new values into the same DeviceTensors and
+        call Replay()."""
+        init()
+        names, arr, n = self._pack(user_inputs)
+        self._captured = self._borrowed  # the record reads these buffers on every replay
+        st = L.lib().lx_graph_capture(self._h, n, names, arr, int(use_initializers))
+        self.LastError = "" if st == L.OK else L.last_error()
+        self.LastStatus = st
+        return st == L.OK
+
+    def Replay(self) -> bool:
+        """Runs the captured execution again with one launch (lx_graph_replay)."""
+        st = L.lib().lx_graph_replay(self._h)
+        self.LastError = "" if st == L.OK else L.last_error()
+        self.LastStatus = st
+        return st == L.OK
+
+    def ReleaseCapture(self):
+        L.lib().lx_graph_release_capture(self._h)
+        self._captured = []
 
     def ExecuteNode(self, user_inputs, node_label: str, use_initializers: bool = True) -> bool:
         """ComputationalGraph.ExecuteNode (ComputationalGraph.cs:274-334)."""

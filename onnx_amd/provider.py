@@ -73,6 +73,13 @@ class DeviceTensor:
                "lx_tensor_upload")
         return t
 
+    def upload(self, arr):
+        """Writes host values into this tensor's device storage in place (same shape and dtype): what a
+        captured graph execution's inputs need between replays."""
+        arr = np.ascontiguousarray(np.asarray(arr, dtype=self.dtype)).reshape(self.shape)
+        _check(L.lib().lx_tensor_upload(ctypes.byref(self.h), ctypes.c_void_p(arr.ctypes.data), arr.nbytes),
+               "lx_tensor_upload")
+
     @classmethod
     def wrap(cls, ptr: int, shape, dtype, capacity: int, keepalive=None):
         """Non-owning view of existing device memory (e.g. a torch tensor)."""

@@ -278,3 +278,77 @@ def test_deferred_integer_division_and_cast_checks(hip, dt):
     g, ok = _exec(nodes, {"a": a, "b": np.array([2, 3, 1], dt)}, [], ["y"])
     assert ok, g.LastError
     assert np.array_equal(g.Output("y").to_numpy(), np.array([3, -3, 4], np.int8))
+
+
+# ---- captured executions (lx_graph_capture / lx_graph_replay) ---------------------------------
+def _ln_graph(fuse):
+    model = W.model(ln_nodes(), [("x", np.float32, (4, 64, 128))], [("y", np.float32, ())], LN_INITS(128))
+    g = Model.Load(model)
+    if fuse:
+        g.Fuse()
+    return g
+
+
+@pytest.mark.parametrize("fuse", [False, True])
+def test_capture_replays_match_eager_executions(hip, fuse):
+    """Every replay, with new data written into the captured input buffer and eager executions and
+    synchronisations between the replays, equals an eager execution on the same data bit for bit."""
+    rng = np.random.default_rng(70)
+    g, eager = _ln_graph(fuse), _ln_graph(fuse)
+    xs = [(rng.standard_normal((4, 64, 128)) * 3).astype(np.float32) for _ in range(4)]
+    xd = DeviceTensor.from_numpy(xs[0])
+    assert g.Capture([xd]), g.LastError
+    for i, x in enumerate(xs):
+        xd.upload(x)
+        assert g.Replay(), g.LastError
+        got = g.Output("y").to_numpy()
+        assert eager.Execute([DeviceTensor.from_numpy(x)]), eager.LastError
+        assert bits(got, eager.Output("y").to_numpy()), i
+        # eager work on the same graph object between replays does not disturb the record
+        assert g.Execute([DeviceTensor.from_numpy(xs[(i + 1) % 4])]), g.LastError
+    g.ReleaseCapture()
+    assert not g.Replay() and "no captured execution" in g.LastError
+
+
+def test_capture_with_gather_reports_failures_per_replay(hip):
+    table = np.arange(12, dtype=np.float32).reshape(4, 3)
+    nodes = [W.node("Gather", ["table", "ids"], ["e"], "gather"), W.node("Mul", ["e", "two"], ["y"], "mul")]
+    model = W.model(nodes, [("ids", np.int64, (2,))], [("y", np.float32, ())],
+                    [("table", table), ("two", np.array(2.0, np.float32))])
+    g = Model.Load(model)
+    ids = DeviceTensor.from_numpy(np.array([0, 1], np.int64))
+    assert g.Capture([ids]), g.LastError
+    for v, good in (([3, 2], True), ([1, 4], False), ([-1, -4], True)):
+        ids.upload(np.array(v, np.int64))
+        assert g.Replay() == good, g.LastError
+        if good:
+            assert np.array_equal(g.Output("y").to_numpy(), table[v] * 2)
+        else:
+            assert g.LastError == ("Execution of node 1 gather with op Gather failed: Index was outside the bounds "
+                                   "of the array.")
+
+
+def test_capture_refuses_device_computed_shapes(hip):
+    """Reshape whose target shape is computed on the device needs that shape on the host mid-execution:
+    such a graph executes but cannot be captured."""
+    nodes = [W.node("Add", ["s", "zero"], ["shape"], "add"), W.node("Reshape", ["x", "shape"], ["y"], "reshape")]
+    model = W.model(nodes, [("x", np.float32, (2, 6)), ("s", np.int64, (2,))], [("y", np.float32, ())],
+                    [("zero", np.zeros(2, np.int64))])
+    g = Model.Load(model)
+    ins = {"x": DeviceTensor.from_numpy(np.arange(12, dtype=np.float32).reshape(2, 6)),
+           "s": DeviceTensor.from_numpy(np.array([3, 4], np.int64))}
+    assert g.Execute(ins), g.LastError
+    assert g.Output("y").to_numpy().shape == (3, 4)
+    assert not g.Capture(ins) and g.LastStatus == L.ERR_NOT_SUPPORTED
+    assert g.Execute(ins), g.LastError   # the stream is usable afterwards
+
+
+def test_capture_memory_is_released(hip):
+    g = _ln_graph(False)
+    x = DeviceTensor.from_numpy(np.ones((4, 64, 128), np.float32))
+    live0 = L.pool_stats()[0]
+    assert g.Capture([x]), g.LastError
+    assert g.Replay(), g.LastError
+    g.ReleaseCapture()
+    g.Reset()
+    assert L.pool_stats()[0] <= live0 + 4096   # the check records stay with the graph
