@@ -491,6 +491,33 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     del table, ids, emb
     torch.cuda.empty_cache()
 
+    # a whole BERT-base encoder layer (batch 8 x 512 tokens) through the graph runtime: 74 ONNX nodes
+    # node by node, fused (LayerNorm / GELU / mask+Softmax / residual chains), and the fused graph captured
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from bert_layer import bert_layer
+    from onnx_amd.graph import Model
+    model, bins, _, _ = bert_layer(8, 512, 5)
+    bdev = {k: DeviceTensor.from_numpy(v) for k, v in bins.items()}
+    layer_flops = 2.0 * 4096 * (4 * 768 * 768 + 2 * 768 * 3072) + 2 * 2.0 * 8 * 12 * 512 * 512 * 64
+    for label, fuse, capture in (("74 nodes", False, False), ("fused", True, False), ("fused, captured", True, True)):
+        gl = Model.Load(model)
+        if fuse:
+            gl.Fuse()
+        if capture:
+            assert gl.Capture(bdev), gl.LastError
+
+        def layer_step(i, gl=gl, capture=capture):
+            if not (gl.Replay() if capture else gl.Execute(bdev)):
+                raise RuntimeError(gl.LastError)
+        ms = wall_time(torch, layer_step, max(8, steps // 16), max(2, warmup // 4))
+        d = {"op": f"BERT-base encoder layer [8,512,768], {label} (per execution)", "us": round(ms * 1e3, 1),
+             "tokens_per_s": round(4096 / (ms * 1e-3), 1), "TFLOP/s": round(layer_flops / (ms * 1e-3) / 1e12, 2),
+             "flops": layer_flops}
+        log(json.dumps(d))
+        res.append(d)
+        gl.close()
+    del bdev
+
     # MatMul (row f2): fp32 MFMA, compute-bound; BERT-base shapes at batch 8 x 512 tokens
     for name, sa, sb in (("MatMul fp32 [4096,768]x[768,768] (dense)", (4096, 768), (768, 768)),
                          ("MatMul fp32 [4096,768]x[768,2304] (fused QKV projection)", (4096, 768), (768, 2304)),

@@ -1,0 +1,57 @@
+"""A whole BERT-base encoder layer through the device graph runtime: every
+operator family of the device path at once (elementwise / broadcast /
+reductions / Softmax, MatMul, data movement, the graph executor with and
+without fusion, capture).
+
+Bar: the layer composes ~60 float32 operators whose summation orders differ from
+the reference's serial loops, so it is judged against an independent float64
+evaluation: the device's largest error is at most 4x the largest error of the
+reference's own float32 node-by-node evaluation (the oracle) plus 1e-6."""
+import numpy as np
+import pytest
+
+from onnx_amd import DeviceTensor
+from onnx_amd.graph import Model
+from oracle import graph_oracle as GO
+
+from bert_layer import bert_layer, bert_layer_f64
+from test_gpu_graph import _dict_nodes
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def layer():
+    model, ins, inits, nodes = bert_layer(2, 64, 11)
+    ref = GO.run(_dict_nodes(nodes), ins, inits)["y"]
+    t64 = bert_layer_f64(ins, inits)
+    return model, ins, ref, t64
+
+
+@pytest.mark.parametrize("mode", ["nodes", "fused", "captured"])
+def test_bert_layer_accuracy(hip, layer, mode):
+    model, ins, ref, t64 = layer
+    g = Model.Load(model)
+    if mode != "nodes":
+        assert g.Fuse() == 6
+    dev = {k: DeviceTensor.from_numpy(v) for k, v in ins.items()}
+    ok = g.Capture(dev) if mode == "captured" else g.Execute(dev)
+    assert ok, g.LastError
+    y = g.Output("y").to_numpy()
+    assert y.shape == ref.shape and np.isfinite(y).all()
+    err_ref = np.abs(ref.astype(np.float64) - t64).max()
+    err_dev = np.abs(y.astype(np.float64) - t64).max()
+    print(f"BERT layer {mode}: device max error {err_dev:.3g}, reference float32 max error {err_ref:.3g}")
+    assert err_dev <= 4 * err_ref + 1e-6, (err_dev, err_ref)
+    if mode == "captured":   # a replay on new inputs written into the captured buffers
+        x2 = (ins["x"] * 0.5).astype(np.float32)
+        dev["x"].upload(x2)
+        assert g.Replay(), g.LastError
+        t64b = bert_layer_f64({"x": x2, "mask": ins["mask"]}, _inits(layer))
+        assert np.abs(g.Output("y").to_numpy().astype(np.float64) - t64b).max() <= 4 * err_ref + 1e-6
+
+
+def _inits(layer):
+    # the initializers of the fixture's model (same seed)
+    _, _, inits, _ = bert_layer(2, 64, 11)
+    return inits

@@ -207,3 +207,26 @@ def test_graph_builder_api_and_fusion_without_onnx_bytes():
     g.AddNode("Mul", ["half", "c"], ["y"], "mul2")
     g.AddOutput("y")
     assert g.Fuse() == 1 and [n.Op for n in g.Nodes] == ["GeluErf"]
+
+
+# ---- a whole BERT-base encoder layer ---------------------------------------------------------
+def test_bert_layer_oracle_against_float64():
+    """The oracle's node-by-node float32 evaluation of a BERT layer (the reference's arithmetic) stays within
+    1e-5 of an independent float64 evaluation: pins the graph oracle on a composite of every op kind."""
+    from bert_layer import bert_layer, bert_layer_f64
+    from oracle import graph_oracle as GO
+    from test_gpu_graph import _dict_nodes
+    _, ins, inits, nodes = bert_layer(1, 16, 3)
+    ref = GO.run(_dict_nodes(nodes), ins, inits)["y"]
+    assert np.abs(ref - bert_layer_f64(ins, inits)).max() < 1e-5
+
+
+def test_bert_layer_fusion_plan():
+    from bert_layer import bert_layer
+    model, _, _, _ = bert_layer(1, 16, 3)
+    g = Model.Load(model)
+    assert g.Fuse() == 6
+    ops = [n.Op for n in g.Nodes]
+    assert ops.count("LayerNormDecomposed") == 2 and ops.count("GeluErf") == 1 and ops.count("AddSoftmax") == 1
+    assert ops.count("ElementwiseChain") == 2 and ops.count("MatMul") == 8
+    assert [n.Name for n in g.Nodes if n.Op == "ElementwiseChain"] == ["residual1", "residual2"]
