@@ -50,13 +50,14 @@ __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, in
 constexpr int kFBK = 16, kFPad = 4;
 
 template <int BM, int BN, int WM, int WN, bool VEC>
-__global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A, const float *__restrict__ B,
-                                                    float *__restrict__ C, MatMulArgs p) {
+__global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__restrict__ A, const float *__restrict__ B,
+                                                             float *__restrict__ C, MatMulArgs p) {
+    constexpr int NTHR = WM * WN * 64;               // threads of the block
     constexpr int WTM = BM / WM, WTN = BN / WN;      // wave tile
     constexpr int MT = WTM / 32, NT = WTN / 32;      // MFMA tiles per wave
-    static_assert(WM * WN == 4 && MT * 32 == WTM && NT * 32 == WTN, "four waves of whole 32x32 tiles");
+    static_assert((WM * WN == 4 || WM * WN == 8) && MT * 32 == WTM && NT * 32 == WTN, "waves of whole 32x32 tiles");
     constexpr int AV = BM * kFBK / 4, BV = BN * kFBK / 4;  // float4 of A and of B per K step
-    constexpr int LA = (AV + 255) / 256, LB = (BV + 255) / 256;
+    constexpr int LA = (AV + NTHR - 1) / NTHR, LB = (BV + NTHR - 1) / NTHR;
     constexpr int BQ = BN / 4;                       // float4 per B row
     __shared__ float As[2][kFBK][BM + kFPad];
     __shared__ float Bs[2][kFBK][BN + kFPad];
@@ -69,14 +70,14 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
     const float *Bb = B + bo;
     float *Cb = C + (p.batch_base + blockIdx.z) * (int64_t)M * N;
 
-    // global -> register staging one K step ahead: float4 e = t + 256 h of the step's
+    // global -> register staging one K step ahead: float4 e = t + NTHR h of the step's
     // A tile (row e / 4, k 4 (e % 4)) and B tile (k row e / BQ, column 4 (e % BQ))
     float4 ra[LA], rb[LB];
     auto load = [&](int k0) {
 #pragma unroll
         for (int h = 0; h < LA; h++) {
-            const int e = t + 256 * h;
-            if (AV % 256 != 0 && e >= AV) continue;
+            const int e = t + NTHR * h;
+            if (AV % NTHR != 0 && e >= AV) continue;
             const int r = row0 + e / 4, kk = k0 + (e % 4) * 4;
             if constexpr (VEC) {
                 ra[h] = (r < M && kk < K) ? *reinterpret_cast<const float4 *>(Ab + (int64_t)r * K + kk)
@@ -90,8 +91,8 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
         }
 #pragma unroll
         for (int h = 0; h < LB; h++) {
-            const int e = t + 256 * h;
-            if (BV % 256 != 0 && e >= BV) continue;
+            const int e = t + NTHR * h;
+            if (BV % NTHR != 0 && e >= BV) continue;
             const int kb = k0 + e / BQ, c = col0 + (e % BQ) * 4;
             if constexpr (VEC) {
                 rb[h] = (kb < K && c < N) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)kb * N + c)
@@ -107,8 +108,8 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
     auto store = [&](int buf) {
 #pragma unroll
         for (int h = 0; h < LA; h++) {
-            const int e = t + 256 * h;
-            if (AV % 256 != 0 && e >= AV) continue;
+            const int e = t + NTHR * h;
+            if (AV % NTHR != 0 && e >= AV) continue;
             const int r = e / 4, kk = (e % 4) * 4;
             As[buf][kk + 0][r] = ra[h].x;
             As[buf][kk + 1][r] = ra[h].y;
@@ -117,8 +118,8 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
         }
 #pragma unroll
         for (int h = 0; h < LB; h++) {
-            const int e = t + 256 * h;
-            if (BV % 256 != 0 && e >= BV) continue;
+            const int e = t + NTHR * h;
+            if (BV % NTHR != 0 && e >= BV) continue;
             *reinterpret_cast<float4 *>(&Bs[buf][e / BQ][(e % BQ) * 4]) = rb[h];
         }
     };
@@ -174,8 +175,9 @@ __global__ __launch_bounds__(256) void k_matmul_f32(const float *__restrict__ A,
 template <int BM, int BN, int WM, int WN>
 static void launch_f32(const float *a, const float *b, float *c, const MatMulArgs &p, bool vec, hipStream_t s) {
     dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
-    if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true>), g, dim3(256), 0, s, a, b, c, p);
-    else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false>), g, dim3(256), 0, s, a, b, c, p);
+    const dim3 blk(WM * WN * 64);
+    if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true>), g, blk, 0, s, a, b, c, p);
+    else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false>), g, blk, 0, s, a, b, c, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -336,11 +338,14 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
             int bm, bn;
             double eff;
         };
+        // (eight-wave 256x128 / 128x256 tiles measured 129.6 against 126.3 TFLOP/s at 4096^3 and far
+        // slower wherever they leave fewer than two blocks per CU: not worth a candidate)
         static const Tile cand[] = {{128, 128, 1.0}, {128, 96, 0.93}, {96, 128, 0.93},
                                     {128, 64, 0.85}, {64, 128, 0.85}, {64, 64, 0.65}};
+        constexpr int kCand = (int)(sizeof(cand) / sizeof(cand[0]));
         int best = 5;
         double best_cost = 0;
-        for (int i = 0; i < 6; i++) {
+        for (int i = 0; i < kCand; i++) {
             const int64_t blocks =
                 (int64_t)((p.m + cand[i].bm - 1) / cand[i].bm) * ((p.n + cand[i].bn - 1) / cand[i].bn) * p.batch;
             if (blocks < 512) continue;
