@@ -190,6 +190,10 @@ int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_
                            lx_tensor *Y);
 /* Add(S, mask) -> Softmax(axis) with the mask broadcast against S. */
 int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_tensor *Y);
+/* Div(S, scale) (divide != 0) or Mul(S, scale) -> [Add(., mask) when mask != NULL] -> Softmax(axis): the
+ * scaled attention scores of BERT-class models.  scale is a one-element tensor. */
+int lx_ScaleAddSoftmax(const lx_tensor *S, const lx_tensor *scale, int32_t divide, const lx_tensor *mask, int32_t axis,
+                       lx_tensor *Y);
 /* A linear chain of Float elementwise nodes in one pass (no single reference counterpart: it replaces
  * consecutive CPUExecutionProvider.Add/Sub/Mul/Div/Pow/Sqrt/Erf calls, CPUExecutionProvider.cs:82-236,
  * 380-409, whose intermediates have no other consumer).  acc = inputs[0]; instruction k applies ops[k]:
@@ -241,8 +245,8 @@ int lx_graph_set_attr_tensor(lx_graph *g, int32_t node, const char *attr, int32_
 int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
 /* Pattern fusion (no reference counterpart; the reference runs every node):
  * replaces the GELU subgraph (Div sqrt2 -> Erf -> Add 1 -> Mul x -> Mul 0.5), the decomposed
- * LayerNorm (ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul -> Add) and
- * Add(mask) -> Softmax by the fused kernels when every intermediate has exactly one consumer and is
+ * LayerNorm (ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul -> Add),
+ * Add(mask) -> Softmax and Div / Mul by a scalar constant -> Add(mask) -> Softmax by the fused kernels when every intermediate has exactly one consumer and is
  * not a graph output; then every linear chain of two or more Float elementwise nodes
  * (Add/Sub/Mul/Div/Pow/Sqrt/Erf) whose intermediates have one consumer by an ElementwiseChain node
  * (lx_ElementwiseChain).  *n_fused = number of fused nodes made. */

@@ -631,7 +631,7 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
 }
 
 int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
-                const char *opn);
+                const char *opn, const lx_tensor *scale = nullptr, int scale_div = 1);
 
 }  // namespace
 
@@ -873,6 +873,14 @@ int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_te
     return run_softmax(S, mask, axis, 1, Y, "Softmax");
 }
 
+int lx_ScaleAddSoftmax(const lx_tensor *S, const lx_tensor *scale, int32_t divide, const lx_tensor *mask, int32_t axis,
+                       lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!S) return missing_input(divide ? "Div" : "Mul", "A");
+    if (!scale) return missing_input(divide ? "Div" : "Mul", "B");
+    return run_softmax(S, mask, axis, 1, Y, "Softmax", scale, divide ? 1 : 0);
+}
+
 int lx_GeluErf(const lx_tensor *X, lx_tensor *Y) {
     REQUIRE_INIT();
     if (!X) return missing_input("Div", "A");
@@ -1048,12 +1056,19 @@ int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_
 
 namespace {
 
+// Softmax(axis) of X, optionally of (X / scale) or (X * scale) (a one-element tensor) and of that plus a
+// mask broadcast against X: the operators the reference runs one by one, each element rounded as they
+// round it, in one kernel when the row-per-wave kernel takes the whole operation, else node by node.
 int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
-                const char *opn) {
+                const char *opn, const lx_tensor *scale, int scale_div) {
     REQUIRE_INIT();
     if (!X) return missing_input(opn, "input");
     int st;
     if ((st = check_tensor(X, "input"))) return st;
+    if (scale) {
+        if ((st = check_tensor(scale, "scale"))) return st;
+        if (scale->dtype != X->dtype) return wrong_type_same("B");
+    }
     if (mask) {
         if ((st = check_tensor(mask, "mask"))) return st;
         if (mask->dtype != X->dtype) return wrong_type_same("B");
@@ -1077,16 +1092,17 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
     sa.r = r;
     sa.inner = inner;
     sa.vec = vec;
+    bool fusable = true;  // the row-per-wave kernel takes the mask (and the scale)
     if (mask) {
         lx_bcast_plan p;
         st = plan(X->rank, X->dims, mask->rank, mask->dims, &p);
-        if (st == LX_ERR_CANNOT_BROADCAST) return cannot_broadcast(X, mask);
-        if (st) return st;
-        if (X->dtype != LX_FLOAT && X->dtype != LX_DOUBLE) return type_not_supported("Add", "A", X);
-        bool same_shape = p.out_rank == X->rank;
+        if (st == LX_ERR_CANNOT_BROADCAST && !scale) return cannot_broadcast(X, mask);
+        if (st && st != LX_ERR_CANNOT_BROADCAST) return st;
+        if (X->dtype != LX_FLOAT && X->dtype != LX_DOUBLE && !scale) return type_not_supported("Add", "A", X);
+        bool same_shape = st == LX_OK && p.out_rank == X->rank;
         for (int i = 0; same_shape && i < X->rank; i++) same_shape = p.out_dims[i] == X->dims[i];
-        bool fusable = same_shape && softmax_mask_fusable(X->dtype, r, inner, outer, vec) &&
-                       (vec == 1 || aligned16(mask->data));
+        fusable = same_shape && softmax_mask_fusable(X->dtype, r, inner, outer, vec) &&
+                  (vec == 1 || aligned16(mask->data));
         if (fusable) {
             // mask strides in X's frame (no collapsing of the softmax axis)
             int64_t ms[LX_MAX_RANK];
@@ -1123,19 +1139,35 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
                 }
             }
         }
-        if (!fusable) {
+    }
+    if (scale) {
+        // the scale must leave X's shape as it is (one element, rank <= X's) for the kernel to apply it
+        bool ok = fusable && numel(scale) == 1 && scale->rank <= X->rank &&
+                  softmax_mask_fusable(X->dtype, r, inner, outer, vec) &&
+                  (X->dtype == LX_FLOAT || X->dtype == LX_DOUBLE);
+        if (!ok) {  // node by node: Div / Mul, then (Add +) Softmax
             lx_tensor t{};
-            st = run_binary(kAdd, X, mask, &t);
-            if (!st) st = run_softmax(&t, nullptr, ax, 1, Y, opn);
+            st = run_binary(scale_div ? kDiv : kMul, X, scale, &t);
+            if (!st) st = run_softmax(&t, mask, ax, 1, Y, opn);
             lx_tensor_free(&t);
             return st;
         }
+        sa.scale = scale->data;
+        sa.scale_div = scale_div;
+    }
+    if (mask && !fusable) {
+        lx_tensor t{};
+        st = run_binary(kAdd, X, mask, &t);
+        if (!st) st = run_softmax(&t, nullptr, ax, 1, Y, opn);
+        lx_tensor_free(&t);
+        return st;
     }
     if (X->dtype != LX_FLOAT && X->dtype != LX_DOUBLE) return type_not_supported(opn, "input", X);
     if ((st = prepare_output(Y, X->dtype, X->rank, X->dims))) return st;
     if (vec > 1 && !aligned16(Y->data)) {
         sa.vec = 1;
-        if (sa.mask && sa.r > 64 * 8) return set_err(LX_ERR_INVALID_ARGUMENT, "output storage must be 16-byte aligned");
+        if ((sa.mask || sa.scale) && sa.r > 64 * 8)
+            return set_err(LX_ERR_INVALID_ARGUMENT, "output storage must be 16-byte aligned");
     }
     sa.x = X->data;
     sa.y = Y->data;

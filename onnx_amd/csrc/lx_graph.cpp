@@ -654,6 +654,21 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!same) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
     }
+    if (op == "ScaleAddSoftmax") {
+        Value *sv, *cv, *mv;
+        if ((st = X.input(n, 0, &sv)) || (st = X.input(n, 1, &cv)) || (st = X.input(n, 2, &mv))) return st;
+        if (!sv || !cv || !mv || (sv->t.dtype != LX_FLOAT && sv->t.dtype != LX_DOUBLE) || cv->t.dtype != sv->t.dtype ||
+            mv->t.dtype != sv->t.dtype || numel(cv->t) != 1 || cv->t.rank > sv->t.rank)
+            return run_unfused(X, n, outs);
+        lx_bcast_plan p;
+        if (lx_plan_broadcast(sv->t.rank, sv->t.dims, mv->t.rank, mv->t.dims, &p) != LX_OK) return run_unfused(X, n, outs);
+        bool same = p.out_rank == sv->t.rank;
+        for (int i = 0; same && i < p.out_rank; i++) same = p.out_dims[i] == sv->t.dims[i];
+        if (!same) return run_unfused(X, n, outs);
+        int32_t axis = -1, divide = 1;
+        if (attr_int(n, "axis", &axis) < 0 || attr_int(n, "divide", &divide) < 0) return LX_ERR_INVALID_ARGUMENT;
+        return run_op([&](lx_tensor *y) { return lx_ScaleAddSoftmax(T(sv), T(cv), divide, T(mv), axis, y); }, outs);
+    }
     if (op == "ElementwiseChain") {
         std::vector<const lx_tensor *> ts;
         for (size_t k = 0; k < n.in.size(); k++) {
@@ -842,17 +857,46 @@ struct Fuser {
         return true;
     }
 
-    // Add(S, mask) -> Softmax
+    // Add(S, mask) -> Softmax, and Div(S, c) / Mul(S, c) -> Add(., mask) -> Softmax for a Float scalar
+    // constant c (the scaled attention scores)
     bool add_softmax(int i0, GNode *f, std::vector<int> *nodes) {
         if (!is(i0, "Add", 2)) return false;
         int i1 = only_consumer(N(i0).out[0]);
         if (!is(i1, "Softmax", 1)) return false;
+        auto ax = N(i1).attrs.find("axis");
+        if (ax != N(i1).attrs.end()) f->attrs["axis"] = ax->second;
+        f->out = N(i1).out;
+        for (int side = 0; side < 2; side++) {  // the Add operand that a scaling node produces
+            const std::string &sv = N(i0).in[side];
+            int is_ = -1;
+            for (int k = 0; k < i0; k++)
+                if (!used[k] && N(k).out.size() == 1 && N(k).out[0] == sv) is_ = k;
+            if (is_ < 0 || only_consumer(sv) != i0 || N(i0).in[1 - side] == sv) continue;
+            const GNode &sc = N(is_);
+            float c;
+            std::string src, cname;
+            int divide;
+            if (is(is_, "Div", 2) && scalar_f32(sc.in[1], &c)) {
+                src = sc.in[0], cname = sc.in[1], divide = 1;
+            } else if (is(is_, "Mul", 2) && scalar_f32(sc.in[1], &c)) {
+                src = sc.in[0], cname = sc.in[1], divide = 0;
+            } else if (is(is_, "Mul", 2) && scalar_f32(sc.in[0], &c)) {
+                src = sc.in[1], cname = sc.in[0], divide = 0;
+            } else {
+                continue;
+            }
+            *nodes = {is_, i0, i1};
+            f->op = "ScaleAddSoftmax";
+            f->in = {src, cname, N(i0).in[1 - side]};
+            Attr a;
+            a.kind = kAttrInt;
+            a.i = divide;
+            f->attrs["divide"] = a;
+            return true;
+        }
         *nodes = {i0, i1};
         f->op = "AddSoftmax";
         f->in = N(i0).in;
-        f->out = N(i1).out;
-        auto ax = N(i1).attrs.find("axis");
-        if (ax != N(i1).attrs.end()) f->attrs["axis"] = ax->second;
         return true;
     }
 

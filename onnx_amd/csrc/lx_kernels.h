@@ -116,6 +116,8 @@ struct SoftmaxArgs {
     const void *mask;        // nullptr = no mask (only for inner == 1)
     int mask_inner;          // 1 = mask contiguous along r, 0 = broadcast along r
     NdLayout mask_rows;      // row -> mask offset (nouter axes over the rows)
+    const void *scale;       // nullptr, or one element: x / scale (scale_div) or x * scale, before the mask
+    int scale_div;
 };
 hipError_t launch_softmax(const SoftmaxArgs &args, hipStream_t s);
 bool softmax_mask_fusable(int dtype, int64_t r, int64_t inner, int64_t outer, int vec);

@@ -93,7 +93,7 @@ __device__ __forceinline__ void softmax_row_load(const T *__restrict__ x, int64_
 template <typename T, int V, int NV, int NOUT>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
-                                                          NdLayout mrows) {
+                                                          NdLayout mrows, const T *__restrict__ scale, int scale_div) {
     constexpr bool MASK = NOUT != 0;
     __shared__ ExpTable tab;
     if constexpr (std::is_same<T, float>::value) {
@@ -105,10 +105,21 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6);
     if (row >= rows) return;
     Vec<T, V> cur[NV], nxt[NV], mcur[NV], mnxt[NV];
+    const T sv = scale ? scale[0] : T(1);
     softmax_row_load<T, V, NV, NOUT>(x, row, r, lane, mask, mask_inner, mrows, cur, mcur);
     for (; row < rows; row += W) {
         const int64_t next = row + W;
         if (next < rows) softmax_row_load<T, V, NV, NOUT>(x, next, r, lane, mask, mask_inner, mrows, nxt, mnxt);
+        if (scale) {  // the Div (or Mul) node before the mask Add: the same IEEE operation per element
+#pragma unroll
+            for (int c = 0; c < NV; c++) {
+                const int col = (c * 64 + lane) * V;
+                if (col < r) {
+#pragma unroll
+                    for (int k = 0; k < V; k++) cur[c].v[k] = scale_div ? cur[c].v[k] / sv : cur[c].v[k] * sv;
+                }
+            }
+        }
         if constexpr (MASK) {
 #pragma unroll
             for (int c = 0; c < NV; c++) {
@@ -228,7 +239,7 @@ static hipError_t softmax_wave_launch(const SoftmaxArgs &a, hipStream_t s) {
 #define LX_SM_CASE(N)                                                                                           \
     case N:                                                                                                     \
         hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, a.outer, r, \
-                           m, a.mask_inner, a.mask_rows);                                                       \
+                           m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);              \
         break;
     switch (nv) {
         LX_SM_CASE(1) LX_SM_CASE(2) LX_SM_CASE(3) LX_SM_CASE(4) LX_SM_CASE(5) LX_SM_CASE(6) LX_SM_CASE(7) LX_SM_CASE(8)
@@ -263,7 +274,7 @@ static hipError_t softmax_typed(const SoftmaxArgs &a, hipStream_t s) {
             return softmax_wave_dispatch<T, 1, false>(a, s);
         }
     }
-    if (a.mask) return hipErrorInvalidValue;  // the host falls back to Add + Softmax
+    if (a.mask || a.scale) return hipErrorInvalidValue;  // the host falls back to Div / Add + Softmax
     if (a.inner == 1) {
         hipLaunchKernelGGL((k_softmax_block<T>), dim3((unsigned)a.outer), dim3(kSBlock), 0, s, (const T *)a.x, (T *)a.y,
                            a.r);

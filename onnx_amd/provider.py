@@ -354,6 +354,17 @@ class HipExecutionProvider:
         return _result("ElementwiseChain", st, y, out)
 
     @staticmethod
+    def ScaleAddSoftmax(S, scale, divide=True, mask=None, axis=-1, out=None):
+        """Div(S, scale) (or Mul) -> Add(., mask) -> Softmax(axis) in one kernel (lx_ScaleAddSoftmax)."""
+        init()
+        S, scale = _as_tensor(S), _as_tensor(scale)
+        m = _as_tensor(mask) if mask is not None else None
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_ScaleAddSoftmax(_ptr(S), _ptr(scale), int(bool(divide)), _ptr(m) if m is not None else None,
+                                        int(axis), ctypes.byref(y))
+        return _result("ScaleAddSoftmax", st, y, out)
+
+    @staticmethod
     def GeluErf(X, out=None):
         init()
         X = _as_tensor(X)

@@ -164,3 +164,48 @@ def test_graph_chain_broadcast_failure_reports_the_original_node(hip):
     g1, n1, ok1 = _graph_run(nodes, {"x": x}, inits, ["y"], True)
     assert n1 == 1 and not ok0 and not ok1
     assert g1.LastError == g0.LastError and "second" in g0.LastError
+
+
+# ---- Div / Mul by a scalar -> Add(mask) -> Softmax in one kernel (lx_ScaleAddSoftmax) ------------------
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+@pytest.mark.parametrize("shape,mshape", [((2, 12, 64, 512), (2, 1, 1, 512)), ((3, 5, 70), (3, 1, 70)),
+                                          ((4, 8, 4096), None), ((2, 3, 9000), (2, 1, 9000))])
+def test_scale_add_softmax_equals_the_nodes(hip, dt, shape, mshape):
+    """Bit-identical to the node-by-node device path (Div, Add, Softmax), including the shapes the fused
+    kernel does not take (rows longer than its registers hold: node by node inside the call)."""
+    rng = np.random.default_rng(31)
+    s = (rng.standard_normal(shape) * 20).astype(dt)
+    c = np.array(8.0, dt)
+    m = None if mshape is None else np.where(rng.uniform(size=mshape) < 0.2, -10000.0, 0.0).astype(dt)
+    for divide in (True, False):
+        r = HIP.ScaleAddSoftmax(dev(s), dev(c), divide, None if m is None else dev(m))
+        assert r.Status == OpStatus.Success, r.Message
+        got = r.Outputs[0].to_numpy()
+        t = (HIP.Div if divide else HIP.Mul)(dev(s), dev(c)).Outputs[0]
+        if m is not None:
+            t = HIP.Add(t, dev(m)).Outputs[0]
+        ref = HIP.Softmax(t, -1).Outputs[0].to_numpy()
+        assert got.shape == ref.shape and np.array_equal(got.view(np.uint8), ref.view(np.uint8)), divide
+
+
+def test_scale_add_softmax_graph(hip):
+    from test_gpu_graph import _dict_nodes
+    rng = np.random.default_rng(32)
+    s = (rng.standard_normal((2, 12, 64, 128)) * 30).astype(np.float32)
+    mask = np.where(rng.uniform(size=(2, 1, 1, 128)) < 0.25, -10000.0, 0.0).astype(np.float32)
+    nodes = [W.node("Div", ["s", "c"], ["t"], "scale"), W.node("Add", ["t", "mask"], ["u"], "add"),
+             W.node("Softmax", ["u"], ["y"], "sm", axis=-1)]
+    inits = [("c", np.array(8.0, np.float32))]
+    outs = {}
+    for fuse in (False, True):
+        g, ok = None, None
+        model = W.model(nodes, [("s", np.float32, s.shape), ("mask", np.float32, mask.shape)],
+                        [("y", np.float32, ())], inits)
+        g = Model.Load(model)
+        n = g.Fuse() if fuse else 0
+        assert g.Execute({"s": DeviceTensor.from_numpy(s), "mask": DeviceTensor.from_numpy(mask)}), g.LastError
+        outs[fuse] = (n, g.Output("y").to_numpy())
+    assert outs[True][0] == 1 and bits(outs[True][1], outs[False][1])
+    ref = GO.run(_dict_nodes(nodes), {"s": s, "mask": mask}, dict(inits))["y"]
+    err = np.abs(outs[True][1].astype(np.float64) - ref.astype(np.float64))
+    assert np.all(err <= 1e-5 * np.maximum(1.0, np.abs(ref))), err.max()

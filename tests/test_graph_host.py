@@ -227,6 +227,19 @@ def test_bert_layer_fusion_plan():
     g = Model.Load(model)
     assert g.Fuse() == 6
     ops = [n.Op for n in g.Nodes]
-    assert ops.count("LayerNormDecomposed") == 2 and ops.count("GeluErf") == 1 and ops.count("AddSoftmax") == 1
+    assert ops.count("LayerNormDecomposed") == 2 and ops.count("GeluErf") == 1 and ops.count("ScaleAddSoftmax") == 1
+    assert "Div" not in ops   # the scores' Div by sqrt(64) went into ScaleAddSoftmax
     assert ops.count("ElementwiseChain") == 2 and ops.count("MatMul") == 8
     assert [n.Name for n in g.Nodes if n.Op == "ElementwiseChain"] == ["residual1", "residual2"]
+
+
+def test_scaled_softmax_pattern():
+    nodes = [W.node("Div", ["x", "c"], ["s"], "scale"), W.node("Add", ["mask", "s"], ["t"], "add"),
+             W.node("Softmax", ["t"], ["y"], "sm", axis=-1)]
+    inits = [("c", np.array(8.0, np.float32)), ("mask", np.zeros((1, 8), np.float32))]
+    assert _fused(nodes, inits) == (1, [("sm", "ScaleAddSoftmax")])
+    mul = [W.node("Mul", ["c", "x"], ["s"], "scale")] + nodes[1:]
+    assert _fused(mul, inits) == (1, [("sm", "ScaleAddSoftmax")])
+    # a divisor that is not a scalar constant: the plain Add -> Softmax pattern
+    inits2 = [("c", np.full(8, 8.0, np.float32)), ("mask", np.zeros((1, 8), np.float32))]
+    assert _fused(nodes, inits2) == (1, [("scale", "Div"), ("sm", "AddSoftmax")])
