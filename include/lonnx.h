@@ -180,6 +180,14 @@ int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_t axis, int
 int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, const int64_t *ends, int32_t n_ends,
              const int64_t *axes, int32_t n_axes, const int64_t *steps, int32_t n_steps, lx_tensor *Y);
 
+/* MatMul(A, B) -> Add(., bias) [-> Add(., residual)] (no single reference counterpart: the
+ * CPUExecutionProvider.MatMul and .Add calls of a projection with bias and a residual connection,
+ * CPUExecutionProvider.cs:82-113, 359-378).  Float, with bias a row vector of the product's last axis and
+ * residual of the product's shape: both Adds in the MatMul's epilogue, each rounded as the Add node
+ * rounds it; otherwise the MatMul and the Adds run one after the other.  residual may be NULL. */
+int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
+                 lx_tensor *Y);
+
 /* ---- fused subgraphs (one kernel each; every intermediate keeps the float32
  * rounding of the separate ONNX node it replaces) ------------------------- */
 /* Div(X, sqrt2) -> Erf -> Add 1 -> Mul X -> Mul 0.5 (the ONNX GELU subgraph;
@@ -246,7 +254,8 @@ int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
 /* Pattern fusion (no reference counterpart; the reference runs every node):
  * replaces the GELU subgraph (Div sqrt2 -> Erf -> Add 1 -> Mul x -> Mul 0.5), the decomposed
  * LayerNorm (ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul -> Add),
- * Add(mask) -> Softmax and Div / Mul by a scalar constant -> Add(mask) -> Softmax by the fused kernels when every intermediate has exactly one consumer and is
+ * Add(mask) -> Softmax, Div / Mul by a scalar constant -> Add(mask) -> Softmax and MatMul -> Add(row-vector
+ * constant) [-> Add] by the fused kernels when every intermediate has exactly one consumer and is
  * not a graph output; then every linear chain of two or more Float elementwise nodes
  * (Add/Sub/Mul/Div/Pow/Sqrt/Erf) whose intermediates have one consumer by an ElementwiseChain node
  * (lx_ElementwiseChain).  *n_fused = number of fused nodes made. */

@@ -1272,6 +1272,32 @@ int densify(int dt, MView *v, std::vector<void *> &temps) {
     return LX_OK;
 }
 
+// lx_MatMulAdd's Adds, applied in the MatMul's epilogue when the bias is a row vector of the output's
+// last axis and the residual has the output's shape (Float); `applied` tells the caller
+struct MatMulEpilogue {
+    const lx_tensor *bias = nullptr, *res = nullptr;
+    bool applied = false;
+};
+thread_local MatMulEpilogue *t_mm_epi = nullptr;
+
+bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dims) {
+    if (out_rank < 2) return false;
+    const int64_t n = out_dims[out_rank - 1];
+    if (e.bias) {
+        const lx_tensor *b = e.bias;
+        if (b->dtype != LX_FLOAT || b->rank < 1 || b->rank > out_rank || b->dims[b->rank - 1] != n) return false;
+        for (int i = 0; i < b->rank - 1; i++)
+            if (b->dims[i] != 1) return false;
+    }
+    if (e.res) {
+        const lx_tensor *r = e.res;
+        if (r->dtype != LX_FLOAT || r->rank != out_rank) return false;
+        for (int i = 0; i < out_rank; i++)
+            if (r->dims[i] != out_dims[i]) return false;
+    }
+    return true;
+}
+
 int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, lx_tensor *Y,
                std::vector<void *> &temps) {
     int st;
@@ -1279,6 +1305,10 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     if ((st = prepare_output(Y, dt, out_rank, out_dims))) return st;
     MatMulArgs p;
     memset(&p, 0, sizeof p);
+    if (t_mm_epi && dt == LX_FLOAT && epilogue_fits(*t_mm_epi, out_rank, out_dims)) {
+        p.bias = t_mm_epi->bias ? (const float *)t_mm_epi->bias->data : nullptr;
+        p.res = t_mm_epi->res ? (const float *)t_mm_epi->res->data : nullptr;
+    }
     p.m = (int32_t)x.dims[x.rank - 2];
     p.k = (int32_t)x.dims[x.rank - 1];
     p.n = (int32_t)y.dims[y.rank - 1];
@@ -1293,12 +1323,13 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     if (p.nbatch > kMaxOuter) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d batch axes are supported.", kMaxOuter);
     if (x.dims[x.rank - 2] > INT32_MAX || x.dims[x.rank - 1] > INT32_MAX || y.dims[y.rank - 1] > INT32_MAX)
         return set_err(LX_ERR_NOT_SUPPORTED, "Matrix dimensions beyond 2^31 are not supported.");
-    if (p.k == 0) {  // empty inner dimension: every output is 0
+    if (p.k == 0) {  // empty inner dimension: every output is 0 (the Adds, if any, run afterwards)
         int64_t n = numel(Y);
         HIPCHECK(launch_fill(Y->data, n, (int)esize(dt), 0, g.stream), "MatMul");
         return LX_OK;
     }
     HIPCHECK(launch_matmul(dt, x.data, y.data, Y->data, p, g.stream), "MatMul");
+    if (t_mm_epi && (p.bias || p.res)) t_mm_epi->applied = true;
     return LX_OK;
 }
 
@@ -1372,6 +1403,50 @@ extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     std::vector<void *> temps;
     st = matmul_views(A->dtype, dense_view(A), dense_view(B), Y, temps);
     for (void *t : temps) (void)pool_release(t);
+    return st;
+}
+
+extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
+                            lx_tensor *Y) {
+    REQUIRE_INIT();
+    if (!bias) return missing_input("Add", "B");
+    int st;
+    if ((st = check_tensor(bias, "B")) || (residual && (st = check_tensor(residual, "B")))) return st;
+    if (!Y) return set_err(LX_ERR_INVALID_ARGUMENT, "The output tensor handle is null.");
+    const bool caller_storage = Y->data != nullptr;
+    MatMulEpilogue epi;
+    epi.bias = bias;
+    epi.res = residual;
+    t_mm_epi = &epi;
+    lx_tensor c = caller_storage ? *Y : lx_tensor{};
+    st = lx_MatMul(A, B, caller_storage ? &c : Y);
+    t_mm_epi = nullptr;
+    if (st) return st;
+    if (epi.applied) {
+        if (caller_storage) *Y = c;
+        return LX_OK;
+    }
+    // node by node: C + bias, then + residual, into new tensors (either Add may broadcast to a larger
+    // shape than the product's)
+    lx_tensor *prod = caller_storage ? &c : Y;
+    lx_tensor t1{}, t2{};
+    st = run_binary(kAdd, prod, bias, &t1);
+    if (!st && residual) st = run_binary(kAdd, &t1, residual, &t2);
+    lx_tensor *out = residual ? &t2 : &t1;
+    if (!st) {
+        if (caller_storage) {
+            if (!(st = prepare_output(Y, out->dtype, out->rank, out->dims)) && numel(out))
+                HIPCHECK(hipMemcpyAsync(Y->data, out->data, numel(out) * esize(out->dtype), hipMemcpyDeviceToDevice,
+                                        g.stream),
+                         "MatMulAdd");
+        } else {
+            lx_tensor_free(Y);
+            *Y = *out;
+            *out = lx_tensor{};
+        }
+    }
+    lx_tensor_free(&t1);
+    lx_tensor_free(&t2);
     return st;
 }
 

@@ -654,6 +654,22 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!same) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
     }
+    if (op == "MatMulAdd") {
+        Value *av, *bv, *cv, *rv = nullptr;
+        if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &bv)) || (st = X.input(n, 2, &cv))) return st;
+        if (n.in.size() > 3 && (st = X.input(n, 3, &rv))) return st;
+        // the epilogue's shapes (A [..., M, K] x W [K, N] + bias [N] (+ residual [..., M, N])), else the nodes
+        bool fits = av && bv && cv && av->t.dtype == LX_FLOAT && bv->t.dtype == LX_FLOAT && cv->t.dtype == LX_FLOAT &&
+                    av->t.rank >= 2 && bv->t.rank == 2 && av->t.dims[av->t.rank - 1] == bv->t.dims[0] &&
+                    cv->t.rank == 1 && cv->t.dims[0] == bv->t.dims[1];
+        if (fits && n.in.size() > 3) {
+            fits = rv && rv->t.dtype == LX_FLOAT && rv->t.rank == av->t.rank;
+            for (int i = 0; fits && i < av->t.rank - 1; i++) fits = rv->t.dims[i] == av->t.dims[i];
+            fits = fits && rv->t.dims[av->t.rank - 1] == bv->t.dims[1];
+        }
+        if (!fits) return run_unfused(X, n, outs);
+        return run_op([&](lx_tensor *y) { return lx_MatMulAdd(T(av), T(bv), T(cv), rv ? T(rv) : nullptr, y); }, outs);
+    }
     if (op == "ScaleAddSoftmax") {
         Value *sv, *cv, *mv;
         if ((st = X.input(n, 0, &sv)) || (st = X.input(n, 1, &cv)) || (st = X.input(n, 2, &mv))) return st;
@@ -857,6 +873,31 @@ struct Fuser {
         return true;
     }
 
+    // MatMul(A, W) -> Add(., b) [-> Add(., r)] for a Float row-vector constant b: the projection with
+    // its bias (and residual) in one MatMul epilogue
+    bool matmul_add(int i0, GNode *f, std::vector<int> *nodes) {
+        if (!is(i0, "MatMul", 2)) return false;
+        const std::string &prod = N(i0).out[0];
+        const int i1 = only_consumer(prod);
+        std::string bias;
+        if (!is(i1, "Add", 2) || !other(i1, prod, &bias)) return false;
+        auto it = consts.find(bias);
+        if (it == consts.end() || it->second->dtype != LX_FLOAT || it->second->rank != 1) return false;
+        *nodes = {i0, i1};
+        f->op = "MatMulAdd";
+        f->in = {N(i0).in[0], N(i0).in[1], bias};
+        f->out = N(i1).out;
+        const std::string &biased = N(i1).out[0];
+        const int i2 = only_consumer(biased);
+        std::string res;
+        if (is(i2, "Add", 2) && other(i2, biased, &res)) {
+            nodes->push_back(i2);
+            f->in.push_back(res);
+            f->out = N(i2).out;
+        }
+        return true;
+    }
+
     // Add(S, mask) -> Softmax, and Div(S, c) / Mul(S, c) -> Add(., mask) -> Softmax for a Float scalar
     // constant c (the scaled attention scores)
     bool add_softmax(int i0, GNode *f, std::vector<int> *nodes) {
@@ -985,7 +1026,9 @@ struct Fuser {
             if (used[i]) continue;
             GNode f;
             std::vector<int> nodes;
-            if (layernorm(i, &f, &nodes) || gelu(i, &f, &nodes) || add_softmax(i, &f, &nodes)) place(f, nodes);
+            if (layernorm(i, &f, &nodes) || gelu(i, &f, &nodes) || add_softmax(i, &f, &nodes) ||
+                matmul_add(i, &f, &nodes))
+                place(f, nodes);
         }
         for (int i = 0; i < (int)g->nodes.size(); i++) {
             GNode f;

@@ -354,6 +354,16 @@ class HipExecutionProvider:
         return _result("ElementwiseChain", st, y, out)
 
     @staticmethod
+    def MatMulAdd(A, B, bias, residual=None, out=None):
+        """MatMul(A, B) -> Add bias [-> Add residual] with the Adds in the MatMul's epilogue (lx_MatMulAdd)."""
+        init()
+        A, B, bias = _as_tensor(A), _as_tensor(B), _as_tensor(bias)
+        r = _as_tensor(residual) if residual is not None else None
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_MatMulAdd(_ptr(A), _ptr(B), _ptr(bias), _ptr(r), ctypes.byref(y))
+        return _result("MatMulAdd", st, y, out)
+
+    @staticmethod
     def ScaleAddSoftmax(S, scale, divide=True, mask=None, axis=-1, out=None):
         """Div(S, scale) (or Mul) -> Add(., mask) -> Softmax(axis) in one kernel (lx_ScaleAddSoftmax)."""
         init()

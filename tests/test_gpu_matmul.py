@@ -121,3 +121,41 @@ def test_errors(hip):
     assert r.Message == "The rank of each tensor in matrix multiplication must be greater than 1."
     r = HIP.MatMul(dev(np.ones((2, 3, 4), np.float32)), dev(np.ones((5, 4, 2), np.float32)))
     assert r.Message == "The tensor shapes are not compatible for broadcasting."
+
+
+# ---- MatMul -> Add bias [-> Add residual] with the Adds in the epilogue (lx_MatMulAdd) -------------------
+def _nodes(a, b, bias, res):
+    t = HIP.MatMul(dev(a), dev(b)).Outputs[0]
+    t = HIP.Add(t, dev(bias)).Outputs[0]
+    if res is not None:
+        t = HIP.Add(t, dev(res)).Outputs[0]
+    return t.to_numpy()
+
+
+@pytest.mark.parametrize("sa,sb,sbias,sres", [
+    ((256, 768), (768, 768), (768,), None), ((4, 64, 768), (768, 256), (256,), (4, 64, 256)),
+    ((2, 3, 33, 40), (40, 70), (1, 70), (2, 3, 33, 70)), ((128, 64), (64, 96), (96,), (128, 96)),
+    # shapes the epilogue does not take: the MatMul and the Adds one after the other
+    ((64, 32), (32, 48), (64, 48), None), ((64, 32), (32, 48), (48,), (48,)), ((5, 32), (32, 48), (3, 1, 48), None)])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_matmul_add_equals_the_nodes(hip, sa, sb, sbias, sres, dt):
+    rng = np.random.default_rng(57)
+    a, b = rng.standard_normal(sa).astype(dt), rng.standard_normal(sb).astype(dt)
+    bias = rng.standard_normal(sbias).astype(dt)
+    res = None if sres is None else rng.standard_normal(sres).astype(dt)
+    r = HIP.MatMulAdd(dev(a), dev(b), dev(bias), None if res is None else dev(res))
+    assert r.Status == OpStatus.Success, r.Message
+    got, ref = r.Outputs[0].to_numpy(), _nodes(a, b, bias, res)
+    assert got.shape == ref.shape and np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+
+
+def test_matmul_add_into_caller_storage(hip):
+    rng = np.random.default_rng(58)
+    a, b = rng.standard_normal((96, 64)).astype(np.float32), rng.standard_normal((64, 80)).astype(np.float32)
+    bias, res = rng.standard_normal(80).astype(np.float32), rng.standard_normal((96, 80)).astype(np.float32)
+    out = DeviceTensor.empty((96, 80), np.float32)
+    r = HIP.MatMulAdd(dev(a), dev(b), dev(bias), dev(res), out=out)
+    assert r.Status == OpStatus.Success, r.Message
+    assert np.array_equal(out.to_numpy().view(np.uint32), _nodes(a, b, bias, res).view(np.uint32))
+    r = HIP.MatMulAdd(dev(a), dev(b), dev(np.ones(81, np.float32)))
+    assert r.Code == L.ERR_CANNOT_BROADCAST
