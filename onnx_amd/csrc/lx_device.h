@@ -230,6 +230,34 @@ __host__ __device__ __forceinline__ float recip_newton2(float d, float seed) {
     return __builtin_fmaf(e, y, y);
 }
 
+// Truncated quotient a / b of int32 operands (b != 0, not INT_MIN / -1) in
+// double precision, in place of the integer expansion (five quarter-rate
+// 32-bit multiplies plus sign fix-ups): y = 1/b from a seed of relative error
+// below 2^-21, one Newton step (error e -> e^2 + 2^-53, below 2^-41.9), then
+// q = trunc((a + sign(a) * 0.5) * y).
+// Exact: (|a| + 0.5)/|b| = |q| + f with f in [0.5/|b|, 1 - 0.5/|b|], and the
+// computed product is within ((2^31 + 0.5)/|b|) * 2^-41.8 < 2^-10/|b| of that
+// value (the conversions and a +- 0.5 are exact), so truncation lands on q.
+// Checked on the host against integer division with seeds perturbed by
+// +-2^-21; the device seed is v_rcp_f32 of the float nearest b, whose error
+// (rcp within 2^-22 on every float in [1, 2^31], checked on the device, plus
+// 2^-24 for rounding b to float) stays below 2^-21.
+template <typename SeedFn>
+__host__ __device__ __forceinline__ int32_t sdiv32_core(int32_t a, int32_t b, SeedFn seed) {
+    const double d = (double)b;
+    double y = seed(d);
+    const double e = __builtin_fma(-d, y, 1.0);
+    y = __builtin_fma(e, y, y);
+    const double n = (double)a;
+    return (int32_t)((n + __builtin_copysign(0.5, n)) * y);
+}
+
+struct RcpSeedF32 {
+    __device__ __forceinline__ double operator()(double d) const { return (double)__builtin_amdgcn_rcpf((float)d); }
+};
+
+__device__ __forceinline__ int32_t sdiv32_lx(int32_t a, int32_t b) { return sdiv32_core(a, b, RcpSeedF32()); }
+
 // ---------------------------------------------------------------------------
 // MathOps.Erf(float) (MathOps.cs:988-1010): Abramowitz & Stegun 7.1.26 in
 // float32, one rounding per operation, exp = expf_lx.

@@ -22,6 +22,7 @@ namespace lx {
 
 constexpr int kBlock = 256;
 constexpr int kMaxBlocks = 1 << 24;  // beyond this the kernels loop
+constexpr int kDivVecsPerLane = 4;   // integer Div: vectors loaded per lane before computing
 
 template <int CODE> struct CType;
 template <> struct CType<kFloat> { using T = float; };
@@ -131,6 +132,33 @@ __device__ __forceinline__ T bin_apply(T l, T r, uint64_t idx, ErrFlags *e) {
     }
 }
 
+// The V elements of one vector.  Integer division (int32, int64): when every
+// divisor in the vector is nonzero, no pair is MIN / -1 and every int64 operand
+// lies inside int32, the quotients come from the branch-free double-precision
+// division; any other vector takes the element-wise path with its error records.
+template <int OP, typename T, int V>
+__device__ __forceinline__ Vec<T, V> bin_apply_vec(const Vec<T, V> &va, const Vec<T, V> &vb, uint64_t idx0,
+                                                   ErrFlags *e) {
+    Vec<T, V> vy;
+    if constexpr (OP == kDiv && std::is_integral<T>::value && sizeof(T) >= 4) {
+        bool plain = true;
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const T l = va.v[k], r = vb.v[k];
+            plain = plain && r != 0 && !(l == (T)std::numeric_limits<int32_t>::min() && r == (T)-1);
+            if constexpr (sizeof(T) == 8) plain = plain && l == (T)(int32_t)l && r == (T)(int32_t)r;
+        }
+        if (plain) {
+#pragma unroll
+            for (int k = 0; k < V; k++) vy.v[k] = (T)sdiv32_lx((int32_t)va.v[k], (int32_t)vb.v[k]);
+            return vy;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < V; k++) vy.v[k] = bin_apply<OP, T>(va.v[k], vb.v[k], idx0 + k, e);
+    return vy;
+}
+
 // SAME / SCALAR_A / SCALAR_B: dense output walk with 16-byte vectors.
 template <int OP, typename T, int LAYOUT, int V>
 __global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a, const T *__restrict__ b,
@@ -140,16 +168,18 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a,
     if constexpr (LAYOUT == kScalarA) sa = a[0];
     if constexpr (LAYOUT == kScalarB) sb = b[0];
     for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < nv; i += (int64_t)gridDim.x * kBlock) {
-        Vec<T, V> va, vb, vy;
+        Vec<T, V> va, vb;
         if constexpr (LAYOUT != kScalarA) va = vload_nt<T, V>(a + i * V);
-        if constexpr (LAYOUT != kScalarB) vb = vload_nt<T, V>(b + i * V);
+        else {
 #pragma unroll
-        for (int k = 0; k < V; k++) {
-            T l = (LAYOUT == kScalarA) ? sa : va.v[k];
-            T r = (LAYOUT == kScalarB) ? sb : vb.v[k];
-            vy.v[k] = bin_apply<OP, T>(l, r, (uint64_t)(i * V + k), errs);
+            for (int k = 0; k < V; k++) va.v[k] = sa;
         }
-        vstore_nt<T, V>(y + i * V, vy);
+        if constexpr (LAYOUT != kScalarB) vb = vload_nt<T, V>(b + i * V);
+        else {
+#pragma unroll
+            for (int k = 0; k < V; k++) vb.v[k] = sb;
+        }
+        vstore_nt<T, V>(y + i * V, bin_apply_vec<OP, T, V>(va, vb, (uint64_t)(i * V), errs));
     }
     const int64_t tail = n - nv * V;
     if (blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
@@ -165,44 +195,57 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a,
 // (1) or broadcast (0) for A/B.  32-bit vector index with fast division.
 // a_nt / b_nt: the operand is read exactly once (no broadcast axis), so it is
 // streamed with nontemporal loads; broadcast operands are re-read and must stay
-// cacheable.
-template <int OP, typename T, int AIN, int BIN, int V>
+// cacheable.  U vectors per lane, a grid stride apart, all loaded before any is
+// computed: ops with many instructions per element (integer Div) keep more
+// bytes in flight per wave.
+template <typename T, int AIN, int BIN, int V>
+__device__ __forceinline__ void nd_load(const T *__restrict__ a, const T *__restrict__ b, uint32_t v,
+                                        const NdLayout &L, int a_nt, int b_nt, Vec<T, V> &va, Vec<T, V> &vb) {
+    uint32_t row = fdiv(v, L.inner_v);
+    uint32_t cv = v - row * L.inner_v.d;
+    int64_t ao = 0, bo = 0;
+    uint32_t rr = row;
+#pragma unroll
+    for (int d = 0; d < kMaxOuter; d++) {
+        if (d < L.nouter) {
+            uint32_t q = fdiv(rr, L.odiv[d]);
+            uint32_t id = rr - q * L.odiv[d].d;
+            ao += (int64_t)id * L.a_str[d];
+            bo += (int64_t)id * L.b_str[d];
+            rr = q;
+        }
+    }
+    const int64_t col = (int64_t)cv * V;
+    if constexpr (AIN) va = a_nt ? vload_nt<T, V>(a + ao + col) : vload<T, V>(a + ao + col);
+    else {
+        T s = a[ao];
+#pragma unroll
+        for (int k = 0; k < V; k++) va.v[k] = s;
+    }
+    if constexpr (BIN) vb = b_nt ? vload_nt<T, V>(b + bo + col) : vload<T, V>(b + bo + col);
+    else {
+        T s = b[bo];
+#pragma unroll
+        for (int k = 0; k < V; k++) vb.v[k] = s;
+    }
+}
+
+template <int OP, typename T, int AIN, int BIN, int V, int U>
 __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, const T *__restrict__ b,
                                                       T *__restrict__ y, uint32_t nv, NdLayout L, int a_nt, int b_nt,
                                                       ErrFlags *errs) {
-    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nv; v += gridDim.x * kBlock) {
-        uint32_t row = fdiv(v, L.inner_v);
-        uint32_t cv = v - row * L.inner_v.d;
-        int64_t ao = 0, bo = 0;
-        uint32_t rr = row;
+    const uint32_t stride = gridDim.x * kBlock;
+    for (uint32_t v0 = blockIdx.x * kBlock + threadIdx.x; v0 < nv; v0 += stride * U) {
+        Vec<T, V> va[U], vb[U];
 #pragma unroll
-        for (int d = 0; d < kMaxOuter; d++) {
-            if (d < L.nouter) {
-                uint32_t q = fdiv(rr, L.odiv[d]);
-                uint32_t id = rr - q * L.odiv[d].d;
-                ao += (int64_t)id * L.a_str[d];
-                bo += (int64_t)id * L.b_str[d];
-                rr = q;
-            }
+        for (int u = 0; u < U; u++)
+            if (u == 0 || v0 + u * stride < nv) nd_load<T, AIN, BIN, V>(a, b, v0 + u * stride, L, a_nt, b_nt, va[u], vb[u]);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t v = v0 + u * stride;
+            if (u == 0 || v < nv)
+                vstore_nt<T, V>(y + (int64_t)v * V, bin_apply_vec<OP, T, V>(va[u], vb[u], (uint64_t)v * V, errs));
         }
-        const int64_t col = (int64_t)cv * V;
-        Vec<T, V> va, vb, vy;
-        if constexpr (AIN) va = a_nt ? vload_nt<T, V>(a + ao + col) : vload<T, V>(a + ao + col);
-        else {
-            T s = a[ao];
-#pragma unroll
-            for (int k = 0; k < V; k++) va.v[k] = s;
-        }
-        if constexpr (BIN) vb = b_nt ? vload_nt<T, V>(b + bo + col) : vload<T, V>(b + bo + col);
-        else {
-            T s = b[bo];
-#pragma unroll
-            for (int k = 0; k < V; k++) vb.v[k] = s;
-        }
-#pragma unroll
-        for (int k = 0; k < V; k++)
-            vy.v[k] = bin_apply<OP, T>(va.v[k], vb.v[k], (uint64_t)v * V + k, errs);
-        vstore_nt<T, V>(y + (int64_t)v * V, vy);
     }
 }
 
@@ -223,14 +266,13 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd64(const T *__restrict__ a,
             rr = q;
         }
         const int64_t col = cv * V;
-        Vec<T, V> vy;
+        Vec<T, V> va, vb;
 #pragma unroll
         for (int k = 0; k < V; k++) {
-            T l = AIN ? a[ao + col + k] : a[ao];
-            T r = BIN ? b[bo + col + k] : b[bo];
-            vy.v[k] = bin_apply<OP, T>(l, r, (uint64_t)(v * V + k), errs);
+            va.v[k] = AIN ? a[ao + col + k] : a[ao];
+            vb.v[k] = BIN ? b[bo + col + k] : b[bo];
         }
-        vstore<T, V>(y + v * V, vy);
+        vstore<T, V>(y + v * V, bin_apply_vec<OP, T, V>(va, vb, (uint64_t)(v * V), errs));
     }
 }
 
@@ -256,16 +298,19 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
     // small launch-latency-bound arrays (C1), run fastest with one per lane.
     const int64_t nv = A.n / V;
     const bool two = (A.a_once || A.b_once) && nv >= (1 << 20);
-    const int g = grid_for(two ? (nv + 1) / 2 : nv, kBlock);
     const int key = A.a_inner * 2 + A.b_inner;
     if (nv < (1ll << 31)) {
+        constexpr int U = (OP == kDiv && std::is_integral<T>::value && sizeof(T) >= 4) ? kDivVecsPerLane : 1;
+        const int64_t lanes = (U > 1 && nv >= (1 << 20)) ? (nv + U - 1) / U : two ? (nv + 1) / 2 : nv;
+        const int g = grid_for(lanes, kBlock);
         switch (key) {
-        case 3: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
-        case 2: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
-        case 1: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
-        default: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        case 3: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 1, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        case 2: hipLaunchKernelGGL((k_binary_nd<OP, T, 1, 0, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        case 1: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 1, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
+        default: hipLaunchKernelGGL((k_binary_nd<OP, T, 0, 0, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)nv, A.nd, A.a_once, A.b_once, errs); break;
         }
     } else {
+        const int g = grid_for(two ? (nv + 1) / 2 : nv, kBlock);
         switch (key) {
         case 3: hipLaunchKernelGGL((k_binary_nd64<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nv, A.nd, A, errs); break;
         case 2: hipLaunchKernelGGL((k_binary_nd64<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nv, A.nd, A, errs); break;

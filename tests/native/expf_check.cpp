@@ -147,3 +147,76 @@ long long lx_test_gelu_mismatches(void) {
     return bad;
 }
 }
+
+namespace {
+// 1/d perturbed by a relative factor (1 + rel): a stand-in for a hardware
+// reciprocal seed of that accuracy
+struct ScaledSeed {
+    double rel;
+    double operator()(double d) const { return (1.0 / d) * (1.0 + rel); }
+};
+
+inline uint64_t splitmix(uint64_t &s) {
+    uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// quotients around multiples of the divisor magnitude ub: |a| = k*ub - 1, k*ub,
+// k*ub + ub - 1 for the smallest and largest k and random k in between (|a| and
+// ub up to 2^31), each with every sign of a and b that int32 represents
+inline long long sdiv_one(int64_t a, int64_t b, const ScaledSeed &seed) {
+    if (a < INT32_MIN || a > INT32_MAX || b < INT32_MIN || b > INT32_MAX || b == 0) return 0;
+    if (a == INT32_MIN && b == -1) return 0;  // an error case, never divided
+    const int64_t q = a / b;                   // C truncation, as the reference
+    return lx::sdiv32_core((int32_t)a, (int32_t)b, seed) != (int32_t)q ? 1 : 0;
+}
+
+long long sdiv_cases(uint32_t ub, uint64_t &rng, const ScaledSeed &seed) {
+    long long bad = 0;
+    const uint64_t kmax = 0x80000000ull / ub;
+    uint64_t ks[24] = {0, 1, 2, 3, kmax, kmax - 1};
+    for (int i = 6; i < 24; i++) ks[i] = splitmix(rng) % (kmax + 1);
+    for (uint64_t k : ks) {
+        const int64_t base = (int64_t)(k * ub);
+        const int64_t cand[3] = {base - 1, base, base + ub - 1};
+        for (int64_t a : cand) {
+            if (a < 0) continue;
+            bad += sdiv_one(a, ub, seed) + sdiv_one(-a, ub, seed) + sdiv_one(a, -(int64_t)ub, seed) +
+                   sdiv_one(-a, -(int64_t)ub, seed);
+        }
+    }
+    return bad;
+}
+}  // namespace
+
+extern "C" {
+// sdiv32_core against C integer division, with the seed 1/d scaled by
+// (1 + rel): every divisor magnitude up to 2^20 and 2^22 random larger ones up
+// to 2^31, each at multiples of the divisor; all a, b in [-2^10, 2^10); and
+// the extreme values.  Returns the mismatch count.
+long long lx_test_sdiv32_mismatches(double rel) {
+    const ScaledSeed seed{rel};
+    long long bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic, 4096)
+    for (long long ub = 1; ub <= (1ll << 20); ub++) {
+        uint64_t rng = (uint64_t)ub * 7919u;
+        bad += sdiv_cases((uint32_t)ub, rng, seed);
+    }
+#pragma omp parallel for reduction(+ : bad) schedule(dynamic, 4096)
+    for (long long i = 0; i < (1ll << 22); i++) {
+        uint64_t rng = (uint64_t)i ^ 0x5851f42d4c957f2dull;
+        uint32_t ub = (uint32_t)(splitmix(rng) >> 33) + 1;  // [1, 2^31]
+        if (ub <= (1u << 20)) ub |= 1u << 20;
+        bad += sdiv_cases(ub, rng, seed);
+    }
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (long long a = -1024; a < 1024; a++)
+        for (long long b = -1024; b < 1024; b++) bad += sdiv_one(a, b, seed);
+    const int64_t ext[] = {0, 1, -1, 2, -2, 3, INT32_MAX, INT32_MAX - 1, INT32_MIN, INT32_MIN + 1, 1 << 30, -(1 << 30)};
+    for (int64_t a : ext)
+        for (int64_t b : ext) bad += sdiv_one(a, b, seed);
+    return bad;
+}
+}

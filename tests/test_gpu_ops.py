@@ -165,6 +165,50 @@ def test_int_div_reused_divisor(hip, dt):
 
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64])
+def test_int_div_quotients_next_to_multiples(hip, dt):
+    """Dividends k*b - 1, k*b and k*b + b - 1 (and their negations) for divisors across the 32-bit range
+    -- where a quotient computed through a reciprocal would first go wrong -- bit-exact."""
+    rng = np.random.default_rng(27)
+    b = np.concatenate([np.arange(1, 2049), rng.integers(2049, 2**31 - 1, 6000),
+                        [2**31 - 1, 2**31 - 2, 2**30, 2**30 + 1, 65535, 65536, 65537]]).astype(np.int64)
+    kmax = (2**31 - 1) // b
+    k = np.minimum(rng.integers(0, 2**31, b.size) % (kmax + 1), kmax)
+    cols = [k * b - 1, k * b, k * b + b - 1, kmax * b, kmax * b + (2**31 - 1 - kmax * b)]
+    a = np.clip(np.stack(cols, 1), -(2**31) + 1, 2**31 - 1)
+    bb = np.broadcast_to(b[:, None], a.shape)
+    a = np.concatenate([a, -a, a, -a]).astype(dt)
+    bb = np.concatenate([bb, bb, -bb, -bb]).astype(dt)
+    a[:3, 0] = np.iinfo(np.int32).min   # |INT_MIN| = 2^31 over 1, 2, 3
+    assert_bits(ok(HIP.Div(dev(a), dev(bb))), O.binary(O.DIV, a, bb))
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
+@pytest.mark.parametrize("inner", [700003, 700004])
+def test_int_div_large_broadcast(hip, dt, inner):
+    """Over 2^20 vectors (several vectors per lane, loaded before they are divided), a ragged total and an
+    inner axis that does / does not take 16-byte vectors: bit-exact, and the first failing element decides the
+    error when the failures lie in a lane's later vectors (output rows 1 and 2 of 3)."""
+    rng = np.random.default_rng(28)
+    a = rng.integers(-(2**31), 2**31, (1, 2, inner), dtype=np.int64).astype(dt)
+    b = rng.integers(-(2**31), 2**31, (3, 1, inner), dtype=np.int64).astype(dt)
+    b[b == 0] = 9
+    b[b == -1] = -9
+    a[a == np.iinfo(dt).min] = 5
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), O.binary(O.DIV, a, b))
+    for ovf_row, dbz_row, code in ((1, 2, L.ERR_OVERFLOW), (2, 1, L.ERR_DIVIDE_BY_ZERO)):
+        a1, b1 = a.copy(), b.copy()
+        k = inner // 3
+        a1[0, 1, k], b1[ovf_row, 0, k] = np.iinfo(dt).min, -1   # fails at (ovf_row, 1, k) only
+        b1[dbz_row, 0, 2 * k] = 0                                # fails at (dbz_row, 0 and 1, 2k)
+        flat_a = np.broadcast_to(a1, (3, 2, inner)).reshape(-1)
+        flat_b = np.broadcast_to(b1, (3, 2, inner)).reshape(-1)
+        first_dbz = np.flatnonzero(flat_b == 0)[0]
+        first_ovf = np.flatnonzero((flat_a == np.iinfo(dt).min) & (flat_b == -1))[0]
+        assert (first_ovf < first_dbz) == (code == L.ERR_OVERFLOW)
+        assert HIP.Div(dev(a1), dev(b1)).Code == code
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
 def test_int_div_errors(hip, dt):
     info = np.iinfo(dt)
     r = HIP.Div(dev(np.array([4, 5, 6, 7], dt)), dev(np.array([1, 2, 0, 1], dt)))
@@ -452,6 +496,17 @@ def test_device_reciprocal_is_correctly_rounded(hip):
     assert lib.lx_test_device_recip(out) == 0
     assert out[0] == 0, f"{out[0]} reciprocals differ from 1/d ({out[1]} seeds off by one ulp)"
     assert out[2] == 0
+
+
+def test_device_rcp_f32_error_bound(hip):
+    """v_rcp_f32 is within 2^-22 relative of 1/d for every float d in [1, 2^31]: with the 2^-24 of rounding an
+    int32 divisor to float, the integer-division seed stays inside the 2^-21 that the host check of
+    sdiv32_core proves sufficient (tests/test_host_abi.py)."""
+    lib = ctypes.CDLL(os.path.join(HERE, "native", "librcp_check.so"))
+    out = ctypes.c_double()
+    assert lib.lx_test_device_rcp_error(ctypes.byref(out)) == 0
+    print(f"v_rcp_f32 largest relative error on [1, 2^31]: {out.value:.3g} (2^{np.log2(out.value):.2f})")
+    assert 0 < out.value <= 2.0 ** -22
 
 
 def test_gelu_chain_bit_exact(hip):

@@ -117,6 +117,8 @@ def _native():
     for f in ("lx_test_div_sqrt2_mismatches", "lx_test_expf_nonpos_mismatches", "lx_test_erf_fast_mismatches",
               "lx_test_gelu_mismatches"):
         getattr(lib, f).restype = ctypes.c_longlong
+    lib.lx_test_sdiv32_mismatches.restype = ctypes.c_longlong
+    lib.lx_test_sdiv32_mismatches.argtypes = [ctypes.c_double]
     return lib
 
 
@@ -183,3 +185,21 @@ def test_fused_gelu_equals_unfused_chain():
     argument) returns the unfused five-node chain's bits for all 2^32 inputs."""
     lib = _native()
     assert lib.lx_test_gelu_mismatches() == 0
+
+
+@pytest.mark.parametrize("rel", [0.0, 2.0 ** -21, -(2.0 ** -21)])
+def test_integer_division_by_double_reciprocal(rel):
+    """The device int32 quotient (sdiv32_core: double reciprocal from a seed,
+    one Newton step, trunc((a + sign(a) 0.5) * y)) equals C integer division for
+    every divisor magnitude up to 2^20 and 2^22 random larger ones, at the
+    dividends next to multiples of the divisor with every sign, all a, b in
+    [-2^10, 2^10) and the extreme values -- from an exact seed and from seeds
+    off by 2^-21 either way (the device seed is within 2^-21: see
+    test_device_rcp_f32_error_bound)."""
+    assert _native().lx_test_sdiv32_mismatches(rel) == 0
+
+
+def test_integer_division_check_detects_a_weak_seed():
+    """The same check fails when the seed is too coarse for one Newton step (2^-8 off):
+    the check can see a wrong quotient."""
+    assert _native().lx_test_sdiv32_mismatches(2.0 ** -8) > 0
