@@ -400,8 +400,7 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
         nb = (64 * 4096 + 256 * 4096 + 64 * 256 * 4096) * es
         for op in ("Add", "Mul"):
             run(f"C4 {op} {str(dt)[6:]}", nb, Y4.numel(), lambda i, op=op: getattr(HIP, op)(wA4, wB4, out=wY4), 1, k=k3)
-        # Div checks the device error flags (one sync per call): eager timing, host clock per call, and the
-        # device time of each call (flag reset + kernel + flag copy) from events on the launch stream
+        # Div checks the device error flags (one readback per call): eager timing, host clock per call
         nd = max(8, k3)
         for _ in range(2):
             HIP.Div(wA4, wB4, out=wY4)
@@ -412,14 +411,6 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
         torch.cuda.synchronize()
         record(f"C4 Div {str(dt)[6:]} (eager, includes error-flag readback)", nb, Y4.numel(),
                (time.perf_counter() - t0) * 1e3 / nd)
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(nd)]
-        for e0, e1 in evs:
-            e0.record()
-            HIP.Div(wA4, wB4, out=wY4)
-            e1.record()
-        torch.cuda.synchronize()
-        record(f"C4 Div {str(dt)[6:]} (device time per call: flag reset + kernel + flag copy)", nb, Y4.numel(),
-               float(np.median([e0.elapsed_time(e1) for e0, e1 in evs])))
         if dt == torch.int64:
             Yc = torch.empty(64, 256, 4096, device=dev, dtype=torch.float32)
             wYc = wrap(Yc)

@@ -8,6 +8,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -34,8 +35,19 @@ struct State {
     void *workspace = nullptr;
     int64_t ws_bytes = 0;
     ErrFlags *errs = nullptr;      // device
-    ErrFlags *errs_host = nullptr; // pinned host
+    struct Mailbox *mail = nullptr;      // mapped, coherent pinned host memory
+    struct Mailbox *mail_dev = nullptr;  // the same memory as the device addresses it
+    uint64_t mail_seq = 0;
 };
+// Small device-to-host reads (error records) land here: a one-block kernel copies the words and
+// then writes a sequence number, which the host polls.  One mailbox per library: calls are
+// single-threaded, as the reference's provider is.
+constexpr int64_t kMailWords = 8192;  // 64 KiB: 4096 error records
+struct Mailbox {
+    alignas(128) uint64_t seq;
+    alignas(128) uint64_t words[kMailWords];
+};
+
 State g;
 thread_local std::string g_err;
 
@@ -225,6 +237,7 @@ thread_local ErrFlags *t_defer_slot = nullptr;
 thread_local DeferredCheck *t_defer_rec = nullptr;
 
 int read_errs(ErrFlags *out);
+int read_device(const void *src, size_t bytes, void *dst);
 
 // the error record a checking launch writes, cleared first (one small kernel, never a memset:
 // the stream may be under capture): the deferred slot or the library's own record
@@ -281,10 +294,39 @@ int read_errs(ErrFlags *out) {
     if (cs != hipStreamCaptureStatusNone)
         return set_err(LX_ERR_NOT_SUPPORTED, "This operator checks its inputs on the device and reads the result "
                                              "back; it cannot run on a stream under capture.");
-    HIPCHECK(hipMemcpyAsync(g.errs_host, g.errs, sizeof(ErrFlags), hipMemcpyDeviceToHost, g.stream),
-             "hipMemcpyAsync(errors)");
-    HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
-    *out = *g.errs_host;
+    return read_device(g.errs, sizeof(ErrFlags), out);
+}
+
+// The host polls the mailbox's sequence number; every 50 us it asks the stream whether work is still
+// pending, so a device fault ends the wait with that fault's error instead of spinning on.
+int read_device(const void *src, size_t bytes, void *dst) {
+    if (bytes == 0) return LX_OK;
+    if (bytes % 8 || bytes / 8 > (size_t)kMailWords) {
+        HIPCHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g.stream), "hipMemcpyAsync(read back)");
+        HIPCHECK(hipStreamSynchronize(g.stream), "hipStreamSynchronize");
+        return LX_OK;
+    }
+    const uint64_t want = ++g.mail_seq;
+    HIPCHECK(launch_publish((const uint64_t *)src, (int64_t)(bytes / 8), g.mail_dev->words, &g.mail_dev->seq, want,
+                            g.stream),
+             "launch publish");
+    auto seen = [] { return __atomic_load_n(&g.mail->seq, __ATOMIC_ACQUIRE) == g.mail_seq; };
+    const auto t0 = std::chrono::steady_clock::now();
+    auto next_query = std::chrono::microseconds(50);
+    for (uint32_t spin = 1; !seen(); spin++) {
+        __builtin_ia32_pause();
+        if (spin % 256) continue;
+        const auto dt = std::chrono::steady_clock::now() - t0;
+        if (dt < next_query) continue;
+        next_query = std::chrono::duration_cast<std::chrono::microseconds>(dt) + std::chrono::microseconds(50);
+        const hipError_t q = hipStreamQuery(g.stream);
+        if (q == hipSuccess) {
+            if (seen()) break;
+            return set_err(LX_ERR_HIP, "reading back device results: the stream finished without publishing them");
+        }
+        if (q != hipErrorNotReady) return hip_fail(q, "reading back device results");
+    }
+    std::memcpy(dst, g.mail->words, bytes);
     return LX_OK;
 }
 
@@ -652,6 +694,7 @@ void api_defer_checks(ErrFlags *slot, DeferredCheck *rec) {
     t_defer_rec = rec;
 }
 int api_check_status(const DeferredCheck &rec, const ErrFlags &flags) { return check_status(rec.kind, rec.dst, flags); }
+int api_read_device(const void *src, size_t bytes, void *dst) { return read_device(src, bytes, dst); }
 }  // namespace lx
 
 // ===========================================================================
@@ -678,7 +721,11 @@ int lx_init(int32_t device) {
     HIPCHECK(hipStreamCreateWithFlags(&g.own_stream, hipStreamDefault), "hipStreamCreate");
     g.stream = g.own_stream;
     HIPCHECK(hipMalloc(&g.errs, sizeof(ErrFlags)), "hipMalloc(errors)");
-    HIPCHECK(hipHostMalloc((void **)&g.errs_host, sizeof(ErrFlags), hipHostMallocDefault), "hipHostMalloc");
+    HIPCHECK(hipHostMalloc((void **)&g.mail, sizeof(Mailbox), hipHostMallocMapped | hipHostMallocCoherent),
+             "hipHostMalloc(mailbox)");
+    HIPCHECK(hipHostGetDevicePointer((void **)&g.mail_dev, g.mail, 0), "hipHostGetDevicePointer(mailbox)");
+    g.mail->seq = 0;
+    g.mail_seq = 0;
 
     g.device = device;
     g.init = true;
@@ -694,7 +741,7 @@ int lx_shutdown(void) {
     if (g.workspace) (void)hipFree(g.workspace);
     if (g.errs) (void)hipFree(g.errs);
 
-    if (g.errs_host) (void)hipHostFree(g.errs_host);
+    if (g.mail) (void)hipHostFree(g.mail);
     if (g.own_stream) (void)hipStreamDestroy(g.own_stream);
     g = State();
     return LX_OK;

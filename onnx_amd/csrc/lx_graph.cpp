@@ -1126,12 +1126,10 @@ int first_device_failure(lx_graph *g, const std::vector<DeferredCheck> &recs, in
         if (recs[k].kind != kCheckNone) last = k;
     if (last < 0) return LX_OK;
     std::vector<ErrFlags> flags(last + 1);
-    hipError_t e = hipMemcpyAsync(flags.data(), g->check_slots.t.data, flags.size() * sizeof(ErrFlags),
-                                  hipMemcpyDeviceToHost, api_stream());
-    if (e == hipSuccess) e = hipStreamSynchronize(api_stream());
-    if (e != hipSuccess) {
+    const int rd = api_read_device(g->check_slots.t.data, flags.size() * sizeof(ErrFlags), flags.data());
+    if (rd) {
         *j = last;
-        return fail(LX_ERR_HIP, fmt("reading the check records: %s", hipGetErrorString(e)));
+        return rd;
     }
     for (int k = 0; k <= last; k++) {
         if (recs[k].kind == kCheckNone) continue;

@@ -26,6 +26,9 @@ struct DeferredCheck {
 };
 struct ErrFlags;
 void api_defer_checks(ErrFlags *slot, DeferredCheck *rec);
+// Reads `bytes` (a multiple of 8) of device memory into host memory after the work queued on the
+// library stream: the caller returns as soon as the device has written them (no stream-sync wake-up).
+int api_read_device(const void *src, size_t bytes, void *dst);
 int api_check_status(const DeferredCheck &rec, const ErrFlags &flags);  // sets lx_last_error on failure
 
 }  // namespace lx
