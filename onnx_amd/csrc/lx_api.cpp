@@ -674,6 +674,7 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
 
 int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
                 const char *opn, const lx_tensor *scale = nullptr, int scale_div = 1);
+bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, int vec, int64_t V, SoftmaxArgs &sa);
 
 }  // namespace
 
@@ -1106,6 +1107,45 @@ namespace {
 // Softmax(axis) of X, optionally of (X / scale) or (X * scale) (a one-element tensor) and of that plus a
 // mask broadcast against X: the operators the reference runs one by one, each element rounded as they
 // round it, in one kernel when the row-per-wave kernel takes the whole operation, else node by node.
+// The mask of a last-axis Softmax over scores of shape dims, as the row-per-wave kernel reads it:
+// contiguous or broadcast along the row, and the row index decomposed over the collapsed row axes
+// (size-1 axes dropped, contiguous ones merged).  False when the kernel cannot take it.
+bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, int vec, int64_t V, SoftmaxArgs &sa) {
+    const int64_t r = dims[rank - 1];
+    // mask strides in the scores' frame (no collapsing of the softmax axis)
+    int64_t ms[LX_MAX_RANK];
+    int64_t stv = 1;
+    for (int i = rank - 1; i >= 0; i--) {
+        int k = i - (rank - mask->rank);
+        if (k < 0) { ms[i] = 0; continue; }
+        ms[i] = (mask->dims[k] == 1 && dims[i] != 1) ? 0 : stv;
+        stv *= mask->dims[k];
+    }
+    sa.mask_inner = (r > 1 && ms[rank - 1] != 0) ? 1 : 0;
+    if (sa.mask_inner && vec > 1 && r % V != 0) return false;
+    // row axes 0..rank-2: collapse (drop size 1, merge contiguous)
+    int64_t cd[LX_MAX_RANK], cs[LX_MAX_RANK];
+    int n = 0;
+    for (int i = rank - 2; i >= 0; i--) {
+        if (dims[i] == 1) continue;
+        if (n > 0 && ms[i] == cs[n - 1] * cd[n - 1]) {
+            cd[n - 1] *= dims[i];
+            continue;
+        }
+        cd[n] = dims[i];
+        cs[n] = ms[i];
+        n++;
+    }
+    if (n > kMaxOuter) return false;
+    sa.mask = mask->data;
+    sa.mask_rows.nouter = n;
+    for (int d = 0; d < n; d++) {
+        sa.mask_rows.odiv[d] = make_fastdiv((uint32_t)cd[d]);
+        sa.mask_rows.a_str[d] = cs[d];
+    }
+    return true;
+}
+
 int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
                 const char *opn, const lx_tensor *scale, int scale_div) {
     REQUIRE_INIT();
@@ -1119,6 +1159,33 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
     if (mask) {
         if ((st = check_tensor(mask, "mask"))) return st;
         if (mask->dtype != X->dtype) return wrong_type_same("B");
+    }
+    // a scale or mask that makes the tensor larger than X: the nodes one by one, Softmax's axis being
+    // relative to the larger sum, as the Softmax node's is
+    auto grows = [&](const lx_tensor *t) {
+        lx_bcast_plan bp;
+        if (!t || plan(X->rank, X->dims, t->rank, t->dims, &bp) != LX_OK) return false;
+        if (bp.out_rank != X->rank) return true;
+        for (int i = 0; i < X->rank; i++)
+            if (bp.out_dims[i] != X->dims[i]) return true;
+        return false;
+    };
+    if (grows(scale) || grows(mask)) {
+        lx_tensor t0{}, t1{};
+        const lx_tensor *x = X;
+        st = LX_OK;
+        if (scale) {
+            st = run_binary(scale_div ? kDiv : kMul, X, scale, &t0);
+            x = &t0;
+        }
+        if (!st && mask) {
+            st = run_binary(kAdd, x, mask, &t1);
+            x = &t1;
+        }
+        if (!st) st = run_softmax(x, nullptr, axis, has_axis, Y, opn);
+        lx_tensor_free(&t0);
+        lx_tensor_free(&t1);
+        return st;
     }
     const int rank = X->rank;
     int ax = has_axis ? axis : -1;
@@ -1149,43 +1216,7 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
         bool same_shape = st == LX_OK && p.out_rank == X->rank;
         for (int i = 0; same_shape && i < X->rank; i++) same_shape = p.out_dims[i] == X->dims[i];
         fusable = same_shape && softmax_mask_fusable(X->dtype, r, inner, outer, vec) &&
-                  (vec == 1 || aligned16(mask->data));
-        if (fusable) {
-            // mask strides in X's frame (no collapsing of the softmax axis)
-            int64_t ms[LX_MAX_RANK];
-            int64_t stv = 1;
-            for (int i = rank - 1; i >= 0; i--) {
-                int k = i - (rank - mask->rank);
-                if (k < 0) { ms[i] = 0; continue; }
-                ms[i] = (mask->dims[k] == 1 && X->dims[i] != 1) ? 0 : stv;
-                stv *= mask->dims[k];
-            }
-            sa.mask_inner = (r > 1 && ms[rank - 1] != 0) ? 1 : 0;
-            if (r == 1) sa.mask_inner = 0;
-            if (sa.mask_inner && vec > 1 && r % V != 0) fusable = false;
-            // row axes 0..rank-2: collapse (drop size 1, merge contiguous)
-            int64_t cd[LX_MAX_RANK], cs[LX_MAX_RANK];
-            int n = 0;
-            for (int i = rank - 2; i >= 0; i--) {
-                if (X->dims[i] == 1) continue;
-                if (n > 0 && ms[i] == cs[n - 1] * cd[n - 1]) {
-                    cd[n - 1] *= X->dims[i];
-                    continue;
-                }
-                cd[n] = X->dims[i];
-                cs[n] = ms[i];
-                n++;
-            }
-            if (n > kMaxOuter) fusable = false;
-            if (fusable) {
-                sa.mask = mask->data;
-                sa.mask_rows.nouter = n;
-                for (int d = 0; d < n; d++) {
-                    sa.mask_rows.odiv[d] = make_fastdiv((uint32_t)cd[d]);
-                    sa.mask_rows.a_str[d] = cs[d];
-                }
-            }
-        }
+                  (vec == 1 || aligned16(mask->data)) && softmax_mask_layout(rank, X->dims, mask, vec, V, sa);
     }
     if (scale) {
         // the scale must leave X's shape as it is (one element, rank <= X's) for the kernel to apply it

@@ -28,6 +28,22 @@ __device__ __forceinline__ T exp_elem(T d, const ExpTable &tab) {
     else return ::exp(d);
 }
 
+// x / sv for a power of two sv whose reciprocal is a normal number equals x * (1 / sv) for every x:
+// both are the correctly rounded value of the same real number.  Returns whether sv is such a
+// power of two, and its exact reciprocal.
+__device__ __forceinline__ bool exact_pow2_recip(float sv, float *r) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, sv), e = (b >> 23) & 0xffu;
+    if ((b & 0x7fffffu) != 0 || e < 1 || e > 253) return false;
+    *r = __builtin_bit_cast(float, (b & 0x80000000u) | ((254u - e) << 23));
+    return true;
+}
+__device__ __forceinline__ bool exact_pow2_recip(double sv, double *r) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, sv), e = (b >> 52) & 0x7ffu;
+    if ((b & 0xfffffffffffffull) != 0 || e < 1 || e > 2045) return false;
+    *r = __builtin_bit_cast(double, (b & 0x8000000000000000ull) | ((2046ull - e) << 52));
+    return true;
+}
+
 template <typename T>
 __device__ __forceinline__ T div_row(T e, T s, T rs) {
     if constexpr (std::is_same<T, float>::value) return div_by_row_lx(e, s, rs);
@@ -106,6 +122,9 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     if (row >= rows) return;
     Vec<T, V> cur[NV], nxt[NV], mcur[NV], mnxt[NV];
     const T sv = scale ? scale[0] : T(1);
+    // a division by a power of two runs as the multiplication by its exact reciprocal
+    T sf = sv;
+    const bool smul = !scale_div || exact_pow2_recip(sv, &sf);
     softmax_row_load<T, V, NV, NOUT>(x, row, r, lane, mask, mask_inner, mrows, cur, mcur);
     for (; row < rows; row += W) {
         const int64_t next = row + W;
@@ -116,7 +135,7 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
                 const int col = (c * 64 + lane) * V;
                 if (col < r) {
 #pragma unroll
-                    for (int k = 0; k < V; k++) cur[c].v[k] = scale_div ? cur[c].v[k] / sv : cur[c].v[k] * sv;
+                    for (int k = 0; k < V; k++) cur[c].v[k] = smul ? cur[c].v[k] * sf : cur[c].v[k] / sv;
                 }
             }
         }

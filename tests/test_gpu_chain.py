@@ -188,6 +188,42 @@ def test_scale_add_softmax_equals_the_nodes(hip, dt, shape, mshape):
         assert got.shape == ref.shape and np.array_equal(got.view(np.uint8), ref.view(np.uint8)), divide
 
 
+@pytest.mark.parametrize("c", [8.0, -8.0, 0.125, 2.0 ** 126, 2.0 ** -126, 2.0 ** -140, 3.0, 1e-30])
+def test_scale_add_softmax_scales_equal_the_div_node(hip, c):
+    """A division by a power of two runs as the multiplication by its exact reciprocal (the same correctly
+    rounded value); other divisors -- and powers of two whose reciprocal is not a normal float -- divide.
+    Either way the node's bits, over magnitudes that overflow, underflow to denormals and cancel."""
+    rng = np.random.default_rng(34)
+    s = (rng.standard_normal((4, 8, 96)) * np.float32(10.0) ** rng.integers(-40, 39, (4, 8, 96))).astype(np.float32)
+    s[0, 0, :8] = [3.4e38, -3.4e38, 1e-45, -1e-45, 1.17e-38, 0.0, -0.0, 6e-39]
+    m = np.where(rng.uniform(size=(4, 1, 96)) < 0.2, -10000.0, 0.0).astype(np.float32)
+    cc = np.array(c, np.float32)
+    t = HIP.Add(HIP.Div(dev(s), dev(cc)).Outputs[0], dev(m)).Outputs[0]
+    ref = HIP.Softmax(t, -1).Outputs[0].to_numpy()
+    r = HIP.ScaleAddSoftmax(dev(s), dev(cc), True, dev(m))
+    assert r.Status == OpStatus.Success, r.Message
+    assert bits(r.Outputs[0].to_numpy(), ref)
+
+
+@pytest.mark.parametrize("axis", [-1, 4])
+def test_scale_add_softmax_with_a_mask_that_grows_the_scores(hip, axis):
+    """A mask of higher rank than the scores makes the Add's output larger: Softmax's axis is the sum's,
+    as for the Softmax node, and the result is the nodes' (fused and unfused paths)."""
+    rng = np.random.default_rng(33)
+    s = (rng.standard_normal((2, 4, 6, 32)) * 10).astype(np.float32)
+    m = np.where(rng.uniform(size=(3, 2, 4, 1, 32)) < 0.3, -10000.0, 0.0).astype(np.float32)
+    c = np.array(8.0, np.float32)
+    t = HIP.Add(HIP.Div(dev(s), dev(c)).Outputs[0], dev(m)).Outputs[0]
+    ref = HIP.Softmax(t, axis).Outputs[0].to_numpy()
+    r = HIP.ScaleAddSoftmax(dev(s), dev(c), True, dev(m), axis)
+    assert r.Status == OpStatus.Success, r.Message
+    assert bits(r.Outputs[0].to_numpy(), ref) and np.isfinite(ref).all()
+    ref2 = HIP.Softmax(HIP.Add(dev(s), dev(m)).Outputs[0], axis).Outputs[0].to_numpy()
+    r2 = HIP.AddSoftmax(dev(s), dev(m), axis)
+    assert r2.Status == OpStatus.Success, r2.Message
+    assert bits(r2.Outputs[0].to_numpy(), ref2)
+
+
 def test_scale_add_softmax_graph(hip):
     from test_gpu_graph import _dict_nodes
     rng = np.random.default_rng(32)
