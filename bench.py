@@ -315,6 +315,16 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     wX, wY, wg, wb = [wrap(t) for t in X], [wrap(t) for t in Y], wrap(gam), wrap(bet)
     run("C2 LayerNorm fused", LN_BYTES, 8 * 512 * 768,
         lambda i: HIP.LayerNormDecomposed(wX[i % LN_SETS], wg, wb, 1e-12, out=wY[i % LN_SETS]), LN_SETS)
+    # the same with the host round trip a caller holding host arrays pays (as the C# provider's managed
+    # tensors are): X uploaded from pageable host memory, the kernel, Y read back; host clock per step
+    Xh = [x.cpu().numpy() for x in X[:2]]
+
+    def ln_host(i):
+        wX[i % 2].upload(Xh[i % 2])
+        HIP.LayerNormDecomposed(wX[i % 2], wg, wb, 1e-12, out=wY[i % 2])
+        wY[i % 2].to_numpy()
+    record("C2 LayerNorm fused, including upload of X and download of Y (pageable host memory)", LN_BYTES,
+           8 * 512 * 768, wall_time(torch, ln_host, max(16, steps // 8), warmup))
     # unfused: 9 launches through the operator API, intermediates preallocated
     tm = {k: [torch.empty(8, 512, 1, device=dev) for _ in range(LN_SETS)] for k in ("mean", "var", "ve", "sd")}
     tf = {k: [torch.empty(*LN_SHAPE, device=dev) for _ in range(LN_SETS)] for k in ("d", "p", "n", "m")}
