@@ -1351,21 +1351,29 @@ int densify(int dt, MView *v, std::vector<void *> &temps) {
 }
 
 // lx_MatMulAdd's Adds, applied in the MatMul's epilogue when the bias is a row vector of the output's
-// last axis and the residual has the output's shape (Float); `applied` tells the caller
+// last axis (or one such row per batch: [batch..., 1, n] for an output [batch..., m, n]) and the
+// residual has the output's shape (Float); `applied` tells the caller
 struct MatMulEpilogue {
     const lx_tensor *bias = nullptr, *res = nullptr;
     bool applied = false;
 };
 thread_local MatMulEpilogue *t_mm_epi = nullptr;
 
-bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dims) {
+bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dims, int64_t *bias_bstr) {
     if (out_rank < 2) return false;
     const int64_t n = out_dims[out_rank - 1];
+    *bias_bstr = 0;
     if (e.bias) {
         const lx_tensor *b = e.bias;
         if (b->dtype != LX_FLOAT || b->rank < 1 || b->rank > out_rank || b->dims[b->rank - 1] != n) return false;
-        for (int i = 0; i < b->rank - 1; i++)
-            if (b->dims[i] != 1) return false;
+        bool shared = true;  // [1, ..., 1, n]
+        for (int i = 0; i < b->rank - 1; i++) shared = shared && b->dims[i] == 1;
+        if (!shared) {       // [batch..., 1, n]: a row per batch
+            if (b->rank != out_rank || b->dims[out_rank - 2] != 1) return false;
+            for (int i = 0; i < out_rank - 2; i++)
+                if (b->dims[i] != out_dims[i]) return false;
+            *bias_bstr = n;
+        }
     }
     if (e.res) {
         const lx_tensor *r = e.res;
@@ -1383,8 +1391,10 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     if ((st = prepare_output(Y, dt, out_rank, out_dims))) return st;
     MatMulArgs p;
     memset(&p, 0, sizeof p);
-    if (t_mm_epi && dt == LX_FLOAT && epilogue_fits(*t_mm_epi, out_rank, out_dims)) {
+    int64_t bias_bstr = 0;
+    if (t_mm_epi && dt == LX_FLOAT && epilogue_fits(*t_mm_epi, out_rank, out_dims, &bias_bstr)) {
         p.bias = t_mm_epi->bias ? (const float *)t_mm_epi->bias->data : nullptr;
+        p.bias_bstr = bias_bstr;
         p.res = t_mm_epi->res ? (const float *)t_mm_epi->res->data : nullptr;
     }
     p.m = (int32_t)x.dims[x.rank - 2];

@@ -654,6 +654,39 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!same) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
     }
+    if (op == "MatMulAddGroup") {
+        Value *av, *wv, *bv;
+        if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &wv)) || (st = X.input(n, 2, &bv))) return st;
+        // A [..., M, K] as [1, M', K] (M' the product of A's axes but the last) times W [G, K, N] plus the
+        // bias rows [G, 1, N]: the product [G, M', N] in one launch, its G slices the outputs
+        const int64_t G = (int64_t)n.out.size();
+        bool fits = av && wv && bv && av->t.dtype == LX_FLOAT && av->t.rank >= 2 && wv->t.rank == 3 &&
+                    wv->t.dims[0] == G && av->t.dims[av->t.rank - 1] == wv->t.dims[1] && bv->t.rank == 3 &&
+                    bv->t.dims[0] == G && bv->t.dims[1] == 1 && bv->t.dims[2] == wv->t.dims[2];
+        if (!fits) return run_unfused(X, n, outs);
+        const int64_t K = wv->t.dims[1], Nn = wv->t.dims[2], M = numel(av->t) / (K > 0 ? K : 1);
+        lx_tensor a3 = av->t;
+        a3.owns = 0;
+        a3.rank = 3;
+        a3.dims[0] = 1;
+        a3.dims[1] = M;
+        a3.dims[2] = K;
+        lx_tensor y{};
+        if ((st = lx_MatMulAdd(&a3, &wv->t, &bv->t, nullptr, &y))) {
+            lx_tensor_free(&y);
+            return run_unfused(X, n, outs);
+        }
+        const Value whole = value_from_output(y);
+        for (int64_t gi = 0; gi < G; gi++) {
+            Value v = whole;
+            v.t.data = (char *)y.data + gi * M * Nn * (int64_t)sizeof(float);
+            v.t.rank = av->t.rank;
+            for (int i = 0; i < LX_MAX_RANK; i++) v.t.dims[i] = i < av->t.rank - 1 ? av->t.dims[i] : 0;
+            v.t.dims[av->t.rank - 1] = Nn;
+            outs.push_back(v);
+        }
+        return LX_OK;
+    }
     if (op == "MatMulAdd") {
         Value *av, *bv, *cv, *rv = nullptr;
         if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &bv)) || (st = X.input(n, 2, &cv))) return st;
@@ -1043,7 +1076,71 @@ struct Fuser {
             if (!used[i]) out.push_back(g->nodes[i]);
         }
         g->nodes.swap(out);
-        return fused;
+        return fused - group_projections();
+    }
+
+    // MatMulAdd nodes (no residual) that share their input A, with constant Float weights [K, N] of one
+    // shape and constant biases [N]: one MatMulAddGroup node over the stacked weights [G, K, N] and
+    // biases [G, 1, N] -- one batched launch instead of G launches that each leave CUs idle (the Q, K, V
+    // projections of an attention layer).  Its outputs are the G slices of one [G, M, N] product, each
+    // bit-identical to its MatMulAdd.  Placed where the first of them was.  Returns the nodes removed.
+    int group_projections() {
+        index();
+        std::map<std::pair<std::string, std::pair<int64_t, int64_t>>, std::vector<int>> groups;
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            const GNode &n = g->nodes[i];
+            if (n.op != "MatMulAdd" || n.in.size() != 3 || n.out.size() != 1) continue;
+            auto w = consts.find(n.in[1]), b = consts.find(n.in[2]);
+            if (w == consts.end() || b == consts.end()) continue;
+            const HostTensor &W = *w->second, &B = *b->second;
+            if (W.dtype != LX_FLOAT || W.rank != 2 || B.dtype != LX_FLOAT || B.rank != 1 || B.dims[0] != W.dims[1] ||
+                W.bytes.size() != (size_t)W.numel() * 4 || B.bytes.size() != (size_t)B.numel() * 4)
+                continue;
+            groups[{n.in[0], {W.dims[0], W.dims[1]}}].push_back(i);
+        }
+        std::set<int> drop;
+        std::map<int, GNode> at;
+        for (auto &kv : groups) {
+            const std::vector<int> &ms = kv.second;
+            if (ms.size() < 2) continue;
+            const int64_t K = kv.first.second.first, Nn = kv.first.second.second, G = (int64_t)ms.size();
+            GNode f;
+            f.op = "MatMulAddGroup";
+            f.name = g->nodes[ms[0]].name;
+            f.index = g->nodes[ms[0]].index;
+            auto w = std::make_shared<HostTensor>(), b = std::make_shared<HostTensor>();
+            w->dtype = b->dtype = LX_FLOAT;
+            w->rank = b->rank = 3;
+            w->dims[0] = b->dims[0] = G;
+            w->dims[1] = K;
+            w->dims[2] = b->dims[2] = Nn;
+            b->dims[1] = 1;
+            for (int i : ms) {
+                const GNode &n = g->nodes[i];
+                const HostTensor &W = *consts[n.in[1]], &B = *consts[n.in[2]];
+                w->bytes.insert(w->bytes.end(), W.bytes.begin(), W.bytes.end());
+                b->bytes.insert(b->bytes.end(), B.bytes.begin(), B.bytes.end());
+                f.out.push_back(n.out[0]);
+                for (auto &o : n.fused_from) f.fused_from.push_back(o);
+                if (n.fused_from.empty()) f.fused_from.push_back(n);
+            }
+            const std::string wn = "__group_w_" + f.name, bn = "__group_b_" + f.name;
+            g->initializers.push_back({wn, w});
+            g->initializers.push_back({bn, b});
+            f.in = {kv.first.first, wn, bn};
+            at[ms[0]] = f;
+            for (size_t k = 1; k < ms.size(); k++) drop.insert(ms[k]);
+        }
+        if (at.empty()) return 0;
+        std::vector<GNode> out;
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            if (drop.count(i)) continue;
+            auto it = at.find(i);
+            out.push_back(it != at.end() ? it->second : g->nodes[i]);
+        }
+        const int removed = (int)(g->nodes.size() - out.size());
+        g->nodes.swap(out);
+        return removed;
     }
 };
 

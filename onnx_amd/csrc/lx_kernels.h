@@ -142,10 +142,11 @@ struct MatMulArgs {
     int64_t bdims[kMaxOuter];
     int64_t a_bstr[kMaxOuter];
     int64_t b_bstr[kMaxOuter];
-    // optional epilogue (Float only): C = (A B + bias[col]) + res[same index], each add rounded as the
-    // separate Add node rounds it
+    // optional epilogue (Float only): C = (A B + bias[batch * bias_bstr + col]) + res[same index], each
+    // add rounded as the separate Add node rounds it
     const float *bias;
     const float *res;
+    int64_t bias_bstr;  // 0: one bias row for every batch; n: a bias row per batch (linear batch index)
 };
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);
 

@@ -159,19 +159,20 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
         buf ^= 1;
     }
     const float *Rb = p.res ? p.res + (p.batch_base + blockIdx.z) * (int64_t)M * N : nullptr;
+    const float *Bias = p.bias ? p.bias + (p.batch_base + blockIdx.z) * p.bias_bstr : nullptr;
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
         for (int j = 0; j < NT; j++) {
             const int c = col0 + wc + 32 * j + (l % 32);
             if (c >= N) continue;
-            const float bc = p.bias ? p.bias[c] : 0.0f;
+            const float bc = Bias ? Bias[c] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int row = row0 + wr + 32 * i + 8 * (r / 4) + 4 * (l / 32) + (r % 4);
                 if (row < M) {
                     float v = acc[i][j][r];
-                    if (p.bias) v = v + bc;
+                    if (Bias) v = v + bc;
                     if (Rb) v = v + Rb[(int64_t)row * N + c];
                     Cb[(int64_t)row * N + c] = v;
                 }

@@ -159,3 +159,48 @@ def test_matmul_add_into_caller_storage(hip):
     assert np.array_equal(out.to_numpy().view(np.uint32), _nodes(a, b, bias, res).view(np.uint32))
     r = HIP.MatMulAdd(dev(a), dev(b), dev(np.ones(81, np.float32)))
     assert r.Code == L.ERR_CANNOT_BROADCAST
+
+
+def test_matmul_add_bias_row_per_batch_equals_the_nodes(hip):
+    """A bias of one row per batch ([G, 1, N] against a product [G, M, N]) in the epilogue: the MatMul, then
+    the broadcast Add, bit for bit; a bias that matches neither form runs the Add node."""
+    rng = np.random.default_rng(90)
+    a = rng.standard_normal((1, 96, 64)).astype(np.float32)
+    w = rng.standard_normal((3, 64, 80)).astype(np.float32)
+    for bshape in [(3, 1, 80), (1, 80), (80,), (3, 96, 80)]:
+        b = rng.standard_normal(bshape).astype(np.float32)
+        r = HIP.MatMulAdd(dev(a), dev(w), dev(b))
+        assert r.Status == OpStatus.Success, r.Message
+        got = r.Outputs[0].to_numpy()
+        ref = HIP.Add(HIP.MatMul(dev(a), dev(w)).Outputs[0], dev(b)).Outputs[0].to_numpy()
+        assert got.shape == ref.shape and np.array_equal(got.view(np.uint32), ref.view(np.uint32)), bshape
+
+
+def test_grouped_projections_equal_the_separate_ones(hip):
+    """Three MatMul -> Add bias projections of one input become one MatMulAddGroup node (one batched launch,
+    outputs as slices of one product); every output equals the unfused graph's bit for bit, including
+    through a consumer that reads a slice (Reshape / Transpose of the middle one)."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    rng = np.random.default_rng(91)
+    x = rng.standard_normal((2, 40, 96)).astype(np.float32)
+    inits = []
+    nodes = []
+    for t in "qkv":
+        inits += [(f"w{t}", (rng.standard_normal((96, 64)) * 0.1).astype(np.float32)),
+                  (f"b{t}", rng.standard_normal(64).astype(np.float32))]
+        nodes += [W.node("MatMul", ["x", f"w{t}"], [f"{t}0"], f"{t}_proj"),
+                  W.node("Add", [f"{t}0", f"b{t}"], [f"{t}"], f"{t}_bias")]
+    inits.append(("shape", np.array([2, 40, 4, 16], np.int64)))
+    nodes += [W.node("Reshape", ["k", "shape"], ["kr"], "k_heads"),
+              W.node("Transpose", ["kr"], ["kt"], "k_perm", perm=[0, 2, 3, 1])]
+    outs = ["q", "kt", "v"]
+    res = {}
+    for fuse in (False, True):
+        g = Model.Load(W.model(nodes, [("x", np.float32, x.shape)], [(o, np.float32, ()) for o in outs], inits))
+        if fuse:
+            assert g.Fuse() == 1 and [n.Op for n in g.Nodes][0] == "MatMulAddGroup"
+        assert g.Execute({"x": dev(x)}), g.LastError
+        res[fuse] = [g.Output(o).to_numpy() for o in outs]
+    for u, f in zip(res[False], res[True]):
+        assert u.shape == f.shape and np.array_equal(u.view(np.uint32), f.view(np.uint32))
