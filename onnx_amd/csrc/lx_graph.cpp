@@ -184,6 +184,16 @@ int host_ints(Value &v, std::vector<int64_t> *out) {
     return LX_OK;
 }
 
+// a small integer vector (or scalar) whose values the host holds: the shape arithmetic of exported
+// models (Shape -> Gather -> Unsqueeze -> Concat -> Reshape), evaluated on the host so that the Reshape
+// reading it needs no download and the graph stays capturable
+constexpr int64_t kHostShapeMax = 64;
+bool host_int_vector(const Value *v) {
+    if (!v || !v->host || (v->t.dtype != LX_INT64 && v->t.dtype != LX_INT32) || v->t.rank > 1) return false;
+    const int64_t n = numel(v->t);
+    return n <= kHostShapeMax && (int64_t)v->host->bytes.size() == n * api_esize(v->t.dtype);
+}
+
 bool same_host_tensor(const HostTensor &a, const HostTensor &b) {
     if (a.dtype != b.dtype || a.rank != b.rank || a.bytes != b.bytes) return false;
     for (int i = 0; i < a.rank; i++)
@@ -431,15 +441,35 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
     }
     if (op == "Concat") {  // CPU.Concat(graph.GetInputTensors(Inputs), RequiredInt("axis")) (Node.cs:150)
         std::vector<const lx_tensor *> ins;
+        std::vector<Value *> vs;
         for (size_t k = 0; k < n.in.size(); k++) {
             Value *v;
             if ((st = X.input(n, k, &v))) return st;
             ins.push_back(T(v));
+            vs.push_back(v);
         }
         int32_t axis;
         int r = attr_int(n, "axis", &axis);
         if (r < 0) return LX_ERR_INVALID_ARGUMENT;
         if (r == 0) return failure("The Int attribute axis is required but was not found.");
+        // shape arithmetic: rank-1 integer vectors known on the host, joined on the host
+        bool host = !vs.empty() && (axis == 0 || axis == -1);
+        int64_t total = 0;
+        for (Value *v : vs) {
+            host = host && host_int_vector(v) && v->t.rank == 1 && v->t.dtype == vs[0]->t.dtype;
+            if (host) total += numel(v->t);
+        }
+        if (host && total > 0 && total <= kHostShapeMax) {
+            auto h = std::make_shared<HostTensor>();
+            h->dtype = vs[0]->t.dtype;
+            h->rank = 1;
+            h->dims[0] = total;
+            for (Value *v : vs) h->bytes.insert(h->bytes.end(), v->host->bytes.begin(), v->host->bytes.end());
+            Value out;
+            if ((st = value_from_host_cached(X.g, n.out.empty() ? n.name : n.out[0], h, &out))) return st;
+            outs.push_back(out);
+            return LX_OK;
+        }
         return run_op([&](lx_tensor *y) { return lx_Concat(ins.data(), (int32_t)ins.size(), axis, 1, y); }, outs);
     }
     if (op == "Gather") {  // CPU.Gather(InputTensor(0), InputTensor(1), Int("axis")) (Node.cs:154)
@@ -447,6 +477,29 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         int32_t axis = 0;
         int r = attr_int(n, "axis", &axis);
         if (r < 0) return LX_ERR_INVALID_ARGUMENT;
+        // shape arithmetic: elements of a rank-1 integer vector known on the host, picked on the host
+        // when every index lies inside it (after one wrap of a negative index, as the device operator)
+        if (a && b && host_int_vector(a) && a->t.rank == 1 && host_int_vector(b) && (axis == 0 || axis == -1)) {
+            std::vector<int64_t> idx;
+            const int64_t len = a->t.dims[0], es = api_esize(a->t.dtype);
+            bool inside = host_ints(*b, &idx) == LX_OK;
+            for (auto &i : idx) {
+                if (i < 0) i += len;
+                inside = inside && i >= 0 && i < len;
+            }
+            if (inside) {
+                auto h = std::make_shared<HostTensor>();
+                h->dtype = a->t.dtype;
+                h->rank = b->t.rank;
+                for (int d = 0; d < b->t.rank; d++) h->dims[d] = b->t.dims[d];
+                for (int64_t i : idx)
+                    h->bytes.insert(h->bytes.end(), a->host->bytes.begin() + i * es, a->host->bytes.begin() + (i + 1) * es);
+                Value out;
+                if ((st = value_from_host_cached(X.g, n.out.empty() ? n.name : n.out[0], h, &out))) return st;
+                outs.push_back(out);
+                return LX_OK;
+            }
+        }
         return run_op([&](lx_tensor *y) { return lx_Gather(T(a), T(b), axis, r, y); }, outs);
     }
     if (op == "Slice") {  // CPU.Slice(InputTensor(0..4)) (Node.cs:156; CPUExecutionProvider.cs:548-600)

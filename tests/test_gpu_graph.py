@@ -352,3 +352,39 @@ def test_capture_memory_is_released(hip):
     g.ReleaseCapture()
     g.Reset()
     assert L.pool_stats()[0] <= live0 + 4096   # the check records stay with the graph
+
+
+def _dynamic_reshape_model(idx=0):
+    """Shape -> Gather -> Concat -> Reshape: the shape arithmetic of an exported model (the batch size read
+    at run time).  A rank-0 initializer loads as shape [1] here, as the reference's TensorUtil reads it, so
+    the index is written as [idx] and no Unsqueeze is needed."""
+    nodes = [W.node("Shape", ["x"], ["s"], "shape"),
+             W.node("Gather", ["s", "i"], ["b"], "gather", axis=0),
+             W.node("Concat", ["b", "rest"], ["tgt"], "concat", axis=0),
+             W.node("Reshape", ["x", "tgt"], ["r"], "reshape"),
+             W.node("Transpose", ["r"], ["y"], "perm", perm=[0, 2, 1, 3])]
+    inits = [("i", np.array([idx], np.int64)), ("rest", np.array([40, 4, 24], np.int64))]
+    return W.model(nodes, [("x", np.float32, (2, 40, 96))], [("y", np.float32, ())], inits)
+
+
+def test_shape_arithmetic_runs_on_the_host_and_captures(hip):
+    """Gather / Concat over small integer vectors the host knows are computed there: the Reshape reads its
+    target without a download, and the graph can be captured and replayed (it could not while the shape
+    vector came back from the device)."""
+    x = np.random.default_rng(95).standard_normal((2, 40, 96)).astype(np.float32)
+    ref = x.reshape(2, 40, 4, 24).transpose(0, 2, 1, 3)
+    g = Model.Load(_dynamic_reshape_model())
+    dx = DeviceTensor.from_numpy(x)
+    assert g.Execute({"x": dx}), g.LastError
+    assert np.array_equal(g.Output("y").to_numpy(), ref)
+    assert g.Capture({"x": dx}), g.LastError
+    for scale in (1.0, -2.0):
+        dx.upload(x * scale)
+        assert g.Replay(), g.LastError
+        assert np.array_equal(g.Output("y").to_numpy(), (x * scale).reshape(2, 40, 4, 24).transpose(0, 2, 1, 3))
+
+
+def test_shape_arithmetic_out_of_range_index_fails_as_the_device_operator(hip):
+    g = Model.Load(_dynamic_reshape_model(idx=5))
+    assert not g.Execute({"x": DeviceTensor.from_numpy(np.zeros((2, 40, 96), np.float32))})
+    assert "gather" in g.LastError and "outside the bounds" in g.LastError
