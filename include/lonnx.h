@@ -182,9 +182,10 @@ int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, con
 
 /* MatMul(A, B) -> Add(., bias) [-> Add(., residual)] (no single reference counterpart: the
  * CPUExecutionProvider.MatMul and .Add calls of a projection with bias and a residual connection,
- * CPUExecutionProvider.cs:82-113, 359-378).  Float, with bias a row vector of the product's last axis and
- * residual of the product's shape: both Adds in the MatMul's epilogue, each rounded as the Add node
- * rounds it; otherwise the MatMul and the Adds run one after the other.  residual may be NULL. */
+ * CPUExecutionProvider.cs:82-113, 359-378).  Float, with bias a row vector of the product's last axis (or
+ * one such row per batch, [batch..., 1, n] for a product [batch..., m, n]) and residual of the product's
+ * shape: both Adds in the MatMul's epilogue, each rounded as the Add node rounds it; otherwise the MatMul
+ * and the Adds run one after the other.  residual may be NULL. */
 int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
                  lx_tensor *Y);
 
