@@ -71,14 +71,15 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     float *Cb = C + (p.batch_base + blockIdx.z) * (int64_t)M * N;
 
     // global -> register staging one K step ahead: float4 e = t + NTHR h of the step's
-    // A tile (row e / 4, k 4 (e % 4)) and B tile (k row e / BQ, column 4 (e % BQ))
+    // A tile (row e / KQ, k 4 (e % KQ)) and B tile (k row e / BQ, column 4 (e % BQ))
+    constexpr int KQ = kFBK / 4;                     // float4 per A row of a K step
     float4 ra[LA], rb[LB];
     auto load = [&](int k0) {
 #pragma unroll
         for (int h = 0; h < LA; h++) {
             const int e = t + NTHR * h;
             if (AV % NTHR != 0 && e >= AV) continue;
-            const int r = row0 + e / 4, kk = k0 + (e % 4) * 4;
+            const int r = row0 + e / KQ, kk = k0 + (e % KQ) * 4;
             if constexpr (VEC) {
                 ra[h] = (r < M && kk < K) ? *reinterpret_cast<const float4 *>(Ab + (int64_t)r * K + kk)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
         for (int h = 0; h < LA; h++) {
             const int e = t + NTHR * h;
             if (AV % NTHR != 0 && e >= AV) continue;
-            const int r = e / 4, kk = (e % 4) * 4;
+            const int r = e / KQ, kk = (e % KQ) * 4;
             As[buf][kk + 0][r] = ra[h].x;
             As[buf][kk + 1][r] = ra[h].y;
             As[buf][kk + 2][r] = ra[h].z;
