@@ -315,6 +315,11 @@ def bench_all(torch, HIP, DeviceTensor, set_stream, steps, warmup):
     wX, wY, wg, wb = [wrap(t) for t in X], [wrap(t) for t in Y], wrap(gam), wrap(bet)
     run("C2 LayerNorm fused", LN_BYTES, 8 * 512 * 768,
         lambda i: HIP.LayerNormDecomposed(wX[i % LN_SETS], wg, wb, 1e-12, out=wY[i % LN_SETS]), LN_SETS)
+    # the practical ceiling at this size: a plain device copy of the same bytes (Cast float -> float, 16-byte
+    # nontemporal loads and stores) over the same 16 buffer sets; at 25 MB per launch the ramp and drain of
+    # one launch cost about as much as the transfer itself
+    run("C2 size-matched copy X -> Y (Cast float->float, same buffer sets)", 2 * 8 * 512 * 768 * 4, 8 * 512 * 768,
+        lambda i: HIP.Cast(wX[i % LN_SETS], 1, out=wY[i % LN_SETS]), LN_SETS)
     # the same with the host round trip a caller holding host arrays pays (as the C# provider's managed
     # tensors are): X uploaded from pageable host memory, the kernel, Y read back; host clock per step
     Xh = [x.cpu().numpy() for x in X[:2]]
