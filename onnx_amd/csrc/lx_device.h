@@ -242,14 +242,24 @@ __host__ __device__ __forceinline__ float recip_newton2(float d, float seed) {
 // +-2^-21; the device seed is v_rcp_f32 of the float nearest b, whose error
 // (rcp within 2^-22 on every float in [1, 2^31], checked on the device, plus
 // 2^-24 for rounding b to float) stays below 2^-21.
+// The two halves are separate so that a divisor shared by several dividends
+// has its reciprocal computed once; sdiv32_core is their composition.
 template <typename SeedFn>
-__host__ __device__ __forceinline__ int32_t sdiv32_core(int32_t a, int32_t b, SeedFn seed) {
+__host__ __device__ __forceinline__ double sdiv32_recip(int32_t b, SeedFn seed) {
     const double d = (double)b;
     double y = seed(d);
     const double e = __builtin_fma(-d, y, 1.0);
-    y = __builtin_fma(e, y, y);
+    return __builtin_fma(e, y, y);
+}
+
+__host__ __device__ __forceinline__ int32_t sdiv32_quot(int32_t a, double y) {
     const double n = (double)a;
     return (int32_t)((n + __builtin_copysign(0.5, n)) * y);
+}
+
+template <typename SeedFn>
+__host__ __device__ __forceinline__ int32_t sdiv32_core(int32_t a, int32_t b, SeedFn seed) {
+    return sdiv32_quot(a, sdiv32_recip(b, seed));
 }
 
 struct RcpSeedF32 {
@@ -257,6 +267,7 @@ struct RcpSeedF32 {
 };
 
 __device__ __forceinline__ int32_t sdiv32_lx(int32_t a, int32_t b) { return sdiv32_core(a, b, RcpSeedF32()); }
+__device__ __forceinline__ double sdiv32_recip_lx(int32_t b) { return sdiv32_recip(b, RcpSeedF32()); }
 
 // ---------------------------------------------------------------------------
 // MathOps.Erf(float) (MathOps.cs:988-1010): Abramowitz & Stegun 7.1.26 in

@@ -265,6 +265,93 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, c
     }
 }
 
+// Integer Div whose divisor does not vary along the outermost output axis (b
+// stride 0 there, as in [64,1,4096] / [1,256,4096]).  Lane t takes divisor
+// vector vr = t mod rest (rest = vectors per outermost index) and the U
+// outermost indices r = (t / rest) * U + u: the reciprocals of the divisor
+// (seed and Newton step, most of the division's instructions) are computed
+// once for U quotients.  Same arithmetic, fallback and error records per
+// element as k_binary_nd.
+template <typename T, int AIN, int BIN, int V, int U>
+__global__ __launch_bounds__(kBlock) void k_div_rows(const T *__restrict__ a, const T *__restrict__ b,
+                                                     T *__restrict__ y, uint32_t lanes, FastDiv rest,
+                                                     uint32_t R, NdLayout L, int a_nt, int b_nt, ErrFlags *errs) {
+    const int top = L.nouter - 1;
+    const int64_t a_top = L.a_str[top];
+    for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < lanes; t += gridDim.x * kBlock) {
+        const uint32_t chunk = fdiv(t, rest);
+        const uint32_t vr = t - chunk * rest.d;
+        const uint32_t row = fdiv(vr, L.inner_v);
+        const uint32_t cv = vr - row * L.inner_v.d;
+        int64_t ao = 0, bo = 0;
+        uint32_t rr = row;
+#pragma unroll
+        for (int d = 0; d < kMaxOuter - 1; d++) {
+            if (d < top) {
+                uint32_t q = fdiv(rr, L.odiv[d]);
+                uint32_t id = rr - q * L.odiv[d].d;
+                ao += (int64_t)id * L.a_str[d];
+                bo += (int64_t)id * L.b_str[d];
+                rr = q;
+            }
+        }
+        const int64_t col = (int64_t)cv * V;
+        Vec<T, V> vb;
+        if constexpr (BIN) vb = b_nt ? vload_nt<T, V>(b + bo + col) : vload<T, V>(b + bo + col);
+        else {
+            const T sv = b[bo];
+#pragma unroll
+            for (int k = 0; k < V; k++) vb.v[k] = sv;
+        }
+        const uint32_t r0 = chunk * U;
+        Vec<T, V> va[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (u == 0 || r0 + u < R) {
+                const T *ap = a + ao + (int64_t)(r0 + u) * a_top;
+                if constexpr (AIN) va[u] = a_nt ? vload_nt<T, V>(ap + col) : vload<T, V>(ap + col);
+                else {
+                    const T sv = ap[0];
+#pragma unroll
+                    for (int k = 0; k < V; k++) va[u].v[k] = sv;
+                }
+            }
+        }
+        bool bplain = true;
+        double yr[V];
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const T r = vb.v[k];
+            bplain = bplain && r != 0;
+            if constexpr (sizeof(T) == 8) bplain = bplain && r == (T)(int32_t)r;
+            yr[k] = sdiv32_recip_lx((int32_t)r);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (u == 0 || r0 + u < R) {
+                const uint32_t v = (r0 + u) * rest.d + vr;
+                bool plain = bplain;
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    const T l = va[u].v[k], r = vb.v[k];
+                    plain = plain && !(l == (T)std::numeric_limits<int32_t>::min() && r == (T)-1);
+                    if constexpr (sizeof(T) == 8) plain = plain && l == (T)(int32_t)l;
+                }
+                Vec<T, V> vy;
+                if (plain) {
+#pragma unroll
+                    for (int k = 0; k < V; k++) vy.v[k] = (T)sdiv32_quot((int32_t)va[u].v[k], yr[k]);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < V; k++)
+                        vy.v[k] = bin_apply<kDiv, T>(va[u].v[k], vb.v[k], (uint64_t)v * V + k, errs);
+                }
+                vstore_nt<T, V>(y + (int64_t)v * V, vy);
+            }
+        }
+    }
+}
+
 // Same as k_binary_nd for more than 2^31 vectors: 64-bit index arithmetic.
 template <int OP, typename T, int AIN, int BIN, int V>
 __global__ __launch_bounds__(kBlock) void k_binary_nd64(const T *__restrict__ a, const T *__restrict__ b,
@@ -317,6 +404,25 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
     const int key = A.a_inner * 2 + A.b_inner;
     if (nv < (1ll << 31)) {
         constexpr int U = (OP == kDiv && std::is_integral<T>::value && sizeof(T) >= 4) ? kDivVecsPerLane : 1;
+        if constexpr (U > 1) {
+            // divisor constant along the outermost axis: one reciprocal per U quotients
+            const int top = A.nd.nouter - 1;
+            if (nv >= (1 << 20) && top >= 0 && A.nd.b_str[top] == 0 && A.nd.odiv[top].d >= 2 &&
+                nv % A.nd.odiv[top].d == 0) {
+                const uint32_t R = A.nd.odiv[top].d;
+                const int64_t rest = nv / R;
+                const int64_t lanes = rest * ((R + U - 1) / U);
+                const FastDiv fr = make_fastdiv((uint32_t)rest);
+                const int g = grid_for(lanes, kBlock);
+                switch (key) {
+                case 3: hipLaunchKernelGGL((k_div_rows<T, 1, 1, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 2: hipLaunchKernelGGL((k_div_rows<T, 1, 0, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 1: hipLaunchKernelGGL((k_div_rows<T, 0, 1, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                default: hipLaunchKernelGGL((k_div_rows<T, 0, 0, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                }
+                return hipGetLastError();
+            }
+        }
         const int64_t lanes = (U > 1 && nv >= (1 << 20)) ? (nv + U - 1) / U : two ? (nv + 1) / 2 : nv;
         const int g = grid_for(lanes, kBlock);
         switch (key) {

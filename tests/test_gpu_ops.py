@@ -209,6 +209,44 @@ def test_int_div_large_broadcast(hip, dt, inner):
 
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64])
+@pytest.mark.parametrize("a_shape,b_shape", [((7, 3, 200004), (1, 3, 200004)),   # 16-byte vectors
+                                             ((7, 3, 200003), (1, 3, 200003)),   # one element per vector
+                                             ((5, 1, 4096), (1, 256, 4096)),     # C4's layout, 5 rows
+                                             ((6, 4, 262148), (1, 4, 1))])       # divisor broadcast on the inner axis
+def test_int_div_divisor_shared_along_the_outer_axis(hip, dt, a_shape, b_shape):
+    """A divisor that is constant along the outermost output axis has its reciprocal computed once for several
+    quotients (row counts 5-7: not a multiple of the rows per lane).  Bit-exact against the oracle, int64
+    operands outside int32 take the 64-bit path, and the first failing element in output order decides the
+    error."""
+    rng = np.random.default_rng(29)
+    a = rng.integers(-(2**31), 2**31, a_shape, dtype=np.int64)
+    big = rng.integers(-(2**31), 2**31, b_shape, dtype=np.int64)
+    b = np.where(rng.random(b_shape) < 0.5, rng.integers(-1000, 1001, b_shape), big)
+    b[b == 0] = 9
+    b[b == -1] = -9
+    if dt == np.int64:
+        a.flat[::101] *= 3**20
+        b.flat[::103] = b.flat[::103] * 1000 + 1
+    a, b = a.astype(dt), b.astype(dt)
+    a[a == np.iinfo(dt).min] = 5
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), O.binary(O.DIV, a, b))
+    out = np.broadcast_shapes(a_shape, b_shape)
+
+    def at(shape, o):
+        return tuple(o[d] if shape[d] > 1 else 0 for d in range(3))
+    for o_ovf in ((0, 0, 1), tuple(n - 1 for n in out)):
+        a1, b1 = a.copy(), b.copy()
+        b1[at(b_shape, tuple(n // 2 for n in out))] = 0
+        a1[at(a_shape, o_ovf)], b1[at(b_shape, o_ovf)] = np.iinfo(dt).min, -1
+        flat_a = np.broadcast_to(a1, out).reshape(-1)
+        flat_b = np.broadcast_to(b1, out).reshape(-1)
+        first_dbz = np.flatnonzero(flat_b == 0)[0]
+        first_ovf = np.flatnonzero((flat_a == np.iinfo(dt).min) & (flat_b == -1))[0]
+        code = L.ERR_OVERFLOW if first_ovf < first_dbz else L.ERR_DIVIDE_BY_ZERO
+        assert HIP.Div(dev(a1), dev(b1)).Code == code
+
+
+@pytest.mark.parametrize("dt", [np.int32, np.int64])
 def test_int_div_errors(hip, dt):
     info = np.iinfo(dt)
     r = HIP.Div(dev(np.array([4, 5, 6, 7], dt)), dev(np.array([1, 2, 0, 1], dt)))
