@@ -400,10 +400,11 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
     // With an operand streamed once, two vectors per lane: the index
     // decomposition and the NdLayout argument loads are amortised (C3 mask Add
     // on MI355X: 68 us with one vector per lane, 62 us with two, slower again
-    // with four).  Outputs built only from re-read broadcast operands (C4), and
-    // small launch-latency-bound arrays (C1), run fastest with one per lane.
+    // with four; [8,512,768] - [8,512,1]: 5.98 -> 5.81 us).  Outputs built only
+    // from re-read broadcast operands (C4), and small launch-latency-bound
+    // arrays (C1, below 2^16 vectors), run fastest with one per lane.
     const int64_t nv = A.n / V;
-    const bool two = (A.a_once || A.b_once) && nv >= (1 << 20);
+    const bool two = (A.a_once || A.b_once) && nv >= (1 << 16);
     const int key = A.a_inner * 2 + A.b_inner;
     if (nv < (1ll << 31)) {
         constexpr int U = (OP == kDiv && std::is_integral<T>::value && sizeof(T) >= 4) ? kDivVecsPerLane : 1;
