@@ -35,6 +35,7 @@ struct State {
     void *workspace = nullptr;
     int64_t ws_bytes = 0;
     ErrFlags *errs = nullptr;      // device
+    bool errs_clean = false;       // errs holds its cleared state: the last eager check's publish reset it
     struct Mailbox *mail = nullptr;      // mapped, coherent pinned host memory
     struct Mailbox *mail_dev = nullptr;  // the same memory as the device addresses it
     uint64_t mail_seq = 0;
@@ -237,15 +238,24 @@ thread_local ErrFlags *t_defer_slot = nullptr;
 thread_local DeferredCheck *t_defer_rec = nullptr;
 
 int read_errs(ErrFlags *out);
-int read_device(const void *src, size_t bytes, void *dst);
+int read_device(const void *src, size_t bytes, void *dst, bool reset_src = false);
 
 // the error record a checking launch writes, cleared first (one small kernel, never a memset:
-// the stream may be under capture): the deferred slot or the library's own record
+// the stream may be under capture): the deferred slot or the library's own record.  The library's
+// record needs no clearing after an eager check, whose read-back clears it on the device; a stream
+// under capture always records the clearing kernel (a replay must not depend on eager history).
 int check_begin(int kind, int dst, ErrFlags **errs) {
     *errs = t_defer_slot ? t_defer_slot : g.errs;
     if (t_defer_slot && t_defer_rec) {
         t_defer_rec->kind = kind;
         t_defer_rec->dst = dst;
+    }
+    if (!t_defer_slot) {
+        const bool clean = g.errs_clean;
+        g.errs_clean = false;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIPCHECK(hipStreamIsCapturing(g.stream, &cs), "hipStreamIsCapturing");
+        if (clean && cs == hipStreamCaptureStatusNone) return LX_OK;
     }
     HIPCHECK(launch_reset_errs(*errs, g.stream), "reset error flags");
     return LX_OK;
@@ -294,12 +304,15 @@ int read_errs(ErrFlags *out) {
     if (cs != hipStreamCaptureStatusNone)
         return set_err(LX_ERR_NOT_SUPPORTED, "This operator checks its inputs on the device and reads the result "
                                              "back; it cannot run on a stream under capture.");
-    return read_device(g.errs, sizeof(ErrFlags), out);
+    static_assert(sizeof(ErrFlags) % 8 == 0 && sizeof(ErrFlags) / 8 <= kMailWords, "the record takes the mailbox path");
+    const int st = read_device(g.errs, sizeof(ErrFlags), out, true);
+    if (st == LX_OK) g.errs_clean = true;
+    return st;
 }
 
 // The host polls the mailbox's sequence number; every 50 us it asks the stream whether work is still
 // pending, so a device fault ends the wait with that fault's error instead of spinning on.
-int read_device(const void *src, size_t bytes, void *dst) {
+int read_device(const void *src, size_t bytes, void *dst, bool reset_src) {
     if (bytes == 0) return LX_OK;
     if (bytes % 8 || bytes / 8 > (size_t)kMailWords) {
         HIPCHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g.stream), "hipMemcpyAsync(read back)");
@@ -308,7 +321,7 @@ int read_device(const void *src, size_t bytes, void *dst) {
     }
     const uint64_t want = ++g.mail_seq;
     HIPCHECK(launch_publish((const uint64_t *)src, (int64_t)(bytes / 8), g.mail_dev->words, &g.mail_dev->seq, want,
-                            g.stream),
+                            reset_src ? (uint64_t *)const_cast<void *>(src) : nullptr, g.stream),
              "launch publish");
     auto seen = [] { return __atomic_load_n(&g.mail->seq, __ATOMIC_ACQUIRE) == g.mail_seq; };
     const auto t0 = std::chrono::steady_clock::now();

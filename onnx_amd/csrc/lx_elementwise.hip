@@ -79,17 +79,23 @@ hipError_t launch_reset_errs(ErrFlags *e, hipStream_t s) {
 
 // One block: every lane copies its words and fences at system scope, the block
 // meets, then lane 0 stores the sequence number with release semantics.
-__global__ __launch_bounds__(kBlock) void k_publish(const uint64_t *__restrict__ src, int64_t n,
-                                                    uint64_t *__restrict__ dst, uint64_t *seq_dst, uint64_t seq) {
-    for (int64_t i = threadIdx.x; i < n; i += kBlock) dst[i] = src[i];
+// reset (null, or src itself): each word is set to all ones after it has been
+// copied, by the thread that read it -- the cleared state of an error record,
+// so the next check on the stream needs no reset launch of its own
+__global__ __launch_bounds__(kBlock) void k_publish(const uint64_t *src, int64_t n, uint64_t *__restrict__ dst,
+                                                    uint64_t *seq_dst, uint64_t seq, uint64_t *reset) {
+    for (int64_t i = threadIdx.x; i < n; i += kBlock) {
+        dst[i] = src[i];
+        if (reset) reset[i] = ~0ull;
+    }
     __threadfence_system();
     __syncthreads();
     if (threadIdx.x == 0) __hip_atomic_store(seq_dst, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 hipError_t launch_publish(const uint64_t *src, int64_t n, uint64_t *dst, uint64_t *seq_dst, uint64_t seq,
-                          hipStream_t s) {
-    hipLaunchKernelGGL(k_publish, dim3(1), dim3(kBlock), 0, s, src, n, dst, seq_dst, seq);
+                          uint64_t *reset, hipStream_t s) {
+    hipLaunchKernelGGL(k_publish, dim3(1), dim3(kBlock), 0, s, src, n, dst, seq_dst, seq, reset);
     return hipGetLastError();
 }
 

@@ -52,8 +52,9 @@ struct BinArgs {
 hipError_t launch_reset_errs(ErrFlags *e, hipStream_t s);
 // Copies n 64-bit words from device memory into mapped host memory, then writes seq to *seq_dst
 // after a system-scope release: the host waits for the sequence number instead of the stream.
+// reset: null, or src itself, whose words are then set to all ones once copied.
 hipError_t launch_publish(const uint64_t *src, int64_t n, uint64_t *dst, uint64_t *seq_dst, uint64_t seq,
-                          hipStream_t s);
+                          uint64_t *reset, hipStream_t s);
 hipError_t launch_binary(const BinArgs &args, ErrFlags *errs, hipStream_t s);
 hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, int vec, hipStream_t s);
 hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,

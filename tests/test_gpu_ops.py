@@ -410,6 +410,38 @@ def test_cast_int64_to_float_rounding(hip):
     assert_bits(ok(HIP.Cast(dev(x), O.FLOAT)), O.cast(x, O.FLOAT))
 
 
+def test_checked_calls_in_a_row_report_their_own_status(hip):
+    """Integer Div, Gather and narrowing Cast share one device error record; after each eager check the
+    read-back leaves it cleared, and the next check starts from that.  A failure is never reported again by
+    a later call, and a success never hides a later failure."""
+    a = np.arange(1, 9, dtype=np.int32)
+    table = np.arange(12, dtype=np.float32).reshape(4, 3)
+    steps = [
+        ("div", lambda: HIP.Div(dev(a), dev(np.full(8, 2, np.int32))), None),
+        ("div by zero", lambda: HIP.Div(dev(a), dev(np.array([1, 2, 3, 0, 5, 6, 7, 8], np.int32))),
+         L.ERR_DIVIDE_BY_ZERO),
+        ("gather", lambda: HIP.Gather(dev(table), dev(np.array([3, -4, 0], np.int64)), 0), None),
+        ("gather out of range", lambda: HIP.Gather(dev(table), dev(np.array([1, 4], np.int64)), 0),
+         L.ERR_INVALID_ARGUMENT),
+        ("gather out of range again", lambda: HIP.Gather(dev(table), dev(np.array([-5], np.int64)), 0),
+         L.ERR_INVALID_ARGUMENT),
+        ("cast", lambda: HIP.Cast(dev(np.array([1.5, -2.5], np.float64)), O.INT32), None),
+        ("cast overflow", lambda: HIP.Cast(dev(np.array([300], np.int32)), O.UINT8), L.ERR_OVERFLOW),
+        ("div overflow", lambda: HIP.Div(dev(np.array([-(2**31)], np.int32)), dev(np.array([-1], np.int32))),
+         L.ERR_OVERFLOW),
+        ("div after failures", lambda: HIP.Div(dev(a), dev(np.full(8, 3, np.int32))), None),
+        ("cast after", lambda: HIP.Cast(dev(np.array([255], np.int32)), O.UINT8), None),
+    ]
+    for _ in range(2):
+        for name, call, code in steps:
+            r = call()
+            if code is None:
+                assert r.Status == OpStatus.Success, (name, r.Message)
+            else:
+                assert r.Status == OpStatus.Failure and r.Code == code, (name, r.Code, r.Message)
+    assert_bits(ok(HIP.Div(dev(a), dev(np.full(8, -3, np.int32)))), O.binary(O.DIV, a, np.full(8, -3, np.int32)))
+
+
 def test_cast_overflow_errors(hip):
     for vals, dt, to in [([1.0, 2147483647.5], np.float64, O.INT32), ([np.nan], np.float32, O.INT64),
                          ([300], np.int32, O.UINT8), ([-1], np.int64, O.UINT64), ([2**40], np.int64, O.INT32)]:
