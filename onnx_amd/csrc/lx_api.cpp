@@ -137,6 +137,18 @@ int64_t numel(const lx_tensor *t) { return numel_of(t->rank, t->dims); }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// Whether the fused LayerNorm kernel, which applies gamma / beta along X's last axis, computes what the
+// reference's Mul / Add nodes compute (ITensor.Broadcast, ITensor.cs:92-117): the affine tensor must be
+// [1, ..., 1, r] with r X's last dimension and no more axes than X.  Any other shape either broadcasts
+// differently (gamma [r, 1] against X [r, r] runs down the columns) or cannot broadcast at all, and takes
+// the node-by-node path, which gives the reference's result or its CannotBroadcast.
+bool layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X) {
+    if (t->rank < 1 || t->rank > X->rank || t->dims[t->rank - 1] != X->dims[X->rank - 1]) return false;
+    for (int i = 0; i < t->rank - 1; i++)
+        if (t->dims[i] != 1) return false;
+    return true;
+}
+
 // structural validity of a caller-provided tensor
 int check_tensor(const lx_tensor *t, const char *name) {
     if (t->rank < 0 || t->rank > LX_MAX_RANK)
@@ -242,8 +254,9 @@ int read_device(const void *src, size_t bytes, void *dst, bool reset_src = false
 
 // the error record a checking launch writes, cleared first (one small kernel, never a memset:
 // the stream may be under capture): the deferred slot or the library's own record.  The library's
-// record needs no clearing after an eager check, whose read-back clears it on the device; a stream
-// under capture always records the clearing kernel (a replay must not depend on eager history).
+// record needs no clearing after an eager check, whose read-back clears it on the device.  A deferred
+// slot is always cleared by a recorded kernel (a replay must not depend on eager history); an eager
+// check on a stream under capture is refused before it records anything.
 int check_begin(int kind, int dst, ErrFlags **errs) {
     *errs = t_defer_slot ? t_defer_slot : g.errs;
     if (t_defer_slot && t_defer_rec) {
@@ -251,11 +264,17 @@ int check_begin(int kind, int dst, ErrFlags **errs) {
         t_defer_rec->dst = dst;
     }
     if (!t_defer_slot) {
-        const bool clean = g.errs_clean;
-        g.errs_clean = false;
+        // an eager check ends in a host read, which a stream under capture cannot make: refuse before
+        // anything is recorded, so no recorded graph ever writes the library's record (a replay would
+        // leave it dirty behind the host's back)
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         HIPCHECK(hipStreamIsCapturing(g.stream, &cs), "hipStreamIsCapturing");
-        if (clean && cs == hipStreamCaptureStatusNone) return LX_OK;
+        if (cs != hipStreamCaptureStatusNone)
+            return set_err(LX_ERR_NOT_SUPPORTED, "This operator checks its inputs on the device and reads the result "
+                                                 "back; it cannot run on a stream under capture.");
+        const bool clean = g.errs_clean;
+        g.errs_clean = false;
+        if (clean) return LX_OK;
     }
     HIPCHECK(launch_reset_errs(*errs, g.stream), "reset error flags");
     return LX_OK;
@@ -708,6 +727,7 @@ void api_defer_checks(ErrFlags *slot, DeferredCheck *rec) {
     t_defer_rec = rec;
 }
 int api_check_status(const DeferredCheck &rec, const ErrFlags &flags) { return check_status(rec.kind, rec.dst, flags); }
+bool api_layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X) { return layernorm_affine_fits(t, X); }
 int api_read_device(const void *src, size_t bytes, void *dst) { return read_device(src, bytes, dst); }
 }  // namespace lx
 
@@ -1081,8 +1101,7 @@ int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_
         return st;
     const int64_t r = X->rank > 0 ? X->dims[X->rank - 1] : 0;
     const bool fused = X->dtype == LX_FLOAT && gamma->dtype == LX_FLOAT && beta->dtype == LX_FLOAT && X->rank >= 1 &&
-                       numel(gamma) == r && numel(beta) == r && gamma->rank >= 1 && beta->rank >= 1 &&
-                       gamma->rank <= X->rank && beta->rank <= X->rank && layernorm_supported(r) &&
+                       layernorm_affine_fits(gamma, X) && layernorm_affine_fits(beta, X) && layernorm_supported(r) &&
                        numel(X) / r < (1ll << 31) &&  // one block per row
                        aligned16(X->data) && aligned16(gamma->data) && aligned16(beta->data);
     if (fused) {

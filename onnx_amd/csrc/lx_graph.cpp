@@ -229,6 +229,14 @@ struct Exec {
         if (it != g->input_vals.end()) { *out = &it->second; return LX_OK; }
         auto ii = g->init_dev.find(name);
         if (ii != g->init_dev.end()) { *out = &ii->second; return LX_OK; }
+        for (auto &kv : g->initializers) {  // read only by the original nodes of a fused subgraph
+            if (kv.first != name) continue;
+            Value v;
+            int st = value_from_host(kv.second, &v);
+            if (st) return st;
+            *out = &(g->init_dev[name] = v);
+            return LX_OK;
+        }
         auto vi = g->values.find(name);
         if (vi != g->values.end()) { *out = &vi->second; return LX_OK; }
         if (is_node_output(name))
@@ -685,8 +693,10 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
     }
     if (op == "LayerNormDecomposed") {
         if ((st = X.input(n, 0, &a)) || (st = X.input(n, 1, &b)) || (st = X.input(n, 2, &c))) return st;
+        // the fused kernel applies gamma and beta along the last axis: other shapes run the nodes, which
+        // broadcast them as the reference does (or fail with its CannotBroadcast)
         if (!a || !b || !c || a->t.dtype != LX_FLOAT || b->t.dtype != LX_FLOAT || c->t.dtype != LX_FLOAT ||
-            a->t.rank < 1)
+            a->t.rank < 1 || !api_layernorm_affine_fits(&b->t, &a->t) || !api_layernorm_affine_fits(&c->t, &a->t))
             return run_unfused(X, n, outs);
         const Attr *eps = find_attr(n, "epsilon");
         const float e = eps ? eps->f : 1e-12f;
@@ -733,6 +743,7 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         for (int64_t gi = 0; gi < G; gi++) {
             Value v = whole;
             v.t.data = (char *)y.data + gi * M * Nn * (int64_t)sizeof(float);
+            v.t.capacity = M * Nn * (int64_t)sizeof(float);  // the slice's own bytes, not the whole product's
             v.t.rank = av->t.rank;
             for (int i = 0; i < LX_MAX_RANK; i++) v.t.dims[i] = i < av->t.rank - 1 ? av->t.dims[i] : 0;
             v.t.dims[av->t.rank - 1] = Nn;
@@ -1137,6 +1148,29 @@ struct Fuser {
     // biases [G, 1, N] -- one batched launch instead of G launches that each leave CUs idle (the Q, K, V
     // projections of an attention layer).  Its outputs are the G slices of one [G, M, N] product, each
     // bit-identical to its MatMulAdd.  Placed where the first of them was.  Returns the nodes removed.
+    // a tensor name that no initializer, fused constant, graph input or output, or node input or output
+    // (the original nodes of fused subgraphs included) uses: nodes may be unnamed, so a name derived from
+    // a node's could repeat
+    std::string fresh_name(const char *prefix) {
+        std::set<std::string> taken(g->outputs.begin(), g->outputs.end());
+        for (auto &kv : g->initializers) taken.insert(kv.first);
+        for (auto &kv : g->fused_consts) taken.insert(kv.first);
+        for (auto &in : g->inputs) taken.insert(in.name);
+        std::vector<const GNode *> todo;
+        for (auto &n : g->nodes) todo.push_back(&n);
+        while (!todo.empty()) {
+            const GNode *n = todo.back();
+            todo.pop_back();
+            taken.insert(n->in.begin(), n->in.end());
+            taken.insert(n->out.begin(), n->out.end());
+            for (auto &m : n->fused_from) todo.push_back(&m);
+        }
+        for (;;) {
+            std::string s = prefix + std::to_string(g->fused_names++);
+            if (!taken.count(s)) return s;
+        }
+    }
+
     int group_projections() {
         index();
         std::map<std::pair<std::string, std::pair<int64_t, int64_t>>, std::vector<int>> groups;
@@ -1177,9 +1211,9 @@ struct Fuser {
                 for (auto &o : n.fused_from) f.fused_from.push_back(o);
                 if (n.fused_from.empty()) f.fused_from.push_back(n);
             }
-            const std::string wn = "__group_w_" + f.name, bn = "__group_b_" + f.name;
-            g->initializers.push_back({wn, w});
-            g->initializers.push_back({bn, b});
+            const std::string wn = fresh_name("__group_w_"), bn = fresh_name("__group_b_");
+            g->fused_consts.push_back({wn, w});
+            g->fused_consts.push_back({bn, b});
             f.in = {kv.first.first, wn, bn};
             at[ms[0]] = f;
             for (size_t k = 1; k < ms.size(); k++) drop.insert(ms[k]);
@@ -1197,13 +1231,30 @@ struct Fuser {
     }
 };
 
+// the names an execution can read from the initializers without a fallback: inputs of the current
+// nodes, graph outputs, and graph inputs (which an initializer of the same name may serve)
+std::set<std::string> live_names(const lx_graph *g) {
+    std::set<std::string> live(g->outputs.begin(), g->outputs.end());
+    for (auto &n : g->nodes) live.insert(n.in.begin(), n.in.end());
+    for (auto &in : g->inputs) live.insert(in.name);
+    return live;
+}
+
+// Uploads the initializers an execution reads and the fused constants.  An initializer that only the
+// original nodes of a fused subgraph read (the separate Q / K / V weights once they are stacked) stays in
+// host memory and is uploaded by the first lookup that needs it, i.e. when a fused node falls back to its
+// original nodes.
 int upload_initializers(lx_graph *g) {
-    for (auto &kv : g->initializers) {
-        if (g->init_dev.count(kv.first)) continue;
-        Value v;
-        int st = value_from_host(kv.second, &v);
-        if (st) return st;
-        g->init_dev[kv.first] = v;
+    const std::set<std::string> live = live_names(g);
+    for (auto *list : {&g->initializers, &g->fused_consts}) {
+        for (auto &kv : *list) {
+            if (g->init_dev.count(kv.first)) continue;
+            if (list == &g->initializers && !live.count(kv.first)) continue;
+            Value v;
+            int st = value_from_host(kv.second, &v);
+            if (st) return st;
+            g->init_dev[kv.first] = v;
+        }
     }
     return LX_OK;
 }
@@ -1433,8 +1484,9 @@ int lx_graph_add_initializer(lx_graph *g, const char *name, int32_t dtype, int32
     if (nbytes != want || (want > 0 && !host))
         return failure(fmt("Initializer %s holds %lld bytes, its shape needs %lld.", name, (long long)nbytes, (long long)want));
     h->bytes.assign((const uint8_t *)host, (const uint8_t *)host + nbytes);
-    for (auto &kv : g->initializers)
-        if (kv.first == name) return failure(fmt("An item with the same key has already been added. Key: %s", name));
+    for (auto *list : {&g->initializers, &g->fused_consts})
+        for (auto &kv : *list)
+            if (kv.first == name) return failure(fmt("An item with the same key has already been added. Key: %s", name));
     g->initializers.push_back({name, h});
     g->init_dev.erase(name);
     return LX_OK;
@@ -1548,6 +1600,14 @@ int lx_graph_fuse(lx_graph *g, int32_t *n_fused) {
     f.g = g;
     int k = f.run();
     if (n_fused) *n_fused = k;
+    // device copies of initializers that no remaining node reads (uploaded at load) are dropped; a
+    // fallback to the original nodes uploads them again on first use
+    const std::set<std::string> live = live_names(g);
+    for (auto it = g->init_dev.begin(); it != g->init_dev.end();) {
+        bool keep = live.count(it->first) > 0;
+        for (auto &kv : g->fused_consts) keep = keep || kv.first == it->first;
+        it = keep ? std::next(it) : g->init_dev.erase(it);
+    }
     return LX_OK;
 }
 

@@ -93,6 +93,9 @@ struct lx_graph {
     std::vector<lx::GInput> inputs;
     std::vector<std::string> outputs;
     std::vector<std::pair<std::string, std::shared_ptr<lx::HostTensor>>> initializers;
+    // constants made by fusion (stacked projection weights): served like initializers, not listed as them
+    std::vector<std::pair<std::string, std::shared_ptr<lx::HostTensor>>> fused_consts;
+    int64_t fused_names = 0;                    // counter behind the fused constants' names
     std::map<std::string, lx::Value> init_dev;  // initializers resident in HBM
     std::map<std::string, lx::Value> input_vals;  // graph.Inputs of the current execution
     std::map<std::string, lx::Value> values;    // node outputs of the current execution

@@ -6,6 +6,8 @@
 
 #include <string>
 
+#include "../../include/lonnx.h"
+
 namespace lx {
 
 int api_set_error(int code, const std::string &message);  // sets lx_last_error, returns code
@@ -30,5 +32,10 @@ void api_defer_checks(ErrFlags *slot, DeferredCheck *rec);
 // library stream: the caller returns as soon as the device has written them (no stream-sync wake-up).
 int api_read_device(const void *src, size_t bytes, void *dst);
 int api_check_status(const DeferredCheck &rec, const ErrFlags &flags);  // sets lx_last_error on failure
+
+// Whether gamma / beta of a decomposed LayerNorm are [1, ..., 1, r] against X (r = X's last dimension,
+// rank at most X's): the shapes for which the fused kernel's last-axis affine step equals the Mul / Add
+// nodes' broadcast.
+bool api_layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X);
 
 }  // namespace lx

@@ -96,6 +96,38 @@ def test_c2_layernorm_graph(hip, fuse, shape):
     assert close(got["y"], ref["y"], np.abs(ref["y"]))
 
 
+@pytest.mark.parametrize("shape,gshape", [((8, 512, 768), (768, 1)), ((768, 768), (768, 1)), ((16, 64), (2, 32))])
+def test_layernorm_graph_affine_shapes_follow_the_nodes(hip, shape, gshape):
+    """A fused LayerNorm node whose gamma is not [1, ..., 1, r] runs its nine nodes: the same result bit for
+    bit as the unfused graph when gamma broadcasts down the columns, the same failure (node, op, message)
+    when it cannot broadcast."""
+    rng = np.random.default_rng(27)
+    r = shape[-1]
+    x = (rng.standard_normal(shape) * 2).astype(np.float32)
+    inits = LN_INITS(r)
+    inits[3] = ("gamma", (1 + 0.02 * rng.standard_normal(gshape)).astype(np.float32))
+    inits[4] = ("beta", (0.02 * rng.standard_normal(r)).astype(np.float32))
+    res = {}
+    for fuse in (False, True):
+        g = Model.Load(W.model(ln_nodes(), [("x", np.float32, shape)], [("y", np.float32, shape)], inits))
+        if fuse:
+            assert g.Fuse() == 1 and [n.Op for n in g.Nodes] == ["LayerNormDecomposed"]
+        ok_ = g.Execute({"x": DeviceTensor.from_numpy(x)})
+        res[fuse] = (ok_, g.LastError if not ok_ else g.Output("y").to_numpy())
+        g.close()
+    try:
+        ref = GO.run(_dict_nodes(ln_nodes()), {"x": x}, dict(inits), 13)["y"]
+    except Exception:
+        ref = None
+    if gshape[0] == shape[-2]:
+        assert res[False][0] and res[True][0], res
+        assert bits(res[False][1], res[True][1])
+        assert ref is not None and close(res[True][1], ref, np.abs(ref))
+    else:
+        assert not res[False][0] and not res[True][0] and ref is None
+        assert res[False][1] == res[True][1] and "mulg" in res[True][1], res
+
+
 @pytest.mark.parametrize("fuse", [False, True])
 def test_c3_mask_softmax_graph(hip, fuse):
     rng = np.random.default_rng(3)

@@ -204,3 +204,56 @@ def test_grouped_projections_equal_the_separate_ones(hip):
         res[fuse] = [g.Output(o).to_numpy() for o in outs]
     for u, f in zip(res[False], res[True]):
         assert u.shape == f.shape and np.array_equal(u.view(np.uint32), f.view(np.uint32))
+
+
+def _two_unnamed_projection_layers(rng):
+    """Two layers of three MatMul -> Add bias projections each, every node unnamed (ONNX allows it); the
+    second layer reads the first one's V and has weights of its own."""
+    import onnx_writer as W
+    inits, nodes = [], []
+    for layer, src in ((0, "x"), (1, "v0")):
+        for t in "qkv":
+            inits += [(f"w{t}{layer}", (rng.standard_normal((64, 64)) * 0.1).astype(np.float32)),
+                      (f"b{t}{layer}", rng.standard_normal(64).astype(np.float32))]
+            nodes += [W.node("MatMul", [src, f"w{t}{layer}"], [f"{t}{layer}p"]),
+                      W.node("Add", [f"{t}{layer}p", f"b{t}{layer}"], [f"{t}{layer}"])]
+    return nodes, inits
+
+
+def test_grouped_projections_of_unnamed_layers_keep_their_own_weights(hip):
+    """Each group of unnamed projections stacks its own weights: the fused graph equals the unfused one bit
+    for bit in both layers (a name derived from the node's name would let the second group read the
+    first group's stacked weights)."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    rng = np.random.default_rng(92)
+    x = rng.standard_normal((2, 40, 64)).astype(np.float32)
+    nodes, inits = _two_unnamed_projection_layers(rng)
+    outs = ["q0", "k0", "v0", "q1", "k1", "v1"]
+    res = {}
+    for fuse in (False, True):
+        g = Model.Load(W.model(nodes, [("x", np.float32, x.shape)], [(o, np.float32, ()) for o in outs], inits))
+        if fuse:
+            assert g.Fuse() == 2 and [n.Op for n in g.Nodes] == ["MatMulAddGroup", "MatMulAddGroup"]
+        assert g.Execute({"x": dev(x)}), g.LastError
+        res[fuse] = [g.Output(o).to_numpy() for o in outs]
+        g.close()
+    for o, u, f in zip(outs, res[False], res[True]):
+        assert u.shape == f.shape and np.array_equal(u.view(np.uint32), f.view(np.uint32)), o
+
+
+def test_grouped_projection_slice_capacity_is_its_own(hip):
+    """An output slice of a grouped projection reports its own bytes as capacity, so reusing it as output
+    storage cannot write past the slice."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    rng = np.random.default_rng(93)
+    x = rng.standard_normal((2, 40, 64)).astype(np.float32)
+    nodes, inits = _two_unnamed_projection_layers(rng)
+    g = Model.Load(W.model(nodes[:6], [("x", np.float32, x.shape)], [(o, np.float32, ()) for o in ("q0", "k0", "v0")],
+                           inits[:6]))
+    assert g.Fuse() == 1
+    assert g.Execute({"x": dev(x)}), g.LastError
+    for o in ("q0", "k0", "v0"):
+        assert g.Output(o).h.capacity == 2 * 40 * 64 * 4, o
+    g.close()

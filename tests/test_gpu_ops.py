@@ -607,6 +607,55 @@ def test_layernorm(hip, shape):
     assert np.all(err <= 1e-5 * np.maximum(1.0, np.abs(ref))), err.max()
 
 
+def _layernorm_nodes(x, g, b):
+    """The nine operators one by one through the C ABI (what the reference's graph runs)."""
+    two, eps, ax = dev(np.array(2.0, np.float32)), dev(np.array(1e-12, np.float32)), [-1]
+    X = dev(x)
+    mean = HIP.ReduceMean(X, ax, 1).Outputs[0]
+    d = HIP.Sub(X, mean).Outputs[0]
+    p = HIP.Pow(d, two).Outputs[0]
+    var = HIP.ReduceMean(p, ax, 1).Outputs[0]
+    sd = HIP.Sqrt(HIP.Add(var, eps).Outputs[0]).Outputs[0]
+    m = HIP.Mul(HIP.Div(d, sd).Outputs[0], dev(g))
+    if m.Status != OpStatus.Success:
+        return m
+    return HIP.Add(m.Outputs[0], dev(b))
+
+
+@pytest.mark.parametrize("xs,gs,bs,expect", [
+    ((8, 512, 768), (768, 1), (768,), "cannot"),     # Mul [8,512,768] x [768,1]: 512 vs 768
+    ((4, 16, 768), (2, 384), (768,), "cannot"),      # same element count, other shape
+    ((4, 16, 768), (768,), (1, 2, 384), "cannot"),   # beta of the wrong shape
+    ((768, 768), (768, 1), (768,), "columns"),       # gamma broadcast down the columns
+    ((64, 64), (64,), (64, 1), "columns"),           # beta down the columns
+    ((8, 512, 768), (1, 1, 768), (1, 768), "fused"),  # leading ones: the fused kernel's shape
+])
+def test_layernorm_affine_shapes_follow_the_nodes(hip, xs, gs, bs, expect):
+    """The fused LayerNorm applies gamma / beta along the last axis; any other affine shape must give what
+    the reference's Mul / Add nodes give: CannotBroadcast (ITensor.cs:113-117) or their broadcast."""
+    rng = np.random.default_rng(26)
+    x = (rng.standard_normal(xs) * 2).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(gs)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(bs)).astype(np.float32)
+    r = HIP.LayerNormDecomposed(dev(x), dev(g), dev(b), 1e-12)
+    if expect == "cannot":
+        assert r.Code == L.ERR_CANNOT_BROADCAST, (r.Code, r.Message)
+        with pytest.raises(O.OracleError):
+            O.layernorm_decomposed(x, g, b, np.float32(1e-12))
+        return
+    assert r.Status == OpStatus.Success, r.Message
+    got = r.Outputs[0].to_numpy()
+    ref = O.layernorm_decomposed(x, g, b, np.float32(1e-12))
+    assert got.shape == ref.shape == x.shape
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * np.maximum(1.0, np.abs(ref))), err.max()
+    if expect == "columns":
+        # not the last-axis application: the node-by-node path, bit for bit
+        assert_bits(got, ok(_layernorm_nodes(x, g, b)))
+        wrong = O.layernorm_decomposed(x, g.reshape(-1), b.reshape(-1), np.float32(1e-12))
+        assert np.abs(wrong - ref).max() > 1e-3
+
+
 def test_output_reuse_and_capacity(hip):
     a = dev(np.arange(12, dtype=np.float32).reshape(3, 4))
     out = DeviceTensor.empty((3, 4), np.float32)

@@ -247,3 +247,17 @@ def test_scaled_softmax_pattern():
     # a divisor that is not a scalar constant: the plain Add -> Softmax pattern
     inits2 = [("c", np.full(8, 8.0, np.float32)), ("mask", np.zeros((1, 8), np.float32))]
     assert _fused(nodes, inits2) == (1, [("scale", "Div"), ("sm", "AddSoftmax")])
+
+
+def test_grouped_projection_constants_are_not_initializers():
+    """Grouping unnamed projections makes one stacked weight / bias pair per group under names no other
+    tensor uses; the graph's initializer list (graph.Initializers) stays what the model holds."""
+    from test_gpu_matmul import _two_unnamed_projection_layers
+    rng = np.random.default_rng(94)
+    nodes, inits = _two_unnamed_projection_layers(rng)
+    outs = ["q0", "k0", "v0", "q1", "k1", "v1"]
+    g = Model.Load(W.model(nodes, [("x", np.float32, (2, 40, 64))], [(o, np.float32, ()) for o in outs], inits))
+    before = g.InitializerInfo
+    assert g.Fuse() == 2
+    assert [n.Op for n in g.Nodes] == ["MatMulAddGroup", "MatMulAddGroup"]
+    assert g.InitializerInfo == before and len(before) == 12
