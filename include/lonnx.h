@@ -216,6 +216,13 @@ enum { LX_CHAIN_ADD = 0, LX_CHAIN_SUB = 1, LX_CHAIN_MUL = 2, LX_CHAIN_DIV = 3, L
 int lx_ElementwiseChain(const lx_tensor *const *inputs, int32_t n_in, const int32_t *ops, const int32_t *operands,
                         int32_t n_ops, lx_tensor *Y);
 
+/* ---- diagnostics (no reference counterpart) ---------------------------------
+ * The HBM ceiling a read-only stream reaches on this GPU, the bound of the whole-tensor reductions:
+ * reads `bytes` (a multiple of 16, 16-byte aligned) at src with nontemporal 16-byte loads and writes one
+ * 32-bit XOR of what each block read to out, which holds out_bytes / 4 words (the launch uses at most
+ * that many blocks of 256 lanes, each reading 4 x 4 KiB per grid-stride step).  Stream-ordered. */
+int lx_read_probe(const void *src, int64_t bytes, void *out, int64_t out_bytes);
+
 /* ---- graph runtime: ComputationalGraph + Node.Execute on the device -------
  * (src/Lokad.Onnx.Backend/ComputationalGraph.cs, Node.cs, Model.cs).  Graph
  * inputs, initializers, intermediates and outputs stay in HBM for the whole

@@ -14,7 +14,7 @@ LIB = os.path.join(HERE, "liblonnx_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("LONNX_OFFLOAD_ARCH", "gfx950")
 
-SOURCES = ["lx_elementwise.hip", "lx_reduce.hip", "lx_softmax.hip", "lx_matmul.hip", "lx_movement.hip", "lx_api.cpp",
+SOURCES = ["lx_elementwise.hip", "lx_reduce.hip", "lx_softmax.hip", "lx_matmul.hip", "lx_movement.hip", "lx_probe.hip", "lx_api.cpp",
            "lx_pool.cpp", "lx_graph.cpp", "lx_onnx.cpp"]
 
 # -ffp-contract=off: no FMA contraction of separately rounded float ops.

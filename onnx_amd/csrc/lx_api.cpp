@@ -137,6 +137,28 @@ int64_t numel(const lx_tensor *t) { return numel_of(t->rank, t->dims); }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// [lo, hi] of an integer element type (Bool as 0..1); false for floating types
+bool int_range(int t, __int128 *lo, __int128 *hi) {
+    switch (t) {
+    case LX_BOOL: *lo = 0; *hi = 1; return true;
+    case LX_UINT8: *lo = 0; *hi = UINT8_MAX; return true;
+    case LX_INT8: *lo = INT8_MIN; *hi = INT8_MAX; return true;
+    case LX_UINT16: *lo = 0; *hi = UINT16_MAX; return true;
+    case LX_INT16: *lo = INT16_MIN; *hi = INT16_MAX; return true;
+    case LX_UINT32: *lo = 0; *hi = UINT32_MAX; return true;
+    case LX_INT32: *lo = INT32_MIN; *hi = INT32_MAX; return true;
+    case LX_UINT64: *lo = 0; *hi = UINT64_MAX; return true;
+    case LX_INT64: *lo = INT64_MIN; *hi = INT64_MAX; return true;
+    default: return false;
+    }
+}
+
+// whether every value of integer type src is a value of integer type dst
+bool int_range_contains(int dst, int src) {
+    __int128 dl, dh, sl, sh;
+    return int_range(dst, &dl, &dh) && int_range(src, &sl, &sh) && dl <= sl && sh <= dh;
+}
+
 // Whether the fused LayerNorm kernel, which applies gamma / beta along X's last axis, computes what the
 // reference's Mul / Add nodes compute (ITensor.Broadcast, ITensor.cs:92-117): the affine tensor must be
 // [1, ..., 1, r] with r X's last dimension and no more axes than X.  Any other shape either broadcasts
@@ -918,8 +940,10 @@ int lx_Cast(const lx_tensor *X, int64_t to, lx_tensor *Y) {
     const int64_t n = numel(X);
     if (n == 0) return LX_OK;
     const int src = X->dtype;
-    // only conversions into an integer type can raise OverflowException
-    const bool can_overflow = dst != LX_FLOAT && dst != LX_DOUBLE && dst != LX_BOOL && src != dst;
+    // only conversions into an integer type can raise OverflowException, and only when the source's
+    // values are not all inside the target's range (widening integer casts cannot)
+    const bool can_overflow = dst != LX_FLOAT && dst != LX_DOUBLE && dst != LX_BOOL && src != dst &&
+                              !int_range_contains(dst, src);
     const int vec = aligned16(X->data) && aligned16(Y->data) ? 2 : 1;
     ErrFlags *errs = g.errs;
     if (can_overflow && (st = check_begin(kCheckCast, dst, &errs))) return st;
@@ -960,6 +984,14 @@ int lx_ScaleAddSoftmax(const lx_tensor *S, const lx_tensor *scale, int32_t divid
     if (!S) return missing_input(divide ? "Div" : "Mul", "A");
     if (!scale) return missing_input(divide ? "Div" : "Mul", "B");
     return run_softmax(S, mask, axis, 1, Y, "Softmax", scale, divide ? 1 : 0);
+}
+
+int lx_read_probe(const void *src, int64_t bytes, void *out, int64_t out_bytes) {
+    REQUIRE_INIT();
+    if (!src || !out || bytes < 0 || out_bytes < 4) return set_err(LX_ERR_INVALID_ARGUMENT, "invalid probe arguments");
+    if (bytes % 16 || !aligned16(src)) return set_err(LX_ERR_INVALID_ARGUMENT, "the probe reads whole aligned 16-byte vectors");
+    HIPCHECK(launch_read_probe(src, bytes, (uint32_t *)out, out_bytes / 4, g.stream), "read probe");
+    return LX_OK;
 }
 
 int lx_GeluErf(const lx_tensor *X, lx_tensor *Y) {

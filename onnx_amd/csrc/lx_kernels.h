@@ -60,6 +60,8 @@ hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, in
 hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,
                        hipStream_t s);
 hipError_t launch_gelu_erf(const float *x, float *y, int64_t n, int vec, hipStream_t s);
+// Reads `bytes` (16-byte vectors) with nontemporal loads, one word per block into out (at most max_blocks).
+hipError_t launch_read_probe(const void *src, int64_t bytes, uint32_t *out, int64_t max_blocks, hipStream_t s);
 
 // Elementwise chain (float32): acc = in[0], then per instruction k
 //   binary op[k] in BinOp:   acc = acc op in[j]   (operand[k] = j >= 0)
