@@ -153,6 +153,16 @@ int lx_Cast(const lx_tensor *input, int64_t to, lx_tensor *Y);
  * axes: n_axes < 0 means the axes input is absent; keepdims / noop: < 0 means attribute absent. */
 int lx_ReduceSum(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims,
                  int32_t noop_with_empty_axes, lx_tensor *Y);
+/* ReduceSum that allocates nothing (no counterpart in the reference): for callers that cannot call
+ * hipMalloc -- code under HIP graph capture, tight serving loops, harnesses that forbid allocation.  Same
+ * arguments, validation, results and errors as lx_ReduceSum, except that Y must already hold device storage
+ * of sufficient capacity, and that split partials (at most 2 MiB) and the intermediate of each pass of a
+ * multi-pass reduction (at most 1 MiB each) live in a 4 MiB static device array per GPU instead of the
+ * library's workspace and pool; a reduction that needs more fails with LX_ERR_NOT_SUPPORTED before
+ * anything is launched.  Calls on one GPU share that array: calls that overlap on one GPU (other
+ * streams or threads) race. */
+int lx_ReduceSum_noalloc(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims,
+                         int32_t noop_with_empty_axes, lx_tensor *Y);
 /* CPUExecutionProvider.ReduceMean (CPUExecutionProvider.cs:642-660). */
 int lx_ReduceMean(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int32_t keepdims,
                   int32_t noop_with_empty_axes, lx_tensor *Y);

@@ -87,6 +87,7 @@ SIGNATURES = {
     "lx_Erf": (_c.c_int, [_T, _T]),
     "lx_Cast": (_c.c_int, [_T, _c.c_int64, _T]),
     "lx_ReduceSum": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _c.c_int32, _T]),
+    "lx_ReduceSum_noalloc": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _c.c_int32, _T]),
     "lx_ReduceMean": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _c.c_int32, _T]),
     "lx_ReduceMax": (_c.c_int, [_T, _i64p, _c.c_int32, _c.c_int32, _T]),
     "lx_Softmax": (_c.c_int, [_T, _c.c_int32, _c.c_int32, _T]),

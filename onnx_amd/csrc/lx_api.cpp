@@ -52,6 +52,25 @@ struct Mailbox {
 State g;
 thread_local std::string g_err;
 
+// ---- the allocation-free entry point's device memory ------------------------------------------
+// One file-scope device array per GPU, loaded with the library's code object and held until the
+// process ends.  Its name is a host-side stand-in: host code uses only the address hipGetSymbolAddress
+// returns for the current device (scratch_addr), resolved once per device by lx_init.  Layout: split
+// partials first, then two slots for the intermediates of multi-pass reductions.  Every allocation-free
+// call on a GPU shares that GPU's array, which keeps the last call's contents (nothing in it needs to
+// start at zero: partials and intermediates are written before they are read); calls that overlap on
+// one GPU (other streams, other threads) race.
+constexpr int64_t kScratchWsBytes = 2 << 20;    // partials: the reduction planner never needs more
+constexpr int64_t kScratchTempBytes = 1 << 20;  // per intermediate slot
+constexpr int64_t kScratchBytes = kScratchWsBytes + 2 * kScratchTempBytes;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+void *scratch_addr[kMaxDevices] = {nullptr};
+
+struct NoAlloc {
+    char *base;  // scratch_addr of the library's device
+};
+
 int set_err(int code, const char *fmt, ...) {
     char buf[1024];
     va_list ap;
@@ -582,8 +601,11 @@ int run_unary(const char *opn, int op, const lx_tensor *X, const char *xname, lx
 // reductions (CPUExecutionProvider.cs:623-678, TensorOps.cs:1561-1891)
 // ---------------------------------------------------------------------------
 int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims,
-               lx_tensor *Y) {
+               lx_tensor *Y, const NoAlloc *na = nullptr) {
     REQUIRE_INIT();
+    if (na && (!Y || !Y->data))
+        return set_err(LX_ERR_INVALID_ARGUMENT, "%s without allocation writes into the caller's storage: the output "
+                                                "tensor must hold a device pointer.", opn);
     if (!X) return missing_input(opn, "data");
     int st;
     if ((st = check_tensor(X, "data"))) return st;
@@ -661,56 +683,26 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         grps.push_back({nout, false});
         nred = 1;
     }
-    // passes: reduce the innermost reduced group first
-    const void *src = X->data;
-    void *tmp[2] = {nullptr, nullptr};
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    (void)hipStreamIsCapturing(g.stream, &cs);
-    const bool capturing = cs != hipStreamCaptureStatusNone;
-    int pass = 0;
-    int result = LX_OK;
+    // passes, innermost reduced group first: planned in full before anything is launched
+    struct Pass { int64_t outer, r, inner; int vec; int64_t ws, out_bytes; };
+    std::vector<Pass> passes;
+    bool src_aligned = aligned16(X->data);
     while (nred > 0) {
         int gi = -1;
         for (int i = (int)grps.size() - 1; i >= 0; i--)
             if (grps[i].red) { gi = i; break; }
-        int64_t outer = 1, inner = 1;
-        for (int i = 0; i < gi; i++) outer *= grps[i].size;
-        for (int i = gi + 1; i < (int)grps.size(); i++) inner *= grps[i].size;
-        const int64_t r = grps[gi].size;
-        const bool last = nred == 1;
-        void *dst;
-        if (last) dst = Y->data;
-        else {
-            int slot = pass & 1;
-            release_temp(tmp[slot], capturing);
-            tmp[slot] = nullptr;
-            hipError_t e = alloc_temp(&tmp[slot], std::max<int64_t>(outer * inner * es, 16), capturing);
-            if (e != hipSuccess) { result = hip_fail(e, "device allocation (temporary)"); break; }
-            dst = tmp[slot];
-        }
-        ReduceArgs ra;
-        memset(&ra, 0, sizeof ra);
-        ra.op = op;
-        ra.dtype = dt;
-        ra.x = src;
-        ra.y = dst;
-        ra.outer = outer;
-        ra.r = r;
-        ra.inner = inner;
-        ra.pre_div = pass == 0;
-        ra.post_div = last;
-        ra.r_total = R;
+        Pass ps;
+        ps.outer = 1;
+        ps.inner = 1;
+        for (int i = 0; i < gi; i++) ps.outer *= grps[i].size;
+        for (int i = gi + 1; i < (int)grps.size(); i++) ps.inner *= grps[i].size;
+        ps.r = grps[gi].size;
         const int64_t V = 16 / es;
-        const bool al = aligned16(src);
-        ra.vec = (al && ((inner == 1 && r % V == 0) || (inner > 1 && inner % V == 0))) ? (int)V : 1;
-        int64_t wsb = reduce_workspace_bytes(dt, outer, r, inner, ra.vec);
-        if ((result = ensure_workspace(wsb))) break;
-        ra.workspace = g.workspace;
-        ra.ws_bytes = g.ws_bytes;
-
-        hipError_t e = launch_reduce(ra, g.stream);
-        if (e != hipSuccess) { result = hip_fail(e, opn); break; }
-        src = dst;
+        ps.vec = (src_aligned && ((ps.inner == 1 && ps.r % V == 0) || (ps.inner > 1 && ps.inner % V == 0))) ? (int)V : 1;
+        ps.ws = reduce_workspace_bytes(dt, ps.outer, ps.r, ps.inner, ps.vec);
+        ps.out_bytes = std::max<int64_t>(ps.outer * ps.inner * es, 16);
+        passes.push_back(ps);
+        src_aligned = true;  // temporaries are 256-byte aligned
         grps.erase(grps.begin() + gi);
         // merge neighbours that became adjacent kept groups
         std::vector<Grp> m;
@@ -720,7 +712,64 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         }
         grps.swap(m);
         nred--;
-        pass++;
+    }
+    if (na) {  // every partial and temporary must fit the static scratch array
+        for (size_t k = 0; k < passes.size(); k++) {
+            if (passes[k].ws > kScratchWsBytes)
+                return set_err(LX_ERR_NOT_SUPPORTED, "%s without allocation: the reduction needs %lld bytes of partials, "
+                               "the scratch array holds %lld.", opn, (long long)passes[k].ws, (long long)kScratchWsBytes);
+            if (k + 1 < passes.size() && passes[k].out_bytes > kScratchTempBytes)
+                return set_err(LX_ERR_NOT_SUPPORTED, "%s without allocation: an intermediate of %lld bytes exceeds the "
+                               "scratch array's %lld-byte slot.", opn, (long long)passes[k].out_bytes,
+                               (long long)kScratchTempBytes);
+        }
+    }
+    const void *src = X->data;
+    void *tmp[2] = {nullptr, nullptr};
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    (void)hipStreamIsCapturing(g.stream, &cs);
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    int result = LX_OK;
+    for (size_t pass = 0; pass < passes.size(); pass++) {
+        const Pass &ps = passes[pass];
+        const bool last = pass + 1 == passes.size();
+        void *dst;
+        const int slot = pass & 1;
+        if (last) {
+            dst = Y->data;
+        } else if (na) {
+            dst = na->base + kScratchWsBytes + slot * kScratchTempBytes;
+        } else {
+            release_temp(tmp[slot], capturing);
+            tmp[slot] = nullptr;
+            hipError_t e = alloc_temp(&tmp[slot], ps.out_bytes, capturing);
+            if (e != hipSuccess) { result = hip_fail(e, "device allocation (temporary)"); break; }
+            dst = tmp[slot];
+        }
+        ReduceArgs ra;
+        memset(&ra, 0, sizeof ra);
+        ra.op = op;
+        ra.dtype = dt;
+        ra.x = src;
+        ra.y = dst;
+        ra.outer = ps.outer;
+        ra.r = ps.r;
+        ra.inner = ps.inner;
+        ra.pre_div = pass == 0;
+        ra.post_div = last;
+        ra.r_total = R;
+        ra.vec = ps.vec;
+        if (na) {
+            ra.workspace = na->base;
+            ra.ws_bytes = kScratchWsBytes;
+        } else {
+            if ((result = ensure_workspace(ps.ws))) break;
+            ra.workspace = g.workspace;
+            ra.ws_bytes = g.ws_bytes;
+        }
+        hipError_t e = launch_reduce(ra, g.stream);
+        if (e != hipSuccess) { result = hip_fail(e, opn); break; }
+        src = dst;
     }
     for (void *t : tmp) release_temp(t, capturing);
     return result;
@@ -782,6 +831,14 @@ int lx_init(int32_t device) {
     HIPCHECK(hipHostGetDevicePointer((void **)&g.mail_dev, g.mail, 0), "hipHostGetDevicePointer(mailbox)");
     g.mail->seq = 0;
     g.mail_seq = 0;
+
+    if (device >= kMaxDevices)
+        return set_err(LX_ERR_NOT_SUPPORTED, "Devices beyond %d are not supported.", kMaxDevices - 1);
+    if (!scratch_addr[device]) {  // once per device, with the device current
+        void *p = nullptr;
+        HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        scratch_addr[device] = p;
+    }
 
     g.device = device;
     g.init = true;
@@ -955,6 +1012,14 @@ int lx_ReduceSum(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_
                  lx_tensor *Y) {
     (void)noop;  // read but unused by TensorOps.ReduceSum (TensorOps.cs:1615)
     return run_reduce("ReduceSum", kSum, X, axes, n_axes, keepdims, Y);
+}
+
+int lx_ReduceSum_noalloc(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
+                         lx_tensor *Y) {
+    (void)noop;
+    REQUIRE_INIT();
+    NoAlloc na{(char *)scratch_addr[g.device]};
+    return run_reduce("ReduceSum", kSum, X, axes, n_axes, keepdims, Y, &na);
 }
 
 int lx_ReduceMean(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
