@@ -286,8 +286,9 @@ class Workloads:
         self.ceilings = [
             ("copy 1 GiB (Cast float->float, nontemporal 16-byte vectors)", 2 * self.Yb.numel() * 4, self.Yb.numel(),
              lambda i: HIP.Cast(self.wYb, 1, out=wZc), 1, kbig),
-            ("read 1 GiB (lx_read_probe, nontemporal 16-byte vectors, 4 per lane)", self.Yb.numel() * 4,
-             self.Yb.numel(), lambda i: lib.lx_read_probe(yb, self.Yb.numel() * 4, po, 4 << 16), 1, kbig),
+            # 512 blocks (two per CU): the fastest read shape of a sweep over 256 .. 65536 blocks on MI355X
+            ("read 1 GiB (lx_read_probe, nontemporal 16-byte vectors, 4 per lane, 512 blocks)", self.Yb.numel() * 4,
+             self.Yb.numel(), lambda i: lib.lx_read_probe(yb, self.Yb.numel() * 4, po, 4 * 512), 1, kbig),
             ("copy 25 MB X -> Y over C2's 16 sets (Cast float->float)", 2 * 8 * 512 * 768 * 4, 8 * 512 * 768,
              lambda i: HIP.Cast(wX[i % LN_SETS], 1, out=wY[i % LN_SETS]), LN_SETS, k2),
         ]

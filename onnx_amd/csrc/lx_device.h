@@ -108,6 +108,34 @@ __device__ __forceinline__ T wave_reduce(T v, F f) {
     return v;
 }
 
+// Wave64 reduction of a float over data-parallel-primitive (DPP) lane moves, which
+// issue as ordinary VALU operations, instead of the LDS crossbar that __shfl_xor
+// compiles to (ds_bpermute: tens of cycles each, six in a chain).  Within each
+// 16-lane row: quad_perm [1,0,3,2] and [2,3,0,1] (pairs, then quads),
+// row_half_mirror (lane i with 7 - i: the two quads of each half row) and
+// row_mirror (lane i with 15 - i: the two halves); every lane of a row then holds
+// the row's value.  The four rows are read from lanes 0, 16, 32, 48 and combined
+// as f(f(r0, r1), f(r2, r3)).  A fixed order: deterministic, and the same value in
+// every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+template <typename F>
+__device__ __forceinline__ float wave_reduce_dpp(float v, F f) {
+    v = f(v, dpp_move<0xb1>(v));   // quad_perm [1,0,3,2]
+    v = f(v, dpp_move<0x4e>(v));   // quad_perm [2,3,0,1]
+    v = f(v, dpp_move<0x141>(v));  // row_half_mirror
+    v = f(v, dpp_move<0x140>(v));  // row_mirror
+    const int b = __builtin_bit_cast(int, v);
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+    return f(f(r0, r1), f(r2, r3));
+}
+
 // ---------------------------------------------------------------------------
 // expf bit-identical to the host glibc expf that .NET's MathF.Exp calls.
 //

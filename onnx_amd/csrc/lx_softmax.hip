@@ -44,6 +44,24 @@ __device__ __forceinline__ bool exact_pow2_recip(double sv, double *r) {
     return true;
 }
 
+// the row's max / sum across the wave: DPP lane moves for float (kSoftmaxDpp), the shuffle butterfly otherwise
+constexpr bool kSoftmaxDpp = true;
+template <typename T, typename F>
+__device__ __forceinline__ T row_reduce(T v, F f) {
+    if constexpr (std::is_same<T, float>::value && kSoftmaxDpp) return wave_reduce_dpp(v, f);
+    else return wave_reduce(v, f);
+}
+
+// ReduceMax's step with the seed-0 accumulator (TensorOps.cs:1820-1827): keep m unless v > m.  For float
+// the IEEE maxNum instruction gives the same Softmax: a quiet NaN v never wins either way, a signalling
+// NaN may win the max but then its row is NaN throughout in both cases (its exponential enters the sum),
+// and the sign of a zero maximum is invisible in x - max.
+template <typename T>
+__device__ __forceinline__ T row_max(T m, T v) {
+    if constexpr (std::is_same<T, float>::value) return __builtin_fmaxf(m, v);
+    else return v > m ? v : m;
+}
+
 template <typename T>
 __device__ __forceinline__ T div_row(T e, T s, T rs) {
     if constexpr (std::is_same<T, float>::value) return div_by_row_lx(e, s, rs);
@@ -75,7 +93,7 @@ __device__ __forceinline__ int64_t mask_row_offset(uint32_t row, const NdLayout 
 // Loads one row's vectors (and, with a mask, the mask vectors it adds): the
 // mask loads go first so that a wave waiting for them never waits for loads
 // issued after them.
-template <typename T, int V, int NV, int NOUT>
+template <typename T, int V, int NV, int NOUT, bool FULL>
 __device__ __forceinline__ void softmax_row_load(const T *__restrict__ x, int64_t row, int r, int lane,
                                                  const T *__restrict__ mask, int mask_inner, const NdLayout &mrows,
                                                  Vec<T, V> (&xv)[NV], Vec<T, V> (&mv)[NV]) {
@@ -84,7 +102,7 @@ __device__ __forceinline__ void softmax_row_load(const T *__restrict__ x, int64_
 #pragma unroll
         for (int c = 0; c < NV; c++) {
             const int col = (c * 64 + lane) * V;
-            if (col < r) {
+            if (FULL || col < r) {
                 if (mask_inner) {
                     mv[c] = vload<T, V>(m + col);
                 } else {
@@ -98,15 +116,16 @@ __device__ __forceinline__ void softmax_row_load(const T *__restrict__ x, int64_
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * V;
-        if (col < r) xv[c] = vload_nt<T, V>(x + row * (int64_t)r + col);
+        if (FULL || col < r) xv[c] = vload_nt<T, V>(x + row * (int64_t)r + col);
     }
 }
 
 // Rows of length r <= 64*V*NV held in registers, one wave per row at a time.
 // Each wave walks rows w, w + W, ... (W = all waves of the grid) and loads the
 // next row (and its mask vectors) while it finishes the current one.  NOUT:
-// mask row axes (0 = no mask; see mask_row_offset).
-template <typename T, int V, int NV, int NOUT>
+// mask row axes (0 = no mask; see mask_row_offset).  FULL: r == 64*V*NV, every
+// lane holds NV whole vectors (no per-vector bounds, one straight-line body).
+template <typename T, int V, int NV, int NOUT, bool FULL>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
                                                           NdLayout mrows, const T *__restrict__ scale, int scale_div) {
@@ -125,15 +144,15 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     // a division by a power of two runs as the multiplication by its exact reciprocal
     T sf = sv;
     const bool smul = !scale_div || exact_pow2_recip(sv, &sf);
-    softmax_row_load<T, V, NV, NOUT>(x, row, r, lane, mask, mask_inner, mrows, cur, mcur);
+    softmax_row_load<T, V, NV, NOUT, FULL>(x, row, r, lane, mask, mask_inner, mrows, cur, mcur);
     for (; row < rows; row += W) {
         const int64_t next = row + W;
-        if (next < rows) softmax_row_load<T, V, NV, NOUT>(x, next, r, lane, mask, mask_inner, mrows, nxt, mnxt);
+        if (next < rows) softmax_row_load<T, V, NV, NOUT, FULL>(x, next, r, lane, mask, mask_inner, mrows, nxt, mnxt);
         if (scale) {  // the Div (or Mul) node before the mask Add: the same IEEE operation per element
 #pragma unroll
             for (int c = 0; c < NV; c++) {
                 const int col = (c * 64 + lane) * V;
-                if (col < r) {
+                if (FULL || col < r) {
 #pragma unroll
                     for (int k = 0; k < V; k++) cur[c].v[k] = smul ? cur[c].v[k] * sf : cur[c].v[k] / sv;
                 }
@@ -143,7 +162,7 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
 #pragma unroll
             for (int c = 0; c < NV; c++) {
                 const int col = (c * 64 + lane) * V;
-                if (col < r) {
+                if (FULL || col < r) {
 #pragma unroll
                     for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mcur[c].v[k];
                 }
@@ -154,17 +173,17 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
 #pragma unroll
         for (int c = 0; c < NV; c++) {
             const int col = (c * 64 + lane) * V;
-            if (col < r) {
+            if (FULL || col < r) {
 #pragma unroll
-                for (int k = 0; k < V; k++) mx = cur[c].v[k] > mx ? cur[c].v[k] : mx;
+                for (int k = 0; k < V; k++) mx = row_max<T>(mx, cur[c].v[k]);
             }
         }
-        mx = wave_reduce(mx, [](T a, T b) { return b > a ? b : a; });
+        mx = row_reduce<T>(mx, [](T a, T b) { return row_max<T>(a, b); });
         T sum = T(0);
 #pragma unroll
         for (int c = 0; c < NV; c++) {
             const int col = (c * 64 + lane) * V;
-            if (col < r) {
+            if (FULL || col < r) {
 #pragma unroll
                 for (int k = 0; k < V; k++) {
                     cur[c].v[k] = exp_elem<T>(cur[c].v[k] - mx, tab);
@@ -172,13 +191,13 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
                 }
             }
         }
-        sum = wave_reduce(sum, [](T a, T b) { return a + b; });
+        sum = row_reduce<T>(sum, [](T a, T b) { return a + b; });
         const T rs = T(1) / sum;
         T *q = y + row * (int64_t)r;
 #pragma unroll
         for (int c = 0; c < NV; c++) {
             const int col = (c * 64 + lane) * V;
-            if (col < r) {
+            if (FULL || col < r) {
                 Vec<T, V> o;
 #pragma unroll
                 for (int k = 0; k < V; k++) o.v[k] = div_row<T>(cur[c].v[k], sum, rs);
@@ -255,10 +274,15 @@ static hipError_t softmax_wave_launch(const SoftmaxArgs &a, hipStream_t s) {
     const T *x = (const T *)a.x;
     T *y = (T *)a.y;
     const T *m = (const T *)a.mask;
+    const bool full = r == nv * 64 * V;
 #define LX_SM_CASE(N)                                                                                           \
     case N:                                                                                                     \
-        hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, a.outer, r, \
-                           m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);              \
+        if (full && N <= 4)                                                                                     \
+            hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT, (N <= 4)>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, \
+                               a.outer, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);      \
+        else                                                                                                    \
+            hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT, false>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y,  \
+                               a.outer, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);      \
         break;
     switch (nv) {
         LX_SM_CASE(1) LX_SM_CASE(2) LX_SM_CASE(3) LX_SM_CASE(4) LX_SM_CASE(5) LX_SM_CASE(6) LX_SM_CASE(7) LX_SM_CASE(8)
