@@ -345,6 +345,43 @@ def test_pow(hip):
     assert same.all(), (g, r)
 
 
+def _pow_cases(rng, n):
+    """Pairs over the regimes of powf: positive bases with exponents up to |y| = 100, negative bases with
+    integer exponents (sign from the exponent's parity), results that overflow to inf or underflow through
+    the denormals to 0, and bases near 1."""
+    q = n // 5
+    x = [np.exp(rng.uniform(-2.3, 2.3, q)), -np.exp(rng.uniform(-2.3, 2.3, q)), rng.uniform(0.5, 2.0, q),
+         np.exp(rng.uniform(2.3, 7, q)), np.exp(rng.uniform(-12, -7, n - 4 * q))]
+    y = [rng.uniform(-30, 30, q), rng.integers(-40, 41, q).astype(np.float64), rng.uniform(-100, 100, q),
+         rng.uniform(10, 20, q), rng.uniform(8, 16, n - 4 * q)]
+    return np.concatenate(x).astype(np.float32), np.concatenate(y).astype(np.float32)
+
+
+def test_pow_wide(hip):
+    """10^6 pairs against the host powf within 2 ulp: the device evaluates (float)pow((double)x, (double)y),
+    the double result within about one double ulp, so one float rounding from the correctly rounded float;
+    overflow, underflow (denormals included), signs of negative bases and NaN for negative bases with
+    non-integer exponents agree exactly."""
+    rng = np.random.default_rng(16)
+    x, y = _pow_cases(rng, 10**6)
+    got = ok(HIP.Pow(dev(x), dev(y)))
+    ref = O.binary(O.POW, x, y)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    np.testing.assert_array_equal(np.isinf(got), np.isinf(ref))
+    fin = ~nan & np.isfinite(ref)
+    assert np.array_equal(np.signbit(got[fin]), np.signbit(ref[fin]))
+    u = ulps(got[fin], ref[fin])
+    assert u.max() <= 2, (u.max(), x[fin][np.argmax(u)], y[fin][np.argmax(u)])
+    # the regimes are all present: overflow, exact zeros from underflow, denormals, negative results
+    assert np.isinf(ref).sum() > 1000 and (ref == 0).sum() > 1000
+    assert ((ref != 0) & (np.abs(ref) < np.finfo(np.float32).tiny)).sum() > 100 and (ref < 0).sum() > 10000
+    # negative bases with non-integer exponents: NaN
+    xn = -np.exp(rng.uniform(-2, 2, 10000)).astype(np.float32)
+    yn = (rng.integers(-20, 20, 10000) + 0.5).astype(np.float32)
+    assert np.isnan(ok(HIP.Pow(dev(xn), dev(yn)))).all() and np.isnan(O.binary(O.POW, xn, yn)).all()
+
+
 def test_sqrt_bit_exact(hip):
     rng = np.random.default_rng(15)
     x = np.concatenate([rng.uniform(0, 1e6, 100000), [0.0, -0.0, 1e-45, 1e-40, np.inf, -1.0, np.nan]]).astype(np.float32)
@@ -368,10 +405,24 @@ def test_erf_bit_exact(hip):
 
 
 def test_erf_double(hip):
-    x = np.linspace(-5, 5, 10001)
+    """MathOps.Erf(double) with the device's double exp against the formula with the host's exp.  The result
+    is 1 - P with P = poly * t * exp(-x^2) <= 1, and a one-ulp difference of the exponential moves P by at most
+    one ulp of 1 (2^-53), so the bar is 2 ulp at the scale max(|erf|, 0.5), the granularity of 1 - P: within
+    2 ulp of erf itself wherever |erf| >= 0.5, within 2^-52 absolute below."""
+    rng = np.random.default_rng(17)
+    x = np.concatenate([np.linspace(-6, 6, 20001), rng.standard_normal(200000), rng.uniform(-1e-3, 1e-3, 20000),
+                        [0.0, -0.0, 1e-300, -1e-300, 30.0, -30.0]])
     got = ok(HIP.Erf(dev(x)))
     ref = O.unary(O.ERF, x)
-    assert np.max(np.abs(got - ref)) <= 1e-15  # device exp vs host exp inside the double formula
+    scale = np.spacing(np.maximum(np.abs(ref), 0.5))
+    err = np.abs(got - ref) / scale
+    assert err.max() <= 2, (err.max(), x[np.argmax(err)])
+    # the formula's values at the ends: at 0 the coefficients sum to 0.999999999, so erf(+-0) = 1e-9 (sign +1
+    # for -0 too, as x < 0 is false); erf(+-30) = +-1
+    assert got[-6] == ref[-6] == got[-5] and abs(got[-6] - 1e-9) < 1e-16 and got[-2] == 1.0 and got[-1] == -1.0
+    xn = np.array([np.nan, np.inf, -np.inf])
+    gn = ok(HIP.Erf(dev(xn)))
+    assert np.isnan(gn[0]) and gn[1] == 1.0 and gn[2] == -1.0
 
 
 CAST_TYPES = [O.FLOAT, O.DOUBLE, O.UINT8, O.INT8, O.UINT16, O.INT16, O.INT32, O.UINT32, O.INT64, O.UINT64, O.BOOL]
@@ -537,6 +588,31 @@ def test_softmax_default_axis_and_masked_rows(hip):
     np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
     assert np.isnan(ref[0]).all() and not np.isnan(ref[1]).any()
     assert_bits(got[1], ref[1])
+
+
+@pytest.mark.parametrize("r", [256, 512, 768, 500, 96])
+def test_softmax_special_values_in_rows(hip, r):
+    """Rows holding a quiet NaN, a signalling NaN, +-0, +-inf and all-negative values, on the straight-line
+    path (rows that fill the wave's vectors: 256, 512, 768) and the bounded one: the NaN rows, the infinite
+    rows and the finite ones come out as the reference's five-step composite gives them."""
+    rng = np.random.default_rng(28)
+    x = (rng.standard_normal((12, r)) * 3).astype(np.float32)
+    x[0, 5] = np.nan                                             # quiet NaN: the whole row NaN
+    x[1, 7] = np.uint32(0x7f800001).view(np.float32)             # signalling NaN: the whole row NaN
+    x[2, :] = -np.abs(x[2, :]) - 1.0                             # max below the seed 0
+    x[2, 3] = -0.0
+    x[3, :] = 0.0                                                # all zeros, one -0
+    x[3, 9] = -0.0
+    x[4, 11] = np.inf                                            # +inf: inf - inf = NaN
+    x[5, 13] = -np.inf                                           # -inf: exp(-inf) = 0
+    x[6, :] = -30000.0                                           # every entry below the seed: 0 / 0
+    got = ok(HIP.Softmax(dev(x), -1))
+    ref = O.softmax(x, -1)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    assert nan[0].all() and nan[1].all() and nan[4].all() and nan[6].all() and not nan[5].any()
+    err = np.abs(got.astype(np.float64) - ref)[~nan]
+    assert np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30), err.max()
 
 
 @pytest.mark.parametrize("s_shape,m_shape", [((4, 3, 64, 512), (4, 1, 1, 512)), ((2, 3, 5, 96), (3, 1, 96)),

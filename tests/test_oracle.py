@@ -173,6 +173,39 @@ def test_erf_bound_and_special_values():
     assert math.isnan(O.erf_f32(float("nan")))
 
 
+def _same_or_both_nan(a, b):
+    return (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+
+
+def test_gelu_chain_loop_equals_the_five_ops():
+    """The oracle's single-loop GELU (the full-size C5 checker) is the five-node composite Div -> Erf -> Add ->
+    Mul -> Mul of the pinned operators, bit for bit: on 10^7 inputs -- normal samples, random 32-bit patterns
+    (every exponent, denormals, infinities, NaNs) and the neighbourhood of 0."""
+    rng = np.random.default_rng(31)
+    x = np.concatenate([rng.standard_normal(4_000_000).astype(np.float32),
+                        rng.integers(0, 2**32, 5_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32),
+                        rng.uniform(-1e-3, 1e-3, 1_000_000).astype(np.float32),
+                        np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, -1e-45, 3.4e38, -3.4e38], np.float32)])
+    fast, comp = O.gelu_chain_fast(x), O.gelu_erf(x)
+    assert _same_or_both_nan(fast, comp).all()
+
+
+def test_sqrt_equals_ieee_square_root():
+    """The oracle's Sqrt (the reference's Vector.SquareRoot / MathF.Sqrt, TensorOps.cs:315-317) is the correctly
+    rounded IEEE square root: numpy's float32 sqrt, bit for bit, over random bit patterns (negative inputs and
+    -inf give NaN, -0 gives -0) and float64 likewise."""
+    rng = np.random.default_rng(32)
+    x = rng.integers(0, 2**32, 2_000_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([x, np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-45, 4.0, 2.0], np.float32)])
+    with np.errstate(invalid="ignore"):
+        ref = np.sqrt(x)
+    got = O.unary(O.SQRT, x)
+    assert _same_or_both_nan(got, ref).all()
+    assert np.signbit(got[-7]) and got[-6] == np.inf and got[-2] == 2.0
+    d = np.abs(rng.standard_normal(100000)) * 1e10
+    assert np.array_equal(O.unary(O.SQRT, d), np.sqrt(d))
+
+
 def test_serial_fold_matches_sequential_accumulate():
     rng = np.random.default_rng(4)
     x = rng.uniform(-1, 1, (64, 4096)).astype(np.float32)
