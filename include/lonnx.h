@@ -307,6 +307,27 @@ int lx_graph_output(lx_graph *g, const char *name, lx_tensor *out);
 /* ComputationalGraph.Reset (ComputationalGraph.cs:336-349): drops intermediates and outputs (their
  * storage returns to the pool). */
 int lx_graph_reset(lx_graph *g);
+/* ---- node profiling: the device twin of Profiler (src/Lokad.Onnx.Base/Profiler.cs:24-97) ----
+ * Profiler.Enabled / StartNodeProfile / StopNodeProfile (ComputationalGraph.cs:241-243), per graph: while
+ * enabled, every node an execution runs (the failing one included) appends one record, NodeProfile's
+ * NodeId and Op plus the two stages a device node has: math_ms (OpStage.Math), the device time between
+ * HIP events recorded on the library stream before and after the node, so the records of one execution
+ * add up to its device span, and host_ms, the host time of the node's dispatch (argument validation,
+ * broadcast planning and launches: OpStage.ValidateArguments / GraphOrchestration; broadcast copies do
+ * not exist on the device).  A profiled execution waits for its last event before it returns.  Captured
+ * executions and replays are not profiled.  Records accumulate until lx_graph_profile_reset. */
+typedef struct lx_node_profile {
+    int64_t node_id;     /* the node's position in the graph as built (a fused node: its last original node) */
+    int32_t node_index;  /* its position in the current node list (lx_graph_node_info) */
+    char op[36];         /* op type, NUL-terminated (a fused node: its fused op, e.g. LayerNormDecomposed) */
+    double math_ms;
+    double host_ms;
+} lx_node_profile;
+int lx_graph_set_profiling(lx_graph *g, int32_t enabled);
+int32_t lx_graph_profile_count(const lx_graph *g);
+int lx_graph_profile(const lx_graph *g, int32_t i, lx_node_profile *out);
+int lx_graph_profile_reset(lx_graph *g);
+
 /* introspection for callers and tests */
 int32_t lx_graph_node_count(const lx_graph *g);
 int lx_graph_node_info(const lx_graph *g, int32_t i, char *op_type, int32_t op_len, char *name, int32_t name_len);

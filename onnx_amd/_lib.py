@@ -43,6 +43,16 @@ class LxTensor(ctypes.Structure):
     ]
 
 
+class LxNodeProfile(ctypes.Structure):
+    _fields_ = [
+        ("node_id", ctypes.c_int64),
+        ("node_index", ctypes.c_int32),
+        ("op", ctypes.c_char * 36),
+        ("math_ms", ctypes.c_double),
+        ("host_ms", ctypes.c_double),
+    ]
+
+
 class LxPlan(ctypes.Structure):
     _fields_ = [
         ("status", ctypes.c_int32),
@@ -132,6 +142,10 @@ SIGNATURES = {
                                          _c.c_int32]),
     "lx_graph_output": (_c.c_int, [_c.c_void_p, _c.c_char_p, _T]),
     "lx_graph_reset": (_c.c_int, [_c.c_void_p]),
+    "lx_graph_set_profiling": (_c.c_int, [_c.c_void_p, _c.c_int32]),
+    "lx_graph_profile_count": (_c.c_int32, [_c.c_void_p]),
+    "lx_graph_profile": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.POINTER(LxNodeProfile)]),
+    "lx_graph_profile_reset": (_c.c_int, [_c.c_void_p]),
     "lx_graph_node_count": (_c.c_int32, [_c.c_void_p]),
     "lx_graph_node_info": (_c.c_int, [_c.c_void_p, _c.c_int32, _c.c_char_p, _c.c_int32, _c.c_char_p, _c.c_int32]),
     "lx_graph_input_count": (_c.c_int32, [_c.c_void_p]),

@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstring>
+#include <chrono>
 #include <set>
 #include <string>
 #include <vector>
@@ -1357,6 +1358,60 @@ int report_device_failure(lx_graph *g, int j, int st) {
 // ComputationalGraph.Execute (ComputationalGraph.cs:199-272).  recording != null: the execution is
 // being captured into a HIP graph -- nothing may wait for the device, so the deferred checks are
 // handed to the caller (who reads them after each replay) instead of read back here.
+// Per-node timing of one execution for lx_graph_set_profiling: boundary events on the library stream,
+// host time per node; finish() (also run by the destructor) waits for the last event and appends records.
+struct NodeProfiler {
+    lx_graph *g;
+    bool on;
+    int used = 0;
+    std::vector<NodeProf> pend;
+    NodeProfiler(lx_graph *gr, bool enabled) : g(gr), on(enabled) {}
+    ~NodeProfiler() { finish(); }
+    int event(hipEvent_t *e) {
+        auto &ev = g->prof_events.ev;
+        if (used == (int)ev.size()) {
+            hipEvent_t x;
+            hipError_t r = hipEventCreate(&x);
+            if (r != hipSuccess) return fail(LX_ERR_HIP, fmt("hipEventCreate: %s", hipGetErrorString(r)));
+            ev.push_back(x);
+        }
+        *e = ev[used++];
+        hipError_t r = hipEventRecord(*e, api_stream());
+        if (r != hipSuccess) return fail(LX_ERR_HIP, fmt("hipEventRecord: %s", hipGetErrorString(r)));
+        return LX_OK;
+    }
+    int start() {
+        if (!on) return LX_OK;
+        hipEvent_t e;
+        return event(&e);
+    }
+    void node_done(int k, const GNode &node, std::chrono::steady_clock::time_point h0) {
+        if (!on) return;
+        NodeProf p;
+        p.node_id = node.index >= 0 ? node.index : k;
+        p.node_index = k;
+        p.op = node.op;
+        p.host_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0).count();
+        hipEvent_t e;
+        if (event(&e) != LX_OK) {  // no timing for this execution from here on
+            on = false;
+            return;
+        }
+        pend.push_back(p);
+    }
+    void finish() {
+        if (!on || pend.empty()) return;
+        on = false;
+        auto &ev = g->prof_events.ev;
+        if (hipEventSynchronize(ev[pend.size()]) != hipSuccess) return;
+        for (size_t i = 0; i < pend.size(); i++) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) pend[i].math_ms = ms;
+            g->profile.push_back(pend[i]);
+        }
+    }
+};
+
 int execute_impl(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs, int32_t use_initializers,
                  std::vector<DeferredCheck> *recording) {
     int st = upload_initializers(g);
@@ -1394,13 +1449,20 @@ int execute_impl(lx_graph *g, int32_t n, const char *const *names, const lx_tens
     std::vector<DeferredCheck> recs(nn);
     ErrFlags *slots = (ErrFlags *)g->check_slots.t.data;
     Exec X{g};
+    // Profiler.StartNodeProfile / StopNodeProfile (ComputationalGraph.cs:241-243) on the device: an event at
+    // every node boundary (not under capture, where events would become graph nodes), the records appended
+    // once the last event has completed, on every way out of the loop
+    NodeProfiler prof(g, g->profiling && !recording);
+    if ((st = prof.start())) return st;
     for (int k = 0; k < nn; k++) {
         const GNode &node = g->nodes[k];
         std::vector<Value> outs;
         // a node that cannot check gets no slot: a check it did make would be read back at once
         api_defer_checks(slots && may_check(node) ? slots + k : nullptr, &recs[k]);
+        const auto h0 = std::chrono::steady_clock::now();
         st = run_node(X, node, outs);
         api_defer_checks(nullptr, nullptr);
+        prof.node_done(k, node, h0);
         if (!st && outs.size() != node.out.size())
             st = failure(fmt("The operation returned %d outputs but the graph node has %d outputs.", (int)outs.size(),
                              (int)node.out.size()));
@@ -1434,7 +1496,42 @@ int execute_impl(lx_graph *g, int32_t n, const char *const *names, const lx_tens
 }  // namespace
 
 // ===========================================================================
+namespace lx {
+EventPool::~EventPool() {
+    for (hipEvent_t e : ev) (void)hipEventDestroy(e);
+}
+}  // namespace lx
+
 extern "C" {
+
+int lx_graph_set_profiling(lx_graph *g, int32_t enabled) {
+    if (!g) return failure("null graph");
+    g->profiling = enabled != 0;
+    return LX_OK;
+}
+
+int32_t lx_graph_profile_count(const lx_graph *g) { return g ? (int32_t)g->profile.size() : 0; }
+
+static void copy_str(const std::string &s, char *buf, int32_t len);
+
+int lx_graph_profile(const lx_graph *g, int32_t i, lx_node_profile *out) {
+    if (!g || !out) return failure("null argument");
+    if (i < 0 || i >= (int32_t)g->profile.size()) return failure("invalid profile record index");
+    const NodeProf &p = g->profile[i];
+    memset(out, 0, sizeof *out);
+    out->node_id = p.node_id;
+    out->node_index = p.node_index;
+    copy_str(p.op, out->op, (int32_t)sizeof out->op);
+    out->math_ms = p.math_ms;
+    out->host_ms = p.host_ms;
+    return LX_OK;
+}
+
+int lx_graph_profile_reset(lx_graph *g) {
+    if (!g) return failure("null graph");
+    g->profile.clear();
+    return LX_OK;
+}
 
 int lx_graph_create(int64_t opset, lx_graph **out) {
     if (!out) return failure("out is null");

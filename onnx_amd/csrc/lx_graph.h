@@ -84,6 +84,22 @@ struct GraphCapture {
     ~GraphCapture();
 };
 
+// One executed node (Profiler.NodeProfile, Profiler.cs:22): the node, its device time between HIP events
+// recorded at node boundaries on the library stream (OpStage.Math) and the host time of its dispatch.
+struct NodeProf {
+    int64_t node_id = 0;     // position in the graph as built (fused nodes: their last original node)
+    int32_t node_index = 0;  // position in the current node list
+    std::string op;
+    double math_ms = 0.0;
+    double host_ms = 0.0;
+};
+
+// HIP events reused by profiled executions (destroyed with the graph).
+struct EventPool {
+    std::vector<hipEvent_t> ev;
+    ~EventPool();
+};
+
 }  // namespace lx
 
 struct lx_graph {
@@ -103,4 +119,7 @@ struct lx_graph {
     std::map<std::string, lx::Value> host_cache;  // uploaded Constant / Shape outputs, reused while unchanged
     std::unique_ptr<lx::GraphCapture> capture;    // lx_graph_capture's record, if any
     std::vector<std::string> node_outputs;      // every name a node produces (IntermediateOutputs + Outputs)
+    bool profiling = false;                     // Profiler.Enabled, per graph
+    std::vector<lx::NodeProf> profile;          // Profiler.Profile: every node executed while enabled
+    lx::EventPool prof_events;
 };

@@ -151,6 +151,27 @@ class ComputationalGraph:
             res.append(nm.value.decode())
         return res
 
+    # ---- profiling (Profiler.Enabled / Profiler.Profile) ---------------------
+    def EnableProfiling(self, enabled: bool = True):
+        """Per-node timing of later executions (Profiler.Enabled for this graph)."""
+        _check(L.lib().lx_graph_set_profiling(self._h, 1 if enabled else 0), "lx_graph_set_profiling")
+
+    @property
+    def Profile(self) -> List[dict]:
+        """One record per node executed while profiling (Profiler.Profile): node_id, node_index, op,
+        math_ms (device time between the node's boundary events) and host_ms (its dispatch)."""
+        lib = L.lib()
+        out = []
+        for i in range(lib.lx_graph_profile_count(self._h)):
+            p = L.LxNodeProfile()
+            _check(lib.lx_graph_profile(self._h, i, ctypes.byref(p)), "lx_graph_profile")
+            out.append({"node_id": p.node_id, "node_index": p.node_index, "op": p.op.decode(),
+                        "math_ms": p.math_ms, "host_ms": p.host_ms})
+        return out
+
+    def ResetProfile(self):
+        _check(L.lib().lx_graph_profile_reset(self._h), "lx_graph_profile_reset")
+
     def Fuse(self) -> int:
         """Replace the GELU, decomposed-LayerNorm and Add+Softmax subgraphs by their
         fused kernels, then linear chains of Float elementwise nodes by one

@@ -420,3 +420,72 @@ def test_shape_arithmetic_out_of_range_index_fails_as_the_device_operator(hip):
     g = Model.Load(_dynamic_reshape_model(idx=5))
     assert not g.Execute({"x": DeviceTensor.from_numpy(np.zeros((2, 40, 96), np.float32))})
     assert "gather" in g.LastError and "outside the bounds" in g.LastError
+
+
+def test_profiling_c2_graph_node_times_add_up_to_the_execution():
+    """Profiler.StartNodeProfile / StopNodeProfile on the device: the nine-node LayerNorm graph records nine
+    nodes with the reference's op types in node order, every node with device time, and the node times add
+    up to the execution's wall time within 10% (the boundary events telescope); a second execution appends
+    nine more; reset clears them; a fused graph records its one fused node."""
+    import time
+    rng = np.random.default_rng(29)
+    shape = (64, 512, 768)
+    x = DeviceTensor.from_numpy((rng.standard_normal(shape) * 2).astype(np.float32))
+    inits = LN_INITS(768)
+    ops = ["ReduceMean", "Sub", "Pow", "ReduceMean", "Add", "Sqrt", "Div", "Mul", "Add"]
+    g = Model.Load(W.model(ln_nodes(), [("x", np.float32, shape)], [("y", np.float32, shape)], inits))
+    assert g.Execute({"x": x}), g.LastError      # warm: uploads, pool
+    assert g.Profile == []                        # not enabled
+    g.EnableProfiling(True)
+    walls = []
+    for _ in range(3):
+        g.ResetProfile()
+        onnx_sync()
+        t0 = time.perf_counter()
+        assert g.Execute({"x": x}), g.LastError
+        walls.append((time.perf_counter() - t0) * 1e3)
+        prof = g.Profile
+        assert [p["op"] for p in prof] == ops and [p["node_id"] for p in prof] == list(range(9))
+        assert all(p["math_ms"] > 0 and p["host_ms"] > 0 for p in prof)
+        total = sum(p["math_ms"] for p in prof)
+        if abs(total - walls[-1]) <= 0.1 * walls[-1]:
+            break
+    assert abs(total - walls[-1]) <= 0.1 * walls[-1], (total, walls)
+    assert g.Execute({"x": x}), g.LastError
+    assert len(g.Profile) == 18
+    g.ResetProfile()
+    assert g.Profile == []
+    g.EnableProfiling(False)
+    assert g.Execute({"x": x}), g.LastError
+    assert g.Profile == []
+    g.close()
+    gf = Model.Load(W.model(ln_nodes(), [("x", np.float32, shape)], [("y", np.float32, shape)], inits))
+    assert gf.Fuse() == 1
+    gf.EnableProfiling(True)
+    assert gf.Execute({"x": x}), gf.LastError
+    prof = gf.Profile
+    assert [p["op"] for p in prof] == ["LayerNormDecomposed"] and prof[0]["node_id"] == 8 and prof[0]["math_ms"] > 0
+    gf.close()
+
+
+def test_profiling_records_the_failing_node():
+    """As the reference stops its node profile after Execute returns, the failing node is recorded too,
+    and nothing after it."""
+    rng = np.random.default_rng(30)
+    nodes = [W.node("Add", ["a", "b"], ["s"], "add"), W.node("Div", ["s", "z"], ["q"], "div"),
+             W.node("Mul", ["q", "b"], ["p"], "mul")]
+    a = rng.standard_normal((4, 64)).astype(np.float32)
+    b = rng.standard_normal((4, 64)).astype(np.float32)
+    z = rng.standard_normal((3, 64)).astype(np.float32)   # Div [4,64] / [3,64]: CannotBroadcast on the host
+    g = Model.Load(W.model(nodes, [("a", np.float32, a.shape), ("b", np.float32, b.shape), ("z", np.float32, z.shape)],
+                           [("p", np.float32, a.shape)], []))
+    g.EnableProfiling(True)
+    ok_ = g.Execute({"a": DeviceTensor.from_numpy(a), "b": DeviceTensor.from_numpy(b), "z": DeviceTensor.from_numpy(z)})
+    assert not ok_ and "div" in g.LastError and "broadcast" in g.LastError
+    assert [p["op"] for p in g.Profile] == ["Add", "Div"]
+    g.close()
+
+
+def onnx_sync():
+    import onnx_amd
+    onnx_amd.synchronize()

@@ -261,3 +261,18 @@ def test_grouped_projection_constants_are_not_initializers():
     assert g.Fuse() == 2
     assert [n.Op for n in g.Nodes] == ["MatMulAddGroup", "MatMulAddGroup"]
     assert g.InitializerInfo == before and len(before) == 12
+
+
+def test_profiling_switch_and_empty_profile():
+    """The profiling switch and the record list exist without a device: nothing is recorded until an
+    execution runs, and a record index past the end fails with a status, not a crash."""
+    import ctypes
+    from onnx_amd import _lib as L
+    g = Model.Load(W.model(ln_nodes(), [("x", np.float32, (2, 8))], [("y", np.float32, (2, 8))], LN_INITS()))
+    assert g.Profile == []
+    g.EnableProfiling(True)
+    g.EnableProfiling(False)
+    g.ResetProfile()
+    rec = L.LxNodeProfile()
+    assert L.lib().lx_graph_profile(g._h, 0, ctypes.byref(rec)) != L.OK
+    assert ctypes.sizeof(L.LxNodeProfile) == 8 + 4 + 36 + 8 + 8
