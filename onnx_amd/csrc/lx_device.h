@@ -244,18 +244,15 @@ __host__ __device__ __forceinline__ float expf_nonpos_lx(float x, const ExpTable
 #define LX_INV_SQRT2F_D (1.0 / 1.41421353816986083984375)
 __host__ __device__ __forceinline__ float div_sqrt2f_lx(float x) { return (float)((double)x * LX_INV_SQRT2F_D); }
 
-// Correctly rounded 1/d for d in [1, 2^126) from a float seed, two float
-// Newton steps:  e = 1 - d*y,  y' = y + e*y  (each one FMA).  Exact for every
-// such d and every seed within 1 ulp of 1/d, except that a d whose significand
-// is all ones (2^k * (2 - 2^-23)) needs the correctly rounded reciprocal as its
-// seed: from the seed one ulp below, y' stops on the tie 2^-k/2.  Checked for
-// all d and seeds by the test suite on the host; the device test checks the
-// v_rcp_f32-seeded result against IEEE division for every d in [1, 2^125].
-__host__ __device__ __forceinline__ float recip_newton2(float d, float seed) {
-    float e = __builtin_fmaf(-d, seed, 1.0f);
-    float y = __builtin_fmaf(e, seed, seed);
-    e = __builtin_fmaf(-d, y, 1.0f);
-    return __builtin_fmaf(e, y, y);
+// Correctly rounded 1/d for d in [1, 2^126) from a float seed by one float Newton step, e = 1 - d*y (one FMA),
+// y' = y + e*y (one FMA).  From the correctly rounded seed the result is exact for every such d; from a seed one
+// ulp off it is exact except at 33 significands per binade (32 seeds from above, 1 from below): both checked by
+// enumeration on the host.  v_rcp_f32 is one ulp off on about a tenth of the floats, but never at those 33
+// significands: with its seed the step equals IEEE 1.0f / d for every float d in [1, 2^126), checked on the
+// device for every d by the test suite.
+__host__ __device__ __forceinline__ float recip_newton1(float d, float seed) {
+    const float e = __builtin_fmaf(-d, seed, 1.0f);
+    return __builtin_fmaf(e, seed, seed);
 }
 
 // Truncated quotient a / b of int32 operands (b != 0, not INT_MIN / -1) in
@@ -332,8 +329,8 @@ __device__ __forceinline__ float div_by_row_lx(float a, float s, float rs) {
 // |x| > 1.3e38, where expf(-x*x) is exactly 0 and the product poly*t*0 is 0
 // for any finite t; NaN also clamps and still yields NaN through expf.  The
 // result equals erf_lx bit for bit for all 2^32 inputs (checked on the host
-// with the correctly rounded seed; recip_newton2 gives the same reciprocal
-// from the device seed).
+// with the correctly rounded seed; recip_newton1 gives the same reciprocal
+// from the device seed, checked on the device for every d).
 template <typename SeedFn>
 __host__ __device__ __forceinline__ float erf_fast_core(float x, const ExpTable &tab, SeedFn seed) {
     const float a1 = 0.254829592f;
@@ -346,7 +343,7 @@ __host__ __device__ __forceinline__ float erf_fast_core(float x, const ExpTable 
     x = __builtin_fabsf(x);
     float d = 1.0f + p * x;
     d = d < 0x1p125f ? d : 0x1p125f;
-    float t = recip_newton2(d, seed(d));
+    float t = recip_newton1(d, seed(d));
     float poly = ((((a5 * t + a4) * t) + a3) * t + a2) * t + a1;
     float e = expf_nonpos_lx(-x * x, tab);
     float y = 1.0f - poly * t * e;
@@ -379,7 +376,7 @@ __host__ __device__ __forceinline__ float gelu_erf_core(float x, const ExpTable 
     const float ax = __builtin_fabsf(a);
     float d = 1.0f + p * ax;
     d = d < 0x1p125f ? d : 0x1p125f;
-    const float t = recip_newton2(d, seed(d));
+    const float t = recip_newton1(d, seed(d));
     const float poly = ((((a5 * t + a4) * t) + a3) * t + a2) * t + a1;
     const float e = expf_core_lx(__builtin_fmaxf(-ax * ax, -104.0f), tab);
     const float erf = __builtin_copysignf(1.0f - poly * t * e, a);

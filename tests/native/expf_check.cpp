@@ -65,28 +65,21 @@ long long lx_test_div_sqrt2_mismatches(void) {
     return bad;
 }
 
-// every d in [1, 2^126) with every seed within 1 ulp of 1/d: number of
-// (d, seed) pairs where recip_newton2 differs from 1/d, split into d with an
-// all-ones significand (out[1]) and every other d (out[0])
+// every d in [1, 2^126): out[0] = d where one Newton step from the correctly rounded seed differs from 1/d,
+// out[1] = (d, seed) pairs with a seed one ulp off where it does
 void lx_test_recip_mismatches(long long *out) {
-    long long bad = 0, ones = 0;
+    long long bad = 0, off = 0;
     const uint32_t lo = bits(1.0f), hi = bits(0x1p126f);
-#pragma omp parallel for reduction(+ : bad, ones) schedule(static)
+#pragma omp parallel for reduction(+ : bad, off) schedule(static)
     for (long long u = lo; u < (long long)hi; u++) {
         float d = fbits((uint32_t)u);
         float cr = 1.0f / d;
-        for (int k = -1; k <= 1; k++) {
-            float seed = fbits(bits(cr) + k);
-            if (!same(lx::recip_newton2(d, seed), cr)) {
-                if ((u & 0x7fffff) == 0x7fffff) ones++;
-                else bad++;
-            }
-        }
-        // the correctly rounded seed itself is always a fixed point
-        if (!same(lx::recip_newton2(d, cr), cr)) bad++;
+        if (!same(lx::recip_newton1(d, cr), cr)) bad++;
+        for (int k = -1; k <= 1; k += 2)
+            if (!same(lx::recip_newton1(d, fbits(bits(cr) + k)), cr)) off++;
     }
     out[0] = bad;
-    out[1] = ones;
+    out[1] = off;
 }
 
 // every x <= 0 (sign bit set), +0 and NaN: expf_nonpos_lx(x) == expf(x)

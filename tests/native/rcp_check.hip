@@ -1,5 +1,5 @@
 // TEST HELPER (device): checks on the GPU that the v_rcp_f32-seeded reciprocal
-// used by the Erf / GELU kernels (recip_newton2 in lx_device.h) equals IEEE
+// used by the Erf / GELU kernels (recip_newton1 in lx_device.h) equals IEEE
 // float division 1.0f / d for every float d in [1, 2^126), and measures the
 // largest relative error of v_rcp_f32 itself over every float in [1, 2^31]
 // (the seeds of the integer division, sdiv32_core).  Built for gfx950 by
@@ -14,8 +14,8 @@ namespace {
 constexpr uint32_t kLo = 0x3f800000u;  // 1.0f
 constexpr uint32_t kHi = 0x7e800000u;  // 2^126
 
-// counts[0]: recip_newton2 != 1/d; counts[1]: seed != 1/d (informational);
-// counts[2]: seed != 1/d where d's significand is all ones
+// counts[0]: recip_newton1 from the v_rcp_f32 seed != 1/d; counts[1]: seed != 1/d (informational: the
+// seeds the Newton step repairs); counts[2]: seed != 1/d where d's significand is all ones
 __global__ void k_check(unsigned long long *counts) {
     unsigned long long bad = 0, seed_off = 0, ones_off = 0;
     const uint32_t stride = gridDim.x * blockDim.x;
@@ -23,7 +23,7 @@ __global__ void k_check(unsigned long long *counts) {
         const float d = __builtin_bit_cast(float, u);
         const float cr = 1.0f / d;
         const float seed = __builtin_amdgcn_rcpf(d);
-        const float y = lx::recip_newton2(d, seed);
+        const float y = lx::recip_newton1(d, seed);
         bad += __builtin_bit_cast(uint32_t, y) != __builtin_bit_cast(uint32_t, cr);
         const bool off = __builtin_bit_cast(uint32_t, seed) != __builtin_bit_cast(uint32_t, cr);
         seed_off += off;
@@ -81,3 +81,4 @@ extern "C" int lx_test_device_recip(long long *out) {
     (void)hipFree(d);
     return (int)e;
 }
+

@@ -633,15 +633,16 @@ def test_add_softmax(hip, s_shape, m_shape):
 
 
 def test_device_reciprocal_is_correctly_rounded(hip):
-    """The Erf / GELU reciprocal (v_rcp_f32 seed, two float Newton steps)
-    equals IEEE 1.0f / d on the device for every float d in [1, 2^126); in
-    particular v_rcp_f32 is exact on the all-ones significands, the one case
-    the Newton steps do not repair from an off-by-one seed."""
+    """The Erf / GELU reciprocal (v_rcp_f32 seed, one float Newton step) equals
+    IEEE 1.0f / d on the device for every float d in [1, 2^126): the step
+    repairs every seed v_rcp_f32 gives one ulp off (about a tenth of them), and
+    v_rcp_f32 is exact at the 33 significands per binade where a one-ulp seed
+    would not be repaired (the host enumeration finds exactly those)."""
     lib = ctypes.CDLL(os.path.join(HERE, "native", "librcp_check.so"))
     out = (ctypes.c_longlong * 3)()
     assert lib.lx_test_device_recip(out) == 0
     assert out[0] == 0, f"{out[0]} reciprocals differ from 1/d ({out[1]} seeds off by one ulp)"
-    assert out[2] == 0
+    assert out[1] > 0   # the check sees off-by-one seeds: the Newton step is doing work
 
 
 def test_device_rcp_f32_error_bound(hip):

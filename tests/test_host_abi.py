@@ -158,18 +158,17 @@ def test_division_free_sequences_are_exact():
     """The device Erf / GELU replace IEEE divisions and the expf early-outs by
     exact equivalents; each is proven here by exhaustion on the host:
       x / 1.4142135f  == (float)(x * (double)(1/1.4142135f))   for all 2^32 x
-      1 / d           == two float Newton steps from any seed within 1 ulp,
-                         for every float d in [1, 2^126), except that a d with
-                         an all-ones significand needs the correctly rounded
-                         seed (the device check covers v_rcp_f32 there)
+      1 / d           == one float Newton step from the correctly rounded seed
+                         for every float d in [1, 2^126); from a seed one ulp
+                         off it fails at exactly 33 significands per binade
+                         (the device check shows v_rcp_f32 never lands there)
       expf(x)         == the clamped early-out-free expf for every x <= 0."""
     lib = _native()
     assert lib.lx_test_div_sqrt2_mismatches() == 0
     out = (ctypes.c_longlong * 2)()
     lib.lx_test_recip_mismatches(out)
     assert out[0] == 0
-    # exactly the two off-by-one seeds of each of the 126 all-ones significands
-    assert out[1] == 2 * 126
+    assert out[1] == 33 * 126
     assert lib.lx_test_expf_nonpos_mismatches() == 0
 
 
