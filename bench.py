@@ -712,27 +712,34 @@ def bench_extras(torch, HIP, DeviceTensor, set_stream, steps, warmup, W):
 
 # ---------------------------------------------------------------------------
 def headline_c5(torch, W, steps, warmup):
-    """K steps of C5 (GELU, ReduceSum(axis 1), ReduceMean(all)) on the launch stream, a HIP event before
-    and after every kernel: returns (ms per step, {op: ms per launch})."""
-    fns = (("gelu", W.gelu), ("rsum", W.rsum), ("rmean", W.rmean))
+    """K steps of C5 (GELU, ReduceSum(axis 1), ReduceMean(all)) on the launch stream.  A HIP event before
+    and after every GELU launch (the roofline kernel) and one after the last step: each event is a queue
+    packet that adds about 3.4 us of device time, so the two reductions are timed together, as the rest of
+    the step.  Returns (ms per step, {"gelu": ms per launch, "reductions": ms per step}, host wall ms per step)."""
+    fns = (W.gelu, W.rsum, W.rmean)
     for _ in range(warmup):
-        for _, f in fns:
+        for f in fns:
             r = f()
             if r.Code:
                 raise RuntimeError(r.Message)
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fns) + 1)] for _ in range(steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     for s in range(steps):
         ev[s][0].record()
-        for j, (_, f) in enumerate(fns):
-            f()
-            ev[s][j + 1].record()
+        W.gelu()
+        ev[s][1].record()
+        W.rsum()
+        W.rmean()
+    end.record()
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    total = ev[0][0].elapsed_time(ev[-1][-1])
-    per = {nm: sum(ev[s][j].elapsed_time(ev[s][j + 1]) for s in range(steps)) / steps for j, (nm, _) in enumerate(fns)}
-    return total / steps, per, wall_ms / steps
+    total = ev[0][0].elapsed_time(end)
+    gelu = sum(ev[s][0].elapsed_time(ev[s][1]) for s in range(steps)) / steps
+    nxt = [ev[s + 1][0] for s in range(steps - 1)] + [end]
+    red = sum(ev[s][1].elapsed_time(nxt[s]) for s in range(steps)) / steps
+    return total / steps, {"gelu": gelu, "reductions": red}, wall_ms / steps
 
 
 def main():
@@ -781,8 +788,8 @@ def main():
     ms, per, wall = headline_c5(torch, W, args.steps, args.warmup)
     gbs = C5_STEP_BYTES / (ms * 1e-3) / 1e9
     gelu_gbs = GELU_BYTES / (per["gelu"] * 1e-3) / 1e9
-    log(f"C5 step {ms * 1e3:.1f} us ({gbs:.0f} GB/s): GELU {per['gelu'] * 1e3:.1f} us, ReduceSum(axis 1) "
-        f"{per['rsum'] * 1e3:.1f} us, ReduceMean(all) {per['rmean'] * 1e3:.1f} us; host wall {wall * 1e3:.1f} us/step")
+    log(f"C5 step {ms * 1e3:.1f} us ({gbs:.0f} GB/s): GELU {per['gelu'] * 1e3:.1f} us, ReduceSum(axis 1) + "
+        f"ReduceMean(all) {per['reductions'] * 1e3:.1f} us; host wall {wall * 1e3:.1f} us/step")
     out = {
         "metric": "achieved HBM GB/s (% of MI355X peak) per op + elements/s vs C# CPU path",
         "value": round(gbs, 2),
@@ -800,10 +807,10 @@ def main():
                                "X[32,2048,3072] f32, ReduceSum(axis=1) and ReduceMean(all) on Y[256,4096,256] f32",
                    "algorithmic_bytes_per_step": C5_STEP_BYTES,
                    "elements_per_s": round((W.X5.numel() + 2 * W.Yb.numel()) / (ms * 1e-3), 1),
-                   "per_op_us": {"gelu": round(per["gelu"] * 1e3, 2), "reduce_sum_axis1": round(per["rsum"] * 1e3, 2),
-                                 "reduce_mean_all": round(per["rmean"] * 1e3, 2)},
+                   "per_op_us": {"gelu": round(per["gelu"] * 1e3, 2),
+                                 "reduce_sum_axis1 + reduce_mean_all": round(per["reductions"] * 1e3, 2)},
                    "timing": "K eager steps on one dedicated stream (the library's launch stream), HIP events "
-                             "recorded on it between consecutive kernels"},
+                             "recorded on it before and after every GELU launch and after the last step"},
         "roofline": {"bound": "hbm", "achieved": round(gelu_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": round(gelu_gbs / PEAK_HBM_GBS, 4), "traffic": None, "kernel": "lx::k_gelu_erf<4>",
                      "kernel_us": round(per["gelu"] * 1e3, 2), "algorithmic_bytes_per_launch": GELU_BYTES},

@@ -632,6 +632,23 @@ def test_add_softmax(hip, s_shape, m_shape):
     assert np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30), err.max()
 
 
+@pytest.mark.parametrize("s_shape,m_shape", [((3, 5, 1001, 64), (3, 1, 1, 64)), ((2, 7, 999, 128), (2, 1, 999, 1)),
+                                             ((5, 2003, 96), (5, 1, 96)), ((2, 7, 4999, 64), (2, 1, 4999, 1))])
+def test_add_softmax_mask_rows_change_along_the_rows(hip, s_shape, m_shape):
+    """Mask rows that change part-way through a block's rows (odd rows per batch), a mask that changes on
+    every row ([b, 1, q, 1], broadcast along the row), and more rows than the row kernel has waves (69,986
+    rows: waves take a second row, whose mask row differs from their first)."""
+    rng = np.random.default_rng(31)
+    s = (rng.standard_normal(s_shape) * 3).astype(np.float32)
+    m = np.where(rng.uniform(size=m_shape) < 0.125, -10000.0, rng.uniform(-1, 1, size=m_shape)).astype(np.float32)
+    got = ok(HIP.AddSoftmax(dev(s), dev(m), -1))
+    ref = O.add_softmax(s, m, -1)
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    err = np.abs(got.astype(np.float64) - ref)[~nan]
+    assert np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30), err.max()
+
+
 def test_device_reciprocal_is_correctly_rounded(hip):
     """The Erf / GELU reciprocal (v_rcp_f32 seed, one float Newton step) equals
     IEEE 1.0f / d on the device for every float d in [1, 2^126): the step
