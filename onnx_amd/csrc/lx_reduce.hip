@@ -166,24 +166,42 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restri
 
 // Finishing pass of the split row reduction: one block per row folds the
 // row's partials (each lane a fixed stride of them, then the block tree).
+// One wave per row folds the row's partials: each lane loads kFinishPer of them at once (one memory
+// round trip for up to 64 * kFinishPer partials), folds them in chunk order, and the wave combines the
+// lanes.  A 256-lane block whose lanes loaded their partials one dependent load at a time and combined
+// the waves through LDS made the C5 ReduceMean (512 partials) up to 0.8 us slower.
+constexpr int kFinishPer = 8;
 template <int OP, typename T>
-__global__ __launch_bounds__(kRBlock) void k_reduce_rows_finish(const typename Red<OP, T>::A *__restrict__ partial,
-                                                                T *__restrict__ y, int nchunks, int post, int64_t R) {
+__global__ __launch_bounds__(64) void k_reduce_rows_finish(const typename Red<OP, T>::A *__restrict__ partial,
+                                                           T *__restrict__ y, int nchunks, int post, int64_t R) {
     using RD = Red<OP, T>;
     using A = typename RD::A;
     const int64_t row = blockIdx.x;
+    const A *p = partial + row * nchunks;
+    const int lane = threadIdx.x;
     A t = RD::ident();
-    for (int q = threadIdx.x; q < nchunks; q += kRBlock) t = RD::comb(t, partial[row * nchunks + q]);
-    t = block_reduce<OP, T>(t);
-    if (threadIdx.x == 0) y[row] = RD::fin(t, post, R);
+    for (int q0 = 0; q0 < nchunks; q0 += 64 * kFinishPer) {
+        A v[kFinishPer];
+#pragma unroll
+        for (int u = 0; u < kFinishPer; u++) {
+            const int q = q0 + u * 64 + lane;
+            v[u] = q < nchunks ? p[q] : RD::ident();
+        }
+#pragma unroll
+        for (int u = 0; u < kFinishPer; u++) t = RD::comb(t, v[u]);
+    }
+    t = wave_reduce(t, [](A a, A b) { return RD::comb(a, b); });
+    if (lane == 0) y[row] = RD::fin(t, post, R);
 }
 
 // inner > 1: grid (column tiles * outer, rsplit).  ct lanes cover ct column
 // vectors; 256/ct row slices.  Rows are taken in groups of nrs consecutive
 // rows, group g going to split g % rsplit, so the splits sweep the slab
 // together.  Slices are combined in LDS; with rsplit > 1 each split writes a
-// partial and k_reduce_cols_finish folds them in split order.
-template <int OP, typename T, int V>
+// partial and k_reduce_cols_finish folds them in split order.  UN: row vectors
+// each lane loads before folding them (in row order, so the fold is the same
+// for every UN).
+template <int OP, typename T, int V, int UN>
 __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x,
                                                          typename Red<OP, T>::A *__restrict__ partial,
                                                          T *__restrict__ y, int64_t outer, int64_t r, int64_t inner,
@@ -206,17 +224,14 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x
     if (cv < inner_v) {
         const T *p = x + (o * r) * inner + cv * V;
         int64_t j = (int64_t)s * nrs + rs;
-        for (; j + 3 * G < r; j += 4 * G) {
-            Vec<T, V> a0 = vload_nt<T, V>(p + j * inner);
-            Vec<T, V> a1 = vload_nt<T, V>(p + (j + G) * inner);
-            Vec<T, V> a2 = vload_nt<T, V>(p + (j + 2 * G) * inner);
-            Vec<T, V> a3 = vload_nt<T, V>(p + (j + 3 * G) * inner);
+        for (; j + (UN - 1) * G < r; j += UN * G) {
+            Vec<T, V> a[UN];
 #pragma unroll
-            for (int k = 0; k < V; k++) {
-                acc[k] = RD::comb(acc[k], RD::load(a0.v[k], pre, R));
-                acc[k] = RD::comb(acc[k], RD::load(a1.v[k], pre, R));
-                acc[k] = RD::comb(acc[k], RD::load(a2.v[k], pre, R));
-                acc[k] = RD::comb(acc[k], RD::load(a3.v[k], pre, R));
+            for (int u = 0; u < UN; u++) a[u] = vload_nt<T, V>(p + (j + u * G) * inner);
+#pragma unroll
+            for (int u = 0; u < UN; u++) {
+#pragma unroll
+                for (int k = 0; k < V; k++) acc[k] = RD::comb(acc[k], RD::load(a[u].v[k], pre, R));
             }
         }
         for (; j < r; j += G) {
@@ -278,6 +293,13 @@ struct RedPlan {
 };
 
 static constexpr int64_t kTargetBlocks = 2048;
+// a column reduction with fewer blocks than this splits its rows into slices (up to kTargetBlocks blocks in
+// all, folded by a second launch); each lane keeps kColsUnroll row vectors in flight.  C5's [256,4096,256]
+// axis 1 has 512 blocks: unsplit with eight vectors in flight it reads at 7.0 TB/s in one launch (152.8 us),
+// against 155.2 us for four slices, four vectors and the folding launch (sixteen vectors: 236 us, the
+// registers no longer fit)
+static constexpr int64_t kColsSplitBelow = 512;
+static constexpr int kColsUnroll = 8;
 // blocks over all rows of a split row reduction: 512 (two per CU) read a 1 GiB row at 7.1 TB/s on MI355X,
 // against 6.9 with 1024 and 6.8 with 2048; the finishing pass stays a separate launch (a last-block finish
 // inside this launch, one device-scope release fence per block, took 20 us longer)
@@ -310,7 +332,7 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
     const int64_t base = tiles * outer;
     const int nrs = kRBlock / ct;
     int64_t rsplit = 1;
-    if (base < kTargetBlocks) {
+    if (base < kColsSplitBelow) {
         rsplit = ceil_div(kTargetBlocks, base);
         int64_t maxs = ceil_div(r, (int64_t)nrs * 16);  // >= 16 rows per slice
         if (rsplit > maxs) rsplit = maxs;
@@ -340,11 +362,11 @@ static hipError_t reduce_typed_v(const ReduceArgs &a, hipStream_t s) {
         hipLaunchKernelGGL((k_reduce_rows_split<OP, T, V>), dim3(p.nchunks, (unsigned)a.outer), dim3(kRBlock), 0, s, x,
                            ws, y, a.r, p.nchunks, a.pre_div, a.post_div, a.r_total);
         if (p.nchunks > 1)
-            hipLaunchKernelGGL((k_reduce_rows_finish<OP, T>), dim3((unsigned)a.outer), dim3(kRBlock), 0, s, ws, y,
+            hipLaunchKernelGGL((k_reduce_rows_finish<OP, T>), dim3((unsigned)a.outer), dim3(64), 0, s, ws, y,
                                p.nchunks, a.post_div, a.r_total);
     } else {
         const int64_t tiles = ceil_div(a.inner / V, p.ct);
-        hipLaunchKernelGGL((k_reduce_cols<OP, T, V>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
+        hipLaunchKernelGGL((k_reduce_cols<OP, T, V, kColsUnroll>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
                            dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rsplit, a.pre_div,
                            a.post_div, a.r_total);
         if (p.rsplit > 1) {
