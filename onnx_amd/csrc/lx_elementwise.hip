@@ -81,9 +81,22 @@ hipError_t launch_reset_errs(ErrFlags *e, hipStream_t s) {
 // meets, then lane 0 stores the sequence number with release semantics.
 // reset (null, or src itself): each word is set to all ones after it has been
 // copied, by the thread that read it -- the cleared state of an error record,
-// so the next check on the stream needs no reset launch of its own
+// so the next check on the stream needs no reset launch of its own.  A record of at
+// most kPublishFew words (an error record) is copied by lane 0 alone, whose release
+// store then orders its own copies: no fence or barrier of the other lanes.
+constexpr int64_t kPublishFew = 4;
 __global__ __launch_bounds__(kBlock) void k_publish(const uint64_t *src, int64_t n, uint64_t *__restrict__ dst,
                                                     uint64_t *seq_dst, uint64_t seq, uint64_t *reset) {
+    if (n <= kPublishFew) {
+        if (threadIdx.x == 0) {
+            for (int64_t i = 0; i < n; i++) {
+                dst[i] = src[i];
+                if (reset) reset[i] = ~0ull;
+            }
+            __hip_atomic_store(seq_dst, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
+        return;
+    }
     for (int64_t i = threadIdx.x; i < n; i += kBlock) {
         dst[i] = src[i];
         if (reset) reset[i] = ~0ull;
@@ -95,7 +108,7 @@ __global__ __launch_bounds__(kBlock) void k_publish(const uint64_t *src, int64_t
 
 hipError_t launch_publish(const uint64_t *src, int64_t n, uint64_t *dst, uint64_t *seq_dst, uint64_t seq,
                           uint64_t *reset, hipStream_t s) {
-    hipLaunchKernelGGL(k_publish, dim3(1), dim3(kBlock), 0, s, src, n, dst, seq_dst, seq, reset);
+    hipLaunchKernelGGL(k_publish, dim3(1), dim3(n <= kPublishFew ? 64 : kBlock), 0, s, src, n, dst, seq_dst, seq, reset);
     return hipGetLastError();
 }
 
