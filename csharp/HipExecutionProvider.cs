@@ -381,5 +381,17 @@ public unsafe class HipExecutionProvider : Runtime
         LxTensor r = residual is null ? default : args.In(residual);
         return Done(op, HipNative.lx_MatMulAdd(&a, &b, &c, residual is null ? null : &r, &y), y, A, B);
     }
+
+    /// <summary>MatMul -> Add bias -> the GELU subgraph (a BERT FFN's first projection) in one launch.</summary>
+    public static OpResult MatMulAddGelu(ITensor? A, ITensor? B, ITensor? bias)
+    {
+        var op = OpType.MatMul;
+        if (A is null) return MissingInput(op, nameof(A));
+        if (B is null) return MissingInput(op, nameof(B));
+        if (bias is null) return MissingInput(OpType.Add, "B");
+        using var args = new Args();
+        LxTensor a = args.In(A), b = args.In(B), c = args.In(bias), y = default;
+        return Done(op, HipNative.lx_MatMulAddGelu(&a, &b, &c, &y), y, A, B);
+    }
     #endregion
 }

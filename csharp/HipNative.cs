@@ -126,6 +126,7 @@ internal static unsafe class HipNative
     // ---- fused subgraphs (one kernel each, every node's float32 rounding kept) ----------------
     [DllImport(Lib)] public static extern int lx_MatMulAdd(LxTensor* a, LxTensor* b, LxTensor* bias, LxTensor* residual,
                                                            LxTensor* y);
+    [DllImport(Lib)] public static extern int lx_MatMulAddGelu(LxTensor* a, LxTensor* b, LxTensor* bias, LxTensor* y);
     [DllImport(Lib)] public static extern int lx_GeluErf(LxTensor* x, LxTensor* y);
     [DllImport(Lib)] public static extern int lx_LayerNormDecomposed(LxTensor* x, LxTensor* gamma, LxTensor* beta,
                                                                      float eps, LxTensor* y);

@@ -198,6 +198,11 @@ int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, con
  * and the Adds run one after the other.  residual may be NULL. */
 int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
                  lx_tensor *Y);
+/* MatMul(A, B) -> Add(., bias) -> the ONNX GELU subgraph Div(., sqrt2) -> Erf -> Add 1 -> Mul . -> Mul 0.5
+ * (a BERT FFN's first projection; the graph runtime's fusion of those seven nodes).  Float: the Add and
+ * the GELU in the MatMul's epilogue, every node rounded as it rounds (bias as for lx_MatMulAdd); otherwise
+ * lx_MatMulAdd's path followed by lx_GeluErf. */
+int lx_MatMulAddGelu(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, lx_tensor *Y);
 
 /* ---- fused subgraphs (one kernel each; every intermediate keeps the float32
  * rounding of the separate ONNX node it replaces) ------------------------- */

@@ -110,6 +110,7 @@ SIGNATURES = {
     "lx_Gather": (_c.c_int, [_T, _T, _c.c_int32, _c.c_int32, _T]),
     "lx_Slice": (_c.c_int, [_T, _i64p, _c.c_int32, _i64p, _c.c_int32, _i64p, _c.c_int32, _i64p, _c.c_int32, _T]),
     "lx_MatMulAdd": (_c.c_int, [_T, _T, _T, _T, _T]),
+    "lx_MatMulAddGelu": (_c.c_int, [_T, _T, _T, _T]),
     "lx_ScaleAddSoftmax": (_c.c_int, [_T, _T, _c.c_int32, _T, _c.c_int32, _T]),
     "lx_ElementwiseChain": (_c.c_int, [_c.POINTER(_T), _c.c_int32, _i32p, _i32p, _c.c_int32, _T]),
     "lx_read_probe": (_c.c_int, [_c.c_void_p, _c.c_int64, _c.c_void_p, _c.c_int64]),

@@ -1484,6 +1484,7 @@ int densify(int dt, MView *v, std::vector<void *> &temps) {
 // residual has the output's shape (Float); `applied` tells the caller
 struct MatMulEpilogue {
     const lx_tensor *bias = nullptr, *res = nullptr;
+    bool gelu = false;  // then the GELU subgraph on each result (lx_MatMulAddGelu)
     bool applied = false;
 };
 thread_local MatMulEpilogue *t_mm_epi = nullptr;
@@ -1525,6 +1526,7 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
         p.bias = t_mm_epi->bias ? (const float *)t_mm_epi->bias->data : nullptr;
         p.bias_bstr = bias_bstr;
         p.res = t_mm_epi->res ? (const float *)t_mm_epi->res->data : nullptr;
+        p.gelu = t_mm_epi->gelu ? 1 : 0;
     }
     p.m = (int32_t)x.dims[x.rank - 2];
     p.k = (int32_t)x.dims[x.rank - 1];
@@ -1546,7 +1548,7 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
         return LX_OK;
     }
     HIPCHECK(launch_matmul(dt, x.data, y.data, Y->data, p, g.stream), "MatMul");
-    if (t_mm_epi && (p.bias || p.res)) t_mm_epi->applied = true;
+    if (t_mm_epi && (p.bias || p.res || p.gelu)) t_mm_epi->applied = true;
     return LX_OK;
 }
 
@@ -1623,8 +1625,11 @@ extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     return st;
 }
 
-extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
-                            lx_tensor *Y) {
+// MatMul -> Add bias [-> Add residual] [-> the GELU subgraph]: in the MatMul's epilogue when the shapes fit
+// (Float), else the MatMul and then each node's operator, into new tensors (an Add may broadcast to a larger
+// shape than the product's)
+int matmul_add_run(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
+                   bool gelu, lx_tensor *Y) {
     REQUIRE_INIT();
     if (!bias) return missing_input("Add", "B");
     int st;
@@ -1634,6 +1639,7 @@ extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_ten
     MatMulEpilogue epi;
     epi.bias = bias;
     epi.res = residual;
+    epi.gelu = gelu;
     t_mm_epi = &epi;
     lx_tensor c = caller_storage ? *Y : lx_tensor{};
     st = lx_MatMul(A, B, caller_storage ? &c : Y);
@@ -1643,19 +1649,21 @@ extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_ten
         if (caller_storage) *Y = c;
         return LX_OK;
     }
-    // node by node: C + bias, then + residual, into new tensors (either Add may broadcast to a larger
-    // shape than the product's)
     lx_tensor *prod = caller_storage ? &c : Y;
-    lx_tensor t1{}, t2{};
+    lx_tensor t1{}, t2{}, t3{};
     st = run_binary(kAdd, prod, bias, &t1);
     if (!st && residual) st = run_binary(kAdd, &t1, residual, &t2);
     lx_tensor *out = residual ? &t2 : &t1;
+    if (!st && gelu) {
+        st = lx_GeluErf(out, &t3);
+        out = &t3;
+    }
     if (!st) {
         if (caller_storage) {
             if (!(st = prepare_output(Y, out->dtype, out->rank, out->dims)) && numel(out))
                 HIPCHECK(hipMemcpyAsync(Y->data, out->data, numel(out) * esize(out->dtype), hipMemcpyDeviceToDevice,
                                         g.stream),
-                         "MatMulAdd");
+                         gelu ? "MatMulAddGelu" : "MatMulAdd");
         } else {
             lx_tensor_free(Y);
             *Y = *out;
@@ -1664,7 +1672,17 @@ extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_ten
     }
     lx_tensor_free(&t1);
     lx_tensor_free(&t2);
+    lx_tensor_free(&t3);
     return st;
+}
+
+extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
+                            lx_tensor *Y) {
+    return matmul_add_run(A, B, bias, residual, false, Y);
+}
+
+extern "C" int lx_MatMulAddGelu(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, lx_tensor *Y) {
+    return matmul_add_run(A, B, bias, nullptr, true, Y);
 }
 
 // ===========================================================================

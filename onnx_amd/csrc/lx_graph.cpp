@@ -768,6 +768,17 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!fits) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_MatMulAdd(T(av), T(bv), T(cv), rv ? T(rv) : nullptr, y); }, outs);
     }
+    if (op == "MatMulAddGelu") {
+        Value *av, *bv, *cv;
+        if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &bv)) || (st = X.input(n, 2, &cv))) return st;
+        // the epilogue's shapes (A [..., M, K] x W [K, N] + bias [N], Float), else the nodes
+        const bool fits = av && bv && cv && av->t.dtype == LX_FLOAT && bv->t.dtype == LX_FLOAT &&
+                          cv->t.dtype == LX_FLOAT && av->t.rank >= 2 && bv->t.rank == 2 &&
+                          av->t.dims[av->t.rank - 1] == bv->t.dims[0] && cv->t.rank == 1 &&
+                          cv->t.dims[0] == bv->t.dims[1];
+        if (!fits) return run_unfused(X, n, outs);
+        return run_op([&](lx_tensor *y) { return lx_MatMulAddGelu(T(av), T(bv), T(cv), y); }, outs);
+    }
     if (op == "ScaleAddSoftmax") {
         Value *sv, *cv, *mv;
         if ((st = X.input(n, 0, &sv)) || (st = X.input(n, 1, &cv)) || (st = X.input(n, 2, &mv))) return st;
@@ -986,6 +997,23 @@ struct Fuser {
         f->in = {N(i0).in[0], N(i0).in[1], bias};
         f->out = N(i1).out;
         const std::string &biased = N(i1).out[0];
+        // -> the GELU subgraph on the biased product (a BERT FFN's first projection): its two consumers of
+        // the product, the Div and the Mul x, both in the pattern
+        auto cb = consumers.find(biased);
+        if (!graph_outputs.count(biased) && cb != consumers.end() && cb->second.size() == 2) {
+            for (int k : cb->second) {
+                GNode fg;
+                std::vector<int> gn;
+                if (!gelu(k, &fg, &gn) || fg.in[0] != biased) continue;
+                bool inside = true;
+                for (int c : cb->second) inside = inside && std::find(gn.begin(), gn.end(), c) != gn.end();
+                if (!inside) continue;
+                nodes->insert(nodes->end(), gn.begin(), gn.end());
+                f->op = "MatMulAddGelu";
+                f->out = fg.out;
+                return true;
+            }
+        }
         const int i2 = only_consumer(biased);
         std::string res;
         if (is(i2, "Add", 2) && other(i2, biased, &res)) {

@@ -150,6 +150,9 @@ struct MatMulArgs {
     const float *bias;
     const float *res;
     int64_t bias_bstr;  // 0: one bias row for every batch; n: a bias row per batch (linear batch index)
+    // then, when gelu != 0, the ONNX GELU subgraph Div(., sqrt 2) -> Erf -> Add 1 -> Mul . -> Mul 0.5 on
+    // each result, every node rounded as it rounds (Float)
+    int32_t gelu;
 };
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);
 

@@ -49,7 +49,7 @@ __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, in
 // about 144 TF/s on MI355X; the 128x128 tile runs large GEMMs at 127-131 TF/s.
 constexpr int kFBK = 16, kFPad = 4;
 
-template <int BM, int BN, int WM, int WN, bool VEC>
+template <int BM, int BN, int WM, int WN, bool VEC, bool GELU>
 __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__restrict__ A, const float *__restrict__ B,
                                                              float *__restrict__ C, MatMulArgs p) {
     constexpr int NTHR = WM * WN * 64;               // threads of the block
@@ -61,6 +61,8 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     constexpr int BQ = BN / 4;                       // float4 per B row
     __shared__ float As[2][kFBK][BM + kFPad];
     __shared__ float Bs[2][kFBK][BN + kFPad];
+    __shared__ ExpTable tab;  // the GELU epilogue's exponential (filled before the first barrier)
+    if constexpr (GELU) exp_table_fill(tab);
     const int M = p.m, N = p.n, K = p.k;
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
@@ -175,6 +177,7 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
                     float v = acc[i][j][r];
                     if (Bias) v = v + bc;
                     if (Rb) v = v + Rb[(int64_t)row * N + c];
+                    if constexpr (GELU) v = gelu_erf_lx(v, tab);
                     Cb[(int64_t)row * N + c] = v;
                 }
             }
@@ -185,8 +188,13 @@ template <int BM, int BN, int WM, int WN>
 static void launch_f32(const float *a, const float *b, float *c, const MatMulArgs &p, bool vec, hipStream_t s) {
     dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
     const dim3 blk(WM * WN * 64);
-    if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true>), g, blk, 0, s, a, b, c, p);
-    else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false>), g, blk, 0, s, a, b, c, p);
+    if (p.gelu) {
+        if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true, true>), g, blk, 0, s, a, b, c, p);
+        else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false, true>), g, blk, 0, s, a, b, c, p);
+    } else {
+        if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true, false>), g, blk, 0, s, a, b, c, p);
+        else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false, false>), g, blk, 0, s, a, b, c, p);
+    }
 }
 
 // ---------------------------------------------------------------------------

@@ -364,6 +364,16 @@ class HipExecutionProvider:
         return _result("MatMulAdd", st, y, out)
 
     @staticmethod
+    def MatMulAddGelu(A, B, bias, out=None):
+        """MatMul(A, B) -> Add bias -> the ONNX GELU subgraph, the Add and GELU in the MatMul's epilogue
+        (lx_MatMulAddGelu)."""
+        init()
+        A, B, bias = _as_tensor(A), _as_tensor(B), _as_tensor(bias)
+        y = out.h if out is not None else L.LxTensor()
+        st = L.lib().lx_MatMulAddGelu(_ptr(A), _ptr(B), _ptr(bias), ctypes.byref(y))
+        return _result("MatMulAddGelu", st, y, out)
+
+    @staticmethod
     def ScaleAddSoftmax(S, scale, divide=True, mask=None, axis=-1, out=None):
         """Div(S, scale) (or Mul) -> Add(., mask) -> Softmax(axis) in one kernel (lx_ScaleAddSoftmax)."""
         init()

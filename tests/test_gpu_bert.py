@@ -33,7 +33,7 @@ def test_bert_layer_accuracy(hip, layer, mode):
     model, ins, ref, t64 = layer
     g = Model.Load(model)
     if mode != "nodes":
-        assert g.Fuse() == 8
+        assert g.Fuse() == 7
     dev = {k: DeviceTensor.from_numpy(v) for k, v in ins.items()}
     ok = g.Capture(dev) if mode == "captured" else g.Execute(dev)
     assert ok, g.LastError

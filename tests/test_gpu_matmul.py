@@ -257,3 +257,77 @@ def test_grouped_projection_slice_capacity_is_its_own(hip):
     for o in ("q0", "k0", "v0"):
         assert g.Output(o).h.capacity == 2 * 40 * 64 * 4, o
     g.close()
+
+
+def _gelu_nodes(t):
+    """The ONNX GELU subgraph's five separate device operators on t (the reference's node-by-node path)."""
+    c = lambda v: dev(np.array(v, t.dtype))  # noqa: E731
+    d = HIP.Div(dev(t), c(1.4142135623730951 if t.dtype == np.float64 else np.float32(1.4142135))).Outputs[0]
+    e = HIP.Erf(d).Outputs[0]
+    a = HIP.Add(e, c(1.0)).Outputs[0]
+    m = HIP.Mul(dev(t), a).Outputs[0]
+    return HIP.Mul(m, c(0.5)).Outputs[0].to_numpy()
+
+
+@pytest.mark.parametrize("sa,sb,sbias", [((256, 768), (768, 3072), (3072,)), ((2, 64, 768), (768, 256), (256,)),
+                                         ((127, 65), (65, 129), (129,)), ((3, 33, 40), (3, 40, 70), (3, 1, 70)),
+                                         ((64, 32), (32, 48), (64, 48))])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_matmul_add_gelu_equals_the_nodes(hip, sa, sb, sbias, dt):
+    """MatMul -> Add bias -> GELU (Div sqrt2, Erf, Add 1, Mul x, Mul 0.5) as one launch with the Add and the
+    GELU in the MatMul's epilogue, bit for bit the seven separate operators: a BERT FFN shape, a batch, ragged
+    tiles, a bias row per batch; a bias that is no row vector, and Double, run the nodes."""
+    rng = np.random.default_rng(61)
+    a = rng.standard_normal(sa).astype(dt)
+    b = (rng.standard_normal(sb) * 0.1).astype(dt)
+    bias = rng.standard_normal(sbias).astype(dt)
+    r = HIP.MatMulAddGelu(dev(a), dev(b), dev(bias))
+    assert r.Status == OpStatus.Success, r.Message
+    got = r.Outputs[0].to_numpy()
+    pre = HIP.Add(HIP.MatMul(dev(a), dev(b)).Outputs[0], dev(bias)).Outputs[0].to_numpy()
+    ref = _gelu_nodes(pre)
+    assert got.shape == ref.shape and got.dtype == ref.dtype
+    assert np.array_equal(got.view(np.uint8), ref.view(np.uint8))
+
+
+def test_matmul_add_gelu_special_values_and_caller_storage(hip):
+    """Pre-activations that saturate the GELU (|x| up to 1e5, where erf rounds to +-1), zeros, and NaN / inf
+    products, into caller storage: bit for bit the separate operators."""
+    rng = np.random.default_rng(62)
+    a = (rng.standard_normal((96, 64)) * np.logspace(-3, 3, 64)).astype(np.float32)
+    a[0, 0], a[1, :], a[2, 5] = np.nan, 0.0, np.inf
+    b = rng.standard_normal((64, 80)).astype(np.float32)
+    bias = rng.standard_normal(80).astype(np.float32)
+    out = DeviceTensor.empty((96, 80), np.float32)
+    r = HIP.MatMulAddGelu(dev(a), dev(b), dev(bias), out=out)
+    assert r.Status == OpStatus.Success, r.Message
+    pre = HIP.Add(HIP.MatMul(dev(a), dev(b)).Outputs[0], dev(bias)).Outputs[0].to_numpy()
+    assert np.array_equal(out.to_numpy().view(np.uint32), _gelu_nodes(pre).view(np.uint32))
+
+
+def test_ffn_gelu_graph_fuses_into_one_node(hip):
+    """MatMul -> Add bias -> the GELU nodes in a graph become one MatMulAddGelu node whose output equals the
+    unfused graph's bit for bit; with the biased product also a graph output the GELU stays a node of its own."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    rng = np.random.default_rng(94)
+    x = rng.standard_normal((2, 40, 96)).astype(np.float32)
+    inits = [("w", (rng.standard_normal((96, 128)) * 0.1).astype(np.float32)),
+             ("b", rng.standard_normal(128).astype(np.float32)), ("sqrt2", np.array(1.4142135, np.float32)),
+             ("one", np.array(1.0, np.float32)), ("half", np.array(0.5, np.float32))]
+    nodes = [W.node("MatMul", ["x", "w"], ["f0"], "ffn_in"), W.node("Add", ["f0", "b"], ["f1"], "ffn_bias"),
+             W.node("Div", ["f1", "sqrt2"], ["g0"], "gelu_div"), W.node("Erf", ["g0"], ["g1"], "gelu_erf"),
+             W.node("Add", ["g1", "one"], ["g2"], "gelu_add"), W.node("Mul", ["f1", "g2"], ["g3"], "gelu_mul"),
+             W.node("Mul", ["g3", "half"], ["y"], "gelu_half")]
+    res = {}
+    for fuse, outs in ((False, ["y"]), (True, ["y"]), ("escape", ["y", "f1"])):
+        g = Model.Load(W.model(nodes, [("x", np.float32, x.shape)], [(o, np.float32, ()) for o in outs], inits))
+        if fuse is True:
+            assert g.Fuse() == 1 and [n.Op for n in g.Nodes] == ["MatMulAddGelu"]
+        elif fuse == "escape":
+            assert g.Fuse() == 2 and [n.Op for n in g.Nodes] == ["MatMulAdd", "GeluErf"]
+        assert g.Execute({"x": dev(x)}), g.LastError
+        res[fuse] = g.Output("y").to_numpy()
+        g.close()
+    for k in (True, "escape"):
+        assert np.array_equal(res[False].view(np.uint32), res[k].view(np.uint32)), k
