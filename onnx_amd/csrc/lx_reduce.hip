@@ -81,7 +81,8 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
     using RD = Red<OP, T>;
     using A = typename RD::A;
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6);
+    // the wave's index from lane 0: the row's address arithmetic runs once per wave on the scalar unit
+    const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= rows) return;
     const T *p = x + row * r;
     A acc = RD::ident();

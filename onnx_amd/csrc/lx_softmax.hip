@@ -137,7 +137,9 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     }
     const int lane = threadIdx.x & 63;
     const int64_t W = (int64_t)gridDim.x * (kSBlock / 64);
-    int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6);
+    // the wave's index, read from lane 0 so the row and everything derived from it (the mask row offset,
+    // the row's base addresses) are computed once per wave on the scalar unit
+    int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= rows) return;
     Vec<T, V> cur[NV], nxt[NV], mcur[NV], mnxt[NV];
     const T sv = scale ? scale[0] : T(1);
