@@ -1,0 +1,251 @@
+"""Randomised differential tests: many small random cases per operator family, the HIP path against the CPU
+oracle on the same inputs.  Results are compared bit for bit (integer ops, Cast, float elementwise ops, data
+movement; a NaN matches any NaN) or within the reduction / Softmax bars, and where the reference fails
+(shapes that do not broadcast, integer division by zero or MIN / -1, casts out of range, gather indices out
+of range) the device must fail with the same status.  Shapes are drawn with ranks 0-5 and dimensions 1-7,
+broadcast operands with dropped leading axes and size-1 axes, values with special values mixed in.  Seeded:
+every run draws the same cases."""
+import numpy as np
+import pytest
+
+from onnx_amd import DeviceTensor, HipExecutionProvider as HIP, OpStatus
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+FLOATS = (np.float32, np.float64)
+CAST_TYPES = [O.FLOAT, O.DOUBLE, O.UINT8, O.INT8, O.UINT16, O.INT16, O.INT32, O.UINT32, O.INT64, O.UINT64, O.BOOL]
+
+
+def dev(a):
+    return DeviceTensor.from_numpy(np.asarray(a))
+
+
+def same_bits(got, ref):
+    """Bit-equal arrays of one shape and dtype, any NaN matching any NaN."""
+    if got.shape != ref.shape or got.dtype != ref.dtype:
+        return False
+    if got.dtype.kind == "f":
+        nan = np.isnan(ref)
+        if not np.array_equal(np.isnan(got), nan):
+            return False
+        g, r = got[~nan], ref[~nan]
+        return np.array_equal(g.view(np.uint8) if g.size else g, r.view(np.uint8) if r.size else r)
+    return np.array_equal(got, ref)
+
+
+def check(r, oracle_fn, compare, case):
+    """The device result r against the oracle: equal statuses when the oracle fails, else compare()."""
+    try:
+        ref = oracle_fn()
+    except O.OracleError as e:
+        assert r.Status != OpStatus.Success and r.Code == e.status, (case, r.Code, e.status, r.Message)
+        return
+    assert r.Status == OpStatus.Success, (case, r.Message)
+    got = r.Outputs[0].to_numpy()
+    assert compare(got, ref), (case, got, ref)
+
+
+def rand_shape(rng, rmin=0, rmax=5, dmax=7):
+    return tuple(int(d) for d in rng.integers(1, dmax + 1, int(rng.integers(rmin, rmax + 1))))
+
+
+def broadcast_pair(rng):
+    out = rand_shape(rng)
+
+    def operand():
+        r = int(rng.integers(0, len(out) + 1))
+        return tuple(1 if rng.random() < 0.3 else d for d in out[len(out) - r:])
+    a, b = operand(), operand()
+    if rng.random() < 0.1 and len(b) > 0:  # a pair that does not broadcast (when a dimension can clash)
+        k = int(rng.integers(0, len(b)))
+        b = b[:k] + (b[k] + 1 if b[k] > 1 else 2,) + b[k + 1:]
+    return a, b
+
+
+def values(rng, shape, dt, special=0.05):
+    if np.dtype(dt).kind == "f":
+        x = np.array(rng.standard_normal(shape) * 10.0 ** rng.uniform(-3, 3, shape), dt)
+        if x.size:
+            m = np.asarray(rng.random(x.shape) < special)
+            pool = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1e-40, -3e-39, 1.0, -1.0], dt)
+            x[m] = pool[rng.integers(0, pool.size, int(m.sum()))]
+        return np.asarray(x, dt)
+    if dt == np.bool_:
+        return rng.random(shape) < 0.5
+    info = np.iinfo(dt)
+    return np.asarray(rng.integers(info.min, info.max, shape, dtype=dt, endpoint=True))
+
+
+def divisors(rng, shape, dt):
+    """Divisors for integer Div: mostly small magnitudes, with zeros and -1 now and then."""
+    if np.dtype(dt).kind == "f":
+        return values(rng, shape, dt)
+    info = np.iinfo(dt)
+    lo = -1000 if info.min < 0 else 0
+    b = np.asarray(rng.integers(lo, 1000, shape, dtype=np.int64), np.int64)
+    if b.size:
+        b = np.where(b == 0, 7, b)
+        m = rng.random(b.shape)
+        b = np.where(m < 0.03, 0, b)
+        if info.min < 0:
+            b = np.where((m >= 0.03) & (m < 0.06), -1, b)
+        big = rng.integers(info.min // 2 + 1, info.max // 2, b.shape, dtype=np.int64) if info.max > 2**31 else b
+        b = np.where((m >= 0.06) & (m < 0.12), big, b)
+    return np.asarray(b, dt)
+
+
+def dividends(rng, shape, dt):
+    a = values(rng, shape, dt)
+    if np.dtype(dt).kind == "i" and a.size:  # MIN now and then, to meet a divisor of -1
+        a = np.where(rng.random(a.shape) < 0.05, np.iinfo(dt).min, a).astype(dt)
+    return np.asarray(a, dt)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.uint8, np.int32, np.int64])
+@pytest.mark.parametrize("op", ["Add", "Sub", "Mul", "Div"])
+def test_binary_random(hip, op, dt):
+    rng = np.random.default_rng([11, ["Add", "Sub", "Mul", "Div"].index(op), np.dtype(dt).num])
+    code = {"Add": O.ADD, "Sub": O.SUB, "Mul": O.MUL, "Div": O.DIV}[op]
+    for case in range(150):
+        sa, sb = broadcast_pair(rng)
+        if op == "Div":
+            a, b = dividends(rng, sa, dt), divisors(rng, sb, dt)
+        else:
+            a, b = values(rng, sa, dt), values(rng, sb, dt)
+        r = getattr(HIP, op)(dev(a), dev(b))
+        check(r, lambda: O.binary(code, a, b), same_bits, (op, dt, sa, sb, case))
+
+
+def reduction_bar(dt):
+    def compare(got, ref, x_abs):
+        if got.shape != ref.shape:
+            return False
+        nan = np.isnan(ref)
+        if not np.array_equal(np.isnan(got), nan):
+            return False
+        err = np.abs(got.astype(np.float64) - ref.astype(np.float64))[~nan]
+        return bool(np.all(err <= (1e-5 if dt == np.float32 else 1e-12) * x_abs[~nan] + 1e-30))
+    return compare
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64])
+@pytest.mark.parametrize("op", ["ReduceSum", "ReduceMean", "ReduceMax"])
+def test_reduce_random(hip, op, dt):
+    rng = np.random.default_rng([12, ["ReduceSum", "ReduceMean", "ReduceMax"].index(op), np.dtype(dt).num])
+    code = {"ReduceSum": O.RSUM, "ReduceMean": O.RMEAN, "ReduceMax": O.RMAX}[op]
+    for case in range(150):
+        shape = rand_shape(rng, 1, 4, 9)
+        x = values(rng, shape, dt, special=0.0) if np.dtype(dt).kind == "f" else \
+            np.asarray(rng.integers(-(2**20), 2**20, shape), dt)
+        r_ = len(shape)
+        k = int(rng.integers(0, r_ + 1))
+        axes = None if k == 0 else [int(a) - (r_ if rng.random() < 0.3 else 0)
+                                    for a in rng.choice(r_, size=k, replace=False)]
+        kd = int(rng.integers(0, 2))
+        r = getattr(HIP, op)(dev(x), axes, kd)
+        ax = tuple(range(r_)) if axes is None else tuple(a % r_ for a in axes)
+        if np.dtype(dt).kind != "f" or op == "ReduceMax":
+            compare = same_bits
+        else:
+            x_abs = np.abs(x.astype(np.float64)).sum(axis=ax, keepdims=bool(kd))
+            if op == "ReduceMean":
+                x_abs = x_abs / max(1, int(np.prod([shape[a] for a in ax])))
+            bar = reduction_bar(dt)
+            compare = lambda got, ref, bar=bar, x_abs=x_abs: bar(got, ref, np.asarray(x_abs))  # noqa: E731
+        check(r, lambda: O.reduce(code, x, axes, bool(kd)), compare, (op, dt, shape, axes, kd, case))
+
+
+@pytest.mark.parametrize("dt", FLOATS)
+def test_softmax_random(hip, dt):
+    rng = np.random.default_rng([13, np.dtype(dt).num])
+    for case in range(200):
+        shape = rand_shape(rng, 1, 4, 9)
+        x = (rng.standard_normal(shape) * 4).astype(dt)
+        axis = int(rng.integers(-len(shape), len(shape)))
+        r = HIP.Softmax(dev(x), axis)
+
+        def compare(got, ref):
+            nan = np.isnan(ref)
+            if got.shape != ref.shape or not np.array_equal(np.isnan(got), nan):
+                return False
+            err = np.abs(got.astype(np.float64) - ref)[~nan]
+            return bool(np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30))
+        check(r, lambda: O.softmax(x, axis), compare, (dt, shape, axis, case))
+
+
+def test_cast_random(hip):
+    rng = np.random.default_rng(14)
+    for case in range(400):
+        src, dst = (int(v) for v in rng.choice(CAST_TYPES, 2))
+        shape = rand_shape(rng, 0, 3, 9)
+        dt = O.NP_OF[src]
+        if np.dtype(dt).kind == "f":
+            x = values(rng, shape, dt)
+            x = np.asarray(x * np.asarray(10.0 ** rng.integers(0, 12, shape), dt), dt) if x.size else x
+        else:
+            x = values(rng, shape, dt)
+        r = HIP.Cast(dev(x), dst)
+        check(r, lambda: O.cast(x, dst), same_bits, (src, dst, shape, case))
+
+
+MOVE_TYPES = [np.float32, np.float64, np.uint8, np.int16, np.int32, np.int64, np.bool_]
+
+
+def test_transpose_random(hip):
+    rng = np.random.default_rng(15)
+    for case in range(200):
+        dt = MOVE_TYPES[case % len(MOVE_TYPES)]
+        shape = rand_shape(rng, 0, 5, 7)
+        x = values(rng, shape, dt, special=0.0)
+        perm = None if rng.random() < 0.2 else [int(p) - (len(shape) if rng.random() < 0.3 else 0)
+                                                for p in rng.permutation(len(shape))]
+        r = HIP.Transpose(dev(x), perm)
+        check(r, lambda: O.transpose(x, perm), same_bits, (dt, shape, perm, case))
+
+
+def test_slice_random(hip):
+    rng = np.random.default_rng(16)
+    for case in range(250):
+        dt = MOVE_TYPES[case % len(MOVE_TYPES)]
+        shape = rand_shape(rng, 1, 4, 9)
+        x = values(rng, shape, dt, special=0.0)
+        r_ = len(shape)
+        n = int(rng.integers(1, r_ + 1))
+        axes = [int(a) for a in rng.choice(r_, size=n, replace=False)]
+        starts = [int(rng.integers(-12, 12)) for _ in range(n)]
+        ends = [int(rng.integers(-12, 12)) for _ in range(n)]
+        steps = [int(rng.choice([-3, -2, -1, 1, 2, 3])) for _ in range(n)]
+        ax = [a - r_ if rng.random() < 0.3 else a for a in axes]
+        r = HIP.Slice(dev(x), starts, ends, ax, steps)
+        check(r, lambda: O.slice_(x, starts, ends, ax, steps), same_bits, (dt, shape, starts, ends, ax, steps, case))
+
+
+def test_gather_random(hip):
+    rng = np.random.default_rng(17)
+    for case in range(250):
+        dt = MOVE_TYPES[case % len(MOVE_TYPES)]
+        shape = rand_shape(rng, 1, 4, 7)
+        x = values(rng, shape, dt, special=0.0)
+        axis = int(rng.integers(-len(shape), len(shape)))
+        dim = shape[axis]
+        ishape = rand_shape(rng, 0, min(2, len(shape)), 5)
+        lo, hi = (-dim - 1, dim + 1) if rng.random() < 0.2 else (-dim, dim)
+        idx = np.asarray(rng.integers(lo, hi, ishape), np.int64 if rng.random() < 0.5 else np.int32)
+        r = HIP.Gather(dev(x), dev(idx), axis)
+        check(r, lambda: O.gather(x, idx, axis), same_bits, (dt, shape, axis, ishape, case))
+
+
+def test_concat_random(hip):
+    rng = np.random.default_rng(18)
+    for case in range(200):
+        dt = MOVE_TYPES[case % len(MOVE_TYPES)]
+        shape = rand_shape(rng, 1, 4, 6)
+        axis = int(rng.integers(-len(shape), len(shape)))
+        xs = []
+        for _ in range(int(rng.integers(2, 5))):
+            s = list(shape)
+            s[axis] = int(rng.integers(1, 6))
+            xs.append(values(rng, tuple(s), dt, special=0.0))
+        r = HIP.Concat([dev(v) for v in xs], axis)
+        check(r, lambda: O.concat(xs, axis), same_bits, (dt, shape, axis, case))
