@@ -777,7 +777,7 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
 
 int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t has_axis, lx_tensor *Y,
                 const char *opn, const lx_tensor *scale = nullptr, int scale_div = 1);
-bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, int vec, int64_t V, SoftmaxArgs &sa);
+bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, SoftmaxArgs &sa);
 
 }  // namespace
 
@@ -1239,7 +1239,7 @@ namespace {
 // The mask of a last-axis Softmax over scores of shape dims, as the row-per-wave kernel reads it:
 // contiguous or broadcast along the row, and the row index decomposed over the collapsed row axes
 // (size-1 axes dropped, contiguous ones merged).  False when the kernel cannot take it.
-bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, int vec, int64_t V, SoftmaxArgs &sa) {
+bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, SoftmaxArgs &sa) {
     const int64_t r = dims[rank - 1];
     // mask strides in the scores' frame (no collapsing of the softmax axis)
     int64_t ms[LX_MAX_RANK];
@@ -1251,7 +1251,6 @@ bool softmax_mask_layout(int rank, const int64_t *dims, const lx_tensor *mask, i
         stv *= mask->dims[k];
     }
     sa.mask_inner = (r > 1 && ms[rank - 1] != 0) ? 1 : 0;
-    if (sa.mask_inner && vec > 1 && r % V != 0) return false;
     // row axes 0..rank-2: collapse (drop size 1, merge contiguous)
     int64_t cd[LX_MAX_RANK], cs[LX_MAX_RANK];
     int n = 0;
@@ -1345,7 +1344,7 @@ int run_softmax(const lx_tensor *X, const lx_tensor *mask, int32_t axis, int32_t
         bool same_shape = st == LX_OK && p.out_rank == X->rank;
         for (int i = 0; same_shape && i < X->rank; i++) same_shape = p.out_dims[i] == X->dims[i];
         fusable = same_shape && softmax_mask_fusable(X->dtype, r, inner, outer, vec) &&
-                  (vec == 1 || aligned16(mask->data)) && softmax_mask_layout(rank, X->dims, mask, vec, V, sa);
+                  softmax_mask_layout(rank, X->dims, mask, sa);
     }
     if (scale) {
         // the scale must leave X's shape as it is (one element, rank <= X's) for the kernel to apply it

@@ -6,9 +6,12 @@
 //   m = ReduceMax(x, axis) (seed 0)   d = x - m   e = MathF.Exp(d)
 //   s = ReduceSum(e, axis)            y = e / s   (true division)
 // Here: one wave64 per row with the row in registers (rows up to 2048 floats),
-// the exponential bit-identical to the host expf (expf_lx), the sum as a
-// wave butterfly.  Only the order of the sum differs from the reference.
-// Other shapes (axis not innermost, long rows) take a three-pass kernel.
+// or one block per row with the row in registers (up to 65536 floats), x read
+// once and y written once; rows of any length with 16-byte accesses (an
+// unaligned head and a tail held one element per lane).  The exponential is
+// bit-identical to the host expf (expf_lx), the sums run over lane moves.
+// Only the order of the sum differs from the reference.  Other shapes (axis
+// not innermost, longer rows, unaligned storage) take three-pass kernels.
 #include <type_traits>
 
 #include "lx_device.h"
@@ -214,6 +217,231 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     }
 }
 
+// ---------------------------------------------------------------------------
+// Rows of any length with 16-byte accesses.  A row starting at element s0 of
+// x splits into its head (the head = (-s0) mod V elements before its first
+// 16-byte boundary), nvb whole aligned vectors, and its tail (the fewer than V
+// elements after them).  Head and tail, ne = r - nvb*V <= 2V - 2 elements, are
+// held one element per lane in lanes 0 .. ne-1: lane l < head holds column l,
+// lane head <= l < ne holds column nvb*V + l.  y has x's layout, so the same
+// split addresses the output.
+// ---------------------------------------------------------------------------
+struct RagRow {
+    int head, nvb, ne;
+};
+
+template <int V>
+__device__ __forceinline__ RagRow rag_row(int64_t s0, int r) {
+    int head = (int)((V - (s0 & (V - 1))) & (V - 1));
+    if (head > r) head = r;
+    const int nvb = (r - head) / V;
+    return {head, nvb, r - nvb * V};
+}
+
+template <int V>
+__device__ __forceinline__ int rag_col(const RagRow &g, int lane) {
+    return lane < g.head ? lane : g.nvb * V + lane;
+}
+
+// The row's elements: vector c of lane l is whole vector c*S + l (S = lanes of the row: 64 for a wave,
+// the block size for a block), the lane's extra element as above.
+template <typename T, int V, int NV, int S>
+__device__ __forceinline__ void rag_load(const T *__restrict__ x, int64_t s0, const RagRow &g, int lane,
+                                         Vec<T, V> (&v)[NV], T &e) {
+    const T *p = x + s0 + g.head;
+#pragma unroll
+    for (int c = 0; c < NV; c++)
+        if (c * S + lane < g.nvb) v[c] = vload_nt<T, V>(p + (int64_t)(c * S + lane) * V);
+    if (lane < g.ne) e = x[s0 + rag_col<V>(g, lane)];
+}
+
+// x / scale or x * scale (the Div / Mul node), then + mask (the Add node), element by element.  A mask
+// row contiguous along the row is read by vectors when it is 16-byte aligned at the row's first whole
+// vector, by elements otherwise.
+template <typename T, int V, int NV, int S>
+__device__ __forceinline__ void rag_scale_mask(Vec<T, V> (&v)[NV], T &e, const RagRow &g, int lane, bool scaled,
+                                               bool smul, T sf, T sv, const T *m, int mask_inner) {
+    if (scaled) {
+#pragma unroll
+        for (int c = 0; c < NV; c++)
+            if (c * S + lane < g.nvb) {
+#pragma unroll
+                for (int k = 0; k < V; k++) v[c].v[k] = smul ? v[c].v[k] * sf : v[c].v[k] / sv;
+            }
+        e = smul ? e * sf : e / sv;
+    }
+    if (!m) return;
+    if (!mask_inner) {
+        const T m0 = m[0];
+#pragma unroll
+        for (int c = 0; c < NV; c++)
+            if (c * S + lane < g.nvb) {
+#pragma unroll
+                for (int k = 0; k < V; k++) v[c].v[k] = v[c].v[k] + m0;
+            }
+        e = e + m0;
+        return;
+    }
+    const T *mb = m + g.head;
+    const bool al = ((uintptr_t)mb & 15) == 0;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int vi = c * S + lane;
+        if (vi < g.nvb) {
+            Vec<T, V> mv;
+            if (al) {
+                mv = vload<T, V>(mb + (int64_t)vi * V);
+            } else {
+#pragma unroll
+                for (int k = 0; k < V; k++) mv.v[k] = mb[(int64_t)vi * V + k];
+            }
+#pragma unroll
+            for (int k = 0; k < V; k++) v[c].v[k] = v[c].v[k] + mv.v[k];
+        }
+    }
+    if (lane < g.ne) e = e + m[rag_col<V>(g, lane)];
+}
+
+// max (seed 0) of the lane's elements, their exponentials x - max in place and the lane's sum of them
+template <typename T, int V, int NV, int S>
+__device__ __forceinline__ T rag_lane_max(const Vec<T, V> (&v)[NV], T e, const RagRow &g, int lane) {
+    T mx = T(0);
+#pragma unroll
+    for (int c = 0; c < NV; c++)
+        if (c * S + lane < g.nvb) {
+#pragma unroll
+            for (int k = 0; k < V; k++) mx = row_max<T>(mx, v[c].v[k]);
+        }
+    if (lane < g.ne) mx = row_max<T>(mx, e);
+    return mx;
+}
+
+template <typename T, int V, int NV, int S>
+__device__ __forceinline__ T rag_lane_exp_sum(Vec<T, V> (&v)[NV], T &e, T mx, const RagRow &g, int lane,
+                                              const ExpTable &tab) {
+    T sum = T(0);
+#pragma unroll
+    for (int c = 0; c < NV; c++)
+        if (c * S + lane < g.nvb) {
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                v[c].v[k] = exp_elem<T>(v[c].v[k] - mx, tab);
+                sum = sum + v[c].v[k];
+            }
+        }
+    if (lane < g.ne) {
+        e = exp_elem<T>(e - mx, tab);
+        sum = sum + e;
+    }
+    return sum;
+}
+
+template <typename T, int V, int NV, int S>
+__device__ __forceinline__ void rag_store(T *__restrict__ y, int64_t s0, const RagRow &g, int lane,
+                                          const Vec<T, V> (&v)[NV], T e, T sum, T rs) {
+    T *q = y + s0 + g.head;
+#pragma unroll
+    for (int c = 0; c < NV; c++)
+        if (c * S + lane < g.nvb) {
+            Vec<T, V> o;
+#pragma unroll
+            for (int k = 0; k < V; k++) o.v[k] = div_row<T>(v[c].v[k], sum, rs);
+            vstore_nt<T, V>(q + (int64_t)(c * S + lane) * V, o);
+        }
+    if (lane < g.ne) y[s0 + rag_col<V>(g, lane)] = div_row<T>(e, sum, rs);
+}
+
+// Row per wave for rows whose length is not a multiple of V (or whose mask is not 16-byte aligned), up to
+// 64*V*NV + V - 1 elements: the walk of k_softmax_wave, rows split as above.
+template <typename T, int V, int NV, int NOUT>
+__global__ __launch_bounds__(kSBlock) void k_softmax_wave_rag(const T *__restrict__ x, T *__restrict__ y,
+                                                              int64_t rows, int r, const T *__restrict__ mask,
+                                                              int mask_inner, NdLayout mrows,
+                                                              const T *__restrict__ scale, int scale_div) {
+    __shared__ ExpTable tab;
+    if constexpr (std::is_same<T, float>::value) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    const int lane = threadIdx.x & 63;
+    const int64_t W = (int64_t)gridDim.x * (kSBlock / 64);
+    int64_t row = (int64_t)blockIdx.x * (kSBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (row >= rows) return;
+    const T sv = scale ? scale[0] : T(1);
+    T sf = sv;
+    const bool smul = !scale_div || exact_pow2_recip(sv, &sf);
+    Vec<T, V> cur[NV], nxt[NV];
+    T ecur = T(0), enxt = T(0);
+    RagRow gc = rag_row<V>(row * (int64_t)r, r), gn = gc;
+    rag_load<T, V, NV, 64>(x, row * (int64_t)r, gc, lane, cur, ecur);
+    for (; row < rows; row += W) {
+        const int64_t next = row + W, s0 = row * (int64_t)r;
+        if (next < rows) {
+            gn = rag_row<V>(next * (int64_t)r, r);
+            rag_load<T, V, NV, 64>(x, next * (int64_t)r, gn, lane, nxt, enxt);
+        }
+        const T *m = nullptr;
+        if constexpr (NOUT != 0) m = mask + mask_row_offset<NOUT>((uint32_t)row, mrows);
+        rag_scale_mask<T, V, NV, 64>(cur, ecur, gc, lane, scale != nullptr, smul, sf, sv, m, mask_inner);
+        T mx = rag_lane_max<T, V, NV, 64>(cur, ecur, gc, lane);
+        mx = row_reduce<T>(mx, [](T a, T b) { return row_max<T>(a, b); });
+        T sum = rag_lane_exp_sum<T, V, NV, 64>(cur, ecur, mx, gc, lane, tab);
+        sum = row_reduce<T>(sum, [](T a, T b) { return a + b; });
+        rag_store<T, V, NV, 64>(y, s0, gc, lane, cur, ecur, sum, T(1) / sum);
+#pragma unroll
+        for (int c = 0; c < NV; c++) cur[c] = nxt[c];
+        ecur = enxt;
+        gc = gn;
+    }
+}
+
+// max or sum over the block, the same value returned to every lane: the waves' values through LDS,
+// folded in wave order (deterministic)
+template <typename T, int B, typename F>
+__device__ __forceinline__ T block_allreduce(T v, T *red, F f) {
+    v = row_reduce<T>(v, f);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    T t = red[0];
+#pragma unroll
+    for (int w = 1; w < B / 64; w++) t = f(t, red[w]);
+    __syncthreads();  // red is written again by the next reduction
+    return t;
+}
+
+// inner == 1, rows longer than a wave holds (up to B*V*NV + V - 1 elements): one block of B lanes per row,
+// the row in registers, so x is read once and y written once; rows split as above.
+template <typename T, int V, int NV, int B, bool MASK>
+__global__ __launch_bounds__(B) void k_softmax_rows(const T *__restrict__ x, T *__restrict__ y, int64_t rows, int r,
+                                                    const T *__restrict__ mask, int mask_inner, NdLayout mrows,
+                                                    const T *__restrict__ scale, int scale_div) {
+    __shared__ ExpTable tab;
+    __shared__ T red[B / 64];
+    if constexpr (std::is_same<T, float>::value) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    const int tid = threadIdx.x;
+    const T sv = scale ? scale[0] : T(1);
+    T sf = sv;
+    const bool smul = !scale_div || exact_pow2_recip(sv, &sf);
+    for (int64_t row = blockIdx.x; row < rows; row += gridDim.x) {
+        const int64_t s0 = row * (int64_t)r;
+        const RagRow g = rag_row<V>(s0, r);
+        Vec<T, V> v[NV];
+        T e = T(0);
+        rag_load<T, V, NV, B>(x, s0, g, tid, v, e);
+        const T *m = nullptr;
+        if constexpr (MASK) m = mask + mask_row_offset<-1>((uint32_t)row, mrows);
+        rag_scale_mask<T, V, NV, B>(v, e, g, tid, scale != nullptr, smul, sf, sv, m, mask_inner);
+        T mx = rag_lane_max<T, V, NV, B>(v, e, g, tid);
+        mx = block_allreduce<T, B>(mx, red, [](T a, T b) { return row_max<T>(a, b); });
+        T sum = rag_lane_exp_sum<T, V, NV, B>(v, e, mx, g, tid, tab);
+        sum = block_allreduce<T, B>(sum, red, [](T a, T b) { return a + b; });
+        rag_store<T, V, NV, B>(y, s0, g, tid, v, e, sum, T(1) / sum);
+    }
+}
+
 // inner == 1, long rows: one block per row, three passes over the row.
 template <typename T>
 __global__ __launch_bounds__(kSBlock) void k_softmax_block(const T *__restrict__ x, T *__restrict__ y, int64_t r) {
@@ -305,16 +533,83 @@ static hipError_t softmax_wave_dispatch(const SoftmaxArgs &a, hipStream_t s) {
     }
 }
 
+template <typename T, int V, int NOUT>
+static hipError_t softmax_rag_launch(const SoftmaxArgs &a, hipStream_t s) {
+    const int r = (int)a.r;
+    int nv = (int)((r / V + 63) / 64);
+    if (nv < 1) nv = 1;
+    int64_t g = (a.outer + kSBlock / 64 - 1) / (kSBlock / 64);
+    if (g > kSoftmaxMaxBlocks) g = kSoftmaxMaxBlocks;
+    const T *x = (const T *)a.x;
+    T *y = (T *)a.y;
+    const T *m = (const T *)a.mask;
+#define LX_SMR_CASE(N)                                                                                             \
+    case N:                                                                                                        \
+        hipLaunchKernelGGL((k_softmax_wave_rag<T, V, N, NOUT>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, a.outer, \
+                           r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);                      \
+        break;
+    switch (nv) {
+        LX_SMR_CASE(1) LX_SMR_CASE(2) LX_SMR_CASE(3) LX_SMR_CASE(4) LX_SMR_CASE(5) LX_SMR_CASE(6) LX_SMR_CASE(7) LX_SMR_CASE(8)
+    default: return hipErrorInvalidValue;
+    }
+#undef LX_SMR_CASE
+    return hipGetLastError();
+}
+
+template <typename T, int V>
+static hipError_t softmax_rag_dispatch(const SoftmaxArgs &a, hipStream_t s) {
+    if (!a.mask) return softmax_rag_launch<T, V, 0>(a, s);
+    switch (a.mask_rows.nouter) {
+    case 1: return softmax_rag_launch<T, V, 1>(a, s);
+    case 2: return softmax_rag_launch<T, V, 2>(a, s);
+    case 3: return softmax_rag_launch<T, V, 3>(a, s);
+    default: return softmax_rag_launch<T, V, -1>(a, s);
+    }
+}
+
+template <typename T, int V, int NV, int B>
+static hipError_t softmax_rows_launch(const SoftmaxArgs &a, hipStream_t s) {
+    const int64_t g = a.outer < (1 << 20) ? a.outer : (1 << 20);
+    const T *x = (const T *)a.x;
+    T *y = (T *)a.y;
+    constexpr bool kMaskable = NV * V * (int)sizeof(T) <= 128;  // registers for the mask add
+    if (a.mask) {
+        if constexpr (kMaskable)
+            hipLaunchKernelGGL((k_softmax_rows<T, V, NV, B, true>), dim3((unsigned)g), dim3(B), 0, s, x, y, a.outer,
+                               (int)a.r, (const T *)a.mask, a.mask_inner, a.mask_rows, (const T *)a.scale,
+                               a.scale_div);
+        else
+            return hipErrorInvalidValue;
+    } else {
+        hipLaunchKernelGGL((k_softmax_rows<T, V, NV, B, false>), dim3((unsigned)g), dim3(B), 0, s, x, y, a.outer,
+                           (int)a.r, (const T *)nullptr, 0, a.mask_rows, (const T *)a.scale, a.scale_div);
+    }
+    return hipGetLastError();
+}
+
+// Whole 16-byte vectors a row-in-registers kernel holds at most: blocks of 1024 lanes with 16 vectors each
+// for float rows, 8 each for double rows and rows with a mask or scale (16 spill registers there).
+constexpr int64_t kSoftmaxRowVecs = 1024 * 16, kSoftmaxRowVecsMasked = 1024 * 8;
+
 template <typename T>
 static hipError_t softmax_typed(const SoftmaxArgs &a, hipStream_t s) {
     constexpr int VW = VecWidth<T>::value;
-    const bool wave_ok = a.inner == 1 && a.r <= 64 * VW * 8 && a.outer < (1ll << 31);
-    if (wave_ok) {
-        if (a.vec > 1 && a.r % VW == 0) {
-            if (a.mask) return softmax_wave_dispatch<T, VW, true>(a, s);
-            return softmax_wave_dispatch<T, VW, false>(a, s);
-        }
-        if (a.r <= 64 * 8) {
+    if (a.inner == 1 && a.outer < (1ll << 31)) {
+        if (a.vec > 1) {
+            // x and y 16-byte aligned: rows held in registers, 16-byte accesses
+            const int64_t nvr = a.r / VW;
+            const bool mask_al = !a.mask || !a.mask_inner || ((uintptr_t)a.mask & 15) == 0;
+            if (a.r % VW == 0 && mask_al && a.r <= 64 * VW * 8) {
+                if (a.mask) return softmax_wave_dispatch<T, VW, true>(a, s);
+                return softmax_wave_dispatch<T, VW, false>(a, s);
+            }
+            if (nvr <= 64 * 8) return softmax_rag_dispatch<T, VW>(a, s);
+            if (nvr <= 256 * 4) return softmax_rows_launch<T, VW, 4, 256>(a, s);
+            if (nvr <= 256 * 8) return softmax_rows_launch<T, VW, 8, 256>(a, s);
+            if (nvr <= kSoftmaxRowVecsMasked) return softmax_rows_launch<T, VW, 8, 1024>(a, s);
+            if constexpr (std::is_same<T, float>::value)
+                if (nvr <= kSoftmaxRowVecs && !a.mask && !a.scale) return softmax_rows_launch<T, VW, 16, 1024>(a, s);
+        } else if (a.r <= 64 * 8) {
             if (a.mask) return softmax_wave_dispatch<T, 1, true>(a, s);
             return softmax_wave_dispatch<T, 1, false>(a, s);
         }
@@ -336,8 +631,8 @@ static hipError_t softmax_typed(const SoftmaxArgs &a, hipStream_t s) {
 // True when launch_softmax can apply the mask inside the kernel.
 bool softmax_mask_fusable(int dtype, int64_t r, int64_t inner, int64_t outer, int vec) {
     const int vw = dtype == kFloat ? 4 : 2;
-    if (inner != 1 || outer >= (1ll << 31) || r > 64 * vw * 8) return false;
-    return (vec > 1 && r % vw == 0) || r <= 64 * 8;
+    if (inner != 1 || outer >= (1ll << 31)) return false;
+    return (vec > 1 && r / vw <= kSoftmaxRowVecsMasked) || r <= 64 * 8;
 }
 
 hipError_t launch_softmax(const SoftmaxArgs &a, hipStream_t s) {

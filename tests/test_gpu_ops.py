@@ -7,7 +7,9 @@ Bars (written per test):
   <= 2 ulp  : Pow with a non-2 exponent (device pow vs host powf)
   reductions: |gpu - ref| <= 1e-5 * sum|x| over the reduced slice (the
               reference folds serially; any parallel order differs)
-  softmax   : |gpu - ref| <= 1e-5 * |ref| (+1e-30 for underflowed entries)
+  softmax   : |gpu - ref| <= 1e-5 * |ref| (+1e-30 for underflowed entries); rows of any
+              length: + |ref - truth|, the reference's own rounding against float64 (its
+              serial sum of a long row is up to ~1e-4 relative away from the exact one)
 """
 import ctypes
 import json
@@ -647,6 +649,69 @@ def test_add_softmax_mask_rows_change_along_the_rows(hip, s_shape, m_shape):
     np.testing.assert_array_equal(np.isnan(got), nan)
     err = np.abs(got.astype(np.float64) - ref)[~nan]
     assert np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30), err.max()
+
+
+def softmax_close(got, ref, pre):
+    """got within 1e-5 * |ref| of the reference's Softmax of `pre` (the scores after any Div / Add node),
+    beyond the reference's own rounding: its serial float sum of a long row is up to ~1e-4 relative away
+    from the exact sum (8e-5 at 65535 N(0, 3) entries), which no other order of the sum can reproduce.  So
+    |got - ref| <= 1e-5 |ref| + |ref - truth|, truth being the same Softmax in float64 (seed-0 max, NaN rows
+    NaN): whatever the device gets within 1e-5 of the truth passes, and the bar is 1e-5 where the
+    reference's sum is exact enough."""
+    nan = np.isnan(ref)
+    np.testing.assert_array_equal(np.isnan(got), nan)
+    p = pre.astype(np.float64)
+    with np.errstate(all="ignore"):
+        m = np.fmax(np.max(np.where(np.isnan(p), -np.inf, p), -1, keepdims=True), 0.0)
+        e = np.exp(p - m)
+        truth = e / e.sum(-1, keepdims=True)
+    slack = np.abs(ref.astype(np.float64) - truth)
+    err = np.abs(got.astype(np.float64) - ref)
+    bad = ~nan & ~(err <= 1e-5 * np.abs(ref) + slack + 1e-30)
+    assert not bad.any(), (np.flatnonzero(bad)[:5], err[bad][:5], ref[bad][:5])
+
+
+SOFTMAX_ROW_LENGTHS = [1, 2, 3, 5, 7, 63, 65, 255, 257, 513, 1023, 2047, 2049, 2051, 2052, 4093, 4097, 8191, 8195,
+                       16389, 32767, 32771, 65535, 65539, 70001]
+
+
+@pytest.mark.parametrize("r", SOFTMAX_ROW_LENGTHS)
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_softmax_any_row_length(hip, r, dt):
+    """Rows of every length class: row per wave (whole vectors, or an unaligned head and a tail held one
+    element per lane), row per block in registers (256 or 1024 lanes, 4 to 16 vectors each), and the
+    three-pass kernel beyond.  Seven rows, so every head length 0..3 occurs; special values in the head,
+    the tail and the body."""
+    rng = np.random.default_rng(r)
+    x = (rng.standard_normal((7, r)) * 3).astype(dt)
+    if r >= 16:
+        x[1, 0] = np.nan                   # in the first row's head or first vector
+        x[2, r - 1] = np.inf               # in a tail: inf - inf = NaN
+        x[3, r - 2] = -np.inf              # exp(-inf) = 0
+        x[4, :] = -30000.0                 # below the seed 0: 0 / 0
+        x[5, r // 2] = 80.0                # one dominant entry
+    got = ok(HIP.Softmax(dev(x), -1))
+    softmax_close(got, O.softmax(x, -1), x)
+
+
+@pytest.mark.parametrize("r", [7, 70, 513, 1023, 2049, 4093, 9001, 32771])
+@pytest.mark.parametrize("dt", [np.float32, np.float64])
+def test_add_softmax_any_row_length(hip, r, dt):
+    """A mask row contiguous along the row whose rows start off 16-byte boundaries ([b, 1, 1, r] with r not
+    a multiple of 4: read by elements), a mask broadcast along the row ([b, h, q, 1]) and a scale, on every
+    row kernel: bit-identical to the Div / Add / Softmax nodes and within the bar of the oracle."""
+    rng = np.random.default_rng(r + 7)
+    q = 3
+    s = (rng.standard_normal((2, 3, q, r)) * 3).astype(dt)
+    for mshape in [(2, 1, 1, r), (2, 3, q, 1), (r,)]:
+        m = np.where(rng.uniform(size=mshape) < 0.125, -10000.0, rng.uniform(-1, 1, mshape)).astype(dt)
+        got = ok(HIP.AddSoftmax(dev(s), dev(m), -1))
+        softmax_close(got, O.add_softmax(s, m, -1), O.binary(O.ADD, s, m))
+        c = np.array(8.0, dt)
+        r2 = HIP.ScaleAddSoftmax(dev(s), dev(c), True, dev(m))
+        assert r2.Status == OpStatus.Success, r2.Message
+        t = HIP.Add(HIP.Div(dev(s), dev(c)).Outputs[0], dev(m)).Outputs[0]
+        assert_bits(r2.Outputs[0].to_numpy(), ok(HIP.Softmax(t, -1)))
 
 
 def test_device_reciprocal_is_correctly_rounded(hip):
