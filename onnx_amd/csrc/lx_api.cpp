@@ -573,6 +573,7 @@ int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
             if (p.b_strides[i] == 0) args.b_once = 0;
         }
         args.vec = (al && inner % V == 0) ? (int)V : 1;
+        args.rag = V > 1 && al && inner % V != 0 && p.numel < (1ll << 31);
         nd_layout(p, args.vec, args.nd, &args);
         break;
     }
@@ -698,7 +699,8 @@ int run_reduce(const char *opn, int op, const lx_tensor *X, const int64_t *axes,
         for (int i = gi + 1; i < (int)grps.size(); i++) ps.inner *= grps[i].size;
         ps.r = grps[gi].size;
         const int64_t V = 16 / es;
-        ps.vec = (src_aligned && ((ps.inner == 1 && ps.r % V == 0) || (ps.inner > 1 && ps.inner % V == 0))) ? (int)V : 1;
+        // rows (inner == 1) of any length: an unaligned head and a tail go element by element
+        ps.vec = (src_aligned && (ps.inner == 1 || ps.inner % V == 0)) ? (int)V : 1;
         ps.ws = reduce_workspace_bytes(dt, ps.outer, ps.r, ps.inner, ps.vec);
         ps.out_bytes = std::max<int64_t>(ps.outer * ps.inner * es, 16);
         passes.push_back(ps);

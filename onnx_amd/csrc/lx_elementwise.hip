@@ -401,6 +401,82 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd64(const T *__restrict__ a,
     }
 }
 
+// kNd outputs whose inner axis is not a multiple of V (every pointer 16-byte aligned, n < 2^31): the
+// output is walked in whole 16-byte vectors of its flat index.  An operand without broadcast axes has the
+// output's layout and is read by vectors at the same flat index (flat = 1); a broadcast operand element by
+// element: the vector's first element decomposed into (row, column), the next ones stepped along the row,
+// the row's operand offsets decomposed again where the vector crosses into the next row.  The n mod V
+// last elements are taken by lanes of block 0.  L.inner_v holds the inner length in elements.
+template <int OP, typename T, int AIN, int BIN, int V>
+__global__ __launch_bounds__(kBlock) void k_binary_rag(const T *__restrict__ a, const T *__restrict__ b,
+                                                       T *__restrict__ y, uint32_t nvec, uint32_t n, NdLayout L,
+                                                       int a_flat, int b_flat, ErrFlags *errs) {
+    const uint32_t inner = L.inner_v.d;
+    auto offsets = [&](uint32_t row, int64_t &ao, int64_t &bo) {
+        ao = 0;
+        bo = 0;
+#pragma unroll
+        for (int d = 0; d < kMaxOuter; d++) {
+            if (d < L.nouter) {
+                const uint32_t q = fdiv(row, L.odiv[d]);
+                const uint32_t id = row - q * L.odiv[d].d;
+                ao += (int64_t)id * L.a_str[d];
+                bo += (int64_t)id * L.b_str[d];
+                row = q;
+            }
+        }
+    };
+    for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < nvec; v += gridDim.x * kBlock) {
+        const uint32_t f = v * V;
+        Vec<T, V> va, vb;
+        if (a_flat) va = vload_nt<T, V>(a + f);
+        if (b_flat) vb = vload_nt<T, V>(b + f);
+        if (!a_flat || !b_flat) {
+            uint32_t row = fdiv(f, L.inner_v);
+            uint32_t col = f - row * inner;
+            int64_t ao, bo;
+            offsets(row, ao, bo);
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                if (!a_flat) va.v[k] = AIN ? a[ao + col] : a[ao];
+                if (!b_flat) vb.v[k] = BIN ? b[bo + col] : b[bo];
+                if (++col == inner) {
+                    col = 0;
+                    offsets(++row, ao, bo);
+                }
+            }
+        }
+        vstore_nt<T, V>(y + f, bin_apply_vec<OP, T, V>(va, vb, (uint64_t)f, errs));
+    }
+    const uint32_t done = nvec * V;
+    if (blockIdx.x == 0 && threadIdx.x < n - done) {
+        const uint32_t f = done + threadIdx.x;
+        const uint32_t row = fdiv(f, L.inner_v), col = f - row * inner;
+        int64_t ao, bo;
+        offsets(row, ao, bo);
+        const T l = a_flat ? a[f] : (AIN ? a[ao + col] : a[ao]);
+        const T r = b_flat ? b[f] : (BIN ? b[bo + col] : b[bo]);
+        y[f] = bin_apply<OP, T>(l, r, (uint64_t)f, errs);
+    }
+}
+
+template <int OP, typename T>
+static hipError_t binary_rag(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
+    constexpr int V = VecWidth<T>::value;
+    const T *a = (const T *)A.a;
+    const T *b = (const T *)A.b;
+    T *y = (T *)A.y;
+    const uint32_t n = (uint32_t)A.n, nvec = n / V;
+    const int g = grid_for(nvec > 0 ? nvec : 1, kBlock);
+    switch (A.a_inner * 2 + A.b_inner) {
+    case 3: hipLaunchKernelGGL((k_binary_rag<OP, T, 1, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nvec, n, A.nd, A.a_once, A.b_once, errs); break;
+    case 2: hipLaunchKernelGGL((k_binary_rag<OP, T, 1, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nvec, n, A.nd, A.a_once, A.b_once, errs); break;
+    case 1: hipLaunchKernelGGL((k_binary_rag<OP, T, 0, 1, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nvec, n, A.nd, A.a_once, A.b_once, errs); break;
+    default: hipLaunchKernelGGL((k_binary_rag<OP, T, 0, 0, V>), dim3(g), dim3(kBlock), 0, s, a, b, y, nvec, n, A.nd, A.a_once, A.b_once, errs); break;
+    }
+    return hipGetLastError();
+}
+
 template <int OP, typename T, int V>
 static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
     const T *a = (const T *)A.a;
@@ -468,6 +544,7 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
 
 template <int OP, typename T>
 static hipError_t binary_typed(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
+    if (A.layout == kNd && A.rag) return binary_rag<OP, T>(A, errs, s);
     if (A.vec > 1) return binary_typed_v<OP, T, VecWidth<T>::value>(A, errs, s);
     return binary_typed_v<OP, T, 1>(A, errs, s);
 }

@@ -40,6 +40,8 @@ struct BinArgs {
     int a_inner, b_inner;   // kNd: 1 = contiguous innermost axis, 0 = broadcast
     int a_once, b_once;     // kNd: operand has no broadcast axis (read once: streamed)
     int vec;                // 1 = scalar element access, else 16-byte vectors
+    int rag;                // kNd, inner axis not a multiple of the vector width, every pointer 16-byte
+                            // aligned, fewer than 2^31 elements: output by 16-byte vectors of the flat index
     const void *a;
     const void *b;
     void *y;

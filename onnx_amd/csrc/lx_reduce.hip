@@ -74,6 +74,15 @@ __device__ __forceinline__ typename Red<OP, T>::A block_reduce(typename Red<OP, 
     return t;  // valid in thread 0
 }
 
+// A row of r elements starting at element s0 of a 16-byte aligned x, read with whole aligned vectors: its
+// head (the (-s0) mod V elements before the first 16-byte boundary), nv vectors, and its tail (the fewer
+// than V elements after them).  Rows whose length is a multiple of V start aligned (head and tail empty).
+template <int V>
+__device__ __forceinline__ int64_t row_head(int64_t s0, int64_t r) {
+    const int64_t h = (V - (s0 & (V - 1))) & (V - 1);
+    return h < r ? h : r;
+}
+
 // inner == 1, one wave per row.
 template <int OP, typename T, int V>
 __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
@@ -84,9 +93,15 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
     // the wave's index from lane 0: the row's address arithmetic runs once per wave on the scalar unit
     const int64_t row = (int64_t)blockIdx.x * (kRBlock / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     if (row >= rows) return;
-    const T *p = x + row * r;
+    const int64_t s0 = row * r, head = row_head<V>(s0, r);
+    const T *p = x + s0 + head;
     A acc = RD::ident();
-    const int64_t nv = r / V;
+    const int64_t nv = (r - head) / V;
+    // the head and tail elements (fewer than 2V, lane l < head column l, lane head <= l < ne column nv*V + l),
+    // loaded before the vectors so the row costs one memory round trip
+    const bool has_e = lane < r - nv * V;
+    T xe = T(0);
+    if (has_e) xe = x[s0 + (lane < head ? lane : nv * V + lane)];
     int64_t j = lane;
     for (; j + 64 * 3 < nv; j += 64 * 4) {
         Vec<T, V> v0 = vload_nt<T, V>(p + j * V);
@@ -107,7 +122,7 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
 #pragma unroll
         for (int k = 0; k < V; k++) acc = RD::comb(acc, RD::load(v0.v[k], pre, R));
     }
-    for (int64_t t = nv * V + lane; t < r; t += 64) acc = RD::comb(acc, RD::load(p[t], pre, R));
+    if (has_e) acc = RD::comb(acc, RD::load(xe, pre, R));
     acc = wave_reduce(acc, [](A a, A b) { return RD::comb(a, b); });
     if (lane == 0) y[row] = RD::fin(acc, post, R);
 }
@@ -126,8 +141,9 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restri
     constexpr int64_t kTile = 4 * kRBlock;
     const int64_t row = blockIdx.y;
     const int c = blockIdx.x;
-    const T *p = x + row * r;
-    const int64_t nv = r / V;  // r % V == 0 whenever V > 1
+    const int64_t s0 = row * r, head = row_head<V>(s0, r);
+    const T *p = x + s0 + head;
+    const int64_t nv = (r - head) / V;
     const int64_t step = (int64_t)nchunks * kTile;
     // one accumulator per vector component: V independent chains of four combines per tile instead of one
     // chain of 4 V, so the adds of a tile finish before the next tile's loads return
@@ -157,6 +173,9 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_split(const T *__restri
     A acc = accv[0];
 #pragma unroll
     for (int k = 1; k < V; k++) acc = RD::comb(acc, accv[k]);
+    // block 0 takes the head and the tail elements (fewer than 2V): lane l < head column l, lane
+    // head <= l < ne column nv*V + l
+    if (c == 0 && threadIdx.x < r - nv * V) acc = RD::comb(acc, RD::load(x[s0 + (threadIdx.x < head ? threadIdx.x : nv * V + threadIdx.x)], pre, R));
     acc = block_reduce<OP, T>(acc);
     if (nchunks == 1) {
         if (threadIdx.x == 0) y[row] = RD::fin(acc, post, R);
@@ -325,10 +344,13 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
         return p;
     }
     const int64_t inner_v = inner / V > 0 ? inner / V : 1;
-    // at most 32 column vectors per tile, so a wave covers two rows (C4's int64 [64,256,4096] axis 1:
-    // 96 -> 82 us against 64-wide tiles; C5's float [256,4096,256]: 164 -> 158 us; 16-wide tiles slow C5)
+    // at most 512 bytes of a row per tile: 32 column vectors of 16 bytes, so a wave covers two rows (C4's
+    // int64 [64,256,4096] axis 1: 96 -> 82 us against 64-wide tiles; C5's float [256,4096,256]: 164 -> 158
+    // us; 16-wide tiles slow C5).  Single elements (an inner axis that is not a multiple of the vector
+    // width): 1 KB of a row per tile, 256 floats ([4128,255,255] axis 1: 271 us with 128-float tiles, 217)
+    const int ct_max = V == 1 ? 1024 / (int)sizeof(A) : 512 / (V * (int)sizeof(A));
     int ct = 1;
-    while (ct < 32 && ct < inner_v) ct <<= 1;
+    while (ct < ct_max && ct < inner_v) ct <<= 1;
     const int64_t tiles = ceil_div(inner_v, ct);
     const int64_t base = tiles * outer;
     const int nrs = kRBlock / ct;
@@ -367,7 +389,9 @@ static hipError_t reduce_typed_v(const ReduceArgs &a, hipStream_t s) {
                                p.nchunks, a.post_div, a.r_total);
     } else {
         const int64_t tiles = ceil_div(a.inner / V, p.ct);
-        hipLaunchKernelGGL((k_reduce_cols<OP, T, V, kColsUnroll>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
+        // the same bytes in flight per lane for every vector width: 8 rows of 16-byte vectors, 32 of floats
+        constexpr int UN = kColsUnroll * VecWidth<T>::value / V;
+        hipLaunchKernelGGL((k_reduce_cols<OP, T, V, UN>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
                            dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rsplit, a.pre_div,
                            a.post_div, a.r_total);
         if (p.rsplit > 1) {

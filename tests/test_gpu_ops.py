@@ -135,6 +135,37 @@ def test_int64_div_large_operands(hip):
     assert_bits(ok(HIP.Div(dev(a), dev(b))), O.binary(O.DIV, a, b))
 
 
+RAGGED_BINARY_SHAPES = [((262, 1023), (1023,)), ((262, 1023), (262, 1)), ((5, 1, 1023), (1, 7, 1023)),
+                        ((9, 3), (4, 9, 3)), ((2, 3, 5, 1), (1, 1, 5, 7)), ((4001,), (1,)), ((33, 17), (17,)),
+                        ((64, 1, 4095), (1, 256, 4095))]
+
+
+@pytest.mark.parametrize("sa,sb", RAGGED_BINARY_SHAPES)
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.uint8, np.int32, np.int64])
+def test_binary_ragged_inner_axis(hip, sa, sb, dt):
+    """Broadcast outputs whose inner axis is not a multiple of the vector width: whole 16-byte output
+    vectors over the flat index, an operand of the output's shape read by vectors, a broadcast operand
+    element by element across row boundaries (inner axes of 3 and 7 cross several per vector).  Bit-exact
+    for all four ops; integer Div with a zero divisor reports DivideByZero as the reference does."""
+    rng = np.random.default_rng(len(sa) * 100 + sa[-1])
+    if np.dtype(dt).kind == "f":
+        a, b = rng.standard_normal(sa).astype(dt), rng.standard_normal(sb).astype(dt)
+    else:
+        info = np.iinfo(dt)
+        a = rng.integers(info.min, info.max, sa, dtype=dt, endpoint=True)
+        b = rng.integers(1 if dt == np.uint8 else -1000, 1000, sb).astype(dt)
+        b[b == 0] = 3
+        if dt != np.uint8:
+            b[b == -1] = 5
+    for op, code in [("Add", O.ADD), ("Sub", O.SUB), ("Mul", O.MUL), ("Div", O.DIV)]:
+        assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
+    if np.dtype(dt).kind != "f" and b.size > 1:
+        b0 = b.copy()
+        b0.reshape(-1)[b0.size // 2] = 0
+        r = HIP.Div(dev(a), dev(b0))
+        assert r.Status == OpStatus.Failure and r.Code == L.ERR_DIVIDE_BY_ZERO
+
+
 @pytest.mark.parametrize("dt", [np.int32, np.int64])
 def test_int_div_reused_divisor(hip, dt):
     """Broadcast and scalar divisors, all magnitudes: bit-exact quotients,
@@ -561,6 +592,38 @@ def test_reduce_double(hip):
         got = ok(getattr(HIP, name)(dev(x), [1]))
         ref = O.reduce(code, x, [1], True)
         np.testing.assert_allclose(got, ref, rtol=0, atol=1e-12)
+
+
+RAGGED_REDUCE_CASES = [
+    ((7, 1), [-1]), ((7, 3), [-1]), ((7, 5), [-1]), ((9, 63), [-1]), ((9, 65), [-1]), ((9, 1023), [-1]),
+    ((5, 8191), [-1]), ((3, 8193), [-1]), ((3, 100003), [-1]),   # row per wave, split rows (r > 8192)
+    ((1000001,), None), ((3000003,), None), ((2, 3, 1000001), None),  # whole tensors not a multiple of 4
+    ((5, 1000, 255), [1]), ((3, 77, 49), [1]), ((2, 3001, 7), [1]), ((64, 3, 1022), [1]),  # inner not % 4
+]
+
+
+@pytest.mark.parametrize("shape,axes", RAGGED_REDUCE_CASES)
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64])
+def test_reduce_ragged_rows_and_columns(hip, shape, axes, dt):
+    """Rows whose length is not a multiple of the vector width (an unaligned head and a tail read element
+    by element around whole 16-byte vectors; several rows, so every head length occurs), whole tensors of
+    such sizes (the split row kernel), and column reductions over an inner axis of such a width."""
+    rng = np.random.default_rng(sum(shape))
+    if np.dtype(dt).kind == "f":
+        x = rng.uniform(-1, 1, shape).astype(dt)
+    else:
+        x = rng.integers(-(2**20), 2**20, shape).astype(dt)
+    ax = tuple(range(len(shape))) if axes is None else tuple(a % len(shape) for a in axes)
+    absum = np.abs(x.astype(np.float64)).sum(axis=ax, keepdims=True)
+    names = [("ReduceSum", O.RSUM), ("ReduceMean", O.RMEAN)] + ([("ReduceMax", O.RMAX)] if np.dtype(dt).kind == "f" else [])
+    for name, code in names:
+        got = ok(getattr(HIP, name)(dev(x), axes, 1))
+        ref = O.reduce(code, x, axes, True)
+        if name == "ReduceMax" or np.dtype(dt).kind != "f":
+            assert_bits(got, ref)
+        else:
+            r = int(np.prod([shape[a] for a in ax]))
+            assert_reduction(got, ref, absum / (r if name == "ReduceMean" else 1))
 
 
 def test_reduce_max_seed_zero_and_nan(hip):
