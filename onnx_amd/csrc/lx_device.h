@@ -8,6 +8,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "lx_plan.h"
 
 #pragma clang fp contract(off)
@@ -134,6 +136,31 @@ __device__ __forceinline__ float wave_reduce_dpp(float v, F f) {
     const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
     const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
     return f(f(r0, r1), f(r2, r3));
+}
+
+// Reduction within aligned groups of L lanes (L a power of two, at most 64): every lane of a group ends
+// with the group's value.  Float over DPP for the steps inside a 16-lane row -- quad_perm [1,0,3,2] and
+// [2,3,0,1], then row_half_mirror and row_mirror, each combining two halves that already hold their own
+// values, so with a commutative f every lane gets the same result -- and a shuffle across rows for L = 32;
+// other types over the shuffle butterfly; the whole wave as wave_reduce_dpp / wave_reduce.  A fixed order:
+// deterministic.
+template <int L, typename T, typename F>
+__device__ __forceinline__ T group_reduce(T v, F f) {
+    static_assert(L >= 1 && L <= 64 && (L & (L - 1)) == 0, "groups of 1 to 64 lanes");
+    if constexpr (L == 64) {
+        if constexpr (std::is_same<T, float>::value) return wave_reduce_dpp(v, f);
+        else return wave_reduce(v, f);
+    } else if constexpr (std::is_same<T, float>::value) {
+        if constexpr (L >= 2) v = f(v, dpp_move<0xb1>(v));
+        if constexpr (L >= 4) v = f(v, dpp_move<0x4e>(v));
+        if constexpr (L >= 8) v = f(v, dpp_move<0x141>(v));
+        if constexpr (L >= 16) v = f(v, dpp_move<0x140>(v));
+        if constexpr (L >= 32) v = f(v, __shfl_xor(v, 16, 64));
+    } else {
+#pragma unroll
+        for (int off = L / 2; off >= 1; off >>= 1) v = f(v, __shfl_xor(v, off, 64));
+    }
+    return v;
 }
 
 // ---------------------------------------------------------------------------

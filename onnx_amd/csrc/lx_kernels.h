@@ -131,7 +131,8 @@ struct SoftmaxArgs {
 hipError_t launch_softmax(const SoftmaxArgs &args, hipStream_t s);
 bool softmax_mask_fusable(int dtype, int64_t r, int64_t inner, int64_t outer, int vec);
 
-// LayerNorm decomposed into its ONNX nodes, rows of length r (r % 4 == 0, r <= 4096).
+// LayerNorm decomposed into its ONNX nodes, rows of length r (1 <= r <= 4099; x, gamma, beta, y 16-byte
+// aligned).
 hipError_t launch_layernorm(const float *x, const float *gamma, const float *beta, float eps, float *y,
                             int64_t rows, int64_t r, hipStream_t s);
 bool layernorm_supported(int64_t r);

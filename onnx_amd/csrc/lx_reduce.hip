@@ -127,6 +127,54 @@ __global__ __launch_bounds__(kRBlock) void k_reduce_rows_wave(const T *__restric
     if (lane == 0) y[row] = RD::fin(acc, post, R);
 }
 
+// inner == 1, short rows (at most 64 whole vectors plus head and tail): L lanes per row (a power of two),
+// 64 / L rows per wave at a time, two rows per group in flight; the row split of k_reduce_rows_wave
+// within each group of L lanes.
+template <int OP, typename T, int V, int L>
+__global__ __launch_bounds__(kRBlock) void k_reduce_rows_group(const T *__restrict__ x, T *__restrict__ y,
+                                                               int64_t rows, int64_t r, int pre, int post,
+                                                               int64_t R) {
+    using RD = Red<OP, T>;
+    using A = typename RD::A;
+    constexpr int RW = 64 / L;
+    const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+    const int64_t W = (int64_t)gridDim.x * (kRBlock / 64) * RW;
+    int64_t row = ((int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6)) * RW + lane / L;
+    // one row's whole vector (lane gl < nv) and extra element (gl < r - nv*V) of this lane
+    auto load = [&](int64_t rw, Vec<T, V> &v, T &e, bool &hv, bool &he) {
+        const int64_t s0 = rw * r, head = row_head<V>(s0, r), nv = (r - head) / V;
+        hv = gl < nv;
+        he = gl < r - nv * V;
+        if (hv) v = vload_nt<T, V>(x + s0 + head + (int64_t)gl * V);
+        if (he) e = x[s0 + (gl < head ? gl : nv * V + gl)];
+    };
+    for (; row < rows; row += 2 * W) {
+        const int64_t row2 = row + W;
+        Vec<T, V> v0, v1;
+        T e0 = T(0), e1 = T(0);
+        bool hv0, he0, hv1 = false, he1 = false;
+        load(row, v0, e0, hv0, he0);
+        if (row2 < rows) load(row2, v1, e1, hv1, he1);
+        A a0 = RD::ident(), a1 = RD::ident();
+        if (hv0) {
+#pragma unroll
+            for (int k = 0; k < V; k++) a0 = RD::comb(a0, RD::load(v0.v[k], pre, R));
+        }
+        if (he0) a0 = RD::comb(a0, RD::load(e0, pre, R));
+        if (hv1) {
+#pragma unroll
+            for (int k = 0; k < V; k++) a1 = RD::comb(a1, RD::load(v1.v[k], pre, R));
+        }
+        if (he1) a1 = RD::comb(a1, RD::load(e1, pre, R));
+        a0 = group_reduce<L>(a0, [](A p, A q) { return RD::comb(p, q); });
+        a1 = group_reduce<L>(a1, [](A p, A q) { return RD::comb(p, q); });
+        if (gl == 0) {
+            y[row] = RD::fin(a0, post, R);
+            if (row2 < rows) y[row2] = RD::fin(a1, post, R);
+        }
+    }
+}
+
 // inner == 1, long rows: grid (nchunks, rows).  The row is cut into tiles of
 // 4 x 256 vectors; block c takes tiles c, c + nchunks, ... and each lane loads
 // the 4 vectors t, t+256, t+512, t+768 of a tile together, so at any moment
@@ -378,6 +426,27 @@ static hipError_t reduce_typed_v(const ReduceArgs &a, hipStream_t s) {
     if (p.ws > a.ws_bytes) return hipErrorInvalidValue;
     A *ws = (A *)a.workspace;
     if (p.kind == 0) {
+        // short rows: L lanes per row, enough for its whole vectors and its head and tail elements (none
+        // when r is a multiple of V: every row then starts aligned)
+        const int64_t ne_max = a.r % V == 0 ? 0 : (a.r < 2 * V - 2 ? a.r : 2 * V - 2);
+        int L = 1;
+        while (L < a.r / V || L < ne_max) L <<= 1;
+        if (L <= 64) {
+            const int64_t per_block = (int64_t)(kRBlock / 64) * (64 / L) * 2;
+            int64_t g = ceil_div(a.outer, per_block);
+            if (g > (1 << 20)) g = 1 << 20;
+#define LX_RG_CASE(N)                                                                                           \
+    case N:                                                                                                     \
+        hipLaunchKernelGGL((k_reduce_rows_group<OP, T, V, N>), dim3((unsigned)g), dim3(kRBlock), 0, s, x, y, a.outer, \
+                           a.r, a.pre_div, a.post_div, a.r_total);                                              \
+        break;
+            switch (L) {
+                LX_RG_CASE(1) LX_RG_CASE(2) LX_RG_CASE(4) LX_RG_CASE(8) LX_RG_CASE(16) LX_RG_CASE(32) LX_RG_CASE(64)
+            default: return hipErrorInvalidValue;
+            }
+#undef LX_RG_CASE
+            return hipGetLastError();
+        }
         int g = (int)ceil_div(a.outer, kRBlock / 64);
         hipLaunchKernelGGL((k_reduce_rows_wave<OP, T, V>), dim3(g), dim3(kRBlock), 0, s, x, y, a.outer, a.r,
                            a.pre_div, a.post_div, a.r_total);
@@ -519,15 +588,146 @@ __global__ __launch_bounds__(kLnBlock) void k_layernorm(const float *__restrict_
     }
 }
 
-bool layernorm_supported(int64_t r) { return r >= 4 && r <= 4096 && (r % 4) == 0; }
+template <int L>
+__device__ __forceinline__ float lanes_sum(float v) {
+    if constexpr (L == 64) return wave_reduce_dpp(v, [](float a, float b) { return a + b; });
+    else return group_reduce<L>(v, [](float a, float b) { return a + b; });
+}
+
+// LayerNorm rows of any length up to 256 NV + 3 and short rows: L lanes per row (64 / L rows per wave at
+// a time), the row split into an unaligned head, whole 16-byte vectors and a tail (head and tail one
+// element per lane: lane l < head column l, lane head <= l < ne column nv*4 + l), the same node-by-node
+// rounding as k_layernorm.  gamma and beta are read by vectors where the row's first whole vector falls
+// on a 16-byte boundary of the row (head 0, as every row when r is a multiple of 4), element by element
+// otherwise.
+template <int NV, int L>
+__global__ __launch_bounds__(kRBlock) void k_layernorm_rag(const float *__restrict__ x,
+                                                           const float *__restrict__ gamma,
+                                                           const float *__restrict__ beta, float eps,
+                                                           float *__restrict__ y, int64_t rows, int r) {
+    constexpr int RW = 64 / L;
+    const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+    const int64_t W = (int64_t)gridDim.x * (kRBlock / 64) * RW;
+    for (int64_t row = ((int64_t)blockIdx.x * (kRBlock / 64) + (threadIdx.x >> 6)) * RW + lane / L; row < rows;
+         row += W) {
+        const int64_t s0 = row * (int64_t)r;
+        const int head = (int)row_head<4>(s0, r);
+        const int nv = (r - head) / 4, ne = r - nv * 4;
+        const bool he = gl < ne;
+        const int ec = gl < head ? gl : nv * 4 + gl;
+        const float *p = x + s0 + head;
+        Vec<float, 4> v[NV];
+        float e = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NV; c++)
+            if (c * L + gl < nv) v[c] = vload_nt<float, 4>(p + (c * L + gl) * 4);
+        if (he) e = x[s0 + ec];
+        float s = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NV; c++)
+            if (c * L + gl < nv) s = s + ((v[c].v[0] + v[c].v[1]) + (v[c].v[2] + v[c].v[3]));
+        if (he) s = s + e;
+        s = lanes_sum<L>(s);
+        const float fr = (float)r;
+        const float mean = s / fr;
+        float s2 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            if (c * L + gl < nv) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) v[c].v[k] = v[c].v[k] - mean;
+                float p0 = v[c].v[0] * v[c].v[0], p1 = v[c].v[1] * v[c].v[1];
+                float p2 = v[c].v[2] * v[c].v[2], p3 = v[c].v[3] * v[c].v[3];
+                s2 = s2 + ((p0 + p1) + (p2 + p3));
+            }
+        }
+        if (he) {
+            e = e - mean;
+            s2 = s2 + e * e;
+        }
+        s2 = lanes_sum<L>(s2);
+        const float var = s2 / fr;
+        const float ve = var + eps;
+        const float sd = __builtin_sqrtf(ve);
+        const float rsd = 1.0f / sd;
+        float *q = y + s0 + head;
+        const float *ga = gamma + head, *be = beta + head;
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const int vi = c * L + gl;
+            if (vi < nv) {
+                Vec<float, 4> g, b, o;
+                if (head == 0) {
+                    g = vload<float, 4>(ga + vi * 4);
+                    b = vload<float, 4>(be + vi * 4);
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) {
+                        g.v[k] = ga[vi * 4 + k];
+                        b.v[k] = be[vi * 4 + k];
+                    }
+                }
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    float nrm = div_by_row_lx(v[c].v[k], sd, rsd);
+                    float m = nrm * g.v[k];
+                    o.v[k] = m + b.v[k];
+                }
+                vstore_nt<float, 4>(q + vi * 4, o);
+            }
+        }
+        if (he) {
+            float nrm = div_by_row_lx(e, sd, rsd);
+            float m = nrm * gamma[ec];
+            y[s0 + ec] = m + beta[ec];
+        }
+    }
+}
+
+// Rows of 1 to 4099 elements (whole vectors of at most 16 per lane of a wave, plus head and tail).
+bool layernorm_supported(int64_t r) { return r >= 1 && r / 4 <= 1024; }
+
+template <int NV, int L>
+static void launch_layernorm_rag(const float *x, const float *gamma, const float *beta, float eps, float *y,
+                                 int64_t rows, int r, hipStream_t s) {
+    int64_t g = ceil_div(rows, (int64_t)(kRBlock / 64) * (64 / L));
+    if (g > (1 << 20)) g = 1 << 20;
+    hipLaunchKernelGGL((k_layernorm_rag<NV, L>), dim3((unsigned)g), dim3(kRBlock), 0, s, x, gamma, beta, eps, y, rows,
+                       r);
+}
 
 hipError_t launch_layernorm(const float *x, const float *gamma, const float *beta, float eps, float *y, int64_t rows,
                             int64_t r, hipStream_t s) {
     if (rows == 0) return hipSuccess;
     if (!layernorm_supported(r)) return hipErrorInvalidValue;
+    const int ri = (int)r;
+    if (r % 4 != 0 || r < 256) {
+        // short rows: L lanes per row; other rows of any length: a wave per row
+        const int64_t ne_max = r % 4 == 0 ? 0 : (r < 6 ? r : 6);
+        int L = 1;
+        while (L < r / 4 || L < ne_max) L <<= 1;
+        switch (L) {
+        case 1: launch_layernorm_rag<1, 1>(x, gamma, beta, eps, y, rows, ri, s); break;
+        case 2: launch_layernorm_rag<1, 2>(x, gamma, beta, eps, y, rows, ri, s); break;
+        case 4: launch_layernorm_rag<1, 4>(x, gamma, beta, eps, y, rows, ri, s); break;
+        case 8: launch_layernorm_rag<1, 8>(x, gamma, beta, eps, y, rows, ri, s); break;
+        case 16: launch_layernorm_rag<1, 16>(x, gamma, beta, eps, y, rows, ri, s); break;
+        case 32: launch_layernorm_rag<1, 32>(x, gamma, beta, eps, y, rows, ri, s); break;
+        default: {
+            const int nvw = (int)ceil_div(r / 4, 64);
+            switch (nvw) {
+            case 1: launch_layernorm_rag<1, 64>(x, gamma, beta, eps, y, rows, ri, s); break;
+            case 2: launch_layernorm_rag<2, 64>(x, gamma, beta, eps, y, rows, ri, s); break;
+            case 3: case 4: launch_layernorm_rag<4, 64>(x, gamma, beta, eps, y, rows, ri, s); break;
+            case 5: case 6: case 7: case 8: launch_layernorm_rag<8, 64>(x, gamma, beta, eps, y, rows, ri, s); break;
+            default: launch_layernorm_rag<16, 64>(x, gamma, beta, eps, y, rows, ri, s); break;
+            }
+        }
+        }
+        return hipGetLastError();
+    }
     const int nv = (int)ceil_div(r, 256);
     const int g = (int)ceil_div(rows, kLnBlock / 64);
-    const int ri = (int)r;
 #define LX_LN_CASE(N) \
     case N: hipLaunchKernelGGL((k_layernorm<N>), dim3(g), dim3(kLnBlock), 0, s, x, gamma, beta, eps, y, rows, ri); break;
     switch (nv) {

@@ -395,6 +395,52 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave_rag(const T *__restric
     }
 }
 
+// Short rows (at most 32 whole vectors plus head and tail): L lanes per row (a power of two below 64),
+// 64 / L rows per wave at a time, where one row per wave would leave most lanes idle.  Each group of L
+// lanes walks its rows like the wave of k_softmax_wave_rag (next row loaded while the current one is
+// finished), with the same row split, scale and mask.
+template <typename T, int V, int L, int NOUT>
+__global__ __launch_bounds__(kSBlock) void k_softmax_group(const T *__restrict__ x, T *__restrict__ y,
+                                                           int64_t rows, int r, const T *__restrict__ mask,
+                                                           int mask_inner, NdLayout mrows,
+                                                           const T *__restrict__ scale, int scale_div) {
+    __shared__ ExpTable tab;
+    if constexpr (std::is_same<T, float>::value) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    constexpr int RW = 64 / L;  // rows per wave
+    const int lane = threadIdx.x & 63, gl = lane & (L - 1);
+    const int64_t W = (int64_t)gridDim.x * (kSBlock / 64) * RW;
+    int64_t row = ((int64_t)blockIdx.x * (kSBlock / 64) + (threadIdx.x >> 6)) * RW + lane / L;
+    if (row >= rows) return;
+    const T sv = scale ? scale[0] : T(1);
+    T sf = sv;
+    const bool smul = !scale_div || exact_pow2_recip(sv, &sf);
+    Vec<T, V> cur[1], nxt[1];
+    T ecur = T(0), enxt = T(0);
+    RagRow gc = rag_row<V>(row * (int64_t)r, r), gn = gc;
+    rag_load<T, V, 1, L>(x, row * (int64_t)r, gc, gl, cur, ecur);
+    for (; row < rows; row += W) {
+        const int64_t next = row + W, s0 = row * (int64_t)r;
+        if (next < rows) {
+            gn = rag_row<V>(next * (int64_t)r, r);
+            rag_load<T, V, 1, L>(x, next * (int64_t)r, gn, gl, nxt, enxt);
+        }
+        const T *m = nullptr;
+        if constexpr (NOUT != 0) m = mask + mask_row_offset<NOUT>((uint32_t)row, mrows);
+        rag_scale_mask<T, V, 1, L>(cur, ecur, gc, gl, scale != nullptr, smul, sf, sv, m, mask_inner);
+        T mx = rag_lane_max<T, V, 1, L>(cur, ecur, gc, gl);
+        mx = group_reduce<L>(mx, [](T a, T b) { return row_max<T>(a, b); });
+        T sum = rag_lane_exp_sum<T, V, 1, L>(cur, ecur, mx, gc, gl, tab);
+        sum = group_reduce<L>(sum, [](T a, T b) { return a + b; });
+        rag_store<T, V, 1, L>(y, s0, gc, gl, cur, ecur, sum, T(1) / sum);
+        cur[0] = nxt[0];
+        ecur = enxt;
+        gc = gn;
+    }
+}
+
 // max or sum over the block, the same value returned to every lane: the waves' values through LDS,
 // folded in wave order (deterministic)
 template <typename T, int B, typename F>
@@ -567,6 +613,38 @@ static hipError_t softmax_rag_dispatch(const SoftmaxArgs &a, hipStream_t s) {
     }
 }
 
+template <typename T, int V, int NOUT>
+static hipError_t softmax_group_launch(const SoftmaxArgs &a, int L, hipStream_t s) {
+    const int64_t per_block = (int64_t)(kSBlock / 64) * (64 / L);  // rows a block takes at a time
+    int64_t g = (a.outer + per_block - 1) / per_block;
+    if (g > kSoftmaxMaxBlocks) g = kSoftmaxMaxBlocks;
+    const T *x = (const T *)a.x;
+    T *y = (T *)a.y;
+    const T *m = (const T *)a.mask;
+#define LX_SMG_CASE(N)                                                                                             \
+    case N:                                                                                                        \
+        hipLaunchKernelGGL((k_softmax_group<T, V, N, NOUT>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, a.outer,   \
+                           (int)a.r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);               \
+        break;
+    switch (L) {
+        LX_SMG_CASE(1) LX_SMG_CASE(2) LX_SMG_CASE(4) LX_SMG_CASE(8) LX_SMG_CASE(16) LX_SMG_CASE(32)
+    default: return hipErrorInvalidValue;
+    }
+#undef LX_SMG_CASE
+    return hipGetLastError();
+}
+
+template <typename T, int V>
+static hipError_t softmax_group_dispatch(const SoftmaxArgs &a, int L, hipStream_t s) {
+    if (!a.mask) return softmax_group_launch<T, V, 0>(a, L, s);
+    switch (a.mask_rows.nouter) {
+    case 1: return softmax_group_launch<T, V, 1>(a, L, s);
+    case 2: return softmax_group_launch<T, V, 2>(a, L, s);
+    case 3: return softmax_group_launch<T, V, 3>(a, L, s);
+    default: return softmax_group_launch<T, V, -1>(a, L, s);
+    }
+}
+
 template <typename T, int V, int NV, int B>
 static hipError_t softmax_rows_launch(const SoftmaxArgs &a, hipStream_t s) {
     const int64_t g = a.outer < (1 << 20) ? a.outer : (1 << 20);
@@ -598,6 +676,12 @@ static hipError_t softmax_typed(const SoftmaxArgs &a, hipStream_t s) {
         if (a.vec > 1) {
             // x and y 16-byte aligned: rows held in registers, 16-byte accesses
             const int64_t nvr = a.r / VW;
+            // short rows: L lanes per row, enough for its whole vectors and its head and tail elements
+            // (none when r is a multiple of VW: every row then starts aligned)
+            const int64_t ne_max = a.r % VW == 0 ? 0 : (a.r < 2 * VW - 2 ? a.r : 2 * VW - 2);
+            int L = 1;
+            while (L < nvr || L < ne_max) L <<= 1;
+            if (L <= 32) return softmax_group_dispatch<T, VW>(a, L, s);
             const bool mask_al = !a.mask || !a.mask_inner || ((uintptr_t)a.mask & 15) == 0;
             if (a.r % VW == 0 && mask_al && a.r <= 64 * VW * 8) {
                 if (a.mask) return softmax_wave_dispatch<T, VW, true>(a, s);

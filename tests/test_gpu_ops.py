@@ -596,6 +596,8 @@ def test_reduce_double(hip):
 
 RAGGED_REDUCE_CASES = [
     ((7, 1), [-1]), ((7, 3), [-1]), ((7, 5), [-1]), ((9, 63), [-1]), ((9, 65), [-1]), ((9, 1023), [-1]),
+    ((1031, 1), [-1]), ((1031, 4), [-1]), ((1031, 7), [-1]), ((1031, 16), [-1]), ((777, 49), [-1]),   # L lanes
+    ((1031, 64), [-1]), ((515, 128), [-1]), ((515, 100), [-1]), ((4097, 2), [-1]), ((3, 5, 33), [-1]),  # per row
     ((5, 8191), [-1]), ((3, 8193), [-1]), ((3, 100003), [-1]),   # row per wave, split rows (r > 8192)
     ((1000001,), None), ((3000003,), None), ((2, 3, 1000001), None),  # whole tensors not a multiple of 4
     ((5, 1000, 255), [1]), ((3, 77, 49), [1]), ((2, 3001, 7), [1]), ((64, 3, 1022), [1]),  # inner not % 4
@@ -734,19 +736,19 @@ def softmax_close(got, ref, pre):
     assert not bad.any(), (np.flatnonzero(bad)[:5], err[bad][:5], ref[bad][:5])
 
 
-SOFTMAX_ROW_LENGTHS = [1, 2, 3, 5, 7, 63, 65, 255, 257, 513, 1023, 2047, 2049, 2051, 2052, 4093, 4097, 8191, 8195,
-                       16389, 32767, 32771, 65535, 65539, 70001]
+SOFTMAX_ROW_LENGTHS = [1, 2, 3, 4, 5, 7, 8, 16, 31, 49, 63, 64, 65, 100, 127, 128, 129, 255, 256, 257, 513, 1023,
+                       2047, 2049, 2051, 2052, 4093, 4097, 8191, 8195, 16389, 32767, 32771, 65535, 65539, 70001]
 
 
 @pytest.mark.parametrize("r", SOFTMAX_ROW_LENGTHS)
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 def test_softmax_any_row_length(hip, r, dt):
-    """Rows of every length class: row per wave (whole vectors, or an unaligned head and a tail held one
-    element per lane), row per block in registers (256 or 1024 lanes, 4 to 16 vectors each), and the
-    three-pass kernel beyond.  Seven rows, so every head length 0..3 occurs; special values in the head,
-    the tail and the body."""
+    """Rows of every length class: short rows with L lanes per row (several rows per wave), row per wave
+    (whole vectors, or an unaligned head and a tail held one element per lane), row per block in registers
+    (256 or 1024 lanes, 4 to 16 vectors each), and the three-pass kernel beyond.  1031 short rows or seven
+    long ones, so every head length 0..3 occurs; special values in the head, the tail and the body."""
     rng = np.random.default_rng(r)
-    x = (rng.standard_normal((7, r)) * 3).astype(dt)
+    x = (rng.standard_normal((1031 if r <= 256 else 7, r)) * 3).astype(dt)
     if r >= 16:
         x[1, 0] = np.nan                   # in the first row's head or first vector
         x[2, r - 1] = np.inf               # in a tail: inf - inf = NaN
@@ -757,14 +759,14 @@ def test_softmax_any_row_length(hip, r, dt):
     softmax_close(got, O.softmax(x, -1), x)
 
 
-@pytest.mark.parametrize("r", [7, 70, 513, 1023, 2049, 4093, 9001, 32771])
+@pytest.mark.parametrize("r", [3, 7, 49, 64, 70, 128, 513, 1023, 2049, 4093, 9001, 32771])
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 def test_add_softmax_any_row_length(hip, r, dt):
     """A mask row contiguous along the row whose rows start off 16-byte boundaries ([b, 1, 1, r] with r not
     a multiple of 4: read by elements), a mask broadcast along the row ([b, h, q, 1]) and a scale, on every
     row kernel: bit-identical to the Div / Add / Softmax nodes and within the bar of the oracle."""
     rng = np.random.default_rng(r + 7)
-    q = 3
+    q = 37 if r <= 128 else 3
     s = (rng.standard_normal((2, 3, q, r)) * 3).astype(dt)
     for mshape in [(2, 1, 1, r), (2, 3, q, 1), (r,)]:
         m = np.where(rng.uniform(size=mshape) < 0.125, -10000.0, rng.uniform(-1, 1, mshape)).astype(dt)
@@ -825,6 +827,24 @@ def test_layernorm(hip, shape):
     got = ok(HIP.LayerNormDecomposed(dev(x), dev(g), dev(b), 1e-12))
     ref = O.layernorm_decomposed(x, g, b, np.float32(1e-12))
     # mean / variance are sums in a different order: 1e-5 relative to max(1, |y|)
+    err = np.abs(got.astype(np.float64) - ref)
+    assert np.all(err <= 1e-5 * np.maximum(1.0, np.abs(ref))), err.max()
+
+
+@pytest.mark.parametrize("r", [1, 2, 3, 4, 5, 7, 8, 16, 31, 49, 64, 100, 127, 128, 255, 257, 1023, 2049, 4093, 4099,
+                               4100])
+def test_layernorm_any_row_length(hip, r):
+    """Every row-length class of the fused LayerNorm: short rows with L lanes per row (several rows per
+    wave, 1031 rows so every head length and partial waves occur), rows of any length with an unaligned
+    head and a tail (gamma / beta read element by element where a row's vectors are off their 16-byte
+    boundaries), the wave-per-row kernel, and beyond 4099 the nine nodes."""
+    rng = np.random.default_rng(r + 3)
+    rows = 1031 if r <= 256 else 9
+    x = (rng.standard_normal((rows, r)) * 2).astype(np.float32)
+    g = (1 + 0.02 * rng.standard_normal(r)).astype(np.float32)
+    b = (0.02 * rng.standard_normal(r)).astype(np.float32)
+    got = ok(HIP.LayerNormDecomposed(dev(x), dev(g), dev(b), 1e-12))
+    ref = O.layernorm_decomposed(x, g, b, np.float32(1e-12))
     err = np.abs(got.astype(np.float64) - ref)
     assert np.all(err <= 1e-5 * np.maximum(1.0, np.abs(ref))), err.max()
 
