@@ -206,6 +206,20 @@ __device__ __forceinline__ void exp_table_fill(ExpTable &s) {
     if (threadIdx.x < 32) s.t[threadIdx.x] = kExp2fTable[threadIdx.x];
 }
 
+// The same fill into a table that only the calling wave reads (one-wave blocks,
+// or one table per wave): lanes 0..31 write one entry each.  A wave's LDS
+// operations execute in issue order, so its later lookups see the entries; the
+// wavefront-scope fences and the wave barrier keep the compiler from moving a
+// lookup above the writes.  No block barrier: a block's first global loads can
+// be issued before the fill and are not held up by it.
+__device__ __forceinline__ void exp_table_fill_wave(ExpTable &s) {
+    const int lane = threadIdx.x & 63;
+    if (lane < 32) s.t[lane] = kExp2fTable[lane];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Fills a table on the host (host restatement used by the tests).
 __host__ inline void exp_table_fill_host(ExpTable &s) {
     constexpr uint64_t tab[32] = LX_EXP2F_TABLE;
@@ -224,7 +238,8 @@ __host__ __device__ __forceinline__ double expf_scale(uint64_t ki, const ExpTabl
 
 // The glibc expf method (ARM optimized-routines, N = 32 table, degree-3
 // polynomial, FMA variant) without its special-case early-outs: equal to the
-// host expf for every x in [-104, 88] (callers bound the argument).
+// host expf for every x in [-104, 88], and +0 like the host's for x in
+// [-105.07, -104) (callers bound the argument).
 __host__ __device__ __forceinline__ float expf_core_lx(float x, const ExpTable &tab) {
     double xd = (double)x;
     double kd = __builtin_fma(LX_EXPF_INVLN2N, xd, LX_EXPF_SHIFT);
@@ -386,11 +401,16 @@ __device__ __forceinline__ float erf_fast_lx(float x, const ExpTable &tab) { ret
 // One element of the GELU subgraph Div(x, sqrt 2) -> Erf -> Add 1 -> Mul x ->
 // Mul 0.5, every node rounded as the reference rounds it, with two rewrites
 // of the Erf node that the chain's output cannot see: the sign of erf is
-// copied from its argument (erf(-0) becomes -0, and -0 + 1 == +0 + 1), and the
-// exponential's argument is clamped with a max that sends NaN to -104 (a NaN
-// argument comes from a NaN x, which reaches the output through x * b either
-// way).  Equal to the unfused chain bit for bit for all 2^32 inputs (NaN for
-// NaN), checked on the host with the correctly rounded seed.
+// copied from its argument (erf(-0) becomes -0, and -0 + 1 == +0 + 1), and
+// |a| is clamped to 10.25 before both of its uses.  For |a| >= 10.25 the
+// exponential's argument -a*a lies below expf's underflow threshold (-103.97)
+// with or without the clamp, so the exponential is +0 and erf is +-1 exactly,
+// whatever the reciprocal t; the clamp keeps d = 1 + p|a| within [1, 4.4] and
+// the exponential's argument within [-105.07, 0] (no separate clamps of
+// either), and sends a NaN |a| to 10.25 (a NaN a comes from a NaN x, which
+// reaches the output through x * b either way).  Equal to the unfused chain
+// bit for bit for all 2^32 inputs (NaN for NaN), checked on the host with the
+// correctly rounded seed.
 template <typename SeedFn>
 __host__ __device__ __forceinline__ float gelu_erf_core(float x, const ExpTable &tab, SeedFn seed) {
     const float a1 = 0.254829592f;
@@ -400,12 +420,12 @@ __host__ __device__ __forceinline__ float gelu_erf_core(float x, const ExpTable 
     const float a5 = 1.061405429f;
     const float p = 0.3275911f;
     const float a = div_sqrt2f_lx(x);
-    const float ax = __builtin_fabsf(a);
-    float d = 1.0f + p * ax;
-    d = d < 0x1p125f ? d : 0x1p125f;
+    const float aa = __builtin_fabsf(a);
+    const float ax = aa < 10.25f ? aa : 10.25f;
+    const float d = 1.0f + p * ax;
     const float t = recip_newton1(d, seed(d));
     const float poly = ((((a5 * t + a4) * t) + a3) * t + a2) * t + a1;
-    const float e = expf_core_lx(__builtin_fmaxf(-ax * ax, -104.0f), tab);
+    const float e = expf_core_lx(-ax * ax, tab);
     const float erf = __builtin_copysignf(1.0f - poly * t * e, a);
     const float b = erf + 1.0f;
     const float c = x * b;

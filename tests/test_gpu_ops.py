@@ -803,6 +803,34 @@ def test_device_rcp_f32_error_bound(hip):
     assert 0 < out.value <= 2.0 ** -22
 
 
+@pytest.mark.parametrize("offset", [0, 1])
+def test_table_maps_at_tile_edges(hip, offset):
+    """GELU and Erf run in one-wave blocks over tiles of 2 x 64 vectors: sizes on both sides of every
+    tile, vector and wave edge, the scalar tail, and (offset 1) pointers 4 bytes past 16-byte alignment,
+    which take the one-float-per-vector form.  Bits equal the oracle's; the float before and after the
+    output stay untouched."""
+    rng = np.random.default_rng(31 + offset)
+    for n in [1, 3, 4, 5, 63, 64, 65, 127, 128, 129, 255, 256, 257, 511, 512, 513, 4099, 65536 + 7]:
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        x[rng.integers(0, n, max(1, n // 50))] = np.float32(np.inf)
+        # x at the start of a (256-byte aligned) allocation, or one float into it
+        pad = np.full(offset, 7.0, np.float32)
+        buf = dev(np.concatenate([pad, x, [7.0, 7.0]]).astype(np.float32))
+        base = buf.h.data + 4 * offset
+        for op, ref in (("GeluErf", O.gelu_erf(x)), ("Erf", O.unary(O.ERF, x))):
+            out = dev(np.full(n + 2, 9.0, np.float32))
+            xo = DeviceTensor.wrap(base, (n,), np.float32, 4 * n, keepalive=buf)
+            yo = DeviceTensor.wrap(out.h.data + 4 * offset, (n,), np.float32, 4 * n, keepalive=out)
+            r = getattr(HIP, op)(xo, out=yo)
+            assert r.Status == OpStatus.Success, r.Message
+            full = out.to_numpy()
+            got = full[offset:offset + n]
+            same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+            assert same.all(), f"{op} n={n} offset={offset}: {(~same).sum()} mismatches"
+            guard = np.delete(full, np.arange(offset, offset + n))
+            assert (guard == 9.0).all(), f"{op} n={n} offset={offset} wrote outside its output"
+
+
 def test_gelu_chain_bit_exact(hip):
     rng = np.random.default_rng(24)
     x = np.concatenate([rng.standard_normal(300001), [0.0, -0.0, 1e-7, -8.0, 8.0, np.inf, -np.inf]]).astype(np.float32)
