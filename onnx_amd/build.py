@@ -20,10 +20,13 @@ SOURCES = ["lx_elementwise.hip", "lx_reduce.hip", "lx_softmax.hip", "lx_matmul.h
 # -ffp-contract=off: no FMA contraction of separately rounded float ops.
 # -fhip-fp32-correctly-rounded-divide-sqrt: IEEE division / sqrt (the reference's semantics).
 # -packed-fp32-ops off: no v_pk_*_f32 generation.
+# -disable-licm-promotion: LLVM's loop-invariant code motion promotes a store out of a loop whose trip
+#   count is one (a template's U = 1 or NV = 1 instance, before the loop is unrolled) and the promoted
+#   store loses its nontemporal hint: 44 streaming stores of this library compiled as ordinary stores.
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-gpu-flush-denormals-to-zero",
-    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-mllvm", "-disable-licm-promotion",
     "-Wall", "-Wno-unused-function", "-I", os.path.join(HERE, "..", "include"),
 ]
 

@@ -12,6 +12,7 @@
 // bit-identical to the host expf (expf_lx), the sums run over lane moves.
 // Only the order of the sum differs from the reference.  Other shapes (axis
 // not innermost, longer rows, unaligned storage) take three-pass kernels.
+#include <algorithm>
 #include <type_traits>
 
 #include "lx_device.h"
@@ -123,11 +124,80 @@ __device__ __forceinline__ void softmax_row_load(const T *__restrict__ x, int64_
     }
 }
 
+// One row held in registers by one wave: the optional Div / Mul by a scalar, the mask add, the seed-0 max,
+// the exponentials and their sum, and the division; y's row written with streaming stores.  cur holds the
+// row (and mcur its mask vectors) as softmax_row_load left them.
+template <typename T, int V, int NV, int NOUT, bool FULL, bool NTS = true>
+__device__ __forceinline__ void softmax_row_body(Vec<T, V> (&cur)[NV], const Vec<T, V> (&mcur)[NV], T *__restrict__ q,
+                                                 int r, int lane, bool has_scale, T sv, T sf, bool smul,
+                                                 const ExpTable &tab) {
+    constexpr bool MASK = NOUT != 0;
+    if (has_scale) {  // the Div (or Mul) node before the mask Add: the same IEEE operation per element
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const int col = (c * 64 + lane) * V;
+            if (FULL || col < r) {
+#pragma unroll
+                for (int k = 0; k < V; k++) cur[c].v[k] = smul ? cur[c].v[k] * sf : cur[c].v[k] / sv;
+            }
+        }
+    }
+    if constexpr (MASK) {
+#pragma unroll
+        for (int c = 0; c < NV; c++) {
+            const int col = (c * 64 + lane) * V;
+            if (FULL || col < r) {
+#pragma unroll
+                for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mcur[c].v[k];
+            }
+        }
+    }
+    // ReduceMax with seed 0 (TensorOps.cs:1820-1827)
+    T mx = T(0);
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (FULL || col < r) {
+#pragma unroll
+            for (int k = 0; k < V; k++) mx = row_max<T>(mx, cur[c].v[k]);
+        }
+    }
+    mx = row_reduce<T>(mx, [](T a, T b) { return row_max<T>(a, b); });
+    T sum = T(0);
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (FULL || col < r) {
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                cur[c].v[k] = exp_elem<T>(cur[c].v[k] - mx, tab);
+                sum = sum + cur[c].v[k];
+            }
+        }
+    }
+    sum = row_reduce<T>(sum, [](T a, T b) { return a + b; });
+    const T rs = T(1) / sum;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * V;
+        if (FULL || col < r) {
+            Vec<T, V> o;
+#pragma unroll
+            for (int k = 0; k < V; k++) o.v[k] = div_row<T>(cur[c].v[k], sum, rs);
+            if constexpr (NTS) vstore_nt<T, V>(q + col, o);
+            else vstore<T, V>(q + col, o);
+        }
+    }
+}
+
 // Rows of length r <= 64*V*NV held in registers, one wave per row at a time.
 // Each wave walks rows w, w + W, ... (W = all waves of the grid) and loads the
 // next row (and its mask vectors) while it finishes the current one.  NOUT:
 // mask row axes (0 = no mask; see mask_row_offset).  FULL: r == 64*V*NV, every
 // lane holds NV whole vectors (no per-vector bounds, one straight-line body).
+// Rows of exactly 256 to 1024 floats go to k_softmax_row1 instead (C3 on MI355X:
+// Softmax 73.1 -> 66.8 us, Add mask + Softmax 67.0 -> 63.3 us, with its
+// ordinary stores); this kernel takes the other row lengths.
 template <typename T, int V, int NV, int NOUT, bool FULL>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
@@ -153,68 +223,36 @@ __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ 
     for (; row < rows; row += W) {
         const int64_t next = row + W;
         if (next < rows) softmax_row_load<T, V, NV, NOUT, FULL>(x, next, r, lane, mask, mask_inner, mrows, nxt, mnxt);
-        if (scale) {  // the Div (or Mul) node before the mask Add: the same IEEE operation per element
-#pragma unroll
-            for (int c = 0; c < NV; c++) {
-                const int col = (c * 64 + lane) * V;
-                if (FULL || col < r) {
-#pragma unroll
-                    for (int k = 0; k < V; k++) cur[c].v[k] = smul ? cur[c].v[k] * sf : cur[c].v[k] / sv;
-                }
-            }
-        }
-        if constexpr (MASK) {
-#pragma unroll
-            for (int c = 0; c < NV; c++) {
-                const int col = (c * 64 + lane) * V;
-                if (FULL || col < r) {
-#pragma unroll
-                    for (int k = 0; k < V; k++) cur[c].v[k] = cur[c].v[k] + mcur[c].v[k];
-                }
-            }
-        }
-        // ReduceMax with seed 0 (TensorOps.cs:1820-1827)
-        T mx = T(0);
-#pragma unroll
-        for (int c = 0; c < NV; c++) {
-            const int col = (c * 64 + lane) * V;
-            if (FULL || col < r) {
-#pragma unroll
-                for (int k = 0; k < V; k++) mx = row_max<T>(mx, cur[c].v[k]);
-            }
-        }
-        mx = row_reduce<T>(mx, [](T a, T b) { return row_max<T>(a, b); });
-        T sum = T(0);
-#pragma unroll
-        for (int c = 0; c < NV; c++) {
-            const int col = (c * 64 + lane) * V;
-            if (FULL || col < r) {
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    cur[c].v[k] = exp_elem<T>(cur[c].v[k] - mx, tab);
-                    sum = sum + cur[c].v[k];
-                }
-            }
-        }
-        sum = row_reduce<T>(sum, [](T a, T b) { return a + b; });
-        const T rs = T(1) / sum;
-        T *q = y + row * (int64_t)r;
-#pragma unroll
-        for (int c = 0; c < NV; c++) {
-            const int col = (c * 64 + lane) * V;
-            if (FULL || col < r) {
-                Vec<T, V> o;
-#pragma unroll
-                for (int k = 0; k < V; k++) o.v[k] = div_row<T>(cur[c].v[k], sum, rs);
-                vstore_nt<T, V>(q + col, o);
-            }
-        }
+        softmax_row_body<T, V, NV, NOUT, FULL>(cur, mcur, y + row * (int64_t)r, r, lane, scale != nullptr, sv, sf,
+                                               smul, tab);
 #pragma unroll
         for (int c = 0; c < NV; c++) {
             cur[c] = nxt[c];
             if constexpr (MASK) mcur[c] = mnxt[c];
         }
     }
+}
+
+// The same rows, one row per one-wave block and no loop: the block issues its row's loads, then fills its
+// own expf table (exp_table_fill_wave), so no barrier stands between its start and its loads, and the wave
+// ends right after its stores.  The output goes out with ordinary stores, measured faster here than
+// streaming ones.  row0: the first row of this launch (launches of at most kMaxRowBlocks).
+constexpr int64_t kMaxRowBlocks = 1ll << 24;
+template <typename T, int V, int NV, int NOUT, bool FULL>
+__global__ __launch_bounds__(64) void k_softmax_row1(const T *__restrict__ x, T *__restrict__ y, int64_t row0,
+                                                     int r, const T *__restrict__ mask, int mask_inner,
+                                                     NdLayout mrows, const T *__restrict__ scale, int scale_div) {
+    __shared__ ExpTable tab;
+    const int lane = threadIdx.x;
+    const int64_t row = row0 + blockIdx.x;
+    Vec<T, V> cur[NV], mcur[NV];
+    softmax_row_load<T, V, NV, NOUT, FULL>(x, row, r, lane, mask, mask_inner, mrows, cur, mcur);
+    if constexpr (std::is_same<T, float>::value) exp_table_fill_wave(tab);
+    const T sv = scale ? scale[0] : T(1);
+    T sf = sv;
+    const bool smul = !scale_div || exact_pow2_recip(sv, &sf);
+    softmax_row_body<T, V, NV, NOUT, FULL, false>(cur, mcur, y + row * (int64_t)r, r, lane, scale != nullptr, sv, sf,
+                                                  smul, tab);
 }
 
 // ---------------------------------------------------------------------------
@@ -551,20 +589,25 @@ static hipError_t softmax_wave_launch(const SoftmaxArgs &a, hipStream_t s) {
     T *y = (T *)a.y;
     const T *m = (const T *)a.mask;
     const bool full = r == nv * 64 * V;
+#define LX_SM_ROW1(N, F)                                                                                        \
+    for (int64_t r0 = 0; r0 < a.outer; r0 += kMaxRowBlocks)                                                     \
+        hipLaunchKernelGGL((k_softmax_row1<T, V, N, NOUT, F>), dim3((unsigned)std::min(kMaxRowBlocks, a.outer - r0)), \
+                           dim3(64), 0, s, x, y, r0, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);
 #define LX_SM_CASE(N)                                                                                           \
     case N:                                                                                                     \
-        if (full && N <= 4)                                                                                     \
-            hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT, (N <= 4)>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, \
-                               a.outer, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);      \
-        else                                                                                                    \
+        if (full && N <= 4) {                                                                                   \
+            LX_SM_ROW1(N, true)                                                                                 \
+        } else {                                                                                                \
             hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT, false>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y,  \
                                a.outer, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);      \
+        }                                                                                                       \
         break;
     switch (nv) {
         LX_SM_CASE(1) LX_SM_CASE(2) LX_SM_CASE(3) LX_SM_CASE(4) LX_SM_CASE(5) LX_SM_CASE(6) LX_SM_CASE(7) LX_SM_CASE(8)
     default: return hipErrorInvalidValue;
     }
 #undef LX_SM_CASE
+#undef LX_SM_ROW1
     return hipGetLastError();
 }
 
