@@ -125,6 +125,48 @@ def test_int_binary_bit_exact(hip, op, dt):
     assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
 
 
+# Large outputs with one operand read once take the one-wave tile kernel (2 x 64 vectors per block): shapes
+# past 2^16 vectors whose vector counts leave a partial last tile, operand A or B streamed, the other
+# broadcast along rows, columns or both.
+TILE_SHAPES = [
+    ((67, 1531, 16), (1531, 16)),      # B broadcast along the outer axis
+    ((3, 1, 262160), (3, 7, 262160)),  # A broadcast along the middle axis
+    ((8191, 144), (8191, 1)),          # per-row statistic
+    ((1, 96), (12007, 96)),            # A broadcast, B streamed
+]
+
+
+@pytest.mark.parametrize("sa,sb", TILE_SHAPES)
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
+def test_binary_streamed_operand_tiles(hip, sa, sb, dt):
+    rng = np.random.default_rng(hash((sa, sb, np.dtype(dt).str)) & 0xffff)
+    if np.issubdtype(dt, np.floating):
+        a, b = rng.standard_normal(sa).astype(dt), rng.standard_normal(sb).astype(dt)
+    else:
+        info = np.iinfo(dt)
+        a = rng.integers(info.min, info.max, sa, dtype=dt, endpoint=True)
+        b = rng.integers(info.min, info.max, sb, dtype=dt, endpoint=True)
+        b[b == 0] = 3
+        if dt != np.uint8:
+            b[b == -1] = 5
+    for op, code in (("Add", O.ADD), ("Sub", O.SUB), ("Mul", O.MUL), ("Div", O.DIV)):
+        assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
+
+
+def test_uint8_div_by_zero_in_tiles(hip):
+    """A zero divisor in a streamed uint8 operand fails the call with the reference's status, whichever tile
+    holds it, and the next call succeeds."""
+    a = np.full((8191, 1, 144), 200, np.uint8)
+    for pos in [(0, 0, 0), (4096, 1, 64), (8190, 2, 143)]:
+        b = np.full((8191, 3, 144), 7, np.uint8)
+        b[pos] = 0
+        r = HIP.Div(dev(a), dev(b))
+        assert r.Status == OpStatus.Failure and r.Code == L.ERR_DIVIDE_BY_ZERO, pos
+        assert "divide by zero" in r.Message
+    b = np.full((8191, 3, 144), 7, np.uint8)
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), O.binary(O.DIV, a, b))
+
+
 def test_int64_div_large_operands(hip):
     rng = np.random.default_rng(13)
     a = rng.integers(-(2**62), 2**62, 4099, dtype=np.int64)
