@@ -478,7 +478,7 @@ def live_traffic(specs, steps, timeout_s=240):
 
 def profile_traffic():
     """Fallback: the GELU kernel's traffic from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", "k_gelu_erf_c5_traffic.txt")
+    path = os.path.join(ROOT, "profiles", "gelu_c5_traffic.txt")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
