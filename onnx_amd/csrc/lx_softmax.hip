@@ -195,9 +195,10 @@ __device__ __forceinline__ void softmax_row_body(Vec<T, V> (&cur)[NV], const Vec
 // next row (and its mask vectors) while it finishes the current one.  NOUT:
 // mask row axes (0 = no mask; see mask_row_offset).  FULL: r == 64*V*NV, every
 // lane holds NV whole vectors (no per-vector bounds, one straight-line body).
-// Rows of exactly 256 to 1024 floats go to k_softmax_row1 instead (C3 on MI355X:
+// Rows of exactly 256 or 512 floats go to k_softmax_row1 instead (C3 on MI355X:
 // Softmax 73.1 -> 66.8 us, Add mask + Softmax 67.0 -> 63.3 us, with its
-// ordinary stores); this kernel takes the other row lengths.
+// ordinary stores; on 400 MB of rows of 768 and 1024 floats it was 2-10%
+// slower than this kernel); this kernel takes the other row lengths.
 template <typename T, int V, int NV, int NOUT, bool FULL>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
@@ -591,12 +592,15 @@ static hipError_t softmax_wave_launch(const SoftmaxArgs &a, hipStream_t s) {
     const bool full = r == nv * 64 * V;
 #define LX_SM_ROW1(N, F)                                                                                        \
     for (int64_t r0 = 0; r0 < a.outer; r0 += kMaxRowBlocks)                                                     \
-        hipLaunchKernelGGL((k_softmax_row1<T, V, N, NOUT, F>), dim3((unsigned)std::min(kMaxRowBlocks, a.outer - r0)), \
+        hipLaunchKernelGGL((k_softmax_row1<T, V, (N <= 2 ? N : 2), NOUT, F>), dim3((unsigned)std::min(kMaxRowBlocks, a.outer - r0)), \
                            dim3(64), 0, s, x, y, r0, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);
 #define LX_SM_CASE(N)                                                                                           \
     case N:                                                                                                     \
-        if (full && N <= 4) {                                                                                   \
+        if (full && N <= 2) {                                                                                   \
             LX_SM_ROW1(N, true)                                                                                 \
+        } else if (full && N <= 4) {                                                                            \
+            hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT, (N <= 4)>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y, \
+                               a.outer, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);      \
         } else {                                                                                                \
             hipLaunchKernelGGL((k_softmax_wave<T, V, N, NOUT, false>), dim3((unsigned)g), dim3(kSBlock), 0, s, x, y,  \
                                a.outer, r, m, a.mask_inner, a.mask_rows, (const T *)a.scale, a.scale_div);      \
