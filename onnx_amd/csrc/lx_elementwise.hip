@@ -290,10 +290,12 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, c
 
 // Broadcast ops with an operand read once, on large arrays: one-wave blocks over tiles of 64 * U vectors
 // (vector u of lane l at tile * 64 * U + u * 64 + l), all U loaded before any is computed, no loop, so a
-// wave ends right after its stores, which are ordinary stores (C3 mask Add 63.5 -> 62.2 us, C2's Sub and
-// Div nodes 43.6 -> 41.7 us for the nine nodes on MI355X).  Outputs built only from re-read broadcast
-// operands (C4) stay with k_binary_nd: one-wave blocks ran them 35% slower.  tile0: the first tile of
-// this launch.
+// wave ends right after its streaming stores.  Measured on MI355X against k_binary_nd's 256-lane blocks,
+// interleaved in one process: C3 mask Add 62.7 -> 62.2 us, C2's per-row Sub / Div and gamma Mul on
+// [8,512,768] 6.3 -> 5.8-6.1 us, 400 MB of x * gamma[1536] 126.2 -> 125.5 us and [1,96] + [N,96]
+// 127.5 -> 122.4 us, C3 in double 65.1 -> 62.3 us.  Ordinary stores lost up to 8% on the re-read row
+// operands (x * gamma).  Outputs built only from re-read broadcast operands (C4) stay with k_binary_nd:
+// one-wave blocks ran them 35% slower.  tile0: the first tile of this launch.
 template <int OP, typename T, int AIN, int BIN, int V, int U>
 __global__ __launch_bounds__(64) void k_binary_tile(const T *__restrict__ a, const T *__restrict__ b,
                                                     T *__restrict__ y, uint32_t nv, uint32_t tile0, NdLayout L,
@@ -306,7 +308,7 @@ __global__ __launch_bounds__(64) void k_binary_tile(const T *__restrict__ a, con
 #pragma unroll
     for (int u = 0; u < U; u++) {
         const uint32_t v = v0 + u * 64;
-        if (v < nv) vstore<T, V>(y + (int64_t)v * V, bin_apply_vec<OP, T, V>(va[u], vb[u], (uint64_t)v * V, errs));
+        if (v < nv) vstore_nt<T, V>(y + (int64_t)v * V, bin_apply_vec<OP, T, V>(va[u], vb[u], (uint64_t)v * V, errs));
     }
 }
 
@@ -877,11 +879,11 @@ static hipError_t cast_typed(const void *x, void *y, int64_t n, int vec, ErrFlag
         int g = grid_for((n / E + 1) / 2, kBlock);
         hipLaunchKernelGGL((k_cast<SRC, DST, E, 2>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);
     } else if (vec > 1 && n / E >= kCastTwoMax && sizeof(S) == sizeof(D)) {
-        // large same-width casts: one-wave blocks (1 GiB float copy 331.8 -> 322.9 us on MI355X)
+        // large same-width casts: one-wave blocks (1 GiB float copy 329.6 -> 322.6 us on MI355X)
         int g = grid_for(n / E, 64);
         hipLaunchKernelGGL((k_cast<SRC, DST, E, 1, 64>), dim3(g), dim3(64), 0, s, (const S *)x, (D *)y, n, errs);
     } else if (vec > 1 && n / E >= kCastTwoMax && sizeof(S) > sizeof(D)) {
-        // large narrowing casts: ordinary stores (C4 int64 -> float32 130.0 -> 121.7 us against streaming
+        // large narrowing casts: ordinary stores (C4 int64 -> float32 129.4 -> 121.5 us against streaming
         // stores; 123.4 us in one-wave blocks)
         int g = grid_for(n / E, kBlock);
         hipLaunchKernelGGL((k_cast<SRC, DST, E, 1, kBlock, false>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);

@@ -195,10 +195,11 @@ __device__ __forceinline__ void softmax_row_body(Vec<T, V> (&cur)[NV], const Vec
 // next row (and its mask vectors) while it finishes the current one.  NOUT:
 // mask row axes (0 = no mask; see mask_row_offset).  FULL: r == 64*V*NV, every
 // lane holds NV whole vectors (no per-vector bounds, one straight-line body).
-// Rows of exactly 256 or 512 floats go to k_softmax_row1 instead (C3 on MI355X:
-// Softmax 73.1 -> 66.8 us, Add mask + Softmax 67.0 -> 63.3 us, with its
-// ordinary stores; on 400 MB of rows of 768 and 1024 floats it was 2-10%
-// slower than this kernel); this kernel takes the other row lengths.
+// Rows of exactly 256 or 512 floats go to k_softmax_row1 instead (C3 on MI355X,
+// interleaved in one process: Softmax 64.0 -> 60.5 us, Add mask + Softmax
+// 63.9 -> 61.0 us, with its ordinary stores; on 400 MB of rows of 768 and 1024
+// floats it was 2-10% slower than this kernel); this kernel takes the other
+// row lengths.
 template <typename T, int V, int NV, int NOUT, bool FULL>
 __global__ __launch_bounds__(kSBlock) void k_softmax_wave(const T *__restrict__ x, T *__restrict__ y, int64_t rows,
                                                           int r, const T *__restrict__ mask, int mask_inner,
