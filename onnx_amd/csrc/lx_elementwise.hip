@@ -996,6 +996,59 @@ __device__ __forceinline__ void chain_step(int op, Vec<float, V> &acc, const Vec
 // NIN: inputs held in registers (n_in <= NIN)
 extern __shared__ ExpTable chain_lds[];  // the expf table of chains with Erf (dynamic LDS: none otherwise)
 
+// One vector of every input of the chain (inputs with a broadcast inner axis: their one element across
+// the vector).
+template <int V, int NIN>
+__device__ __forceinline__ void chain_load(const ChainArgs &A, uint32_t v, Vec<float, V> (&x)[NIN]) {
+    const uint32_t row = fdiv(v, A.inner_v);
+    const uint32_t cv = v - row * A.inner_v.d;
+    int64_t off[NIN];
+#pragma unroll
+    for (int j = 0; j < NIN; j++) off[j] = 0;
+    uint32_t rr = row;
+    for (int d = 0; d < A.nouter; d++) {
+        const uint32_t q = fdiv(rr, A.odiv[d]);
+        const int64_t id = rr - q * A.odiv[d].d;
+#pragma unroll
+        for (int j = 0; j < NIN; j++)
+            if (j < A.n_in) off[j] += id * A.str[j][d];
+        rr = q;
+    }
+    const int64_t col = (int64_t)cv * V;
+#pragma unroll
+    for (int j = 0; j < NIN; j++) {
+        if (j < A.n_in) {
+            if ((A.inner_mode >> j) & 1) {
+                // ordinary loads: streaming loads measured slower here (C3-sized Add -> Mul
+                // chain 106 against 86 us on MI355X)
+                x[j] = vload<float, V>(A.in[j] + off[j] + col);
+            } else {
+                const float sv = A.in[j][off[j]];
+#pragma unroll
+                for (int k = 0; k < V; k++) x[j].v[k] = sv;
+            }
+        }
+    }
+}
+
+// The chain's instructions over one vector of inputs.
+template <int V, int NIN, bool ERF, bool POW>
+__device__ __forceinline__ Vec<float, V> chain_eval(const ChainArgs &A, const Vec<float, V> (&x)[NIN],
+                                                    const ExpTable &tab) {
+    Vec<float, V> acc = x[0];
+    for (int i = 0; i < A.n_ops; i++) {
+        const int o = A.operand[i];
+        const int j = o < 0 ? -o - 1 : o;
+        Vec<float, V> xj = x[0];
+#pragma unroll
+        for (int jj = 1; jj < NIN; jj++)
+            if (jj == j) xj = x[jj];
+        chain_step<V, ERF, POW>(A.op[i], acc, xj, o < 0, tab);
+    }
+    return acc;
+}
+
+// Small chains: a grid-stride loop in 256-lane blocks, one vector per lane.
 template <int V, int NIN, bool ERF, bool POW>
 __global__ __launch_bounds__(kBlock) void k_chain(ChainArgs A) {
     ExpTable &tab = chain_lds[0];
@@ -1004,53 +1057,49 @@ __global__ __launch_bounds__(kBlock) void k_chain(ChainArgs A) {
         __syncthreads();
     }
     for (uint32_t v = blockIdx.x * kBlock + threadIdx.x; v < A.nv; v += gridDim.x * kBlock) {
-        const uint32_t row = fdiv(v, A.inner_v);
-        const uint32_t cv = v - row * A.inner_v.d;
-        int64_t off[NIN];
-#pragma unroll
-        for (int j = 0; j < NIN; j++) off[j] = 0;
-        uint32_t rr = row;
-        for (int d = 0; d < A.nouter; d++) {
-            const uint32_t q = fdiv(rr, A.odiv[d]);
-            const int64_t id = rr - q * A.odiv[d].d;
-#pragma unroll
-            for (int j = 0; j < NIN; j++)
-                if (j < A.n_in) off[j] += id * A.str[j][d];
-            rr = q;
-        }
-        const int64_t col = (int64_t)cv * V;
         Vec<float, V> x[NIN];
+        chain_load<V, NIN>(A, v, x);
+        vstore_nt<float, V>(A.y + (int64_t)v * V, chain_eval<V, NIN, ERF, POW>(A, x, tab));
+    }
+}
+
+// Chains of 2^16 or more vectors: one-wave blocks over tiles of 64 * U vectors, every input of all U loaded
+// before any is computed, no loop; a chain with Erf fills the wave's own expf table after its loads.
+// Interleaved in one process on MI355X against k_chain: C3-sized Add mask -> Mul scalar 78.5 -> 69.8 us,
+// C2-sized Sub row -> Mul gamma 8.3 -> 7.0 us; on C1's 12,288 vectors it was slower (2.6 -> 3.6 us), so
+// small chains stay with k_chain.  tile0: the first tile of this launch.
+constexpr int64_t kChainTileMin = 1 << 16;
+template <int V, int NIN, bool ERF, bool POW, int U>
+__global__ __launch_bounds__(64) void k_chain_tile(ChainArgs A, uint32_t tile0) {
+    __shared__ ExpTable tab;
+    const uint32_t v0 = (tile0 + blockIdx.x) * (64u * U) + threadIdx.x;
+    Vec<float, V> x[U][NIN];
 #pragma unroll
-        for (int j = 0; j < NIN; j++) {
-            if (j < A.n_in) {
-                if ((A.inner_mode >> j) & 1) {
-                    // ordinary loads: streaming loads measured slower here (C3-sized Add -> Mul
-                    // chain 106 against 86 us on MI355X)
-                    x[j] = vload<float, V>(A.in[j] + off[j] + col);
-                } else {
-                    const float sv = A.in[j][off[j]];
+    for (int u = 0; u < U; u++)
+        if (v0 + u * 64 < A.nv) chain_load<V, NIN>(A, v0 + u * 64, x[u]);
+    if constexpr (ERF) exp_table_fill_wave(tab);
 #pragma unroll
-                    for (int k = 0; k < V; k++) x[j].v[k] = sv;
-                }
-            }
-        }
-        Vec<float, V> acc = x[0];
-        for (int i = 0; i < A.n_ops; i++) {
-            const int o = A.operand[i];
-            const int j = o < 0 ? -o - 1 : o;
-            Vec<float, V> xj = x[0];
-#pragma unroll
-            for (int jj = 1; jj < NIN; jj++)
-                if (jj == j) xj = x[jj];
-            chain_step<V, ERF, POW>(A.op[i], acc, xj, o < 0, tab);
-        }
-        vstore_nt<float, V>(A.y + (int64_t)v * V, acc);
+    for (int u = 0; u < U; u++) {
+        const uint32_t v = v0 + u * 64;
+        if (v < A.nv) vstore_nt<float, V>(A.y + (int64_t)v * V, chain_eval<V, NIN, ERF, POW>(A, x[u], tab));
     }
 }
 
 template <int V, int NIN>
 static void launch_chain_v(const ChainArgs &A, int g, bool pow, hipStream_t s) {
     const size_t lds = sizeof(ExpTable);
+    if (A.nv >= kChainTileMin) {
+        constexpr int U = 2;
+        const int64_t ntiles = ((int64_t)A.nv + 64 * U - 1) / (64 * U);
+        for (int64_t t0 = 0; t0 < ntiles; t0 += kMaxBlocks) {
+            const int gt = (int)std::min<int64_t>(kMaxBlocks, ntiles - t0);
+            if (A.uses_erf && pow) hipLaunchKernelGGL((k_chain_tile<V, NIN, true, true, U>), dim3(gt), dim3(64), 0, s, A, (uint32_t)t0);
+            else if (A.uses_erf) hipLaunchKernelGGL((k_chain_tile<V, NIN, true, false, U>), dim3(gt), dim3(64), 0, s, A, (uint32_t)t0);
+            else if (pow) hipLaunchKernelGGL((k_chain_tile<V, NIN, false, true, U>), dim3(gt), dim3(64), 0, s, A, (uint32_t)t0);
+            else hipLaunchKernelGGL((k_chain_tile<V, NIN, false, false, U>), dim3(gt), dim3(64), 0, s, A, (uint32_t)t0);
+        }
+        return;
+    }
     if (A.uses_erf && pow) hipLaunchKernelGGL((k_chain<V, NIN, true, true>), dim3(g), dim3(kBlock), lds, s, A);
     else if (A.uses_erf) hipLaunchKernelGGL((k_chain<V, NIN, true, false>), dim3(g), dim3(kBlock), lds, s, A);
     else if (pow) hipLaunchKernelGGL((k_chain<V, NIN, false, true>), dim3(g), dim3(kBlock), 0, s, A);
@@ -1061,8 +1110,8 @@ hipError_t launch_chain(const ChainArgs &A, hipStream_t s) {
     if (A.nv == 0) return hipSuccess;
     bool pow = false;
     for (int i = 0; i < A.n_ops; i++) pow = pow || A.op[i] == kPow;
-    // large chains without the expf table: two vectors per lane, as the binary kernels do
-    const int64_t work = A.uses_erf ? lane_work(A.nv, true) : (A.nv >= (1u << 20) ? (A.nv + 1) / 2 : A.nv);
+    // small chains with the expf table: several vectors per lane, so the table fill is paid once per four
+    const int64_t work = A.uses_erf ? lane_work(A.nv, true) : A.nv;
     const int g = grid_for(work, kBlock);
     if (A.vec == 4) {
         if (A.n_in <= 2) launch_chain_v<4, 2>(A, g, pow, s);

@@ -89,6 +89,13 @@ CASES = [
     # the output shape grows along the chain (rank-0 and lower-rank starts)
     ([(), (6,), (2, 6), (3, 1, 1)], [("Add", 1), ("Mul", 2), ("Sub", 3, True), ("Erf",)]),
     ([(64,), (16, 64), (4, 16, 1)], [("Mul", 1), ("Add", 2), ("Pow", 0, True)]),
+    # 2^16 vectors and more take the one-wave tile kernel: the C3 pattern, the GELU chain with Erf, eight
+    # inputs with Pow, a partial last tile, and an inner axis that does not divide by 4 (one float per vector)
+    ([(5, 300, 176), (5, 1, 176), ()], [("Add", 1), ("Mul", 2)]),
+    ([(3, 301, 292), (), (), ()], [("Div", 1), ("Erf",), ("Add", 2), ("Mul", 0, True), ("Mul", 3)]),
+    ([(2, 257, 516), (516,), (2, 1, 516), (257, 1), (), (1, 1, 1), (2, 257, 1), (1, 257, 516)],
+     [("Sub", 1), ("Mul", 2, True), ("Add", 3), ("Div", 4, True), ("Pow", 5), ("Sqrt",), ("Sub", 6), ("Add", 7)]),
+    ([(7, 9363), (9363,), ()], [("Mul", 1), ("Erf",), ("Sub", 2, True)]),
 ]
 
 
