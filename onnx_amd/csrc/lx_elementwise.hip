@@ -23,10 +23,16 @@ namespace lx {
 
 constexpr int kBlock = 256;
 constexpr int kMaxBlocks = 1 << 24;  // beyond this the kernels loop
-constexpr int kDivVecsPerLane = 4;
+constexpr int kDivVecsPerLane = 4;  // integer Div: vectors loaded per lane before computing
 // Cast: two vectors per lane for arrays of [2^16, 2^22) vectors (a 25 MB float copy: 5.75 -> 4.86 us on
 // MI355X); one per lane above (an 805 MB int64 -> float Cast: 125 us with one, 132 us with two)
-constexpr int64_t kCastTwoMin = 1 << 16, kCastTwoMax = 1 << 22;   // integer Div: vectors loaded per lane before computing
+constexpr int64_t kCastTwoMin = 1 << 16, kCastTwoMax = 1 << 22;
+// Arrays of kTileUMin to kTileUMax vectors (8 to 32 MB of floats) run as one-wave tiles of 4 x 64 vectors:
+// measured on MI355X (graph replays over rotating buffers), C2's [8,512,768] - [8,512,1] 5.9 -> 5.2 us and
+// * gamma[768] 6.1 -> 5.4 us against tiles of 2 x 64, a 17 MB copy 6.9 -> 6.1-6.5 us against two vectors per
+// lane in 256-lane blocks; outside the window four vectors per lane were slower (8 MB +14%, 67 MB +3%, 400 MB
+// +4%: too few blocks below it, too little overlap above).
+constexpr int64_t kTileUMin = 1 << 19, kTileUMax = 1 << 21;
 
 template <int CODE> struct CType;
 template <> struct CType<kFloat> { using T = float; };
@@ -225,6 +231,49 @@ __global__ __launch_bounds__(kBlock) void k_binary_flat(const T *__restrict__ a,
         int64_t i = nv * V + threadIdx.x;
         T l = (LAYOUT == kScalarA) ? sa : a[i];
         T r = (LAYOUT == kScalarB) ? sb : b[i];
+        y[i] = bin_apply<OP, T>(l, r, (uint64_t)i, errs);
+    }
+}
+
+// The same layouts on mid-sized arrays (kTileUMin to kTileUMax vectors): one-wave blocks over tiles of
+// 64 * U vectors, all loaded before any is computed, no loop.  tile0: the first tile of this launch.
+template <int OP, typename T, int LAYOUT, int V, int U>
+__global__ __launch_bounds__(64) void k_binary_flat_tile(const T *__restrict__ a, const T *__restrict__ b,
+                                                         T *__restrict__ y, int64_t n, int64_t tile0, ErrFlags *errs) {
+    const int64_t nv = n / V;
+    T sa = T(), sb = T();
+    if constexpr (LAYOUT == kScalarA) sa = a[0];
+    if constexpr (LAYOUT == kScalarB) sb = b[0];
+    const int64_t i0 = (tile0 + blockIdx.x) * (64 * U) + threadIdx.x;
+    Vec<T, V> va[U], vb[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int64_t i = i0 + u * 64;
+        if (i < nv) {
+            if constexpr (LAYOUT != kScalarA) va[u] = vload_nt<T, V>(a + i * V);
+            if constexpr (LAYOUT != kScalarB) vb[u] = vload_nt<T, V>(b + i * V);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int64_t i = i0 + u * 64;
+        if (i < nv) {
+            if constexpr (LAYOUT == kScalarA) {
+#pragma unroll
+                for (int k = 0; k < V; k++) va[u].v[k] = sa;
+            }
+            if constexpr (LAYOUT == kScalarB) {
+#pragma unroll
+                for (int k = 0; k < V; k++) vb[u].v[k] = sb;
+            }
+            vstore_nt<T, V>(y + i * V, bin_apply_vec<OP, T, V>(va[u], vb[u], (uint64_t)(i * V), errs));
+        }
+    }
+    const int64_t tail = n - nv * V;
+    if (tile0 + blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
+        const int64_t i = nv * V + threadIdx.x;
+        const T l = (LAYOUT == kScalarA) ? sa : a[i];
+        const T r = (LAYOUT == kScalarB) ? sb : b[i];
         y[i] = bin_apply<OP, T>(l, r, (uint64_t)i, errs);
     }
 }
@@ -502,11 +551,41 @@ static hipError_t binary_rag(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <int OP, typename T, int V, int TU>
+static hipError_t binary_tiles(const BinArgs &A, int key, int64_t nv, ErrFlags *errs, hipStream_t s) {
+    const T *a = (const T *)A.a;
+    const T *b = (const T *)A.b;
+    T *y = (T *)A.y;
+    const int64_t ntiles = (nv + 64 * TU - 1) / (64 * TU);
+    for (int64_t t0 = 0; t0 < ntiles; t0 += kMaxBlocks) {
+        const int g = (int)std::min<int64_t>(kMaxBlocks, ntiles - t0);
+        switch (key) {
+        case 3: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 1, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        case 2: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 0, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        case 1: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 1, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        default: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 0, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        }
+    }
+    return hipGetLastError();
+}
+
 template <int OP, typename T, int V>
 static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
     const T *a = (const T *)A.a;
     const T *b = (const T *)A.b;
     T *y = (T *)A.y;
+    if (A.layout != kNd && A.n / V >= kTileUMin && A.n / V < kTileUMax) {
+        const int64_t ntiles = (A.n / V + 255) / 256;
+        for (int64_t t0 = 0; t0 < ntiles; t0 += kMaxBlocks) {
+            const int g = (int)std::min<int64_t>(kMaxBlocks, ntiles - t0);
+            switch (A.layout) {
+            case kSame: hipLaunchKernelGGL((k_binary_flat_tile<OP, T, kSame, V, 4>), dim3(g), dim3(64), 0, s, a, b, y, A.n, t0, errs); break;
+            case kScalarA: hipLaunchKernelGGL((k_binary_flat_tile<OP, T, kScalarA, V, 4>), dim3(g), dim3(64), 0, s, a, b, y, A.n, t0, errs); break;
+            default: hipLaunchKernelGGL((k_binary_flat_tile<OP, T, kScalarB, V, 4>), dim3(g), dim3(64), 0, s, a, b, y, A.n, t0, errs); break;
+            }
+        }
+        return hipGetLastError();
+    }
     if (A.layout != kNd) {
         int64_t nv = A.n / V;
         int g = grid_for(nv > 0 ? nv : 1, kBlock);
@@ -548,18 +627,8 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
             }
         }
         if (U == 1 && two) {
-            constexpr int TU = 2;
-            const int64_t ntiles = (nv + 64 * TU - 1) / (64 * TU);
-            for (int64_t t0 = 0; t0 < ntiles; t0 += kMaxBlocks) {
-                const int g = (int)std::min<int64_t>(kMaxBlocks, ntiles - t0);
-                switch (key) {
-                case 3: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 1, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-                case 2: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 0, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-                case 1: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 1, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-                default: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 0, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-                }
-            }
-            return hipGetLastError();
+            if (nv >= kTileUMin && nv < kTileUMax) return binary_tiles<OP, T, V, 4>(A, key, nv, errs, s);
+            return binary_tiles<OP, T, V, 2>(A, key, nv, errs, s);
         }
         const int64_t lanes = (U > 1 && nv >= (1 << 20)) ? (nv + U - 1) / U : two ? (nv + 1) / 2 : nv;
         const int g = grid_for(lanes, kBlock);
@@ -870,12 +939,50 @@ __global__ __launch_bounds__(B) void k_cast(const typename CType<SRC>::T *__rest
     if (ovf) atomicMin(&errs->first_ovf, 0ull);
 }
 
+// Mid-sized casts (kTileUMin to kTileUMax vectors): one-wave blocks over tiles of 64 * 4 vectors, all four
+// loaded before any is converted, no loop.  tile0: the first tile of this launch.
+template <int SRC, int DST, int E, int U>
+__global__ __launch_bounds__(64) void k_cast_tile(const typename CType<SRC>::T *__restrict__ x,
+                                                  typename CType<DST>::T *__restrict__ y, int64_t n, int64_t tile0,
+                                                  ErrFlags *errs) {
+    using S = typename CType<SRC>::T;
+    using D = typename CType<DST>::T;
+    const int64_t nv = n / E;
+    bool ovf = false;
+    const int64_t i0 = (tile0 + blockIdx.x) * (64 * U) + threadIdx.x;
+    Vec<S, E> vx[U];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (i0 + u * 64 < nv) vx[u] = vload_nt<S, E>(x + (i0 + u * 64) * E);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (i0 + u * 64 < nv) {
+            Vec<D, E> vy;
+#pragma unroll
+            for (int k = 0; k < E; k++) vy.v[k] = cast_apply<SRC, DST>(vx[u].v[k], ovf);
+            vstore_nt<D, E>(y + (i0 + u * 64) * E, vy);
+        }
+    }
+    const int64_t tail = n - nv * E;
+    if (tile0 + blockIdx.x == 0 && (int64_t)threadIdx.x < tail) {
+        const int64_t i = nv * E + threadIdx.x;
+        y[i] = cast_apply<SRC, DST>(x[i], ovf);
+    }
+    if (ovf) atomicMin(&errs->first_ovf, 0ull);
+}
+
 template <int SRC, int DST>
 static hipError_t cast_typed(const void *x, void *y, int64_t n, int vec, ErrFlags *errs, hipStream_t s) {
     using S = typename CType<SRC>::T;
     using D = typename CType<DST>::T;
     constexpr int E = 16 / (sizeof(S) < sizeof(D) ? sizeof(S) : sizeof(D));  // 16 bytes on the narrower side
-    if (vec > 1 && n / E >= kCastTwoMin && n / E < kCastTwoMax) {
+    if (vec > 1 && n / E >= kTileUMin && n / E < kTileUMax) {
+        const int64_t ntiles = (n / E + 255) / 256;
+        for (int64_t t0 = 0; t0 < ntiles; t0 += kMaxBlocks) {
+            const int g = (int)std::min<int64_t>(kMaxBlocks, ntiles - t0);
+            hipLaunchKernelGGL((k_cast_tile<SRC, DST, E, 4>), dim3(g), dim3(64), 0, s, (const S *)x, (D *)y, n, t0, errs);
+        }
+    } else if (vec > 1 && n / E >= kCastTwoMin && n / E < kCastTwoMax) {
         int g = grid_for((n / E + 1) / 2, kBlock);
         hipLaunchKernelGGL((k_cast<SRC, DST, E, 2>), dim3(g), dim3(kBlock), 0, s, (const S *)x, (D *)y, n, errs);
     } else if (vec > 1 && n / E >= kCastTwoMax && sizeof(S) == sizeof(D)) {

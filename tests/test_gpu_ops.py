@@ -153,6 +153,74 @@ def test_binary_streamed_operand_tiles(hip, sa, sb, dt):
         assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
 
 
+# Arrays of 2^19 to 2^21 vectors run as one-wave tiles of 4 x 64 vectors (broadcast, same-shape and scalar
+# layouts, casts): sizes at both ends of that window, with tails and partial tiles.
+MID_VEC = {np.float32: 4, np.float64: 2, np.int32: 4, np.int64: 2, np.uint8: 16}
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("edge", ["low", "high"])
+def test_binary_mid_size_tiles(hip, dt, edge):
+    vw = MID_VEC[dt]
+    nvec = (1 << 19) + 77 if edge == "low" else (1 << 21) - 131
+    n = nvec * vw + 3
+    rows = 1031
+    per_row = -(-(nvec * vw) // rows) if edge == "low" else (nvec * vw) // rows
+    inner = (-(-per_row // vw) if edge == "low" else per_row // vw) * vw
+    assert (1 << 19) <= rows * inner // vw < (1 << 21)
+    rng = np.random.default_rng(nvec % 1000 + vw)
+    def draw(shape):
+        if np.issubdtype(dt, np.floating):
+            return rng.standard_normal(shape).astype(dt)
+        info = np.iinfo(dt)
+        v = rng.integers(max(info.min, -1000), min(info.max, 1000), shape, dtype=dt, endpoint=True)
+        v[v == 0] = 3
+        if dt != np.uint8:
+            v[v == -1] = 5
+        return v
+    a, b, c = draw(n), draw(n), draw(())
+    m, r = draw((rows, inner)), draw((rows, 1))
+    for op, code in (("Add", O.ADD), ("Sub", O.SUB), ("Mul", O.MUL), ("Div", O.DIV)):
+        assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))           # same shape
+        assert_bits(ok(getattr(HIP, op)(dev(a), dev(c))), O.binary(code, a, c))           # scalar B
+        assert_bits(ok(getattr(HIP, op)(dev(c), dev(b))), O.binary(code, c, b))           # scalar A
+        if not (op == "Div" and dt in (np.int32, np.int64)):
+            assert_bits(ok(getattr(HIP, op)(dev(m), dev(r))), O.binary(code, m, r))       # per-row operand
+
+
+def test_uint8_div_by_zero_in_mid_size_tiles(hip):
+    n = ((1 << 19) + 5) * 16 + 7
+    a = np.full(n, 200, np.uint8)
+    for pos in [0, n // 2, n - 8, n - 1]:
+        b = np.full(n, 7, np.uint8)
+        b[pos] = 0
+        r = HIP.Div(dev(a), dev(b))
+        assert r.Status == OpStatus.Failure and r.Code == L.ERR_DIVIDE_BY_ZERO, pos
+
+
+@pytest.mark.parametrize("src,to", [(np.float32, O.FLOAT), (np.int64, O.FLOAT), (np.float32, O.INT32),
+                                    (np.int32, O.INT64), (np.float64, O.UINT8), (np.int64, O.INT32)])
+def test_cast_mid_size_tiles(hip, src, to):
+    narrow = min(np.dtype(src).itemsize, np.dtype(O.NP_OF[to]).itemsize)
+    e = 16 // narrow
+    rng = np.random.default_rng(int(e) + to)
+    for nvec in [(1 << 19) + 9, (1 << 21) - 3]:
+        n = nvec * e + 5
+        if np.issubdtype(src, np.floating):
+            x = (rng.standard_normal(n) * 50).astype(src)
+        else:
+            x = rng.integers(-100, 100, n, dtype=src)
+        if to == O.UINT8:
+            x = (np.abs(x) % 250).astype(src)
+        assert_bits(ok(HIP.Cast(dev(x), to)), O.cast(x, to))
+        if to in (O.INT32, O.UINT8) and src != np.int32:
+            for pos in [0, n // 3, n - 1]:
+                y = x.copy()
+                y[pos] = 1e10 if np.issubdtype(src, np.floating) else 2 ** 40
+                r = HIP.Cast(dev(y), to)
+                assert r.Status == OpStatus.Failure and r.Code == L.ERR_OVERFLOW, pos
+
+
 def test_uint8_div_by_zero_in_tiles(hip):
     """A zero divisor in a streamed uint8 operand fails the call with the reference's status, whichever tile
     holds it, and the next call succeeds."""
