@@ -117,6 +117,50 @@ def test_binary_random(hip, op, dt):
         check(r, lambda: O.binary(code, a, b), same_bits, (op, dt, sa, sb, case))
 
 
+def large_broadcast_pair(rng, vw):
+    """An output of 2^18 to 2^23 elements (about 2^16 to 2^21 vectors: the one-wave tile paths), ranks 2-4,
+    the inner axis a whole number of 16-byte vectors or not, each axis held by one operand or both."""
+    r = int(rng.integers(2, 5))
+    total = int(2 ** rng.uniform(18, 23))
+    lead = [int(d) for d in rng.integers(2, 12, r - 1)]
+    inner = max(1, total // int(np.prod(lead)))
+    if rng.random() < 0.7:
+        inner = max(vw, inner // vw * vw)
+    out = tuple(lead + [inner])
+
+    # per axis: which operand holds it (the other broadcasts it), so the output is `out` itself; half the time
+    # one operand holds every axis (it is read once); leading axes broadcast may also be dropped
+    owner = rng.integers(0, 3, r)   # 0: both, 1: a only, 2: b only
+    if rng.random() < 0.5:
+        owner = np.where(owner == 2, 0, owner)
+    a = [d if o != 2 else 1 for d, o in zip(out, owner)]
+    b = [d if o != 1 else 1 for d, o in zip(out, owner)]
+    while len(a) > 0 and a[0] == 1 and rng.random() < 0.5:
+        a = a[1:]
+    while len(b) > 0 and b[0] == 1 and rng.random() < 0.5:
+        b = b[1:]
+    if rng.random() < 0.5:
+        a, b = b, a
+    return tuple(a), tuple(b)
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.uint8, np.int32, np.int64])
+def test_binary_random_large(hip, dt):
+    """Random broadcast pairs at the sizes of the tile kernels, every op, bit for bit against the oracle."""
+    rng = np.random.default_rng([14, np.dtype(dt).num])
+    vw = 16 // np.dtype(dt).itemsize
+    for case in range(24):
+        op = ["Add", "Sub", "Mul", "Div"][case % 4]
+        code = {"Add": O.ADD, "Sub": O.SUB, "Mul": O.MUL, "Div": O.DIV}[op]
+        sa, sb = large_broadcast_pair(rng, vw)
+        if op == "Div":
+            a, b = dividends(rng, sa, dt), divisors(rng, sb, dt)
+        else:
+            a, b = values(rng, sa, dt), values(rng, sb, dt)
+        r = getattr(HIP, op)(dev(a), dev(b))
+        check(r, lambda: O.binary(code, a, b), same_bits, (op, dt, sa, sb, case))
+
+
 def reduction_bar(dt):
     def compare(got, ref, x_abs):
         if got.shape != ref.shape:
