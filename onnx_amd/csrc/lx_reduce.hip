@@ -269,16 +269,16 @@ __global__ __launch_bounds__(64) void k_reduce_rows_finish(const typename Red<OP
 // partial and k_reduce_cols_finish folds them in split order.  UN: row vectors
 // each lane loads before folding them (in row order, so the fold is the same
 // for every UN).
-template <int OP, typename T, int V, int UN>
-__global__ __launch_bounds__(kRBlock) void k_reduce_cols(const T *__restrict__ x,
+template <int OP, typename T, int V, int UN, int B>
+__global__ __launch_bounds__(B) void k_reduce_cols(const T *__restrict__ x,
                                                          typename Red<OP, T>::A *__restrict__ partial,
                                                          T *__restrict__ y, int64_t outer, int64_t r, int64_t inner,
                                                          int ct, int rsplit, int pre, int post, int64_t R) {
     using RD = Red<OP, T>;
     using A = typename RD::A;
-    __shared__ A sm[kRBlock * V];
+    __shared__ A sm[B * V];
     const int t = threadIdx.x;
-    const int cvt = t % ct, rs = t / ct, nrs = kRBlock / ct;
+    const int cvt = t % ct, rs = t / ct, nrs = B / ct;
     const int64_t inner_v = inner / V;
     const int64_t tiles = (inner_v + ct - 1) / ct;
     const int64_t o = (int64_t)blockIdx.x / tiles;
@@ -357,6 +357,7 @@ struct RedPlan {
     int nchunks;
     int ct;
     int rsplit;
+    int block;   // cols: lanes per block (256 or 512)
     int64_t ws;  // partial bytes
 };
 
@@ -393,17 +394,24 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
     }
     const int64_t inner_v = inner / V > 0 ? inner / V : 1;
     // at most 512 bytes of a row per tile: 32 column vectors of 16 bytes, so a wave covers two rows (C4's
-    // int64 [64,256,4096] axis 1: 96 -> 82 us against 64-wide tiles; C5's float [256,4096,256]: 164 -> 158
-    // us; 16-wide tiles slow C5).  Single elements (an inner axis that is not a multiple of the vector
-    // width): 1 KB of a row per tile, 256 floats ([4128,255,255] axis 1: 271 us with 128-float tiles, 217)
-    const int ct_max = V == 1 ? 1024 / (int)sizeof(A) : 512 / (V * (int)sizeof(A));
+    // int64 [64,256,4096] axis 1: 96 -> 82 us against 64-wide tiles; 16-wide tiles slow C5).  Rows of at most
+    // 64 vectors (1 KB) are taken whole by one tile: C5's float [256,4096,256] 155.8 -> 150.7 us and int32 of
+    // the same shape 155.8 -> 150.8 us against two 512-byte tiles, unsplit although that leaves one block per
+    // CU.  Single elements (an inner axis that is not a multiple of the vector width): 1 KB of a row per tile,
+    // 256 floats ([4128,255,255] axis 1: 271 us with 128-float tiles, 217)
+    const bool whole = V > 1 && inner_v <= 64;
+    const int ct_max = V == 1 ? 1024 / (int)sizeof(A) : whole ? 64 : 512 / (V * (int)sizeof(A));
     int ct = 1;
     while (ct < ct_max && ct < inner_v) ct <<= 1;
     const int64_t tiles = ceil_div(inner_v, ct);
     const int64_t base = tiles * outer;
-    const int nrs = kRBlock / ct;
+    // wide rows (more than 64 vectors) over 256 or more reduced rows: 512-lane blocks, sixteen row slices
+    // per tile (C4 int64 82.6 -> 80.0 us, int32 [32,512,8192] 82.5 -> 80.8 us, float [64,1024,1024] 40.8 ->
+    // 40.2 us; over 64 reduced rows they were 31% slower)
+    p.block = (!whole && V > 1 && r >= 256) ? 512 : kRBlock;
+    const int nrs = p.block / ct;
     int64_t rsplit = 1;
-    if (base < kColsSplitBelow) {
+    if (base < (whole ? 256 : kColsSplitBelow)) {
         rsplit = ceil_div(kTargetBlocks, base);
         int64_t maxs = ceil_div(r, (int64_t)nrs * 16);  // >= 16 rows per slice
         if (rsplit > maxs) rsplit = maxs;
@@ -460,9 +468,14 @@ static hipError_t reduce_typed_v(const ReduceArgs &a, hipStream_t s) {
         const int64_t tiles = ceil_div(a.inner / V, p.ct);
         // the same bytes in flight per lane for every vector width: 8 rows of 16-byte vectors, 32 of floats
         constexpr int UN = kColsUnroll * VecWidth<T>::value / V;
-        hipLaunchKernelGGL((k_reduce_cols<OP, T, V, UN>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
-                           dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rsplit, a.pre_div,
-                           a.post_div, a.r_total);
+        if (p.block == 512)
+            hipLaunchKernelGGL((k_reduce_cols<OP, T, V, UN, 512>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
+                               dim3(512), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rsplit, a.pre_div,
+                               a.post_div, a.r_total);
+        else
+            hipLaunchKernelGGL((k_reduce_cols<OP, T, V, UN, kRBlock>), dim3((unsigned)(tiles * a.outer), (unsigned)p.rsplit),
+                               dim3(kRBlock), 0, s, x, ws, y, a.outer, a.r, a.inner, p.ct, p.rsplit, a.pre_div,
+                               a.post_div, a.r_total);
         if (p.rsplit > 1) {
             const int64_t nout = a.outer * a.inner;
             int64_t g = ceil_div(nout, kRBlock);

@@ -652,6 +652,9 @@ REDUCE_CASES = [
     ((16, 300, 64), [1]),         # strided middle axis
     ((4, 4096, 33), [1]),         # ragged inner
     ((256, 64, 256), [1]),
+    ((300, 777, 256), [1]),       # whole 1 KB rows per tile, unsplit
+    ((5, 4096, 192), [1]),        # whole rows per tile, split over row slices
+    ((3, 300, 1040), [1]),        # wide rows over 256+ reduced rows: 512-lane blocks
     ((5, 6, 7, 8), [0, 2]),       # two passes
     ((5, 6, 7, 8), [3, 1]),
     ((4, 5, 6), None),            # all axes
@@ -685,7 +688,7 @@ def test_reduce_float(hip, shape, axes, kd):
 
 
 @pytest.mark.parametrize("dt", [np.int32, np.int64])
-@pytest.mark.parametrize("shape,axes", [((64, 256, 40), [1]), ((9, 777), [-1]), ((3, 4, 5, 6), [0, 2]), ((2, 300000), None),
+@pytest.mark.parametrize("shape,axes", [((64, 256, 40), [1]), ((8, 300, 1032), [1]), ((9, 777), [-1]), ((3, 4, 5, 6), [0, 2]), ((2, 300000), None),
                                         ((2, 5, 3), [1])])
 def test_reduce_int_exact(hip, dt, shape, axes):
     rng = np.random.default_rng(20)
