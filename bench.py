@@ -229,7 +229,7 @@ class Workloads:
         wS, wM, wT, wO = w(self.S3), w(self.M3), w(self.T3), w(self.O3)
         ne3 = self.S3.numel()
         spec("C3", "Add mask [16,12,512,512]+[16,1,1,512]", 402685952, ne3, lambda i: HIP.Add(wS, wM, out=wT), 1, kbig,
-             kernels="k_binary_nd<0,float>")
+             kernels="k_binary_tile<0,float,U=2>")
         spec("C3", "Softmax(-1) [16,12,512,512]", 402653184, ne3, lambda i: HIP.Softmax(wT, -1, out=wO), 1, kbig,
              kernels="k_softmax_wave")
         spec("C3", "Add mask + Softmax fused", 402685952, ne3, lambda i: HIP.AddSoftmax(wS, wM, -1, out=wO), 1, kbig,
@@ -237,7 +237,8 @@ class Workloads:
 
         # C4: int64 / int32 A[64,1,4096] ~ U[-2^20,2^20] op B[1,256,4096] ~ U[1,1024]
         self.c4 = {}
-        for dt, es, nm in ((torch.int64, 8, "int64"), (torch.int32, 4, "int32")):
+        for dt, es, nm, kb in ((torch.int64, 8, "int64", "k_binary_tile<{},int64,128 lanes>"),
+                               (torch.int32, 4, "int32", "k_binary_nd<{},int32>")):
             A4 = torch.randint(-(2**20), 2**20 + 1, (64, 1, 4096), device=dev, dtype=dt, generator=gen)
             B4 = torch.randint(1, 1025, (1, 256, 4096), device=dev, dtype=dt, generator=gen)
             Y4 = torch.empty(64, 256, 4096, device=dev, dtype=dt)
@@ -246,9 +247,9 @@ class Workloads:
             nb = (64 * 4096 + 256 * 4096 + 64 * 256 * 4096) * es
             ne = Y4.numel()
             spec("C4", f"Add {nm}", nb, ne, lambda i, a=wA4, b=wB4, y=wY4: HIP.Add(a, b, out=y), 1, kbig,
-                 kernels=f"k_binary_nd<0,{nm}>")
+                 kernels=kb.format(0))
             spec("C4", f"Mul {nm}", nb, ne, lambda i, a=wA4, b=wB4, y=wY4: HIP.Mul(a, b, out=y), 1, kbig,
-                 kernels=f"k_binary_nd<2,{nm}>")
+                 kernels=kb.format(2))
             spec("C4", f"Div {nm} (per eager call: kernel + error-record readback)", nb, ne,
                  lambda i, a=wA4, b=wB4, y=wY4: HIP.Div(a, b, out=y), 1, kbig, timing="eager",
                  kernels="k_div_rows + k_publish")

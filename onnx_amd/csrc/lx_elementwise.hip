@@ -343,20 +343,23 @@ __global__ __launch_bounds__(kBlock) void k_binary_nd(const T *__restrict__ a, c
 // interleaved in one process: C3 mask Add 62.7 -> 62.2 us, C2's per-row Sub / Div and gamma Mul on
 // [8,512,768] 6.3 -> 5.8-6.1 us, 400 MB of x * gamma[1536] 126.2 -> 125.5 us and [1,96] + [N,96]
 // 127.5 -> 122.4 us, C3 in double 65.1 -> 62.3 us.  Ordinary stores lost up to 8% on the re-read row
-// operands (x * gamma).  Outputs built only from re-read broadcast operands (C4) stay with k_binary_nd:
-// one-wave blocks ran them 35% slower.  tile0: the first tile of this launch.
-template <int OP, typename T, int AIN, int BIN, int V, int U>
-__global__ __launch_bounds__(64) void k_binary_tile(const T *__restrict__ a, const T *__restrict__ b,
-                                                    T *__restrict__ y, uint32_t nv, uint32_t tile0, NdLayout L,
-                                                    int a_nt, int b_nt, ErrFlags *errs) {
-    const uint32_t v0 = (tile0 + blockIdx.x) * (64u * U) + threadIdx.x;
+// operands (x * gamma).  Outputs built only from re-read broadcast operands (C4) ran 35% slower in
+// one-wave blocks; for 8-byte elements they take B = 128 lanes, one vector each (int64 [64,1,4096] +
+// [1,256,4096]: 76.4-79 -> 75.3-75.9 us against k_binary_nd's 256-lane grid-stride loop; 64 lanes 116 us,
+// 128 x 2 vectors 79 us; 4-byte elements lost 1 us and stay with k_binary_nd).  tile0: the first tile
+// of this launch.
+template <int OP, typename T, int AIN, int BIN, int V, int U, int B = 64>
+__global__ __launch_bounds__(B) void k_binary_tile(const T *__restrict__ a, const T *__restrict__ b,
+                                                   T *__restrict__ y, uint32_t nv, uint32_t tile0, NdLayout L,
+                                                   int a_nt, int b_nt, ErrFlags *errs) {
+    const uint32_t v0 = (tile0 + blockIdx.x) * (uint32_t)(B * U) + threadIdx.x;
     Vec<T, V> va[U], vb[U];
 #pragma unroll
     for (int u = 0; u < U; u++)
-        if (v0 + u * 64 < nv) nd_load<T, AIN, BIN, V>(a, b, v0 + u * 64, L, a_nt, b_nt, va[u], vb[u]);
+        if (v0 + u * B < nv) nd_load<T, AIN, BIN, V>(a, b, v0 + u * B, L, a_nt, b_nt, va[u], vb[u]);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        const uint32_t v = v0 + u * 64;
+        const uint32_t v = v0 + u * B;
         if (v < nv) vstore_nt<T, V>(y + (int64_t)v * V, bin_apply_vec<OP, T, V>(va[u], vb[u], (uint64_t)v * V, errs));
     }
 }
@@ -551,19 +554,19 @@ static hipError_t binary_rag(const BinArgs &A, ErrFlags *errs, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <int OP, typename T, int V, int TU>
+template <int OP, typename T, int V, int TU, int B = 64>
 static hipError_t binary_tiles(const BinArgs &A, int key, int64_t nv, ErrFlags *errs, hipStream_t s) {
     const T *a = (const T *)A.a;
     const T *b = (const T *)A.b;
     T *y = (T *)A.y;
-    const int64_t ntiles = (nv + 64 * TU - 1) / (64 * TU);
+    const int64_t ntiles = (nv + B * TU - 1) / (B * TU);
     for (int64_t t0 = 0; t0 < ntiles; t0 += kMaxBlocks) {
         const int g = (int)std::min<int64_t>(kMaxBlocks, ntiles - t0);
         switch (key) {
-        case 3: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 1, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-        case 2: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 0, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-        case 1: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 1, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
-        default: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 0, V, TU>), dim3(g), dim3(64), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        case 3: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 1, V, TU, B>), dim3(g), dim3(B), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        case 2: hipLaunchKernelGGL((k_binary_tile<OP, T, 1, 0, V, TU, B>), dim3(g), dim3(B), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        case 1: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 1, V, TU, B>), dim3(g), dim3(B), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
+        default: hipLaunchKernelGGL((k_binary_tile<OP, T, 0, 0, V, TU, B>), dim3(g), dim3(B), 0, s, a, b, y, (uint32_t)nv, (uint32_t)t0, A.nd, A.a_once, A.b_once, errs); break;
         }
     }
     return hipGetLastError();
@@ -630,6 +633,7 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
             if (nv >= kTileUMin && nv < kTileUMax) return binary_tiles<OP, T, V, 4>(A, key, nv, errs, s);
             return binary_tiles<OP, T, V, 2>(A, key, nv, errs, s);
         }
+        if (U == 1 && sizeof(T) == 8 && nv >= (1 << 20)) return binary_tiles<OP, T, V, 1, 128>(A, key, nv, errs, s);
         const int64_t lanes = (U > 1 && nv >= (1 << 20)) ? (nv + U - 1) / U : two ? (nv + 1) / 2 : nv;
         const int g = grid_for(lanes, kBlock);
         switch (key) {

@@ -188,6 +188,27 @@ def test_binary_mid_size_tiles(hip, dt, edge):
             assert_bits(ok(getattr(HIP, op)(dev(m), dev(r))), O.binary(code, m, r))       # per-row operand
 
 
+# Outputs built only from re-read broadcast operands, 8-byte elements, at least 2^20 vectors: 128-lane
+# tiles of one vector per lane.  Even inner axes run two elements per vector, odd ones one; the vector
+# counts are not multiples of 128.
+@pytest.mark.parametrize("dt", [np.float64, np.int64])
+@pytest.mark.parametrize("shape_a,shape_b", [((33, 1, 4002), (1, 17, 4002)), ((37, 1, 6001), (1, 29, 6001)),
+                                              ((2, 1, 30, 1, 962), (1, 5, 1, 37, 962))])
+def test_binary_wide_broadcast_8byte(hip, dt, shape_a, shape_b):
+    rng = np.random.default_rng(sum(shape_a) + sum(shape_b))
+    if dt == np.float64:
+        a, b = rng.standard_normal(shape_a), rng.standard_normal(shape_b)
+    else:
+        a = rng.integers(-(1 << 40), 1 << 40, shape_a, dtype=np.int64)
+        b = rng.integers(-(1 << 20), 1 << 20, shape_b, dtype=np.int64)
+        a[a == 0], b[b == 0] = 3, 7
+    a, b = a.astype(dt), b.astype(dt)
+    assert np.broadcast_shapes(shape_a, shape_b) and np.prod(np.broadcast_shapes(shape_a, shape_b)) >= 1 << 21
+    for op, code in (("Add", O.ADD), ("Sub", O.SUB), ("Mul", O.MUL), ("Div", O.DIV)):
+        assert_bits(ok(getattr(HIP, op)(dev(a), dev(b))), O.binary(code, a, b))
+        assert_bits(ok(getattr(HIP, op)(dev(b), dev(a))), O.binary(code, b, a))
+
+
 def test_uint8_div_by_zero_in_mid_size_tiles(hip):
     n = ((1 << 19) + 5) * 16 + 7
     a = np.full(n, 200, np.uint8)
