@@ -24,6 +24,10 @@ namespace lx {
 constexpr int kBlock = 256;
 constexpr int kMaxBlocks = 1 << 24;  // beyond this the kernels loop
 constexpr int kDivVecsPerLane = 4;  // integer Div: vectors loaded per lane before computing
+// integer Div by a divisor constant along the outermost axis: rows per lane sharing one reciprocal, by
+// element size (C4 [64,1,4096] / [1,256,4096] on MI355X: int64 per eager call 96-97 us with 4 rows, 86-91
+// with 2, 90 with 3, 118-124 with 1; int32 kernel 44 us with 4, 47 with 2, 48 with 8)
+template <typename T> constexpr int kDivRowsPerLane = sizeof(T) == 8 ? 2 : 4;
 // Cast: two vectors per lane for arrays of [2^16, 2^22) vectors (a 25 MB float copy: 5.75 -> 4.86 us on
 // MI355X); one per lane above (an 805 MB int64 -> float Cast: 125 us with one, 132 us with two)
 constexpr int64_t kCastTwoMin = 1 << 16, kCastTwoMax = 1 << 22;
@@ -615,16 +619,17 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
             const int top = A.nd.nouter - 1;
             if (nv >= (1 << 20) && top >= 0 && A.nd.b_str[top] == 0 && A.nd.odiv[top].d >= 2 &&
                 nv % A.nd.odiv[top].d == 0) {
+                constexpr int UR = kDivRowsPerLane<T>;
                 const uint32_t R = A.nd.odiv[top].d;
                 const int64_t rest = nv / R;
-                const int64_t lanes = rest * ((R + U - 1) / U);
+                const int64_t lanes = rest * ((R + UR - 1) / UR);
                 const FastDiv fr = make_fastdiv((uint32_t)rest);
                 const int g = grid_for(lanes, kBlock);
                 switch (key) {
-                case 3: hipLaunchKernelGGL((k_div_rows<T, 1, 1, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
-                case 2: hipLaunchKernelGGL((k_div_rows<T, 1, 0, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
-                case 1: hipLaunchKernelGGL((k_div_rows<T, 0, 1, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
-                default: hipLaunchKernelGGL((k_div_rows<T, 0, 0, V, U>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 3: hipLaunchKernelGGL((k_div_rows<T, 1, 1, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 2: hipLaunchKernelGGL((k_div_rows<T, 1, 0, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 1: hipLaunchKernelGGL((k_div_rows<T, 0, 1, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                default: hipLaunchKernelGGL((k_div_rows<T, 0, 0, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
                 }
                 return hipGetLastError();
             }
