@@ -24,10 +24,12 @@ namespace lx {
 constexpr int kBlock = 256;
 constexpr int kMaxBlocks = 1 << 24;  // beyond this the kernels loop
 constexpr int kDivVecsPerLane = 4;  // integer Div: vectors loaded per lane before computing
-// integer Div by a divisor constant along the outermost axis: rows per lane sharing one reciprocal, by
-// element size (C4 [64,1,4096] / [1,256,4096] on MI355X: int64 per eager call 96-97 us with 4 rows, 86-91
-// with 2, 90 with 3, 118-124 with 1; int32 kernel 44 us with 4, 47 with 2, 48 with 8)
+// integer Div by a divisor constant along the outermost axis: rows per lane sharing one reciprocal, and
+// lanes per block, by element size (C4 [64,1,4096] / [1,256,4096] on MI355X, kernel time over 100 launches
+// in one process: int64 86.5 us with 4 rows in 256-lane blocks, 84.3 with 2 rows, 82.1 with 2 rows in
+// 128-lane blocks; int32 43.6 us with 4 rows, 44.4 with 2, 43.8 with 2 in 128-lane blocks)
 template <typename T> constexpr int kDivRowsPerLane = sizeof(T) == 8 ? 2 : 4;
+template <typename T> constexpr int kDivRowsBlock = sizeof(T) == 8 ? 128 : kBlock;
 // Cast: two vectors per lane for arrays of [2^16, 2^22) vectors (a 25 MB float copy: 5.75 -> 4.86 us on
 // MI355X); one per lane above (an 805 MB int64 -> float Cast: 125 us with one, 132 us with two)
 constexpr int64_t kCastTwoMin = 1 << 16, kCastTwoMax = 1 << 22;
@@ -375,13 +377,13 @@ __global__ __launch_bounds__(B) void k_binary_tile(const T *__restrict__ a, cons
 // (seed and Newton step, most of the division's instructions) are computed
 // once for U quotients.  Same arithmetic, fallback and error records per
 // element as k_binary_nd.
-template <typename T, int AIN, int BIN, int V, int U>
-__global__ __launch_bounds__(kBlock) void k_div_rows(const T *__restrict__ a, const T *__restrict__ b,
+template <typename T, int AIN, int BIN, int V, int U, int B = kBlock>
+__global__ __launch_bounds__(B) void k_div_rows(const T *__restrict__ a, const T *__restrict__ b,
                                                      T *__restrict__ y, uint32_t lanes, FastDiv rest,
                                                      uint32_t R, NdLayout L, int a_nt, int b_nt, ErrFlags *errs) {
     const int top = L.nouter - 1;
     const int64_t a_top = L.a_str[top];
-    for (uint32_t t = blockIdx.x * kBlock + threadIdx.x; t < lanes; t += gridDim.x * kBlock) {
+    for (uint32_t t = blockIdx.x * B + threadIdx.x; t < lanes; t += gridDim.x * B) {
         const uint32_t chunk = fdiv(t, rest);
         const uint32_t vr = t - chunk * rest.d;
         const uint32_t row = fdiv(vr, L.inner_v);
@@ -624,12 +626,13 @@ static hipError_t binary_typed_v(const BinArgs &A, ErrFlags *errs, hipStream_t s
                 const int64_t rest = nv / R;
                 const int64_t lanes = rest * ((R + UR - 1) / UR);
                 const FastDiv fr = make_fastdiv((uint32_t)rest);
-                const int g = grid_for(lanes, kBlock);
+                constexpr int BR = kDivRowsBlock<T>;
+                const int g = grid_for(lanes, BR);
                 switch (key) {
-                case 3: hipLaunchKernelGGL((k_div_rows<T, 1, 1, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
-                case 2: hipLaunchKernelGGL((k_div_rows<T, 1, 0, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
-                case 1: hipLaunchKernelGGL((k_div_rows<T, 0, 1, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
-                default: hipLaunchKernelGGL((k_div_rows<T, 0, 0, V, UR>), dim3(g), dim3(kBlock), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 3: hipLaunchKernelGGL((k_div_rows<T, 1, 1, V, UR, BR>), dim3(g), dim3(BR), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 2: hipLaunchKernelGGL((k_div_rows<T, 1, 0, V, UR, BR>), dim3(g), dim3(BR), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                case 1: hipLaunchKernelGGL((k_div_rows<T, 0, 1, V, UR, BR>), dim3(g), dim3(BR), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
+                default: hipLaunchKernelGGL((k_div_rows<T, 0, 0, V, UR, BR>), dim3(g), dim3(BR), 0, s, a, b, y, (uint32_t)lanes, fr, R, A.nd, A.a_once, A.b_once, errs); break;
                 }
                 return hipGetLastError();
             }
