@@ -231,9 +231,9 @@ class Workloads:
         spec("C3", "Add mask [16,12,512,512]+[16,1,1,512]", 402685952, ne3, lambda i: HIP.Add(wS, wM, out=wT), 1, kbig,
              kernels="k_binary_tile<0,float,U=2>")
         spec("C3", "Softmax(-1) [16,12,512,512]", 402653184, ne3, lambda i: HIP.Softmax(wT, -1, out=wO), 1, kbig,
-             kernels="k_softmax_wave")
+             kernels="k_softmax_row1")
         spec("C3", "Add mask + Softmax fused", 402685952, ne3, lambda i: HIP.AddSoftmax(wS, wM, -1, out=wO), 1, kbig,
-             kernels="k_softmax_wave (mask)")
+             kernels="k_softmax_row1 (mask)")
 
         # C4: int64 / int32 A[64,1,4096] ~ U[-2^20,2^20] op B[1,256,4096] ~ U[1,1024]
         self.c4 = {}
