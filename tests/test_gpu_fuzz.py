@@ -200,6 +200,60 @@ def test_reduce_random(hip, op, dt):
         check(r, lambda: O.reduce(code, x, axes, bool(kd)), compare, (op, dt, shape, axes, kd, case))
 
 
+def large_reduce_case(rng, vw):
+    """A shape of 2^14 to 2^22 elements and the axes to reduce, drawn to reach each reduction plan: long rows
+    split over blocks (a few rows of more than 8192 elements), many short rows, column reductions with narrow
+    (at most 64 vectors) and wide inner axes, few output columns (rows split into slices), and two reduced
+    axis groups (two passes).  Dimensions are multiples of the vector width or ragged."""
+    def dim(lo, hi):
+        d = int(rng.integers(lo, hi + 1))
+        return d - d % vw + (0 if rng.random() < 0.5 else int(rng.integers(1, vw))) if d > vw else d
+    kind = int(rng.integers(0, 6))
+    if kind == 0:    # long rows, few of them
+        shape, axes = (int(rng.integers(1, 33)), dim(8193, 120000)), [-1]
+    elif kind == 1:  # many short rows
+        shape, axes = (int(rng.integers(2000, 30000)), dim(1, 150)), [1]
+    elif kind == 2:  # columns, narrow inner axis
+        shape, axes = (int(rng.integers(1, 40)), int(rng.integers(200, 3000)), dim(1, 64 * vw)), [1]
+    elif kind == 3:  # columns, wide inner axis
+        shape, axes = (int(rng.integers(1, 6)), int(rng.integers(256, 1200)), dim(64 * vw + 1, 3000)), [1]
+    elif kind == 4:  # few output columns: rows cut into slices
+        shape, axes = (int(rng.integers(1, 3)), int(rng.integers(5000, 60000)), dim(1, 24)), [-2]
+    else:            # two reduced groups
+        shape, axes = (int(rng.integers(2, 9)), int(rng.integers(2, 50)), int(rng.integers(2, 9)), dim(100, 2000)), [0, 2]
+    n = int(np.prod(shape))
+    if n > (1 << 22):
+        shape = (max(1, shape[0] * (1 << 22) // n),) + shape[1:]
+    return shape, axes
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32, np.int64])
+@pytest.mark.parametrize("op", ["ReduceSum", "ReduceMean", "ReduceMax"])
+def test_reduce_random_large(hip, op, dt):
+    """Random shapes at the sizes where the reduction planner picks its split-row, row-group, whole-row-tile,
+    wide-column and row-slice kernels: bit for bit for integers and ReduceMax, within the reduction bar for
+    float sums and means."""
+    rng = np.random.default_rng([16, ["ReduceSum", "ReduceMean", "ReduceMax"].index(op), np.dtype(dt).num])
+    code = {"ReduceSum": O.RSUM, "ReduceMean": O.RMEAN, "ReduceMax": O.RMAX}[op]
+    vw = 16 // np.dtype(dt).itemsize
+    for case in range(18):
+        shape, axes = large_reduce_case(rng, vw)
+        x = values(rng, shape, dt, special=0.0) if np.dtype(dt).kind == "f" else \
+            np.asarray(rng.integers(-(2**20), 2**20, shape), dt)
+        kd = case % 2
+        r = getattr(HIP, op)(dev(x), axes, kd)
+        ax = tuple(a % len(shape) for a in axes)
+        if np.dtype(dt).kind != "f" or op == "ReduceMax":
+            compare = same_bits
+        else:
+            x_abs = np.abs(x.astype(np.float64)).sum(axis=ax, keepdims=bool(kd))
+            if op == "ReduceMean":
+                x_abs = x_abs / int(np.prod([shape[a] for a in ax]))
+            bar = reduction_bar(dt)
+            compare = lambda got, ref, bar=bar, x_abs=x_abs: bar(got, ref, np.asarray(x_abs))  # noqa: E731
+        check(r, lambda: O.reduce(code, x, axes, bool(kd)), compare, (op, dt, shape, axes, kd, case))
+
+
 @pytest.mark.parametrize("dt", FLOATS)
 def test_softmax_random(hip, dt):
     rng = np.random.default_rng([13, np.dtype(dt).num])
@@ -215,6 +269,38 @@ def test_softmax_random(hip, dt):
                 return False
             err = np.abs(got.astype(np.float64) - ref)[~nan]
             return bool(np.all(err <= 1e-5 * np.abs(ref[~nan]) + 1e-30))
+        check(r, lambda: O.softmax(x, axis), compare, (dt, shape, axis, case))
+
+
+@pytest.mark.parametrize("dt", FLOATS)
+def test_softmax_random_large(hip, dt):
+    """Rows of 1 to 6000 elements, up to 2^21 elements in all, along the last axis or an inner one (ragged
+    and vector-aligned rows alike): within 1e-5 |ref| of the oracle beyond the reference's own rounding.
+    The reference sums a row serially in float32, which drifts up to ~1e-5 relative from the exact sum over
+    a few thousand N(0, 4) entries (1.08e-5 on a row of 2703), an error no other summation order can
+    reproduce; so |got - ref| <= 1e-5 |ref| + |ref - truth|, truth being the same Softmax in float64 (seed-0
+    max), the rule of the fixed-shape Softmax tests."""
+    rng = np.random.default_rng([17, np.dtype(dt).num])
+    for case in range(30):
+        n = int(rng.integers(1, 6001))
+        if case % 3 == 2:
+            shape, axis = (int(rng.integers(1, 9)), n, int(rng.integers(1, 40))), 1
+        else:
+            shape, axis = (int(rng.integers(1, 6)), int(rng.integers(1, max(2, (1 << 21) // n // 5))), n), -1
+        x = (rng.standard_normal(shape) * 4).astype(dt)
+        r = HIP.Softmax(dev(x), axis)
+
+        def compare(got, ref, x=x, axis=axis):
+            nan = np.isnan(ref)
+            if got.shape != ref.shape or not np.array_equal(np.isnan(got), nan):
+                return False
+            p = x.astype(np.float64)
+            m = np.fmax(p.max(axis=axis, keepdims=True), 0.0)
+            e = np.exp(p - m)
+            truth = e / e.sum(axis=axis, keepdims=True)
+            slack = np.abs(ref.astype(np.float64) - truth)
+            err = np.abs(got.astype(np.float64) - ref)
+            return bool(np.all((err <= 1e-5 * np.abs(ref) + slack + 1e-30)[~nan]))
         check(r, lambda: O.softmax(x, axis), compare, (dt, shape, axis, case))
 
 
