@@ -380,9 +380,13 @@ def cpu_ops(c5_target_s=4.0, target_s=1.0):
 # ---------------------------------------------------------------------------
 # HBM traffic: rocprofv3 counter passes over `bench.py --probe`
 # ---------------------------------------------------------------------------
+HEADLINE_PROBE_STEPS = 3
+
+
 def run_probe(torch, HIP, DeviceTensor, steps):
     """Child of a rocprofv3 --pmc pass: a copy of known size (the calibration), then each per-config op
-    launched twice, every segment opened by a marker kernel (Cast uint8 -> int16 of 16 elements)."""
+    launched twice, then three headline steps (GELU, ReduceSum, ReduceMean in the step's order), every
+    segment opened by a marker kernel (Cast uint8 -> int16 of 16 elements)."""
     W = Workloads(torch, HIP, DeviceTensor, steps)
     mk_in = DeviceTensor.from_numpy(np.arange(16, dtype=np.uint8))
     mk_out = DeviceTensor.empty((16,), np.int16)
@@ -403,47 +407,73 @@ def run_probe(torch, HIP, DeviceTensor, steps):
             sp["fn"](i)
         torch.cuda.synchronize()
     marker()
+    for _ in range(HEADLINE_PROBE_STEPS):
+        W.gelu()
+        W.rsum()
+        W.rmean()
+    torch.cuda.synchronize()
+    marker()
     print("probe done", flush=True)
 
 
 def parse_counters(path, counter):
-    """Per-segment lists of (kernel name, counter value) from a counter_collection.csv, segments split at
-    the marker kernel."""
+    """Per-segment lists of (kernel name, counter value, duration in ns) from a counter_collection.csv,
+    segments split at the marker kernel, and the markers' own (value, duration) pairs."""
     rows = []
     with open(path) as f:
         for r in csv.DictReader(f):
             if r["Counter_Name"] != counter:
                 continue
-            rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+            dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) if r.get("End_Timestamp") else 0
+            rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]), dur))
     rows.sort()
-    segs, cur = [], None
-    for _, name, v in rows:
+    segs, cur, markers = [], None, []
+    for _, name, v, dur in rows:
         if MARKER in name:
+            markers.append((v, dur))
             if cur is not None:
                 segs.append(cur)
             cur = []
             continue
         if cur is not None and "lx::" in name:
-            cur.append((name, v))
+            cur.append((name, v, dur))
     # the probe ends with a marker: whatever follows it is not a segment
-    return segs
+    return segs, markers
+
+
+def short(name):
+    return name.split("(")[0].replace("void ", "")
+
+
+XCDS = 8            # MI355X: 256 CUs in 8 XCDs; rocprofv3 sums a GRBM counter over the XCDs
+RATED_MHZ = 2400.0  # MI355X peak engine clock (the agent's Max_Engine_Clk_Fcompute)
+
+
+def clock_of(seg, pred, c0):
+    """Shader clock (MHz) of the dispatches in a GRBM_GUI_ACTIVE segment whose name satisfies `pred`: busy
+    cycles per XCD, less the `c0` cycles the counter adds to every dispatch outside its timestamps, over
+    the dispatches' durations."""
+    sel = [(v / XCDS - c0, d) for n, v, d in seg if pred(n)]
+    ns = sum(d for _, d in sel)
+    return round(sum(c for c, _ in sel) / ns * 1e3, 1) if ns else None
 
 
 def live_traffic(specs, steps, timeout_s=240):
-    """Two rocprofv3 passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py --probe`; returns
-    ({op index: (fetch bytes, write bytes, kernel names)}, calibration dict) or (None, reason)."""
+    """Three rocprofv3 passes over `bench.py --probe`: FETCH_SIZE, WRITE_SIZE and GRBM_GUI_ACTIVE (busy
+    cycles, for the shader clock).  Returns ({op index: (fetch bytes, write bytes, kernel names)},
+    calibration dict, clock dict) or (None, reason, None)."""
     exe = shutil.which("rocprofv3")
     if not exe:
-        return None, "rocprofv3 not found"
+        return None, "rocprofv3 not found", None
     out = os.path.join(ROOT, "gpurun_out", "bench_counters")
     shutil.rmtree(out, ignore_errors=True)
     os.makedirs(out, exist_ok=True)
     env = dict(os.environ, TMPDIR="/tmp")
     res = {}
-    for counter, tag in (("FETCH_SIZE", "f"), ("WRITE_SIZE", "w")):
+    for counter, tag in (("FETCH_SIZE", "f"), ("WRITE_SIZE", "w"), ("GRBM_GUI_ACTIVE", "c")):
         cmd = [exe, "--pmc", counter, "--output-format", "csv", "-d", os.path.join(out, tag), "-o", tag, "--",
                sys.executable, os.path.join(ROOT, "bench.py"), "--probe", "--steps", str(steps)]
-        log(f"traffic pass {counter}: " + " ".join(cmd))
+        log(f"counter pass {counter}: " + " ".join(cmd))
         with open(os.path.join(out, f"{tag}.log"), "w") as lf:
             p = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=lf, stderr=subprocess.STDOUT,
                                  start_new_session=True)
@@ -452,29 +482,51 @@ def live_traffic(specs, steps, timeout_s=240):
             except subprocess.TimeoutExpired:
                 os.killpg(p.pid, signal.SIGKILL)
                 p.wait()
-                return None, f"{counter} pass timed out after {timeout_s} s"
+                return None, f"{counter} pass timed out after {timeout_s} s", None
         done = "probe done" in open(os.path.join(out, f"{tag}.log")).read()
         files = glob.glob(os.path.join(out, tag, "**", "*counter_collection.csv"), recursive=True)
         if not done or not files:
-            return None, f"{counter} pass failed (rc {p.returncode})"
-        res[counter] = parse_counters(files[0], counter)
-        log(f"traffic pass {counter}: {len(res[counter])} segments (rc {p.returncode})")
-    f, wr = res["FETCH_SIZE"], res["WRITE_SIZE"]
-    if len(f) != len(specs) + 1 or len(wr) != len(specs) + 1:
-        return None, f"segment count {len(f)}/{len(wr)} != {len(specs) + 1}"
-    cf = sum(v for _, v in f[0])
-    cw = sum(v for _, v in wr[0])
-    calib = {"kernel": f[0][0][0].split("(")[0].replace("void ", "") if f[0] else "?",
+            return None, f"{counter} pass failed (rc {p.returncode})", None
+        res[counter], marks = parse_counters(files[0], counter)
+        if counter == "GRBM_GUI_ACTIVE":
+            # the counter's busy window is longer than the dispatch: a constant per dispatch, measured on the
+            # 16-element marker kernels (about 2 us, taken to run at the rated clock, so that c0 errs by
+            # at most a few hundred cycles: under 0.5% of a 150 us kernel's clock)
+            mc = sorted(v / XCDS for v, _ in marks)
+            md = sorted(d for _, d in marks)
+            c0 = mc[len(mc) // 2] - RATED_MHZ * 1e-3 * md[len(md) // 2]
+        log(f"counter pass {counter}: {len(res[counter])} segments (rc {p.returncode})")
+    f, wr, ck = res["FETCH_SIZE"], res["WRITE_SIZE"], res["GRBM_GUI_ACTIVE"]
+    nseg = len(specs) + 2
+    if len(f) != nseg or len(wr) != nseg or len(ck) != nseg:
+        return None, f"segment count {len(f)}/{len(wr)}/{len(ck)} != {nseg}", None
+    cf = sum(v for _, v, _ in f[0])
+    cw = sum(v for _, v, _ in wr[0])
+    calib = {"kernel": short(f[0][0][0]) if f[0] else "?",
              "bytes_read": CALIB_BYTES, "bytes_written": CALIB_BYTES, "FETCH_SIZE_KiB": round(cf, 1),
              "WRITE_SIZE_KiB": round(cw, 1), "fetch_factor": round(CALIB_BYTES / (cf * 1024), 5),
              "write_factor": round(CALIB_BYTES / (cw * 1024), 5)}
     per = {}
     for i in range(len(specs)):
         fs, ws = f[i + 1], wr[i + 1]
-        names = sorted({n.split("(")[0].replace("void ", "") for n, _ in fs})
-        per[i] = (sum(v for _, v in fs) / 2 * 1024 * calib["fetch_factor"],
-                  sum(v for _, v in ws) / 2 * 1024 * calib["write_factor"], names)
-    return per, calib
+        names = sorted({short(n) for n, _, _ in fs})
+        per[i] = (sum(v for _, v, _ in fs) / 2 * 1024 * calib["fetch_factor"],
+                  sum(v for _, v, _ in ws) / 2 * 1024 * calib["write_factor"], names)
+    gi = next(i for i, sp in enumerate(specs) if sp["op"].startswith("GELU"))
+    head = ck[-1]
+    is_gelu = lambda n: "GeluOp" in n  # noqa: E731
+    clock = {"source": "rocprofv3 --pmc GRBM_GUI_ACTIVE over bench.py --probe (the profiler serialises the "
+                       f"dispatches): busy cycles / {XCDS} XCDs, less a per-dispatch constant of {round(c0)} "
+                       "cycles measured on the marker kernels, / dispatch duration",
+             "rated_mhz": RATED_MHZ,
+             "calibration_copy_mhz": clock_of(ck[0], lambda n: True, c0),
+             "gelu_back_to_back_mhz": clock_of(ck[gi + 1], is_gelu, c0),
+             "gelu_in_headline_steps_mhz": clock_of(head, is_gelu, c0),
+             "reduce_sum_in_headline_steps_mhz": clock_of(head, lambda n: "reduce_cols" in n, c0),
+             "reduce_mean_in_headline_steps_mhz": clock_of(head, lambda n: "reduce_rows_split" in n, c0),
+             "gelu_in_headline_steps_us": [round(d / 1e3, 1) for n, v, d in head if is_gelu(n)],
+             "gelu_back_to_back_us": [round(d / 1e3, 1) for n, v, d in ck[gi + 1] if is_gelu(n)]}
+    return per, calib, clock
 
 
 def profile_traffic():
@@ -712,11 +764,22 @@ def bench_extras(torch, HIP, DeviceTensor, set_stream, steps, warmup, W):
 
 
 # ---------------------------------------------------------------------------
+def spread(v):
+    """min / median / max / mean of a list of per-step times (us), and the means of its first and last
+    fifth, which show a drift over the timed region (a clock still ramping, say)."""
+    s = sorted(v)
+    q = max(1, len(v) // 5)
+    return {"min": round(s[0], 2), "median": round(s[len(s) // 2], 2), "max": round(s[-1], 2),
+            "mean": round(sum(v) / len(v), 2), "first_fifth_mean": round(sum(v[:q]) / q, 2),
+            "last_fifth_mean": round(sum(v[-q:]) / q, 2)}
+
+
 def headline_c5(torch, W, steps, warmup):
     """K steps of C5 (GELU, ReduceSum(axis 1), ReduceMean(all)) on the launch stream.  A HIP event before
     and after every GELU launch (the roofline kernel) and one after the last step: each event is a queue
     packet that adds about 3.4 us of device time, so the two reductions are timed together, as the rest of
-    the step.  Returns (ms per step, {"gelu": ms per launch, "reductions": ms per step}, host wall ms per step)."""
+    the step.  Returns (ms per step, {"gelu": ms per launch, "reductions": ms per step}, host wall ms per
+    step, {"gelu": [us per step], "reductions": [us per step]})."""
     fns = (W.gelu, W.rsum, W.rmean)
     for _ in range(warmup):
         for f in fns:
@@ -737,10 +800,11 @@ def headline_c5(torch, W, steps, warmup):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
     total = ev[0][0].elapsed_time(end)
-    gelu = sum(ev[s][0].elapsed_time(ev[s][1]) for s in range(steps)) / steps
+    gelu_us = [ev[s][0].elapsed_time(ev[s][1]) * 1e3 for s in range(steps)]
     nxt = [ev[s + 1][0] for s in range(steps - 1)] + [end]
-    red = sum(ev[s][1].elapsed_time(nxt[s]) for s in range(steps)) / steps
-    return total / steps, {"gelu": gelu, "reductions": red}, wall_ms / steps
+    red_us = [ev[s][1].elapsed_time(nxt[s]) * 1e3 for s in range(steps)]
+    return (total / steps, {"gelu": sum(gelu_us) / steps * 1e-3, "reductions": sum(red_us) / steps * 1e-3},
+            wall_ms / steps, {"gelu": gelu_us, "reductions": red_us})
 
 
 def main():
@@ -786,7 +850,7 @@ def main():
     torch.cuda.synchronize()
 
     # ---- headline: C5 ----
-    ms, per, wall = headline_c5(torch, W, args.steps, args.warmup)
+    ms, per, wall, per_step = headline_c5(torch, W, args.steps, args.warmup)
     gbs = C5_STEP_BYTES / (ms * 1e-3) / 1e9
     gelu_gbs = GELU_BYTES / (per["gelu"] * 1e-3) / 1e9
     log(f"C5 step {ms * 1e3:.1f} us ({gbs:.0f} GB/s): GELU {per['gelu'] * 1e3:.1f} us, ReduceSum(axis 1) + "
@@ -810,6 +874,10 @@ def main():
                    "elements_per_s": round((W.X5.numel() + 2 * W.Yb.numel()) / (ms * 1e-3), 1),
                    "per_op_us": {"gelu": round(per["gelu"] * 1e3, 2),
                                  "reduce_sum_axis1 + reduce_mean_all": round(per["reductions"] * 1e3, 2)},
+                   "per_step_us": {"gelu": spread(per_step["gelu"]),
+                                   "reduce_sum_axis1 + reduce_mean_all": spread(per_step["reductions"])},
+                   "per_step_us_list": {"gelu": [round(v, 1) for v in per_step["gelu"]],
+                                        "reduce_sum_axis1 + reduce_mean_all": [round(v, 1) for v in per_step["reductions"]]},
                    "timing": "K eager steps on one dedicated stream (the library's launch stream), HIP events "
                              "recorded on it before and after every GELU launch and after the last step"},
         "roofline": {"bound": "hbm", "achieved": round(gelu_gbs, 2), "peak": PEAK_HBM_GBS, "unit": "GB/s",
@@ -846,7 +914,9 @@ def main():
     # ---- HBM traffic per launch (rocprofv3 counters) ----
     if args.traffic == "live":
         torch.cuda.synchronize()
-        per_t, calib = live_traffic(W.specs, args.steps)
+        per_t, calib, clock = live_traffic(W.specs, args.steps)
+        if clock is not None:
+            out["roofline"]["clock"] = clock
         if per_t is None:
             log(f"live traffic unavailable: {calib}")
             out["roofline"]["traffic"] = profile_traffic()

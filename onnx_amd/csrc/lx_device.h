@@ -239,7 +239,12 @@ __host__ __device__ __forceinline__ double expf_scale(uint64_t ki, const ExpTabl
 // The glibc expf method (ARM optimized-routines, N = 32 table, degree-3
 // polynomial, FMA variant) without its special-case early-outs: equal to the
 // host expf for every x in [-104, 88], and +0 like the host's for x in
-// [-105.07, -104) (callers bound the argument).
+// [-105.07, -104) (callers bound the argument).  The polynomial
+// 1 + C2 r + C1 r^2 + C0 r^3 is evaluated in Horner form (three FMAs) where the
+// published routine splits it (C0 r + C1, r^2, C2 r + 1, one FMA joining them)
+// for instruction-level parallelism: the two doubles differ in their last bits
+// only, and on every float x in [-104, 88] both round to the host expf's float
+// (checked by exhaustion on the host), with one instruction less.
 __host__ __device__ __forceinline__ float expf_core_lx(float x, const ExpTable &tab) {
     double xd = (double)x;
     double kd = __builtin_fma(LX_EXPF_INVLN2N, xd, LX_EXPF_SHIFT);
@@ -247,10 +252,9 @@ __host__ __device__ __forceinline__ float expf_core_lx(float x, const ExpTable &
     kd -= LX_EXPF_SHIFT;
     double r = __builtin_fma(LX_EXPF_INVLN2N, xd, -kd);
     double s = expf_scale(ki, tab);
-    double z = __builtin_fma(LX_EXPF_C0, r, LX_EXPF_C1);
-    double r2 = r * r;
-    double y = __builtin_fma(LX_EXPF_C2, r, 1.0);
-    y = __builtin_fma(z, r2, y);
+    double y = __builtin_fma(LX_EXPF_C0, r, LX_EXPF_C1);
+    y = __builtin_fma(y, r, LX_EXPF_C2);
+    y = __builtin_fma(y, r, 1.0);
     y = y * s;
     return (float)y;
 }
@@ -278,13 +282,21 @@ __host__ __device__ __forceinline__ float expf_nonpos_lx(float x, const ExpTable
     return expf_core_lx(x, tab);
 }
 
-// Correctly rounded float quotient x / 1.4142135f (= float32(sqrt 2)) without a
-// division: one double product rounded once.  x / c is never closer than
-// 2^-49 (relative) to a float rounding boundary, the double product errs by at
-// most 2^-52, so the rounding always agrees with IEEE division (denormal
-// results included).  Checked for all 2^32 inputs by the test suite.
-#define LX_INV_SQRT2F_D (1.0 / 1.41421353816986083984375)
-__host__ __device__ __forceinline__ float div_sqrt2f_lx(float x) { return (float)((double)x * LX_INV_SQRT2F_D); }
+// Float quotient x / 1.4142135f (= float32(sqrt 2)) without a division, in two
+// float operations: q = fma(x, zh, x * zl) with zh + zl the reciprocal of the
+// divisor split into two floats (zh = 1/c rounded to float, zl = the rest
+// rounded to float; Brisebarre, Muller and Raina, "Accelerating correctly
+// rounded floating-point division when the divisor is known in advance", IEEE
+// Trans. Computers 53(8), 2004).  Correctly rounded for every |x| >= 2^-100
+// (checked by exhaustion on the host); below that x * zl loses bits to
+// underflow and the quotient can be one ulp off, which the GELU element never
+// sees (there d = 1 and the exponential is 1 whatever the quotient's last bit:
+// its own exhaustive check covers these inputs).
+#define LX_INV_SQRT2F_HI 0x1.6a09e6p-1f
+#define LX_INV_SQRT2F_LO 0x1.9fcef4p-26f
+__host__ __device__ __forceinline__ float div_sqrt2f_lx(float x) {
+    return __builtin_fmaf(x, LX_INV_SQRT2F_HI, x * LX_INV_SQRT2F_LO);
+}
 
 // Correctly rounded 1/d for d in [1, 2^126) from a float seed by one float Newton step, e = 1 - d*y (one FMA),
 // y' = y + e*y (one FMA).  From the correctly rounded seed the result is exact for every such d; from a seed one
@@ -408,9 +420,11 @@ __device__ __forceinline__ float erf_fast_lx(float x, const ExpTable &tab) { ret
 // whatever the reciprocal t; the clamp keeps d = 1 + p|a| within [1, 4.4] and
 // the exponential's argument within [-105.07, 0] (no separate clamps of
 // either), and sends a NaN |a| to 10.25 (a NaN a comes from a NaN x, which
-// reaches the output through x * b either way).  Equal to the unfused chain
-// bit for bit for all 2^32 inputs (NaN for NaN), checked on the host with the
-// correctly rounded seed.
+// reaches the output through x * b either way).  The Div node is
+// div_sqrt2f_lx, exact for |x| >= 2^-100; below, its last bit cannot reach the
+// output (d rounds to 1 and the exponential to 1 either way).  Equal to the
+// unfused chain bit for bit for all 2^32 inputs (NaN for NaN), checked on the
+// host with the correctly rounded seed.
 template <typename SeedFn>
 __host__ __device__ __forceinline__ float gelu_erf_core(float x, const ExpTable &tab, SeedFn seed) {
     const float a1 = 0.254829592f;

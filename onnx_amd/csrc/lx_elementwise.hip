@@ -708,29 +708,50 @@ constexpr int kTabMapU = 2;
 
 template <typename F, int V, int U>
 __global__ __launch_bounds__(64) void k_map_tab(const float *__restrict__ x, float *__restrict__ y, int64_t n,
-                                                int64_t tile0, F f) {
+                                                int64_t tile0, uint32_t whole, F f) {
     __shared__ ExpTable tab;
     const int lane = threadIdx.x;
     const int64_t nv = n / V;
-    Vec<float, V> vx[U];
-    const int64_t i0 = (tile0 + blockIdx.x) * (64 * U) + lane;
+    const int64_t v0 = (tile0 + blockIdx.x) * (64 * U);
     // the wave's issue priority raised from its first instruction: waves already running win arbitration
     // over those just dispatched, so the waves holding loaded data finish first (C5 GELU on MI355X,
     // interleaved in one process: 250.5 -> 248.4 us mean of nine pairs; raised only for the loads 256 us,
     // only for the arithmetic 253 us)
     __builtin_amdgcn_s_setprio(3);
+    Vec<float, V> vx[U];
+    if (blockIdx.x < whole) {
+        // a whole tile (the launch's first `whole` blocks, a scalar test): the tile's base is uniform (scalar registers) and each lane adds one 32-bit byte
+        // offset, the vectors u > 0 lying at immediate offsets from it, so no lane computes a 64-bit
+        // address or a bounds test
+        const char *xt = reinterpret_cast<const char *>(x + v0 * V);
+        char *yt = reinterpret_cast<char *>(y + v0 * V);
+        const uint32_t off = (uint32_t)lane * (uint32_t)(V * sizeof(float));
 #pragma unroll
-    for (int u = 0; u < U; u++)
-        if (i0 + u * 64 < nv) vx[u] = vload_nt<float, V>(x + (i0 + u * 64) * V);
-    exp_table_fill_wave(tab);
+        for (int u = 0; u < U; u++)
+            vx[u] = vload_nt<float, V>(reinterpret_cast<const float *>(xt + off + u * 64 * V * sizeof(float)));
+        exp_table_fill_wave(tab);
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        const int64_t i = i0 + u * 64;
-        if (i < nv) {
+        for (int u = 0; u < U; u++) {
             Vec<float, V> vy;
 #pragma unroll
             for (int k = 0; k < V; k++) vy.v[k] = f(vx[u].v[k], tab);
-            vstore_nt<float, V>(y + i * V, vy);
+            vstore_nt<float, V>(reinterpret_cast<float *>(yt + off + u * 64 * V * sizeof(float)), vy);
+        }
+    } else {
+        const int64_t i0 = v0 + lane;
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (i0 + u * 64 < nv) vx[u] = vload_nt<float, V>(x + (i0 + u * 64) * V);
+        exp_table_fill_wave(tab);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t i = i0 + u * 64;
+            if (i < nv) {
+                Vec<float, V> vy;
+#pragma unroll
+                for (int k = 0; k < V; k++) vy.v[k] = f(vx[u].v[k], tab);
+                vstore_nt<float, V>(y + i * V, vy);
+            }
         }
     }
     const int64_t tail = n - nv * V;
@@ -749,8 +770,9 @@ static hipError_t launch_map_tab(const float *x, float *y, int64_t n, int vec, F
     const int64_t ntiles = (n / V + 64 * kTabMapU - 1) / (64 * kTabMapU);
     for (int64_t t0 = 0; t0 < (ntiles > 0 ? ntiles : 1); t0 += kMaxBlocks) {
         const int g = (int)std::max<int64_t>(1, std::min<int64_t>(kMaxBlocks, ntiles - t0));
-        if (V == 4) hipLaunchKernelGGL((k_map_tab<F, 4, kTabMapU>), dim3(g), dim3(64), 0, s, x, y, n, t0, f);
-        else hipLaunchKernelGGL((k_map_tab<F, 1, kTabMapU>), dim3(g), dim3(64), 0, s, x, y, n, t0, f);
+        const uint32_t whole = (uint32_t)std::max<int64_t>(0, std::min<int64_t>(g, (n / V) / (64 * kTabMapU) - t0));
+        if (V == 4) hipLaunchKernelGGL((k_map_tab<F, 4, kTabMapU>), dim3(g), dim3(64), 0, s, x, y, n, t0, whole, f);
+        else hipLaunchKernelGGL((k_map_tab<F, 1, kTabMapU>), dim3(g), dim3(64), 0, s, x, y, n, t0, whole, f);
     }
     return hipGetLastError();
 }

@@ -53,14 +53,33 @@ static inline float fbits(uint32_t u) {
 }
 static inline bool same(float a, float b) { return bits(a) == bits(b) || (a != a && b != b); }
 
-// all 2^32 x: div_sqrt2f_lx(x) == x / 1.4142135f
-long long lx_test_div_sqrt2_mismatches(void) {
+// all 2^32 x: div_sqrt2f_lx(x) against x / 1.4142135f.  out[0] = mismatches with |x| >= 2^-100 (none
+// allowed), out[1] = mismatches below (results near the denormal range, where x * zl underflows)
+void lx_test_div_sqrt2_mismatches(long long *out) {
     const volatile float c = 1.41421353816986083984375f;
+    long long big = 0, tiny = 0;
+#pragma omp parallel for reduction(+ : big, tiny) schedule(static)
+    for (long long u = 0; u < (1ll << 32); u++) {
+        float x = fbits((uint32_t)u);
+        if (!same(lx::div_sqrt2f_lx(x), x / c)) {
+            if (__builtin_fabsf(x) >= 0x1p-100f) big++;
+            else tiny++;
+        }
+    }
+    out[0] = big;
+    out[1] = tiny;
+}
+
+// every float x in [lo, hi] (lo <= hi, both finite): expf_core_lx(x) == expf(x)
+long long lx_test_expf_core_range_mismatches(float lo, float hi) {
+    lx::ExpTable tab;
+    lx::exp_table_fill_host(tab);
     long long bad = 0;
 #pragma omp parallel for reduction(+ : bad) schedule(static)
     for (long long u = 0; u < (1ll << 32); u++) {
         float x = fbits((uint32_t)u);
-        if (!same(lx::div_sqrt2f_lx(x), x / c)) bad++;
+        if (!(x >= lo && x <= hi)) continue;
+        if (!same(lx::expf_core_lx(x, tab), expf(x))) bad++;
     }
     return bad;
 }
