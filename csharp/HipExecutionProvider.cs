@@ -87,6 +87,43 @@ public unsafe class HipExecutionProvider : Runtime
         };
     }
 
+    #region Profiling
+    static bool deviceProfiling;
+    static readonly List<(OpProfile Stage, int Record)> pendingMath = new();
+
+    /// <summary>Profiler.StartOpStage(OpStage.Math) (Profiler.cs:71-80) for a call about to run on the device, as
+    /// the reference opens it before its arithmetic (CPUExecutionProvider.cs:92-103).  The stopwatch would time
+    /// only the launch, so the library records the call's device time between two HIP events
+    /// (lx_set_op_profiling) and ResolveDeviceProfile writes it into this stage.</summary>
+    static void MathStage()
+    {
+        if (!Profiler.Enabled) return;
+        if (!deviceProfiling)
+        {
+            HipNative.Check(HipNative.lx_set_op_profiling(1), "lx_set_op_profiling");
+            deviceProfiling = true;
+        }
+        Profiler.StartOpStage(OpStage.Math);
+        pendingMath.Add((Profiler.CurrentOpProfile, HipNative.lx_op_profile_count()));
+    }
+
+    /// <summary>Writes the device time of every call made since the last resolve into its OpStage.Math record
+    /// (waiting for the calls' last events), then clears the library's records.  The graph executor calls it
+    /// after its node loop when Profiler.Enabled, before the profile is read.</summary>
+    public static void ResolveDeviceProfile()
+    {
+        foreach (var (stage, record) in pendingMath)
+        {
+            if (record >= HipNative.lx_op_profile_count()) continue;
+            LxOpProfile p;
+            HipNative.Check(HipNative.lx_op_profile(record, &p), "lx_op_profile");
+            stage.Time = TimeSpan.FromMilliseconds(p.MathMs);
+        }
+        pendingMath.Clear();
+        HipNative.Check(HipNative.lx_op_profile_reset(), "lx_op_profile_reset");
+    }
+    #endregion
+
     delegate int BinaryFn(LxTensor* a, LxTensor* b, LxTensor* y);
     delegate int UnaryFn(LxTensor* a, LxTensor* y);
 
@@ -99,6 +136,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (A.ElementType != B.ElementType) return WrongInputType(op, nameof(B), "Input tensors must be of the same type.", B);
         using var args = new Args();
         LxTensor a = args.In(A), b = args.In(B), y = default;
+        MathStage();
         return Done(op, fn(&a, &b, &y), y, A, B);
     }
 
@@ -107,6 +145,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (X is null) return MissingInput(op, name);
         using var args = new Args();
         LxTensor x = args.In(X), y = default;
+        MathStage();
         return Done(op, fn(&x, &y), y, X, null, name);
     }
     #endregion
@@ -167,6 +206,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (B is null) return MissingInput(op, nameof(B));
         using var args = new Args();
         LxTensor a = args.In(A), b = args.In(B), y = default;
+        MathStage();
         return Done(op, HipNative.lx_MatMul(&a, &b, &y), y, A, B);
     }
 
@@ -184,6 +224,7 @@ public unsafe class HipExecutionProvider : Runtime
         LxTensor x = args.In(data), y = default;
         var p = perm?.Select(v => (long)v).ToArray() ?? new long[1];
         int st;
+        MathStage();
         fixed (long* pp = p) st = HipNative.lx_Transpose(&x, pp, perm?.Length ?? -1, &y);
         if (st == 0 && y.Owns == 0) return Success(op, DeviceTensor.From(data));
         return Done(op, st, y, data);
@@ -203,6 +244,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (input is null) return MissingInput(op, nameof(input));
         using var args = new Args();
         LxTensor x = args.In(input), y = default;
+        MathStage();
         return Done(op, HipNative.lx_Cast(&x, to, &y), y, input);
     }
 
@@ -218,6 +260,7 @@ public unsafe class HipExecutionProvider : Runtime
         for (int i = 0; i < inputs.Length; i++) ts[i] = args.In(inputs[i]);
         LxTensor y = default;
         int st;
+        MathStage();
         fixed (LxTensor* p = ts)
         {
             var ptrs = stackalloc LxTensor*[Math.Max(ts.Length, 1)];
@@ -239,6 +282,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (indices.Rank > data.Rank) return WrongInputShape(op, nameof(indices), data.Rank, indices);
         using var args = new Args();
         LxTensor x = args.In(data), i = args.In(indices), y = default;
+        MathStage();
         return Done(op, HipNative.lx_Gather(&x, &i, axis ?? 0, axis.HasValue ? 1 : 0, &y), y, data, null, nameof(data));
     }
 
@@ -263,6 +307,7 @@ public unsafe class HipExecutionProvider : Runtime
         using var args = new Args();
         LxTensor x = args.In(data), y = default;
         int st;
+        MathStage();
         fixed (long* ps = s, pe = e, pa = a, pp = p)
             st = HipNative.lx_Slice(&x, ps, s.Length, pe, e.Length, pa, axes is null ? -1 : a.Length, pp,
                                     steps is null ? -1 : p.Length, &y);
@@ -298,6 +343,7 @@ public unsafe class HipExecutionProvider : Runtime
         using var args = new Args();
         LxTensor x = args.In(data), y = default;
         int st;
+        MathStage();
         fixed (long* pa = ax) st = fn(&x, pa, axes is null ? -1 : ax.Length, keepdims ?? -1, noop ?? -1, &y);
         return Done(op, st, y, data, null, nameof(data));
     }
@@ -318,6 +364,7 @@ public unsafe class HipExecutionProvider : Runtime
         using var args = new Args();
         LxTensor x = args.In(data), y = default;
         int st;
+        MathStage();
         fixed (long* pa = ax) st = HipNative.lx_ReduceMax(&x, pa, axes is null ? -1 : ax.Length, _keep_dims ?? -1, &y);
         return Done(op, st, y, data, null, nameof(data));
     }
@@ -328,6 +375,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (input is null) return MissingInput(op, nameof(input));
         using var args = new Args();
         LxTensor x = args.In(input), y = default;
+        MathStage();
         return Done(op, HipNative.lx_Softmax(&x, _axis ?? -1, _axis.HasValue ? 1 : 0, &y), y, input, null, nameof(input));
     }
 
@@ -357,6 +405,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (beta is null) return MissingInput(OpType.Add, "B");
         using var args = new Args();
         LxTensor x = args.In(X), g = args.In(gamma), b = args.In(beta), y = default;
+        MathStage();
         return Done(op, HipNative.lx_LayerNormDecomposed(&x, &g, &b, eps, &y), y, X, gamma, "data");
     }
 
@@ -367,6 +416,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (mask is null) return MissingInput(OpType.Add, "B");
         using var args = new Args();
         LxTensor s = args.In(S), m = args.In(mask), y = default;
+        MathStage();
         return Done(op, HipNative.lx_AddSoftmax(&s, &m, axis, &y), y, S, mask, "input");
     }
 
@@ -379,6 +429,7 @@ public unsafe class HipExecutionProvider : Runtime
         using var args = new Args();
         LxTensor a = args.In(A), b = args.In(B), c = args.In(bias), y = default;
         LxTensor r = residual is null ? default : args.In(residual);
+        MathStage();
         return Done(op, HipNative.lx_MatMulAdd(&a, &b, &c, residual is null ? null : &r, &y), y, A, B);
     }
 
@@ -391,6 +442,7 @@ public unsafe class HipExecutionProvider : Runtime
         if (bias is null) return MissingInput(OpType.Add, "B");
         using var args = new Args();
         LxTensor a = args.In(A), b = args.In(B), c = args.In(bias), y = default;
+        MathStage();
         return Done(op, HipNative.lx_MatMulAddGelu(&a, &b, &c, &y), y, A, B);
     }
     #endregion

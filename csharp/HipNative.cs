@@ -64,6 +64,22 @@ public unsafe struct LxNodeProfile
     public fixed byte Op[36];    // NUL-terminated ASCII
     public double MathMs;        // OpStage.Math: device time between the node's boundary events
     public double HostMs;        // host time of the node's dispatch
+    public double StartMs;       // device time from the execution's first boundary event to the node's start
+
+    public string OpName()
+    {
+        fixed (byte* p = Op) return Marshal.PtrToStringAnsi((IntPtr)p) ?? "";
+    }
+}
+
+/// <summary>lx_call_profile: one operator call made while lx_set_op_profiling is on (its OpStage.Math stage).</summary>
+[StructLayout(LayoutKind.Sequential)]
+public unsafe struct LxOpProfile
+{
+    public fixed byte Op[36];    // NUL-terminated ASCII
+    public double MathMs;        // device time between the HIP events around the call's launches
+    public double HostMs;        // host time of the call
+    public double StartMs;       // device time from the first record since the last reset
 
     public string OpName()
     {
@@ -81,6 +97,10 @@ internal static unsafe class HipNative
     [DllImport(Lib)] public static extern IntPtr lx_last_error();
     [DllImport(Lib)] public static extern IntPtr lx_version();
     [DllImport(Lib)] public static extern int lx_set_stream(IntPtr hipStream);
+    [DllImport(Lib)] public static extern int lx_set_op_profiling(int enabled);
+    [DllImport(Lib)] public static extern int lx_op_profile_count();
+    [DllImport(Lib)] public static extern int lx_op_profile(int i, LxOpProfile* p);
+    [DllImport(Lib)] public static extern int lx_op_profile_reset();
     [DllImport(Lib)] public static extern IntPtr lx_get_stream();
     [DllImport(Lib)] public static extern int lx_synchronize();
     [DllImport(Lib)] public static extern long lx_dtype_size(int dtype);

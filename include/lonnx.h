@@ -231,6 +231,27 @@ enum { LX_CHAIN_ADD = 0, LX_CHAIN_SUB = 1, LX_CHAIN_MUL = 2, LX_CHAIN_DIV = 3, L
 int lx_ElementwiseChain(const lx_tensor *const *inputs, int32_t n_in, const int32_t *ops, const int32_t *operands,
                         int32_t n_ops, lx_tensor *Y);
 
+/* ---- operator profiling: the OpStage.Math stage of eager calls ------------------
+ * The reference's operators open profiler stages as they go (Profiler.StartOpStage, Profiler.cs:71-80;
+ * CPUExecutionProvider.cs:92-103) and its stopwatch closes the last one, Math, when Node.Execute returns
+ * (ComputationalGraph.cs:241-243).  On the device a call returns after queueing its kernels, so a host
+ * clock would time the launch; these records time the device work instead.  While enabled, every
+ * operator call from outside the library (lx_Add ... lx_Slice and the fused operators; not the calls a
+ * graph execution makes, which lx_graph_set_profiling covers) appends one record with two HIP events on
+ * the library stream, before the call's first launch and after its last.  Nothing waits for them when the
+ * call returns: lx_op_profile waits for the record's second event.  Calls on a stream under capture are
+ * recorded untimed (math_ms 0).  Records accumulate until lx_op_profile_reset. */
+typedef struct lx_call_profile {
+    char op[36];         /* the operator, NUL-terminated (Add, ..., LayerNormDecomposed) */
+    double math_ms;      /* device time between the call's two events (OpStage.Math); 0 if not timed */
+    double host_ms;      /* host time spent in the call: validation, planning, launches (and any readback) */
+    double start_ms;     /* device time from the first timed record since the last reset to this one */
+} lx_call_profile;
+int lx_set_op_profiling(int32_t enabled);
+int32_t lx_op_profile_count(void);
+int lx_op_profile(int32_t i, lx_call_profile *out);
+int lx_op_profile_reset(void);
+
 /* ---- diagnostics (no reference counterpart) ---------------------------------
  * The HBM ceiling a read-only stream reaches on this GPU, the bound of the whole-tensor reductions:
  * reads `bytes` (a multiple of 16, 16-byte aligned) at src with nontemporal 16-byte loads and writes one
@@ -325,8 +346,9 @@ typedef struct lx_node_profile {
     int64_t node_id;     /* the node's position in the graph as built (a fused node: its last original node) */
     int32_t node_index;  /* its position in the current node list (lx_graph_node_info) */
     char op[36];         /* op type, NUL-terminated (a fused node: its fused op, e.g. LayerNormDecomposed) */
-    double math_ms;
-    double host_ms;
+    double math_ms;      /* device time between the node's boundary events (OpStage.Math); 0 if not timed */
+    double host_ms;      /* host time of the node's dispatch (OpStage.GraphOrchestration) */
+    double start_ms;     /* device time from the execution's first boundary event to this node's start */
 } lx_node_profile;
 int lx_graph_set_profiling(lx_graph *g, int32_t enabled);
 int32_t lx_graph_profile_count(const lx_graph *g);

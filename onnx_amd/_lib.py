@@ -50,6 +50,16 @@ class LxNodeProfile(ctypes.Structure):
         ("op", ctypes.c_char * 36),
         ("math_ms", ctypes.c_double),
         ("host_ms", ctypes.c_double),
+        ("start_ms", ctypes.c_double),
+    ]
+
+
+class LxOpProfile(ctypes.Structure):
+    _fields_ = [
+        ("op", ctypes.c_char * 36),
+        ("math_ms", ctypes.c_double),
+        ("host_ms", ctypes.c_double),
+        ("start_ms", ctypes.c_double),
     ]
 
 
@@ -78,6 +88,10 @@ SIGNATURES = {
     "lx_last_error": (_c.c_char_p, []),
     "lx_version": (_c.c_char_p, []),
     "lx_set_stream": (_c.c_int, [_c.c_void_p]),
+    "lx_set_op_profiling": (_c.c_int, [_c.c_int32]),
+    "lx_op_profile_count": (_c.c_int32, []),
+    "lx_op_profile": (_c.c_int, [_c.c_int32, _c.c_void_p]),
+    "lx_op_profile_reset": (_c.c_int, []),
     "lx_get_stream": (_c.c_void_p, []),
     "lx_synchronize": (_c.c_int, []),
     "lx_dtype_size": (_c.c_int64, [_c.c_int32]),

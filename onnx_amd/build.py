@@ -13,6 +13,10 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "liblonnx_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("LONNX_OFFLOAD_ARCH", "gfx950")
+if ARCH != "gfx950":
+    # the one-step reciprocal of Erf / GELU and the int32 division seed are proven exact with gfx950's
+    # v_rcp_f32 only (tests/native/rcp_check.hip checks every seed on the device)
+    raise SystemExit(f"liblonnx_hip is built for gfx950 only (LONNX_OFFLOAD_ARCH={ARCH})")
 
 SOURCES = ["lx_elementwise.hip", "lx_reduce.hip", "lx_softmax.hip", "lx_matmul.hip", "lx_movement.hip", "lx_probe.hip", "lx_api.cpp",
            "lx_pool.cpp", "lx_graph.cpp", "lx_onnx.cpp"]

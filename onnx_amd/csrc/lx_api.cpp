@@ -39,6 +39,7 @@ struct State {
     struct Mailbox *mail = nullptr;      // mapped, coherent pinned host memory
     struct Mailbox *mail_dev = nullptr;  // the same memory as the device addresses it
     uint64_t mail_seq = 0;
+    uint64_t scan_seq = 0;               // the divisor scans' sequence (Mailbox::scan)
 };
 // Small device-to-host reads (error records) land here: a one-block kernel copies the words and
 // then writes a sequence number, which the host polls.  One mailbox per library: calls are
@@ -47,6 +48,7 @@ constexpr int64_t kMailWords = 8192;  // 64 KiB: 4096 error records
 struct Mailbox {
     alignas(128) uint64_t seq;
     alignas(128) uint64_t words[kMailWords];
+    alignas(128) uint64_t scan[kDivScanSlots];  // one verdict per block of a divisor scan (k_div_scan)
 };
 
 State g;
@@ -60,7 +62,7 @@ thread_local std::string g_err;
 // call on a GPU shares that GPU's array, which keeps the last call's contents (nothing in it needs to
 // start at zero: partials and intermediates are written before they are read); calls that overlap on
 // one GPU (other streams, other threads) race.
-constexpr int64_t kScratchWsBytes = 2 << 20;    // partials: the reduction planner never needs more
+constexpr int64_t kScratchWsBytes = kReducePartialBytes;  // partials: the reduction planner caps them here
 constexpr int64_t kScratchTempBytes = 1 << 20;  // per intermediate slot
 constexpr int64_t kScratchBytes = kScratchWsBytes + 2 * kScratchTempBytes;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
@@ -403,6 +405,39 @@ int read_device(const void *src, size_t bytes, void *dst, bool reset_src) {
     return LX_OK;
 }
 
+// Waits for the `blocks` slots of the divisor scan `seq` (the watchdog of read_device: every 50 us it asks
+// the stream whether work is pending) and ORs their verdict bits into *bits.
+int wait_div_scan(int blocks, uint64_t seq, uint32_t *bits) {
+    int seen = 0;
+    uint32_t acc = 0;
+    auto advance = [&] {
+        while (seen < blocks) {
+            const uint64_t v = __atomic_load_n(&g.mail->scan[seen], __ATOMIC_ACQUIRE);
+            if ((v >> 2) != seq) return false;
+            acc |= (uint32_t)(v & 3);
+            seen++;
+        }
+        return true;
+    };
+    const auto t0 = std::chrono::steady_clock::now();
+    auto next_query = std::chrono::microseconds(50);
+    for (uint32_t spin = 1; !advance(); spin++) {
+        __builtin_ia32_pause();
+        if (spin % 256) continue;
+        const auto dt = std::chrono::steady_clock::now() - t0;
+        if (dt < next_query) continue;
+        next_query = std::chrono::duration_cast<std::chrono::microseconds>(dt) + std::chrono::microseconds(50);
+        const hipError_t q = hipStreamQuery(g.stream);
+        if (q == hipSuccess) {
+            if (advance()) break;
+            return set_err(LX_ERR_HIP, "reading back device results: the stream finished without publishing them");
+        }
+        if (q != hipErrorNotReady) return hip_fail(q, "reading back device results");
+    }
+    *bits = acc;
+    return LX_OK;
+}
+
 // ---------------------------------------------------------------------------
 // broadcast planner
 // ---------------------------------------------------------------------------
@@ -581,8 +616,35 @@ int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     const bool int_div = op == kDiv && (A->dtype == LX_INT32 || A->dtype == LX_INT64 || A->dtype == LX_UINT8);
     ErrFlags *errs = g.errs;
     if (int_div && (st = check_begin(kCheckDiv, 0, &errs))) return st;
+    // An eager call must know before it returns whether an element divides by zero or overflows
+    // (CPUExecutionProvider.cs:177-206 throws from the call).  When the divisor is at most 1/16 of the
+    // output, a scan of the divisor alone, queued before the quotient kernel, answers that: with no zero
+    // and (signed) no minus one in B no element can fail, and the call returns as soon as the scan's
+    // blocks have stored their verdicts, while the quotient kernel runs.  Otherwise the call waits for the
+    // quotient kernel's own record, which names the first failing element.
+    const int64_t nb = numel(B);
+    const bool prescan = int_div && !t_defer_slot && nb > 0 && nb * 16 <= p.numel;
+    int scan_blocks = 0;
+    uint64_t scan_seq = 0;
+    if (prescan) {
+        scan_blocks = div_scan_blocks(nb, (int)es);
+        scan_seq = ++g.scan_seq;
+        HIPCHECK(launch_div_scan(A->dtype, B->data, nb, aligned16(B->data) ? 1 : 0, g.mail_dev->scan, scan_seq,
+                                 g.stream),
+                 "divisor scan");
+    }
     HIPCHECK(launch_binary(args, errs, g.stream), opn);
-    return int_div ? check_end(kCheckDiv, 0) : LX_OK;
+    if (!int_div) return LX_OK;
+    if (prescan) {
+        uint32_t bits = 0;
+        if ((st = wait_div_scan(scan_blocks, scan_seq, &bits))) return st;
+        if (bits == 0) {
+            // no element can fail, so the quotient kernel records nothing: the record stays cleared
+            g.errs_clean = true;
+            return LX_OK;
+        }
+    }
+    return check_end(kCheckDiv, 0);
 }
 
 int run_unary(const char *opn, int op, const lx_tensor *X, const char *xname, lx_tensor *Y) {
@@ -802,6 +864,84 @@ void api_defer_checks(ErrFlags *slot, DeferredCheck *rec) {
 int api_check_status(const DeferredCheck &rec, const ErrFlags &flags) { return check_status(rec.kind, rec.dst, flags); }
 bool api_layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X) { return layernorm_affine_fits(t, X); }
 int api_read_device(const void *src, size_t bytes, void *dst) { return read_device(src, bytes, dst); }
+
+// ---- eager operator profiling (lx_set_op_profiling) ----------------------------------------------------
+// The device twin of the OpStage.Math stage the reference's operators open (Profiler.StartOpStage,
+// Profiler.cs:71-80; CPUExecutionProvider.cs:92-103): while enabled, every operator call made from outside
+// the library appends one record with two HIP events recorded on the library stream, before the call's
+// first launch and after its last.  Nothing waits for them: a record's device time is read when the caller
+// asks for it, so consecutive calls stay asynchronous and their intervals tile the stream.  Calls made by
+// another operator or by a graph execution are not recorded (graphs have their own node profile).
+namespace {
+struct OpRecord {
+    std::string op;
+    hipEvent_t e0 = nullptr, e1 = nullptr;  // null: not timed (capture, or an event failed)
+    double host_ms = 0.0;
+};
+struct OpProfiler {
+    bool on = false;
+    std::vector<OpRecord> recs;
+    std::vector<hipEvent_t> spare;
+    hipEvent_t take() {
+        if (!spare.empty()) {
+            hipEvent_t e = spare.back();
+            spare.pop_back();
+            return e;
+        }
+        hipEvent_t e = nullptr;
+        return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+    }
+    void give(hipEvent_t e) {
+        if (e) spare.push_back(e);
+    }
+    void clear() {
+        for (auto &r : recs) {
+            give(r.e0);
+            give(r.e1);
+        }
+        recs.clear();
+    }
+    void destroy() {
+        clear();
+        for (hipEvent_t e : spare) (void)hipEventDestroy(e);
+        spare.clear();
+    }
+} g_ops;
+thread_local int t_op_depth = 0;
+}  // namespace
+
+OpScope::OpScope(const char *op) {
+    if (t_op_depth++ != 0 || !op || !g_ops.on || !g.init) return;
+    active_ = true;
+    op_ = op;
+    h0_ = std::chrono::steady_clock::now();
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g.stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return;
+    e0_ = g_ops.take();
+    if (e0_ && hipEventRecord(e0_, g.stream) != hipSuccess) {
+        g_ops.give(e0_);
+        e0_ = nullptr;
+    }
+}
+
+OpScope::~OpScope() {
+    t_op_depth--;
+    if (!active_) return;
+    OpRecord r;
+    r.op = op_;
+    if (e0_) {
+        hipEvent_t e1 = g_ops.take();
+        if (e1 && hipEventRecord(e1, g.stream) == hipSuccess) {
+            r.e0 = e0_;
+            r.e1 = e1;
+        } else {
+            g_ops.give(e0_);
+            g_ops.give(e1);
+        }
+    }
+    r.host_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0_).count();
+    g_ops.recs.push_back(std::move(r));
+}
 }  // namespace lx
 
 // ===========================================================================
@@ -822,36 +962,50 @@ int lx_init(int32_t device) {
     HIPCHECK(hipGetDeviceCount(&count), "hipGetDeviceCount");
     if (device < 0 || device >= count)
         return set_err(LX_ERR_INVALID_ARGUMENT, "Device %d does not exist (%d devices).", device, count);
-    HIPCHECK(hipSetDevice(device), "hipSetDevice");
-    // a blocking stream: it orders with the legacy default stream, so work a caller
-    // enqueues there (torch's default stream, events around library calls) sees ours
-    HIPCHECK(hipStreamCreateWithFlags(&g.own_stream, hipStreamDefault), "hipStreamCreate");
-    g.stream = g.own_stream;
-    HIPCHECK(hipMalloc(&g.errs, sizeof(ErrFlags)), "hipMalloc(errors)");
-    HIPCHECK(hipHostMalloc((void **)&g.mail, sizeof(Mailbox), hipHostMallocMapped | hipHostMallocCoherent),
-             "hipHostMalloc(mailbox)");
-    HIPCHECK(hipHostGetDevicePointer((void **)&g.mail_dev, g.mail, 0), "hipHostGetDevicePointer(mailbox)");
-    g.mail->seq = 0;
-    g.mail_seq = 0;
-
     if (device >= kMaxDevices)
         return set_err(LX_ERR_NOT_SUPPORTED, "Devices beyond %d are not supported.", kMaxDevices - 1);
+    HIPCHECK(hipSetDevice(device), "hipSetDevice");
+    // every resource below is released again if a later step fails, so a failed lx_init leaves nothing
+    // behind and can be retried
+    State s;
+    auto undo = [&s](int st) {
+        if (s.workspace) (void)hipFree(s.workspace);
+        if (s.errs) (void)hipFree(s.errs);
+        if (s.mail) (void)hipHostFree(s.mail);
+        if (s.own_stream) (void)hipStreamDestroy(s.own_stream);
+        return st;
+    };
+    hipError_t e;
+    // a blocking stream: it orders with the legacy default stream, so work a caller
+    // enqueues there (torch's default stream, events around library calls) sees ours
+    if ((e = hipStreamCreateWithFlags(&s.own_stream, hipStreamDefault)) != hipSuccess)
+        return undo(hip_fail(e, "hipStreamCreate"));
+    if ((e = hipMalloc(&s.errs, sizeof(ErrFlags))) != hipSuccess) return undo(hip_fail(e, "hipMalloc(errors)"));
+    if ((e = hipHostMalloc((void **)&s.mail, sizeof(Mailbox), hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess)
+        return undo(hip_fail(e, "hipHostMalloc(mailbox)"));
+    if ((e = hipHostGetDevicePointer((void **)&s.mail_dev, s.mail, 0)) != hipSuccess)
+        return undo(hip_fail(e, "hipHostGetDevicePointer(mailbox)"));
     if (!scratch_addr[device]) {  // once per device, with the device current
         void *p = nullptr;
-        HIPCHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess)
+            return undo(hip_fail(e, "hipGetSymbolAddress(scratch)"));
         scratch_addr[device] = p;
     }
-
-    g.device = device;
-    g.init = true;
-    int st = ensure_workspace(1 << 20);
-    if (st) return st;
+    if ((e = hipMalloc(&s.workspace, 1 << 20)) != hipSuccess) return undo(hip_fail(e, "hipMalloc(workspace)"));
+    s.ws_bytes = 1 << 20;
+    s.mail->seq = 0;
+    for (int i = 0; i < kDivScanSlots; i++) s.mail->scan[i] = 0;
+    s.stream = s.own_stream;
+    s.device = device;
+    s.init = true;
+    g = s;
     return LX_OK;
 }
 
 int lx_shutdown(void) {
     if (!g.init) return LX_OK;
     (void)hipDeviceSynchronize();
+    g_ops.destroy();
     (void)pool_trim(g.stream);
     if (g.workspace) (void)hipFree(g.workspace);
     if (g.errs) (void)hipFree(g.errs);
@@ -859,6 +1013,41 @@ int lx_shutdown(void) {
     if (g.mail) (void)hipHostFree(g.mail);
     if (g.own_stream) (void)hipStreamDestroy(g.own_stream);
     g = State();
+    return LX_OK;
+}
+
+int lx_set_op_profiling(int32_t enabled) {
+    g_ops.on = enabled != 0;
+    return LX_OK;
+}
+
+int32_t lx_op_profile_count(void) { return (int32_t)g_ops.recs.size(); }
+
+int lx_op_profile(int32_t i, lx_call_profile *out) {
+    if (!out) return set_err(LX_ERR_INVALID_ARGUMENT, "null argument");
+    if (i < 0 || i >= (int32_t)g_ops.recs.size()) return set_err(LX_ERR_INVALID_ARGUMENT, "invalid profile record index");
+    const OpRecord &r = g_ops.recs[i];
+    memset(out, 0, sizeof *out);
+    snprintf(out->op, sizeof out->op, "%s", r.op.c_str());
+    out->host_ms = r.host_ms;
+    if (!r.e0) return LX_OK;
+    HIPCHECK(hipEventSynchronize(r.e1), "hipEventSynchronize");
+    float ms = 0.0f;
+    HIPCHECK(hipEventElapsedTime(&ms, r.e0, r.e1), "hipEventElapsedTime");
+    out->math_ms = ms;
+    // the start offset from the first timed record since the last reset
+    for (const OpRecord &f : g_ops.recs) {
+        if (!f.e0) continue;
+        float at = 0.0f;
+        HIPCHECK(hipEventElapsedTime(&at, f.e0, r.e0), "hipEventElapsedTime");
+        out->start_ms = at;
+        break;
+    }
+    return LX_OK;
+}
+
+int lx_op_profile_reset(void) {
+    g_ops.clear();
     return LX_OK;
 }
 
@@ -976,15 +1165,16 @@ int lx_plan_broadcast(int32_t ra, const int64_t *da, int32_t rb, const int64_t *
     return st;
 }
 
-int lx_Add(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kAdd, A, B, Y); }
-int lx_Sub(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kSub, A, B, Y); }
-int lx_Mul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kMul, A, B, Y); }
-int lx_Div(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kDiv, A, B, Y); }
-int lx_Pow(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { return run_binary(kPow, A, B, Y); }
-int lx_Sqrt(const lx_tensor *A, lx_tensor *Y) { return run_unary("Sqrt", kSqrt, A, "A", Y); }
-int lx_Erf(const lx_tensor *X, lx_tensor *Y) { return run_unary("Erf", kErf, X, "X", Y); }
+int lx_Add(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { OpScope prof("Add"); return run_binary(kAdd, A, B, Y); }
+int lx_Sub(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { OpScope prof("Sub"); return run_binary(kSub, A, B, Y); }
+int lx_Mul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { OpScope prof("Mul"); return run_binary(kMul, A, B, Y); }
+int lx_Div(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { OpScope prof("Div"); return run_binary(kDiv, A, B, Y); }
+int lx_Pow(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) { OpScope prof("Pow"); return run_binary(kPow, A, B, Y); }
+int lx_Sqrt(const lx_tensor *A, lx_tensor *Y) { OpScope prof("Sqrt"); return run_unary("Sqrt", kSqrt, A, "A", Y); }
+int lx_Erf(const lx_tensor *X, lx_tensor *Y) { OpScope prof("Erf"); return run_unary("Erf", kErf, X, "X", Y); }
 
 int lx_Cast(const lx_tensor *X, int64_t to, lx_tensor *Y) {
+    OpScope prof("Cast");
     REQUIRE_INIT();
     if (!X) return missing_input("Cast", "input");
     int st;
@@ -1012,6 +1202,7 @@ int lx_Cast(const lx_tensor *X, int64_t to, lx_tensor *Y) {
 
 int lx_ReduceSum(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
                  lx_tensor *Y) {
+    OpScope prof("ReduceSum");
     (void)noop;  // read but unused by TensorOps.ReduceSum (TensorOps.cs:1615)
     return run_reduce("ReduceSum", kSum, X, axes, n_axes, keepdims, Y);
 }
@@ -1026,19 +1217,23 @@ int lx_ReduceSum_noalloc(const lx_tensor *X, const int64_t *axes, int32_t n_axes
 
 int lx_ReduceMean(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, int32_t noop,
                   lx_tensor *Y) {
+    OpScope prof("ReduceMean");
     (void)noop;
     return run_reduce("ReduceMean", kMean, X, axes, n_axes, keepdims, Y);
 }
 
 int lx_ReduceMax(const lx_tensor *X, const int64_t *axes, int32_t n_axes, int32_t keepdims, lx_tensor *Y) {
+    OpScope prof("ReduceMax");
     return run_reduce("ReduceMax", kMax, X, axes, n_axes, keepdims, Y);
 }
 
 int lx_Softmax(const lx_tensor *X, int32_t axis, int32_t has_axis, lx_tensor *Y) {
+    OpScope prof("Softmax");
     return run_softmax(X, nullptr, axis, has_axis, Y, "Softmax");
 }
 
 int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_tensor *Y) {
+    OpScope prof("AddSoftmax");
     REQUIRE_INIT();
     if (!S) return missing_input("Add", "A");
     if (!mask) return missing_input("Add", "B");
@@ -1047,6 +1242,7 @@ int lx_AddSoftmax(const lx_tensor *S, const lx_tensor *mask, int32_t axis, lx_te
 
 int lx_ScaleAddSoftmax(const lx_tensor *S, const lx_tensor *scale, int32_t divide, const lx_tensor *mask, int32_t axis,
                        lx_tensor *Y) {
+    OpScope prof("ScaleAddSoftmax");
     REQUIRE_INIT();
     if (!S) return missing_input(divide ? "Div" : "Mul", "A");
     if (!scale) return missing_input(divide ? "Div" : "Mul", "B");
@@ -1057,11 +1253,13 @@ int lx_read_probe(const void *src, int64_t bytes, void *out, int64_t out_bytes) 
     REQUIRE_INIT();
     if (!src || !out || bytes < 0 || out_bytes < 4) return set_err(LX_ERR_INVALID_ARGUMENT, "invalid probe arguments");
     if (bytes % 16 || !aligned16(src)) return set_err(LX_ERR_INVALID_ARGUMENT, "the probe reads whole aligned 16-byte vectors");
+    if ((uintptr_t)out % 4) return set_err(LX_ERR_INVALID_ARGUMENT, "the probe writes 32-bit words: out must be 4-byte aligned");
     HIPCHECK(launch_read_probe(src, bytes, (uint32_t *)out, out_bytes / 4, g.stream), "read probe");
     return LX_OK;
 }
 
 int lx_GeluErf(const lx_tensor *X, lx_tensor *Y) {
+    OpScope prof("GeluErf");
     REQUIRE_INIT();
     if (!X) return missing_input("Div", "A");
     int st;
@@ -1091,6 +1289,7 @@ int lx_GeluErf(const lx_tensor *X, lx_tensor *Y) {
 
 int lx_ElementwiseChain(const lx_tensor *const *inputs, int32_t n_in, const int32_t *ops, const int32_t *operands,
                         int32_t n_ops, lx_tensor *Y) {
+    OpScope prof("ElementwiseChain");
     REQUIRE_INIT();
     if (!inputs || n_in < 1 || n_in > kChainMaxIn)
         return set_err(LX_ERR_INVALID_ARGUMENT, "An elementwise chain takes 1 to %d inputs.", kChainMaxIn);
@@ -1191,6 +1390,7 @@ int lx_ElementwiseChain(const lx_tensor *const *inputs, int32_t n_in, const int3
 
 int lx_LayerNormDecomposed(const lx_tensor *X, const lx_tensor *gamma, const lx_tensor *beta, float eps,
                            lx_tensor *Y) {
+    OpScope prof("LayerNormDecomposed");
     REQUIRE_INIT();
     if (!X) return missing_input("ReduceMean", "data");
     if (!gamma) return missing_input("Mul", "B");
@@ -1609,6 +1809,7 @@ int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vect
 }  // namespace
 
 extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
+    OpScope prof("MatMul");
     REQUIRE_INIT();
     if (!A) return missing_input("MatMul", "A");
     if (!B) return missing_input("MatMul", "B");
@@ -1679,10 +1880,12 @@ int matmul_add_run(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias
 
 extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
                             lx_tensor *Y) {
+    OpScope prof("MatMulAdd");
     return matmul_add_run(A, B, bias, residual, false, Y);
 }
 
 extern "C" int lx_MatMulAddGelu(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, lx_tensor *Y) {
+    OpScope prof("MatMulAddGelu");
     return matmul_add_run(A, B, bias, nullptr, true, Y);
 }
 
@@ -1716,6 +1919,7 @@ int view_copy(int dt, const void *src, void *dst, const ViewCopyArgs &a) {
 }  // namespace
 
 extern "C" int lx_Transpose(const lx_tensor *data, const int64_t *perm, int32_t n_perm, lx_tensor *Y) {
+    OpScope prof("Transpose");
     REQUIRE_INIT();
     if (!data) return missing_input("Transpose", "data");
     int st;
@@ -1781,6 +1985,7 @@ extern "C" int lx_Transpose(const lx_tensor *data, const int64_t *perm, int32_t 
 }
 
 extern "C" int lx_Concat(const lx_tensor *const *inputs, int32_t n, int32_t axis, int32_t has_axis, lx_tensor *Y) {
+    OpScope prof("Concat");
     REQUIRE_INIT();
     if (!inputs || n < 0) return missing_input("Concat", "inputs");
     int st;
@@ -1845,6 +2050,7 @@ extern "C" int lx_Concat(const lx_tensor *const *inputs, int32_t n, int32_t axis
 
 extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_t axis, int32_t has_axis,
                          lx_tensor *Y) {
+    OpScope prof("Gather");
     REQUIRE_INIT();
     if (!data) return missing_input("Gather", "data");
     if (!indices) return missing_input("Gather", "indices");
@@ -1895,6 +2101,7 @@ extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_
 extern "C" int lx_Slice(const lx_tensor *data, const int64_t *starts, int32_t n_starts, const int64_t *ends,
                         int32_t n_ends, const int64_t *axes, int32_t n_axes, const int64_t *steps, int32_t n_steps,
                         lx_tensor *Y) {
+    OpScope prof("Slice");
     REQUIRE_INIT();
     if (!data) return missing_input("Slice", "data");
     if (!starts || n_starts < 0) return missing_input("Slice", "starts");

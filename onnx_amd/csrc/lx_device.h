@@ -6,6 +6,13 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+// The exact float reciprocal of Erf / GELU (recip_newton1: one Newton step) and the int32 division seed
+// are proven with gfx950's v_rcp_f32 (every seed checked on that device); another architecture's
+// reciprocal could land on the significands where one step is not exact.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "liblonnx_hip device code is built for gfx950 only"
+#endif
 #include <stdint.h>
 
 #include <type_traits>

@@ -125,6 +125,86 @@ hipError_t launch_publish(const uint64_t *src, int64_t n, uint64_t *dst, uint64_
     return hipGetLastError();
 }
 
+constexpr int kDivScanU = 2;      // vectors per lane, all loaded before any is tested
+constexpr int kDivScanBlock = 1024;
+
+// Eager integer Div whose divisor is much smaller than its output: the divisor alone decides whether the
+// call can throw (a zero divides by zero, and for signed types a minus one can overflow against MIN).
+// Each block ORs what its lanes find (bit 0: a zero, bit 1: a minus one) and stores (seq << 2) | bits into
+// its own slot of mapped host memory with one relaxed system-scope store: the verdict is the stored word
+// itself, so no fence orders anything before it, and no block waits for another.  The loads are ordinary
+// (cacheable): the quotient kernel queued behind reads the same divisor.
+template <typename T>
+__global__ __launch_bounds__(kDivScanBlock) void k_div_scan(const T *__restrict__ b, int64_t n, int vec,
+                                                     uint64_t *slots, uint64_t seq) {
+    constexpr int V = 16 / (int)sizeof(T);
+    constexpr bool kSigned = std::is_signed<T>::value;
+    bool zero = false, minus1 = false;
+    const int64_t nv = vec ? n / V : 0;
+    // kDivScanU vectors per lane issued before any is tested, in 1024-lane blocks: the scan is one round
+    // trip of many waves, not a chain of them (C4's 8 MB int64 divisor is one step of 256 blocks; with
+    // 256-lane blocks and eight rounds of loads it took 6.5 us, with 256-lane blocks and eight vectors
+    // per lane about 4)
+    const int64_t step = (int64_t)gridDim.x * kDivScanBlock * kDivScanU;
+    for (int64_t i0 = (int64_t)blockIdx.x * kDivScanBlock * kDivScanU + threadIdx.x; i0 < nv; i0 += step) {
+        Vec<T, V> v[kDivScanU];
+#pragma unroll
+        for (int u = 0; u < kDivScanU; u++)
+            if (i0 + u * kDivScanBlock < nv) v[u] = vload<T, V>(b + (i0 + u * kDivScanBlock) * V);
+#pragma unroll
+        for (int u = 0; u < kDivScanU; u++) {
+            if (i0 + u * kDivScanBlock < nv) {
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    zero = zero || v[u].v[k] == (T)0;
+                    if constexpr (kSigned) minus1 = minus1 || v[u].v[k] == (T)-1;
+                }
+            }
+        }
+    }
+    const int64_t stride = (int64_t)gridDim.x * kDivScanBlock;
+    for (int64_t i = nv * V + (int64_t)blockIdx.x * kDivScanBlock + threadIdx.x; i < n; i += stride) {
+        zero = zero || b[i] == (T)0;
+        if constexpr (kSigned) minus1 = minus1 || b[i] == (T)-1;
+    }
+    __shared__ uint32_t waves[kDivScanBlock / 64];
+    const uint32_t w = (__ballot(zero) ? 1u : 0u) | (__ballot(minus1) ? 2u : 0u);
+    if ((threadIdx.x & 63) == 0) waves[threadIdx.x >> 6] = w;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t all = 0;
+#pragma unroll
+        for (int i = 0; i < kDivScanBlock / 64; i++) all |= waves[i];
+        __hip_atomic_store(slots + blockIdx.x, (seq << 2) | all, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+int div_scan_blocks(int64_t n, int esize) {
+    const int64_t vecs = (n * esize + 15) / 16;
+    const int64_t g = (vecs + kDivScanBlock * kDivScanU - 1) / (kDivScanBlock * kDivScanU);
+    return (int)std::max<int64_t>(1, std::min<int64_t>(g, kDivScanSlots));
+}
+
+hipError_t launch_div_scan(int dtype, const void *b, int64_t n, int vec, uint64_t *slots, uint64_t seq,
+                           hipStream_t s) {
+    switch (dtype) {
+    case kInt32:
+        hipLaunchKernelGGL(k_div_scan<int32_t>, dim3(div_scan_blocks(n, 4)), dim3(kDivScanBlock), 0, s, (const int32_t *)b, n,
+                           vec, slots, seq);
+        break;
+    case kInt64:
+        hipLaunchKernelGGL(k_div_scan<int64_t>, dim3(div_scan_blocks(n, 8)), dim3(kDivScanBlock), 0, s, (const int64_t *)b, n,
+                           vec, slots, seq);
+        break;
+    case kUInt8:
+        hipLaunchKernelGGL(k_div_scan<uint8_t>, dim3(div_scan_blocks(n, 1)), dim3(kDivScanBlock), 0, s, (const uint8_t *)b, n,
+                           vec, slots, seq);
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 // Binary element operation with C# semantics.
 //   float/double: IEEE-754 round to nearest even (TensorOps.cs:241-297).

@@ -1388,10 +1388,13 @@ int report_device_failure(lx_graph *g, int j, int st) {
 // handed to the caller (who reads them after each replay) instead of read back here.
 // Per-node timing of one execution for lx_graph_set_profiling: boundary events on the library stream,
 // host time per node; finish() (also run by the destructor) waits for the last event and appends records.
+// Every executed node appends one record.  If an event cannot be recorded, timing stops there: the nodes
+// timed up to that point keep their device times and the later ones are appended with math_ms = 0.
 struct NodeProfiler {
     lx_graph *g;
     bool on;
-    int used = 0;
+    bool timing = true;  // every node so far has its end event
+    int used = 0;        // events recorded: the start event, then one per timed node
     std::vector<NodeProf> pend;
     NodeProfiler(lx_graph *gr, bool enabled) : g(gr), on(enabled) {}
     ~NodeProfiler() { finish(); }
@@ -1403,9 +1406,9 @@ struct NodeProfiler {
             if (r != hipSuccess) return fail(LX_ERR_HIP, fmt("hipEventCreate: %s", hipGetErrorString(r)));
             ev.push_back(x);
         }
-        *e = ev[used++];
-        hipError_t r = hipEventRecord(*e, api_stream());
+        hipError_t r = hipEventRecord(ev[used], api_stream());
         if (r != hipSuccess) return fail(LX_ERR_HIP, fmt("hipEventRecord: %s", hipGetErrorString(r)));
+        *e = ev[used++];
         return LX_OK;
     }
     int start() {
@@ -1421,20 +1424,22 @@ struct NodeProfiler {
         p.op = node.op;
         p.host_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - h0).count();
         hipEvent_t e;
-        if (event(&e) != LX_OK) {  // no timing for this execution from here on
-            on = false;
-            return;
-        }
+        if (timing && event(&e) != LX_OK) timing = false;
         pend.push_back(p);
     }
     void finish() {
         if (!on || pend.empty()) return;
         on = false;
         auto &ev = g->prof_events.ev;
-        if (hipEventSynchronize(ev[pend.size()]) != hipSuccess) return;
+        const int timed = used - 1;  // nodes whose end event was recorded
+        const bool ready = timed > 0 && hipEventSynchronize(ev[timed]) == hipSuccess;
         for (size_t i = 0; i < pend.size(); i++) {
-            float ms = 0.0f;
-            if (hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess) pend[i].math_ms = ms;
+            float ms = 0.0f, at = 0.0f;
+            if (ready && (int)i < timed && hipEventElapsedTime(&ms, ev[i], ev[i + 1]) == hipSuccess &&
+                hipEventElapsedTime(&at, ev[0], ev[i]) == hipSuccess) {
+                pend[i].math_ms = ms;
+                pend[i].start_ms = at;
+            }
             g->profile.push_back(pend[i]);
         }
     }
@@ -1552,6 +1557,7 @@ int lx_graph_profile(const lx_graph *g, int32_t i, lx_node_profile *out) {
     copy_str(p.op, out->op, (int32_t)sizeof out->op);
     out->math_ms = p.math_ms;
     out->host_ms = p.host_ms;
+    out->start_ms = p.start_ms;
     return LX_OK;
 }
 
@@ -1738,6 +1744,7 @@ int lx_graph_fuse(lx_graph *g, int32_t *n_fused) {
 
 int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs,
                      int32_t use_initializers) {
+    OpScope nested(nullptr);  // operators called by the graph are its nodes, not eager calls
     if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
     if (!g || n < 0 || (n > 0 && !inputs)) return failure("null argument");
     return execute_impl(g, n, names, inputs, use_initializers, nullptr);
@@ -1745,6 +1752,7 @@ int lx_graph_execute(lx_graph *g, int32_t n, const char *const *names, const lx_
 
 int lx_graph_capture(lx_graph *g, int32_t n, const char *const *names, const lx_tensor *inputs,
                      int32_t use_initializers) {
+    OpScope nested(nullptr);  // operators called by the graph are its nodes, not eager calls
     if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
     if (!g || n < 0 || (n > 0 && !inputs)) return failure("null argument");
     g->capture.reset();
@@ -1795,6 +1803,7 @@ int lx_graph_capture(lx_graph *g, int32_t n, const char *const *names, const lx_
 }
 
 int lx_graph_replay(lx_graph *g) {
+    OpScope nested(nullptr);  // operators called by the graph are its nodes, not eager calls
     if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
     if (!g) return failure("null argument");
     if (!g->capture) return fail(LX_ERR_INVALID_ARGUMENT, "The graph has no captured execution.");
@@ -1817,6 +1826,7 @@ int lx_graph_release_capture(lx_graph *g) {
 
 int lx_graph_execute_node(lx_graph *g, const char *node, int32_t n, const char *const *names, const lx_tensor *inputs,
                           int32_t use_initializers) {
+    OpScope nested(nullptr);  // operators called by the graph are its nodes, not eager calls
     if (!api_initialized()) return fail(LX_ERR_NOT_INITIALIZED, "lx_init has not been called");
     if (!g || !node || n < 0 || (n > 0 && !inputs)) return failure("null argument");
     const GNode *nd = nullptr;

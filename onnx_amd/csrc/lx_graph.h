@@ -92,6 +92,7 @@ struct NodeProf {
     std::string op;
     double math_ms = 0.0;
     double host_ms = 0.0;
+    double start_ms = 0.0;   // device time from the execution's first boundary event to this node's start
 };
 
 // HIP events reused by profiled executions (destroyed with the graph).

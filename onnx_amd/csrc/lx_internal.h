@@ -4,6 +4,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <string>
 
 #include "../../include/lonnx.h"
@@ -11,6 +12,23 @@
 namespace lx {
 
 int api_set_error(int code, const std::string &message);  // sets lx_last_error, returns code
+
+// One operator call for lx_set_op_profiling: constructed at the top of an exported operator, it records
+// the call when profiling is on and the call is not nested in another operator or a graph execution (the
+// graph entry points hold an OpScope(nullptr), which records nothing and marks what runs inside as nested).
+class OpScope {
+  public:
+    explicit OpScope(const char *op);
+    ~OpScope();
+    OpScope(const OpScope &) = delete;
+    OpScope &operator=(const OpScope &) = delete;
+
+  private:
+    bool active_ = false;
+    const char *op_ = nullptr;
+    hipEvent_t e0_ = nullptr;
+    std::chrono::steady_clock::time_point h0_;
+};
 bool api_initialized();
 hipStream_t api_stream();
 int64_t api_esize(int dtype);

@@ -57,6 +57,13 @@ hipError_t launch_reset_errs(ErrFlags *e, hipStream_t s);
 // reset: null, or src itself, whose words are then set to all ones once copied.
 hipError_t launch_publish(const uint64_t *src, int64_t n, uint64_t *dst, uint64_t *seq_dst, uint64_t seq,
                           uint64_t *reset, hipStream_t s);
+// Eager integer Div: scans the divisor b (n elements of dtype, 16-byte vectors when vec) for 0 and, for
+// signed types, -1; block i stores (seq << 2) | bits (bit 0: a zero, bit 1: a minus one) into slots[i] of
+// mapped host memory.  div_scan_blocks gives the number of blocks (slots) a launch uses.
+constexpr int kDivScanSlots = 256;
+int div_scan_blocks(int64_t n, int esize);
+hipError_t launch_div_scan(int dtype, const void *b, int64_t n, int vec, uint64_t *slots, uint64_t seq,
+                           hipStream_t s);
 hipError_t launch_binary(const BinArgs &args, ErrFlags *errs, hipStream_t s);
 hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, int vec, hipStream_t s);
 hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,
@@ -112,6 +119,9 @@ struct ReduceArgs {
 hipError_t launch_reduce(const ReduceArgs &args, hipStream_t s);
 // Bytes of workspace launch_reduce needs for these sizes and vector width
 // (vec = 1 or the 16-byte element count, as in ReduceArgs::vec).
+// The most partial bytes a reduction pass's plan uses (column splits are capped to it; split rows need
+// far less): the size of the allocation-free entry point's partials.
+constexpr int64_t kReducePartialBytes = 2 << 20;
 int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inner, int vec);
 
 // Softmax of x viewed as [outer, r, inner] along r, with an optional additive

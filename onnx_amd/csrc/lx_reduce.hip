@@ -416,6 +416,10 @@ static RedPlan plan_reduce(int64_t outer, int64_t r, int64_t inner, int V) {
         int64_t maxs = ceil_div(r, (int64_t)nrs * 16);  // >= 16 rows per slice
         if (rsplit > maxs) rsplit = maxs;
         if (rsplit > 65535) rsplit = 65535;
+        // the partials of every split stay within kReducePartialBytes (a slice fewer at most: [255,1024,256]
+        // axis 1 takes 8 slices instead of 9), the bound the allocation-free entry point's scratch relies on
+        const int64_t cap = kReducePartialBytes / (outer * inner * (int64_t)sizeof(A));
+        if (rsplit > cap) rsplit = cap;
         if (rsplit < 1) rsplit = 1;
     }
     p.kind = 2;

@@ -159,14 +159,15 @@ class ComputationalGraph:
     @property
     def Profile(self) -> List[dict]:
         """One record per node executed while profiling (Profiler.Profile): node_id, node_index, op,
-        math_ms (device time between the node's boundary events) and host_ms (its dispatch)."""
+        math_ms (device time between the node's boundary events), host_ms (its dispatch) and start_ms (device
+        time from the execution's first boundary event to the node's start)."""
         lib = L.lib()
         out = []
         for i in range(lib.lx_graph_profile_count(self._h)):
             p = L.LxNodeProfile()
             _check(lib.lx_graph_profile(self._h, i, ctypes.byref(p)), "lx_graph_profile")
             out.append({"node_id": p.node_id, "node_index": p.node_index, "op": p.op.decode(),
-                        "math_ms": p.math_ms, "host_ms": p.host_ms})
+                        "math_ms": p.math_ms, "host_ms": p.host_ms, "start_ms": p.start_ms})
         return out
 
     def ResetProfile(self):

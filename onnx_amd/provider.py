@@ -190,6 +190,32 @@ def _axes_args(axes):
 class HipExecutionProvider:
     """Static operators with CPUExecutionProvider's signatures."""
 
+    # ---- profiling: the OpStage.Math stage of each call (Profiler.StartOpStage, Profiler.cs:71-80) ----
+    @staticmethod
+    def EnableProfiling(enabled: bool = True):
+        """Device timing of later operator calls (lx_set_op_profiling): each call made while enabled appends
+        one record whose math_ms is the device time between HIP events around its launches."""
+        init()
+        _check(L.lib().lx_set_op_profiling(1 if enabled else 0), "lx_set_op_profiling")
+
+    @staticmethod
+    def Profile() -> List[dict]:
+        """The records since the last reset: op, math_ms (OpStage.Math on the device), host_ms (the call on
+        the host) and start_ms (device time from the first record's start); waits for the calls' events."""
+        init()
+        lib = L.lib()
+        out = []
+        for i in range(lib.lx_op_profile_count()):
+            p = L.LxOpProfile()
+            _check(lib.lx_op_profile(i, ctypes.byref(p)), "lx_op_profile")
+            out.append({"op": p.op.decode(), "math_ms": p.math_ms, "host_ms": p.host_ms, "start_ms": p.start_ms})
+        return out
+
+    @staticmethod
+    def ResetProfile():
+        init()
+        _check(L.lib().lx_op_profile_reset(), "lx_op_profile_reset")
+
     @staticmethod
     def _binary(name, A, B, out=None):
         init()

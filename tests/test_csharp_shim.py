@@ -49,7 +49,8 @@ def test_struct_layouts_follow_the_c_structs():
         body = re.search(r"struct " + struct + r"\s*\{(.*?)\n\}", s, flags=re.S).group(1)
         return re.findall(r"public (?:fixed )?(\w+) (\w+)(?:\[[^\]]*\])?;", body)
     assert [t for t, _ in fields("LxTensor")] == ["int", "int", "long", "IntPtr", "long", "int", "int"]
-    assert [t for t, _ in fields("LxNodeProfile")] == ["long", "int", "byte", "double", "double"]
+    assert [t for t, _ in fields("LxNodeProfile")] == ["long", "int", "byte", "double", "double", "double"]
+    assert [t for t, _ in fields("LxOpProfile")] == ["byte", "double", "double", "double"]
     assert "fixed byte Op[36]" in s
     assert [t for t, _ in fields("LxBroadcastPlan")] == ["int", "int", "long", "int", "int", "long", "long", "long", "long"]
 
@@ -72,3 +73,27 @@ def test_sources_are_balanced():
         s = re.sub(r'"(?:[^"\\]|\\.)*"', '""', re.sub(r"//[^\n]*", "", _cs(f)))
         for o, c in ("{}", "()", "[]"):
             assert s.count(o) == s.count(c), (f, o)
+
+
+def test_provider_opens_a_device_math_stage_before_every_native_operator_call():
+    """With Profiler.Enabled the provider opens OpStage.Math as the reference's operators do
+    (CPUExecutionProvider.cs:92-103), right before each native operator call (after the uploads), and later
+    writes the device time the library recorded for that call into that OpProfile."""
+    s = re.sub(r"//[^\n]*", "", _cs("HipExecutionProvider.cs"))
+    body = s[s.index("static void MathStage()"):]
+    body = body[:body.index("\n    }\n") + 6]
+    assert "if (!Profiler.Enabled) return;" in body
+    assert "HipNative.lx_set_op_profiling(1)" in body
+    assert "Profiler.StartOpStage(OpStage.Math);" in body
+    assert "pendingMath.Add((Profiler.CurrentOpProfile, HipNative.lx_op_profile_count()));" in body
+    resolve = s[s.index("public static void ResolveDeviceProfile()"):]
+    resolve = resolve[:resolve.index("\n    }\n")]
+    assert "HipNative.lx_op_profile(record, &p)" in resolve and "stage.Time = TimeSpan.FromMilliseconds(p.MathMs);" in resolve
+    assert "HipNative.lx_op_profile_reset()" in resolve
+    lines = s.split("\n")
+    calls = [i for i, l in enumerate(lines)
+             if re.search(r"(st = |Done\(op, )(HipNative\.lx_[A-Z]\w*|fn)\(&", l) or "HipNative.lx_Concat(" in l]
+    assert len(calls) == 15
+    for i in calls:
+        back = "\n".join(lines[max(0, i - 6):i + 1])
+        assert "MathStage();" in back, lines[i]

@@ -11,7 +11,7 @@ import ctypes
 import numpy as np
 import pytest
 
-from onnx_amd import DeviceTensor, HipExecutionProvider as HIP
+from onnx_amd import DeviceTensor, HipExecutionProvider as HIP, OpStatus
 from onnx_amd import _lib as L
 from onnx_amd.graph import ComputationalGraph, Model
 from oracle import graph_oracle as GO
@@ -422,11 +422,26 @@ def test_shape_arithmetic_out_of_range_index_fails_as_the_device_operator(hip):
     assert "gather" in g.LastError and "outside the bounds" in g.LastError
 
 
+def _assert_telescoping(prof, wall_ms, tiled=0.99):
+    """Records of consecutive work on one stream never overlap (each starts at or after the previous one's
+    end), and when the device is the bottleneck they tile it: the device times add up to at least `tiled` of
+    the span from the first start to the last end; the span lies within the host's wall time around the
+    work."""
+    for a, b in zip(prof, prof[1:]):
+        assert b["start_ms"] >= a["start_ms"] + a["math_ms"] - 2e-3, (a, b)
+    span = prof[-1]["start_ms"] + prof[-1]["math_ms"] - prof[0]["start_ms"]
+    total = sum(p["math_ms"] for p in prof)
+    assert tiled * span <= total <= span * 1.0001 + 1e-3, (total, span)
+    assert 0.3 * wall_ms <= span <= wall_ms, (span, wall_ms)
+    return span
+
+
 def test_profiling_c2_graph_node_times_add_up_to_the_execution():
-    """Profiler.StartNodeProfile / StopNodeProfile on the device: the nine-node LayerNorm graph records nine
-    nodes with the reference's op types in node order, every node with device time, and the node times add
-    up to the execution's wall time within 10% (the boundary events telescope); a second execution appends
-    nine more; reset clears them; a fused graph records its one fused node."""
+    """Profiler.StartNodeProfile / StopNodeProfile on the device: one execution of the nine-node LayerNorm
+    graph records nine nodes with the reference's op types in node order, every node with device time, and
+    the node times add up to the device span between the execution's first and last boundary events (the
+    events telescope: each node ends at the next node's start); a second execution appends nine more; reset
+    clears them; a fused graph records its one fused node."""
     import time
     rng = np.random.default_rng(29)
     shape = (64, 512, 768)
@@ -437,22 +452,17 @@ def test_profiling_c2_graph_node_times_add_up_to_the_execution():
     assert g.Execute({"x": x}), g.LastError      # warm: uploads, pool
     assert g.Profile == []                        # not enabled
     g.EnableProfiling(True)
-    walls = []
-    for _ in range(3):
-        g.ResetProfile()
-        onnx_sync()
-        t0 = time.perf_counter()
-        assert g.Execute({"x": x}), g.LastError
-        walls.append((time.perf_counter() - t0) * 1e3)
-        prof = g.Profile
-        assert [p["op"] for p in prof] == ops and [p["node_id"] for p in prof] == list(range(9))
-        assert all(p["math_ms"] > 0 and p["host_ms"] > 0 for p in prof)
-        total = sum(p["math_ms"] for p in prof)
-        if abs(total - walls[-1]) <= 0.1 * walls[-1]:
-            break
-    assert abs(total - walls[-1]) <= 0.1 * walls[-1], (total, walls)
+    onnx_sync()
+    t0 = time.perf_counter()
     assert g.Execute({"x": x}), g.LastError
-    assert len(g.Profile) == 18
+    wall = (time.perf_counter() - t0) * 1e3
+    prof = g.Profile
+    assert [p["op"] for p in prof] == ops and [p["node_id"] for p in prof] == list(range(9))
+    assert all(p["math_ms"] > 0 and p["host_ms"] > 0 for p in prof)
+    assert prof[0]["start_ms"] == 0.0
+    _assert_telescoping(prof, wall)
+    assert g.Execute({"x": x}), g.LastError
+    assert len(g.Profile) == 18 and g.Profile[9]["start_ms"] == 0.0
     g.ResetProfile()
     assert g.Profile == []
     g.EnableProfiling(False)
@@ -466,6 +476,66 @@ def test_profiling_c2_graph_node_times_add_up_to_the_execution():
     prof = gf.Profile
     assert [p["op"] for p in prof] == ["LayerNormDecomposed"] and prof[0]["node_id"] == 8 and prof[0]["math_ms"] > 0
     gf.close()
+
+
+def test_profiling_eager_c2_calls_time_the_device_work():
+    """OpStage.Math of eager calls (lx_set_op_profiling): the nine operator calls of the decomposed LayerNorm
+    made through HipExecutionProvider with profiling on record nine calls in order, each with device time
+    between the HIP events around its launches; the records telescope over the calls' device span, which
+    lies within the host wall time; calls made by a graph execution are not recorded as eager calls; reset
+    clears the records and a disabled profiler records nothing."""
+    import time
+    rng = np.random.default_rng(33)
+    shape = (256, 512, 768)   # 400 MB per tensor: each call's kernel outlasts the next call's dispatch
+    x = DeviceTensor.from_numpy((rng.standard_normal(shape) * 2).astype(np.float32))
+    gamma = DeviceTensor.from_numpy((1 + 0.02 * rng.standard_normal(768)).astype(np.float32))
+    beta = DeviceTensor.from_numpy((0.02 * rng.standard_normal(768)).astype(np.float32))
+    two = DeviceTensor.from_numpy(np.array(2.0, np.float32))
+    eps = DeviceTensor.from_numpy(np.array(1e-12, np.float32))
+    axes = [-1]
+
+    def calls():
+        def out(r):
+            assert r.Status == OpStatus.Success, r.Message
+            return r.Outputs[0]
+        mean = out(HIP.ReduceMean(x, axes, 1))
+        d = out(HIP.Sub(x, mean))
+        p = out(HIP.Pow(d, two))
+        var = out(HIP.ReduceMean(p, axes, 1))
+        ve = out(HIP.Add(var, eps))
+        sd = out(HIP.Sqrt(ve))
+        n = out(HIP.Div(d, sd))
+        m = out(HIP.Mul(n, gamma))
+        return out(HIP.Add(m, beta))
+    y_ref = calls().to_numpy()                    # warm: pool
+    HIP.ResetProfile()
+    HIP.EnableProfiling(True)
+    onnx_sync()
+    t0 = time.perf_counter()
+    y = calls()
+    onnx_sync()
+    wall = (time.perf_counter() - t0) * 1e3
+    prof = HIP.Profile()
+    assert [p["op"] for p in prof] == ["ReduceMean", "Sub", "Pow", "ReduceMean", "Add", "Sqrt", "Div", "Mul", "Add"]
+    assert all(p["math_ms"] > 0 and p["host_ms"] > 0 for p in prof), prof
+    assert prof[0]["start_ms"] == 0.0
+    _assert_telescoping(prof, wall, tiled=0.95)
+    # no call's device time beats its algorithmic bytes at the 8 TB/s HBM peak
+    big, row = np.prod(shape) * 4, np.prod(shape[:-1]) * 4
+    moved = [big + row, 2 * big + row, 2 * big + 4, big + row, 2 * row + 4, 2 * row, 2 * big + row,
+             2 * big + 768 * 4, 2 * big + 768 * 4]
+    for p, b in zip(prof, moved):
+        assert p["math_ms"] >= b / 8e12 * 1e3, (p, b)
+    assert np.array_equal(y.to_numpy(), y_ref)
+    g = Model.Load(W.model(ln_nodes(), [("x", np.float32, shape)], [("y", np.float32, shape)], LN_INITS(768)))
+    assert g.Execute({"x": x}), g.LastError
+    assert len(HIP.Profile()) == 9
+    g.close()
+    HIP.ResetProfile()
+    assert HIP.Profile() == []
+    HIP.EnableProfiling(False)
+    calls()
+    assert HIP.Profile() == []
 
 
 def test_profiling_records_the_failing_node():

@@ -410,6 +410,54 @@ def test_int_div_divisor_shared_along_the_outer_axis(hip, dt, a_shape, b_shape):
         assert HIP.Div(dev(a1), dev(b1)).Code == code
 
 
+@pytest.mark.parametrize("dt", [np.int32, np.int64, np.uint8])
+@pytest.mark.parametrize("a_shape,b_shape", [((33, 1, 4096), (1, 16, 4096)),   # B 1/33 of the output
+                                             ((17, 1, 4093), (1, 16, 4093)),   # ragged: B's tail outside the vectors
+                                             ((16, 1, 4096), (1, 256, 4096))])  # 256 scan blocks (C4's B)
+def test_int_div_divisor_scanned_before_the_quotients(hip, dt, a_shape, b_shape):
+    """An eager integer Div whose divisor is at most 1/16 of its output scans the divisor first and returns
+    once the scan finds neither 0 nor (signed) -1; otherwise it waits for the quotient kernel's record.  A
+    0, and separately a -1 against MIN in A, at B's last element (the last output element) give the
+    synchronous status and the oracle's error; a -1 with no MIN opposite it divides normally; clean calls
+    before and after failing ones return their own status and the oracle's bits."""
+    rng = np.random.default_rng(31)
+    info = np.iinfo(dt)
+    if dt == np.uint8:
+        a = rng.integers(0, 256, a_shape).astype(dt)
+        b = rng.integers(1, 256, b_shape).astype(dt)
+    else:
+        a = rng.integers(-(2**20), 2**20 + 1, a_shape).astype(dt)
+        b = rng.integers(1, 1025, b_shape).astype(dt) * np.where(rng.random(b_shape) < 0.5, -1, 1).astype(dt)
+    assert np.prod(b_shape) * 16 <= np.prod(np.broadcast_shapes(a_shape, b_shape))
+    clean = O.binary(O.DIV, a, b)
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), clean)
+    b0 = b.copy()
+    b0.flat[-1] = 0
+    r = HIP.Div(dev(a), dev(b0))
+    assert r.Status == OpStatus.Failure and r.Code == L.ERR_DIVIDE_BY_ZERO, r.Message
+    with pytest.raises(O.OracleError) as e:
+        O.binary(O.DIV, a, b0)
+    assert e.value.status == L.ERR_DIVIDE_BY_ZERO
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), clean)
+    if dt != np.uint8:
+        bm = b.copy()
+        bm.flat[-1] = -1
+        # -1 with no MIN in A: every quotient is defined
+        assert_bits(ok(HIP.Div(dev(a), dev(bm))), O.binary(O.DIV, a, bm))
+        am = a.copy()
+        am.flat[-1] = info.min
+        r = HIP.Div(dev(am), dev(bm))
+        assert r.Status == OpStatus.Failure and r.Code == L.ERR_OVERFLOW, r.Message
+        with pytest.raises(O.OracleError) as e:
+            O.binary(O.DIV, am, bm)
+        assert e.value.status == L.ERR_OVERFLOW
+        # both: the zero comes first in output order
+        bz = bm.copy()
+        bz.flat[0] = 0
+        assert HIP.Div(dev(am), dev(bz)).Code == L.ERR_DIVIDE_BY_ZERO
+    assert_bits(ok(HIP.Div(dev(a), dev(b))), clean)
+
+
 @pytest.mark.parametrize("dt", [np.int32, np.int64])
 def test_int_div_errors(hip, dt):
     info = np.iinfo(dt)
@@ -1077,3 +1125,30 @@ def test_reshape_alias(hip):
     assert v.shape == (2, 3, 4) and v.h.data == a.h.data
     y = ok(HIP.ReduceSum(v, [2], 0))
     np.testing.assert_array_equal(y, np.arange(24, dtype=np.float32).reshape(2, 3, 4).sum(2))
+
+
+def test_read_probe_folds_what_it_reads(hip):
+    """lx_read_probe, the read-ceiling diagnostic: with g blocks (one per 1024 16-byte vectors, at most
+    out_bytes / 4), block b writes the XOR of every vector v with (v mod 1024 g) // 1024 == b.  Checked against
+    a numpy fold of the same words with a partial last block, with grids clipped by out_bytes, and an out
+    pointer that is not 4-byte aligned is refused."""
+    rng = np.random.default_rng(41)
+    nv = 10 * 1024 + 37
+    words = rng.integers(0, 2**32, nv * 4, dtype=np.uint64).astype(np.uint32)
+    src = dev(words)
+    vx = np.bitwise_xor.reduce(words.reshape(nv, 4), axis=1)
+    lib = L.lib()
+    for g in (11, 3, 1):
+        out = DeviceTensor.from_numpy(np.full(g + 2, 0xDEADBEEF, np.uint32))
+        assert lib.lx_read_probe(ctypes.c_void_p(src.h.data), nv * 16, ctypes.c_void_p(out.h.data), 4 * g) == L.OK
+        got = out.to_numpy()
+        want = np.zeros(g, np.uint32)
+        blk = (np.arange(nv) % (1024 * g)) // 1024
+        for b in range(g):
+            want[b] = np.bitwise_xor.reduce(vx[blk == b])
+        assert np.array_equal(got[:g], want), g
+        assert np.all(got[g:] == 0xDEADBEEF), g
+    out = DeviceTensor.from_numpy(np.zeros(4, np.uint32))
+    assert lib.lx_read_probe(ctypes.c_void_p(src.h.data), nv * 16, ctypes.c_void_p(out.h.data + 2), 8) == \
+        L.ERR_INVALID_ARGUMENT
+    assert "4-byte aligned" in L.last_error()

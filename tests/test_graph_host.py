@@ -276,4 +276,9 @@ def test_profiling_switch_and_empty_profile():
     g.ResetProfile()
     rec = L.LxNodeProfile()
     assert L.lib().lx_graph_profile(g._h, 0, ctypes.byref(rec)) != L.OK
-    assert ctypes.sizeof(L.LxNodeProfile) == 8 + 4 + 36 + 8 + 8
+    assert ctypes.sizeof(L.LxNodeProfile) == 8 + 4 + 36 + 8 + 8 + 8
+    # the eager calls' records (lx_set_op_profiling): the same behaviour without a device
+    assert ctypes.sizeof(L.LxOpProfile) == 36 + 4 + 8 + 8 + 8   # op[36], padding to 8, three doubles
+    assert L.lib().lx_op_profile_count() == 0
+    assert L.lib().lx_op_profile(0, ctypes.byref(L.LxOpProfile())) == L.ERR_INVALID_ARGUMENT
+    assert L.lib().lx_op_profile_reset() == L.OK

@@ -40,6 +40,10 @@ CASES = [
     (np.int64, [1, 3], 1, (6, 40, 33, 8), (3, 10, 7, 4)),     # two passes: an intermediate in a scratch slot
     (np.int32, [0, 2], 0, (16, 300, 64), (5, 17, 16)),        # two passes, wrapping int32
     (np.float64, [1], 1, (32, 5000, 6), (2, 3, 6)),           # double, odd inner
+    # few column tiles split over many row slices: the planner caps the partials at the scratch's 2 MiB
+    (np.float32, [1], 1, (255, 1024, 256), (3, 64, 256)),
+    (np.float32, [1], 1, (200, 2048, 256), (7, 100, 256)),
+    (np.float32, [1], 1, (300, 512, 255), (5, 40, 255)),      # unaligned rows: single-element tiles
 ]
 
 
