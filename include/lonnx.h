@@ -156,7 +156,8 @@ int lx_ReduceSum(const lx_tensor *data, const int64_t *axes, int32_t n_axes, int
 /* ReduceSum that allocates nothing (no counterpart in the reference): for callers that cannot call
  * hipMalloc -- code under HIP graph capture, tight serving loops, harnesses that forbid allocation.  Same
  * arguments, validation, results and errors as lx_ReduceSum, except that Y must already hold device storage
- * of sufficient capacity, and that split partials (at most 2 MiB) and the intermediate of each pass of a
+ * of sufficient capacity, and that split partials (at most 2 MiB: the planner caps every reduction's splits
+ * there, so both entry points run the same plan) and the intermediate of each pass of a
  * multi-pass reduction (at most 1 MiB each) live in a 4 MiB static device array per GPU instead of the
  * library's workspace and pool; a reduction that needs more fails with LX_ERR_NOT_SUPPORTED before
  * anything is launched.  Calls on one GPU share that array: calls that overlap on one GPU (other
