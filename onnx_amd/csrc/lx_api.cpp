@@ -39,7 +39,7 @@ struct State {
     struct Mailbox *mail = nullptr;      // mapped, coherent pinned host memory
     struct Mailbox *mail_dev = nullptr;  // the same memory as the device addresses it
     uint64_t mail_seq = 0;
-    uint64_t scan_seq = 0;               // the divisor scans' sequence (Mailbox::scan)
+    uint64_t scan_seq = 0;               // the divisor and index scans' sequence (Mailbox::scan)
 };
 // Small device-to-host reads (error records) land here: a one-block kernel copies the words and
 // then writes a sequence number, which the host polls.  One mailbox per library: calls are
@@ -48,7 +48,7 @@ constexpr int64_t kMailWords = 8192;  // 64 KiB: 4096 error records
 struct Mailbox {
     alignas(128) uint64_t seq;
     alignas(128) uint64_t words[kMailWords];
-    alignas(128) uint64_t scan[kDivScanSlots];  // one verdict per block of a divisor scan (k_div_scan)
+    alignas(128) uint64_t scan[kScanSlots];  // one verdict per block of a divisor or index scan
 };
 
 State g;
@@ -405,9 +405,9 @@ int read_device(const void *src, size_t bytes, void *dst, bool reset_src) {
     return LX_OK;
 }
 
-// Waits for the `blocks` slots of the divisor scan `seq` (the watchdog of read_device: every 50 us it asks
+// Waits for the `blocks` slots of the divisor or index scan `seq` (the watchdog of read_device: every 50 us it asks
 // the stream whether work is pending) and ORs their verdict bits into *bits.
-int wait_div_scan(int blocks, uint64_t seq, uint32_t *bits) {
+int wait_scan(int blocks, uint64_t seq, uint32_t *bits) {
     int seen = 0;
     uint32_t acc = 0;
     auto advance = [&] {
@@ -637,7 +637,7 @@ int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     if (!int_div) return LX_OK;
     if (prescan) {
         uint32_t bits = 0;
-        if ((st = wait_div_scan(scan_blocks, scan_seq, &bits))) return st;
+        if ((st = wait_scan(scan_blocks, scan_seq, &bits))) return st;
         if (bits == 0) {
             // no element can fail, so the quotient kernel records nothing: the record stays cleared
             g.errs_clean = true;
@@ -994,7 +994,7 @@ int lx_init(int32_t device) {
     if ((e = hipMalloc(&s.workspace, 1 << 20)) != hipSuccess) return undo(hip_fail(e, "hipMalloc(workspace)"));
     s.ws_bytes = 1 << 20;
     s.mail->seq = 0;
-    for (int i = 0; i < kDivScanSlots; i++) s.mail->scan[i] = 0;
+    for (int i = 0; i < kScanSlots; i++) s.mail->scan[i] = 0;
     s.stream = s.own_stream;
     s.device = device;
     s.init = true;
@@ -2092,9 +2092,30 @@ extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_
     // that large is outside the axis anyway, so the range check below reports it
     ErrFlags *errs;
     if ((st = check_begin(kCheckGather, 0, &errs))) return st;
+    // as integer Div's divisor scan: with at most 1/16 as many indices as output elements, a scan of the
+    // indices queued before the gather decides whether the call fails, and a clean call returns while the
+    // gather runs; an index out of range takes the gather's own record
+    const bool prescan = !t_defer_slot && nidx * 16 <= outer * nidx * inner;
+    int scan_blocks = 0;
+    uint64_t scan_seq = 0;
+    if (prescan) {
+        scan_blocks = index_scan_blocks(nidx);
+        scan_seq = ++g.scan_seq;
+        HIPCHECK(launch_index_scan(indices->dtype, indices->data, nidx, data->dims[ax], g.mail_dev->scan, scan_seq,
+                                   g.stream),
+                 "index scan");
+    }
     HIPCHECK(launch_gather((int)esize(data->dtype), indices->dtype, data->data, indices->data, Y->data, outer, nidx,
                            inner, data->dims[ax], errs, g.stream),
              "Gather");
+    if (prescan) {
+        uint32_t bits = 0;
+        if ((st = wait_scan(scan_blocks, scan_seq, &bits))) return st;
+        if (bits == 0) {
+            g.errs_clean = true;  // no index can be recorded: the record stays cleared
+            return LX_OK;
+        }
+    }
     return check_end(kCheckGather, 0);
 }
 

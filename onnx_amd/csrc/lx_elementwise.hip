@@ -182,7 +182,7 @@ __global__ __launch_bounds__(kDivScanBlock) void k_div_scan(const T *__restrict_
 int div_scan_blocks(int64_t n, int esize) {
     const int64_t vecs = (n * esize + 15) / 16;
     const int64_t g = (vecs + kDivScanBlock * kDivScanU - 1) / (kDivScanBlock * kDivScanU);
-    return (int)std::max<int64_t>(1, std::min<int64_t>(g, kDivScanSlots));
+    return (int)std::max<int64_t>(1, std::min<int64_t>(g, kScanSlots));
 }
 
 hipError_t launch_div_scan(int dtype, const void *b, int64_t n, int vec, uint64_t *slots, uint64_t seq,
@@ -202,6 +202,52 @@ hipError_t launch_div_scan(int dtype, const void *b, int64_t n, int vec, uint64_
         break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+// Eager Gather whose indices are far fewer than its output's elements: whether every index lies in
+// [-dim, dim) -- the only way the call can fail once its shapes are checked -- from the indices alone, with
+// the same per-block slots and store as k_div_scan (bit 0: an index out of range).
+template <typename I>
+__global__ __launch_bounds__(kDivScanBlock) void k_index_scan(const I *__restrict__ idx, int64_t n, int64_t dim,
+                                                              uint64_t *slots, uint64_t seq) {
+    constexpr int U = 8;  // indices per lane, all loaded before any is tested
+    bool out = false;
+    const int64_t step = (int64_t)gridDim.x * kDivScanBlock * U;
+    for (int64_t i0 = (int64_t)blockIdx.x * kDivScanBlock * U + threadIdx.x; i0 < n; i0 += step) {
+        I v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = i0 + u * kDivScanBlock < n ? idx[i0 + u * kDivScanBlock] : (I)0;
+#pragma unroll
+        for (int u = 0; u < U; u++) out = out || (int64_t)v[u] < -dim || (int64_t)v[u] >= dim;
+    }
+    __shared__ uint32_t waves[kDivScanBlock / 64];
+    const uint32_t w = __ballot(out) ? 1u : 0u;
+    if ((threadIdx.x & 63) == 0) waves[threadIdx.x >> 6] = w;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t all = 0;
+#pragma unroll
+        for (int i = 0; i < kDivScanBlock / 64; i++) all |= waves[i];
+        __hip_atomic_store(slots + blockIdx.x, (seq << 2) | all, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+
+int index_scan_blocks(int64_t n) {
+    const int64_t g = (n + kDivScanBlock * 8 - 1) / (kDivScanBlock * 8);
+    return (int)std::max<int64_t>(1, std::min<int64_t>(g, kScanSlots));
+}
+
+hipError_t launch_index_scan(int idx_dtype, const void *idx, int64_t n, int64_t dim, uint64_t *slots, uint64_t seq,
+                             hipStream_t s) {
+    if (idx_dtype == kInt32)
+        hipLaunchKernelGGL(k_index_scan<int32_t>, dim3(index_scan_blocks(n)), dim3(kDivScanBlock), 0, s,
+                           (const int32_t *)idx, n, dim, slots, seq);
+    else if (idx_dtype == kInt64)
+        hipLaunchKernelGGL(k_index_scan<int64_t>, dim3(index_scan_blocks(n)), dim3(kDivScanBlock), 0, s,
+                           (const int64_t *)idx, n, dim, slots, seq);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -59,11 +59,16 @@ hipError_t launch_publish(const uint64_t *src, int64_t n, uint64_t *dst, uint64_
                           uint64_t *reset, hipStream_t s);
 // Eager integer Div: scans the divisor b (n elements of dtype, 16-byte vectors when vec) for 0 and, for
 // signed types, -1; block i stores (seq << 2) | bits (bit 0: a zero, bit 1: a minus one) into slots[i] of
-// mapped host memory.  div_scan_blocks gives the number of blocks (slots) a launch uses.
-constexpr int kDivScanSlots = 256;
+// mapped host memory (kScanSlots of them).  div_scan_blocks gives the number of blocks (slots) a launch uses.
+constexpr int kScanSlots = 256;
 int div_scan_blocks(int64_t n, int esize);
 hipError_t launch_div_scan(int dtype, const void *b, int64_t n, int vec, uint64_t *slots, uint64_t seq,
                            hipStream_t s);
+// Eager Gather: scans n indices (Int32 / Int64) for a value outside [-dim, dim); block i stores
+// (seq << 2) | bit into slots[i] (bit 0: an index out of range); index_scan_blocks gives the blocks used.
+int index_scan_blocks(int64_t n);
+hipError_t launch_index_scan(int idx_dtype, const void *idx, int64_t n, int64_t dim, uint64_t *slots, uint64_t seq,
+                             hipStream_t s);
 hipError_t launch_binary(const BinArgs &args, ErrFlags *errs, hipStream_t s);
 hipError_t launch_unary(int op, int dtype, const void *x, void *y, int64_t n, int vec, hipStream_t s);
 hipError_t launch_cast(int src, int dst, const void *x, void *y, int64_t n, int vec, ErrFlags *errs,

@@ -161,6 +161,50 @@ def test_binary_random_large(hip, dt):
         check(r, lambda: O.binary(code, a, b), same_bits, (op, dt, sa, sb, case))
 
 
+@pytest.mark.parametrize("dt", [np.uint8, np.int32, np.int64])
+def test_int_div_small_divisor_random(hip, dt):
+    """Integer Div whose divisor is at most 1/16 of the output, the shapes on which an eager call scans the
+    divisor and returns once it holds no 0 (and, signed, no -1): half the divisors are clean, the others hold
+    one 0, or one -1 with or without MIN at a random position of A; the status and the bits are the oracle's
+    (the first failing element in output order decides the error)."""
+    rng = np.random.default_rng([17, np.dtype(dt).num])
+    info = np.iinfo(dt)
+    signed = info.min < 0
+    for case in range(60):
+        r = int(rng.integers(2, 5))
+        out = [int(d) for d in rng.integers(2, 9, r)]
+        out[-1] = int(rng.integers(1, 300))
+        if rng.random() < 0.5:
+            out[-1] = out[-1] // 16 * 16 + 16
+        # the divisor keeps the inner axis and some of the others, the dividend the rest (or all)
+        keep = rng.random(r) < 0.4
+        keep[-1] = True
+        keep[0] = False
+        sb = tuple(d if k else 1 for d, k in zip(out, keep))
+        sa = tuple(out) if rng.random() < 0.5 else tuple(1 if k and i < r - 1 else d for i, (d, k) in enumerate(zip(out, keep)))
+        n_out = int(np.prod(np.broadcast_shapes(sa, sb)))
+        if np.prod(sb) * 16 > n_out:
+            sa = (16,) + sa
+            n_out *= 16
+        a = dividends(rng, sa, dt) if signed else values(rng, sa, dt)
+        lo = 1 if not signed else -1000
+        b = rng.integers(lo, 1001, sb).astype(np.int64)
+        b = np.where((b == 0) | (b == -1), 3, b).astype(dt)
+        if signed:
+            a = np.where(a == info.min, 5, a).astype(dt)
+        kind = rng.random()
+        if kind < 0.5:
+            pass
+        elif kind < 0.7 or not signed:
+            b.flat[int(rng.integers(0, b.size))] = 0
+        else:
+            b.flat[int(rng.integers(0, b.size))] = -1
+            if rng.random() < 0.6:
+                a.flat[int(rng.integers(0, a.size))] = info.min
+        r_ = HIP.Div(dev(a), dev(b))
+        check(r_, lambda: O.binary(O.DIV, a, b), same_bits, ("Div", dt, sa, sb, case))
+
+
 def reduction_bar(dt):
     def compare(got, ref, x_abs):
         if got.shape != ref.shape:

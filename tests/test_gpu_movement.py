@@ -201,6 +201,33 @@ def test_gather_empty_and_errors(hip):
     assert bits(ok(HIP.Gather(a, dev(np.array([9], np.int64)), 0)), np.array([9.0], np.float32))
 
 
+def test_gather_indices_scanned_before_the_gather(hip):
+    """An eager Gather with at most 1/16 as many indices as output elements scans its indices first and
+    returns once every one lies in [-dim, dim); an index out of range at the last position (or one an Int64
+    tensor holds beyond int32) fails with the reference's message, and clean calls before and after failing
+    ones return the oracle's bits."""
+    rng = np.random.default_rng(12)
+    table = rng.standard_normal((1000, 64)).astype(np.float32)
+    dtab = dev(table)
+    for idt in (np.int64, np.int32):
+        ids = rng.integers(-1000, 1000, (8, 512)).astype(idt)
+        want = O.gather(table, ids, 0)
+        assert bits(ok(HIP.Gather(dtab, dev(ids), 0)), want)
+        bads = [1000, -1001] + ([2**40, -(2**33)] if idt == np.int64 else [2**31 - 1, -(2**31)])
+        for bad in bads:
+            b = ids.copy()
+            b.flat[-1] = bad
+            r = HIP.Gather(dtab, dev(b), 0)
+            assert r.Code == L.ERR_INVALID_ARGUMENT and r.Message == "Index was outside the bounds of the array.", bad
+            assert bits(ok(HIP.Gather(dtab, dev(ids), 0)), want)
+    # along an inner axis, many outer rows: [16, 1000, 8] gathered by 40 indices on axis 1
+    d3 = rng.standard_normal((16, 1000, 8)).astype(np.float32)
+    i3 = rng.integers(0, 1000, (40,)).astype(np.int64)
+    assert bits(ok(HIP.Gather(dev(d3), dev(i3), 1)), O.gather(d3, i3, 1))
+    i3[-1] = -1001
+    assert HIP.Gather(dev(d3), dev(i3), 1).Code == L.ERR_INVALID_ARGUMENT
+
+
 # ---- Slice -----------------------------------------------------------------------
 SLICE_CASES = [
     ((10, 10, 10), [0, 0, 0], [2, 2, 2], [0, 1, 2], [1, 1, 1]),
