@@ -158,6 +158,12 @@ int64_t numel(const lx_tensor *t) { return numel_of(t->rank, t->dims); }
 
 bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
 
+// whether the byte ranges [a, a + an) and [b, b + bn) share a byte
+static bool overlaps(const void *a, int64_t an, const void *b, int64_t bn) {
+    const uintptr_t x = (uintptr_t)a, y = (uintptr_t)b;
+    return an > 0 && bn > 0 && x < y + (uintptr_t)bn && y < x + (uintptr_t)an;
+}
+
 // [lo, hi] of an integer element type (Bool as 0..1); false for floating types
 bool int_range(int t, __int128 *lo, __int128 *hi) {
     switch (t) {
@@ -622,8 +628,11 @@ int run_binary(int op, const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     // and (signed) no minus one in B no element can fail, and the call returns as soon as the scan's
     // blocks have stored their verdicts, while the quotient kernel runs.  Otherwise the call waits for the
     // quotient kernel's own record, which names the first failing element.
+    // (an output that overlaps the divisor could write a quotient over a divisor element the kernel has
+    // still to read, after the scan has passed it: such calls wait for the kernel's record)
     const int64_t nb = numel(B);
-    const bool prescan = int_div && !t_defer_slot && nb > 0 && nb * 16 <= p.numel;
+    const bool prescan = int_div && !t_defer_slot && nb > 0 && nb * 16 <= p.numel &&
+                         !overlaps(Y->data, p.numel * es, B->data, nb * es);
     int scan_blocks = 0;
     uint64_t scan_seq = 0;
     if (prescan) {
@@ -2095,7 +2104,9 @@ extern "C" int lx_Gather(const lx_tensor *data, const lx_tensor *indices, int32_
     // as integer Div's divisor scan: with at most 1/16 as many indices as output elements, a scan of the
     // indices queued before the gather decides whether the call fails, and a clean call returns while the
     // gather runs; an index out of range takes the gather's own record
-    const bool prescan = !t_defer_slot && nidx * 16 <= outer * nidx * inner;
+    const bool prescan = !t_defer_slot && nidx * 16 <= outer * nidx * inner &&
+                         !overlaps(Y->data, outer * nidx * inner * esize(data->dtype), indices->data,
+                                   nidx * esize(indices->dtype));
     int scan_blocks = 0;
     uint64_t scan_seq = 0;
     if (prescan) {
