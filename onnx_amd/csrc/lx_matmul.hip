@@ -2,10 +2,12 @@
 // via CPUExecutionProvider.MatMul, CPUExecutionProvider.cs:359-378).
 //
 // float : v_mfma_f32_32x32x2f32 (fp32 products, fp32 accumulation -- the
-//         reference's float32 arithmetic, summed in a different order).
-//         block tiles from 64x64 to 128x128 (128x96 for N = 768) chosen per
-//         shape, K step 16, four waves, double-buffered LDS fed from
-//         registers one K step ahead.
+//         reference's float32 arithmetic, summed in a different order, the
+//         same order in both kernels).  K a multiple of 16 with aligned
+//         operands: a ring of LDS stages filled by direct-to-LDS loads two or
+//         three K steps ahead (k_matmul_f32_dl); otherwise double-buffered LDS
+//         fed from registers one K step ahead (k_matmul_f32).  Block tiles
+//         from 64x64 to 128x128 chosen per shape, K step 16, four waves.
 // double: v_mfma_f64_16x16x4f64, 64x64 block tile, four waves of 32x32.
 // int32 : exact two's-complement multiply-add on the VALU (no int32 MFMA),
 //         16x16 LDS tiles.
@@ -17,6 +19,8 @@
 //   16x16x4 f64: a = A[l%16][l/16], b = B[l/16][l%16], acc[r] = C[l/16 + 4r][l%16]
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "lx_device.h"
 #include "lx_kernels.h"
 
@@ -24,6 +28,7 @@ namespace lx {
 
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef double v4d __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // per-block batch offsets of A, B and C
 __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, int64_t *ao, int64_t *bo) {
@@ -42,11 +47,63 @@ __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, in
 // float: MFMA 32x32x2
 // ---------------------------------------------------------------------------
 
+// Bias / residual / GELU epilogue and store of a wave's MT x NT tiles of 32x32 results (rows r0.., columns
+// c0..).  The MFMA ran as B^T A^T, so acc[i][j][q] = C[r0 + 32 i + l % 32][c0 + 32 j + 8 (q / 4) + 4 (l / 32) +
+// q % 4]: each lane holds four consecutive columns of one row per group of four results (one 16-byte store).
+template <int MT, int NT, bool VEC, bool GELU>
+__device__ __forceinline__ void mm_epilogue(const v16f (&acc)[MT][NT], float *__restrict__ C, const MatMulArgs &p, int r0,
+                                            int c0, int l, const ExpTable &tab) {
+    const int M = p.m, N = p.n;
+    const int64_t bz = p.batch_base + blockIdx.z;
+    float *Cb = C + bz * (int64_t)M * N;
+    const float *Rb = p.res ? p.res + bz * (int64_t)M * N : nullptr;
+    const float *Bias = p.bias ? p.bias + bz * p.bias_bstr : nullptr;
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const int row = r0 + 32 * i + (l % 32);
+        if (row >= M) continue;
+        float *Cr = Cb + (int64_t)row * N;
+        const float *Rr = Rb ? Rb + (int64_t)row * N : nullptr;
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int c = c0 + 32 * j + 8 * q + 4 * (l / 32);
+                float v[4] = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+                if (VEC && c + 3 < N) {
+                    if (Bias) {
+                        const float4 bc = *reinterpret_cast<const float4 *>(Bias + c);
+                        v[0] = v[0] + bc.x; v[1] = v[1] + bc.y; v[2] = v[2] + bc.z; v[3] = v[3] + bc.w;
+                    }
+                    if (Rr) {
+                        const float4 rc = *reinterpret_cast<const float4 *>(Rr + c);
+                        v[0] = v[0] + rc.x; v[1] = v[1] + rc.y; v[2] = v[2] + rc.z; v[3] = v[3] + rc.w;
+                    }
+                    if constexpr (GELU) {
+#pragma unroll
+                        for (int e = 0; e < 4; e++) v[e] = gelu_erf_lx(v[e], tab);
+                    }
+                    *reinterpret_cast<float4 *>(Cr + c) = make_float4(v[0], v[1], v[2], v[3]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (c + e >= N) break;
+                        float x = v[e];
+                        if (Bias) x = x + Bias[c + e];
+                        if (Rr) x = x + Rr[c + e];
+                        if constexpr (GELU) x = gelu_erf_lx(x, tab);
+                        Cr[c + e] = x;
+                    }
+                }
+            }
+    }
+}
+
 // BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
 // = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered in LDS with k
 // as the outer index (A transposed to [k][m], B as [k][n]), so the lanes of a
-// fragment read 32 consecutive floats.  Register-only loops of this MFMA reach
-// about 144 TF/s on MI355X; the 128x128 tile runs large GEMMs at 127-131 TF/s.
+// fragment read 32 consecutive floats.  The kernel for K not a multiple of 16,
+// unaligned operands, K <= 64, N <= 64 and 128x96 tiles beyond one per CU.
 constexpr int kFBK = 16, kFPad = 4;
 
 template <int BM, int BN, int WM, int WN, bool VEC, bool GELU>
@@ -70,7 +127,6 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
     const float *Ab = A + ao;
     const float *Bb = B + bo;
-    float *Cb = C + (p.batch_base + blockIdx.z) * (int64_t)M * N;
 
     // global -> register staging one K step ahead: float4 e = t + NTHR h of the step's
     // A tile (row e / KQ, k 4 (e % KQ)) and B tile (k row e / BQ, column 4 (e % BQ))
@@ -143,45 +199,259 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     int buf = 0;
     for (int kt = 0; kt < nk; kt++) {
         if (kt + 1 < nk) load((kt + 1) * kFBK);
+        // MFMA j of the step takes k = j from lanes 0-31 and k = 8 + j from lanes 32-63, the order of the
+        // direct-load kernel below: every float MatMul sums its products in one order, whichever kernel runs it
 #pragma unroll
-        for (int kk = 0; kk < kFBK; kk += 2) {
-            const int kr = kk + l / 32;
+        for (int j = 0; j < kFBK / 2; j++) {
+            const int kr = 8 * (l / 32) + j;
             float a[MT], b[NT];
 #pragma unroll
             for (int i = 0; i < MT; i++) a[i] = As[buf][kr][wr + 32 * i + (l % 32)];
 #pragma unroll
-            for (int j = 0; j < NT; j++) b[j] = Bs[buf][kr][wc + 32 * j + (l % 32)];
+            for (int jn = 0; jn < NT; jn++) b[jn] = Bs[buf][kr][wc + 32 * jn + (l % 32)];
 #pragma unroll
             for (int i = 0; i < MT; i++)
 #pragma unroll
-                for (int j = 0; j < NT; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int jn = 0; jn < NT; jn++)
+                    acc[i][jn] = __builtin_amdgcn_mfma_f32_32x32x2f32(b[jn], a[i], acc[i][jn], 0, 0, 0);
         }
         if (kt + 1 < nk) store(buf ^ 1);
         __syncthreads();
         buf ^= 1;
     }
-    const float *Rb = p.res ? p.res + (p.batch_base + blockIdx.z) * (int64_t)M * N : nullptr;
-    const float *Bias = p.bias ? p.bias + (p.batch_base + blockIdx.z) * p.bias_bstr : nullptr;
+    mm_epilogue<MT, NT, VEC, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
+}
+
+// Direct-to-LDS pipeline for K a multiple of 16 and 16-byte aligned operands.  Each K step of 16 is one stage of an
+// S-stage ring in LDS, filled by global_load_lds_dwordx4 (16 bytes per lane straight into LDS, no register staging)
+// S - 1 steps ahead of the MFMAs, with one barrier per step.  Stage layout:
+//   A: BM rows of the step's 16 floats (four 16-byte chunks per row, chunk c of row r at slot c ^ swz(r));
+//   B: the step's rows 0-7, then 128 bytes on, rows 8-15, each row BN floats.
+// The K order within a step is permuted: MFMA j (j = 0..7) takes k = j from lanes 0-31 and k = 8 + j from lanes
+// 32-63, so a lane's A operands for the whole step are eight consecutive floats of its row (two 16-byte reads).
+// Rows past M and columns past N read a clamped in-range address (their results are not stored).
+__device__ __forceinline__ int dl_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+// LDS reads the compiler does not track, for the direct-load pipeline below; lds_wait<n>() then waits until at most
+// n of them are outstanding, and keep() after it ties a fragment to that wait so no MFMA using it is scheduled above it.  (The host pass
+// sees empty bodies: the register constraints exist on the device only.)
+__device__ __forceinline__ v4f lds_read_b128(uint32_t addr) {
+    v4f v;
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+#else
+    v = v4f{0.f, 0.f, 0.f, 0.f};
+    (void)addr;
+#endif
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ float lds_read_b32(uint32_t addr) {
+    float v;
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+#else
+    v = 0.f;
+    (void)addr;
+#endif
+    return v;
+}
+// global_load_lds_dwordx4: the lane's 16 bytes at g land in LDS at lds + 16 * lane (lds uniform over the wave)
+__device__ __forceinline__ void load_to_lds16(const float *g, char *lds) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+#else
+    (void)g;
+    (void)lds;
+#endif
+}
+template <int N>
+__device__ __forceinline__ void lds_wait() {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
+#endif
+}
+// no instruction is scheduled across this point
+__device__ __forceinline__ void sched_fence() {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __builtin_amdgcn_sched_barrier(0);
+#endif
+}
+template <typename T>
+__device__ __forceinline__ void keep(T &x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("" : "+v"(x));
+#else
+    (void)x;
+#endif
+}
+
+// s_waitcnt vmcnt(n) lgkmcnt(0), then s_barrier: this wave's direct loads but the last n have landed and its LDS
+// reads are done before any wave passes.  (A __syncthreads would wait for every outstanding direct load.)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_barrier() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+#if defined(__HIP_DEVICE_COMPILE__)
+    __asm__ volatile("s_barrier" ::: "memory");
+#endif
+}
+
+template <int BM, int BN, int WM, int WN, int S, int WMIN, int WMAX, bool GELU>
+__global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WMIN, WMAX))) void k_matmul_f32_dl(const float *__restrict__ A, const float *__restrict__ B,
+                                                                float *__restrict__ C, MatMulArgs p) {
+    constexpr int NW = WM * WN;
+    constexpr int WTM = BM / WM, WTN = BN / WN, MT = WTM / 32, NT = WTN / 32;
+    static_assert(MT * 32 == WTM && NT * 32 == WTN && S >= 2 && S <= 4, "waves of whole 32x32 tiles");
+    constexpr int A_BYTES = BM * 64, B_HALF = BN * 32, B_HI = A_BYTES + B_HALF + 128;
+    constexpr int STAGE = A_BYTES + 2 * B_HALF + 128;
+    static_assert(A_BYTES % 1024 == 0 && B_HALF % 1024 == 0, "whole wave loads");
+    constexpr int LA = A_BYTES / 1024, LBH = B_HALF / 1024, NL = LA + 2 * LBH;
+    constexpr int L = (NL + NW - 1) / NW;  // wave loads per wave per stage (the last one repeated when uneven)
+    // one LDS variable per stage: the compiler then knows that the reads of one stage do not wait for the
+    // direct loads still landing in the others
+    __shared__ __attribute__((aligned(1024))) char sm0[STAGE];
+    __shared__ __attribute__((aligned(1024))) char sm1[STAGE];
+    __shared__ __attribute__((aligned(1024))) char sm2[S > 2 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char sm3[S > 3 ? STAGE : 16];
+    auto stage_mem = [&](auto sidx) -> char * {
+        constexpr int sx = decltype(sidx)::value;
+        if constexpr (sx == 0) return sm0;
+        else if constexpr (sx == 1) return sm1;
+        else if constexpr (sx == 2) return sm2;
+        else return sm3;
+    };
+    __shared__ ExpTable tab;
+    if constexpr (GELU) exp_table_fill(tab);
+    const int M = p.m, N = p.n, K = p.k;
+    const int l = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    int64_t ao, bo;
+    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
+
+    // this wave's loads: a per-lane source address (advanced by `inc` floats per step) and an LDS offset
+    const float *src[L];
+    int64_t inc[L];
+    int dst[L];
+#pragma unroll
+    for (int j = 0; j < L; j++) {
+        const int i = min(w + NW * j, NL - 1);
+        if (i < LA) {
+            const int q = 64 * i + l, r = q >> 2, c = (q & 3) ^ dl_swz(r);
+            src[j] = A + ao + (int64_t)min(row0 + r, M - 1) * K + 4 * c;
+            inc[j] = 16;
+            dst[j] = 1024 * i;
+        } else {
+            const int h = (i - LA) / LBH, wl = (i - LA) % LBH, q = 64 * wl + l;
+            const int k = 8 * h + q / (BN / 4), c = col0 + 4 * (q % (BN / 4));
+            src[j] = B + bo + (int64_t)k * N + min(c, N - 4);
+            inc[j] = 16 * (int64_t)N;
+            dst[j] = A_BYTES + h * (B_HALF + 128) + 1024 * wl;
+        }
+    }
+    auto issue = [&](auto sidx, int kt) {
+        char *base = stage_mem(sidx);
+#pragma unroll
+        for (int j = 0; j < L; j++)
+            load_to_lds16(src[j] + kt * inc[j], base + dst[j]);
+    };
+
+    // fragment offsets within a stage
+    const int wr = (w / WN) * WTM, wc = (w % WN) * WTN, h = l / 32;
+    int aoff[MT][2], boff[NT];
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const int r = wr + 32 * i + (l % 32);
+#pragma unroll
+        for (int e = 0; e < 2; e++) aoff[i][e] = r * 64 + 16 * ((2 * h + e) ^ dl_swz(r));
+    }
+#pragma unroll
+    for (int j = 0; j < NT; j++) boff[j] = (h ? B_HI : A_BYTES) + 4 * (wc + 32 * j + (l % 32));
+
+    v16f acc[MT][NT];
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < NT; j++) {
-            const int c = col0 + wc + 32 * j + (l % 32);
-            if (c >= N) continue;
-            const float bc = Bias ? Bias[c] : 0.0f;
+        for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = row0 + wr + 32 * i + 8 * (r / 4) + 4 * (l / 32) + (r % 4);
-                if (row < M) {
-                    float v = acc[i][j][r];
-                    if (Bias) v = v + bc;
-                    if (Rb) v = v + Rb[(int64_t)row * N + c];
-                    if constexpr (GELU) v = gelu_erf_lx(v, tab);
-                    Cb[(int64_t)row * N + c] = v;
-                }
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int nk = K / 16;
+    // step t: wait for this wave's loads of step t (the S - 2 later steps' loads stay outstanding), barrier
+    // (every wave's loads of step t are visible and stage (t - 1) % S has been read), issue step t + S - 1 into
+    // that stage, then the MFMAs of stage t % S
+    auto step = [&](auto sidx, int t) {
+        constexpr int sx = decltype(sidx)::value;
+        wait_vmcnt_barrier<(S - 2) * L>();
+        // past the last step the ring re-loads step nk - 1 into a stage no later step reads: every step then
+        // issues the same loads, and the wait above is the same count everywhere
+        issue(std::integral_constant<int, (sx + S - 1) % S>(), min(t + S - 1, nk - 1));
+        // the stage's fragments by inline LDS reads, then one lgkmcnt(0): the compiler does not see these reads,
+        // so it adds no wait for the direct loads landing in the other stages; an empty asm on each fragment
+        // after the wait keeps every MFMA below it
+        const uint32_t stg = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stage_mem(sidx);
+        v4f af[MT][2];
+        float bf[NT][8];
+        // two groups, k = 8h + 0..3 then 8h + 4..7: the second group's reads are in flight while the first
+        // group's MFMAs run (LDS reads complete in issue order, so lgkmcnt(G) means the first group is in)
+        constexpr int G = MT + 4 * NT;
+        static_assert(G < 16, "lgkmcnt range");
+        auto read_group = [&](auto ec) {
+            constexpr int e = decltype(ec)::value;
+#pragma unroll
+            for (int i = 0; i < MT; i++) af[i][e] = lds_read_b128(stg + aoff[i][e]);
+#pragma unroll
+            for (int j = 0; j < NT; j++) {
+                const uint32_t b = stg + boff[j];
+                bf[j][4 * e + 0] = lds_read_b32<(4 * e + 0) * BN * 4>(b);
+                bf[j][4 * e + 1] = lds_read_b32<(4 * e + 1) * BN * 4>(b);
+                bf[j][4 * e + 2] = lds_read_b32<(4 * e + 2) * BN * 4>(b);
+                bf[j][4 * e + 3] = lds_read_b32<(4 * e + 3) * BN * 4>(b);
             }
+        };
+        read_group(std::integral_constant<int, 0>());
+        read_group(std::integral_constant<int, 1>());
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            if (e == 0) lds_wait<G>();
+            else lds_wait<0>();
+#pragma unroll
+            for (int i = 0; i < MT; i++) keep(af[i][e]);
+#pragma unroll
+            for (int j = 0; j < NT; j++)
+#pragma unroll
+                for (int kk = 4 * e; kk < 4 * e + 4; kk++) keep(bf[j][kk]);
+#pragma unroll
+            for (int kk = 4 * e; kk < 4 * e + 4; kk++)
+#pragma unroll
+                for (int i = 0; i < MT; i++)
+#pragma unroll
+                    for (int j = 0; j < NT; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][kk], af[i][e][kk % 4], acc[i][j], 0, 0, 0);
+            sched_fence();  // the first group's MFMAs stay above the second wait
         }
+    };
+    issue(std::integral_constant<int, 0>(), 0);
+    if (S > 2) issue(std::integral_constant<int, 1>(), min(1, nk - 1));
+    if (S > 3) issue(std::integral_constant<int, (S > 3 ? 2 : 0)>(), min(2, nk - 1));
+    for (int t = 0; t < nk; t += S) {
+        step(std::integral_constant<int, 0>(), t);
+        if (t + 1 < nk) step(std::integral_constant<int, 1>(), t + 1);
+        if (S > 2 && t + 2 < nk) step(std::integral_constant<int, (S > 2 ? 2 : 0)>(), t + 2);
+        if (S > 3 && t + 3 < nk) step(std::integral_constant<int, (S > 3 ? 3 : 0)>(), t + 3);
+    }
+    // the ring's last loads land before the wave can end (the block's LDS is then handed to another block)
+    __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
+    mm_epilogue<MT, NT, true, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
+}
+
+template <int BM, int BN, int WM, int WN, int S, int WMIN, int WMAX>
+static void launch_f32_dl(const float *a, const float *b, float *c, const MatMulArgs &p, hipStream_t s) {
+    dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
+    const dim3 blk(WM * WN * 64);
+    if (p.gelu) hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, S, WMIN, WMAX, true>), g, blk, 0, s, a, b, c, p);
+    else hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, S, WMIN, WMAX, false>), g, blk, 0, s, a, b, c, p);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -343,7 +613,10 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
     }
     const MatMulArgs &p = p0;
     if (dtype == kFloat) {
-        bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) && (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
+        // VEC: 16-byte loads of A and B and 16-byte epilogue accesses of C, the residual and the bias
+        bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) &&
+                   (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)p.res | (uintptr_t)p.bias) % 16 == 0) &&
+                   p.bias_bstr % 4 == 0;
         for (int d = 0; d < p.nbatch; d++) vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
         // block tile: among the tiles that give each of the 256 CUs two or more blocks (a lone block
         // per CU leaves its barrier and load latencies unhidden: measured 93 against 104 TF/s for
@@ -375,6 +648,40 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         // a short K (at most 64, attention scores): the epilogue outweighs the K loop, and 64x64 tiles run
         // faster than the large ones ([16,12,512,64]x[16,12,64,512]: 70 against 66 TFLOP/s)
         if (p.k <= 64) best = 5;
+        // The direct-load kernel (K a multiple of 16, 16-byte aligned operands) for every shape but short K
+        // (attention scores, K = 64: 84 against 80 TFLOP/s) and narrow N (attention context, N = 64: 102 against
+        // 100); both kernels sum in one order, so the choice never changes a result.  Tile: the one whose busiest
+        // CU has the least work, ceil(blocks / 256) tiles each costing its area over its measured efficiency.
+        // Each tile runs the stage count and occupancy hint measured best for it: 128x128 with two stages and at
+        // most two waves per SIMD (accumulators in AGPRs: 135 TFLOP/s at 4096^3 against 104 with them in VGPRs
+        // for three waves), 128x96 with three stages, the smaller tiles with four and three or more waves.
+        if (vec && p.k % 16 == 0 && p.k > 64 && p.n > 64 && p.m >= 64) {
+            static const Tile dcand[] = {{128, 128, 1.0}, {128, 96, 0.92}, {128, 64, 0.85}, {64, 64, 0.65}};
+            int dt = 0;
+            int64_t dblocks = 0;
+            double bc = 0;
+            for (int i = 0; i < 4; i++) {
+                const int64_t blocks =
+                    (int64_t)((p.m + dcand[i].bm - 1) / dcand[i].bm) * ((p.n + dcand[i].bn - 1) / dcand[i].bn) * p.batch;
+                const double cost = (double)((blocks + 255) / 256) * dcand[i].bm * dcand[i].bn / dcand[i].eff;
+                if (i == 0 || cost < bc) {
+                    dt = i;
+                    dblocks = blocks;
+                    bc = cost;
+                }
+            }
+            // 128x96 beyond one tile per CU: the register-staged kernel is ahead ([4096,768]x[768,2304], 768
+            // tiles: 115 against 111 TFLOP/s)
+            if (dt != 1 || dblocks <= 256) {
+                switch (dt) {
+                case 0: launch_f32_dl<128, 128, 2, 2, 2, 1, 2>(fa, fb, fc, p, s); break;
+                case 1: launch_f32_dl<128, 96, 4, 1, 3, 1, 2>(fa, fb, fc, p, s); break;
+                case 2: launch_f32_dl<128, 64, 2, 2, 4, 3, 8>(fa, fb, fc, p, s); break;
+                default: launch_f32_dl<64, 64, 2, 2, 4, 3, 8>(fa, fb, fc, p, s); break;
+                }
+                return hipGetLastError();
+            }
+        }
         switch (best) {
         case 0: launch_f32<128, 128, 2, 2>(fa, fb, fc, p, vec, s); break;
         case 1: launch_f32<128, 96, 4, 1>(fa, fb, fc, p, vec, s); break;
