@@ -222,9 +222,10 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     mm_epilogue<MT, NT, VEC, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
 }
 
-// Direct-to-LDS pipeline for K a multiple of 16 and 16-byte aligned operands.  Each K step of 16 is one stage of an
-// S-stage ring in LDS, filled by global_load_lds_dwordx4 (16 bytes per lane straight into LDS, no register staging)
-// S - 1 steps ahead of the MFMAs, with one barrier per step.  Stage layout:
+// Direct-to-LDS pipeline for K a multiple of 16 and 16-byte aligned operands.  Each K step of 16 is one stage of a
+// four-stage ring in LDS, filled by global_load_lds_dwordx4 (16 bytes per lane straight into LDS, no register
+// staging) three steps ahead of the MFMAs, with one barrier per step; each wave reads its fragments of a stage one
+// step before it multiplies them.  Stage layout:
 //   A: BM rows of the step's 16 floats (four 16-byte chunks per row, chunk c of row r at slot c ^ swz(r));
 //   B: the step's rows 0-7, then 128 bytes on, rows 8-15, each row BN floats.
 // The K order within a step is permuted: MFMA j (j = 0..7) takes k = j from lanes 0-31 and k = 8 + j from lanes
@@ -312,8 +313,8 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
     // direct loads still landing in the others
     __shared__ __attribute__((aligned(1024))) char sm0[STAGE];
     __shared__ __attribute__((aligned(1024))) char sm1[STAGE];
-    __shared__ __attribute__((aligned(1024))) char sm2[S > 2 ? STAGE : 16];
-    __shared__ __attribute__((aligned(1024))) char sm3[S > 3 ? STAGE : 16];
+    __shared__ __attribute__((aligned(1024))) char sm2[STAGE];
+    __shared__ __attribute__((aligned(1024))) char sm3[STAGE];
     auto stage_mem = [&](auto sidx) -> char * {
         constexpr int sx = decltype(sidx)::value;
         if constexpr (sx == 0) return sm0;
@@ -378,80 +379,92 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     const int nk = K / 16;
-    // step t: wait for this wave's loads of step t (the S - 2 later steps' loads stay outstanding), barrier
-    // (every wave's loads of step t are visible and stage (t - 1) % S has been read), issue step t + S - 1 into
-    // that stage, then the MFMAs of stage t % S
+    // Step t: wait for this wave's loads of step t + 1 (the S - 3 later steps' loads stay outstanding) and for
+    // its own fragments, read during step t - 1; barrier (every wave's loads of step t + 1 are visible, and
+    // stage (t - 1) % S, read during step t - 2, is free); issue step t + S - 1 into that stage; read step
+    // t + 1's fragments; run step t's MFMAs.  No read latency lies between the barrier and the first MFMA.
+    // The fragments are read by inline LDS reads the compiler does not see, so it adds no wait for the direct
+    // loads landing in the other stages; the empty asm on each fragment after the wait keeps every MFMA
+    // below it.
+    v4f caf[MT][2], naf[MT][2];
+    float cbf[NT][8], nbf[NT][8];
+    auto read_all = [&](auto sidx, v4f (&ra)[MT][2], float (&rb)[NT][8]) {
+        const uint32_t stg = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stage_mem(sidx);
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            ra[i][0] = lds_read_b128(stg + aoff[i][0]);
+            ra[i][1] = lds_read_b128(stg + aoff[i][1]);
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const uint32_t b = stg + boff[j];
+            rb[j][0] = lds_read_b32<0 * BN * 4>(b);
+            rb[j][1] = lds_read_b32<1 * BN * 4>(b);
+            rb[j][2] = lds_read_b32<2 * BN * 4>(b);
+            rb[j][3] = lds_read_b32<3 * BN * 4>(b);
+            rb[j][4] = lds_read_b32<4 * BN * 4>(b);
+            rb[j][5] = lds_read_b32<5 * BN * 4>(b);
+            rb[j][6] = lds_read_b32<6 * BN * 4>(b);
+            rb[j][7] = lds_read_b32<7 * BN * 4>(b);
+        }
+    };
     auto step = [&](auto sidx, int t) {
         constexpr int sx = decltype(sidx)::value;
-        wait_vmcnt_barrier<(S - 2) * L>();
+        wait_vmcnt_barrier<(S - 3) * L>();
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+            keep(caf[i][0]);
+            keep(caf[i][1]);
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) keep(cbf[j][kk]);
         // past the last step the ring re-loads step nk - 1 into a stage no later step reads: every step then
         // issues the same loads, and the wait above is the same count everywhere
         issue(std::integral_constant<int, (sx + S - 1) % S>(), min(t + S - 1, nk - 1));
-        // the stage's fragments by inline LDS reads, then one lgkmcnt(0): the compiler does not see these reads,
-        // so it adds no wait for the direct loads landing in the other stages; an empty asm on each fragment
-        // after the wait keeps every MFMA below it
-        const uint32_t stg = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stage_mem(sidx);
-        v4f af[MT][2];
-        float bf[NT][8];
-        // two groups, k = 8h + 0..3 then 8h + 4..7: the second group's reads are in flight while the first
-        // group's MFMAs run (LDS reads complete in issue order, so lgkmcnt(G) means the first group is in)
-        constexpr int G = MT + 4 * NT;
-        static_assert(G < 16, "lgkmcnt range");
-        auto read_group = [&](auto ec) {
-            constexpr int e = decltype(ec)::value;
+        read_all(std::integral_constant<int, (sx + 1) % S>(), naf, nbf);
 #pragma unroll
-            for (int i = 0; i < MT; i++) af[i][e] = lds_read_b128(stg + aoff[i][e]);
+        for (int kk = 0; kk < 8; kk++)
 #pragma unroll
-            for (int j = 0; j < NT; j++) {
-                const uint32_t b = stg + boff[j];
-                bf[j][4 * e + 0] = lds_read_b32<(4 * e + 0) * BN * 4>(b);
-                bf[j][4 * e + 1] = lds_read_b32<(4 * e + 1) * BN * 4>(b);
-                bf[j][4 * e + 2] = lds_read_b32<(4 * e + 2) * BN * 4>(b);
-                bf[j][4 * e + 3] = lds_read_b32<(4 * e + 3) * BN * 4>(b);
-            }
-        };
-        read_group(std::integral_constant<int, 0>());
-        read_group(std::integral_constant<int, 1>());
+            for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (e == 0) lds_wait<G>();
-            else lds_wait<0>();
+                for (int j = 0; j < NT; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cbf[j][kk], caf[i][kk / 4][kk % 4], acc[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < MT; i++) keep(af[i][e]);
-#pragma unroll
-            for (int j = 0; j < NT; j++)
-#pragma unroll
-                for (int kk = 4 * e; kk < 4 * e + 4; kk++) keep(bf[j][kk]);
-#pragma unroll
-            for (int kk = 4 * e; kk < 4 * e + 4; kk++)
-#pragma unroll
-                for (int i = 0; i < MT; i++)
-#pragma unroll
-                    for (int j = 0; j < NT; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(bf[j][kk], af[i][e][kk % 4], acc[i][j], 0, 0, 0);
-            sched_fence();  // the first group's MFMAs stay above the second wait
+        for (int i = 0; i < MT; i++) {
+            caf[i][0] = naf[i][0];
+            caf[i][1] = naf[i][1];
         }
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int kk = 0; kk < 8; kk++) cbf[j][kk] = nbf[j][kk];
     };
     issue(std::integral_constant<int, 0>(), 0);
-    if (S > 2) issue(std::integral_constant<int, 1>(), min(1, nk - 1));
-    if (S > 3) issue(std::integral_constant<int, (S > 3 ? 2 : 0)>(), min(2, nk - 1));
+    issue(std::integral_constant<int, 1>(), min(1, nk - 1));
+    issue(std::integral_constant<int, 2>(), min(2, nk - 1));
+    static_assert(S == 4, "fragments a step ahead need the loads two steps ahead");
+    wait_vmcnt_barrier<(S - 2) * L>();
+    read_all(std::integral_constant<int, 0>(), caf, cbf);
     for (int t = 0; t < nk; t += S) {
         step(std::integral_constant<int, 0>(), t);
         if (t + 1 < nk) step(std::integral_constant<int, 1>(), t + 1);
-        if (S > 2 && t + 2 < nk) step(std::integral_constant<int, (S > 2 ? 2 : 0)>(), t + 2);
-        if (S > 3 && t + 3 < nk) step(std::integral_constant<int, (S > 3 ? 3 : 0)>(), t + 3);
+        if (t + 2 < nk) step(std::integral_constant<int, 2>(), t + 2);
+        if (t + 3 < nk) step(std::integral_constant<int, 3>(), t + 3);
     }
+    lds_wait<0>();
     // the ring's last loads land before the wave can end (the block's LDS is then handed to another block)
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     mm_epilogue<MT, NT, true, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
 }
 
-template <int BM, int BN, int WM, int WN, int S, int WMIN, int WMAX>
+template <int BM, int BN, int WM, int WN, int WMIN, int WMAX>
 static void launch_f32_dl(const float *a, const float *b, float *c, const MatMulArgs &p, hipStream_t s) {
     dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
     const dim3 blk(WM * WN * 64);
-    if (p.gelu) hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, S, WMIN, WMAX, true>), g, blk, 0, s, a, b, c, p);
-    else hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, S, WMIN, WMAX, false>), g, blk, 0, s, a, b, c, p);
+    if (p.gelu) hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, 4, WMIN, WMAX, true>), g, blk, 0, s, a, b, c, p);
+    else hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, 4, WMIN, WMAX, false>), g, blk, 0, s, a, b, c, p);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -649,16 +662,14 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         // faster than the large ones ([16,12,512,64]x[16,12,64,512]: 70 against 66 TFLOP/s)
         if (p.k <= 64) best = 5;
         // The direct-load kernel (K a multiple of 16, 16-byte aligned operands) for every shape but short K
-        // (attention scores, K = 64: 84 against 80 TFLOP/s) and narrow N (attention context, N = 64: 102 against
-        // 100); both kernels sum in one order, so the choice never changes a result.  Tile: the one whose busiest
-        // CU has the least work, ceil(blocks / 256) tiles each costing its area over its measured efficiency.
-        // Each tile runs the stage count and occupancy hint measured best for it: 128x128 with two stages and at
+        // (attention scores, K = 64: the register-staged kernel 81 against 78 TFLOP/s); both kernels sum in one
+        // order, so the choice never changes a result.  Tile: the one whose busiest CU has the least work,
+        // ceil(blocks / 256) tiles each costing its area over its measured efficiency; 128x128 runs with at
         // most two waves per SIMD (accumulators in AGPRs: 135 TFLOP/s at 4096^3 against 104 with them in VGPRs
-        // for three waves), 128x96 with three stages, the smaller tiles with four and three or more waves.
-        if (vec && p.k % 16 == 0 && p.k > 64 && p.n > 64 && p.m >= 64) {
-            static const Tile dcand[] = {{128, 128, 1.0}, {128, 96, 0.92}, {128, 64, 0.85}, {64, 64, 0.65}};
+        // for three waves), 128x96 with one or two, the smaller tiles with three or more.
+        if (vec && p.k % 16 == 0 && p.k > 64 && p.n >= 64 && p.m >= 64) {
+            static const Tile dcand[] = {{128, 128, 1.0}, {128, 96, 0.96}, {64, 64, 0.95}, {128, 64, 0.94}};
             int dt = 0;
-            int64_t dblocks = 0;
             double bc = 0;
             for (int i = 0; i < 4; i++) {
                 const int64_t blocks =
@@ -666,21 +677,16 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
                 const double cost = (double)((blocks + 255) / 256) * dcand[i].bm * dcand[i].bn / dcand[i].eff;
                 if (i == 0 || cost < bc) {
                     dt = i;
-                    dblocks = blocks;
                     bc = cost;
                 }
             }
-            // 128x96 beyond one tile per CU: the register-staged kernel is ahead ([4096,768]x[768,2304], 768
-            // tiles: 115 against 111 TFLOP/s)
-            if (dt != 1 || dblocks <= 256) {
-                switch (dt) {
-                case 0: launch_f32_dl<128, 128, 2, 2, 2, 1, 2>(fa, fb, fc, p, s); break;
-                case 1: launch_f32_dl<128, 96, 4, 1, 3, 1, 2>(fa, fb, fc, p, s); break;
-                case 2: launch_f32_dl<128, 64, 2, 2, 4, 3, 8>(fa, fb, fc, p, s); break;
-                default: launch_f32_dl<64, 64, 2, 2, 4, 3, 8>(fa, fb, fc, p, s); break;
-                }
-                return hipGetLastError();
+            switch (dt) {
+            case 0: launch_f32_dl<128, 128, 2, 2, 1, 2>(fa, fb, fc, p, s); break;
+            case 1: launch_f32_dl<128, 96, 4, 1, 1, 2>(fa, fb, fc, p, s); break;
+            case 2: launch_f32_dl<64, 64, 2, 2, 3, 8>(fa, fb, fc, p, s); break;
+            default: launch_f32_dl<128, 64, 2, 2, 3, 8>(fa, fb, fc, p, s); break;
             }
+            return hipGetLastError();
         }
         switch (best) {
         case 0: launch_f32<128, 128, 2, 2>(fa, fb, fc, p, vec, s); break;
