@@ -20,6 +20,7 @@
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "lx_device.h"
 #include "lx_kernels.h"
@@ -287,6 +288,16 @@ __device__ __forceinline__ void keep(T &x) {
 #endif
 }
 
+// f(integral_constant<int, i>) for i = R0 .. R1 - 1, in order
+template <int R0, typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, R0 + Is>()), ...);
+}
+template <int R0, int R1, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (R1 > R0) static_for_impl<R0>(f, std::make_integer_sequence<int, R1 - R0>());
+}
+
 // s_waitcnt vmcnt(n) lgkmcnt(0), then s_barrier: this wave's direct loads but the last n have landed and its LDS
 // reads are done before any wave passes.  (A __syncthreads would wait for every outstanding direct load.)
 template <int N>
@@ -420,17 +431,37 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
         for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int kk = 0; kk < 8; kk++) keep(cbf[j][kk]);
-        // past the last step the ring re-loads step nk - 1 into a stage no later step reads: every step then
-        // issues the same loads, and the wait above is the same count everywhere
-        issue(std::integral_constant<int, (sx + S - 1) % S>(), min(t + S - 1, nk - 1));
-        read_all(std::integral_constant<int, (sx + 1) % S>(), naf, nbf);
-#pragma unroll
-        for (int kk = 0; kk < 8; kk++)
+        // the MFMAs of k pair kk, then a slice of the next stage's fragment reads (the direct loads after the first
+        // pair): the reads' latency hides under the MFMAs that follow, and the fences keep this order
+        const uint32_t nst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stage_mem(
+            std::integral_constant<int, (sx + 1) % S>());
+        constexpr int R = 2 * MT + 8 * NT;  // fragment reads per stage
+        auto read_one = [&](auto rc) {
+            constexpr int r = decltype(rc)::value;
+            if constexpr (r < 2 * MT) {
+                naf[r / 2][r % 2] = lds_read_b128(nst + aoff[r / 2][r % 2]);
+            } else {
+                constexpr int j = (r - 2 * MT) / 8, kk = (r - 2 * MT) % 8;
+                nbf[j][kk] = lds_read_b32<kk * BN * 4>(nst + boff[j]);
+            }
+        };
+        static_for<0, 8>([&](auto kc) {
+            constexpr int kk = decltype(kc)::value;
 #pragma unroll
             for (int i = 0; i < MT; i++)
 #pragma unroll
                 for (int j = 0; j < NT; j++)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(cbf[j][kk], caf[i][kk / 4][kk % 4], acc[i][j], 0, 0, 0);
+            sched_fence();
+            if constexpr (kk == 0) {
+                // past the last step the ring re-loads step nk - 1 into a stage no later step reads: every
+                // step then issues the same loads, and the wait above is the same count everywhere
+                issue(std::integral_constant<int, (sx + S - 1) % S>(), min(t + S - 1, nk - 1));
+            } else if constexpr (kk <= 6) {
+                static_for<(kk - 1) * R / 6, kk * R / 6>(read_one);
+            }
+            sched_fence();
+        });
 #pragma unroll
         for (int i = 0; i < MT; i++) {
             caf[i][0] = naf[i][0];
