@@ -3,7 +3,7 @@
 //
 // float : v_mfma_f32_32x32x2f32 (fp32 products, fp32 accumulation -- the
 //         reference's float32 arithmetic, summed in a different order, the
-//         same order in both kernels).  K a multiple of 16 with aligned
+//         same order in both kernels).  K a multiple of 64 with aligned
 //         operands: a ring of LDS stages filled by direct-to-LDS loads two or
 //         three K steps ahead (k_matmul_f32_dl); otherwise double-buffered LDS
 //         fed from registers one K step ahead (k_matmul_f32).  Block tiles
@@ -19,6 +19,7 @@
 //   16x16x4 f64: a = A[l%16][l/16], b = B[l/16][l%16], acc[r] = C[l/16 + 4r][l%16]
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <type_traits>
 #include <utility>
 
@@ -103,7 +104,7 @@ __device__ __forceinline__ void mm_epilogue(const v16f (&acc)[MT][NT], float *__
 // BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
 // = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered in LDS with k
 // as the outer index (A transposed to [k][m], B as [k][n]), so the lanes of a
-// fragment read 32 consecutive floats.  The kernel for K not a multiple of 16,
+// fragment read 32 consecutive floats.  The kernel for K not a multiple of 64,
 // unaligned operands, K <= 64, N <= 64 and 128x96 tiles beyond one per CU.
 constexpr int kFBK = 16, kFPad = 4;
 
@@ -223,7 +224,7 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     mm_epilogue<MT, NT, VEC, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
 }
 
-// Direct-to-LDS pipeline for K a multiple of 16 and 16-byte aligned operands.  Each K step of 16 is one stage of a
+// Direct-to-LDS pipeline for K a multiple of 64 and 16-byte aligned operands.  Each K step of 16 is one stage of a
 // four-stage ring in LDS, filled by global_load_lds_dwordx4 (16 bytes per lane straight into LDS, no register
 // staging) three steps ahead of the MFMAs, with one barrier per step; each wave reads its fragments of a stage one
 // step before it multiplies them.  Stage layout:
@@ -234,57 +235,25 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
 // Rows past M and columns past N read a clamped in-range address (their results are not stored).
 __device__ __forceinline__ int dl_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-// LDS reads the compiler does not track, for the direct-load pipeline below; lds_wait<n>() then waits until at most
-// n of them are outstanding, and keep() after it ties a fragment to that wait so no MFMA using it is scheduled above it.  (The host pass
-// sees empty bodies: the register constraints exist on the device only.)
-__device__ __forceinline__ v4f lds_read_b128(uint32_t addr) {
-    v4f v;
-#if defined(__HIP_DEVICE_COMPILE__)
-    __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
-#else
-    v = v4f{0.f, 0.f, 0.f, 0.f};
-    (void)addr;
-#endif
-    return v;
-}
-template <int OFF>
-__device__ __forceinline__ float lds_read_b32(uint32_t addr) {
-    float v;
-#if defined(__HIP_DEVICE_COMPILE__)
-    __asm__ volatile("ds_read_b32 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-#else
-    v = 0.f;
-    (void)addr;
-#endif
-    return v;
-}
-// global_load_lds_dwordx4: the lane's 16 bytes at g land in LDS at lds + 16 * lane (lds uniform over the wave)
+// global_load_lds_dwordx4: the lane's 16 bytes at g land in LDS at lds + 16 * lane (lds uniform over the wave).
+// Written as inline asm so that the compiler does not track these LDS writes: it would otherwise wait for every
+// outstanding direct load before LDS reads of the other stages.  The kernel orders them itself: a stage is read
+// only after an s_waitcnt vmcnt that covers its loads and a barrier.  (Loads the compiler does not count only
+// make its own vmcnt waits longer.)  M0 takes one wait state before the load.
 __device__ __forceinline__ void load_to_lds16(const float *g, char *lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
-    __builtin_amdgcn_global_load_lds(g, (__attribute__((address_space(3))) void *)lds, 16, 0, 0);
+    const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
+    __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(g)
+                     : "memory", "m0");
 #else
     (void)g;
     (void)lds;
-#endif
-}
-template <int N>
-__device__ __forceinline__ void lds_wait() {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __asm__ volatile("s_waitcnt lgkmcnt(%0)" ::"i"(N) : "memory");
 #endif
 }
 // no instruction is scheduled across this point
 __device__ __forceinline__ void sched_fence() {
 #if defined(__HIP_DEVICE_COMPILE__)
     __builtin_amdgcn_sched_barrier(0);
-#endif
-}
-template <typename T>
-__device__ __forceinline__ void keep(T &x) {
-#if defined(__HIP_DEVICE_COMPILE__)
-    __asm__ volatile("" : "+v"(x));
-#else
-    (void)x;
 #endif
 }
 
@@ -390,59 +359,41 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
     const int nk = K / 16;
-    // Step t: wait for this wave's loads of step t + 1 (the S - 3 later steps' loads stay outstanding) and for
-    // its own fragments, read during step t - 1; barrier (every wave's loads of step t + 1 are visible, and
-    // stage (t - 1) % S, read during step t - 2, is free); issue step t + S - 1 into that stage; read step
-    // t + 1's fragments; run step t's MFMAs.  No read latency lies between the barrier and the first MFMA.
-    // The fragments are read by inline LDS reads the compiler does not see, so it adds no wait for the direct
-    // loads landing in the other stages; the empty asm on each fragment after the wait keeps every MFMA
-    // below it.
-    v4f caf[MT][2], naf[MT][2];
-    float cbf[NT][8], nbf[NT][8];
+    // Step t: wait for this wave's loads of step t + 1 (the S - 3 later steps' loads stay outstanding); barrier
+    // (every wave's loads of step t + 1 are visible, and stage (t - 1) % S, read during step t - 2, is free);
+    // issue step t + S - 1 into that stage; read step t + 1's fragments; run step t's MFMAs on the fragments read
+    // during step t - 1.  No read latency lies between the barrier and the first MFMA.  The LDS reads are
+    // ordinary loads, waited for by the compiler; the direct loads are invisible to it (load_to_lds16).
+    // two fragment sets, the current step's and the next's, swapping roles from step to step (no copies)
+    v4f af0[MT][2], af1[MT][2];
+    float bf0[NT][8], bf1[NT][8];
     auto read_all = [&](auto sidx, v4f (&ra)[MT][2], float (&rb)[NT][8]) {
-        const uint32_t stg = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stage_mem(sidx);
+        const char *stg = stage_mem(sidx);
 #pragma unroll
         for (int i = 0; i < MT; i++) {
-            ra[i][0] = lds_read_b128(stg + aoff[i][0]);
-            ra[i][1] = lds_read_b128(stg + aoff[i][1]);
-        }
-#pragma unroll
-        for (int j = 0; j < NT; j++) {
-            const uint32_t b = stg + boff[j];
-            rb[j][0] = lds_read_b32<0 * BN * 4>(b);
-            rb[j][1] = lds_read_b32<1 * BN * 4>(b);
-            rb[j][2] = lds_read_b32<2 * BN * 4>(b);
-            rb[j][3] = lds_read_b32<3 * BN * 4>(b);
-            rb[j][4] = lds_read_b32<4 * BN * 4>(b);
-            rb[j][5] = lds_read_b32<5 * BN * 4>(b);
-            rb[j][6] = lds_read_b32<6 * BN * 4>(b);
-            rb[j][7] = lds_read_b32<7 * BN * 4>(b);
-        }
-    };
-    auto step = [&](auto sidx, int t) {
-        constexpr int sx = decltype(sidx)::value;
-        wait_vmcnt_barrier<(S - 3) * L>();
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-            keep(caf[i][0]);
-            keep(caf[i][1]);
+            ra[i][0] = *reinterpret_cast<const v4f *>(stg + aoff[i][0]);
+            ra[i][1] = *reinterpret_cast<const v4f *>(stg + aoff[i][1]);
         }
 #pragma unroll
         for (int j = 0; j < NT; j++)
 #pragma unroll
-            for (int kk = 0; kk < 8; kk++) keep(cbf[j][kk]);
+            for (int kk = 0; kk < 8; kk++) rb[j][kk] = *reinterpret_cast<const float *>(stg + boff[j] + kk * BN * 4);
+    };
+    auto step = [&](auto sidx, int t, const v4f (&caf)[MT][2], const float (&cbf)[NT][8], v4f (&naf)[MT][2],
+                    float (&nbf)[NT][8]) {
+        constexpr int sx = decltype(sidx)::value;
+        wait_vmcnt_barrier<(S - 3) * L>();
         // the MFMAs of k pair kk, then a slice of the next stage's fragment reads (the direct loads after the first
         // pair): the reads' latency hides under the MFMAs that follow, and the fences keep this order
-        const uint32_t nst = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)stage_mem(
-            std::integral_constant<int, (sx + 1) % S>());
+        const char *nst = stage_mem(std::integral_constant<int, (sx + 1) % S>());
         constexpr int R = 2 * MT + 8 * NT;  // fragment reads per stage
         auto read_one = [&](auto rc) {
             constexpr int r = decltype(rc)::value;
             if constexpr (r < 2 * MT) {
-                naf[r / 2][r % 2] = lds_read_b128(nst + aoff[r / 2][r % 2]);
+                naf[r / 2][r % 2] = *reinterpret_cast<const v4f *>(nst + aoff[r / 2][r % 2]);
             } else {
                 constexpr int j = (r - 2 * MT) / 8, kk = (r - 2 * MT) % 8;
-                nbf[j][kk] = lds_read_b32<kk * BN * 4>(nst + boff[j]);
+                nbf[j][kk] = *reinterpret_cast<const float *>(nst + boff[j] + kk * BN * 4);
             }
         };
         static_for<0, 8>([&](auto kc) {
@@ -462,29 +413,20 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
             }
             sched_fence();
         });
-#pragma unroll
-        for (int i = 0; i < MT; i++) {
-            caf[i][0] = naf[i][0];
-            caf[i][1] = naf[i][1];
-        }
-#pragma unroll
-        for (int j = 0; j < NT; j++)
-#pragma unroll
-            for (int kk = 0; kk < 8; kk++) cbf[j][kk] = nbf[j][kk];
     };
     issue(std::integral_constant<int, 0>(), 0);
     issue(std::integral_constant<int, 1>(), min(1, nk - 1));
     issue(std::integral_constant<int, 2>(), min(2, nk - 1));
-    static_assert(S == 4, "fragments a step ahead need the loads two steps ahead");
+    static_assert(S == 4, "fragments a step ahead need the loads two steps ahead; four steps per loop pass");
     wait_vmcnt_barrier<(S - 2) * L>();
-    read_all(std::integral_constant<int, 0>(), caf, cbf);
+    read_all(std::integral_constant<int, 0>(), af0, bf0);
+    // K is a multiple of 64: whole passes of four steps, each fragment set in the same registers on every pass
     for (int t = 0; t < nk; t += S) {
-        step(std::integral_constant<int, 0>(), t);
-        if (t + 1 < nk) step(std::integral_constant<int, 1>(), t + 1);
-        if (t + 2 < nk) step(std::integral_constant<int, 2>(), t + 2);
-        if (t + 3 < nk) step(std::integral_constant<int, 3>(), t + 3);
+        step(std::integral_constant<int, 0>(), t, af0, bf0, af1, bf1);
+        step(std::integral_constant<int, 1>(), t + 1, af1, bf1, af0, bf0);
+        step(std::integral_constant<int, 2>(), t + 2, af0, bf0, af1, bf1);
+        step(std::integral_constant<int, 3>(), t + 3, af1, bf1, af0, bf0);
     }
-    lds_wait<0>();
     // the ring's last loads land before the wave can end (the block's LDS is then handed to another block)
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
     mm_epilogue<MT, NT, true, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
@@ -692,25 +634,38 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         // a short K (at most 64, attention scores): the epilogue outweighs the K loop, and 64x64 tiles run
         // faster than the large ones ([16,12,512,64]x[16,12,64,512]: 70 against 66 TFLOP/s)
         if (p.k <= 64) best = 5;
-        // The direct-load kernel (K a multiple of 16, 16-byte aligned operands) for every shape but short K
+        // The direct-load kernel (K a multiple of 64, 16-byte aligned operands) for every shape but short K
         // (attention scores, K = 64: the register-staged kernel 81 against 78 TFLOP/s); both kernels sum in one
-        // order, so the choice never changes a result.  Tile: the one whose busiest CU has the least work,
-        // ceil(blocks / 256) tiles each costing its area over its measured efficiency; 128x128 runs with at
-        // most two waves per SIMD (accumulators in AGPRs: 135 TFLOP/s at 4096^3 against 104 with them in VGPRs
-        // for three waves), 128x96 with one or two, the smaller tiles with three or more.
-        if (vec && p.k % 16 == 0 && p.k > 64 && p.n >= 64 && p.m >= 64) {
-            static const Tile dcand[] = {{128, 128, 1.0}, {128, 96, 0.96}, {64, 64, 0.95}, {128, 64, 0.94}};
+        // order, so the choice never changes a result.  Tile: the least cost, where a tile config that holds r
+        // blocks per CU at once (its LDS and its occupancy hint) runs ceil(tiles / (256 r)) rounds, each as long
+        // as min(r, tiles per CU) of its tiles, each costing its area over a measured efficiency.  128x128 runs
+        // with at most two waves per SIMD (accumulators in AGPRs: 135 TFLOP/s at 4096^3 against 104 with them in
+        // VGPRs for three waves), 128x96 with one or two, the smaller tiles with three or more.  One 128x96 tile
+        // per CU over a long K (at least 2048) keeps that tile: its lone wave per SIMD runs the longest
+        // uninterrupted MFMA stream ([4096,3072]x[3072,768]: 133 against 126 TFLOP/s for 64x64).
+        if (vec && p.k % 64 == 0 && p.k > 64 && p.n >= 64 && p.m >= 64) {
+            struct DTile {
+                int bm, bn, resident;
+                double eff;
+            };
+            static const DTile dcand[] = {{128, 128, 2, 1.0}, {128, 96, 2, 0.9}, {64, 64, 4, 0.97}, {128, 64, 3, 0.95}};
+            auto tiles_of = [&](const DTile &c) {
+                return (int64_t)((p.m + c.bm - 1) / c.bm) * ((p.n + c.bn - 1) / c.bn) * p.batch;
+            };
             int dt = 0;
             double bc = 0;
             for (int i = 0; i < 4; i++) {
-                const int64_t blocks =
-                    (int64_t)((p.m + dcand[i].bm - 1) / dcand[i].bm) * ((p.n + dcand[i].bn - 1) / dcand[i].bn) * p.batch;
-                const double cost = (double)((blocks + 255) / 256) * dcand[i].bm * dcand[i].bn / dcand[i].eff;
+                const int64_t tiles = tiles_of(dcand[i]);
+                const int64_t rounds = (tiles + 256 * dcand[i].resident - 1) / (256 * dcand[i].resident);
+                const int64_t per_cu = std::min<int64_t>(dcand[i].resident, (tiles + 255) / 256);
+                const double cost = (double)(rounds * per_cu) * dcand[i].bm * dcand[i].bn / dcand[i].eff;
                 if (i == 0 || cost < bc) {
                     dt = i;
                     bc = cost;
                 }
             }
+            const int64_t t96 = tiles_of(dcand[1]);
+            if (t96 > 192 && t96 <= 256 && p.k >= 2048) dt = 1;
             switch (dt) {
             case 0: launch_f32_dl<128, 128, 2, 2, 1, 2>(fa, fb, fc, p, s); break;
             case 1: launch_f32_dl<128, 96, 4, 1, 1, 2>(fa, fb, fc, p, s); break;

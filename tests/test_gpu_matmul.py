@@ -78,18 +78,18 @@ def test_float_every_block_tile(hip, sa, sb):
     check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
 
 
-@pytest.mark.parametrize("sa,sb", [((4096, 768), (768, 768)), ((2000, 160), (160, 2020)), ((4000, 160), (160, 740)),
-                                   ((4096, 256), (256, 512)), ((200, 96), (96, 196)), ((3, 1, 130, 96), (1, 2, 96, 132)),
-                                   ((64, 80), (80, 68))])
+@pytest.mark.parametrize("sa,sb", [((4096, 768), (768, 768)), ((2000, 192), (192, 2020)), ((4000, 192), (192, 740)),
+                                   ((4096, 256), (256, 512)), ((200, 128), (128, 196)), ((3, 1, 130, 128), (1, 2, 128, 132)),
+                                   ((64, 128), (128, 68)), ((2, 12, 512, 512), (2, 12, 512, 64))])
 def test_float_direct_load_tiles(hip, sa, sb):
-    """K a multiple of 16 above 64 with aligned operands: the direct-to-LDS kernel, on shapes whose tile choice
+    """K a multiple of 64 above 64 with aligned operands: the direct-to-LDS kernel, on shapes whose tile choice
     lands on each of its tiles (128x96 one per CU, 128x128 and 128x96 with partial edge tiles, 128x64, 64x64 with
-    partial tiles, broadcast batches, the smallest shape it takes)."""
+    partial tiles, broadcast batches, the smallest shape it takes, attention context with N = 64)."""
     rng = np.random.default_rng(56)
     check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 96, 196), (2000, 160, 2020), (4096, 768, 768)])
+@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 768, 768), (300, 80, 260)])
 def test_float_kernels_sum_in_one_order(hip, m, k, n):
     """The direct-load kernel and the register-staged one add the products of a dot product in the same order,
     so a product is the same bits whichever runs it: the whole product (direct loads) against its 32-row blocks
@@ -160,7 +160,7 @@ def _nodes(a, b, bias, res):
 
 @pytest.mark.parametrize("sa,sb,sbias,sres", [
     ((256, 768), (768, 768), (768,), None), ((4, 64, 768), (768, 256), (256,), (4, 64, 256)),
-    ((4000, 160), (160, 740), (740,), (4000, 740)), ((2000, 160), (160, 2020), (2020,), None),
+    ((4000, 192), (192, 740), (740,), (4000, 740)), ((2000, 192), (192, 2020), (2020,), None),
     ((2, 3, 33, 40), (40, 70), (1, 70), (2, 3, 33, 70)), ((128, 64), (64, 96), (96,), (128, 96)),
     # shapes the epilogue does not take: the MatMul and the Adds one after the other
     ((64, 32), (32, 48), (64, 48), None), ((64, 32), (32, 48), (48,), (48,)), ((5, 32), (32, 48), (3, 1, 48), None)])
@@ -297,7 +297,8 @@ def _gelu_nodes(t):
 
 
 @pytest.mark.parametrize("sa,sb,sbias", [((256, 768), (768, 3072), (3072,)), ((2, 64, 768), (768, 256), (256,)),
-                                         ((2000, 160), (160, 2020), (2020,)), ((4096, 768), (768, 768), (768,)),
+                                         ((2000, 192), (192, 2020), (2020,)), ((4096, 768), (768, 768), (768,)),
+                                         ((4096, 768), (768, 2304), (2304,)),
                                          ((127, 65), (65, 129), (129,)), ((3, 33, 40), (3, 40, 70), (3, 1, 70)),
                                          ((64, 32), (32, 48), (64, 48))])
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
