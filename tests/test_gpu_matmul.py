@@ -298,14 +298,17 @@ def _gelu_nodes(t):
 
 @pytest.mark.parametrize("sa,sb,sbias", [((256, 768), (768, 3072), (3072,)), ((2, 64, 768), (768, 256), (256,)),
                                          ((2000, 192), (192, 2020), (2020,)), ((4096, 768), (768, 768), (768,)),
-                                         ((4096, 768), (768, 2304), (2304,)),
+                                         ((4096, 768), (768, 2304), (2304,)), ((2048, 256), (256, 4096), (4096,)),
+                                         ((98304, 128), (128, 64), (64,)),
                                          ((127, 65), (65, 129), (129,)), ((3, 33, 40), (3, 40, 70), (3, 1, 70)),
                                          ((64, 32), (32, 48), (64, 48))])
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
 def test_matmul_add_gelu_equals_the_nodes(hip, sa, sb, sbias, dt):
     """MatMul -> Add bias -> GELU (Div sqrt2, Erf, Add 1, Mul x, Mul 0.5) as one launch with the Add and the
     GELU in the MatMul's epilogue, bit for bit the seven separate operators: a BERT FFN shape, a batch, ragged
-    tiles, a bias row per batch; a bias that is no row vector, and Double, run the nodes."""
+    tiles, a bias row per batch; shapes that put several blocks of each direct-load tile on a CU at once (64x64
+    at [4096,768]x[768,2304], 128x128 two per CU, 128x64 three per CU); a bias that is no row vector, and
+    Double, run the nodes."""
     rng = np.random.default_rng(61)
     a = rng.standard_normal(sa).astype(dt)
     b = (rng.standard_normal(sb) * 0.1).astype(dt)
