@@ -89,11 +89,12 @@ def test_float_direct_load_tiles(hip, sa, sb):
     check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 768, 768), (300, 80, 260)])
+@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 768, 768), (320, 192, 260)])
 def test_float_kernels_sum_in_one_order(hip, m, k, n):
     """The direct-load kernel and the register-staged one add the products of a dot product in the same order,
-    so a product is the same bits whichever runs it: the whole product (direct loads) against its 32-row blocks
-    (fewer than 64 rows: the register-staged kernel) and its 64-column blocks (N = 64: the same), bit for bit."""
+    so a product is the same bits whichever kernel and tile runs it: the whole product (direct loads) against
+    its 32-row blocks (fewer than 64 rows: the register-staged kernel) and its 64-column blocks (N = 64: another
+    tile of the direct-load kernel), bit for bit."""
     rng = np.random.default_rng(58)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)
