@@ -239,12 +239,12 @@ __device__ __forceinline__ int dl_swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3;
 // Written as inline asm so that the compiler does not track these LDS writes: it would otherwise wait for every
 // outstanding direct load before LDS reads of the other stages.  The kernel orders them itself: a stage is read
 // only after an s_waitcnt vmcnt that covers its loads and a barrier.  (Loads the compiler does not count only
-// make its own vmcnt waits longer.)  M0 takes one wait state before the load.
+// make its own vmcnt waits longer.)  The LDS address goes in M0 (set by the compiler, an operand of the asm),
+// which takes one wait state before the load.
 __device__ __forceinline__ void load_to_lds16(const float *g, char *lds) {
 #if defined(__HIP_DEVICE_COMPILE__)
     const uint32_t m0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char *)lds;
-    __asm__ volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(g)
-                     : "memory", "m0");
+    __asm__ volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"{m0}"(m0), "v"(g) : "memory");
 #else
     (void)g;
     (void)lds;

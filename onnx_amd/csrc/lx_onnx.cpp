@@ -121,14 +121,6 @@ void read_fixed64s(Reader &r, uint32_t wt, std::vector<uint64_t> *out) {
 
 int bad(const char *what) { return api_set_error(LX_ERR_INVALID_ARGUMENT, fmt("Malformed ONNX model: %s.", what)); }
 
-// TensorElementType names as .NET prints the enum
-const char *tet_name(int64_t t) {
-    static const char *names[] = {"Undefined", "Float", "UInt8", "Int8", "UInt16", "Int16", "Int32", "Int64",
-                                  "String", "Bool", "Float16", "Double", "UInt32", "UInt64", "Complex64",
-                                  "Complex128", "BFloat16"};
-    return (t >= 0 && t <= 16) ? names[t] : "Unknown";
-}
-
 // TensorProto -> HostTensor (TensorExtensions.ToTensor, TensorUtil.cs:14-58)
 int parse_tensor(Reader r, HostTensor *h, std::string *name) {
     std::vector<int64_t> dims, i64;
