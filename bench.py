@@ -744,6 +744,32 @@ def bench_extras(torch, HIP, DeviceTensor, set_stream, steps, warmup, W):
         gl.close()
     del bdev
 
+    # the whole encoder of the reference's benchmark and model-test model (me5s, multilingual-e5-small: 12
+    # layers, hidden 384, 12 heads of 32, FFN 1536; random weights), token ids and attention mask to the last
+    # hidden state, batch 8 x 512 tokens
+    from bert_layer import encoder_model
+    model, eins, _, _ = encoder_model(8, 512, seed=5)
+    edev = {k: DeviceTensor.from_numpy(v) for k, v in eins.items()}
+    h, ffw, heads, nl = 384, 1536, 12, 12
+    enc_flops = nl * (2.0 * 4096 * (4 * h * h + 2 * h * ffw) + 2 * 2.0 * 8 * heads * 512 * 512 * (h // heads))
+    for label, capture in (("fused", False), ("fused, captured", True)):
+        ge = Model.Load(model)
+        ge.Fuse()
+        if capture:
+            assert ge.Capture(edev), ge.LastError
+
+        def enc_step(i, ge=ge, capture=capture):
+            if not (ge.Replay() if capture else ge.Execute(edev)):
+                raise RuntimeError(ge.LastError)
+        ms = wall_time(torch, enc_step, max(8, steps // 16), max(2, warmup // 4))
+        d = {"op": f"me5s-shaped encoder (12 layers, hidden 384) [8,512] tokens, {label} (per execution)",
+             "us": round(ms * 1e3, 1), "tokens_per_s": round(4096 / (ms * 1e-3), 1),
+             "TFLOP/s": round(enc_flops / (ms * 1e-3) / 1e12, 2), "flops": enc_flops}
+        log(json.dumps(d))
+        res.append(d)
+        ge.close()
+    del edev
+
     # MatMul (row f2): fp32 MFMA, compute-bound; BERT-base shapes at batch 8 x 512 tokens
     for name, sa, sb in (("MatMul fp32 [4096,768]x[768,768] (dense)", (4096, 768), (768, 768)),
                          ("MatMul fp32 [4096,768]x[768,2304] (fused QKV projection)", (4096, 768), (768, 2304)),

@@ -108,3 +108,123 @@ def bert_layer_f64(inputs, inits):
     from scipy.special import erf
     g = f * 0.5 * (1.0 + erf(f / math.sqrt(2.0)))
     return ln(g @ d["w2"] + d["b2"] + h1, d["gamma2"], d["beta2"])
+
+
+def encoder_model(batch, seq, layers=12, hidden=384, heads=12, ff=1536, vocab=30522, max_pos=512, seed=0):
+    """A whole BERT-class encoder as ONNX (the node sequence a PyTorch export of a BERT model produces, static
+    shapes), by default shaped like me5s, the model the reference's benchmarks and model test run
+    (multilingual-e5-small: 12 layers, hidden 384, 12 heads of 32, FFN 1536; random weights, a BERT-size
+    vocabulary to keep the embedding table small):
+
+      embeddings  Gather word rows by input_ids + Gather position rows + the token-type-0 row, LayerNorm
+      mask        Unsqueeze attention_mask [B,S] to [B,1,1,S], Cast to float, (1 - m) * -10000
+      layers      each as bert_layer's: Q/K/V projections + heads, scaled masked Softmax attention, output
+                  projection + residual, LayerNorm, Erf-GELU FFN + residual, LayerNorm
+
+    Returns (model bytes, inputs, initializers, node list)."""
+    rng = np.random.default_rng(seed)
+    f32 = np.float32
+    dh = hidden // heads
+
+    def w(*shape, scale=0.02):
+        return (rng.standard_normal(shape) * scale).astype(f32)
+
+    inits = {
+        "word_emb": w(vocab, hidden, scale=0.5), "pos_emb": w(max_pos, hidden, scale=0.5),
+        "tt_row": w(hidden, scale=0.5), "position_ids": np.arange(seq, dtype=np.int64).reshape(1, seq),
+        "gamma_emb": (1 + w(hidden)).astype(f32), "beta_emb": w(hidden),
+        "unsq_axes": np.array([1, 2], np.int64), "neg": np.array(-10000.0, f32),
+        "heads_shape": np.array([batch, seq, heads, dh], np.int64),
+        "hidden_shape": np.array([batch, seq, hidden], np.int64),
+        "scale": np.array(math.sqrt(dh), f32), "axes": np.array([-1], np.int64), "two": np.array(2.0, f32),
+        "eps": np.array(1e-12, f32), "sqrt2": np.array(SQRT2, f32), "one": np.array(1.0, f32),
+        "half": np.array(0.5, f32),
+    }
+    nodes = [W.node("Gather", ["word_emb", "input_ids"], ["we"], "emb_word", axis=0),
+             W.node("Gather", ["pos_emb", "position_ids"], ["pe"], "emb_pos", axis=0),
+             W.node("Add", ["we", "pe"], ["e0"], "emb_add_pos"),
+             W.node("Add", ["e0", "tt_row"], ["e1"], "emb_add_tt")]
+    nodes += _ln("e1", "h_0", "_emb")
+    nodes += [W.node("Unsqueeze", ["attention_mask", "unsq_axes"], ["m0"], "mask_unsqueeze"),
+              W.node("Cast", ["m0"], ["m1"], "mask_cast", to=1),
+              W.node("Sub", ["one", "m1"], ["m2"], "mask_invert"),
+              W.node("Mul", ["m2", "neg"], ["mask"], "mask_scale")]
+    for i in range(layers):
+        sx = f"_L{i}"
+        for k, shape in (("wq", (hidden, hidden)), ("wk", (hidden, hidden)), ("wv", (hidden, hidden)),
+                         ("wo", (hidden, hidden)), ("w1", (hidden, ff)), ("w2", (ff, hidden))):
+            inits[k + sx] = w(*shape)
+        for k, n in (("bq", hidden), ("bk", hidden), ("bv", hidden), ("bo", hidden), ("b1", ff), ("b2", hidden)):
+            inits[k + sx] = w(n)
+        for k in ("1", "2"):
+            inits[f"gamma{k}{sx}"] = (1 + w(hidden)).astype(f32)
+            inits[f"beta{k}{sx}"] = w(hidden)
+        x, y = f"h_{i}", f"h_{i + 1}"
+        for t, perm in (("q", [0, 2, 1, 3]), ("k", [0, 2, 3, 1]), ("v", [0, 2, 1, 3])):
+            nodes += [W.node("MatMul", [x, f"w{t}{sx}"], [f"{t}0{sx}"], f"{t}_proj{sx}"),
+                      W.node("Add", [f"{t}0{sx}", f"b{t}{sx}"], [f"{t}1{sx}"], f"{t}_bias{sx}"),
+                      W.node("Reshape", [f"{t}1{sx}", "heads_shape"], [f"{t}2{sx}"], f"{t}_heads{sx}"),
+                      W.node("Transpose", [f"{t}2{sx}"], [f"{t}h{sx}"], f"{t}_perm{sx}", perm=perm)]
+        nodes += [W.node("MatMul", [f"qh{sx}", f"kh{sx}"], [f"s0{sx}"], f"scores{sx}"),
+                  W.node("Div", [f"s0{sx}", "scale"], [f"s1{sx}"], f"scale{sx}"),
+                  W.node("Add", [f"s1{sx}", "mask"], [f"s2{sx}"], f"mask_add{sx}"),
+                  W.node("Softmax", [f"s2{sx}"], [f"probs{sx}"], f"softmax{sx}", axis=-1),
+                  W.node("MatMul", [f"probs{sx}", f"vh{sx}"], [f"c0{sx}"], f"context{sx}"),
+                  W.node("Transpose", [f"c0{sx}"], [f"c1{sx}"], f"c_perm{sx}", perm=[0, 2, 1, 3]),
+                  W.node("Reshape", [f"c1{sx}", "hidden_shape"], [f"c2{sx}"], f"c_merge{sx}"),
+                  W.node("MatMul", [f"c2{sx}", f"wo{sx}"], [f"o0{sx}"], f"o_proj{sx}"),
+                  W.node("Add", [f"o0{sx}", f"bo{sx}"], [f"o1{sx}"], f"o_bias{sx}"),
+                  W.node("Add", [f"o1{sx}", x], [f"r1{sx}"], f"residual1{sx}")]
+        nodes += _ln(f"r1{sx}", f"a{sx}", f"1{sx}")
+        nodes += [W.node("MatMul", [f"a{sx}", f"w1{sx}"], [f"f0{sx}"], f"ffn_in{sx}"),
+                  W.node("Add", [f"f0{sx}", f"b1{sx}"], [f"f1{sx}"], f"ffn_bias{sx}"),
+                  W.node("Div", [f"f1{sx}", "sqrt2"], [f"g0{sx}"], f"gelu_div{sx}"),
+                  W.node("Erf", [f"g0{sx}"], [f"g1{sx}"], f"gelu_erf{sx}"),
+                  W.node("Add", [f"g1{sx}", "one"], [f"g2{sx}"], f"gelu_add{sx}"),
+                  W.node("Mul", [f"f1{sx}", f"g2{sx}"], [f"g3{sx}"], f"gelu_mul{sx}"),
+                  W.node("Mul", [f"g3{sx}", "half"], [f"g4{sx}"], f"gelu_half{sx}"),
+                  W.node("MatMul", [f"g4{sx}", f"w2{sx}"], [f"f2{sx}"], f"ffn_out{sx}"),
+                  W.node("Add", [f"f2{sx}", f"b2{sx}"], [f"f3{sx}"], f"ffn_out_bias{sx}"),
+                  W.node("Add", [f"f3{sx}", f"a{sx}"], [f"r2{sx}"], f"residual2{sx}")]
+        nodes += _ln(f"r2{sx}", y, f"2{sx}")
+    ids = rng.integers(0, vocab, (batch, seq)).astype(np.int64)
+    am = np.ones((batch, seq), np.int64)
+    for b in range(batch):  # the padding of each sequence: its last positions
+        am[b, seq - (b * 7) % (seq // 4):] = 0
+    # the model's output is the last layer's hidden state (last_hidden_state)
+    nodes[-1] = W.node("Add", [f"m2_L{layers - 1}", f"beta2_L{layers - 1}"], ["last_hidden_state"], f"addb2_L{layers - 1}")
+    model = W.model(nodes, [("input_ids", np.int64, ids.shape), ("attention_mask", np.int64, am.shape)],
+                    [("last_hidden_state", f32, (batch, seq, hidden))], list(inits.items()))
+    return model, {"input_ids": ids, "attention_mask": am}, inits, nodes
+
+
+def encoder_model_f64(inputs, inits, layers=12, heads=12):
+    """The same encoder in float64 numpy (an independent evaluation, for accuracy bounds)."""
+    from scipy.special import erf
+    d = {k: np.asarray(v, np.float64) if np.asarray(v).dtype.kind == "f" else np.asarray(v) for k, v in inits.items()}
+    ids, am = inputs["input_ids"], inputs["attention_mask"]
+    b, s = ids.shape
+    hidden = d["word_emb"].shape[1]
+    dh = hidden // heads
+
+    def ln(t, g, be):
+        m = t.mean(-1, keepdims=True)
+        v = ((t - m) ** 2).mean(-1, keepdims=True)
+        return (t - m) / np.sqrt(v + 1e-12) * g + be
+
+    def split(t):
+        return t.reshape(b, s, heads, dh).transpose(0, 2, 1, 3)
+
+    x = ln(d["word_emb"][ids] + d["pos_emb"][d["position_ids"]] + d["tt_row"], d["gamma_emb"], d["beta_emb"])
+    mask = (1.0 - am.astype(np.float64)).reshape(b, 1, 1, s) * -10000.0
+    for i in range(layers):
+        sx = f"_L{i}"
+        q, k, v = (split(x @ d[f"w{t}{sx}"] + d[f"b{t}{sx}"]) for t in "qkv")
+        sc = q @ k.transpose(0, 1, 3, 2) / math.sqrt(dh) + mask
+        sc = np.exp(sc - sc.max(-1, keepdims=True))
+        c = (sc / sc.sum(-1, keepdims=True) @ v).transpose(0, 2, 1, 3).reshape(b, s, hidden)
+        a = ln(c @ d[f"wo{sx}"] + d[f"bo{sx}"] + x, d[f"gamma1{sx}"], d[f"beta1{sx}"])
+        f = a @ d[f"w1{sx}"] + d[f"b1{sx}"]
+        g = f * 0.5 * (1.0 + erf(f / math.sqrt(2.0)))
+        x = ln(g @ d[f"w2{sx}"] + d[f"b2{sx}"] + a, d[f"gamma2{sx}"], d[f"beta2{sx}"])
+    return x

@@ -221,6 +221,32 @@ def test_bert_layer_oracle_against_float64():
     assert np.abs(ref - bert_layer_f64(ins, inits)).max() < 1e-5
 
 
+def test_encoder_oracle_against_float64():
+    """The oracle's node-by-node float32 evaluation of a two-layer me5s-shaped encoder (embedding Gathers, the
+    attention-mask Unsqueeze / Cast / scale, two encoder layers) stays within 1e-5 of an independent float64
+    evaluation."""
+    from bert_layer import encoder_model, encoder_model_f64
+    from oracle import graph_oracle as GO
+    from test_gpu_graph import _dict_nodes
+    _, ins, inits, nodes = encoder_model(1, 16, layers=2, vocab=500, seed=4)
+    ref = GO.run(_dict_nodes(nodes), ins, inits)["last_hidden_state"]
+    assert np.abs(ref - encoder_model_f64(ins, inits, layers=2)).max() < 1e-5
+
+
+def test_encoder_fusion_plan():
+    """Every layer of the encoder fuses as the single layer does (7 fusions), plus the embedding sum, the
+    embedding LayerNorm and the mask's Sub -> Mul."""
+    from bert_layer import encoder_model
+    model, _, _, _ = encoder_model(1, 16, layers=3, vocab=500, seed=4)
+    g = Model.Load(model)
+    assert g.Fuse() == 3 * 7 + 3
+    ops = [n.Op for n in g.Nodes]
+    assert ops[:7] == ["Gather", "Gather", "ElementwiseChain", "LayerNormDecomposed", "Unsqueeze", "Cast",
+                       "ElementwiseChain"]
+    assert ops.count("MatMulAddGroup") == 3 and ops.count("MatMulAddGelu") == 3 and ops.count("ScaleAddSoftmax") == 3
+    assert ops.count("LayerNormDecomposed") == 1 + 2 * 3 and "Add" not in ops and "Div" not in ops
+
+
 def test_bert_layer_fusion_plan():
     from bert_layer import bert_layer
     model, _, _, _ = bert_layer(1, 16, 3)
