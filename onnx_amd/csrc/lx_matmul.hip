@@ -643,6 +643,12 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         // VGPRs for three waves), 128x96 with one or two, the smaller tiles with three or more.  One 128x96 tile
         // per CU over a long K (at least 2048) keeps that tile: its lone wave per SIMD runs the longest
         // uninterrupted MFMA stream ([4096,3072]x[3072,768]: 133 against 126 TFLOP/s for 64x64).
+        // N of at most 32 (the attention context of 32-wide heads): 128x32 tiles, four waves of 32x32
+        // ([8,12,512,512]x[8,12,512,32]: 65 against 43 TFLOP/s for the register-staged kernel's 64x64)
+        if (vec && p.k % 64 == 0 && p.k > 64 && p.n <= 32 && p.m >= 64) {
+            launch_f32_dl<128, 32, 4, 1, 1, 2>(fa, fb, fc, p, s);
+            return hipGetLastError();
+        }
         if (vec && p.k % 64 == 0 && p.k > 64 && p.n >= 64 && p.m >= 64) {
             struct DTile {
                 int bm, bn, resident;

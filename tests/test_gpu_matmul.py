@@ -80,29 +80,33 @@ def test_float_every_block_tile(hip, sa, sb):
 
 @pytest.mark.parametrize("sa,sb", [((4096, 768), (768, 768)), ((2000, 192), (192, 2020)), ((4000, 192), (192, 740)),
                                    ((4096, 256), (256, 512)), ((200, 128), (128, 196)), ((3, 1, 130, 128), (1, 2, 128, 132)),
-                                   ((64, 128), (128, 68)), ((2, 12, 512, 512), (2, 12, 512, 64))])
+                                   ((64, 128), (128, 68)), ((2, 12, 512, 512), (2, 12, 512, 64)),
+                                   ((2, 12, 512, 512), (2, 12, 512, 32)), ((300, 128), (128, 20))])
 def test_float_direct_load_tiles(hip, sa, sb):
     """K a multiple of 64 above 64 with aligned operands: the direct-to-LDS kernel, on shapes whose tile choice
     lands on each of its tiles (128x96 one per CU, 128x128 and 128x96 with partial edge tiles, 128x64, 64x64 with
-    partial tiles, broadcast batches, the smallest shape it takes, attention context with N = 64)."""
+    partial tiles, broadcast batches, the smallest shape it takes, attention context with N = 64 and N = 32 (128x32
+    tiles), a ragged N = 20)."""
     rng = np.random.default_rng(56)
     check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 768, 768), (320, 192, 260)])
+@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 768, 768), (320, 192, 260),
+                                   (512, 512, 32)])
 def test_float_kernels_sum_in_one_order(hip, m, k, n):
     """The direct-load kernel and the register-staged one add the products of a dot product in the same order,
     so a product is the same bits whichever kernel and tile runs it: the whole product (direct loads) against
     its 32-row blocks (fewer than 64 rows: the register-staged kernel) and its 64-column blocks (N = 64: another
-    tile of the direct-load kernel), bit for bit."""
+    tile of the direct-load kernel), bit for bit; N = 32 takes the 128x32 tile."""
     rng = np.random.default_rng(58)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)
     whole = mm(a, b)
     rows = np.concatenate([mm(a[i:i + 32], b) for i in range(0, m, 32)])
     assert np.array_equal(whole.view(np.uint32), rows.view(np.uint32))
-    cols = np.concatenate([mm(a, np.ascontiguousarray(b[:, j:j + 64])) for j in range(0, n - n % 64, 64)], axis=1)
-    assert np.array_equal(whole[:, :cols.shape[1]].view(np.uint32), cols.view(np.uint32))
+    if n >= 128:
+        cols = np.concatenate([mm(a, np.ascontiguousarray(b[:, j:j + 64])) for j in range(0, n - n % 64, 64)], axis=1)
+        assert np.array_equal(whole[:, :cols.shape[1]].view(np.uint32), cols.view(np.uint32))
 
 
 @pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 70, 33), (33, 65)), ((2, 1, 40, 17), (3, 17, 66))])
