@@ -1752,10 +1752,30 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     if (p.nbatch > kMaxOuter) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d batch axes are supported.", kMaxOuter);
     if (x.dims[x.rank - 2] > INT32_MAX || x.dims[x.rank - 1] > INT32_MAX || y.dims[y.rank - 1] > INT32_MAX)
         return set_err(LX_ERR_NOT_SUPPORTED, "Matrix dimensions beyond 2^31 are not supported.");
+    // One right matrix for every batch and the left matrices stored row after row ([B, S, H] x [H, N]): one
+    // [batch * m, k] x [k, n] product, the same rows with the same sums, in one grid of row tiles
+    bool fold = p.nbatch > 0 && bias_bstr == 0;
+    int64_t rows = x.dims[x.rank - 2];
+    for (int d = p.nbatch - 1; fold && d >= 0; d--) {
+        if (p.bdims[d] != 1) fold = p.b_bstr[d] == 0 && p.a_bstr[d] == rows * p.k;
+        rows *= p.bdims[d];
+    }
+    if (fold && rows <= INT32_MAX) {
+        p.m = (int32_t)rows;
+        p.nbatch = 0;
+        p.batch = 1;
+    }
     if (p.k == 0) {  // empty inner dimension: every output is 0 (the Adds, if any, run afterwards)
         int64_t n = numel(Y);
         HIPCHECK(launch_fill(Y->data, n, (int)esize(dt), 0, g.stream), "MatMul");
         return LX_OK;
+    }
+    // partial products of a split K (stream-ordered pool block, released with the caller's temporaries)
+    if (const int64_t pb = matmul_part_bytes(dt, x.data, y.data, Y->data, p)) {
+        void *w = nullptr;
+        HIPCHECK(pool_alloc((size_t)pb, &w, nullptr, g.stream), "device allocation (temporary)");
+        temps.push_back(w);
+        p.part = (float *)w;
     }
     HIPCHECK(launch_matmul(dt, x.data, y.data, Y->data, p, g.stream), "MatMul");
     if (t_mm_epi && (p.bias || p.res || p.gelu)) t_mm_epi->applied = true;

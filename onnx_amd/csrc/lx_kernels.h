@@ -171,7 +171,16 @@ struct MatMulArgs {
     // then, when gelu != 0, the ONNX GELU subgraph Div(., sqrt 2) -> Erf -> Add 1 -> Mul . -> Mul 0.5 on
     // each result, every node rounded as it rounds (Float)
     int32_t gelu;
+    // Float products with few output tiles split K into equal ranges: each range's partial product goes to
+    // part ([split][batch][m][n] floats, matmul_part_bytes of them, supplied by the caller), then a second
+    // kernel sums the partials in range order and applies the epilogue.  Set by launch_matmul.
+    int32_t split;
+    float *part;
 };
+// Bytes of partial products launch_matmul needs in MatMulArgs::part for these operands (0: no split).  The
+// split depends on m, n and k, and on the batch only through batch <= kMatMulSplitBatch.
+constexpr int64_t kMatMulSplitBatch = 16;
+int64_t matmul_part_bytes(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p);
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);
 
 // Data movement (Transpose, Slice, Concat, expand): for every index j of `dims`

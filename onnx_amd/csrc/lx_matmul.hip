@@ -101,6 +101,64 @@ __device__ __forceinline__ void mm_epilogue(const v16f (&acc)[MT][NT], float *__
     }
 }
 
+// Store of a wave's raw accumulators (no epilogue) into the partial product P (a dense M x N matrix, N a multiple
+// of 4), in mm_epilogue's layout.
+template <int MT, int NT>
+__device__ __forceinline__ void mm_store_part(const v16f (&acc)[MT][NT], float *__restrict__ P, int M, int N, int r0,
+                                              int c0, int l) {
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const int row = r0 + 32 * i + (l % 32);
+        if (row >= M) continue;
+        float *Pr = P + (int64_t)row * N;
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int c = c0 + 32 * j + 8 * q + 4 * (l / 32);
+                if (c < N)
+                    *reinterpret_cast<v4f *>(Pr + c) =
+                        v4f{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+            }
+    }
+}
+
+// C = epilogue(P[0] + P[1] + ... + P[split - 1]) over the split partial products of a launch's batches, summed in
+// that order, then the bias, residual and GELU of mm_epilogue, each rounded as there: 16 bytes per lane.
+template <bool GELU>
+__global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C, MatMulArgs p) {
+    __shared__ ExpTable tab;
+    if constexpr (GELU) {
+        exp_table_fill(tab);
+        __syncthreads();
+    }
+    const int64_t mn = (int64_t)p.m * p.n, nq = mn / 4;
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= nq * p.batch) return;
+    const int64_t zb = i / nq, e = (i - zb * nq) * 4;  // batch of this launch, element of its matrix
+    const int64_t stride = p.batch * mn;                // between the partials of two K ranges
+    const float *P = p.part + zb * mn + e;
+    v4f v = *reinterpret_cast<const v4f *>(P);
+    for (int s = 1; s < p.split; s++) {
+        const v4f x = *reinterpret_cast<const v4f *>(P + s * stride);
+        v[0] = v[0] + x[0]; v[1] = v[1] + x[1]; v[2] = v[2] + x[2]; v[3] = v[3] + x[3];
+    }
+    const int64_t bz = p.batch_base + zb;
+    if (p.bias) {
+        const float4 bc = *reinterpret_cast<const float4 *>(p.bias + bz * p.bias_bstr + e % p.n);
+        v[0] = v[0] + bc.x; v[1] = v[1] + bc.y; v[2] = v[2] + bc.z; v[3] = v[3] + bc.w;
+    }
+    if (p.res) {
+        const float4 rc = *reinterpret_cast<const float4 *>(p.res + bz * mn + e);
+        v[0] = v[0] + rc.x; v[1] = v[1] + rc.y; v[2] = v[2] + rc.z; v[3] = v[3] + rc.w;
+    }
+    if constexpr (GELU) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = gelu_erf_lx(v[k], tab);
+    }
+    *reinterpret_cast<float4 *>(C + bz * mn + e) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
 // BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
 // = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered in LDS with k
 // as the outer index (A transposed to [k][m], B as [k][n]), so the lanes of a
@@ -278,7 +336,9 @@ __device__ __forceinline__ void wait_vmcnt_barrier() {
 #endif
 }
 
-template <int BM, int BN, int WM, int WN, int S, int WMIN, int WMAX, bool GELU>
+// SPLIT: block z = batch * p.split + r computes the partial product of the r-th of p.split equal K ranges (whole
+// passes of four steps) into p.part, without the epilogue (k_matmul_split_sum applies it).
+template <int BM, int BN, int WM, int WN, int S, int WMIN, int WMAX, bool GELU, bool SPLIT = false>
 __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WMIN, WMAX))) void k_matmul_f32_dl(const float *__restrict__ A, const float *__restrict__ B,
                                                                 float *__restrict__ C, MatMulArgs p) {
     constexpr int NW = WM * WN;
@@ -308,8 +368,12 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
     const int l = threadIdx.x & 63;
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
+    // the batch of this launch and, split, the K range: steps [k0, k0 + nk) of 16
+    const int zb = SPLIT ? (int)blockIdx.z / p.split : (int)blockIdx.z;
+    const int nk = SPLIT ? K / 16 / p.split : K / 16;
+    const int k0 = SPLIT ? ((int)blockIdx.z - zb * p.split) * nk * 16 : 0;
     int64_t ao, bo;
-    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
+    batch_offsets(p.batch_base + zb, p, &ao, &bo);
 
     // this wave's loads: a per-lane source address (advanced by `inc` floats per step) and an LDS offset
     const float *src[L];
@@ -320,13 +384,13 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
         const int i = min(w + NW * j, NL - 1);
         if (i < LA) {
             const int q = 64 * i + l, r = q >> 2, c = (q & 3) ^ dl_swz(r);
-            src[j] = A + ao + (int64_t)min(row0 + r, M - 1) * K + 4 * c;
+            src[j] = A + ao + (int64_t)min(row0 + r, M - 1) * K + k0 + 4 * c;
             inc[j] = 16;
             dst[j] = 1024 * i;
         } else {
             const int h = (i - LA) / LBH, wl = (i - LA) % LBH, q = 64 * wl + l;
             const int k = 8 * h + q / (BN / 4), c = col0 + 4 * (q % (BN / 4));
-            src[j] = B + bo + (int64_t)k * N + min(c, N - 4);
+            src[j] = B + bo + (int64_t)(k0 + k) * N + min(c, N - 4);
             inc[j] = 16 * (int64_t)N;
             dst[j] = A_BYTES + h * (B_HALF + 128) + 1024 * wl;
         }
@@ -358,7 +422,6 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    const int nk = K / 16;
     // Step t: wait for this wave's loads of step t + 1 (the S - 3 later steps' loads stay outstanding); barrier
     // (every wave's loads of step t + 1 are visible, and stage (t - 1) % S, read during step t - 2, is free);
     // issue step t + S - 1 into that stage; read step t + 1's fragments; run step t's MFMAs on the fragments read
@@ -429,7 +492,11 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
     }
     // the ring's last loads land before the wave can end (the block's LDS is then handed to another block)
     __builtin_amdgcn_s_waitcnt((7 << 4) | (15 << 8));
-    mm_epilogue<MT, NT, true, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
+    if constexpr (SPLIT)
+        mm_store_part<MT, NT>(acc, p.part + ((int64_t)(blockIdx.z - zb * p.split) * p.batch + zb) * M * N, M, N,
+                              row0 + wr, col0 + wc, l);
+    else
+        mm_epilogue<MT, NT, true, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
 }
 
 template <int BM, int BN, int WM, int WN, int WMIN, int WMAX>
@@ -438,6 +505,16 @@ static void launch_f32_dl(const float *a, const float *b, float *c, const MatMul
     const dim3 blk(WM * WN * 64);
     if (p.gelu) hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, 4, WMIN, WMAX, true>), g, blk, 0, s, a, b, c, p);
     else hipLaunchKernelGGL((k_matmul_f32_dl<BM, BN, WM, WN, 4, WMIN, WMAX, false>), g, blk, 0, s, a, b, c, p);
+}
+
+// Split K (p.split ranges, p.part holding the partials): 64x64 tiles, then the ordered sum with the epilogue.
+static void launch_f32_split(const float *a, const float *b, float *c, const MatMulArgs &p, hipStream_t s) {
+    dim3 g((p.n + 63) / 64, (p.m + 63) / 64, (unsigned)(p.batch * p.split));
+    hipLaunchKernelGGL((k_matmul_f32_dl<64, 64, 2, 2, 4, 3, 8, false, true>), g, dim3(256), 0, s, a, b, c, p);
+    const int64_t nq = (int64_t)p.m * p.n / 4 * p.batch;
+    const dim3 gs((unsigned)((nq + 255) / 256));
+    if (p.gelu) hipLaunchKernelGGL(k_matmul_split_sum<true>, gs, dim3(256), 0, s, c, p);
+    else hipLaunchKernelGGL(k_matmul_split_sum<false>, gs, dim3(256), 0, s, c, p);
 }
 
 template <int BM, int BN, int WM, int WN>
@@ -584,6 +661,39 @@ hipError_t launch_strided_copy(int esize, const void *x, void *y, int rank, cons
     return hipGetLastError();
 }
 
+// VEC: 16-byte loads of A and B and 16-byte epilogue accesses of C, the residual and the bias
+static bool f32_vec(const void *a, const void *b, const void *c, const MatMulArgs &p) {
+    bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) &&
+               (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)p.res | (uintptr_t)p.bias) % 16 == 0) &&
+               p.bias_bstr % 4 == 0;
+    for (int d = 0; d < p.nbatch; d++) vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
+    return vec;
+}
+
+// K ranges of a float product on the direct-load kernel's terms (16-byte operands, K a multiple of 64): with
+// T = ceil(m / 64) ceil(n / 64) tiles of 64x64 per batch matrix, the most ranges, each at least two passes of
+// 64, that divide K / 64 into equal parts and keep T times the ranges within 256 blocks (one per CU); 1 when
+// T alone reaches 128, when the batch exceeds kMatMulSplitBatch, or when K / 64 allows no such range.  A
+// product with few tiles otherwise leaves most CUs idle while its blocks each walk the whole of K ([8,1536] x
+// [1536,384]: 6 blocks).  The ranges depend on m, n and k only (and on the batch only through its bound), so a
+// product's bits are the same in any batch of at most kMatMulSplitBatch matrices, fused or not.
+static int f32_split(const MatMulArgs &p, bool vec) {
+    if (!vec || p.k % 64 != 0 || p.batch > kMatMulSplitBatch) return 1;
+    const int64_t tiles = (int64_t)((p.m + 63) / 64) * ((p.n + 63) / 64);
+    if (tiles >= 128) return 1;
+    const int steps = p.k / 64;
+    int best = 1;
+    for (int r = 2; r <= steps / 2; r++)
+        if (steps % r == 0 && tiles * r <= 256) best = r;
+    return best;
+}
+
+int64_t matmul_part_bytes(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p) {
+    if (dtype != kFloat || p.m == 0 || p.n == 0 || p.batch == 0) return 0;
+    const int r = f32_split(p, f32_vec(a, b, c, p));
+    return r > 1 ? (int64_t)r * p.batch * p.m * p.n * (int64_t)sizeof(float) : 0;
+}
+
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p0, hipStream_t s) {
     if (p0.m == 0 || p0.n == 0 || p0.batch == 0) return hipSuccess;
     // grid z holds at most 65535 batches: larger batch counts take several launches
@@ -599,17 +709,21 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
     }
     const MatMulArgs &p = p0;
     if (dtype == kFloat) {
-        // VEC: 16-byte loads of A and B and 16-byte epilogue accesses of C, the residual and the bias
-        bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) &&
-                   (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)p.res | (uintptr_t)p.bias) % 16 == 0) &&
-                   p.bias_bstr % 4 == 0;
-        for (int d = 0; d < p.nbatch; d++) vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
+        const bool vec = f32_vec(a, b, c, p);
+        const float *fa = (const float *)a, *fb = (const float *)b;
+        float *fc = (float *)c;
+        const int split = f32_split(p, vec);
+        if (split > 1) {
+            if (!p.part) return hipErrorInvalidValue;  // the caller sizes it with matmul_part_bytes
+            MatMulArgs q = p;
+            q.split = split;
+            launch_f32_split(fa, fb, fc, q, s);
+            return hipGetLastError();
+        }
         // block tile: among the tiles that give each of the 256 CUs two or more blocks (a lone block
         // per CU leaves its barrier and load latencies unhidden: measured 93 against 104 TF/s for
         // [4096,3072]x[3072,768]), the one whose busiest CU has the least work -- ceil(blocks / 256)
         // blocks, each costing its area over the tile's relative efficiency; 64x64 when none does
-        const float *fa = (const float *)a, *fb = (const float *)b;
-        float *fc = (float *)c;
         struct Tile {
             int bm, bn;
             double eff;

@@ -91,22 +91,76 @@ def test_float_direct_load_tiles(hip, sa, sb):
     check_float(rng.standard_normal(sa).astype(np.float32), rng.standard_normal(sb).astype(np.float32), 1e-5)
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 768, 768), (320, 192, 260),
+def split_of(m, k, n, batch=1):
+    """K ranges of a float product with 16-byte operands (lx_matmul.hip, f32_split): with T 64x64 tiles per
+    matrix, the most equal ranges of at least two 64-steps each dividing K / 64 with T times them within 256;
+    1 from T = 128 or past a batch of 16."""
+    if k % 64 or n % 4 or batch > 16:
+        return 1
+    tiles = -(-m // 64) * -(-n // 64)
+    if tiles >= 128:
+        return 1
+    steps, best = k // 64, 1
+    for r in range(2, steps // 2 + 1):
+        if steps % r == 0 and tiles * r <= 256:
+            best = r
+    return best
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 192, 768), (320, 192, 260),
                                    (512, 512, 32)])
 def test_float_kernels_sum_in_one_order(hip, m, k, n):
     """The direct-load kernel and the register-staged one add the products of a dot product in the same order,
     so a product is the same bits whichever kernel and tile runs it: the whole product (direct loads) against
     its 32-row blocks (fewer than 64 rows: the register-staged kernel) and its 64-column blocks (N = 64: another
-    tile of the direct-load kernel), bit for bit; N = 32 takes the 128x32 tile."""
+    tile of the direct-load kernel), bit for bit; N = 32 takes the 128x32 tile, and [512,512]x[512,32] and its
+    row blocks split K alike (four ranges)."""
     rng = np.random.default_rng(58)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)
     whole = mm(a, b)
+    assert all(split_of(r, k, n) == split_of(m, k, n) for r in (32, m % 32 or 32))
     rows = np.concatenate([mm(a[i:i + 32], b) for i in range(0, m, 32)])
     assert np.array_equal(whole.view(np.uint32), rows.view(np.uint32))
     if n >= 128:
+        assert split_of(m, k, 64) == split_of(m, k, n) == 1
         cols = np.concatenate([mm(a, np.ascontiguousarray(b[:, j:j + 64])) for j in range(0, n - n % 64, 64)], axis=1)
         assert np.array_equal(whole[:, :cols.shape[1]].view(np.uint32), cols.view(np.uint32))
+
+
+@pytest.mark.parametrize("sa,sb", [((8, 384), (384, 384)), ((8, 1536), (1536, 384)), ((8, 384), (384, 1536)),
+                                   ((1, 1536), (1536, 384)), ((63, 512), (512, 100)), ((512, 768), (768, 768)),
+                                   ((4, 8, 384), (4, 384, 384)), ((3, 1, 80, 1024), (1, 2, 1024, 36)),
+                                   ((200, 4096), (4096, 4))])
+def test_float_split_k_sums_its_ranges_in_order(hip, sa, sb):
+    """Products with few output tiles split K into equal ranges, one partial product each, then add the partials
+    in range order: the split product is, bit for bit, the float32 sum in that order of the unsplit products of
+    its ranges (run whole by either kernel: fewer than 64 rows take the register-staged one; a range product
+    that would split as a product of its own runs with its rows repeated until it has 128 tiles, which leaves
+    each row's bits as they are), and within the MatMul bar of the oracle.  Rows of 8 tokens (the reference's
+    short-text embeddings), M = 1, ragged M and N, a batch per operand, broadcast batches, N = 4, ranges that
+    would split again."""
+    rng = np.random.default_rng(59)
+    a = rng.standard_normal(sa).astype(np.float32)
+    b = rng.standard_normal(sb).astype(np.float32)
+    m, k, n = sa[-2], sa[-1], sb[-1]
+    batch = int(np.prod(np.broadcast_shapes(sa[:-2], sb[:-2])))
+    r = split_of(m, k, n, batch)
+    assert r > 1
+
+    def unsplit(a, b):
+        rep = 1
+        while split_of(m * rep, a.shape[-1], n, batch) > 1:
+            rep *= 2
+        return mm(np.ascontiguousarray(np.concatenate([a] * rep, axis=-2)), b)[..., :m, :]
+
+    kr, ref = k // r, None
+    for i in range(r):
+        part = unsplit(a[..., i * kr:(i + 1) * kr], np.ascontiguousarray(b[..., i * kr:(i + 1) * kr, :]))
+        ref = part if ref is None else (ref + part).astype(np.float32)
+    whole = mm(a, b)
+    assert whole.shape == ref.shape and np.array_equal(whole.view(np.uint32), ref.view(np.uint32))
+    check_float(a, b, 1e-5)
 
 
 @pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 70, 33), (33, 65)), ((2, 1, 40, 17), (3, 17, 66))])
@@ -167,6 +221,9 @@ def _nodes(a, b, bias, res):
     ((256, 768), (768, 768), (768,), None), ((4, 64, 768), (768, 256), (256,), (4, 64, 256)),
     ((4000, 192), (192, 740), (740,), (4000, 740)), ((2000, 192), (192, 2020), (2020,), None),
     ((2, 3, 33, 40), (40, 70), (1, 70), (2, 3, 33, 70)), ((128, 64), (64, 96), (96,), (128, 96)),
+    # split K (few output tiles): the epilogue after the ordered sum of the partials
+    ((8, 384), (384, 384), (384,), (8, 384)), ((1, 8, 1536), (1536, 384), (384,), (1, 8, 384)),
+    ((1, 96, 512), (3, 512, 80), (3, 1, 80), None),
     # shapes the epilogue does not take: the MatMul and the Adds one after the other
     ((64, 32), (32, 48), (64, 48), None), ((64, 32), (32, 48), (48,), (48,)), ((5, 32), (32, 48), (3, 1, 48), None)])
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
@@ -208,22 +265,24 @@ def test_matmul_add_bias_row_per_batch_equals_the_nodes(hip):
         assert got.shape == ref.shape and np.array_equal(got.view(np.uint32), ref.view(np.uint32)), bshape
 
 
-def test_grouped_projections_equal_the_separate_ones(hip):
+@pytest.mark.parametrize("xs,n", [((2, 40, 96), 64), ((1, 8, 384), 384)])
+def test_grouped_projections_equal_the_separate_ones(hip, xs, n):
     """Three MatMul -> Add bias projections of one input become one MatMulAddGroup node (one batched launch,
     outputs as slices of one product); every output equals the unfused graph's bit for bit, including
-    through a consumer that reads a slice (Reshape / Transpose of the middle one)."""
+    through a consumer that reads a slice (Reshape / Transpose of the middle one).  Eight tokens of hidden 384
+    split K (three ranges) in the grouped launch and in each separate one alike."""
     import onnx_writer as W
     from onnx_amd.graph import Model
     rng = np.random.default_rng(91)
-    x = rng.standard_normal((2, 40, 96)).astype(np.float32)
+    x = rng.standard_normal(xs).astype(np.float32)
     inits = []
     nodes = []
     for t in "qkv":
-        inits += [(f"w{t}", (rng.standard_normal((96, 64)) * 0.1).astype(np.float32)),
-                  (f"b{t}", rng.standard_normal(64).astype(np.float32))]
+        inits += [(f"w{t}", (rng.standard_normal((xs[-1], n)) * 0.1).astype(np.float32)),
+                  (f"b{t}", rng.standard_normal(n).astype(np.float32))]
         nodes += [W.node("MatMul", ["x", f"w{t}"], [f"{t}0"], f"{t}_proj"),
                   W.node("Add", [f"{t}0", f"b{t}"], [f"{t}"], f"{t}_bias")]
-    inits.append(("shape", np.array([2, 40, 4, 16], np.int64)))
+    inits.append(("shape", np.array([xs[0], xs[1], 4, n // 4], np.int64)))
     nodes += [W.node("Reshape", ["k", "shape"], ["kr"], "k_heads"),
               W.node("Transpose", ["kr"], ["kt"], "k_perm", perm=[0, 2, 3, 1])]
     outs = ["q", "kt", "v"]
@@ -305,6 +364,7 @@ def _gelu_nodes(t):
                                          ((2000, 192), (192, 2020), (2020,)), ((4096, 768), (768, 768), (768,)),
                                          ((4096, 768), (768, 2304), (2304,)), ((2048, 256), (256, 4096), (4096,)),
                                          ((98304, 128), (128, 64), (64,)),
+                                         ((8, 384), (384, 1536), (1536,)), ((10, 8, 384), (384, 1536), (1536,)),
                                          ((127, 65), (65, 129), (129,)), ((3, 33, 40), (3, 40, 70), (3, 1, 70)),
                                          ((64, 32), (32, 48), (64, 48))])
 @pytest.mark.parametrize("dt", [np.float32, np.float64])
