@@ -769,6 +769,26 @@ def bench_extras(torch, HIP, DeviceTensor, set_stream, steps, warmup, W):
         res.append(d)
         ge.close()
     del edev
+    # the same encoder at the batch sizes of the reference's me5s run benchmarks (Benchmarks.cs:370-423: 1, 10
+    # and 50 strings of 20 characters, 1 and 10 of 200), as b sequences of s tokens, s = 8 and 64 standing for
+    # those strings (their exact token counts depend on the tokenizer), one captured execution each
+    for b, sq in ((1, 8), (10, 8), (50, 8), (1, 64), (10, 64)):
+        model, sins, _, _ = encoder_model(b, sq, seed=5)
+        sdev = {k: DeviceTensor.from_numpy(v) for k, v in sins.items()}
+        ge = Model.Load(model)
+        ge.Fuse()
+        assert ge.Capture(sdev), ge.LastError
+
+        def small_step(i, ge=ge):
+            if not ge.Replay():
+                raise RuntimeError(ge.LastError)
+        ms = wall_time(torch, small_step, max(16, steps // 4), max(2, warmup // 4))
+        d = {"op": f"me5s-shaped encoder [{b},{sq}] tokens, fused, captured (per execution)",
+             "us": round(ms * 1e3, 1), "tokens_per_s": round(b * sq / (ms * 1e-3), 1)}
+        log(json.dumps(d))
+        res.append(d)
+        ge.close()
+        del sdev
 
     # MatMul (row f2): fp32 MFMA, compute-bound; BERT-base shapes at batch 8 x 512 tokens
     for name, sa, sb in (("MatMul fp32 [4096,768]x[768,768] (dense)", (4096, 768), (768, 768)),
@@ -777,7 +797,12 @@ def bench_extras(torch, HIP, DeviceTensor, set_stream, steps, warmup, W):
                          ("MatMul fp32 [4096,3072]x[3072,768] (FFN out)", (4096, 3072), (3072, 768)),
                          ("MatMul fp32 [16,12,512,64]x[16,12,64,512] (attention scores)", (16, 12, 512, 64),
                           (16, 12, 64, 512)),
-                         ("MatMul fp32 [4096,4096]x[4096,4096]", (4096, 4096), (4096, 4096))):
+                         ("MatMul fp32 [4096,4096]x[4096,4096]", (4096, 4096), (4096, 4096)),
+                         # the shapes of the reference's TensorMatMulBenchmarks (Benchmarks.cs:90-160)
+                         ("MatMul fp32 [384,384]x[384,384]", (384, 384), (384, 384)),
+                         ("MatMul fp32 [384,1536]x[1536,384]", (384, 1536), (1536, 384)),
+                         ("MatMul fp32 [6,384,384]x[6,384,384]", (6, 384, 384), (6, 384, 384)),
+                         ("MatMul fp32 [3,4,384,384]x[3,4,384,384]", (3, 4, 384, 384), (3, 4, 384, 384))):
         Am = torch.randn(*sa, device=dev, generator=gen)
         Bm = torch.randn(*sb, device=dev, generator=gen)
         Cm = torch.empty(*(sa[:-1] + sb[-1:]), device=dev)

@@ -1698,6 +1698,7 @@ struct MatMulEpilogue {
     bool applied = false;
 };
 thread_local MatMulEpilogue *t_mm_epi = nullptr;
+thread_local bool t_mm_per_matrix = false;  // api_matmul_add_grouped in progress
 
 bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dims, int64_t *bias_bstr) {
     if (out_rank < 2) return false;
@@ -1738,6 +1739,7 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
         p.res = t_mm_epi->res ? (const float *)t_mm_epi->res->data : nullptr;
         p.gelu = t_mm_epi->gelu ? 1 : 0;
     }
+    p.split_per_matrix = t_mm_per_matrix ? 1 : 0;
     p.m = (int32_t)x.dims[x.rank - 2];
     p.k = (int32_t)x.dims[x.rank - 1];
     p.n = (int32_t)y.dims[y.rank - 1];
@@ -1912,6 +1914,16 @@ extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_ten
     OpScope prof("MatMulAdd");
     return matmul_add_run(A, B, bias, residual, false, Y);
 }
+
+namespace lx {
+int api_matmul_add_grouped(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, lx_tensor *Y) {
+    if (!W || W->rank != 3 || W->dims[0] > kMatMulSplitBatch) return LX_ERR_NOT_SUPPORTED;
+    t_mm_per_matrix = true;
+    const int st = lx_MatMulAdd(A, W, bias, nullptr, Y);
+    t_mm_per_matrix = false;
+    return st;
+}
+}  // namespace lx
 
 extern "C" int lx_MatMulAddGelu(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, lx_tensor *Y) {
     OpScope prof("MatMulAddGelu");

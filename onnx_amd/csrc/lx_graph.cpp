@@ -736,7 +736,7 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         a3.dims[1] = M;
         a3.dims[2] = K;
         lx_tensor y{};
-        if ((st = lx_MatMulAdd(&a3, &wv->t, &bv->t, nullptr, &y))) {
+        if ((st = api_matmul_add_grouped(&a3, &wv->t, &bv->t, &y))) {
             lx_tensor_free(&y);
             return run_unfused(X, n, outs);
         }

@@ -56,4 +56,9 @@ int api_check_status(const DeferredCheck &rec, const ErrFlags &flags);  // sets 
 // nodes' broadcast.
 bool api_layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X);
 
+// lx_MatMulAdd of one left operand [1, M, K] against G stacked weights [G, K, N] and biases [G, 1, N] (the
+// graph's grouped projections): each of the G products splits its K exactly as a product of its own, so each
+// slice is bit-identical to that product.  LX_ERR_NOT_SUPPORTED (no message) for G above 16.
+int api_matmul_add_grouped(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, lx_tensor *Y);
+
 }  // namespace lx

@@ -173,12 +173,15 @@ struct MatMulArgs {
     int32_t gelu;
     // Float products with few output tiles split K into equal ranges: each range's partial product goes to
     // part ([split][batch][m][n] floats, matmul_part_bytes of them, supplied by the caller), then a second
-    // kernel sums the partials in range order and applies the epilogue.  Set by launch_matmul.
+    // kernel sums the partials in range order and applies the epilogue.  split is set by launch_matmul.
     int32_t split;
+    // 1: the split counts the tiles of one matrix, not of the whole batch, so that each matrix of the launch
+    // splits as it would alone (grouped projections, at most kMatMulSplitBatch of them; larger batches then
+    // do not split)
+    int32_t split_per_matrix;
     float *part;
 };
-// Bytes of partial products launch_matmul needs in MatMulArgs::part for these operands (0: no split).  The
-// split depends on m, n and k, and on the batch only through batch <= kMatMulSplitBatch.
+// Bytes of partial products launch_matmul needs in MatMulArgs::part for these operands (0: no split).
 constexpr int64_t kMatMulSplitBatch = 16;
 int64_t matmul_part_bytes(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p);
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);

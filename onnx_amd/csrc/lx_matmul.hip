@@ -671,15 +671,17 @@ static bool f32_vec(const void *a, const void *b, const void *c, const MatMulArg
 }
 
 // K ranges of a float product on the direct-load kernel's terms (16-byte operands, K a multiple of 64): with
-// T = ceil(m / 64) ceil(n / 64) tiles of 64x64 per batch matrix, the most ranges, each at least two passes of
-// 64, that divide K / 64 into equal parts and keep T times the ranges within 256 blocks (one per CU); 1 when
-// T alone reaches 128, when the batch exceeds kMatMulSplitBatch, or when K / 64 allows no such range.  A
-// product with few tiles otherwise leaves most CUs idle while its blocks each walk the whole of K ([8,1536] x
-// [1536,384]: 6 blocks).  The ranges depend on m, n and k only (and on the batch only through its bound), so a
-// product's bits are the same in any batch of at most kMatMulSplitBatch matrices, fused or not.
+// T tiles of 64x64 over the batch (ceil(m / 64) ceil(n / 64) per matrix), the most ranges, each at least two
+// passes of 64, that divide K / 64 into equal parts and keep T times the ranges within 256 blocks (one per
+// CU); 1 when T alone reaches 128 or K / 64 allows no such range.  A product of few tiles otherwise leaves
+// most CUs idle while its blocks each walk the whole of K ([8,1536] x [1536,384]: 6 blocks).  With
+// split_per_matrix, T counts one matrix's tiles (and a batch above kMatMulSplitBatch does not split), so
+// that each matrix of a grouped launch splits as it does alone.
 static int f32_split(const MatMulArgs &p, bool vec) {
-    if (!vec || p.k % 64 != 0 || p.batch > kMatMulSplitBatch) return 1;
-    const int64_t tiles = (int64_t)((p.m + 63) / 64) * ((p.n + 63) / 64);
+    if (!vec || p.k % 64 != 0) return 1;
+    const int64_t per = (int64_t)((p.m + 63) / 64) * ((p.n + 63) / 64);
+    if (p.split_per_matrix && p.batch > kMatMulSplitBatch) return 1;
+    const int64_t tiles = p.split_per_matrix ? per : per * p.batch;
     if (tiles >= 128) return 1;
     const int steps = p.k / 64;
     int best = 1;

@@ -92,12 +92,12 @@ def test_float_direct_load_tiles(hip, sa, sb):
 
 
 def split_of(m, k, n, batch=1):
-    """K ranges of a float product with 16-byte operands (lx_matmul.hip, f32_split): with T 64x64 tiles per
-    matrix, the most equal ranges of at least two 64-steps each dividing K / 64 with T times them within 256;
-    1 from T = 128 or past a batch of 16."""
-    if k % 64 or n % 4 or batch > 16:
+    """K ranges of a float product with 16-byte operands (lx_matmul.hip, f32_split): with T 64x64 tiles over
+    the batch, the most equal ranges of at least two 64-steps each dividing K / 64 with T times them within
+    256; 1 from T = 128."""
+    if k % 64 or n % 4:
         return 1
-    tiles = -(-m // 64) * -(-n // 64)
+    tiles = -(-m // 64) * -(-n // 64) * batch
     if tiles >= 128:
         return 1
     steps, best = k // 64, 1
@@ -265,27 +265,30 @@ def test_matmul_add_bias_row_per_batch_equals_the_nodes(hip):
         assert got.shape == ref.shape and np.array_equal(got.view(np.uint32), ref.view(np.uint32)), bshape
 
 
-@pytest.mark.parametrize("xs,n", [((2, 40, 96), 64), ((1, 8, 384), 384)])
-def test_grouped_projections_equal_the_separate_ones(hip, xs, n):
-    """Three MatMul -> Add bias projections of one input become one MatMulAddGroup node (one batched launch,
+@pytest.mark.parametrize("xs,n,g", [((2, 40, 96), 64, 3), ((1, 8, 384), 384, 3), ((1, 8, 1536), 1536, 3),
+                                    ((1, 8, 384), 64, 17)])
+def test_grouped_projections_equal_the_separate_ones(hip, xs, n, g):
+    """g MatMul -> Add bias projections of one input become one MatMulAddGroup node (one batched launch,
     outputs as slices of one product); every output equals the unfused graph's bit for bit, including
-    through a consumer that reads a slice (Reshape / Transpose of the middle one).  Eight tokens of hidden 384
-    split K (three ranges) in the grouped launch and in each separate one alike."""
+    through a consumer that reads a slice (Reshape / Transpose of the second one).  Eight tokens split K in
+    the grouped launch as in each separate product: three ranges at hidden 384, eight at 1536 (where the
+    group's three matrices together would take three); a group of 17 runs its products one by one."""
     import onnx_writer as W
     from onnx_amd.graph import Model
     rng = np.random.default_rng(91)
     x = rng.standard_normal(xs).astype(np.float32)
     inits = []
     nodes = []
-    for t in "qkv":
+    names = [f"p{i}" for i in range(g)]
+    for t in names:
         inits += [(f"w{t}", (rng.standard_normal((xs[-1], n)) * 0.1).astype(np.float32)),
                   (f"b{t}", rng.standard_normal(n).astype(np.float32))]
-        nodes += [W.node("MatMul", ["x", f"w{t}"], [f"{t}0"], f"{t}_proj"),
-                  W.node("Add", [f"{t}0", f"b{t}"], [f"{t}"], f"{t}_bias")]
+        nodes += [W.node("MatMul", ["x", f"w{t}"], [f"{t}_mm"], f"{t}_proj"),
+                  W.node("Add", [f"{t}_mm", f"b{t}"], [f"{t}"], f"{t}_bias")]
     inits.append(("shape", np.array([xs[0], xs[1], 4, n // 4], np.int64)))
-    nodes += [W.node("Reshape", ["k", "shape"], ["kr"], "k_heads"),
+    nodes += [W.node("Reshape", ["p1", "shape"], ["kr"], "k_heads"),
               W.node("Transpose", ["kr"], ["kt"], "k_perm", perm=[0, 2, 3, 1])]
-    outs = ["q", "kt", "v"]
+    outs = [names[0], "kt"] + names[2:]
     res = {}
     for fuse in (False, True):
         g = Model.Load(W.model(nodes, [("x", np.float32, x.shape)], [(o, np.float32, ()) for o in outs], inits))
