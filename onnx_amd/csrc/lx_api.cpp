@@ -1755,14 +1755,15 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     if (x.dims[x.rank - 2] > INT32_MAX || x.dims[x.rank - 1] > INT32_MAX || y.dims[y.rank - 1] > INT32_MAX)
         return set_err(LX_ERR_NOT_SUPPORTED, "Matrix dimensions beyond 2^31 are not supported.");
     // One right matrix for every batch and the left matrices stored row after row ([B, S, H] x [H, N]): one
-    // [batch * m, k] x [k, n] product, the same rows with the same sums, in one grid of row tiles
+    // [batch * m, k] x [k, n] product, the same rows with the same sums, in one grid of row tiles (at most
+    // 65535 of the smallest, 64 rows: a larger product keeps its batch in the grid's third dimension)
     bool fold = p.nbatch > 0 && bias_bstr == 0;
     int64_t rows = x.dims[x.rank - 2];
     for (int d = p.nbatch - 1; fold && d >= 0; d--) {
         if (p.bdims[d] != 1) fold = p.b_bstr[d] == 0 && p.a_bstr[d] == rows * p.k;
         rows *= p.bdims[d];
     }
-    if (fold && rows <= INT32_MAX) {
+    if (fold && rows <= 65535LL * 64) {
         p.m = (int32_t)rows;
         p.nbatch = 0;
         p.batch = 1;

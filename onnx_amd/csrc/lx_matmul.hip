@@ -679,7 +679,7 @@ static bool f32_vec(const void *a, const void *b, const void *c, const MatMulArg
 // that each matrix of a grouped launch splits as it does alone.
 static int f32_split(const MatMulArgs &p, bool vec) {
     if (!vec || p.k % 64 != 0) return 1;
-    const int64_t per = (int64_t)((p.m + 63) / 64) * ((p.n + 63) / 64);
+    const int64_t per = (((int64_t)p.m + 63) / 64) * (((int64_t)p.n + 63) / 64);
     if (p.split_per_matrix && p.batch > kMatMulSplitBatch) return 1;
     const int64_t tiles = p.split_per_matrix ? per : per * p.batch;
     if (tiles >= 128) return 1;

@@ -163,6 +163,18 @@ def test_float_split_k_sums_its_ranges_in_order(hip, sa, sb):
     check_float(a, b, 1e-5)
 
 
+@pytest.mark.parametrize("batch", [524280, 524288])
+def test_batch_fold_at_the_grid_limit(hip, batch):
+    """A batch of left matrices over one right matrix runs as one product of batch * m rows while its 64-row
+    tiles fit the grid (524280 x 8 rows: exactly 65535 tiles); one more row tile's worth keeps the batch
+    (524288 matrices, in launches of 65535).  Integer values: every sum exact."""
+    rng = np.random.default_rng(92)
+    a = rng.integers(-8, 8, (batch, 8, 4)).astype(np.float32)
+    b = rng.integers(-8, 8, (4, 4)).astype(np.float32)
+    got = mm(a, b)
+    assert got.shape == (batch, 8, 4) and np.array_equal(got, a @ b)
+
+
 @pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 70, 33), (33, 65)), ((2, 1, 40, 17), (3, 17, 66))])
 def test_double(hip, sa, sb):
     rng = np.random.default_rng(52)
