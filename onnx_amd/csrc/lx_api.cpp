@@ -1672,7 +1672,8 @@ const char *net_type(int dt) {
 // the operand is copied to a dense pooled block first
 int densify(int dt, MView *v, std::vector<void *> &temps) {
     const int r = v->rank;
-    if ((v->dims[r - 1] == 1 || v->str[r - 1] == 1) && (v->dims[r - 2] == 1 || v->str[r - 2] == v->dims[r - 1]))
+    // unit column stride and rows that do not overlap (dense, or the rows of a transposed view): as they are
+    if ((v->dims[r - 1] == 1 || v->str[r - 1] == 1) && (v->dims[r - 2] == 1 || v->str[r - 2] >= v->dims[r - 1]))
         return LX_OK;
     int64_t n = 1;
     for (int d = 0; d < r; d++) n *= v->dims[d];
@@ -1699,6 +1700,17 @@ struct MatMulEpilogue {
 };
 thread_local MatMulEpilogue *t_mm_epi = nullptr;
 thread_local bool t_mm_per_matrix = false;  // api_matmul_add_grouped in progress
+thread_local const int *t_mm_yperm = nullptr;  // api_matmul_permuted in progress: the product's permutation
+
+// a permutation of 0 .. rank - 1 that keeps the last axis last
+bool last_axis_perm(const int *perm, int rank) {
+    bool seen[LX_MAX_RANK] = {false};
+    for (int i = 0; i < rank; i++) {
+        if (perm[i] < 0 || perm[i] >= rank || seen[perm[i]]) return false;
+        seen[perm[i]] = true;
+    }
+    return rank >= 1 && perm[rank - 1] == rank - 1;
+}
 
 bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dims, int64_t *bias_bstr) {
     if (out_rank < 2) return false;
@@ -1729,11 +1741,31 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
                std::vector<void *> &temps) {
     int st;
     if ((st = densify(dt, &x, temps)) || (st = densify(dt, &y, temps))) return st;
-    if ((st = prepare_output(Y, dt, out_rank, out_dims))) return st;
+    // the product's element strides in Y: dense, or Y = transpose(product, t_mm_yperm)
+    int64_t pstr[LX_MAX_RANK];
+    const int *yp = t_mm_yperm;
+    if (yp) {
+        if (out_rank < 2 || !last_axis_perm(yp, out_rank)) return LX_ERR_NOT_SUPPORTED;
+        int64_t yd[LX_MAX_RANK];
+        for (int i = 0; i < out_rank; i++) yd[i] = out_dims[yp[i]];
+        if ((st = prepare_output(Y, dt, out_rank, yd))) return st;
+        int64_t s = 1;
+        for (int i = out_rank - 1; i >= 0; i--) {
+            pstr[yp[i]] = s;
+            s *= yd[i];
+        }
+    } else {
+        if ((st = prepare_output(Y, dt, out_rank, out_dims))) return st;
+        int64_t s = 1;
+        for (int i = out_rank - 1; i >= 0; i--) {
+            pstr[i] = s;
+            s *= out_dims[i];
+        }
+    }
     MatMulArgs p;
     memset(&p, 0, sizeof p);
     int64_t bias_bstr = 0;
-    if (t_mm_epi && dt == LX_FLOAT && epilogue_fits(*t_mm_epi, out_rank, out_dims, &bias_bstr)) {
+    if (t_mm_epi && !yp && dt == LX_FLOAT && epilogue_fits(*t_mm_epi, out_rank, out_dims, &bias_bstr)) {
         p.bias = t_mm_epi->bias ? (const float *)t_mm_epi->bias->data : nullptr;
         p.bias_bstr = bias_bstr;
         p.res = t_mm_epi->res ? (const float *)t_mm_epi->res->data : nullptr;
@@ -1749,15 +1781,21 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
         p.bdims[d] = x.dims[d];
         p.a_bstr[d] = x.str[d];
         p.b_bstr[d] = y.str[d];
+        // a single matrix along an axis: its stride is never used (dense value, so the 16-byte tests agree)
+        p.c_bstr[d] = out_dims[d] == 1 ? 0 : pstr[d];
         p.batch *= x.dims[d];
     }
+    // row strides; a single row's is never used (the dense value)
+    p.lda = x.dims[x.rank - 2] == 1 ? x.dims[x.rank - 1] : x.str[x.rank - 2];
+    p.ldb = y.dims[y.rank - 2] == 1 ? y.dims[y.rank - 1] : y.str[y.rank - 2];
+    p.ldc = (out_rank < 2 || p.m == 1) ? p.n : pstr[out_rank - 2];  // out_rank 1: the [1] of two vectors
     if (p.nbatch > kMaxOuter) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d batch axes are supported.", kMaxOuter);
     if (x.dims[x.rank - 2] > INT32_MAX || x.dims[x.rank - 1] > INT32_MAX || y.dims[y.rank - 1] > INT32_MAX)
         return set_err(LX_ERR_NOT_SUPPORTED, "Matrix dimensions beyond 2^31 are not supported.");
     // One right matrix for every batch and the left matrices stored row after row ([B, S, H] x [H, N]): one
     // [batch * m, k] x [k, n] product, the same rows with the same sums, in one grid of row tiles (at most
     // 65535 of the smallest, 64 rows: a larger product keeps its batch in the grid's third dimension)
-    bool fold = p.nbatch > 0 && bias_bstr == 0;
+    bool fold = p.nbatch > 0 && bias_bstr == 0 && !yp && p.lda == p.k;
     int64_t rows = x.dims[x.rank - 2];
     for (int d = p.nbatch - 1; fold && d >= 0; d--) {
         if (p.bdims[d] != 1) fold = p.b_bstr[d] == 0 && p.a_bstr[d] == rows * p.k;
@@ -1858,6 +1896,33 @@ extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
     for (void *t : temps) (void)pool_release(t);
     return st;
 }
+
+namespace lx {
+int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *B, const int *b_perm,
+                        const int *y_perm, lx_tensor *Y) {
+    if (!api_initialized() || !A || !B || A->dtype != LX_FLOAT || B->dtype != LX_FLOAT || A->rank < 2 || B->rank < 2 ||
+        check_tensor(A, "A") || check_tensor(B, "B"))
+        return LX_ERR_NOT_SUPPORTED;
+    MView x = dense_view(A), y = dense_view(B);
+    auto permute = [](MView &v, const int *perm) {
+        if (!perm) return true;
+        if (!last_axis_perm(perm, v.rank)) return false;
+        const MView o = v;
+        for (int i = 0; i < v.rank; i++) {
+            v.dims[i] = o.dims[perm[i]];
+            v.str[i] = o.str[perm[i]];
+        }
+        return true;
+    };
+    if (!permute(x, a_perm) || !permute(y, b_perm)) return LX_ERR_NOT_SUPPORTED;
+    std::vector<void *> temps;
+    t_mm_yperm = y_perm;
+    const int st = matmul_views(LX_FLOAT, x, y, Y, temps);
+    t_mm_yperm = nullptr;
+    for (void *t : temps) (void)pool_release(t);
+    return st;
+}
+}  // namespace lx
 
 // MatMul -> Add bias [-> Add residual] [-> the GELU subgraph]: in the MatMul's epilogue when the shapes fit
 // (Float), else the MatMul and then each node's operator, into new tensors (an Add may broadcast to a larger

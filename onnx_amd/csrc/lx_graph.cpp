@@ -718,6 +718,32 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!same) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
     }
+    if (op == "MatMulPermuted") {
+        Value *av, *bv;
+        if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &bv))) return st;
+        // each permutation as long as its tensor's rank (the output's: the larger operand rank), else the nodes
+        int perm[3][LX_MAX_RANK];
+        const int *use[3] = {nullptr, nullptr, nullptr};
+        static const char *names[3] = {"a_perm", "b_perm", "y_perm"};
+        bool fits = av && bv;
+        for (int k = 0; fits && k < 3; k++) {
+            auto it = n.attrs.find(names[k]);
+            if (it == n.attrs.end()) continue;
+            const int rank = k == 0 ? av->t.rank : k == 1 ? bv->t.rank : std::max(av->t.rank, bv->t.rank);
+            fits = it->second.ints.size() == (size_t)rank;
+            for (int d = 0; fits && d < rank; d++) perm[k][d] = (int)it->second.ints[d];
+            use[k] = perm[k];
+        }
+        if (fits) {
+            lx_tensor y{};
+            if (api_matmul_permuted(&av->t, use[0], &bv->t, use[1], use[2], &y) == LX_OK) {
+                outs.push_back(value_from_output(y));
+                return LX_OK;
+            }
+            lx_tensor_free(&y);
+        }
+        return run_unfused(X, n, outs);
+    }
     if (op == "MatMulAddGroup") {
         Value *av, *wv, *bv;
         if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &wv)) || (st = X.input(n, 2, &bv))) return st;
@@ -1024,6 +1050,49 @@ struct Fuser {
         return true;
     }
 
+    // a Transpose whose perm keeps the last axis last
+    bool keeps_last(int i) const {
+        if (!is(i, "Transpose", 1)) return false;
+        auto it = N(i).attrs.find("perm");
+        if (it == N(i).attrs.end() || it->second.kind != kAttrInts) return false;
+        const std::vector<int64_t> &pm = it->second.ints;
+        return !pm.empty() && pm.size() <= LX_MAX_RANK && pm.back() == (int64_t)pm.size() - 1;
+    }
+    // the unfused node that produces `name`, or -1
+    int producer(const std::string &name) const {
+        for (int k = 0; k < (int)g->nodes.size(); k++)
+            if (!used[k] && N(k).out.size() == 1 && N(k).out[0] == name) return k;
+        return -1;
+    }
+    // Transpose -> MatMul input and MatMul -> Transpose, each Transpose keeping the last axis last and its
+    // tensor read only by the MatMul: the MatMul reads and writes the transposed views through their strides
+    // (an attention layer's Q, V and context heads)
+    bool matmul_permuted(int i0, GNode *f, std::vector<int> *nodes) {
+        if (!is(i0, "MatMul", 2)) return false;
+        const GNode &m = N(i0);
+        std::vector<int> ns = {i0};
+        f->in = m.in;
+        f->out = m.out;
+        static const char *names[2] = {"a_perm", "b_perm"};
+        for (int side = 0; side < 2 && m.in[0] != m.in[1]; side++) {
+            const int t = producer(m.in[side]);
+            if (t < 0 || !keeps_last(t) || only_consumer(m.in[side]) != i0) continue;
+            f->in[side] = N(t).in[0];
+            f->attrs[names[side]] = N(t).attrs.at("perm");
+            ns.push_back(t);
+        }
+        const int c = only_consumer(m.out[0]);
+        if (keeps_last(c)) {
+            f->out = N(c).out;
+            f->attrs["y_perm"] = N(c).attrs.at("perm");
+            ns.push_back(c);
+        }
+        if (ns.size() == 1) return false;
+        f->op = "MatMulPermuted";
+        *nodes = ns;
+        return true;
+    }
+
     // Add(S, mask) -> Softmax, and Div(S, c) / Mul(S, c) -> Add(., mask) -> Softmax for a Float scalar
     // constant c (the scaled attention scores)
     bool add_softmax(int i0, GNode *f, std::vector<int> *nodes) {
@@ -1153,7 +1222,7 @@ struct Fuser {
             GNode f;
             std::vector<int> nodes;
             if (layernorm(i, &f, &nodes) || gelu(i, &f, &nodes) || add_softmax(i, &f, &nodes) ||
-                matmul_add(i, &f, &nodes))
+                matmul_add(i, &f, &nodes) || matmul_permuted(i, &f, &nodes))
                 place(f, nodes);
         }
         for (int i = 0; i < (int)g->nodes.size(); i++) {

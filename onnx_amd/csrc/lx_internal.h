@@ -61,4 +61,11 @@ bool api_layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X);
 // slice is bit-identical to that product.  LX_ERR_NOT_SUPPORTED (no message) for G above 16.
 int api_matmul_add_grouped(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, lx_tensor *Y);
 
+// MatMul of transpose(A, a_perm) and transpose(B, b_perm) (null: the tensor itself), its product stored as
+// transpose(product, y_perm) into Y (null: as it is), Float, each permutation keeping the last axis last: the
+// kernels read and write the transposed views through their strides, and the result is bit for bit the
+// Transpose nodes' and MatMul's.  LX_ERR_NOT_SUPPORTED (no message) for operands it does not take.
+int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *B, const int *b_perm,
+                        const int *y_perm, lx_tensor *Y);
+
 }  // namespace lx

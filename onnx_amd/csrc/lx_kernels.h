@@ -152,9 +152,9 @@ hipError_t launch_layernorm(const float *x, const float *gamma, const float *bet
                             int64_t rows, int64_t r, hipStream_t s);
 bool layernorm_supported(int64_t r);
 
-// MatMul C[batch][m][n] = A[batch][m][k] * B[batch][k][n], row-major matrices;
-// batch index decomposed over bdims (outermost first) with per-operand element
-// strides (0 on broadcast axes); C is dense.
+// MatMul C[batch][m][n] = A[batch][m][k] * B[batch][k][n], matrices with unit column stride and row strides
+// lda / ldb / ldc; batch index decomposed over bdims (outermost first) with per-operand element strides
+// (0 on broadcast axes for A and B).
 struct MatMulArgs {
     int32_t m, n, k;
     int32_t nbatch;
@@ -163,6 +163,10 @@ struct MatMulArgs {
     int64_t bdims[kMaxOuter];
     int64_t a_bstr[kMaxOuter];
     int64_t b_bstr[kMaxOuter];
+    int64_t c_bstr[kMaxOuter];
+    // row strides (elements) of A, B and C; k, n and n for dense matrices.  C other than dense (a transposed
+    // output) only without the epilogue below
+    int64_t lda, ldb, ldc;
     // optional epilogue (Float only): C = (A B + bias[batch * bias_bstr + col]) + res[same index], each
     // add rounded as the separate Add node rounds it
     const float *bias;

@@ -33,16 +33,19 @@ typedef double v4d __attribute__((ext_vector_type(4)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 // per-block batch offsets of A, B and C
-__device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, int64_t *ao, int64_t *bo) {
-    int64_t a = 0, c = 0;
+__device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, int64_t *ao, int64_t *bo,
+                                              int64_t *co) {
+    int64_t a = 0, bb = 0, c = 0;
     for (int d = p.nbatch - 1; d >= 0; d--) {
         const int64_t i = b % p.bdims[d];
         b /= p.bdims[d];
         a += i * p.a_bstr[d];
-        c += i * p.b_bstr[d];
+        bb += i * p.b_bstr[d];
+        c += i * p.c_bstr[d];
     }
     *ao = a;
-    *bo = c;
+    *bo = bb;
+    *co = c;
 }
 
 // ---------------------------------------------------------------------------
@@ -50,21 +53,22 @@ __device__ __forceinline__ void batch_offsets(int64_t b, const MatMulArgs &p, in
 // ---------------------------------------------------------------------------
 
 // Bias / residual / GELU epilogue and store of a wave's MT x NT tiles of 32x32 results (rows r0.., columns
-// c0..).  The MFMA ran as B^T A^T, so acc[i][j][q] = C[r0 + 32 i + l % 32][c0 + 32 j + 8 (q / 4) + 4 (l / 32) +
-// q % 4]: each lane holds four consecutive columns of one row per group of four results (one 16-byte store).
+// c0..) into the batch's C at offset co.  The MFMA ran as B^T A^T, so acc[i][j][q] = C[r0 + 32 i + l % 32][c0 +
+// 32 j + 8 (q / 4) + 4 (l / 32) + q % 4]: each lane holds four consecutive columns of one row per group of four
+// results (one 16-byte store).  The residual and the bias rows are dense.
 template <int MT, int NT, bool VEC, bool GELU>
-__device__ __forceinline__ void mm_epilogue(const v16f (&acc)[MT][NT], float *__restrict__ C, const MatMulArgs &p, int r0,
-                                            int c0, int l, const ExpTable &tab) {
+__device__ __forceinline__ void mm_epilogue(const v16f (&acc)[MT][NT], float *__restrict__ C, const MatMulArgs &p,
+                                            int64_t co, int r0, int c0, int l, const ExpTable &tab) {
     const int M = p.m, N = p.n;
     const int64_t bz = p.batch_base + blockIdx.z;
-    float *Cb = C + bz * (int64_t)M * N;
+    float *Cb = C + co;
     const float *Rb = p.res ? p.res + bz * (int64_t)M * N : nullptr;
     const float *Bias = p.bias ? p.bias + bz * p.bias_bstr : nullptr;
 #pragma unroll
     for (int i = 0; i < MT; i++) {
         const int row = r0 + 32 * i + (l % 32);
         if (row >= M) continue;
-        float *Cr = Cb + (int64_t)row * N;
+        float *Cr = Cb + (int64_t)row * p.ldc;
         const float *Rr = Rb ? Rb + (int64_t)row * N : nullptr;
 #pragma unroll
         for (int j = 0; j < NT; j++)
@@ -156,7 +160,10 @@ __global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C,
 #pragma unroll
         for (int k = 0; k < 4; k++) v[k] = gelu_erf_lx(v[k], tab);
     }
-    *reinterpret_cast<float4 *>(C + bz * mn + e) = make_float4(v[0], v[1], v[2], v[3]);
+    int64_t ao, bo, co;
+    batch_offsets(bz, p, &ao, &bo, &co);
+    const int64_t row = e / p.n;
+    *reinterpret_cast<float4 *>(C + co + row * p.ldc + (e - row * p.n)) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
@@ -183,10 +190,11 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
     const int M = p.m, N = p.n, K = p.k;
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
     const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
-    int64_t ao, bo;
-    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
+    int64_t ao, bo, co;
+    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo, &co);
     const float *Ab = A + ao;
     const float *Bb = B + bo;
+    const int64_t lda = p.lda, ldb = p.ldb;
 
     // global -> register staging one K step ahead: float4 e = t + NTHR h of the step's
     // A tile (row e / KQ, k 4 (e % KQ)) and B tile (k row e / BQ, column 4 (e % BQ))
@@ -199,12 +207,12 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
             if (AV % NTHR != 0 && e >= AV) continue;
             const int r = row0 + e / KQ, kk = k0 + (e % KQ) * 4;
             if constexpr (VEC) {
-                ra[h] = (r < M && kk < K) ? *reinterpret_cast<const float4 *>(Ab + (int64_t)r * K + kk)
+                ra[h] = (r < M && kk < K) ? *reinterpret_cast<const float4 *>(Ab + (int64_t)r * lda + kk)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 float v[4];
 #pragma unroll
-                for (int q = 0; q < 4; q++) v[q] = (r < M && kk + q < K) ? Ab[(int64_t)r * K + kk + q] : 0.f;
+                for (int q = 0; q < 4; q++) v[q] = (r < M && kk + q < K) ? Ab[(int64_t)r * lda + kk + q] : 0.f;
                 ra[h] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
@@ -214,12 +222,12 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
             if (BV % NTHR != 0 && e >= BV) continue;
             const int kb = k0 + e / BQ, c = col0 + (e % BQ) * 4;
             if constexpr (VEC) {
-                rb[h] = (kb < K && c < N) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)kb * N + c)
+                rb[h] = (kb < K && c < N) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)kb * ldb + c)
                                           : make_float4(0.f, 0.f, 0.f, 0.f);
             } else {
                 float v[4];
 #pragma unroll
-                for (int q = 0; q < 4; q++) v[q] = (kb < K && c + q < N) ? Bb[(int64_t)kb * N + c + q] : 0.f;
+                for (int q = 0; q < 4; q++) v[q] = (kb < K && c + q < N) ? Bb[(int64_t)kb * ldb + c + q] : 0.f;
                 rb[h] = make_float4(v[0], v[1], v[2], v[3]);
             }
         }
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
         __syncthreads();
         buf ^= 1;
     }
-    mm_epilogue<MT, NT, VEC, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
+    mm_epilogue<MT, NT, VEC, GELU>(acc, C, p, co, row0 + wr, col0 + wc, l, tab);
 }
 
 // Direct-to-LDS pipeline for K a multiple of 64 and 16-byte aligned operands.  Each K step of 16 is one stage of a
@@ -372,8 +380,8 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
     const int zb = SPLIT ? (int)blockIdx.z / p.split : (int)blockIdx.z;
     const int nk = SPLIT ? K / 16 / p.split : K / 16;
     const int k0 = SPLIT ? ((int)blockIdx.z - zb * p.split) * nk * 16 : 0;
-    int64_t ao, bo;
-    batch_offsets(p.batch_base + zb, p, &ao, &bo);
+    int64_t ao, bo, co;
+    batch_offsets(p.batch_base + zb, p, &ao, &bo, &co);
 
     // this wave's loads: a per-lane source address (advanced by `inc` floats per step) and an LDS offset
     const float *src[L];
@@ -384,14 +392,14 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
         const int i = min(w + NW * j, NL - 1);
         if (i < LA) {
             const int q = 64 * i + l, r = q >> 2, c = (q & 3) ^ dl_swz(r);
-            src[j] = A + ao + (int64_t)min(row0 + r, M - 1) * K + k0 + 4 * c;
+            src[j] = A + ao + (int64_t)min(row0 + r, M - 1) * p.lda + k0 + 4 * c;
             inc[j] = 16;
             dst[j] = 1024 * i;
         } else {
             const int h = (i - LA) / LBH, wl = (i - LA) % LBH, q = 64 * wl + l;
             const int k = 8 * h + q / (BN / 4), c = col0 + 4 * (q % (BN / 4));
-            src[j] = B + bo + (int64_t)(k0 + k) * N + min(c, N - 4);
-            inc[j] = 16 * (int64_t)N;
+            src[j] = B + bo + (int64_t)(k0 + k) * p.ldb + min(c, N - 4);
+            inc[j] = 16 * p.ldb;
             dst[j] = A_BYTES + h * (B_HALF + 128) + 1024 * wl;
         }
     }
@@ -496,7 +504,7 @@ __global__ __launch_bounds__(WM * WN * 64) __attribute__((amdgpu_waves_per_eu(WM
         mm_store_part<MT, NT>(acc, p.part + ((int64_t)(blockIdx.z - zb * p.split) * p.batch + zb) * M * N, M, N,
                               row0 + wr, col0 + wc, l);
     else
-        mm_epilogue<MT, NT, true, GELU>(acc, C, p, row0 + wr, col0 + wc, l, tab);
+        mm_epilogue<MT, NT, true, GELU>(acc, C, p, co, row0 + wr, col0 + wc, l, tab);
 }
 
 template <int BM, int BN, int WM, int WN, int WMIN, int WMAX>
@@ -542,11 +550,11 @@ __global__ __launch_bounds__(256) void k_matmul_f64(const double *__restrict__ A
     const int M = p.m, N = p.n, K = p.k;
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
     const int row0 = blockIdx.y * kDBM, col0 = blockIdx.x * kDBN;
-    int64_t ao, bo;
-    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
+    int64_t ao, bo, co;
+    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo, &co);
     const double *Ab = A + ao;
     const double *Bb = B + bo;
-    double *Cb = C + (p.batch_base + blockIdx.z) * (int64_t)M * N;
+    double *Cb = C + co;
     const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
     v4d acc[2][2];
 #pragma unroll
@@ -561,9 +569,9 @@ __global__ __launch_bounds__(256) void k_matmul_f64(const double *__restrict__ A
         for (int h = 0; h < 4; h++) {
             const int e = t + 256 * h;
             const int ar = e / kDBK, ak = e % kDBK;
-            As[ak][ar] = (row0 + ar < M && k0 + ak < K) ? Ab[(int64_t)(row0 + ar) * K + k0 + ak] : 0.0;
+            As[ak][ar] = (row0 + ar < M && k0 + ak < K) ? Ab[(int64_t)(row0 + ar) * p.lda + k0 + ak] : 0.0;
             const int bk = e / kDBN, bc = e % kDBN;
-            Bs[bk][bc] = (k0 + bk < K && col0 + bc < N) ? Bb[(int64_t)(k0 + bk) * N + col0 + bc] : 0.0;
+            Bs[bk][bc] = (k0 + bk < K && col0 + bc < N) ? Bb[(int64_t)(k0 + bk) * p.ldb + col0 + bc] : 0.0;
         }
         __syncthreads();
 #pragma unroll
@@ -587,7 +595,7 @@ __global__ __launch_bounds__(256) void k_matmul_f64(const double *__restrict__ A
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int row = row0 + wr + 16 * i + l / 16 + 4 * r;
-                if (row < M) Cb[(int64_t)row * N + c] = acc[i][j][r];
+                if (row < M) Cb[(int64_t)row * p.ldc + c] = acc[i][j][r];
             }
         }
 }
@@ -601,20 +609,20 @@ __global__ __launch_bounds__(256) void k_matmul_i32(const int32_t *__restrict__ 
     const int M = p.m, N = p.n, K = p.k;
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
     const int row = blockIdx.y * 16 + ty, col = blockIdx.x * 16 + tx;
-    int64_t ao, bo;
-    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo);
+    int64_t ao, bo, co;
+    batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo, &co);
     const int32_t *Ab = A + ao;
     const int32_t *Bb = B + bo;
     uint32_t acc = 0;
     for (int k0 = 0; k0 < K; k0 += 16) {
-        As[ty][tx] = (row < M && k0 + tx < K) ? (uint32_t)Ab[(int64_t)row * K + k0 + tx] : 0u;
-        Bs[ty][tx] = (k0 + ty < K && col < N) ? (uint32_t)Bb[(int64_t)(k0 + ty) * N + col] : 0u;
+        As[ty][tx] = (row < M && k0 + tx < K) ? (uint32_t)Ab[(int64_t)row * p.lda + k0 + tx] : 0u;
+        Bs[ty][tx] = (k0 + ty < K && col < N) ? (uint32_t)Bb[(int64_t)(k0 + ty) * p.ldb + col] : 0u;
         __syncthreads();
 #pragma unroll
         for (int k = 0; k < 16; k++) acc += As[ty][k] * Bs[k][tx];
         __syncthreads();
     }
-    if (row < M && col < N) C[(p.batch_base + blockIdx.z) * (int64_t)M * N + (int64_t)row * N + col] = (int32_t)acc;
+    if (row < M && col < N) C[co + (int64_t)row * p.ldc + col] = (int32_t)acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -665,8 +673,9 @@ hipError_t launch_strided_copy(int esize, const void *x, void *y, int rank, cons
 static bool f32_vec(const void *a, const void *b, const void *c, const MatMulArgs &p) {
     bool vec = (p.k % 4 == 0) && (p.n % 4 == 0) &&
                (((uintptr_t)a | (uintptr_t)b | (uintptr_t)c | (uintptr_t)p.res | (uintptr_t)p.bias) % 16 == 0) &&
-               p.bias_bstr % 4 == 0;
-    for (int d = 0; d < p.nbatch; d++) vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0);
+               p.bias_bstr % 4 == 0 && p.lda % 4 == 0 && p.ldb % 4 == 0 && p.ldc % 4 == 0;
+    for (int d = 0; d < p.nbatch; d++)
+        vec = vec && (p.a_bstr[d] % 4 == 0) && (p.b_bstr[d] % 4 == 0) && (p.c_bstr[d] % 4 == 0);
     return vec;
 }
 

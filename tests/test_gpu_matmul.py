@@ -312,6 +312,49 @@ def test_grouped_projections_equal_the_separate_ones(hip, xs, n, g):
         assert u.shape == f.shape and np.array_equal(u.view(np.uint32), f.view(np.uint32))
 
 
+@pytest.mark.parametrize("b,s,h,d", [(1, 8, 12, 32), (2, 64, 12, 32), (1, 512, 12, 32), (2, 10, 3, 6)])
+@pytest.mark.parametrize("q_read_twice", [False, True])
+def test_attention_transposes_fold_into_the_products(hip, b, s, h, d, q_read_twice):
+    """Transpose (perm [0,2,1,3]) -> MatMul and MatMul -> Transpose (the attention heads' Q, V and context)
+    fold into MatMulPermuted nodes that read and write the transposed views through their strides; K's
+    Transpose ([0,2,3,1]: its last axis moves) stays a node, and so does Q's when its output is also a graph
+    output.  Every output bit for bit the unfused graph's, executed and captured: 8 tokens, 64, 512 (the
+    context product splits K), heads of 6 (no 16-byte accesses)."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    rng = np.random.default_rng(93)
+    ins = {t: rng.standard_normal((b, s, h, d)).astype(np.float32) for t in "qkv"}
+    nodes = [W.node("Transpose", ["q"], ["qt"], "q_perm", perm=[0, 2, 1, 3]),
+             W.node("Transpose", ["k"], ["kt"], "k_perm", perm=[0, 2, 3, 1]),
+             W.node("Transpose", ["v"], ["vt"], "v_perm", perm=[0, 2, 1, 3]),
+             W.node("MatMul", ["qt", "kt"], ["sc"], "scores"),
+             W.node("Softmax", ["sc"], ["p"], "softmax", axis=-1),
+             W.node("MatMul", ["p", "vt"], ["ctx"], "context"),
+             W.node("Transpose", ["ctx"], ["y"], "ctx_perm", perm=[0, 2, 1, 3])]
+    outs = ["y", "sc"] + (["qt"] if q_read_twice else [])
+    dev = {t: DeviceTensor.from_numpy(v) for t, v in ins.items()}
+    res = {}
+    for mode in ("nodes", "fused", "captured"):
+        g = Model.Load(W.model(nodes, [(t, np.float32, ins[t].shape) for t in "qkv"],
+                               [(o, np.float32, ()) for o in outs], []))
+        if mode != "nodes":
+            assert g.Fuse() == (1 if q_read_twice else 2)
+            assert [n.Op for n in g.Nodes] == (["Transpose", "Transpose", "MatMul", "Softmax", "MatMulPermuted"]
+                                               if q_read_twice else
+                                               ["Transpose", "MatMulPermuted", "Softmax", "MatMulPermuted"])
+        if mode == "captured":
+            assert g.Capture(dev), g.LastError
+            assert g.Replay(), g.LastError
+        else:
+            assert g.Execute(dev), g.LastError
+        res[mode] = [g.Output(o).to_numpy() for o in outs]
+    for mode in ("fused", "captured"):
+        for u, f in zip(res["nodes"], res[mode]):
+            assert u.shape == f.shape and np.array_equal(u.view(np.uint32), f.view(np.uint32)), mode
+    ref = np.swapaxes(np.swapaxes(ins["q"], 1, 2) @ np.swapaxes(ins["k"], 1, 2).swapaxes(2, 3), 1, 1)
+    assert np.allclose(res["fused"][1], ref, rtol=1e-4, atol=1e-4)
+
+
 def _two_unnamed_projection_layers(rng):
     """Two layers of three MatMul -> Add bias projections each, every node unnamed (ONNX allows it); the
     second layer reads the first one's V and has weights of its own."""
