@@ -142,10 +142,20 @@ __global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C,
     const int64_t zb = i / nq, e = (i - zb * nq) * 4;  // batch of this launch, element of its matrix
     const int64_t stride = p.batch * mn;                // between the partials of two K ranges
     const float *P = p.part + zb * mn + e;
+    // the partials eight at a time, all eight loads in flight before the first add (one memory latency per
+    // eight, not one per partial); the adds in range order
+    constexpr int kChunk = 8;
     v4f v = *reinterpret_cast<const v4f *>(P);
-    for (int s = 1; s < p.split; s++) {
-        const v4f x = *reinterpret_cast<const v4f *>(P + s * stride);
-        v[0] = v[0] + x[0]; v[1] = v[1] + x[1]; v[2] = v[2] + x[2]; v[3] = v[3] + x[3];
+    for (int s0 = 1; s0 < p.split; s0 += kChunk) {
+        v4f x[kChunk];
+#pragma unroll
+        for (int c = 0; c < kChunk; c++)
+            if (s0 + c < p.split) x[c] = *reinterpret_cast<const v4f *>(P + (s0 + c) * stride);
+#pragma unroll
+        for (int c = 0; c < kChunk; c++)
+            if (s0 + c < p.split) {
+                v[0] = v[0] + x[c][0]; v[1] = v[1] + x[c][1]; v[2] = v[2] + x[c][2]; v[3] = v[3] + x[c][3];
+            }
     }
     const int64_t bz = p.batch_base + zb;
     if (p.bias) {
@@ -680,9 +690,9 @@ static bool f32_vec(const void *a, const void *b, const void *c, const MatMulArg
 }
 
 // K ranges of a float product on the direct-load kernel's terms (16-byte operands, K a multiple of 64): with
-// T tiles of 64x64 over the batch (ceil(m / 64) ceil(n / 64) per matrix), the most ranges, each at least two
-// passes of 64, that divide K / 64 into equal parts and keep T times the ranges within 256 blocks (one per
-// CU); 1 when T alone reaches 128 or K / 64 allows no such range.  A product of few tiles otherwise leaves
+// T tiles of 64x64 over the batch (ceil(m / 64) ceil(n / 64) per matrix), the most ranges, each a whole number
+// of passes of 64, that divide K / 64 into equal parts and keep T times the ranges within 256 blocks (one per
+// CU); 1 when T alone reaches 128 or K is a single pass.  A product of few tiles otherwise leaves
 // most CUs idle while its blocks each walk the whole of K ([8,1536] x [1536,384]: 6 blocks).  With
 // split_per_matrix, T counts one matrix's tiles (and a batch above kMatMulSplitBatch does not split), so
 // that each matrix of a grouped launch splits as it does alone.
@@ -694,7 +704,7 @@ static int f32_split(const MatMulArgs &p, bool vec) {
     if (tiles >= 128) return 1;
     const int steps = p.k / 64;
     int best = 1;
-    for (int r = 2; r <= steps / 2; r++)
+    for (int r = 2; r <= steps; r++)
         if (steps % r == 0 && tiles * r <= 256) best = r;
     return best;
 }

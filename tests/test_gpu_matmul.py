@@ -93,39 +93,43 @@ def test_float_direct_load_tiles(hip, sa, sb):
 
 def split_of(m, k, n, batch=1):
     """K ranges of a float product with 16-byte operands (lx_matmul.hip, f32_split): with T 64x64 tiles over
-    the batch, the most equal ranges of at least two 64-steps each dividing K / 64 with T times them within
-    256; 1 from T = 128."""
+    the batch, the most equal ranges of whole 64-steps dividing K / 64 with T times them within 256; 1 from
+    T = 128."""
     if k % 64 or n % 4:
         return 1
     tiles = -(-m // 64) * -(-n // 64) * batch
     if tiles >= 128:
         return 1
     steps, best = k // 64, 1
-    for r in range(2, steps // 2 + 1):
+    for r in range(2, steps + 1):
         if steps % r == 0 and tiles * r <= 256:
             best = r
     return best
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 128, 196), (2000, 192, 2020), (4096, 192, 768), (320, 192, 260),
-                                   (512, 512, 32)])
+@pytest.mark.parametrize("m,k,n", [(256, 128, 8192), (8192, 192, 512), (320, 192, 260), (512, 512, 32),
+                                   (2000, 200, 2020)])
 def test_float_kernels_sum_in_one_order(hip, m, k, n):
     """The direct-load kernel and the register-staged one add the products of a dot product in the same order,
-    so a product is the same bits whichever kernel and tile runs it: the whole product (direct loads) against
-    its 32-row blocks (fewer than 64 rows: the register-staged kernel) and its 64-column blocks (N = 64: another
-    tile of the direct-load kernel), bit for bit; N = 32 takes the 128x32 tile, and [512,512]x[512,32] and its
-    row blocks split K alike (four ranges)."""
+    so a product is the same bits whichever kernel and tile runs it, given the same K ranges: the whole product
+    against its 32-row blocks (fewer than 64 rows: the register-staged kernel) and its 64-column blocks (N = 64:
+    another tile), bit for bit, wherever the blocks split K as the whole does -- unsplit at [256,128] x
+    [128,8192] (rows) and [8192,192] x [192,512] (columns), three ranges each at [320,192] x [192,260], eight
+    at [512,512] x [512,32] (128x32 tiles whole); K = 200, the register-staged kernel's tiles only."""
     rng = np.random.default_rng(58)
     a = rng.standard_normal((m, k)).astype(np.float32)
     b = rng.standard_normal((k, n)).astype(np.float32)
     whole = mm(a, b)
-    assert all(split_of(r, k, n) == split_of(m, k, n) for r in (32, m % 32 or 32))
-    rows = np.concatenate([mm(a[i:i + 32], b) for i in range(0, m, 32)])
-    assert np.array_equal(whole.view(np.uint32), rows.view(np.uint32))
-    if n >= 128:
-        assert split_of(m, k, 64) == split_of(m, k, n) == 1
+    checked = 0
+    if all(split_of(r, k, n) == split_of(m, k, n) for r in (32, m % 32 or 32)):
+        rows = np.concatenate([mm(a[i:i + 32], b) for i in range(0, m, 32)])
+        assert np.array_equal(whole.view(np.uint32), rows.view(np.uint32))
+        checked += 1
+    if n >= 128 and split_of(m, k, 64) == split_of(m, k, n):
         cols = np.concatenate([mm(a, np.ascontiguousarray(b[:, j:j + 64])) for j in range(0, n - n % 64, 64)], axis=1)
         assert np.array_equal(whole[:, :cols.shape[1]].view(np.uint32), cols.view(np.uint32))
+        checked += 1
+    assert checked >= 1
 
 
 @pytest.mark.parametrize("sa,sb", [((8, 384), (384, 384)), ((8, 1536), (1536, 384)), ((8, 384), (384, 1536)),
@@ -283,7 +287,7 @@ def test_grouped_projections_equal_the_separate_ones(hip, xs, n, g):
     """g MatMul -> Add bias projections of one input become one MatMulAddGroup node (one batched launch,
     outputs as slices of one product); every output equals the unfused graph's bit for bit, including
     through a consumer that reads a slice (Reshape / Transpose of the second one).  Eight tokens split K in
-    the grouped launch as in each separate product: three ranges at hidden 384, eight at 1536 (where the
+    the grouped launch as in each separate product: six ranges at hidden 384, eight at 1536 (where the
     group's three matrices together would take three); a group of 17 runs its products one by one."""
     import onnx_writer as W
     from onnx_amd.graph import Model
