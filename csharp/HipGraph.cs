@@ -95,7 +95,7 @@ public sealed unsafe class HipGraph : IDisposable
         "GeluErf" => OpType.Erf,
         "LayerNormDecomposed" => OpType.ReduceMean,
         "AddSoftmax" or "ScaleAddSoftmax" => OpType.Softmax,
-        "MatMulAdd" or "MatMulAddGroup" or "MatMulAddGelu" => OpType.MatMul,
+        "MatMulAdd" or "MatMulAddGroup" or "MatMulAddGelu" or "MatMulPermuted" => OpType.MatMul,
         _ => OpType.Add,   // ElementwiseChain
     };
 

@@ -299,11 +299,14 @@ int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
 /* Pattern fusion (no reference counterpart; the reference runs every node):
  * replaces the GELU subgraph (Div sqrt2 -> Erf -> Add 1 -> Mul x -> Mul 0.5), the decomposed
  * LayerNorm (ReduceMean -> Sub -> Pow 2 -> ReduceMean -> Add eps -> Sqrt -> Div -> Mul -> Add),
- * Add(mask) -> Softmax, Div / Mul by a scalar constant -> Add(mask) -> Softmax and MatMul -> Add(row-vector
- * constant) [-> Add] by the fused kernels when every intermediate has exactly one consumer and is
- * not a graph output; then every linear chain of two or more Float elementwise nodes
+ * Add(mask) -> Softmax, Div / Mul by a scalar constant -> Add(mask) -> Softmax, MatMul -> Add(row-vector
+ * constant) [-> Add | -> the GELU subgraph], and Transposes that keep the last axis last around a MatMul
+ * (read or written as strided views) by the fused kernels when every intermediate has exactly one
+ * consumer and is not a graph output; then every linear chain of two or more Float elementwise nodes
  * (Add/Sub/Mul/Div/Pow/Sqrt/Erf) whose intermediates have one consumer by an ElementwiseChain node
- * (lx_ElementwiseChain).  *n_fused = number of fused nodes made. */
+ * (lx_ElementwiseChain); then the MatMul -> Add projections of one input as one grouped launch.
+ * Results equal the unfused graph's bit for bit where the fused kernels' are stated to.
+ * *n_fused = number of fused nodes made. */
 int lx_graph_fuse(lx_graph *g, int32_t *n_fused);
 /* Capture (no reference counterpart; the reference dispatches every node from the host on every
  * execution): runs lx_graph_execute once with these inputs, then records a second execution into a HIP

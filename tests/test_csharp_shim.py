@@ -97,3 +97,16 @@ def test_provider_opens_a_device_math_stage_before_every_native_operator_call():
     for i in calls:
         back = "\n".join(lines[max(0, i - 6):i + 1])
         assert "MathStage();" in back, lines[i]
+
+
+def test_every_fused_op_is_charted_under_a_reference_op():
+    """HipGraph.FusedOp charts each fused node the graph runtime can make (lx_graph.cpp) under an OpType;
+    ElementwiseChain takes the default arm."""
+    src = open(os.path.join(ROOT, "onnx_amd", "csrc", "lx_graph.cpp")).read()
+    made = set(re.findall(r'(?:f\.|f->)op = "(\w+)"', src))
+    assert {"GeluErf", "LayerNormDecomposed", "MatMulAdd", "MatMulAddGroup", "MatMulPermuted"} <= made
+    s = _cs("HipGraph.cs")
+    body = s[s.index("static OpType FusedOp(string name)"):]
+    body = body[:body.index("};")]
+    charted = set(re.findall(r'"(\w+)"', body))
+    assert made - {"ElementwiseChain"} <= charted, made - charted
