@@ -423,3 +423,63 @@ def test_concat_random(hip):
             xs.append(values(rng, tuple(s), dt, special=0.0))
         r = HIP.Concat([dev(v) for v in xs], axis)
         check(r, lambda: O.concat(xs, axis), same_bits, (dt, shape, axis, case))
+
+
+def matmul_case(rng):
+    """Operands of a random MatMul: ranks 1-4, batch axes that broadcast (size 1 or missing), rows and columns
+    across the tile edges, K across the direct-load kernel's, the split's and the batch fold's conditions; one
+    case in twenty with mismatched inner dimensions."""
+    m = int(rng.choice([1, 2, 5, 8, 31, 32, 33, 63, 64, 65, 100, 130, 200]))
+    n = int(rng.choice([1, 3, 4, 8, 20, 32, 36, 64, 68, 100, 128, 196]))
+    k = int(rng.choice([1, 3, 8, 16, 32, 64, 100, 128, 192, 256, 384, 512, 1024]))
+    nb = int(rng.integers(0, 3))
+    batch = tuple(int(d) for d in rng.integers(1, 4, nb))
+    sa = tuple(1 if rng.random() < 0.3 else d for d in batch[int(rng.integers(0, nb + 1)):]) + (m, k)
+    sb = tuple(1 if rng.random() < 0.3 else d for d in batch[int(rng.integers(0, nb + 1)):]) + (k, n)
+    if rng.random() < 0.05:
+        sb = sb[:-2] + (k + 1, n)
+    if rng.random() < 0.08:  # a rank-1 operand (the reference's element-wise broadcast rule)
+        if rng.random() < 0.5:
+            sa = (k,)
+        else:
+            sb = (k,)
+    return sa, sb
+
+
+@pytest.mark.parametrize("dt", [np.float32, np.float64, np.int32])
+def test_matmul_random(hip, dt):
+    """Random MatMuls against the oracle: Int32 bit-exact (wrapping), Float / Double within 1e-5 (1e-13) of
+    sum |a b| per output, the oracle's status where the shapes fail; for Float, MatMulAdd (a bias row, and a
+    residual of the product's shape) bit for bit the MatMul and the Add nodes."""
+    rng = np.random.default_rng({np.float32: 70, np.float64: 71, np.int32: 72}[dt])
+    tol = 1e-5 if dt == np.float32 else 1e-13
+    for case in range(160):
+        sa, sb = matmul_case(rng)
+        if dt == np.int32:
+            a = rng.integers(-1000, 1000, sa).astype(dt)
+            b = rng.integers(-1000, 1000, sb).astype(dt)
+        else:
+            a = rng.standard_normal(sa).astype(dt)
+            b = rng.standard_normal(sb).astype(dt)
+        r = HIP.MatMul(dev(a), dev(b))
+        try:
+            ref = O.matmul(a, b)
+        except O.OracleError as e:
+            assert r.Status != OpStatus.Success and r.Code == e.status, (case, sa, sb, r.Code, e.status)
+            continue
+        assert r.Status == OpStatus.Success, (case, sa, sb, r.Message)
+        got = r.Outputs[0].to_numpy()
+        assert got.shape == ref.shape and got.dtype == ref.dtype, (case, sa, sb)
+        if dt == np.int32:
+            assert np.array_equal(got, ref), (case, sa, sb)
+            continue
+        mag = O.matmul(np.abs(a).astype(np.float64), np.abs(b).astype(np.float64))
+        err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+        assert np.all(err <= tol * mag + 1e-30), (case, sa, sb, float((err / (mag + 1e-30)).max()))
+        if dt == np.float32 and len(sa) >= 2 and len(sb) >= 2:
+            bias = rng.standard_normal(ref.shape[-1]).astype(dt)
+            res = rng.standard_normal(ref.shape).astype(dt)
+            fused = HIP.MatMulAdd(dev(a), dev(b), dev(bias), dev(res))
+            assert fused.Status == OpStatus.Success, (case, sa, sb, fused.Message)
+            nodes = HIP.Add(HIP.Add(r.Outputs[0], dev(bias)).Outputs[0], dev(res)).Outputs[0].to_numpy()
+            assert same_bits(fused.Outputs[0].to_numpy(), nodes), (case, sa, sb)
