@@ -490,3 +490,49 @@ def test_ffn_gelu_graph_fuses_into_one_node(hip):
         g.close()
     for k in (True, "escape"):
         assert np.array_equal(res[False].view(np.uint32), res[k].view(np.uint32)), k
+
+
+def test_transposed_views_random(hip):
+    """Random Transpose -> MatMul <- Transpose -> Transpose graphs of rank 3 and 4: each Transpose whose perm
+    keeps the last axis last folds into the MatMul (read or written through strides), the others stay nodes;
+    the fused graph equals the unfused one bit for bit, executed and captured, and numpy's product within the
+    MatMul bar."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    rng = np.random.default_rng(94)
+
+    def perm(r):
+        if rng.random() < 0.6:  # keeps the last axis last
+            return [int(v) for v in rng.permutation(r - 1)] + [r - 1]
+        return [int(v) for v in rng.permutation(r)]
+
+    folded = 0
+    for case in range(24):
+        r = int(rng.choice([3, 4]))
+        batch = tuple(int(d) for d in rng.integers(1, 4, r - 2))
+        m, k, n = (int(rng.choice(v)) for v in ([1, 8, 33, 64, 100], [16, 64, 128, 384], [4, 32, 36, 64, 128]))
+        A = rng.standard_normal(batch + (m, k)).astype(np.float32)
+        B = rng.standard_normal(batch + (k, n)).astype(np.float32)
+        pa, pb, pc = perm(r), perm(r), perm(r)
+        A0 = np.ascontiguousarray(np.transpose(A, np.argsort(pa)))
+        B0 = np.ascontiguousarray(np.transpose(B, np.argsort(pb)))
+        nodes = [W.node("Transpose", ["a0"], ["a"], "ta", perm=pa), W.node("Transpose", ["b0"], ["b"], "tb", perm=pb),
+                 W.node("MatMul", ["a", "b"], ["c"], "mm"), W.node("Transpose", ["c"], ["y"], "tc", perm=pc)]
+        dev_in = {"a0": DeviceTensor.from_numpy(A0), "b0": DeviceTensor.from_numpy(B0)}
+        res = {}
+        for mode in ("nodes", "fused", "captured"):
+            g = Model.Load(W.model(nodes, [("a0", np.float32, A0.shape), ("b0", np.float32, B0.shape)],
+                                   [("y", np.float32, ())], []))
+            if mode != "nodes":
+                nf = g.Fuse()
+                folded += nf
+                assert nf == (1 if any(p[-1] == r - 1 for p in (pa, pb, pc)) else 0), (case, pa, pb, pc)
+            ok = g.Capture(dev_in) and g.Replay() if mode == "captured" else g.Execute(dev_in)
+            assert ok, (case, g.LastError)
+            res[mode] = g.Output("y").to_numpy()
+        for mode in ("fused", "captured"):
+            assert np.array_equal(res["nodes"].view(np.uint32), res[mode].view(np.uint32)), (case, mode, pa, pb, pc)
+        ref = np.transpose(A.astype(np.float64) @ B.astype(np.float64), pc)
+        mag = np.transpose(np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64), pc)
+        assert np.all(np.abs(res["nodes"] - ref) <= 1e-5 * mag + 1e-30), case
+    assert folded > 0
