@@ -1606,6 +1606,7 @@ struct MView {  // a tensor as the reference's (possibly broadcast) view: elemen
     int64_t dims[LX_MAX_RANK] = {0};
     int64_t str[LX_MAX_RANK] = {0};
     const void *data = nullptr;
+    bool bt = false;  // the matrix stored by columns (set by densify for a right operand that allows it)
 };
 
 MView dense_view(const lx_tensor *t) {
@@ -1670,11 +1671,16 @@ const char *net_type(int dt) {
 
 // the matrix part (last two axes) must be row-major dense for the kernels; otherwise
 // the operand is copied to a dense pooled block first
-int densify(int dt, MView *v, std::vector<void *> &temps) {
+int densify(int dt, MView *v, std::vector<void *> &temps, bool allow_bt = false) {
     const int r = v->rank;
     // unit column stride and rows that do not overlap (dense, or the rows of a transposed view): as they are
     if ((v->dims[r - 1] == 1 || v->str[r - 1] == 1) && (v->dims[r - 2] == 1 || v->str[r - 2] >= v->dims[r - 1]))
         return LX_OK;
+    // a right operand stored by columns (unit row stride, columns that do not overlap), where allowed: as it is
+    if (allow_bt && v->dims[r - 1] > 1 && v->dims[r - 2] > 1 && v->str[r - 2] == 1 && v->str[r - 1] >= v->dims[r - 2]) {
+        v->bt = true;
+        return LX_OK;
+    }
     int64_t n = 1;
     for (int d = 0; d < r; d++) n *= v->dims[d];
     void *p = nullptr;
@@ -1701,6 +1707,7 @@ struct MatMulEpilogue {
 thread_local MatMulEpilogue *t_mm_epi = nullptr;
 thread_local bool t_mm_per_matrix = false;  // api_matmul_add_grouped in progress
 thread_local const int *t_mm_yperm = nullptr;  // api_matmul_permuted in progress: the product's permutation
+thread_local bool t_mm_allow_bt = false;        // api_matmul_permuted in progress: B may be stored by columns
 
 // a permutation of 0 .. rank - 1 that keeps the last axis last
 bool last_axis_perm(const int *perm, int rank) {
@@ -1740,7 +1747,7 @@ bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dim
 int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, lx_tensor *Y,
                std::vector<void *> &temps) {
     int st;
-    if ((st = densify(dt, &x, temps)) || (st = densify(dt, &y, temps))) return st;
+    if ((st = densify(dt, &x, temps)) || (st = densify(dt, &y, temps, t_mm_allow_bt && dt == LX_FLOAT))) return st;
     // the product's element strides in Y: dense, or Y = transpose(product, t_mm_yperm)
     int64_t pstr[LX_MAX_RANK];
     const int *yp = t_mm_yperm;
@@ -1788,6 +1795,10 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     // row strides; a single row's is never used (the dense value)
     p.lda = x.dims[x.rank - 2] == 1 ? x.dims[x.rank - 1] : x.str[x.rank - 2];
     p.ldb = y.dims[y.rank - 2] == 1 ? y.dims[y.rank - 1] : y.str[y.rank - 2];
+    if (y.bt) {  // by columns: the stride between columns
+        p.bt = 1;
+        p.ldb = y.str[y.rank - 1];
+    }
     p.ldc = (out_rank < 2 || p.m == 1) ? p.n : pstr[out_rank - 2];  // out_rank 1: the [1] of two vectors
     if (p.nbatch > kMaxOuter) return set_err(LX_ERR_NOT_SUPPORTED, "At most %d batch axes are supported.", kMaxOuter);
     if (x.dims[x.rank - 2] > INT32_MAX || x.dims[x.rank - 1] > INT32_MAX || y.dims[y.rank - 1] > INT32_MAX)
@@ -1811,8 +1822,11 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
         HIPCHECK(launch_fill(Y->data, n, (int)esize(dt), 0, g.stream), "MatMul");
         return LX_OK;
     }
-    // partial products of a split K (stream-ordered pool block, released with the caller's temporaries)
-    if (const int64_t pb = matmul_part_bytes(dt, x.data, y.data, Y->data, p)) {
+    // partial products of a split K (stream-ordered pool block, released with the caller's temporaries); a B
+    // stored by columns runs only unsplit and without an epilogue (the caller then takes another path)
+    const int64_t pb = matmul_part_bytes(dt, x.data, y.data, Y->data, p);
+    if (p.bt && (pb || p.bias || p.res || p.gelu)) return LX_ERR_NOT_SUPPORTED;
+    if (pb) {
         void *w = nullptr;
         HIPCHECK(pool_alloc((size_t)pb, &w, nullptr, g.stream), "device allocation (temporary)");
         temps.push_back(w);
@@ -1904,9 +1918,15 @@ int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *
         check_tensor(A, "A") || check_tensor(B, "B"))
         return LX_ERR_NOT_SUPPORTED;
     MView x = dense_view(A), y = dense_view(B);
-    auto permute = [](MView &v, const int *perm) {
+    // A: its last axis stays last; B: too, or its last axis becomes the product's K (B read by columns)
+    auto permute = [](MView &v, const int *perm, bool k_last_ok) {
         if (!perm) return true;
-        if (!last_axis_perm(perm, v.rank)) return false;
+        if (!last_axis_perm(perm, v.rank)) {
+            int q[LX_MAX_RANK];  // the same permutation with its last two entries swapped
+            for (int i = 0; i < v.rank; i++) q[i] = perm[i];
+            std::swap(q[v.rank - 1], q[v.rank - 2]);
+            if (!k_last_ok || !last_axis_perm(q, v.rank)) return false;
+        }
         const MView o = v;
         for (int i = 0; i < v.rank; i++) {
             v.dims[i] = o.dims[perm[i]];
@@ -1914,11 +1934,13 @@ int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *
         }
         return true;
     };
-    if (!permute(x, a_perm) || !permute(y, b_perm)) return LX_ERR_NOT_SUPPORTED;
+    if (!permute(x, a_perm, false) || !permute(y, b_perm, true)) return LX_ERR_NOT_SUPPORTED;
     std::vector<void *> temps;
     t_mm_yperm = y_perm;
+    t_mm_allow_bt = true;
     const int st = matmul_views(LX_FLOAT, x, y, Y, temps);
     t_mm_yperm = nullptr;
+    t_mm_allow_bt = false;
     for (void *t : temps) (void)pool_release(t);
     return st;
 }

@@ -1050,13 +1050,16 @@ struct Fuser {
         return true;
     }
 
-    // a Transpose whose perm keeps the last axis last
-    bool keeps_last(int i) const {
+    // a Transpose whose perm keeps the last axis last (or, k_last, puts it second to last: a right operand
+    // then read by columns)
+    bool keeps_last(int i, bool k_last = false) const {
         if (!is(i, "Transpose", 1)) return false;
         auto it = N(i).attrs.find("perm");
         if (it == N(i).attrs.end() || it->second.kind != kAttrInts) return false;
         const std::vector<int64_t> &pm = it->second.ints;
-        return !pm.empty() && pm.size() <= LX_MAX_RANK && pm.back() == (int64_t)pm.size() - 1;
+        const int64_t r = (int64_t)pm.size();
+        if (r == 0 || r > LX_MAX_RANK) return false;
+        return pm[r - 1] == r - 1 || (k_last && r >= 2 && pm[r - 2] == r - 1);
     }
     // the unfused node that produces `name`, or -1
     int producer(const std::string &name) const {
@@ -1064,9 +1067,9 @@ struct Fuser {
             if (!used[k] && N(k).out.size() == 1 && N(k).out[0] == name) return k;
         return -1;
     }
-    // Transpose -> MatMul input and MatMul -> Transpose, each Transpose keeping the last axis last and its
-    // tensor read only by the MatMul: the MatMul reads and writes the transposed views through their strides
-    // (an attention layer's Q, V and context heads)
+    // Transpose -> MatMul input and MatMul -> Transpose, each Transpose keeping the last axis last (the right
+    // operand's may also make it K: read by columns) and its tensor read only by the MatMul: the MatMul reads and
+    // writes the transposed views through their strides (an attention layer's Q, K, V and context heads)
     bool matmul_permuted(int i0, GNode *f, std::vector<int> *nodes) {
         if (!is(i0, "MatMul", 2)) return false;
         const GNode &m = N(i0);
@@ -1076,7 +1079,7 @@ struct Fuser {
         static const char *names[2] = {"a_perm", "b_perm"};
         for (int side = 0; side < 2 && m.in[0] != m.in[1]; side++) {
             const int t = producer(m.in[side]);
-            if (t < 0 || !keeps_last(t) || only_consumer(m.in[side]) != i0) continue;
+            if (t < 0 || !keeps_last(t, side == 1) || only_consumer(m.in[side]) != i0) continue;
             f->in[side] = N(t).in[0];
             f->attrs[names[side]] = N(t).attrs.at("perm");
             ns.push_back(t);

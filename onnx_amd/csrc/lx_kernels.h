@@ -167,6 +167,8 @@ struct MatMulArgs {
     // row strides (elements) of A, B and C; k, n and n for dense matrices.  C other than dense (a transposed
     // output) only without the epilogue below
     int64_t lda, ldb, ldc;
+    // 1: B stored by columns, element (k, n) at n * ldb + k (Float, no epilogue, never split)
+    int32_t bt;
     // optional epilogue (Float only): C = (A B + bias[batch * bias_bstr + col]) + res[same index], each
     // add rounded as the separate Add node rounds it
     const float *bias;

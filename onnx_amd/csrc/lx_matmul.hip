@@ -183,7 +183,9 @@ __global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C,
 // unaligned operands, K <= 64, N <= 64 and 128x96 tiles beyond one per CU.
 constexpr int kFBK = 16, kFPad = 4;
 
-template <int BM, int BN, int WM, int WN, bool VEC, bool GELU>
+// BT: B stored by columns (element (k, n) at n * ldb + k: a transposed view), loaded as A is, along K, and
+// written into the same LDS layout, so the MFMAs and their sums are those of a row-major B.
+template <int BM, int BN, int WM, int WN, bool VEC, bool GELU, bool BT = false>
 __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__restrict__ A, const float *__restrict__ B,
                                                              float *__restrict__ C, MatMulArgs p) {
     constexpr int NTHR = WM * WN * 64;               // threads of the block
@@ -230,6 +232,19 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
         for (int h = 0; h < LB; h++) {
             const int e = t + NTHR * h;
             if (BV % NTHR != 0 && e >= BV) continue;
+            if constexpr (BT) {  // column col0 + e / KQ, k 4 (e % KQ) of the step
+                const int c = col0 + e / KQ, kk = k0 + (e % KQ) * 4;
+                if constexpr (VEC) {
+                    rb[h] = (c < N && kk < K) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)c * ldb + kk)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+                } else {
+                    float v[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) v[q] = (c < N && kk + q < K) ? Bb[(int64_t)c * ldb + kk + q] : 0.f;
+                    rb[h] = make_float4(v[0], v[1], v[2], v[3]);
+                }
+                continue;
+            }
             const int kb = k0 + e / BQ, c = col0 + (e % BQ) * 4;
             if constexpr (VEC) {
                 rb[h] = (kb < K && c < N) ? *reinterpret_cast<const float4 *>(Bb + (int64_t)kb * ldb + c)
@@ -257,7 +272,15 @@ __global__ __launch_bounds__(WM * WN * 64) void k_matmul_f32(const float *__rest
         for (int h = 0; h < LB; h++) {
             const int e = t + NTHR * h;
             if (BV % NTHR != 0 && e >= BV) continue;
-            *reinterpret_cast<float4 *>(&Bs[buf][e / BQ][(e % BQ) * 4]) = rb[h];
+            if constexpr (BT) {
+                const int c = e / KQ, kk = (e % KQ) * 4;
+                Bs[buf][kk + 0][c] = rb[h].x;
+                Bs[buf][kk + 1][c] = rb[h].y;
+                Bs[buf][kk + 2][c] = rb[h].z;
+                Bs[buf][kk + 3][c] = rb[h].w;
+            } else {
+                *reinterpret_cast<float4 *>(&Bs[buf][e / BQ][(e % BQ) * 4]) = rb[h];
+            }
         }
     };
 
@@ -539,6 +562,11 @@ template <int BM, int BN, int WM, int WN>
 static void launch_f32(const float *a, const float *b, float *c, const MatMulArgs &p, bool vec, hipStream_t s) {
     dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
     const dim3 blk(WM * WN * 64);
+    if (p.bt) {  // a transposed view of B, without an epilogue
+        if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true, false, true>), g, blk, 0, s, a, b, c, p);
+        else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false, false, true>), g, blk, 0, s, a, b, c, p);
+        return;
+    }
     if (p.gelu) {
         if (vec) hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, true, true>), g, blk, 0, s, a, b, c, p);
         else hipLaunchKernelGGL((k_matmul_f32<BM, BN, WM, WN, false, true>), g, blk, 0, s, a, b, c, p);
@@ -735,7 +763,7 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         float *fc = (float *)c;
         const int split = f32_split(p, vec);
         if (split > 1) {
-            if (!p.part) return hipErrorInvalidValue;  // the caller sizes it with matmul_part_bytes
+            if (!p.part || p.bt) return hipErrorInvalidValue;  // the caller sizes it with matmul_part_bytes
             MatMulArgs q = p;
             q.split = split;
             launch_f32_split(fa, fb, fc, q, s);
@@ -780,11 +808,12 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         // uninterrupted MFMA stream ([4096,3072]x[3072,768]: 133 against 126 TFLOP/s for 64x64).
         // N of at most 32 (the attention context of 32-wide heads): 128x32 tiles, four waves of 32x32
         // ([8,12,512,512]x[8,12,512,32]: 65 against 43 TFLOP/s for the register-staged kernel's 64x64)
-        if (vec && p.k % 64 == 0 && p.k > 64 && p.n <= 32 && p.m >= 64) {
+        // (B by columns, p.bt: the register-staged kernel only, never split -- the host checks)
+        if (!p.bt && vec && p.k % 64 == 0 && p.k > 64 && p.n <= 32 && p.m >= 64) {
             launch_f32_dl<128, 32, 4, 1, 1, 2>(fa, fb, fc, p, s);
             return hipGetLastError();
         }
-        if (vec && p.k % 64 == 0 && p.k > 64 && p.n >= 64 && p.m >= 64) {
+        if (!p.bt && vec && p.k % 64 == 0 && p.k > 64 && p.n >= 64 && p.m >= 64) {
             struct DTile {
                 int bm, bn, resident;
                 double eff;

@@ -316,14 +316,16 @@ def test_grouped_projections_equal_the_separate_ones(hip, xs, n, g):
         assert u.shape == f.shape and np.array_equal(u.view(np.uint32), f.view(np.uint32))
 
 
-@pytest.mark.parametrize("b,s,h,d", [(1, 8, 12, 32), (2, 64, 12, 32), (1, 512, 12, 32), (2, 10, 3, 6)])
+@pytest.mark.parametrize("b,s,h,d", [(1, 8, 12, 32), (2, 64, 12, 32), (1, 512, 12, 32), (2, 10, 3, 6),
+                                     (1, 8, 12, 128)])
 @pytest.mark.parametrize("q_read_twice", [False, True])
 def test_attention_transposes_fold_into_the_products(hip, b, s, h, d, q_read_twice):
     """Transpose (perm [0,2,1,3]) -> MatMul and MatMul -> Transpose (the attention heads' Q, V and context)
-    fold into MatMulPermuted nodes that read and write the transposed views through their strides; K's
-    Transpose ([0,2,3,1]: its last axis moves) stays a node, and so does Q's when its output is also a graph
-    output.  Every output bit for bit the unfused graph's, executed and captured: 8 tokens, 64, 512 (the
-    context product splits K), heads of 6 (no 16-byte accesses)."""
+    fold into MatMulPermuted nodes that read and write the transposed views through their strides, and so
+    does K's Transpose ([0,2,3,1]), read by columns; Q's stays a node when its output is also a graph output.
+    Every output bit for bit the unfused graph's, executed and captured: 8 tokens, 64, 512 (the context
+    product splits K), heads of 6 (no 16-byte accesses), heads of 128 at 8 tokens (the scores would split K,
+    which a B read by columns does not: that node runs its Transpose and MatMul)."""
     import onnx_writer as W
     from onnx_amd.graph import Model
     rng = np.random.default_rng(93)
@@ -342,10 +344,9 @@ def test_attention_transposes_fold_into_the_products(hip, b, s, h, d, q_read_twi
         g = Model.Load(W.model(nodes, [(t, np.float32, ins[t].shape) for t in "qkv"],
                                [(o, np.float32, ()) for o in outs], []))
         if mode != "nodes":
-            assert g.Fuse() == (1 if q_read_twice else 2)
-            assert [n.Op for n in g.Nodes] == (["Transpose", "Transpose", "MatMul", "Softmax", "MatMulPermuted"]
-                                               if q_read_twice else
-                                               ["Transpose", "MatMulPermuted", "Softmax", "MatMulPermuted"])
+            assert g.Fuse() == 2
+            assert [n.Op for n in g.Nodes] == (["Transpose"] if q_read_twice else []) + [
+                "MatMulPermuted", "Softmax", "MatMulPermuted"]
         if mode == "captured":
             assert g.Capture(dev), g.LastError
             assert g.Replay(), g.LastError
@@ -494,9 +495,9 @@ def test_ffn_gelu_graph_fuses_into_one_node(hip):
 
 def test_transposed_views_random(hip):
     """Random Transpose -> MatMul <- Transpose -> Transpose graphs of rank 3 and 4: each Transpose whose perm
-    keeps the last axis last folds into the MatMul (read or written through strides), the others stay nodes;
-    the fused graph equals the unfused one bit for bit, executed and captured, and numpy's product within the
-    MatMul bar."""
+    keeps the last axis last folds into the MatMul (read or written through strides), and so does the right
+    operand's when it makes its last axis K (read by columns), the others stay nodes; the fused graph equals
+    the unfused one bit for bit, executed and captured, and numpy's product within the MatMul bar."""
     import onnx_writer as W
     from onnx_amd.graph import Model
     rng = np.random.default_rng(94)
@@ -526,7 +527,8 @@ def test_transposed_views_random(hip):
             if mode != "nodes":
                 nf = g.Fuse()
                 folded += nf
-                assert nf == (1 if any(p[-1] == r - 1 for p in (pa, pb, pc)) else 0), (case, pa, pb, pc)
+                folds = pa[-1] == r - 1 or pb[-1] == r - 1 or pb[-2] == r - 1 or pc[-1] == r - 1
+                assert nf == (1 if folds else 0), (case, pa, pb, pc)
             ok = g.Capture(dev_in) and g.Replay() if mode == "captured" else g.Execute(dev_in)
             assert ok, (case, g.LastError)
             res[mode] = g.Output("y").to_numpy()
