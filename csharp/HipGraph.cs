@@ -94,6 +94,7 @@ public sealed unsafe class HipGraph : IDisposable
     {
         "GeluErf" => OpType.Erf,
         "LayerNormDecomposed" => OpType.ReduceMean,
+        "MatMulAddLayerNorm" => OpType.MatMul,
         "AddSoftmax" or "ScaleAddSoftmax" => OpType.Softmax,
         "MatMulAdd" or "MatMulAddGroup" or "MatMulAddGelu" or "MatMulPermuted" => OpType.MatMul,
         _ => OpType.Add,   // ElementwiseChain

@@ -1709,6 +1709,15 @@ thread_local bool t_mm_per_matrix = false;  // api_matmul_add_grouped in progres
 thread_local const int *t_mm_yperm = nullptr;  // api_matmul_permuted in progress: the product's permutation
 thread_local bool t_mm_allow_bt = false;        // api_matmul_permuted in progress: B may be stored by columns
 
+// api_matmul_add_layernorm in progress: the LayerNorm that follows the product (and its epilogue), applied by the
+// split product's ordered sum when the product splits (`applied` tells the caller)
+struct MatMulLayerNorm {
+    const lx_tensor *gamma = nullptr, *beta = nullptr;
+    float eps = 0.0f;
+    bool applied = false;
+};
+thread_local MatMulLayerNorm *t_mm_ln = nullptr;
+
 // a permutation of 0 .. rank - 1 that keeps the last axis last
 bool last_axis_perm(const int *perm, int rank) {
     bool seen[LX_MAX_RANK] = {false};
@@ -1831,6 +1840,19 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
         HIPCHECK(pool_alloc((size_t)pb, &w, nullptr, g.stream), "device allocation (temporary)");
         temps.push_back(w);
         p.part = (float *)w;
+    }
+    // the LayerNorm after the product, in its ordered sum: every requested Add in the epilogue, the rows the
+    // row-per-wave LayerNorm kernel takes, gamma and beta rows of the output's last axis
+    if (t_mm_ln && !yp && (!t_mm_epi || ((!t_mm_epi->bias || p.bias) && (!t_mm_epi->res || p.res))) &&
+        matmul_ln_fusable(dt, x.data, y.data, Y->data, p) && t_mm_ln->gamma->dtype == LX_FLOAT &&
+        t_mm_ln->beta->dtype == LX_FLOAT && layernorm_affine_fits(t_mm_ln->gamma, Y) &&
+        layernorm_affine_fits(t_mm_ln->beta, Y) && aligned16(t_mm_ln->gamma->data) && aligned16(t_mm_ln->beta->data)) {
+        HIPCHECK(launch_matmul_ln(x.data, y.data, Y->data, p, (const float *)t_mm_ln->gamma->data,
+                                  (const float *)t_mm_ln->beta->data, t_mm_ln->eps, g.stream),
+                 "MatMul");
+        t_mm_ln->applied = true;
+        if (t_mm_epi && (p.bias || p.res)) t_mm_epi->applied = true;
+        return LX_OK;
     }
     HIPCHECK(launch_matmul(dt, x.data, y.data, Y->data, p, g.stream), "MatMul");
     if (t_mm_epi && (p.bias || p.res || p.gelu)) t_mm_epi->applied = true;
@@ -2004,6 +2026,26 @@ extern "C" int lx_MatMulAdd(const lx_tensor *A, const lx_tensor *B, const lx_ten
 }
 
 namespace lx {
+int api_matmul_add_layernorm(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, const lx_tensor *residual,
+                             const lx_tensor *gamma, const lx_tensor *beta, float eps, lx_tensor *Y) {
+    if (!api_initialized() || !A || !W || !bias || !gamma || !beta || !Y || Y->data) return LX_ERR_NOT_SUPPORTED;
+    MatMulLayerNorm ln;
+    ln.gamma = gamma;
+    ln.beta = beta;
+    ln.eps = eps;
+    t_mm_ln = &ln;
+    lx_tensor h{};
+    int st = matmul_add_run(A, W, bias, residual, false, &h);
+    t_mm_ln = nullptr;
+    if (!st && ln.applied) {
+        *Y = h;
+        return LX_OK;
+    }
+    if (!st) st = lx_LayerNormDecomposed(&h, gamma, beta, eps, Y);
+    lx_tensor_free(&h);
+    return st;
+}
+
 int api_matmul_add_grouped(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, lx_tensor *Y) {
     if (!W || W->rank != 3 || W->dims[0] > kMatMulSplitBatch) return LX_ERR_NOT_SUPPORTED;
     t_mm_per_matrix = true;

@@ -485,4 +485,58 @@ __device__ __forceinline__ double pow_lx(double x, double y) {
     return ::pow(x, y);
 }
 
+// The decomposed LayerNorm of one row of r floats (r a multiple of 4, at most 256 NV) held by a wave: lane l holds
+// the 16-byte vectors c * 64 + l (c < NV), zero past the row's end.  Each ONNX node keeps its float32 rounding:
+// mean = sum(x) / (float)r;  d = x - mean;  p = d*d (Pow 2);  var = sum(p) / (float)r;  ve = var + eps;
+// sd = sqrtf(ve);  n = d / sd;  m = n * gamma;  y = m + beta, stored to q; the two sums in lane-vector order,
+// then across the wave.  Shared by every kernel that normalises rows this way, so their results are identical.
+// The per-vector bounds checks stay even when r fills every vector: without them the compiler issues the gamma
+// / beta loads with the row's.
+template <int NV>
+__device__ __forceinline__ void ln_row_finish(Vec<float, 4> (&v)[NV], int r, int lane, const float *__restrict__ gamma,
+                                              const float *__restrict__ beta, float eps, float *__restrict__ q) {
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) s = s + ((v[c].v[0] + v[c].v[1]) + (v[c].v[2] + v[c].v[3]));
+    }
+    s = wave_reduce_dpp(s, [](float a, float b) { return a + b; });
+    const float fr = (float)r;
+    const float mean = s / fr;
+    float s2 = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[c].v[k] = v[c].v[k] - mean;
+            float p0 = v[c].v[0] * v[c].v[0], p1 = v[c].v[1] * v[c].v[1];
+            float p2 = v[c].v[2] * v[c].v[2], p3 = v[c].v[3] * v[c].v[3];
+            s2 = s2 + ((p0 + p1) + (p2 + p3));
+        }
+    }
+    s2 = wave_reduce_dpp(s2, [](float a, float b) { return a + b; });
+    const float var = s2 / fr;
+    const float ve = var + eps;
+    const float sd = __builtin_sqrtf(ve);
+    const float rsd = 1.0f / sd;
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col < r) {
+            Vec<float, 4> g = vload<float, 4>(gamma + col);
+            Vec<float, 4> b = vload<float, 4>(beta + col);
+            Vec<float, 4> o;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                float nrm = div_by_row_lx(v[c].v[k], sd, rsd);
+                float m = nrm * g.v[k];
+                o.v[k] = m + b.v[k];
+            }
+            vstore_nt<float, 4>(q + col, o);
+        }
+    }
+}
+
 }  // namespace lx

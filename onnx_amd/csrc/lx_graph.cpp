@@ -718,6 +718,24 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         if (!same) return run_unfused(X, n, outs);
         return run_op([&](lx_tensor *y) { return lx_AddSoftmax(T(s), T(m), axis, y); }, outs);
     }
+    if (op == "MatMulAddLayerNorm") {
+        const size_t nin = n.in.size();
+        Value *av, *wv, *bv, *rv = nullptr, *gv, *ev;
+        if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &wv)) || (st = X.input(n, 2, &bv))) return st;
+        if (nin == 6 && (st = X.input(n, 3, &rv))) return st;
+        if ((st = X.input(n, nin - 2, &gv)) || (st = X.input(n, nin - 1, &ev))) return st;
+        auto eps = n.attrs.find("epsilon");
+        if (av && wv && bv && gv && ev && eps != n.attrs.end() && eps->second.kind == kAttrFloat) {
+            lx_tensor y{};
+            if (api_matmul_add_layernorm(&av->t, &wv->t, &bv->t, rv ? &rv->t : nullptr, &gv->t, &ev->t,
+                                         eps->second.f, &y) == LX_OK) {
+                outs.push_back(value_from_output(y));
+                return LX_OK;
+            }
+            lx_tensor_free(&y);
+        }
+        return run_unfused(X, n, outs);
+    }
     if (op == "MatMulPermuted") {
         Value *av, *bv;
         if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &bv))) return st;
@@ -1241,7 +1259,44 @@ struct Fuser {
             if (!used[i]) out.push_back(g->nodes[i]);
         }
         g->nodes.swap(out);
-        return fused - group_projections();
+        const int grouped = group_projections();
+        return fused - grouped - merge_layernorms();
+    }
+
+    // A MatMulAdd whose result only a LayerNormDecomposed reads (x): one MatMulAddLayerNorm node (inputs A, W,
+    // bias, [residual,] gamma, beta), which normalises the rows in the split product's ordered sum when the
+    // product splits, else runs the two fused kernels.  Placed where the LayerNorm was.  Returns the nodes
+    // removed.
+    int merge_layernorms() {
+        index();
+        std::set<int> drop;
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            const GNode &m = g->nodes[i];
+            if (m.op != "MatMulAdd" || m.out.size() != 1 || (m.in.size() != 3 && m.in.size() != 4)) continue;
+            const int c = only_consumer(m.out[0]);
+            if (c < 0 || drop.count(c)) continue;
+            const GNode &l = g->nodes[c];
+            if (l.op != "LayerNormDecomposed" || l.in.size() != 3 || l.in[0] != m.out[0]) continue;
+            GNode f;
+            f.op = "MatMulAddLayerNorm";
+            f.name = l.name;
+            f.index = l.index;
+            f.in = m.in;
+            f.in.push_back(l.in[1]);
+            f.in.push_back(l.in[2]);
+            f.out = l.out;
+            f.attrs = l.attrs;
+            f.fused_from = m.fused_from;
+            f.fused_from.insert(f.fused_from.end(), l.fused_from.begin(), l.fused_from.end());
+            g->nodes[c] = f;
+            drop.insert(i);
+        }
+        if (drop.empty()) return 0;
+        std::vector<GNode> out;
+        for (int i = 0; i < (int)g->nodes.size(); i++)
+            if (!drop.count(i)) out.push_back(g->nodes[i]);
+        g->nodes.swap(out);
+        return (int)drop.size();
     }
 
     // MatMulAdd nodes (no residual) that share their input A, with constant Float weights [K, N] of one

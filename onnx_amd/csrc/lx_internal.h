@@ -61,6 +61,12 @@ bool api_layernorm_affine_fits(const lx_tensor *t, const lx_tensor *X);
 // slice is bit-identical to that product.  LX_ERR_NOT_SUPPORTED (no message) for G above 16.
 int api_matmul_add_grouped(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, lx_tensor *Y);
 
+// lx_MatMulAdd (bias, optional residual) then lx_LayerNormDecomposed on its result into Y (empty): when the
+// product splits K and every step fits, the split product's ordered sum applies the Adds and the LayerNorm in one
+// launch (the product never written), bit for bit the two calls; otherwise the two calls.
+int api_matmul_add_layernorm(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, const lx_tensor *residual,
+                             const lx_tensor *gamma, const lx_tensor *beta, float eps, lx_tensor *Y);
+
 // MatMul of transpose(A, a_perm) and transpose(B, b_perm) (null: the tensor itself), its product stored as
 // transpose(product, y_perm) into Y (null: as it is), Float, each permutation keeping the last axis last: the
 // kernels read and write the transposed views through their strides, and the result is bit for bit the

@@ -191,6 +191,12 @@ struct MatMulArgs {
 constexpr int64_t kMatMulSplitBatch = 16;
 int64_t matmul_part_bytes(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p);
 hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const MatMulArgs &p, hipStream_t s);
+// A split Float product (its epilogue included, no GELU) whose rows of n (a multiple of 4, 256 to 4096) are then
+// normalised by the decomposed LayerNorm (gamma and beta rows of n): launch_matmul_ln writes the normalised rows
+// into y, bit for bit launch_matmul followed by launch_layernorm on its result, in two launches.
+bool matmul_ln_fusable(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p);
+hipError_t launch_matmul_ln(const void *a, const void *b, void *y, const MatMulArgs &p, const float *gamma,
+                            const float *beta, float eps, hipStream_t s);
 
 // Data movement (Transpose, Slice, Concat, expand): for every index j of `dims`
 //   dst[dst_base + sum_k j_k dst_str[k]] = src[src_base + sum_k j_k src_str[k]]

@@ -176,6 +176,51 @@ __global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C,
     *reinterpret_cast<float4 *>(C + co + row * p.ldc + (e - row * p.n)) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
+// k_matmul_split_sum for a product whose rows are then normalised (the decomposed LayerNorm after a projection and
+// its residual): one wave per row, lane l holding the vectors c * 64 + l as k_layernorm does; each element summed
+// over the partials in range order with the bias and residual exactly as in k_matmul_split_sum, then the row
+// normalised by ln_row_finish into y (dense, the product's shape).  Bit for bit k_matmul_split_sum followed by
+// k_layernorm, without the product's round trip through memory.
+template <int NV>
+__global__ __launch_bounds__(64) void k_matmul_split_sum_ln(const float *__restrict__ gamma, const float *__restrict__ beta,
+                                                             float eps, float *__restrict__ y, MatMulArgs p) {
+    const int lane = threadIdx.x;
+    const int64_t rg = blockIdx.x, zb = rg / p.m, row = rg - zb * p.m;  // row of the launch's batch zb
+    const int N = p.n;
+    const int64_t mn = (int64_t)p.m * N, stride = p.batch * mn, bz = p.batch_base + zb;
+    constexpr int kChunk = 8;
+    Vec<float, 4> v[NV];
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        v[c] = Vec<float, 4>{{0.0f, 0.0f, 0.0f, 0.0f}};
+        if (col >= N) continue;
+        const float *P = p.part + zb * mn + row * N + col;
+        v4f a = *reinterpret_cast<const v4f *>(P);
+        for (int s0 = 1; s0 < p.split; s0 += kChunk) {
+            v4f x[kChunk];
+#pragma unroll
+            for (int q = 0; q < kChunk; q++)
+                if (s0 + q < p.split) x[q] = *reinterpret_cast<const v4f *>(P + (s0 + q) * stride);
+#pragma unroll
+            for (int q = 0; q < kChunk; q++)
+                if (s0 + q < p.split) {
+                    a[0] = a[0] + x[q][0]; a[1] = a[1] + x[q][1]; a[2] = a[2] + x[q][2]; a[3] = a[3] + x[q][3];
+                }
+        }
+        if (p.bias) {
+            const float4 bc = *reinterpret_cast<const float4 *>(p.bias + bz * p.bias_bstr + col);
+            a[0] = a[0] + bc.x; a[1] = a[1] + bc.y; a[2] = a[2] + bc.z; a[3] = a[3] + bc.w;
+        }
+        if (p.res) {
+            const float4 rc = *reinterpret_cast<const float4 *>(p.res + bz * mn + row * N + col);
+            a[0] = a[0] + rc.x; a[1] = a[1] + rc.y; a[2] = a[2] + rc.z; a[3] = a[3] + rc.w;
+        }
+        v[c] = Vec<float, 4>{{a[0], a[1], a[2], a[3]}};
+    }
+    ln_row_finish<NV>(v, N, lane, gamma, beta, eps, y + bz * mn + row * N);
+}
+
 // BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
 // = MT x NT MFMA tiles of 32x32.  K steps of 16, double-buffered in LDS with k
 // as the outer index (A transposed to [k][m], B as [k][n]), so the lanes of a
@@ -735,6 +780,33 @@ static int f32_split(const MatMulArgs &p, bool vec) {
     for (int r = 2; r <= steps; r++)
         if (steps % r == 0 && tiles * r <= 256) best = r;
     return best;
+}
+
+bool matmul_ln_fusable(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p) {
+    return dtype == kFloat && !p.gelu && !p.bt && p.n % 4 == 0 && p.n >= 256 && p.n <= 4096 &&
+           matmul_part_bytes(dtype, a, b, c, p) > 0;
+}
+
+hipError_t launch_matmul_ln(const void *a, const void *b, void *y, const MatMulArgs &p0, const float *gamma,
+                            const float *beta, float eps, hipStream_t s) {
+    if (!matmul_ln_fusable(kFloat, a, b, y, p0) || !p0.part) return hipErrorInvalidValue;
+    MatMulArgs p = p0;
+    p.split = f32_split(p, f32_vec(a, b, y, p));
+    const dim3 g((p.n + 63) / 64, (p.m + 63) / 64, (unsigned)(p.batch * p.split));
+    hipLaunchKernelGGL((k_matmul_f32_dl<64, 64, 2, 2, 4, 3, 8, false, true>), g, dim3(256), 0, s, (const float *)a,
+                       (const float *)b, (float *)y, p);
+    const dim3 gr((unsigned)(p.batch * p.m));
+    float *fy = (float *)y;
+    switch ((p.n + 255) / 256) {
+#define LX_MM_LN_CASE(NV) \
+    case NV: hipLaunchKernelGGL(k_matmul_split_sum_ln<NV>, gr, dim3(64), 0, s, gamma, beta, eps, fy, p); break;
+        LX_MM_LN_CASE(1) LX_MM_LN_CASE(2) LX_MM_LN_CASE(3) LX_MM_LN_CASE(4) LX_MM_LN_CASE(5) LX_MM_LN_CASE(6)
+        LX_MM_LN_CASE(7) LX_MM_LN_CASE(8) LX_MM_LN_CASE(9) LX_MM_LN_CASE(10) LX_MM_LN_CASE(11) LX_MM_LN_CASE(12)
+        LX_MM_LN_CASE(13) LX_MM_LN_CASE(14) LX_MM_LN_CASE(15) LX_MM_LN_CASE(16)
+#undef LX_MM_LN_CASE
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 int64_t matmul_part_bytes(int dtype, const void *a, const void *b, const void *c, const MatMulArgs &p) {

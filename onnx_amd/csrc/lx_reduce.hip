@@ -543,8 +543,7 @@ int64_t reduce_workspace_bytes(int dtype, int64_t outer, int64_t r, int64_t inne
 constexpr int kLnBlock = 64;
 
 // The row sums run over DPP lane moves (wave_reduce_dpp): C2 5.09 -> 5.01 us against the shuffle butterfly.
-// The per-vector bounds checks stay even when r fills every vector: without them the compiler issues the
-// gamma / beta loads with the row's (5.40 us).
+// The row arithmetic is ln_row_finish (lx_device.h).
 template <int NV>
 __global__ __launch_bounds__(kLnBlock) void k_layernorm(const float *__restrict__ x, const float *__restrict__ gamma,
                                                        const float *__restrict__ beta, float eps,
@@ -555,54 +554,13 @@ __global__ __launch_bounds__(kLnBlock) void k_layernorm(const float *__restrict_
     const float *p = x + row * (int64_t)r;
     float *q = y + row * (int64_t)r;
     Vec<float, 4> v[NV];
-    float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * 4;
         if (col < r) v[c] = vload_nt<float, 4>(p + col);
         else v[c] = Vec<float, 4>{{0.0f, 0.0f, 0.0f, 0.0f}};
     }
-#pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * 4;
-        if (col < r) s = s + ((v[c].v[0] + v[c].v[1]) + (v[c].v[2] + v[c].v[3]));
-    }
-    s = wave_reduce_dpp(s, [](float a, float b) { return a + b; });
-    const float fr = (float)r;
-    const float mean = s / fr;
-    float s2 = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * 4;
-        if (col < r) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) v[c].v[k] = v[c].v[k] - mean;
-            float p0 = v[c].v[0] * v[c].v[0], p1 = v[c].v[1] * v[c].v[1];
-            float p2 = v[c].v[2] * v[c].v[2], p3 = v[c].v[3] * v[c].v[3];
-            s2 = s2 + ((p0 + p1) + (p2 + p3));
-        }
-    }
-    s2 = wave_reduce_dpp(s2, [](float a, float b) { return a + b; });
-    const float var = s2 / fr;
-    const float ve = var + eps;
-    const float sd = __builtin_sqrtf(ve);
-    const float rsd = 1.0f / sd;
-#pragma unroll
-    for (int c = 0; c < NV; c++) {
-        const int col = (c * 64 + lane) * 4;
-        if (col < r) {
-            Vec<float, 4> g = vload<float, 4>(gamma + col);
-            Vec<float, 4> b = vload<float, 4>(beta + col);
-            Vec<float, 4> o;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                float nrm = div_by_row_lx(v[c].v[k], sd, rsd);
-                float m = nrm * g.v[k];
-                o.v[k] = m + b.v[k];
-            }
-            vstore_nt<float, 4>(q + col, o);
-        }
-    }
+    ln_row_finish<NV>(v, r, lane, gamma, beta, eps, q);
 }
 
 template <int L>

@@ -538,3 +538,46 @@ def test_transposed_views_random(hip):
         mag = np.transpose(np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64), pc)
         assert np.all(np.abs(res["nodes"] - ref) <= 1e-5 * mag + 1e-30), case
     assert folded > 0
+
+
+@pytest.mark.parametrize("xs,k,n,residual", [((1, 8, 384), 384, 384, True), ((1, 8, 1536), 1536, 384, True),
+                                             ((2, 40, 384), 1536, 768, False), ((1, 8, 384), 384, 4096, True),
+                                             ((8, 512, 384), 384, 384, True), ((1, 8, 384), 384, 200, True)])
+def test_matmul_add_layernorm_equals_the_two_fused_nodes(hip, xs, k, n, residual):
+    """MatMul -> Add bias [-> Add residual] -> the decomposed LayerNorm's nine nodes fuse to one
+    MatMulAddLayerNorm node; it equals lx_MatMulAdd followed by lx_LayerNormDecomposed bit for bit, executed
+    and captured.  Products that split K (8 tokens, hidden 384 and 1536, rows up to 4096) normalise in the
+    ordered sum of the partials; [8,512] tokens (no split) and rows of 200 (another LayerNorm kernel) run the
+    two kernels."""
+    import onnx_writer as W
+    from onnx_amd.graph import Model
+    from bert_layer import _ln
+    rng = np.random.default_rng(95)
+    x = rng.standard_normal(xs[:-1] + (k,)).astype(np.float32)
+    w = (rng.standard_normal((k, n)) * 0.05).astype(np.float32)
+    b = rng.standard_normal(n).astype(np.float32)
+    r = rng.standard_normal(xs[:-1] + (n,)).astype(np.float32)
+    gamma = (1 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    beta = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    inits = [("w", w), ("b", b), ("gamma1", gamma), ("beta1", beta), ("axes", np.array([-1], np.int64)),
+             ("two", np.array(2.0, np.float32)), ("eps", np.array(1e-12, np.float32))]
+    nodes = [W.node("MatMul", ["x", "w"], ["p"], "proj"), W.node("Add", ["p", "b"], ["h0"], "bias")]
+    h = "h0"
+    if residual:
+        nodes.append(W.node("Add", ["h0", "r"], ["h1"], "residual"))
+        h = "h1"
+    nodes += _ln(h, "y", "1")
+    ins = [("x", np.float32, x.shape)] + ([("r", np.float32, r.shape)] if residual else [])
+    dev_in = {"x": dev(x), "r": dev(r)} if residual else {"x": dev(x)}
+    pre = HIP.MatMulAdd(dev(x), dev(w), dev(b), dev(r) if residual else None)
+    assert pre.Status == OpStatus.Success, pre.Message
+    ln = HIP.LayerNormDecomposed(pre.Outputs[0], dev(gamma), dev(beta), 1e-12)
+    assert ln.Status == OpStatus.Success, ln.Message
+    ref = ln.Outputs[0].to_numpy()
+    for mode in ("fused", "captured"):
+        g = Model.Load(W.model(nodes, ins, [("y", np.float32, ())], inits))
+        assert g.Fuse() == 1 and [nd.Op for nd in g.Nodes] == ["MatMulAddLayerNorm"]
+        ok = (g.Capture(dev_in) and g.Replay()) if mode == "captured" else g.Execute(dev_in)
+        assert ok, g.LastError
+        got = g.Output("y").to_numpy()
+        assert got.shape == ref.shape and np.array_equal(got.view(np.uint32), ref.view(np.uint32)), mode
