@@ -624,55 +624,108 @@ static void launch_f32(const float *a, const float *b, float *c, const MatMulArg
 // ---------------------------------------------------------------------------
 // double: MFMA 16x16x4
 // ---------------------------------------------------------------------------
-constexpr int kDBM = 64, kDBN = 64, kDBK = 16, kDPad = 2;
+// BM x BN block tile, four waves in a 2 x 2 grid, each (BM / 2) x (BN / 2) = MT x NT MFMA tiles of 16x16.  K steps
+// of 16, double-buffered in LDS with k as the outer index (A transposed to [k][m], B as [k][n]), fed from
+// registers one step ahead; VEC: 16-byte loads (k, n, the row and batch strides even, the operands 16-byte
+// aligned).  Each dot product is summed in K order, four products per MFMA.
+constexpr int kDBK = 16, kDPad = 2;
 
+template <int BM, int BN, bool VEC>
 __global__ __launch_bounds__(256) void k_matmul_f64(const double *__restrict__ A, const double *__restrict__ B,
                                                     double *__restrict__ C, MatMulArgs p) {
-    __shared__ double As[kDBK][kDBM + kDPad];
-    __shared__ double Bs[kDBK][kDBN + kDPad];
+    constexpr int WTM = BM / 2, WTN = BN / 2, MT = WTM / 16, NT = WTN / 16;
+    constexpr int AV = BM * kDBK / 2, BV = BN * kDBK / 2;  // 16-byte pairs of A and of B per K step
+    static_assert(AV % 256 == 0 && BV % 256 == 0 && MT * 16 == WTM && NT * 16 == WTN, "whole tiles and loads");
+    constexpr int LA = AV / 256, LB = BV / 256;
+    constexpr int KQ = kDBK / 2, BQ = BN / 2;              // pairs per A row and per B row of a step
+    __shared__ double As[2][kDBK][BM + kDPad];
+    __shared__ double Bs[2][kDBK][BN + kDPad];
     const int M = p.m, N = p.n, K = p.k;
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
-    const int row0 = blockIdx.y * kDBM, col0 = blockIdx.x * kDBN;
+    const int row0 = blockIdx.y * BM, col0 = blockIdx.x * BN;
     int64_t ao, bo, co;
     batch_offsets(p.batch_base + blockIdx.z, p, &ao, &bo, &co);
     const double *Ab = A + ao;
     const double *Bb = B + bo;
     double *Cb = C + co;
-    const int wr = (w >> 1) * 32, wc = (w & 1) * 32;
-    v4d acc[2][2];
+    const int64_t lda = p.lda, ldb = p.ldb;
+    double2 ra[LA], rb[LB];
+    auto load = [&](int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+        for (int h = 0; h < LA; h++) {
+            const int e = t + 256 * h;
+            const int r = row0 + e / KQ, kk = k0 + (e % KQ) * 2;
+            if constexpr (VEC) {
+                ra[h] = (r < M && kk < K) ? *reinterpret_cast<const double2 *>(Ab + (int64_t)r * lda + kk)
+                                          : make_double2(0.0, 0.0);
+            } else {
+                ra[h].x = (r < M && kk < K) ? Ab[(int64_t)r * lda + kk] : 0.0;
+                ra[h].y = (r < M && kk + 1 < K) ? Ab[(int64_t)r * lda + kk + 1] : 0.0;
+            }
+        }
 #pragma unroll
-        for (int j = 0; j < 2; j++)
+        for (int h = 0; h < LB; h++) {
+            const int e = t + 256 * h;
+            const int kb = k0 + e / BQ, c = col0 + (e % BQ) * 2;
+            if constexpr (VEC) {
+                rb[h] = (kb < K && c < N) ? *reinterpret_cast<const double2 *>(Bb + (int64_t)kb * ldb + c)
+                                          : make_double2(0.0, 0.0);
+            } else {
+                rb[h].x = (kb < K && c < N) ? Bb[(int64_t)kb * ldb + c] : 0.0;
+                rb[h].y = (kb < K && c + 1 < N) ? Bb[(int64_t)kb * ldb + c + 1] : 0.0;
+            }
+        }
+    };
+    auto store = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < LA; h++) {
+            const int e = t + 256 * h;
+            const int r = e / KQ, kk = (e % KQ) * 2;
+            As[buf][kk][r] = ra[h].x;
+            As[buf][kk + 1][r] = ra[h].y;
+        }
+#pragma unroll
+        for (int h = 0; h < LB; h++) {
+            const int e = t + 256 * h;
+            *reinterpret_cast<double2 *>(&Bs[buf][e / BQ][(e % BQ) * 2]) = rb[h];
+        }
+    };
+    const int wr = (w >> 1) * WTM, wc = (w & 1) * WTN;
+    v4d acc[MT][NT];
+#pragma unroll
+    for (int i = 0; i < MT; i++)
+#pragma unroll
+        for (int j = 0; j < NT; j++)
 #pragma unroll
             for (int r = 0; r < 4; r++) acc[i][j][r] = 0.0;
-    for (int k0 = 0; k0 < K; k0 += kDBK) {
-        // 64x16 A and 16x64 B tiles: four elements of each per thread
-#pragma unroll
-        for (int h = 0; h < 4; h++) {
-            const int e = t + 256 * h;
-            const int ar = e / kDBK, ak = e % kDBK;
-            As[ak][ar] = (row0 + ar < M && k0 + ak < K) ? Ab[(int64_t)(row0 + ar) * p.lda + k0 + ak] : 0.0;
-            const int bk = e / kDBN, bc = e % kDBN;
-            Bs[bk][bc] = (k0 + bk < K && col0 + bc < N) ? Bb[(int64_t)(k0 + bk) * p.ldb + col0 + bc] : 0.0;
-        }
-        __syncthreads();
+    const int nk = (K + kDBK - 1) / kDBK;
+    load(0);
+    store(0);
+    __syncthreads();
+    int buf = 0;
+    for (int kt = 0; kt < nk; kt++) {
+        if (kt + 1 < nk) load((kt + 1) * kDBK);
 #pragma unroll
         for (int kk = 0; kk < kDBK; kk += 4) {
             const int kr = kk + l / 16;
-            double a0 = As[kr][wr + (l % 16)], a1 = As[kr][wr + 16 + (l % 16)];
-            double b0 = Bs[kr][wc + (l % 16)], b1 = Bs[kr][wc + 16 + (l % 16)];
-            acc[0][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc[1][1], 0, 0, 0);
+            double a[MT], b[NT];
+#pragma unroll
+            for (int i = 0; i < MT; i++) a[i] = As[buf][kr][wr + 16 * i + (l % 16)];
+#pragma unroll
+            for (int j = 0; j < NT; j++) b[j] = Bs[buf][kr][wc + 16 * j + (l % 16)];
+#pragma unroll
+            for (int i = 0; i < MT; i++)
+#pragma unroll
+                for (int j = 0; j < NT; j++) acc[i][j] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[i], b[j], acc[i][j], 0, 0, 0);
         }
+        if (kt + 1 < nk) store(buf ^ 1);
         __syncthreads();
+        buf ^= 1;
     }
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < NT; j++) {
             const int c = col0 + wc + 16 * j + (l % 16);
             if (c >= N) continue;
 #pragma unroll
@@ -681,6 +734,16 @@ __global__ __launch_bounds__(256) void k_matmul_f64(const double *__restrict__ A
                 if (row < M) Cb[(int64_t)row * p.ldc + c] = acc[i][j][r];
             }
         }
+}
+
+template <int BM, int BN>
+static void launch_f64(const double *a, const double *b, double *c, const MatMulArgs &p, hipStream_t s) {
+    bool vec = p.k % 2 == 0 && p.n % 2 == 0 && p.lda % 2 == 0 && p.ldb % 2 == 0 &&
+               (((uintptr_t)a | (uintptr_t)b) % 16 == 0);
+    for (int d = 0; d < p.nbatch; d++) vec = vec && p.a_bstr[d] % 2 == 0 && p.b_bstr[d] % 2 == 0;
+    const dim3 g((p.n + BN - 1) / BN, (p.m + BM - 1) / BM, (unsigned)p.batch);
+    if (vec) hipLaunchKernelGGL((k_matmul_f64<BM, BN, true>), g, dim3(256), 0, s, a, b, c, p);
+    else hipLaunchKernelGGL((k_matmul_f64<BM, BN, false>), g, dim3(256), 0, s, a, b, c, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -925,8 +988,12 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         default: launch_f32<64, 64, 2, 2>(fa, fb, fc, p, vec, s); break;
         }
     } else if (dtype == kDouble) {
-        dim3 g((p.n + kDBN - 1) / kDBN, (p.m + kDBM - 1) / kDBM, (unsigned)p.batch);
-        hipLaunchKernelGGL(k_matmul_f64, g, dim3(256), 0, s, (const double *)a, (const double *)b, (double *)c, p);
+        // 128x128 tiles where they give every CU a block, else 64x64
+        const double *da = (const double *)a, *db = (const double *)b;
+        double *dc = (double *)c;
+        const int64_t t128 = (((int64_t)p.m + 127) / 128) * (((int64_t)p.n + 127) / 128) * p.batch;
+        if (t128 >= 256) launch_f64<128, 128>(da, db, dc, p, s);
+        else launch_f64<64, 64>(da, db, dc, p, s);
     } else if (dtype == kInt32) {
         dim3 g((p.n + 15) / 16, (p.m + 15) / 16, (unsigned)p.batch);
         hipLaunchKernelGGL(k_matmul_i32, g, dim3(256), 0, s, (const int32_t *)a, (const int32_t *)b, (int32_t *)c, p);
