@@ -1704,19 +1704,24 @@ struct MatMulEpilogue {
     bool gelu = false;  // then the GELU subgraph on each result (lx_MatMulAddGelu)
     bool applied = false;
 };
-thread_local MatMulEpilogue *t_mm_epi = nullptr;
-thread_local bool t_mm_per_matrix = false;  // api_matmul_add_grouped in progress
-thread_local const int *t_mm_yperm = nullptr;  // api_matmul_permuted in progress: the product's permutation
-thread_local bool t_mm_allow_bt = false;        // api_matmul_permuted in progress: B may be stored by columns
-
-// api_matmul_add_layernorm in progress: the LayerNorm that follows the product (and its epilogue), applied by the
-// split product's ordered sum when the product splits (`applied` tells the caller)
+// The LayerNorm that follows the product (and its epilogue), applied by the split product's ordered sum when the
+// product splits (api_matmul_add_layernorm); `applied` tells the caller
 struct MatMulLayerNorm {
     const lx_tensor *gamma = nullptr, *beta = nullptr;
     float eps = 0.0f;
     bool applied = false;
 };
-thread_local MatMulLayerNorm *t_mm_ln = nullptr;
+
+// What a MatMul call asks beyond A x B, passed down explicitly: the epilogue's Adds (and GELU), the LayerNorm
+// after them, the split rule counting one matrix's tiles (grouped projections), the product stored transposed
+// and a right operand read by columns (the graph's transposed views)
+struct MatMulOpts {
+    MatMulEpilogue *epi = nullptr;
+    MatMulLayerNorm *ln = nullptr;
+    bool per_matrix = false;
+    const int *yperm = nullptr;
+    bool allow_bt = false;
+};
 
 // a permutation of 0 .. rank - 1 that keeps the last axis last
 bool last_axis_perm(const int *perm, int rank) {
@@ -1754,12 +1759,14 @@ bool epilogue_fits(const MatMulEpilogue &e, int out_rank, const int64_t *out_dim
 }
 
 int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, lx_tensor *Y,
-               std::vector<void *> &temps) {
+               std::vector<void *> &temps, const MatMulOpts &o) {
+    MatMulEpilogue *const epi = o.epi;
+    MatMulLayerNorm *const ln = o.ln;
     int st;
-    if ((st = densify(dt, &x, temps)) || (st = densify(dt, &y, temps, t_mm_allow_bt && dt == LX_FLOAT))) return st;
-    // the product's element strides in Y: dense, or Y = transpose(product, t_mm_yperm)
+    if ((st = densify(dt, &x, temps)) || (st = densify(dt, &y, temps, o.allow_bt && dt == LX_FLOAT))) return st;
+    // the product's element strides in Y: dense, or Y = transpose(product, o.yperm)
     int64_t pstr[LX_MAX_RANK];
-    const int *yp = t_mm_yperm;
+    const int *yp = o.yperm;
     if (yp) {
         if (out_rank < 2 || !last_axis_perm(yp, out_rank)) return LX_ERR_NOT_SUPPORTED;
         int64_t yd[LX_MAX_RANK];
@@ -1781,13 +1788,13 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     MatMulArgs p;
     memset(&p, 0, sizeof p);
     int64_t bias_bstr = 0;
-    if (t_mm_epi && !yp && dt == LX_FLOAT && epilogue_fits(*t_mm_epi, out_rank, out_dims, &bias_bstr)) {
-        p.bias = t_mm_epi->bias ? (const float *)t_mm_epi->bias->data : nullptr;
+    if (epi && !yp && dt == LX_FLOAT && epilogue_fits(*epi, out_rank, out_dims, &bias_bstr)) {
+        p.bias = epi->bias ? (const float *)epi->bias->data : nullptr;
         p.bias_bstr = bias_bstr;
-        p.res = t_mm_epi->res ? (const float *)t_mm_epi->res->data : nullptr;
-        p.gelu = t_mm_epi->gelu ? 1 : 0;
+        p.res = epi->res ? (const float *)epi->res->data : nullptr;
+        p.gelu = epi->gelu ? 1 : 0;
     }
-    p.split_per_matrix = t_mm_per_matrix ? 1 : 0;
+    p.split_per_matrix = o.per_matrix ? 1 : 0;
     p.m = (int32_t)x.dims[x.rank - 2];
     p.k = (int32_t)x.dims[x.rank - 1];
     p.n = (int32_t)y.dims[y.rank - 1];
@@ -1843,19 +1850,19 @@ int matmul_run(int dt, MView x, MView y, int out_rank, const int64_t *out_dims, 
     }
     // the LayerNorm after the product, in its ordered sum: every requested Add in the epilogue, the rows the
     // row-per-wave LayerNorm kernel takes, gamma and beta rows of the output's last axis
-    if (t_mm_ln && !yp && (!t_mm_epi || ((!t_mm_epi->bias || p.bias) && (!t_mm_epi->res || p.res))) &&
-        matmul_ln_fusable(dt, x.data, y.data, Y->data, p) && t_mm_ln->gamma->dtype == LX_FLOAT &&
-        t_mm_ln->beta->dtype == LX_FLOAT && layernorm_affine_fits(t_mm_ln->gamma, Y) &&
-        layernorm_affine_fits(t_mm_ln->beta, Y) && aligned16(t_mm_ln->gamma->data) && aligned16(t_mm_ln->beta->data)) {
-        HIPCHECK(launch_matmul_ln(x.data, y.data, Y->data, p, (const float *)t_mm_ln->gamma->data,
-                                  (const float *)t_mm_ln->beta->data, t_mm_ln->eps, g.stream),
+    if (ln && !yp && (!epi || ((!epi->bias || p.bias) && (!epi->res || p.res))) &&
+        matmul_ln_fusable(dt, x.data, y.data, Y->data, p) && ln->gamma->dtype == LX_FLOAT &&
+        ln->beta->dtype == LX_FLOAT && layernorm_affine_fits(ln->gamma, Y) && layernorm_affine_fits(ln->beta, Y) &&
+        aligned16(ln->gamma->data) && aligned16(ln->beta->data)) {
+        HIPCHECK(launch_matmul_ln(x.data, y.data, Y->data, p, (const float *)ln->gamma->data,
+                                  (const float *)ln->beta->data, ln->eps, g.stream),
                  "MatMul");
-        t_mm_ln->applied = true;
-        if (t_mm_epi && (p.bias || p.res)) t_mm_epi->applied = true;
+        ln->applied = true;
+        if (epi && (p.bias || p.res)) epi->applied = true;
         return LX_OK;
     }
     HIPCHECK(launch_matmul(dt, x.data, y.data, Y->data, p, g.stream), "MatMul");
-    if (t_mm_epi && (p.bias || p.res || p.gelu)) t_mm_epi->applied = true;
+    if (epi && (p.bias || p.res || p.gelu)) epi->applied = true;
     return LX_OK;
 }
 
@@ -1867,13 +1874,14 @@ int cols_rows_error(int64_t cols, int64_t rows) {
 }
 
 // Tensor<T>.MatMul (TensorOps.cs:600-705)
-int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vector<void *> &temps) {
+int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vector<void *> &temps,
+                 const MatMulOpts &o) {
     if (x.rank == 0 || y.rank == 0)
         return set_err(LX_ERR_INVALID_ARGUMENT, "The rank of each tensor in matrix multiplication must be greater than 1.");
     if (x.rank == 2 && y.rank == 2) {  // MatMul2D (TensorOps.cs:356-407)
         if (x.dims[1] != y.dims[0]) return cols_rows_error(x.dims[1], y.dims[0]);
         int64_t od[2] = {x.dims[0], y.dims[1]};
-        return matmul_run(dt, x, y, 2, od, Y, temps);
+        return matmul_run(dt, x, y, 2, od, Y, temps, o);
     }
     if (x.rank >= 2 && y.rank >= 2) {
         const int64_t xm = x.dims[x.rank - 2], xk = x.dims[x.rank - 1];
@@ -1891,7 +1899,7 @@ int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vect
         od[br] = xm; od[br + 1] = yn;
         if (!broadcast_view(x, br + 2, dx, &bx) || !broadcast_view(y, br + 2, dy, &by))
             return set_err(LX_ERR_INVALID_ARGUMENT, "The tensor shapes are not compatible for broadcasting.");
-        return matmul_run(dt, bx, by, br + 2, od, Y, temps);
+        return matmul_run(dt, bx, by, br + 2, od, Y, temps, o);
     }
     if (x.rank >= 2 || y.rank >= 2) {  // one operand of rank 1: element-wise broadcast of both, then MatMul
         int r;
@@ -1901,7 +1909,7 @@ int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vect
             !broadcast_view(y, r, bd, &by))
             return set_err(LX_ERR_INVALID_ARGUMENT, "The shapes %s and %s are not compatible for broadcasting.",
                            shape_str(x).c_str(), shape_str(y).c_str());
-        return matmul_views(dt, bx, by, Y, temps);
+        return matmul_views(dt, bx, by, Y, temps, o);
     }
     // both rank 1: [1,n] x [n,1] -> [1,1], then RemoveDim(0) -> [1]
     MView px, py;
@@ -1909,13 +1917,11 @@ int matmul_views(int dt, const MView &x, const MView &y, lx_tensor *Y, std::vect
     py.rank = 2; py.dims[0] = y.dims[0]; py.dims[1] = 1; py.str[0] = y.str[0]; py.str[1] = 1; py.data = y.data;
     if (px.dims[1] != py.dims[0]) return cols_rows_error(px.dims[1], py.dims[0]);
     int64_t od[1] = {1};
-    return matmul_run(dt, px, py, 1, od, Y, temps);
+    return matmul_run(dt, px, py, 1, od, Y, temps, o);
 }
 
-}  // namespace
-
-extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
-    OpScope prof("MatMul");
+// lx_MatMul's checks and product, with the options of the caller
+int matmul_call(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y, const MatMulOpts &o) {
     REQUIRE_INIT();
     if (!A) return missing_input("MatMul", "A");
     if (!B) return missing_input("MatMul", "B");
@@ -1928,9 +1934,16 @@ extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
                                                 "'Lokad.Onnx.Tensor`1[%s]'.",
                        net_type(B->dtype), net_type(A->dtype));
     std::vector<void *> temps;
-    st = matmul_views(A->dtype, dense_view(A), dense_view(B), Y, temps);
+    st = matmul_views(A->dtype, dense_view(A), dense_view(B), Y, temps, o);
     for (void *t : temps) (void)pool_release(t);
     return st;
+}
+
+}  // namespace
+
+extern "C" int lx_MatMul(const lx_tensor *A, const lx_tensor *B, lx_tensor *Y) {
+    OpScope prof("MatMul");
+    return matmul_call(A, B, Y, MatMulOpts{});
 }
 
 namespace lx {
@@ -1958,11 +1971,10 @@ int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *
     };
     if (!permute(x, a_perm, false) || !permute(y, b_perm, true)) return LX_ERR_NOT_SUPPORTED;
     std::vector<void *> temps;
-    t_mm_yperm = y_perm;
-    t_mm_allow_bt = true;
-    const int st = matmul_views(LX_FLOAT, x, y, Y, temps);
-    t_mm_yperm = nullptr;
-    t_mm_allow_bt = false;
+    MatMulOpts o;
+    o.yperm = y_perm;
+    o.allow_bt = true;
+    const int st = matmul_views(LX_FLOAT, x, y, Y, temps, o);
     for (void *t : temps) (void)pool_release(t);
     return st;
 }
@@ -1972,7 +1984,7 @@ int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *
 // (Float), else the MatMul and then each node's operator, into new tensors (an Add may broadcast to a larger
 // shape than the product's)
 int matmul_add_run(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias, const lx_tensor *residual,
-                   bool gelu, lx_tensor *Y) {
+                   bool gelu, lx_tensor *Y, MatMulOpts o = MatMulOpts{}) {
     REQUIRE_INIT();
     if (!bias) return missing_input("Add", "B");
     int st;
@@ -1983,10 +1995,9 @@ int matmul_add_run(const lx_tensor *A, const lx_tensor *B, const lx_tensor *bias
     epi.bias = bias;
     epi.res = residual;
     epi.gelu = gelu;
-    t_mm_epi = &epi;
+    o.epi = &epi;
     lx_tensor c = caller_storage ? *Y : lx_tensor{};
-    st = lx_MatMul(A, B, caller_storage ? &c : Y);
-    t_mm_epi = nullptr;
+    st = matmul_call(A, B, caller_storage ? &c : Y, o);
     if (st) return st;
     if (epi.applied) {
         if (caller_storage) *Y = c;
@@ -2033,10 +2044,10 @@ int api_matmul_add_layernorm(const lx_tensor *A, const lx_tensor *W, const lx_te
     ln.gamma = gamma;
     ln.beta = beta;
     ln.eps = eps;
-    t_mm_ln = &ln;
+    MatMulOpts o;
+    o.ln = &ln;
     lx_tensor h{};
-    int st = matmul_add_run(A, W, bias, residual, false, &h);
-    t_mm_ln = nullptr;
+    int st = matmul_add_run(A, W, bias, residual, false, &h, o);
     if (!st && ln.applied) {
         *Y = h;
         return LX_OK;
@@ -2048,10 +2059,9 @@ int api_matmul_add_layernorm(const lx_tensor *A, const lx_tensor *W, const lx_te
 
 int api_matmul_add_grouped(const lx_tensor *A, const lx_tensor *W, const lx_tensor *bias, lx_tensor *Y) {
     if (!W || W->rank != 3 || W->dims[0] > kMatMulSplitBatch) return LX_ERR_NOT_SUPPORTED;
-    t_mm_per_matrix = true;
-    const int st = lx_MatMulAdd(A, W, bias, nullptr, Y);
-    t_mm_per_matrix = false;
-    return st;
+    MatMulOpts o;
+    o.per_matrix = true;
+    return matmul_add_run(A, W, bias, nullptr, false, Y, o);
 }
 }  // namespace lx
 
