@@ -988,12 +988,13 @@ hipError_t launch_matmul(int dtype, const void *a, const void *b, void *c, const
         default: launch_f32<64, 64, 2, 2>(fa, fb, fc, p, vec, s); break;
         }
     } else if (dtype == kDouble) {
-        // 128x128 tiles where they give every CU a block, else 64x64
+        // the largest of 128x128, 64x64 and 32x32 tiles that gives every CU a block
         const double *da = (const double *)a, *db = (const double *)b;
         double *dc = (double *)c;
-        const int64_t t128 = (((int64_t)p.m + 127) / 128) * (((int64_t)p.n + 127) / 128) * p.batch;
-        if (t128 >= 256) launch_f64<128, 128>(da, db, dc, p, s);
-        else launch_f64<64, 64>(da, db, dc, p, s);
+        auto tiles = [&](int t) { return (((int64_t)p.m + t - 1) / t) * (((int64_t)p.n + t - 1) / t) * p.batch; };
+        if (tiles(128) >= 256) launch_f64<128, 128>(da, db, dc, p, s);
+        else if (tiles(64) >= 256) launch_f64<64, 64>(da, db, dc, p, s);
+        else launch_f64<32, 32>(da, db, dc, p, s);
     } else if (dtype == kInt32) {
         dim3 g((p.n + 15) / 16, (p.m + 15) / 16, (unsigned)p.batch);
         hipLaunchKernelGGL(k_matmul_i32, g, dim3(256), 0, s, (const int32_t *)a, (const int32_t *)b, (int32_t *)c, p);

@@ -181,10 +181,11 @@ def test_batch_fold_at_the_grid_limit(hip, batch):
 
 @pytest.mark.parametrize("sa,sb", [((5, 6), (6, 5)), ((3, 70, 33), (33, 65)), ((2, 1, 40, 17), (3, 17, 66)),
                                    ((300, 130), (130, 260)), ((1000, 512), (512, 700)), ((4096, 256), (256, 1030)),
-                                   ((2, 1, 700, 96), (3, 96, 900)), ((257, 33), (33, 129)), ((2048, 33), (33, 2049))])
+                                   ((2, 1, 700, 96), (3, 96, 900)), ((257, 33), (33, 129)), ((2048, 33), (33, 2049)),
+                                   ((1024, 64), (64, 1030))])
 def test_double(hip, sa, sb):
-    """Double: 128x128 tiles (from 256 of them) and 64x64, 16-byte and scalar loads (odd K or N), ragged edges,
-    broadcast batches."""
+    """Double: 128x128, 64x64 and 32x32 tiles (the largest that gives 256 of them), 16-byte and scalar loads (odd K
+    or N), ragged edges, broadcast batches."""
     rng = np.random.default_rng(52)
     check_float(rng.standard_normal(sa), rng.standard_normal(sb), 1e-13)
 
