@@ -201,7 +201,8 @@ def lib():
 
 def last_error():
     m = lib().lx_last_error()
-    return m.decode() if m else ""
+    # messages are cut at 1023 bytes, which can split a multi-byte character of a name
+    return m.decode(errors="replace") if m else ""
 
 
 def dims_array(shape):

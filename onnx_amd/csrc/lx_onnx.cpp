@@ -28,6 +28,29 @@ std::string fmt(const char *f, ...) {
     return buf;
 }
 
+// Well-formed UTF-8 (RFC 3629): no overlong forms, no surrogates, nothing above U+10FFFF.
+bool utf8_valid(const std::string &s) {
+    const uint8_t *p = (const uint8_t *)s.data(), *e = p + s.size();
+    while (p < e) {
+        uint8_t c = *p++;
+        if (c < 0x80) continue;
+        int n;
+        uint32_t cp, lo;
+        if (c >= 0xc2 && c <= 0xdf) { n = 1; cp = c & 0x1f; lo = 0x80; }
+        else if (c >= 0xe0 && c <= 0xef) { n = 2; cp = c & 0x0f; lo = 0x800; }
+        else if (c >= 0xf0 && c <= 0xf4) { n = 3; cp = c & 0x07; lo = 0x10000; }
+        else return false;
+        if (e - p < n) return false;
+        for (int i = 0; i < n; i++) {
+            if ((p[i] & 0xc0) != 0x80) return false;
+            cp = (cp << 6) | (p[i] & 0x3f);
+        }
+        p += n;
+        if (cp < lo || cp > 0x10ffff || (cp >= 0xd800 && cp <= 0xdfff)) return false;
+    }
+    return true;
+}
+
 // ---- protobuf wire format -------------------------------------------------------
 enum { kVarint = 0, kFixed64 = 1, kLen = 2, kFixed32 = 5 };
 
@@ -64,6 +87,13 @@ struct Reader {
     std::string str() {
         Reader r = sub();
         return std::string((const char *)r.p, (size_t)(r.e - r.p));
+    }
+    // a field of protobuf type string (names, op types, domains) holds UTF-8 text; other bytes
+    // make the message malformed
+    std::string text() {
+        std::string s = str();
+        if (!utf8_valid(s)) ok = false;
+        return s;
     }
     uint32_t fixed32() {
         if (e - p < 4) { ok = false; return 0; }
@@ -136,7 +166,7 @@ int parse_tensor(Reader r, HostTensor *h, std::string *name) {
         case 4: read_fixed32s(r, wt, &f32); break;   // float_data
         case 5: read_varints(r, wt, &i64); break;    // int32_data
         case 7: read_varints(r, wt, &i64); break;    // int64_data
-        case 8: *name = r.str(); break;
+        case 8: *name = r.text(); break;
         case 9: raw = r.str(); break;                // raw_data
         case 10: read_fixed64s(r, wt, &f64); break;  // double_data
         default: r.skip(wt);
@@ -189,7 +219,7 @@ int parse_value_info(Reader r, GInput *v) {
     uint32_t f, wt;
     bool tensor_type = false;
     while (r.more() && r.key(&f, &wt)) {
-        if (f == 1) { v->name = r.str(); continue; }
+        if (f == 1) { v->name = r.text(); continue; }
         if (f != 2) { r.skip(wt); continue; }
         Reader tp = r.sub();  // TypeProto
         uint32_t f2, w2;
@@ -243,7 +273,7 @@ int parse_attr(Reader r, std::string *name, Attr *a) {
     uint32_t f, wt;
     while (r.more() && r.key(&f, &wt)) {
         switch (f) {
-        case 1: *name = r.str(); break;
+        case 1: *name = r.text(); break;
         case 2: { uint32_t u = r.fixed32(); memcpy(&fv, &u, 4); break; }
         case 3: iv = (int64_t)r.varint(); break;
         case 4: sv = r.str(); break;
@@ -289,10 +319,10 @@ int parse_node(Reader r, GNode *n) {
     uint32_t f, wt;
     while (r.more() && r.key(&f, &wt)) {
         switch (f) {
-        case 1: n->in.push_back(r.str()); break;
-        case 2: n->out.push_back(r.str()); break;
-        case 3: n->name = r.str(); break;
-        case 4: n->op = r.str(); break;
+        case 1: n->in.push_back(r.text()); break;
+        case 2: n->out.push_back(r.text()); break;
+        case 3: n->name = r.text(); break;
+        case 4: n->op = r.text(); break;
         case 5: {
             std::string an;
             Attr a;
@@ -322,7 +352,7 @@ int parse_graph(Reader r, lx_graph *g) {
             }
             break;
         }
-        case 2: g->name = r.str(); break;
+        case 2: g->name = r.text(); break;
         case 5: {
             auto h = std::make_shared<HostTensor>();
             std::string name;
@@ -368,7 +398,7 @@ extern "C" int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **
             int64_t version = 0;
             uint32_t f2, w2;
             while (o.more() && o.key(&f2, &w2)) {
-                if (f2 == 1) domain = o.str();
+                if (f2 == 1) domain = o.text();
                 else if (f2 == 2) version = (int64_t)o.varint();
                 else o.skip(w2);
             }

@@ -108,6 +108,29 @@ def test_loader_error_statuses():
     assert L.last_error() == "Cannot convert attribute proto value of type Graph."
 
 
+@pytest.mark.parametrize("name,ok", [(b"caf\xc3\xa9", True), ("节\U0001f600".encode(), True),
+                                     (b"\xc3", False),              # cut short
+                                     (b"\xc0\x80", False),          # overlong NUL
+                                     (b"\xed\xa0\x80", False),      # a UTF-16 surrogate
+                                     (b"\xf4\x90\x80\x80", False),  # above U+10FFFF
+                                     (b"a\xffb", False)])
+def test_loader_names_must_be_utf8(name, ok):
+    """Names are protobuf string fields, which hold UTF-8 text; other bytes make the model malformed."""
+    lib = L.lib()
+    import ctypes
+    h = ctypes.c_void_p()
+    nd = W.f_bytes(1, "x") + W.f_bytes(2, "y") + W.f_bytes(3, name) + W.f_bytes(4, "Sqrt")
+    buf = W.model([nd], [("x", np.float32, (2,))], [("y", np.float32, (2,))])
+    st = lib.lx_graph_load_onnx(buf, len(buf), ctypes.byref(h))
+    if ok:
+        assert st == L.OK
+        g = ComputationalGraph(_handle=h)
+        assert [n.Name for n in g.Nodes] == [name.decode()]
+    else:
+        assert st == L.ERR_INVALID_ARGUMENT
+        assert L.last_error() == "Malformed ONNX model: node."
+
+
 # ---- fusion ---------------------------------------------------------------------
 def gelu_nodes(x="x", y="y", half="half", extra=()):
     return [W.node("Div", [x, "sqrt2"], ["a"], "div"), W.node("Erf", ["a"], ["e"], "erf"),
