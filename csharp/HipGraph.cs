@@ -96,6 +96,7 @@ public sealed unsafe class HipGraph : IDisposable
         "LayerNormDecomposed" => OpType.ReduceMean,
         "MatMulAddLayerNorm" => OpType.MatMul,
         "AddSoftmax" or "ScaleAddSoftmax" => OpType.Softmax,
+        "Attention" => OpType.MatMul,
         "MatMulAdd" or "MatMulAddGroup" or "MatMulAddGelu" or "MatMulPermuted" => OpType.MatMul,
         _ => OpType.Add,   // ElementwiseChain
     };

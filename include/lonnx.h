@@ -304,8 +304,10 @@ int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
  * (read or written as strided views) by the fused kernels when every intermediate has exactly one
  * consumer and is not a graph output; then every linear chain of two or more Float elementwise nodes
  * (Add/Sub/Mul/Div/Pow/Sqrt/Erf) whose intermediates have one consumer by an ElementwiseChain node
- * (lx_ElementwiseChain); then the MatMul -> Add projections of one input as one grouped launch, and a
- * projection whose result only a decomposed LayerNorm reads with that LayerNorm.
+ * (lx_ElementwiseChain); then the MatMul -> Add projections of one input as one grouped launch, a
+ * projection whose result only a decomposed LayerNorm reads with that LayerNorm, and an attention layer's
+ * scores MatMul -> (scaled) masked Softmax -> context MatMul as one launch per execution where every head has
+ * at most 64 rows, keys and columns.
  * Results equal the unfused graph's bit for bit where the fused kernels' are stated to.
  * *n_fused = number of fused nodes made. */
 int lx_graph_fuse(lx_graph *g, int32_t *n_fused);

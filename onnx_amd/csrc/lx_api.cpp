@@ -1978,6 +1978,109 @@ int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *
     for (void *t : temps) (void)pool_release(t);
     return st;
 }
+
+int api_attention(const lx_tensor *Q, const int *q_perm, const lx_tensor *K, const int *k_perm,
+                  const lx_tensor *scale, int scale_div, const lx_tensor *mask, int32_t axis, const lx_tensor *V,
+                  const int *v_perm, const int *y_perm, lx_tensor *Y) {
+    if (!api_initialized() || !Q || !K || !V || !mask || !Y) return LX_ERR_NOT_SUPPORTED;
+    for (const lx_tensor *t : {Q, K, V, mask, scale})
+        if (t && (t->dtype != LX_FLOAT || check_tensor(t, "input"))) return LX_ERR_NOT_SUPPORTED;
+    const int R = Q->rank;
+    if (R < 2 || R - 2 > kMaxOuter || K->rank != R || V->rank != R) return LX_ERR_NOT_SUPPORTED;
+    auto is_perm = [R](const int *p) {
+        if (!p) return true;
+        bool seen[LX_MAX_RANK] = {false};
+        for (int i = 0; i < R; i++) {
+            if (p[i] < 0 || p[i] >= R || seen[p[i]]) return false;
+            seen[p[i]] = true;
+        }
+        return true;
+    };
+    if (!is_perm(q_perm) || !is_perm(k_perm) || !is_perm(v_perm) || !is_perm(y_perm)) return LX_ERR_NOT_SUPPORTED;
+    // the operand views of the two products (a transposed view reads through its strides, as MatMulPermuted does)
+    MView q = dense_view(Q), k = dense_view(K), v = dense_view(V);
+    auto permute = [R](MView &m, const int *perm) {
+        if (!perm) return;
+        const MView o = m;
+        for (int i = 0; i < R; i++) {
+            m.dims[i] = o.dims[perm[i]];
+            m.str[i] = o.str[perm[i]];
+        }
+    };
+    permute(q, q_perm);
+    permute(k, k_perm);
+    permute(v, v_perm);
+    // equal batch axes (no broadcast), heads of at most kAttentionMax: [.., S, D] x [.., D, SK] and [.., S, SK] x
+    // [.., SK, DV]; otherwise the nodes run (and report any shape error)
+    for (int i = 0; i < R - 2; i++)
+        if (k.dims[i] != q.dims[i] || v.dims[i] != q.dims[i]) return LX_ERR_NOT_SUPPORTED;
+    const int64_t S = q.dims[R - 2], D = q.dims[R - 1], SK = k.dims[R - 1], DV = v.dims[R - 1];
+    if (k.dims[R - 2] != D || v.dims[R - 2] != SK) return LX_ERR_NOT_SUPPORTED;
+    for (int64_t e : {S, D, SK, DV})
+        if (e < 1 || e > kAttentionMax) return LX_ERR_NOT_SUPPORTED;
+    int64_t batch = 1;
+    for (int i = 0; i < R - 2; i++) batch *= q.dims[i];
+    if (batch < 1 || batch > 0x7fffffff) return LX_ERR_NOT_SUPPORTED;
+    // the Softmax over the scores' last axis with the scale and mask in its kernel, as run_softmax takes them
+    int64_t sdims[LX_MAX_RANK];
+    for (int i = 0; i < R - 2; i++) sdims[i] = q.dims[i];
+    sdims[R - 2] = S;
+    sdims[R - 1] = SK;
+    if ((axis < 0 ? axis + R : axis) != R - 1) return LX_ERR_NOT_SUPPORTED;
+    if (scale && (numel(scale) != 1 || scale->rank > R)) return LX_ERR_NOT_SUPPORTED;
+    lx_bcast_plan bp;
+    if (plan(R, sdims, mask->rank, mask->dims, &bp) != LX_OK || bp.out_rank != R) return LX_ERR_NOT_SUPPORTED;
+    for (int i = 0; i < R; i++)
+        if (bp.out_dims[i] != sdims[i]) return LX_ERR_NOT_SUPPORTED;
+    SoftmaxArgs sa;
+    memset(&sa, 0, sizeof sa);
+    sa.dtype = LX_FLOAT;
+    if (!softmax_mask_fusable(LX_FLOAT, SK, 1, batch * S, 4) || !softmax_mask_layout(R, sdims, mask, sa))
+        return LX_ERR_NOT_SUPPORTED;
+    // the context [.., S, DV], written through y_perm
+    int64_t cdims[LX_MAX_RANK], ydims[LX_MAX_RANK], cstr[LX_MAX_RANK];
+    for (int i = 0; i < R - 2; i++) cdims[i] = q.dims[i];
+    cdims[R - 2] = S;
+    cdims[R - 1] = DV;
+    for (int i = 0; i < R; i++) ydims[i] = y_perm ? cdims[y_perm[i]] : cdims[i];
+    int st = prepare_output(Y, LX_FLOAT, R, ydims);
+    if (st) return st;
+    int64_t ys = 1;
+    for (int i = R - 1; i >= 0; i--) {
+        cstr[y_perm ? y_perm[i] : i] = ys;
+        ys *= ydims[i];
+    }
+    AttentionArgs a;
+    memset(&a, 0, sizeof a);
+    a.q = (const float *)Q->data;
+    a.k = (const float *)K->data;
+    a.v = (const float *)V->data;
+    a.y = (float *)Y->data;
+    a.s = (int)S;
+    a.sk = (int)SK;
+    a.d = (int)D;
+    a.dv = (int)DV;
+    a.nbatch = R - 2;
+    a.batch = batch;
+    for (int i = 0; i < R - 2; i++) {
+        a.bdims[i] = q.dims[i];
+        a.q_bstr[i] = q.str[i];
+        a.k_bstr[i] = k.str[i];
+        a.v_bstr[i] = v.str[i];
+        a.y_bstr[i] = cstr[i];
+    }
+    a.q_rs = q.str[R - 2], a.q_cs = q.str[R - 1];
+    a.k_rs = k.str[R - 2], a.k_cs = k.str[R - 1];
+    a.v_rs = v.str[R - 2], a.v_cs = v.str[R - 1];
+    a.y_rs = cstr[R - 2], a.y_cs = cstr[R - 1];
+    a.mask = (const float *)mask->data;
+    a.mask_inner = sa.mask_inner;
+    a.mask_rows = sa.mask_rows;
+    a.scale = scale ? (const float *)scale->data : nullptr;
+    a.scale_div = scale_div;
+    HIPCHECK(launch_attention(a, g.stream), "Attention");
+    return LX_OK;
+}
 }  // namespace lx
 
 // MatMul -> Add bias [-> Add residual] [-> the GELU subgraph]: in the MatMul's epilogue when the shapes fit

@@ -762,6 +762,37 @@ int run_node(Exec &X, const GNode &n, std::vector<Value> &outs) {
         }
         return run_unfused(X, n, outs);
     }
+    if (op == "Attention") {
+        // inputs Q, K, V, mask[, scale]; the permutations and the Softmax's attributes as attributes
+        Value *qv, *kv, *vv, *mv, *cv = nullptr;
+        if ((st = X.input(n, 0, &qv)) || (st = X.input(n, 1, &kv)) || (st = X.input(n, 2, &vv)) ||
+            (st = X.input(n, 3, &mv)))
+            return st;
+        if (n.in.size() > 4 && (st = X.input(n, 4, &cv))) return st;
+        int perm[4][LX_MAX_RANK];
+        const int *use[4] = {nullptr, nullptr, nullptr, nullptr};
+        static const char *names[4] = {"q_perm", "k_perm", "v_perm", "y_perm"};
+        bool fits = qv && kv && vv && mv && (n.in.size() == 4 || cv);
+        for (int k = 0; fits && k < 4; k++) {
+            auto it = n.attrs.find(names[k]);
+            if (it == n.attrs.end()) continue;
+            fits = it->second.ints.size() == (size_t)qv->t.rank;
+            for (int d = 0; fits && d < qv->t.rank; d++) perm[k][d] = (int)it->second.ints[d];
+            use[k] = perm[k];
+        }
+        int32_t axis = -1, divide = 1;
+        if (attr_int(n, "axis", &axis) < 0 || attr_int(n, "divide", &divide) < 0) return LX_ERR_INVALID_ARGUMENT;
+        if (fits) {
+            lx_tensor y{};
+            if (api_attention(&qv->t, use[0], &kv->t, use[1], cv ? &cv->t : nullptr, divide, &mv->t, axis, &vv->t,
+                              use[2], use[3], &y) == LX_OK) {
+                outs.push_back(value_from_output(y));
+                return LX_OK;
+            }
+            lx_tensor_free(&y);
+        }
+        return run_unfused(X, n, outs);  // the three fused nodes
+    }
     if (op == "MatMulAddGroup") {
         Value *av, *wv, *bv;
         if ((st = X.input(n, 0, &av)) || (st = X.input(n, 1, &wv)) || (st = X.input(n, 2, &bv))) return st;
@@ -1260,7 +1291,8 @@ struct Fuser {
         }
         g->nodes.swap(out);
         const int grouped = group_projections();
-        return fused - grouped - merge_layernorms();
+        const int merged = merge_layernorms();
+        return fused - grouped - merged - merge_attention();
     }
 
     // A MatMulAdd whose result only a LayerNormDecomposed reads (x): one MatMulAddLayerNorm node (inputs A, W,
@@ -1290,6 +1322,68 @@ struct Fuser {
             f.fused_from.insert(f.fused_from.end(), l.fused_from.begin(), l.fused_from.end());
             g->nodes[c] = f;
             drop.insert(i);
+        }
+        if (drop.empty()) return 0;
+        std::vector<GNode> out;
+        for (int i = 0; i < (int)g->nodes.size(); i++)
+            if (!drop.count(i)) out.push_back(g->nodes[i]);
+        g->nodes.swap(out);
+        return (int)drop.size();
+    }
+
+    // MatMulPermuted (the scores, no output permutation) -> ScaleAddSoftmax / AddSoftmax -> MatMulPermuted (the
+    // context, the probabilities its left operand as they are), each intermediate read only by the next: one
+    // Attention node (inputs Q, K, V, mask[, scale]) that runs the three in one launch where every head fits
+    // and else runs them as they are (its fused_from).  Placed where the context was.  Returns the nodes
+    // removed.
+    int merge_attention() {
+        index();
+        std::set<int> drop;
+        for (int i = 0; i < (int)g->nodes.size(); i++) {
+            const GNode &sn = g->nodes[i];
+            if (sn.op != "MatMulPermuted" || sn.in.size() != 2 || sn.out.size() != 1 || sn.attrs.count("y_perm"))
+                continue;
+            const std::string &scores = sn.out[0];
+            const int c = only_consumer(scores);
+            if (c < 0 || drop.count(c)) continue;
+            const GNode &sm = g->nodes[c];
+            std::string mask, scale;
+            if (sm.op == "ScaleAddSoftmax" && sm.in.size() == 3 && sm.in[0] == scores && sm.in[2] != scores) {
+                scale = sm.in[1];
+                mask = sm.in[2];
+            } else if (sm.op == "AddSoftmax" && sm.in.size() == 2 && (sm.in[0] == scores) != (sm.in[1] == scores)) {
+                mask = sm.in[sm.in[0] == scores ? 1 : 0];
+            } else {
+                continue;
+            }
+            if (sm.out.size() != 1) continue;
+            const int d = only_consumer(sm.out[0]);
+            if (d < 0 || drop.count(d)) continue;
+            const GNode &cn = g->nodes[d];
+            if (cn.op != "MatMulPermuted" || cn.in.size() != 2 || cn.out.size() != 1 || cn.in[0] != sm.out[0] ||
+                cn.in[1] == sm.out[0] || cn.attrs.count("a_perm"))
+                continue;
+            GNode f;
+            f.op = "Attention";
+            f.name = cn.name;
+            f.index = cn.index;
+            f.in = {sn.in[0], sn.in[1], cn.in[1], mask};
+            if (!scale.empty()) f.in.push_back(scale);
+            f.out = cn.out;
+            auto copy = [&](const GNode &from, const char *key, const char *as) {
+                auto it = from.attrs.find(key);
+                if (it != from.attrs.end()) f.attrs[as] = it->second;
+            };
+            copy(sn, "a_perm", "q_perm");
+            copy(sn, "b_perm", "k_perm");
+            copy(cn, "b_perm", "v_perm");
+            copy(cn, "y_perm", "y_perm");
+            copy(sm, "axis", "axis");
+            copy(sm, "divide", "divide");
+            f.fused_from = {sn, sm, cn};
+            g->nodes[d] = f;
+            drop.insert(i);
+            drop.insert(c);
         }
         if (drop.empty()) return 0;
         std::vector<GNode> out;

@@ -73,5 +73,14 @@ int api_matmul_add_layernorm(const lx_tensor *A, const lx_tensor *W, const lx_te
 // Transpose nodes' and MatMul's.  LX_ERR_NOT_SUPPORTED (no message) for operands it does not take.
 int api_matmul_permuted(const lx_tensor *A, const int *a_perm, const lx_tensor *B, const int *b_perm,
                         const int *y_perm, lx_tensor *Y);
+// An attention head's scores transpose(Q, q_perm) x transpose(K, k_perm), their Softmax along the last axis
+// after the optional scale (x / scale when scale_div, else x * scale) and the additive mask, and the context
+// probabilities x transpose(V, v_perm) stored as transpose(context, y_perm) into Y: one launch, bit for bit
+// the MatMulPermuted, ScaleAddSoftmax (AddSoftmax without a scale) and MatMulPermuted nodes it replaces.
+// Float, equal batch axes, and rows, keys and head widths of at most kAttentionMax; LX_ERR_NOT_SUPPORTED (no
+// message) otherwise.
+int api_attention(const lx_tensor *Q, const int *q_perm, const lx_tensor *K, const int *k_perm,
+                  const lx_tensor *scale, int scale_div, const lx_tensor *mask, int32_t axis, const lx_tensor *V,
+                  const int *v_perm, const int *y_perm, lx_tensor *Y);
 
 }  // namespace lx

@@ -146,6 +146,30 @@ struct SoftmaxArgs {
 hipError_t launch_softmax(const SoftmaxArgs &args, hipStream_t s);
 bool softmax_mask_fusable(int dtype, int64_t r, int64_t inner, int64_t outer, int vec);
 
+// Attention heads of at most kAttentionMax rows, keys and columns (Float): per batch, the scores Q K (Q [s, d],
+// K as the product's right operand [d, sk]), their Softmax along the keys with SoftmaxArgs' scale and mask, and
+// the context P V (V [sk, dv]) into y, in one launch -- bit for bit the two MatMul launches and the Softmax
+// launch it replaces (the same MFMA sequence per output as the 64x64 register-staged MatMul kernel, the same
+// lanes per row and reduction order as the grouped Softmax kernel).  Element (i, j) of an operand is at
+// i * rs + j * cs past its batch's offset; batches decompose row-major over bdims.
+constexpr int kAttentionMax = 64;
+struct AttentionArgs {
+    const float *q, *k, *v;
+    float *y;
+    int32_t s, sk, d, dv;
+    int32_t nbatch;
+    int64_t batch;
+    int64_t bdims[kMaxOuter], q_bstr[kMaxOuter], k_bstr[kMaxOuter], v_bstr[kMaxOuter], y_bstr[kMaxOuter];
+    int64_t q_rs, q_cs, k_rs, k_cs, v_rs, v_cs, y_rs, y_cs;
+    // the Softmax between the products, on the scores as a dense [batch * s, sk] tensor
+    const float *mask;
+    int32_t mask_inner;
+    NdLayout mask_rows;
+    const float *scale;
+    int32_t scale_div;
+};
+hipError_t launch_attention(const AttentionArgs &a, hipStream_t s);
+
 // LayerNorm decomposed into its ONNX nodes, rows of length r (1 <= r <= 4099; x, gamma, beta, y 16-byte
 // aligned).
 hipError_t launch_layernorm(const float *x, const float *gamma, const float *beta, float eps, float *y,

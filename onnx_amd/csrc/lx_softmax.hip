@@ -713,6 +713,168 @@ static hipError_t softmax_rows_launch(const SoftmaxArgs &a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Attention heads (launch_attention): one block of 16 waves per batch.
+// ---------------------------------------------------------------------------
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// Scores, Softmax and context of one head.  Q, K and V are first staged in LDS as 64 x 64 tiles with zeros past
+// their rows and columns (every load issued before the first is waited for; Q, K and the scores in rows padded
+// by one float against bank conflicts).  Each wave then runs one 32x32 quarter of a 64x64 product as the
+// MatMul's register-staged kernel runs it: K in steps of 16 (zeros past K), MFMA j of a step taking k = j from
+// lanes 0-31 and k = 8 + j from lanes 32-63, as B^T A^T (lane l % 32 holds row l % 32 of A and column l % 32 of
+// B), so acc[q] is C[row l % 32][column 8 (q / 4) + 4 (l / 32) + q % 4].  The zeros make every product past the
+// operands +0, as the kernel's zero loads do.  The scores go to LDS; each row splits into head, whole vectors
+// and tail by its flat offset in the dense scores tensor, as k_softmax_group<V = 4, L> splits it in memory, and
+// is scaled, masked, reduced over its L lanes and divided by the same functions in the same lanes, in place;
+// the context then reads the probabilities (+0 past the keys) from LDS.
+constexpr int kAttnLd = kAttentionMax + 1;  // padded LDS row of Q, K and the scores
+constexpr int kAttnBlock = 1024;             // 16 waves: the Softmax's rows in one pass
+
+// a rows x cols strided matrix into a 64 x 64 LDS tile of rows of ld floats, zeros past rows and cols: lane t
+// takes column t % 64 of rows t / 64 + 16 u, every load in flight before the first store
+__device__ __forceinline__ void attn_stage(float *__restrict__ dst, int ld, const float *__restrict__ src, int rows,
+                                           int cols, int64_t rs, int64_t cs) {
+    constexpr int RP = kAttnBlock / 64, U = kAttentionMax / RP;  // rows per pass, passes
+    static_assert(kAttentionMax == 64 && U * RP == kAttentionMax, "whole rows of 64 lanes per pass");
+    const int c = threadIdx.x & 63, r0 = threadIdx.x >> 6;
+    const float *p = src + (int64_t)c * cs + (int64_t)r0 * rs;
+    float x[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) x[u] = (c < cols && r0 + RP * u < rows) ? p[(int64_t)(RP * u) * rs] : 0.f;
+#pragma unroll
+    for (int u = 0; u < U; u++) dst[(r0 + RP * u) * ld + c] = x[u];
+}
+
+template <int L, int NOUT>
+__global__ __launch_bounds__(kAttnBlock) void k_attention(AttentionArgs a) {
+    __shared__ ExpTable tab;
+    __shared__ float qs[kAttentionMax * kAttnLd];        // Q [S][D]
+    __shared__ float ks[kAttentionMax * kAttnLd];        // K as rows of keys [SK][D]
+    __shared__ float vs[kAttentionMax * kAttentionMax];  // V [SK][DV]
+    __shared__ float ps[kAttentionMax * kAttnLd];        // scores, then probabilities [S][SK]
+    const int t = threadIdx.x, l = t & 63, w = t >> 6;
+    const int64_t z = blockIdx.x;
+    int64_t qo = 0, ko = 0, vo = 0, yo = 0;
+    {
+        int64_t b = z;
+        for (int d = a.nbatch - 1; d >= 0; d--) {
+            const int64_t i = b % a.bdims[d];
+            b /= a.bdims[d];
+            qo += i * a.q_bstr[d];
+            ko += i * a.k_bstr[d];
+            vo += i * a.v_bstr[d];
+            yo += i * a.y_bstr[d];
+        }
+    }
+    const int S = a.s, SK = a.sk, D = a.d, DV = a.dv;
+    // K's element (kk, j) of the product's right operand is key j's element kk
+    attn_stage(qs, kAttnLd, a.q + qo, S, D, a.q_rs, a.q_cs);
+    attn_stage(ks, kAttnLd, a.k + ko, SK, D, a.k_cs, a.k_rs);
+    attn_stage(vs, kAttentionMax, a.v + vo, SK, DV, a.v_rs, a.v_cs);
+    exp_table_fill(tab);
+    __syncthreads();
+
+    // waves 0-3: one quarter each of the 64x64 products
+    const int wr = 32 * ((w >> 1) & 1), wc = 32 * (w & 1);
+    const int r = wr + (l & 31), c = wc + (l & 31), h = l >> 5;
+    if (w < 4) {
+        v16f acc;
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = 0.f;
+        const float *qa = qs + r * kAttnLd + 8 * h, *kb = ks + c * kAttnLd + 8 * h;
+        for (int kt = 0; kt < D; kt += 16)
+#pragma unroll
+            for (int j = 0; j < 8; j++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[kt + j], qa[kt + j], acc, 0, 0, 0);
+        float *pr = ps + r * kAttnLd + wc + 4 * h;
+#pragma unroll
+        for (int q = 0; q < 16; q++) pr[8 * (q / 4) + q % 4] = acc[q];
+    }
+    __syncthreads();
+
+    constexpr int RW = 64 / L;  // rows per wave at a time
+    const int gl = l & (L - 1);
+    const float sv = a.scale ? a.scale[0] : 1.f;
+    float sf = sv;
+    const bool smul = !a.scale_div || exact_pow2_recip(sv, &sf);
+    for (int i = w * RW + l / L; i < S; i += (kAttnBlock / 64) * RW) {
+        const int64_t row = z * S + i;
+        const RagRow g = rag_row<4>(row * SK, SK);
+        float *pr = ps + i * kAttnLd;
+        Vec<float, 4> v[1];
+        float e = 0.f;
+        if (gl < g.nvb) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[0].v[k] = pr[g.head + 4 * gl + k];
+        }
+        if (gl < g.ne) e = pr[rag_col<4>(g, gl)];
+        const float *m = nullptr;
+        if constexpr (NOUT != 0) m = a.mask + mask_row_offset<NOUT>((uint32_t)row, a.mask_rows);
+        rag_scale_mask<float, 4, 1, L>(v, e, g, gl, a.scale != nullptr, smul, sf, sv, m, a.mask_inner);
+        float mx = rag_lane_max<float, 4, 1, L>(v, e, g, gl);
+        mx = group_reduce<L>(mx, [](float x, float y) { return row_max<float>(x, y); });
+        float sum = rag_lane_exp_sum<float, 4, 1, L>(v, e, mx, g, gl, tab);
+        sum = group_reduce<L>(sum, [](float x, float y) { return x + y; });
+        const float rs = 1.f / sum;
+        if (gl < g.nvb) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) pr[g.head + 4 * gl + k] = div_row<float>(v[0].v[k], sum, rs);
+        }
+        if (gl < g.ne) pr[rag_col<4>(g, gl)] = div_row<float>(e, sum, rs);
+    }
+    __syncthreads();
+
+    if (w < 4 && wr < S && wc < DV) {
+        v16f acc;
+#pragma unroll
+        for (int q = 0; q < 16; q++) acc[q] = 0.f;
+        const float *pa = ps + r * kAttnLd + 8 * h, *vb = vs + 8 * h * kAttentionMax + c;
+        for (int kt = 0; kt < SK; kt += 16)
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[(kt + j) * kAttentionMax], pa[kt + j], acc, 0, 0, 0);
+        float *Y = a.y + yo + (int64_t)r * a.y_rs;
+        if (r < S) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int col = wc + 8 * (q / 4) + 4 * h + q % 4;
+                if (col < DV) Y[col * a.y_cs] = acc[q];
+            }
+        }
+    }
+}
+
+template <int NOUT>
+static hipError_t attention_launch(const AttentionArgs &a, int L, hipStream_t s) {
+    const dim3 g((unsigned)a.batch), blk(kAttnBlock);
+    switch (L) {
+    case 1: hipLaunchKernelGGL((k_attention<1, NOUT>), g, blk, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_attention<2, NOUT>), g, blk, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_attention<4, NOUT>), g, blk, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_attention<8, NOUT>), g, blk, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((k_attention<16, NOUT>), g, blk, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t launch_attention(const AttentionArgs &a, hipStream_t s) {
+    if (a.s < 1 || a.sk < 1 || a.d < 1 || a.dv < 1 || a.s > kAttentionMax || a.sk > kAttentionMax ||
+        a.d > kAttentionMax || a.dv > kAttentionMax || a.batch < 1 || a.batch > 0x7fffffff)
+        return hipErrorInvalidValue;
+    // the lanes per row softmax_typed gives rows of sk floats in 16-byte aligned tensors
+    const int nvr = a.sk / 4, ne_max = a.sk % 4 == 0 ? 0 : (a.sk < 6 ? a.sk : 6);
+    int L = 1;
+    while (L < nvr || L < ne_max) L <<= 1;
+    if (!a.mask) return attention_launch<0>(a, L, s);
+    switch (a.mask_rows.nouter) {
+    case 1: return attention_launch<1>(a, L, s);
+    case 2: return attention_launch<2>(a, L, s);
+    case 3: return attention_launch<3>(a, L, s);
+    default: return attention_launch<-1>(a, L, s);
+    }
+}
+
 // Whole 16-byte vectors a row-in-registers kernel holds at most: blocks of 1024 lanes with 16 vectors each
 // for float rows, 8 each for double rows and rows with a mask or scale (16 spill registers there).
 constexpr int64_t kSoftmaxRowVecs = 1024 * 16, kSoftmaxRowVecsMasked = 1024 * 8;

@@ -39,7 +39,7 @@ def _check(st, what):
 class Node:
     """A graph node as the runtime holds it (after fusion, fused nodes appear with op types GeluErf,
     LayerNormDecomposed, AddSoftmax, ScaleAddSoftmax, MatMulAdd, MatMulAddGelu, MatMulAddGroup,
-    MatMulPermuted, MatMulAddLayerNorm and ElementwiseChain)."""
+    MatMulPermuted, MatMulAddLayerNorm, Attention and ElementwiseChain)."""
 
     def __init__(self, name: str, op: str):
         self.Name, self.Op = name, op

@@ -104,7 +104,7 @@ def test_every_fused_op_is_charted_under_a_reference_op():
     ElementwiseChain takes the default arm."""
     src = open(os.path.join(ROOT, "onnx_amd", "csrc", "lx_graph.cpp")).read()
     made = set(re.findall(r'(?:f\.|f->)op = "(\w+)"', src))
-    assert {"GeluErf", "LayerNormDecomposed", "MatMulAdd", "MatMulAddGroup", "MatMulPermuted"} <= made
+    assert {"GeluErf", "LayerNormDecomposed", "MatMulAdd", "MatMulAddGroup", "MatMulPermuted", "Attention"} <= made
     s = _cs("HipGraph.cs")
     body = s[s.index("static OpType FusedOp(string name)"):]
     body = body[:body.index("};")]

@@ -33,7 +33,7 @@ def test_bert_layer_accuracy(hip, layer, mode):
     model, ins, ref, t64 = layer
     g = Model.Load(model)
     if mode != "nodes":
-        assert g.Fuse() == 7
+        assert g.Fuse() == 5
     dev = {k: DeviceTensor.from_numpy(v) for k, v in ins.items()}
     ok = g.Capture(dev) if mode == "captured" else g.Execute(dev)
     assert ok, g.LastError
@@ -73,7 +73,7 @@ def test_me5s_shaped_encoder_accuracy(hip, encoder, mode):
     model, ins, ref, t64 = encoder
     g = Model.Load(model)
     if mode != "nodes":
-        assert g.Fuse() == 3 * 7 + 3
+        assert g.Fuse() == 3 * 5 + 3
     dev = {k: DeviceTensor.from_numpy(v) for k, v in ins.items()}
     ok = g.Capture(dev) if mode == "captured" else g.Execute(dev)
     assert ok, g.LastError

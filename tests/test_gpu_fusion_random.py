@@ -16,7 +16,7 @@ from onnx_amd.graph import Model
 
 pytestmark = pytest.mark.gpu
 
-REDUCING = {"LayerNormDecomposed", "MatMulAddLayerNorm", "AddSoftmax", "ScaleAddSoftmax"}
+REDUCING = {"LayerNormDecomposed", "MatMulAddLayerNorm", "AddSoftmax", "ScaleAddSoftmax", "Attention"}
 
 
 class Builder:

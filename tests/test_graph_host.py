@@ -257,36 +257,39 @@ def test_encoder_oracle_against_float64():
 
 
 def test_encoder_fusion_plan():
-    """Every layer of the encoder fuses as the single layer does (7 fusions), plus the embedding sum, the
+    """Every layer of the encoder fuses as the single layer does (5 fused nodes), plus the embedding sum, the
     embedding LayerNorm and the mask's Sub -> Mul."""
     from bert_layer import encoder_model
     model, _, _, _ = encoder_model(1, 16, layers=3, vocab=500, seed=4)
     g = Model.Load(model)
-    assert g.Fuse() == 3 * 7 + 3
+    assert g.Fuse() == 3 * 5 + 3
     ops = [n.Op for n in g.Nodes]
     assert ops[:7] == ["Gather", "Gather", "ElementwiseChain", "LayerNormDecomposed", "Unsqueeze", "Cast",
                        "ElementwiseChain"]
-    assert ops.count("MatMulAddGroup") == 3 and ops.count("MatMulAddGelu") == 3 and ops.count("ScaleAddSoftmax") == 3
+    assert ops.count("MatMulAddGroup") == 3 and ops.count("MatMulAddGelu") == 3 and ops.count("Attention") == 3
     assert ops.count("LayerNormDecomposed") == 1 and ops.count("MatMulAddLayerNorm") == 2 * 3
     assert "Add" not in ops and "Div" not in ops
-    assert ops.count("MatMulPermuted") == 2 * 3 and "Transpose" not in ops and "MatMul" not in ops
+    assert "MatMulPermuted" not in ops and "ScaleAddSoftmax" not in ops and "Transpose" not in ops
+    assert "MatMul" not in ops
 
 
 def test_bert_layer_fusion_plan():
     from bert_layer import bert_layer
     model, _, _, _ = bert_layer(1, 16, 3)
     g = Model.Load(model)
-    assert g.Fuse() == 7
+    assert g.Fuse() == 5
     ops = [n.Op for n in g.Nodes]
-    assert ops.count("MatMulAddLayerNorm") == 2 and ops.count("ScaleAddSoftmax") == 1
+    assert ops.count("MatMulAddLayerNorm") == 2 and ops.count("Attention") == 1
     assert "Div" not in ops   # the scores' Div by sqrt(64) went into ScaleAddSoftmax
     # the six projections carry their bias (and the two residual Adds) in the MatMul epilogue, the FFN's
     # first one its GELU too, the two before a LayerNorm that LayerNorm; the Q, K, V projections of the same
     # input run as one grouped launch
     assert "MatMulAdd" not in ops and "LayerNormDecomposed" not in ops and "Add" not in ops and "GeluErf" not in ops
     # the attention products read Q, K (by columns) and V and write the context through the heads'
-    # transposed views: no Transpose node is left
-    assert ops.count("MatMulPermuted") == 2 and "Transpose" not in ops and "MatMul" not in ops
+    # transposed views: no Transpose node is left; scores, masked Softmax and context form one Attention node
+    # (placed where the context's output Transpose was)
+    assert "MatMulPermuted" not in ops and "ScaleAddSoftmax" not in ops and "Transpose" not in ops
+    assert "MatMul" not in ops and [n.Name for n in g.Nodes if n.Op == "Attention"] == ["c_perm"]
     assert [n.Name for n in g.Nodes if n.Op == "MatMulAddLayerNorm"] == ["addb1", "addb2"]
     assert [n.Name for n in g.Nodes if n.Op == "MatMulAddGelu"] == ["gelu_half"]
     assert [n.Name for n in g.Nodes if n.Op == "MatMulAddGroup"] == ["q_bias"]
