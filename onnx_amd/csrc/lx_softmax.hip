@@ -714,30 +714,32 @@ static hipError_t softmax_rows_launch(const SoftmaxArgs &a, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// Attention heads (launch_attention): one block of 16 waves per batch.
+// Attention heads (launch_attention): one block per batch.
 // ---------------------------------------------------------------------------
 typedef float v16f __attribute__((ext_vector_type(16)));
 
-// Scores, Softmax and context of one head.  Q, K and V are first staged in LDS as 64 x 64 tiles with zeros past
-// their rows and columns (every load issued before the first is waited for; Q, K and the scores in rows padded
-// by one float against bank conflicts).  Each wave then runs one 32x32 quarter of a 64x64 product as the
-// MatMul's register-staged kernel runs it: K in steps of 16 (zeros past K), MFMA j of a step taking k = j from
-// lanes 0-31 and k = 8 + j from lanes 32-63, as B^T A^T (lane l % 32 holds row l % 32 of A and column l % 32 of
-// B), so acc[q] is C[row l % 32][column 8 (q / 4) + 4 (l / 32) + q % 4].  The zeros make every product past the
-// operands +0, as the kernel's zero loads do.  The scores go to LDS; each row splits into head, whole vectors
-// and tail by its flat offset in the dense scores tensor, as k_softmax_group<V = 4, L> splits it in memory, and
-// is scaled, masked, reduced over its L lanes and divided by the same functions in the same lanes, in place;
-// the context then reads the probabilities (+0 past the keys) from LDS.
-constexpr int kAttnLd = kAttentionMax + 1;  // padded LDS row of Q, K and the scores
-constexpr int kAttnBlock = 1024;             // 16 waves: the Softmax's rows in one pass
+// Scores, Softmax and context of one head, in T x T tiles (T = 32 or 64) with NT lanes.  Q, K and V are first
+// staged in LDS with zeros past their rows and columns (every load issued before the first is waited for; Q, K
+// and the scores in rows padded by one float against bank conflicts).  Each of the first (T / 32)^2 waves then
+// runs one 32x32 part of the product as the MatMul's register-staged kernel runs the 32x32 quarters of its 64x64
+// tiles: K in steps of 16 (zeros past K), MFMA j of a step taking k = j from lanes 0-31 and k = 8 + j from lanes
+// 32-63, as B^T A^T (lane l % 32 holds row l % 32 of A and column l % 32 of B), so acc[q] is C[row l % 32][column
+// 8 (q / 4) + 4 (l / 32) + q % 4].  The zeros make every product past the operands +0, as the kernel's zero
+// loads do.  The scores go to LDS; each row splits into head, whole vectors and tail by its flat offset in the
+// dense scores tensor, as k_softmax_group<V = 4, L> splits it in memory, and is scaled, masked, reduced over its
+// L lanes and divided by the same functions in the same lanes, in place; the context then reads the
+// probabilities (+0 past the keys) from LDS.  T = 64 takes 16 waves (the Softmax's 64 rows in one pass); T = 32,
+// for heads of at most 32, takes 4 waves and a quarter of the LDS, so that many heads run at once.
 
-// a rows x cols strided matrix into a 64 x 64 LDS tile of rows of ld floats, zeros past rows and cols: lane t
-// takes column t % 64 of rows t / 64 + 16 u, every load in flight before the first store
+// a rows x cols strided matrix into a T x T LDS tile of rows of ld floats, zeros past rows and cols: lane t takes
+// column t % 64 (of the first T) of rows t / 64 + (NT / 64) u, every load in flight before the first store
+template <int T, int NT>
 __device__ __forceinline__ void attn_stage(float *__restrict__ dst, int ld, const float *__restrict__ src, int rows,
                                            int cols, int64_t rs, int64_t cs) {
-    constexpr int RP = kAttnBlock / 64, U = kAttentionMax / RP;  // rows per pass, passes
-    static_assert(kAttentionMax == 64 && U * RP == kAttentionMax, "whole rows of 64 lanes per pass");
+    constexpr int RP = NT / 64, U = T / RP;  // rows per pass, passes
+    static_assert(U * RP == T, "whole rows per pass");
     const int c = threadIdx.x & 63, r0 = threadIdx.x >> 6;
+    if (c >= T) return;
     const float *p = src + (int64_t)c * cs + (int64_t)r0 * rs;
     float x[U];
 #pragma unroll
@@ -746,13 +748,15 @@ __device__ __forceinline__ void attn_stage(float *__restrict__ dst, int ld, cons
     for (int u = 0; u < U; u++) dst[(r0 + RP * u) * ld + c] = x[u];
 }
 
-template <int L, int NOUT>
-__global__ __launch_bounds__(kAttnBlock) void k_attention(AttentionArgs a) {
+template <int T, int NT, int L, int NOUT>
+__global__ __launch_bounds__(NT) void k_attention(AttentionArgs a) {
+    static_assert((T == 32 || T == 64) && NT % 64 == 0 && NT / 64 >= (T / 32) * (T / 32), "a wave per 32x32 part");
+    constexpr int LD = T + 1;  // padded LDS row of Q, K and the scores
     __shared__ ExpTable tab;
-    __shared__ float qs[kAttentionMax * kAttnLd];        // Q [S][D]
-    __shared__ float ks[kAttentionMax * kAttnLd];        // K as rows of keys [SK][D]
-    __shared__ float vs[kAttentionMax * kAttentionMax];  // V [SK][DV]
-    __shared__ float ps[kAttentionMax * kAttnLd];        // scores, then probabilities [S][SK]
+    __shared__ float qs[T * LD];  // Q [S][D]
+    __shared__ float ks[T * LD];  // K as rows of keys [SK][D]
+    __shared__ float vs[T * T];   // V [SK][DV]
+    __shared__ float ps[T * LD];  // scores, then probabilities [S][SK]
     const int t = threadIdx.x, l = t & 63, w = t >> 6;
     const int64_t z = blockIdx.x;
     int64_t qo = 0, ko = 0, vo = 0, yo = 0;
@@ -769,24 +773,25 @@ __global__ __launch_bounds__(kAttnBlock) void k_attention(AttentionArgs a) {
     }
     const int S = a.s, SK = a.sk, D = a.d, DV = a.dv;
     // K's element (kk, j) of the product's right operand is key j's element kk
-    attn_stage(qs, kAttnLd, a.q + qo, S, D, a.q_rs, a.q_cs);
-    attn_stage(ks, kAttnLd, a.k + ko, SK, D, a.k_cs, a.k_rs);
-    attn_stage(vs, kAttentionMax, a.v + vo, SK, DV, a.v_rs, a.v_cs);
+    attn_stage<T, NT>(qs, LD, a.q + qo, S, D, a.q_rs, a.q_cs);
+    attn_stage<T, NT>(ks, LD, a.k + ko, SK, D, a.k_cs, a.k_rs);
+    attn_stage<T, NT>(vs, T, a.v + vo, SK, DV, a.v_rs, a.v_cs);
     exp_table_fill(tab);
     __syncthreads();
 
-    // waves 0-3: one quarter each of the 64x64 products
-    const int wr = 32 * ((w >> 1) & 1), wc = 32 * (w & 1);
+    // the first (T / 32)^2 waves: one 32x32 part each of the T x T products
+    constexpr int P = T / 32, NP = P * P;
+    const int wr = 32 * (w / P % P), wc = 32 * (w % P);
     const int r = wr + (l & 31), c = wc + (l & 31), h = l >> 5;
-    if (w < 4) {
+    if (w < NP) {
         v16f acc;
 #pragma unroll
         for (int q = 0; q < 16; q++) acc[q] = 0.f;
-        const float *qa = qs + r * kAttnLd + 8 * h, *kb = ks + c * kAttnLd + 8 * h;
+        const float *qa = qs + r * LD + 8 * h, *kb = ks + c * LD + 8 * h;
         for (int kt = 0; kt < D; kt += 16)
 #pragma unroll
             for (int j = 0; j < 8; j++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kb[kt + j], qa[kt + j], acc, 0, 0, 0);
-        float *pr = ps + r * kAttnLd + wc + 4 * h;
+        float *pr = ps + r * LD + wc + 4 * h;
 #pragma unroll
         for (int q = 0; q < 16; q++) pr[8 * (q / 4) + q % 4] = acc[q];
     }
@@ -797,10 +802,10 @@ __global__ __launch_bounds__(kAttnBlock) void k_attention(AttentionArgs a) {
     const float sv = a.scale ? a.scale[0] : 1.f;
     float sf = sv;
     const bool smul = !a.scale_div || exact_pow2_recip(sv, &sf);
-    for (int i = w * RW + l / L; i < S; i += (kAttnBlock / 64) * RW) {
+    for (int i = w * RW + l / L; i < S; i += (NT / 64) * RW) {
         const int64_t row = z * S + i;
         const RagRow g = rag_row<4>(row * SK, SK);
-        float *pr = ps + i * kAttnLd;
+        float *pr = ps + i * LD;
         Vec<float, 4> v[1];
         float e = 0.f;
         if (gl < g.nvb) {
@@ -824,15 +829,14 @@ __global__ __launch_bounds__(kAttnBlock) void k_attention(AttentionArgs a) {
     }
     __syncthreads();
 
-    if (w < 4 && wr < S && wc < DV) {
+    if (w < NP && wr < S && wc < DV) {
         v16f acc;
 #pragma unroll
         for (int q = 0; q < 16; q++) acc[q] = 0.f;
-        const float *pa = ps + r * kAttnLd + 8 * h, *vb = vs + 8 * h * kAttentionMax + c;
+        const float *pa = ps + r * LD + 8 * h, *vb = vs + 8 * h * T + c;
         for (int kt = 0; kt < SK; kt += 16)
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                acc = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[(kt + j) * kAttentionMax], pa[kt + j], acc, 0, 0, 0);
+            for (int j = 0; j < 8; j++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[(kt + j) * T], pa[kt + j], acc, 0, 0, 0);
         float *Y = a.y + yo + (int64_t)r * a.y_rs;
         if (r < S) {
 #pragma unroll
@@ -844,18 +848,29 @@ __global__ __launch_bounds__(kAttnBlock) void k_attention(AttentionArgs a) {
     }
 }
 
-template <int NOUT>
+template <int T, int NT, int NOUT>
 static hipError_t attention_launch(const AttentionArgs &a, int L, hipStream_t s) {
-    const dim3 g((unsigned)a.batch), blk(kAttnBlock);
+    const dim3 g((unsigned)a.batch), blk(NT);
     switch (L) {
-    case 1: hipLaunchKernelGGL((k_attention<1, NOUT>), g, blk, 0, s, a); break;
-    case 2: hipLaunchKernelGGL((k_attention<2, NOUT>), g, blk, 0, s, a); break;
-    case 4: hipLaunchKernelGGL((k_attention<4, NOUT>), g, blk, 0, s, a); break;
-    case 8: hipLaunchKernelGGL((k_attention<8, NOUT>), g, blk, 0, s, a); break;
-    case 16: hipLaunchKernelGGL((k_attention<16, NOUT>), g, blk, 0, s, a); break;
+    case 1: hipLaunchKernelGGL((k_attention<T, NT, 1, NOUT>), g, blk, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((k_attention<T, NT, 2, NOUT>), g, blk, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((k_attention<T, NT, 4, NOUT>), g, blk, 0, s, a); break;
+    case 8: hipLaunchKernelGGL((k_attention<T, NT, 8, NOUT>), g, blk, 0, s, a); break;
+    case 16:
+        if constexpr (T == 64) {
+            hipLaunchKernelGGL((k_attention<T, NT, 16, NOUT>), g, blk, 0, s, a);
+            break;
+        }
+        return hipErrorInvalidValue;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+template <int NOUT>
+static hipError_t attention_size(const AttentionArgs &a, int L, hipStream_t s) {
+    if (a.s <= 32 && a.sk <= 32 && a.d <= 32 && a.dv <= 32) return attention_launch<32, 256, NOUT>(a, L, s);
+    return attention_launch<64, 1024, NOUT>(a, L, s);
 }
 
 hipError_t launch_attention(const AttentionArgs &a, hipStream_t s) {
@@ -866,12 +881,12 @@ hipError_t launch_attention(const AttentionArgs &a, hipStream_t s) {
     const int nvr = a.sk / 4, ne_max = a.sk % 4 == 0 ? 0 : (a.sk < 6 ? a.sk : 6);
     int L = 1;
     while (L < nvr || L < ne_max) L <<= 1;
-    if (!a.mask) return attention_launch<0>(a, L, s);
+    if (!a.mask) return attention_size<0>(a, L, s);
     switch (a.mask_rows.nouter) {
-    case 1: return attention_launch<1>(a, L, s);
-    case 2: return attention_launch<2>(a, L, s);
-    case 3: return attention_launch<3>(a, L, s);
-    default: return attention_launch<-1>(a, L, s);
+    case 1: return attention_size<1>(a, L, s);
+    case 2: return attention_size<2>(a, L, s);
+    case 3: return attention_size<3>(a, L, s);
+    default: return attention_size<-1>(a, L, s);
     }
 }
 
