@@ -24,7 +24,7 @@ def attention_model(b, h, s, sk, d, dv, mask_kind, scale, extra_outputs=()):
         inits.append(("c", np.array(np.sqrt(d) if scale == "div" else 1.0 / np.sqrt(d), np.float32)))
         nodes.append(W.node("Div" if scale == "div" else "Mul", ["sc", "c"], ["scaled"], "scale"))
         x = "scaled"
-    mshape = {"b11s": (b, 1, 1, sk), "bhss": (b, h, s, sk), "s": (sk,), "one": (1,)}[mask_kind]
+    mshape = {"b11s": (b, 1, 1, sk), "bhss": (b, h, s, sk), "b1ss": (b, 1, s, sk), "s": (sk,), "one": (1,)}[mask_kind]
     mask = np.where(rng.random(mshape) < 0.2, -10000.0, rng.normal(0, 0.5, mshape)).astype(np.float32)
     inits.append(("mask", mask))
     nodes += [W.node("Add", [x, "mask"], ["t"], "addmask"), W.node("Softmax", ["t"], ["p"], "softmax", axis=-1),
@@ -51,6 +51,7 @@ CASES = [  # b, h, s, sk, d, dv, mask, scale
     (1, 1, 64, 64, 64, 64, "bhss", "div"),
     (2, 2, 64, 64, 32, 32, "b11s", "mul"),     # the me5s heads at 64 tokens
     (2, 2, 33, 64, 64, 33, "s", "div"),
+    (2, 3, 5, 6, 8, 8, "b1ss", "div"),         # a mask over batch and rows, not heads: three row axes
     (1, 1, 65, 65, 32, 32, "b11s", "div"),     # larger than one launch's heads: the three nodes
     (1, 2, 8, 8, 80, 32, "b11s", "div"),
 ]
@@ -86,6 +87,30 @@ def test_attention_node_equals_the_three_nodes(hip, case):
         assert g3.Execute(dev), g3.LastError
         assert np.array_equal(got2.view(np.uint32), g3.Output("y").to_numpy().view(np.uint32))
     g.ReleaseCapture()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_attention_node_random_heads(hip, seed):
+    """Seeded random heads (rows, keys, head and value widths from 1 to 64, masks and scales of every kind): the
+    Attention node equals the three nodes it replaces bit for bit."""
+    rng = np.random.default_rng(100 + seed)
+    for _ in range(8):
+        b, h = int(rng.integers(1, 4)), int(rng.integers(1, 5))
+        s, sk, d, dv = (int(rng.integers(1, 65)) for _ in range(4))
+        mask_kind = ["b11s", "bhss", "b1ss", "one"][int(rng.integers(4))]
+        scale = [None, "div", "mul"][int(rng.integers(3))]
+        if scale is None and mask_kind == "one":  # MatMul -> Add of a [1] constant fuses as a bias row instead
+            mask_kind = "b11s"
+        model, ins = attention_model(b, h, s, sk, d, dv, mask_kind, scale)
+        kept, _ = attention_model(b, h, s, sk, d, dv, mask_kind, scale, extra_outputs=("sc",))
+        dev = {k: DeviceTensor.from_numpy(v) for k, v in ins.items()}
+        g, g3 = Model.Load(model), Model.Load(kept)
+        g.Fuse()
+        g3.Fuse()
+        assert [n.Op for n in g.Nodes] == ["Attention"], (b, h, s, sk, d, dv, mask_kind, scale)
+        assert g3.Execute(dev) and g.Execute(dev), (g.LastError, g3.LastError)
+        got, want = g.Output("y").to_numpy(), g3.Output("y").to_numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (b, h, s, sk, d, dv, mask_kind, scale)
 
 
 def test_attention_node_launch_count(hip):
