@@ -492,9 +492,12 @@ __device__ __forceinline__ double pow_lx(double x, double y) {
 // then across the wave.  Shared by every kernel that normalises rows this way, so their results are identical.
 // The per-vector bounds checks stay even when r fills every vector: without them the compiler issues the gamma
 // / beta loads with the row's.
+// gpre / bpre: gamma's and beta's vectors already loaded by the caller (a latency-bound caller issues them with its
+// other loads), else null.
 template <int NV>
 __device__ __forceinline__ void ln_row_finish(Vec<float, 4> (&v)[NV], int r, int lane, const float *__restrict__ gamma,
-                                              const float *__restrict__ beta, float eps, float *__restrict__ q) {
+                                              const float *__restrict__ beta, float eps, float *__restrict__ q,
+                                              const Vec<float, 4> *gpre = nullptr, const Vec<float, 4> *bpre = nullptr) {
     float s = 0.0f;
 #pragma unroll
     for (int c = 0; c < NV; c++) {
@@ -525,8 +528,8 @@ __device__ __forceinline__ void ln_row_finish(Vec<float, 4> (&v)[NV], int r, int
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * 4;
         if (col < r) {
-            Vec<float, 4> g = vload<float, 4>(gamma + col);
-            Vec<float, 4> b = vload<float, 4>(beta + col);
+            Vec<float, 4> g = gpre ? gpre[c] : vload<float, 4>(gamma + col);
+            Vec<float, 4> b = bpre ? bpre[c] : vload<float, 4>(beta + col);
             Vec<float, 4> o;
 #pragma unroll
             for (int k = 0; k < 4; k++) {

@@ -142,6 +142,11 @@ __global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C,
     const int64_t zb = i / nq, e = (i - zb * nq) * 4;  // batch of this launch, element of its matrix
     const int64_t stride = p.batch * mn;                // between the partials of two K ranges
     const float *P = p.part + zb * mn + e;
+    // the bias and residual loaded with the partials, one memory latency for all (added after them, as before)
+    const int64_t bz = p.batch_base + zb;
+    const float4 bc = p.bias ? *reinterpret_cast<const float4 *>(p.bias + bz * p.bias_bstr + e % p.n)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 rc = p.res ? *reinterpret_cast<const float4 *>(p.res + bz * mn + e) : make_float4(0.f, 0.f, 0.f, 0.f);
     // the partials eight at a time, all eight loads in flight before the first add (one memory latency per
     // eight, not one per partial); the adds in range order
     constexpr int kChunk = 8;
@@ -157,13 +162,10 @@ __global__ __launch_bounds__(256) void k_matmul_split_sum(float *__restrict__ C,
                 v[0] = v[0] + x[c][0]; v[1] = v[1] + x[c][1]; v[2] = v[2] + x[c][2]; v[3] = v[3] + x[c][3];
             }
     }
-    const int64_t bz = p.batch_base + zb;
     if (p.bias) {
-        const float4 bc = *reinterpret_cast<const float4 *>(p.bias + bz * p.bias_bstr + e % p.n);
         v[0] = v[0] + bc.x; v[1] = v[1] + bc.y; v[2] = v[2] + bc.z; v[3] = v[3] + bc.w;
     }
     if (p.res) {
-        const float4 rc = *reinterpret_cast<const float4 *>(p.res + bz * mn + e);
         v[0] = v[0] + rc.x; v[1] = v[1] + rc.y; v[2] = v[2] + rc.z; v[3] = v[3] + rc.w;
     }
     if constexpr (GELU) {
@@ -189,7 +191,18 @@ __global__ __launch_bounds__(64) void k_matmul_split_sum_ln(const float *__restr
     const int N = p.n;
     const int64_t mn = (int64_t)p.m * N, stride = p.batch * mn, bz = p.batch_base + zb;
     constexpr int kChunk = 8;
-    Vec<float, 4> v[NV];
+    // the bias, residual, gamma and beta vectors loaded with the partials, one memory latency for all
+    Vec<float, 4> v[NV], gv[NV], bv[NV];
+    float4 bcv[NV], rcv[NV];
+#pragma unroll
+    for (int c = 0; c < NV; c++) {
+        const int col = (c * 64 + lane) * 4;
+        if (col >= N) continue;
+        gv[c] = vload<float, 4>(gamma + col);
+        bv[c] = vload<float, 4>(beta + col);
+        if (p.bias) bcv[c] = *reinterpret_cast<const float4 *>(p.bias + bz * p.bias_bstr + col);
+        if (p.res) rcv[c] = *reinterpret_cast<const float4 *>(p.res + bz * mn + row * N + col);
+    }
 #pragma unroll
     for (int c = 0; c < NV; c++) {
         const int col = (c * 64 + lane) * 4;
@@ -209,16 +222,16 @@ __global__ __launch_bounds__(64) void k_matmul_split_sum_ln(const float *__restr
                 }
         }
         if (p.bias) {
-            const float4 bc = *reinterpret_cast<const float4 *>(p.bias + bz * p.bias_bstr + col);
+            const float4 bc = bcv[c];
             a[0] = a[0] + bc.x; a[1] = a[1] + bc.y; a[2] = a[2] + bc.z; a[3] = a[3] + bc.w;
         }
         if (p.res) {
-            const float4 rc = *reinterpret_cast<const float4 *>(p.res + bz * mn + row * N + col);
+            const float4 rc = rcv[c];
             a[0] = a[0] + rc.x; a[1] = a[1] + rc.y; a[2] = a[2] + rc.z; a[3] = a[3] + rc.w;
         }
         v[c] = Vec<float, 4>{{a[0], a[1], a[2], a[3]}};
     }
-    ln_row_finish<NV>(v, N, lane, gamma, beta, eps, y + bz * mn + row * N);
+    ln_row_finish<NV>(v, N, lane, gamma, beta, eps, y + bz * mn + row * N, gv, bv);
 }
 
 // BM x BN block tile, four waves in a WM x WN grid, each wave (BM/WM) x (BN/WN)
