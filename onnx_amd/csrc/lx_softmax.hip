@@ -732,18 +732,23 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 // for heads of at most 32, takes 4 waves and a quarter of the LDS, so that many heads run at once.
 
 // a rows x cols strided matrix into a T x T LDS tile of rows of ld floats, zeros past rows and cols: lane t takes
-// column t % 64 (of the first T) of rows t / 64 + (NT / 64) u, every load in flight before the first store
+// column t % 64 (of the first T) of rows t / 64 + (NT / 64) u.  attn_load issues the loads into x, attn_store
+// writes them, so that the loads of all three operands are in flight together.
 template <int T, int NT>
-__device__ __forceinline__ void attn_stage(float *__restrict__ dst, int ld, const float *__restrict__ src, int rows,
-                                           int cols, int64_t rs, int64_t cs) {
+__device__ __forceinline__ void attn_load(float (&x)[T / (NT / 64)], const float *__restrict__ src, int rows, int cols,
+                                          int64_t rs, int64_t cs) {
     constexpr int RP = NT / 64, U = T / RP;  // rows per pass, passes
     static_assert(U * RP == T, "whole rows per pass");
     const int c = threadIdx.x & 63, r0 = threadIdx.x >> 6;
-    if (c >= T) return;
     const float *p = src + (int64_t)c * cs + (int64_t)r0 * rs;
-    float x[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) x[u] = (c < cols && r0 + RP * u < rows) ? p[(int64_t)(RP * u) * rs] : 0.f;
+    for (int u = 0; u < U; u++) x[u] = (c < T && c < cols && r0 + RP * u < rows) ? p[(int64_t)(RP * u) * rs] : 0.f;
+}
+template <int T, int NT>
+__device__ __forceinline__ void attn_store(const float (&x)[T / (NT / 64)], float *__restrict__ dst, int ld) {
+    constexpr int RP = NT / 64, U = T / RP;
+    const int c = threadIdx.x & 63, r0 = threadIdx.x >> 6;
+    if (c >= T) return;
 #pragma unroll
     for (int u = 0; u < U; u++) dst[(r0 + RP * u) * ld + c] = x[u];
 }
@@ -772,10 +777,34 @@ __global__ __launch_bounds__(NT) void k_attention(AttentionArgs a) {
         }
     }
     const int S = a.s, SK = a.sk, D = a.d, DV = a.dv;
+    // this lane's Softmax row (every row in one pass: NT / 64 waves of 64 / L rows cover T rows) and its mask
+    // elements, loaded with Q, K and V: the mask add below reads them as rag_scale_mask reads them
+    constexpr int RW = 64 / L;  // rows per wave
+    static_assert((NT / 64) * RW >= T, "one Softmax pass");
+    const int gl = l & (L - 1), i = w * RW + l / L;
+    const int64_t row = z * S + i;
+    const RagRow g = rag_row<4>(row * SK, SK);
+    float mv[4] = {0.f, 0.f, 0.f, 0.f}, me = 0.f;
+    if (NOUT != 0 && i < S) {
+        const float *m = a.mask + mask_row_offset<NOUT>((uint32_t)row, a.mask_rows);
+        if (!a.mask_inner) {
+            mv[0] = m[0];
+        } else {
+            if (gl < g.nvb) {
+#pragma unroll
+                for (int k = 0; k < 4; k++) mv[k] = m[g.head + 4 * gl + k];
+            }
+            if (gl < g.ne) me = m[rag_col<4>(g, gl)];
+        }
+    }
     // K's element (kk, j) of the product's right operand is key j's element kk
-    attn_stage<T, NT>(qs, LD, a.q + qo, S, D, a.q_rs, a.q_cs);
-    attn_stage<T, NT>(ks, LD, a.k + ko, SK, D, a.k_cs, a.k_rs);
-    attn_stage<T, NT>(vs, T, a.v + vo, SK, DV, a.v_rs, a.v_cs);
+    float xq[T / (NT / 64)], xk[T / (NT / 64)], xv[T / (NT / 64)];
+    attn_load<T, NT>(xq, a.q + qo, S, D, a.q_rs, a.q_cs);
+    attn_load<T, NT>(xk, a.k + ko, SK, D, a.k_cs, a.k_rs);
+    attn_load<T, NT>(xv, a.v + vo, SK, DV, a.v_rs, a.v_cs);
+    attn_store<T, NT>(xq, qs, LD);
+    attn_store<T, NT>(xk, ks, LD);
+    attn_store<T, NT>(xv, vs, T);
     exp_table_fill(tab);
     __syncthreads();
 
@@ -797,14 +826,10 @@ __global__ __launch_bounds__(NT) void k_attention(AttentionArgs a) {
     }
     __syncthreads();
 
-    constexpr int RW = 64 / L;  // rows per wave at a time
-    const int gl = l & (L - 1);
     const float sv = a.scale ? a.scale[0] : 1.f;
     float sf = sv;
     const bool smul = !a.scale_div || exact_pow2_recip(sv, &sf);
-    for (int i = w * RW + l / L; i < S; i += (NT / 64) * RW) {
-        const int64_t row = z * S + i;
-        const RagRow g = rag_row<4>(row * SK, SK);
+    if (i < S) {
         float *pr = ps + i * LD;
         Vec<float, 4> v[1];
         float e = 0.f;
@@ -813,9 +838,23 @@ __global__ __launch_bounds__(NT) void k_attention(AttentionArgs a) {
             for (int k = 0; k < 4; k++) v[0].v[k] = pr[g.head + 4 * gl + k];
         }
         if (gl < g.ne) e = pr[rag_col<4>(g, gl)];
-        const float *m = nullptr;
-        if constexpr (NOUT != 0) m = a.mask + mask_row_offset<NOUT>((uint32_t)row, a.mask_rows);
-        rag_scale_mask<float, 4, 1, L>(v, e, g, gl, a.scale != nullptr, smul, sf, sv, m, a.mask_inner);
+        // rag_scale_mask's scale, then its mask add with the elements loaded above
+        rag_scale_mask<float, 4, 1, L>(v, e, g, gl, a.scale != nullptr, smul, sf, sv, nullptr, 0);
+        if constexpr (NOUT != 0) {
+            if (!a.mask_inner) {
+                if (gl < g.nvb) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) v[0].v[k] = v[0].v[k] + mv[0];
+                }
+                e = e + mv[0];
+            } else {
+                if (gl < g.nvb) {
+#pragma unroll
+                    for (int k = 0; k < 4; k++) v[0].v[k] = v[0].v[k] + mv[k];
+                }
+                if (gl < g.ne) e = e + me;
+            }
+        }
         float mx = rag_lane_max<float, 4, 1, L>(v, e, g, gl);
         mx = group_reduce<L>(mx, [](float x, float y) { return row_max<float>(x, y); });
         float sum = rag_lane_exp_sum<float, 4, 1, L>(v, e, mx, g, gl, tab);
