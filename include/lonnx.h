@@ -294,7 +294,9 @@ int lx_graph_set_attr_floats(lx_graph *g, int32_t node, const char *attr, const 
 int lx_graph_set_attr_string(lx_graph *g, int32_t node, const char *attr, const char *v);
 int lx_graph_set_attr_tensor(lx_graph *g, int32_t node, const char *attr, int32_t dtype, int32_t rank,
                              const int64_t *dims, const void *host, int64_t nbytes);
-/* Model.Parse + Model.Load (Model.cs:14-63) from the bytes of an ONNX ModelProto. */
+/* Model.Parse + Model.Load (Model.cs:14-63) from the bytes of an ONNX ModelProto.  A malformed protobuf,
+ * including a name, op type or domain that is not UTF-8 (protobuf string fields are UTF-8), fails with
+ * LX_ERR_INVALID_ARGUMENT; a field the reference cannot convert fails with LX_ERR_NOT_SUPPORTED and its message. */
 int lx_graph_load_onnx(const void *bytes, int64_t nbytes, lx_graph **out);
 /* Pattern fusion (no reference counterpart; the reference runs every node):
  * replaces the GELU subgraph (Div sqrt2 -> Erf -> Add 1 -> Mul x -> Mul 0.5), the decomposed
