@@ -14,27 +14,27 @@ from onnx_amd.graph import Model
 pytestmark = pytest.mark.gpu
 
 
-def attention_model(b, h, s, sk, d, dv, mask_kind, scale, extra_outputs=()):
+def attention_model(b, h, s, sk, d, dv, mask_kind, scale, extra_outputs=(), dtype=np.float32):
     rng = np.random.default_rng(s * 1000 + sk * 100 + d + 7 * dv)
     nodes = [W.node("Transpose", ["k"], ["kt"], "tk", perm=[0, 1, 3, 2]),
              W.node("MatMul", ["q", "kt"], ["sc"], "scores")]
     inits = []
     x = "sc"
     if scale is not None:
-        inits.append(("c", np.array(np.sqrt(d) if scale == "div" else 1.0 / np.sqrt(d), np.float32)))
+        inits.append(("c", np.array(np.sqrt(d) if scale == "div" else 1.0 / np.sqrt(d), dtype)))
         nodes.append(W.node("Div" if scale == "div" else "Mul", ["sc", "c"], ["scaled"], "scale"))
         x = "scaled"
     mshape = {"b11s": (b, 1, 1, sk), "bhss": (b, h, s, sk), "b1ss": (b, 1, s, sk), "s": (sk,), "one": (1,)}[mask_kind]
-    mask = np.where(rng.random(mshape) < 0.2, -10000.0, rng.normal(0, 0.5, mshape)).astype(np.float32)
+    mask = np.where(rng.random(mshape) < 0.2, -10000.0, rng.normal(0, 0.5, mshape)).astype(dtype)
     inits.append(("mask", mask))
     nodes += [W.node("Add", [x, "mask"], ["t"], "addmask"), W.node("Softmax", ["t"], ["p"], "softmax", axis=-1),
               W.node("MatMul", ["p", "v"], ["ctx"], "context"),
               W.node("Transpose", ["ctx"], ["y"], "heads", perm=[0, 2, 1, 3])]
-    ins = {"q": rng.normal(0, 1, (b, h, s, d)).astype(np.float32),
-           "k": rng.normal(0, 1, (b, h, sk, d)).astype(np.float32),
-           "v": rng.normal(0, 1, (b, h, sk, dv)).astype(np.float32)}
-    outs = [("y", np.float32, (b, s, h, dv))] + [(o, np.float32, ()) for o in extra_outputs]
-    model = W.model(nodes, [(n, np.float32, a.shape) for n, a in ins.items()], outs, inits)
+    ins = {"q": rng.normal(0, 1, (b, h, s, d)).astype(dtype),
+           "k": rng.normal(0, 1, (b, h, sk, d)).astype(dtype),
+           "v": rng.normal(0, 1, (b, h, sk, dv)).astype(dtype)}
+    outs = [("y", dtype, (b, s, h, dv))] + [(o, dtype, ()) for o in extra_outputs]
+    model = W.model(nodes, [(n, dtype, a.shape) for n, a in ins.items()], outs, inits)
     return model, ins
 
 
@@ -111,6 +111,22 @@ def test_attention_node_random_heads(hip, seed):
         assert g3.Execute(dev) and g.Execute(dev), (g.LastError, g3.LastError)
         got, want = g.Output("y").to_numpy(), g3.Output("y").to_numpy()
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (b, h, s, sk, d, dv, mask_kind, scale)
+
+
+def test_attention_node_of_doubles_runs_the_nodes(hip):
+    """Float64 heads: the Attention node runs its three nodes, and they their original nodes (the fused kernels are
+    Float); the result equals the unfused graph's bit for bit."""
+    # unscaled (a Div by a Float64 constant does not join the Softmax: the scaled pattern takes Float scalars)
+    model, ins = attention_model(2, 3, 8, 8, 32, 32, "bhss", None, dtype=np.float64)
+    dev = {k: DeviceTensor.from_numpy(v) for k, v in ins.items()}
+    g, plain = Model.Load(model), Model.Load(model)
+    g.Fuse()
+    assert [n.Op for n in g.Nodes] == ["Attention"]
+    assert plain.Execute(dev), plain.LastError
+    want = plain.Output("y").to_numpy().copy()
+    assert g.Execute(dev), g.LastError
+    got = g.Output("y").to_numpy()
+    assert got.dtype == np.float64 and np.array_equal(got.view(np.uint64), want.view(np.uint64))
 
 
 def test_attention_node_launch_count(hip):
